@@ -1,0 +1,195 @@
+/*
+ * qw_linear.h -- C ABI of the MI355X (gfx950) projection-matmul library.
+ *
+ * The library replaces the projection/matmul layer of the Qwen3.5-0.8B engine
+ * (reference: zhils/Qwen3.5_0.8B_Deploy, src/backend).  Every entry point is
+ * plain C: device pointers, sizes, dtype tags and a hipStream_t.  Nothing here
+ * allocates on the hot path: scratch (split-K partials, counters, argmax keys,
+ * the MLP intermediate) lives in a workspace arena sized at qw_init().
+ *
+ * Conventions
+ *   - Weights are row-major W[N][K] (N = output features, K = input features),
+ *     the reference convention (language_mlp.cpp:69-70, lm_head.cpp:30-36).
+ *   - Activations are row-major x[M][ldx] with M tokens; outputs y[M][ldy].
+ *     ld* of 0 means "packed" (ldx = K, ldy = N).
+ *   - y[m][o] = sum_k W[o][k] * x[m][k], FP32 accumulate.
+ *   - Calls are asynchronous on the given stream and never synchronize the
+ *     host.  One qw_ctx per stream: calls made through one context share its
+ *     workspace, so two streams must not use the same context concurrently.
+ *   - Errors are returned as qw_status; qw_last_error() gives the message of
+ *     the most recent failure on that context.
+ */
+#ifndef QW_LINEAR_H
+#define QW_LINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QW_ABI_VERSION 1
+
+typedef enum {
+    QW_OK = 0,
+    QW_ERR_INVALID = 1,   /* bad argument value (flags, eps, ...)            */
+    QW_ERR_NULL = 2,      /* required pointer is NULL                        */
+    QW_ERR_SHAPE = 3,     /* M/N/K out of range or not a supported multiple  */
+    QW_ERR_DTYPE = 4,     /* dtype / weight-format combination unsupported   */
+    QW_ERR_ALIGN = 5,     /* pointer or leading dimension misaligned         */
+    QW_ERR_WORKSPACE = 6, /* call needs more workspace than qw_init reserved */
+    QW_ERR_HIP = 7,       /* a HIP runtime call failed                       */
+    QW_ERR_NOMEM = 8,     /* device allocation failed (weight packing)       */
+    QW_ERR_STATE = 9      /* call not valid in the current state             */
+} qw_status;
+
+typedef enum { QW_F32 = 0, QW_BF16 = 1, QW_F16 = 2, QW_I8 = 3 } qw_dtype;
+
+/* Stored weight formats.  INT8_ROWSCALE is weight-only INT8 with one FP32
+ * scale per output row (symmetric, the reference recipe mlp_cuda.cu:22-39). */
+typedef enum { QW_WFMT_F32 = 0, QW_WFMT_BF16 = 1, QW_WFMT_INT8_ROWSCALE = 2 } qw_wfmt;
+
+typedef struct qw_ctx qw_ctx;
+typedef struct qw_weight qw_weight;
+typedef struct qw_graph qw_graph;
+
+/* ---- context -------------------------------------------------------------
+ * Replaces the per-operator lazily grown scratch of the reference
+ * (CudaMLP::ensure_buffers, mlp_cuda.cu:229-259, and the per-call
+ * cudaMalloc/cudaFree of CudaMLP::forward, mlp_cuda.cu:302-303,328-329)
+ * with one arena reserved up front.  workspace_bytes = 0 picks the default
+ * (qw_workspace_query(128, 8224, 3584)). */
+qw_status qw_init(qw_ctx** ctx, int device, size_t workspace_bytes);
+qw_status qw_destroy(qw_ctx* ctx);
+/* Workspace needed for calls with up to max_M tokens, max_N output rows
+ * (a GLU weight counts its gate+up rows) and max_K inputs. */
+size_t qw_workspace_query(int max_M, int max_N, int max_K);
+const char* qw_last_error(const qw_ctx* ctx);
+const char* qw_status_string(qw_status s);
+int qw_abi_version(void);
+
+/* ---- weights ---------------------------------------------------------------
+ * Replaces CudaMLP::set_weights (mlp_cuda.cu:261-293: H2D + on-device INT8
+ * quantization), CudaLMHead::set_weight (lm_head_cuda.cu:163-187: host
+ * FP32->BF16) and the set_weights of the attention operators
+ * (linear_attention_cuda.cu:412-466, full_attention_cuda.cu:230-250).
+ *
+ * `w` is a HOST pointer to W[N][K] in dtype `src` (F32, BF16, F16, or I8 when
+ * `scales` gives the per-row FP32 scales of an already quantized matrix).
+ * The library re-lays the matrix out in gfx950 MFMA tile order on the device
+ * and owns the result.  For dst = INT8_ROWSCALE with a floating source the
+ * reference quantization recipe is applied on the device.  K must be a
+ * multiple of 64; any N >= 1 is accepted (rows are padded to 16). */
+qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
+                         const float* scales, qw_weight** out);
+/* Gate/up pair for the SiLU*mul epilogue: both W[N][K]; packed interleaved so
+ * one pass computes silu(gate.x) * (up.x).  Scales as in qw_weight_pack. */
+qw_status qw_weight_pack_glu(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
+                             qw_wfmt dst, int N, int K, const float* gate_scales,
+                             const float* up_scales, qw_weight** out);
+/* Borrow: build a weight object over device memory already in packed order
+ * (e.g. a tied embedding shared with the lm_head, as
+ * CudaLMHead::set_weight_bf16_ptr borrows, lm_head_cuda.cu:189-196).  The
+ * caller keeps ownership of `packed` and `scales`. */
+qw_status qw_weight_wrap_packed(qw_ctx* ctx, void* packed, float* scales, qw_wfmt fmt, int N,
+                                int K, qw_weight** out);
+qw_status qw_weight_free(qw_weight* w);
+/* Size, shape and format of a packed weight (any out pointer may be NULL). */
+qw_status qw_weight_info(const qw_weight* w, int* N, int* K, qw_wfmt* fmt, int* is_glu,
+                         size_t* packed_bytes);
+/* Device pointers of the packed data and of the per-row scales (NULL for
+ * non-INT8 formats). */
+qw_status qw_weight_device_ptrs(const qw_weight* w, const void** packed, const float** scales);
+/* Copy the stored values back to the host in row-major order: dst receives
+ * W[N][K] in the stored dtype (F32, BF16 bits, or INT8) and, for INT8,
+ * scales_dst receives N scales.  For a GLU weight, rows [0,N) are the gate
+ * and [N,2N) the up projection.  Synchronous; used by tests and tools. */
+qw_status qw_weight_unpack(qw_ctx* ctx, const qw_weight* w, void* dst, float* scales_dst);
+
+/* ---- epilogue --------------------------------------------------------------
+ * Fusions available on qw_linear / qw_gemm. */
+enum {
+    QW_EP_RESIDUAL = 1u << 0, /* y = acc + residual[m][o] (residual may alias y) */
+    QW_EP_NORM_X = 1u << 1,   /* x := RMSNorm(x)*(1+gamma) before the product   */
+    QW_EP_SPLIT = 1u << 2     /* rows alternate in blocks of split_period between
+                                 y and y2 (full-attention Q / output gate) */
+};
+
+typedef struct {
+    unsigned flags;
+    const void* residual;   /* QW_EP_RESIDUAL: [M][ld_residual]                */
+    qw_dtype residual_dtype;
+    int ld_residual;        /* 0 = N                                           */
+    const float* gamma;     /* QW_EP_NORM_X: [K] RMSNorm weight, (1+gamma) form */
+    float eps;              /* QW_EP_NORM_X epsilon (reference: 1e-6)           */
+    int split_period;       /* QW_EP_SPLIT: block length (multiple of 16)       */
+    void* y2;               /* QW_EP_SPLIT: second output [M][ldy]              */
+} qw_epilogue;
+
+/* ---- projections -------------------------------------------------------------
+ * y = W.x with the epilogue.  A GLU weight yields y[m][o] = silu(g)*u for its
+ * N logical rows.  Replaces launch_cutlass_gemv[_bf16|_fused_silu]
+ * (cutlass_gemm_wrapper.cuh:202-263), the INT8 GEMV of CudaMLP
+ * (mlp_cuda.cu:158-180), the projection kernels of the attention operators
+ * (linear_attention_cuda.cu:33-45,174-187; full_attention_cuda.cu:31-76,
+ * 78-148,161-172), cublas_sgemm[_add_residual] (cublas_utils.cuh:48-93) and
+ * bf16_gemv[_add] (bf16_gemm.cuh:82-122).  Picks the skinny MFMA kernel for
+ * small M and the LDS-tiled MFMA GEMM for large M.
+ * Supported x dtypes: F32 (any weight), BF16 (BF16/INT8 weights), F16
+ * (BF16/INT8 weights).  y dtype: F32, BF16 or F16. */
+qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx, int M,
+                    void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep, hipStream_t stream);
+
+/* ---- fused MLP ---------------------------------------------------------------
+ * y = [residual +] down( silu(gate.xn) * up.xn ),  xn = gamma ? RMSNorm(x) : x.
+ * Replaces CudaMLP::forward / forward_add_residual (mlp_cuda.cu:295-337; the
+ * residual is ADDED, unlike mlp_cuda.cu:332-337) and the fused post-norm +
+ * MLP + residual of fusion_microbench_kernels.cu:583-609.  `gateup` must be a
+ * GLU weight [I][H], `down` a weight [H][I].  residual may alias y. */
+qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,
+                       qw_dtype xdt, const float* gamma, float eps, const void* residual,
+                       qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream);
+
+/* ---- lm_head + greedy argmax -------------------------------------------------
+ * token_ids[m] = argmax_v sum_k E[v][k]*h[m][k]; ties go to the LOWEST index
+ * (std::max_element, sampler.cpp:41-43).  max_logit (optional) receives the
+ * winning logit.  Replaces CudaLMHead::forward (lm_head_cuda.cu:198-210) +
+ * GpuGreedyArgmaxSampler::sample (gpu_sampler_argmax.cu:69-93) with one launch
+ * and no host round trip. */
+qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M,
+                           int32_t* token_ids, float* max_logit, hipStream_t stream);
+
+/* ---- RMSNorm -----------------------------------------------------------------
+ * y = x / sqrt(mean(x^2) + eps) * (1 + gamma)  (language_common.cpp:21-78,
+ * CudaRMSNorm::forward rmsnorm_cuda.cu:350-368). */
+qw_status qw_rmsnorm(qw_ctx* ctx, const void* x, qw_dtype xdt, const float* gamma, float eps,
+                     void* y, qw_dtype ydt, int M, int K, hipStream_t stream);
+/* residual_out = residual_in + a;  normed = RMSNorm(residual_out)
+ * (CudaRMSNorm::forward_with_residual rmsnorm_cuda.cu:370-394,
+ * launch_fused_rmsnorm_residual fused_kernels.cuh:9-18).  residual_out may
+ * alias residual_in. */
+qw_status qw_residual_rmsnorm(qw_ctx* ctx, const void* residual_in, const void* a, qw_dtype dt,
+                              void* residual_out, void* normed, qw_dtype normed_dt,
+                              const float* gamma, float eps, int M, int K, hipStream_t stream);
+/* h[i] = silu(g[i]) * u[i] for n elements (launch_silu_mul_batch,
+ * fused_kernels.cuh:29-34); all three in dtype dt. */
+qw_status qw_silu_mul(qw_ctx* ctx, const void* g, const void* u, void* h, qw_dtype dt, int64_t n,
+                      hipStream_t stream);
+
+/* ---- graphs --------------------------------------------------------------------
+ * Capture a sequence of qw_* calls on `stream` into a replayable HIP graph
+ * (the role of cudaStreamBeginCapture/cudaGraphLaunch in
+ * CudaEngine::forward_batch_prefill_graph, cuda_engine.cu:454-477).  The qw_*
+ * calls issue no memset and no allocation, so they are capture-safe. */
+qw_status qw_graph_begin(qw_ctx* ctx, hipStream_t stream);
+qw_status qw_graph_end(qw_ctx* ctx, hipStream_t stream, qw_graph** out);
+qw_status qw_graph_launch(qw_graph* g, hipStream_t stream);
+qw_status qw_graph_destroy(qw_graph* g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QW_LINEAR_H */

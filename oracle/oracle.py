@@ -1,0 +1,296 @@
+"""ctypes view of the CPU oracle (oracle/liboracle.so) and of the reference
+build (oracle/_ref/libqwref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, always as the checker, never as the thing measured
+or shipped.  The restated functions live in oracle/qw_oracle.c, each citing the
+reference file:line it follows.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+_REF = None
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+_fl = ctypes.c_float
+
+
+def build():
+    """Compile the oracle (and oracle/_ref when the reference tree exists)."""
+    import subprocess
+    subprocess.check_call(["make", "-s", "-C", _HERE, "all"])
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        sig = {
+            "orc_f32_to_bf16_n": [_f32p, _u16p, _i64],
+            "orc_bf16_to_f32_n": [_u16p, _f32p, _i64],
+            "orc_f32_to_f16_n": [_f32p, _u16p, _i64],
+            "orc_f16_to_f32_n": [_u16p, _f32p, _i64],
+            "orc_linear_f32": [_f32p, _f32p, _f32p, _i, _i, _i],
+            "orc_linear_f64": [_f32p, _f32p, _f64p, _i, _i, _i],
+            "orc_quantize_rowscale": [_f32p, _i8p, _f32p, _i, _i],
+            "orc_linear_int8_dequant": [_i8p, _f32p, _f32p, _f32p, _i, _i, _i],
+            "orc_linear_int8_f64": [_i8p, _f32p, _f32p, _f64p, _i, _i, _i],
+            "orc_rmsnorm": [_f32p, _f32p, _f32p, _i, _i, _fl],
+            "orc_rmsnorm_f64": [_f32p, _f32p, _f64p, _i, _i, ctypes.c_double],
+            "orc_residual_rmsnorm": [_f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _fl],
+            "orc_mlp": [_f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i],
+            "orc_mlp_f64": [_f32p, _f32p, _f32p, _f32p, _f64p, _i, _i, _i],
+            "orc_mlp_block": [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i, _fl],
+            "orc_mlp_block_f64": [_f32p, _f32p, _f32p, _f32p, _f32p, _f64p, _i, _i, _i, ctypes.c_double],
+            "orc_split_q_gate": [_f32p, _f32p, _f32p, _i, _i, _i],
+            "orc_argmax_first": [_f32p, _i64],
+            "orc_lmhead_argmax": [_f32p, _f32p, _i32p, _f32p, _i, _i, _i],
+            "orc_lmhead_argmax_bf16": [_u16p, _u16p, _i32p, _f32p, _i, _i, _i],
+            "orc_lmhead_argmax_int8": [_i8p, _f32p, _f32p, _i32p, _f32p, _i, _i, _i],
+            "orc_fill_normal": [_f32p, _i64, ctypes.c_uint64, _fl, _fl],
+            "orc_fill_uniform": [_f32p, _i64, ctypes.c_uint64, _fl, _fl],
+            "orc_fill_int8_uniform": [_i8p, _i64, ctypes.c_uint64, _i, _i],
+            "orc_silu": [_fl],
+        }
+        for name, args in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = None
+        L.orc_argmax_first.restype = ctypes.c_int32
+        L.orc_silu.restype = ctypes.c_float
+        _LIB = L
+    return _LIB
+
+
+def ref_lib():
+    """The reference's own CPU operators (None when oracle/_ref was not built)."""
+    global _REF
+    if _REF is None:
+        path = os.path.join(_HERE, "_ref", "libqwref.so")
+        if not os.path.exists(path):
+            return None
+        R = ctypes.CDLL(path)
+        R.ref_linear.argtypes = [_f32p, _f32p, _f32p, _i, _i, _i]
+        R.ref_mlp.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i]
+        R.ref_greedy.argtypes = [_f32p, _i]
+        R.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i, _i, _fl]
+        for fn in (R.ref_linear, R.ref_mlp, R.ref_greedy, R.ref_rmsnorm):
+            fn.restype = ctypes.c_int
+        _REF = R
+    return _REF
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+# ---- number formats ------------------------------------------------------
+def to_bf16(x):
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_bf16_n(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def from_bf16(h):
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_bf16_to_f32_n(h.reshape(-1), out.reshape(-1), h.size)
+    return out
+
+
+def to_f16(x):
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f32_to_f16_n(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def from_f16(h):
+    h = _c(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_f16_to_f32_n(h.reshape(-1), out.reshape(-1), h.size)
+    return out
+
+
+def round_bf16(x):
+    return from_bf16(to_bf16(x))
+
+
+def round_f16(x):
+    return from_f16(to_f16(x))
+
+
+# ---- projections -----------------------------------------------------------
+def linear(W, x):
+    W = _c(W, np.float32); x = _c(np.atleast_2d(x), np.float32)
+    N, K = W.shape; M = x.shape[0]
+    y = np.empty((M, N), np.float32)
+    lib().orc_linear_f32(W, x, y, M, N, K)
+    return y
+
+
+def linear_f64(W, x):
+    W = _c(W, np.float32); x = _c(np.atleast_2d(x), np.float32)
+    N, K = W.shape; M = x.shape[0]
+    y = np.empty((M, N), np.float64)
+    lib().orc_linear_f64(W, x, y, M, N, K)
+    return y
+
+
+def quantize_rowscale(W):
+    W = _c(W, np.float32)
+    N, K = W.shape
+    q = np.empty((N, K), np.int8); s = np.empty(N, np.float32)
+    lib().orc_quantize_rowscale(W, q, s, N, K)
+    return q, s
+
+
+def linear_int8(q, s, x):
+    q = _c(q, np.int8); s = _c(s, np.float32); x = _c(np.atleast_2d(x), np.float32)
+    N, K = q.shape; M = x.shape[0]
+    y = np.empty((M, N), np.float32)
+    lib().orc_linear_int8_dequant(q, s, x, y, M, N, K)
+    return y
+
+
+def linear_int8_f64(q, s, x):
+    q = _c(q, np.int8); s = _c(s, np.float32); x = _c(np.atleast_2d(x), np.float32)
+    N, K = q.shape; M = x.shape[0]
+    y = np.empty((M, N), np.float64)
+    lib().orc_linear_int8_f64(q, s, x, y, M, N, K)
+    return y
+
+
+def rmsnorm(x, w, eps=1e-6):
+    x = _c(np.atleast_2d(x), np.float32); w = _c(w, np.float32)
+    M, K = x.shape
+    y = np.empty_like(x)
+    lib().orc_rmsnorm(x, w, y, M, K, eps)
+    return y
+
+
+def rmsnorm_f64(x, w, eps=1e-6):
+    x = _c(np.atleast_2d(x), np.float32); w = _c(w, np.float32)
+    M, K = x.shape
+    y = np.empty((M, K), np.float64)
+    lib().orc_rmsnorm_f64(x, w, y, M, K, eps)
+    return y
+
+
+def residual_rmsnorm(res, a, w, eps=1e-6):
+    res = _c(np.atleast_2d(res), np.float32); a = _c(np.atleast_2d(a), np.float32)
+    w = _c(w, np.float32)
+    M, K = res.shape
+    ro = np.empty_like(res); no = np.empty_like(res)
+    lib().orc_residual_rmsnorm(res, a, w, ro, no, M, K, eps)
+    return ro, no
+
+
+def silu(v):
+    return lib().orc_silu(float(v))
+
+
+def mlp(Wg, Wu, Wd, x):
+    Wg, Wu, Wd = (_c(a, np.float32) for a in (Wg, Wu, Wd))
+    x = _c(np.atleast_2d(x), np.float32)
+    I, H = Wg.shape; M = x.shape[0]
+    y = np.empty((M, H), np.float32)
+    lib().orc_mlp(Wg, Wu, Wd, x, y, M, H, I)
+    return y
+
+
+def mlp_f64(Wg, Wu, Wd, x):
+    Wg, Wu, Wd = (_c(a, np.float32) for a in (Wg, Wu, Wd))
+    x = _c(np.atleast_2d(x), np.float32)
+    I, H = Wg.shape; M = x.shape[0]
+    y = np.empty((M, H), np.float64)
+    lib().orc_mlp_f64(Wg, Wu, Wd, x, y, M, H, I)
+    return y
+
+
+def mlp_block(Wg, Wu, Wd, gamma, x, eps=1e-6):
+    Wg, Wu, Wd, gamma = (_c(a, np.float32) for a in (Wg, Wu, Wd, gamma))
+    x = _c(np.atleast_2d(x), np.float32)
+    I, H = Wg.shape; M = x.shape[0]
+    y = np.empty((M, H), np.float32)
+    lib().orc_mlp_block(Wg, Wu, Wd, gamma, x, y, M, H, I, eps)
+    return y
+
+
+def mlp_block_f64(Wg, Wu, Wd, gamma, x, eps=1e-6):
+    Wg, Wu, Wd, gamma = (_c(a, np.float32) for a in (Wg, Wu, Wd, gamma))
+    x = _c(np.atleast_2d(x), np.float32)
+    I, H = Wg.shape; M = x.shape[0]
+    y = np.empty((M, H), np.float64)
+    lib().orc_mlp_block_f64(Wg, Wu, Wd, gamma, x, y, M, H, I, eps)
+    return y
+
+
+def split_q_gate(q_raw, heads, head_dim):
+    q_raw = _c(np.atleast_2d(q_raw), np.float32)
+    M = q_raw.shape[0]
+    q = np.empty((M, heads * head_dim), np.float32); g = np.empty_like(q)
+    lib().orc_split_q_gate(q_raw, q, g, M, heads, head_dim)
+    return q, g
+
+
+def argmax_first(v):
+    v = _c(v, np.float32).reshape(-1)
+    return int(lib().orc_argmax_first(v, v.size))
+
+
+def lmhead_argmax(E, h):
+    E = _c(E, np.float32); h = _c(np.atleast_2d(h), np.float32)
+    V, K = E.shape; M = h.shape[0]
+    ids = np.empty(M, np.int32); mx = np.empty(M, np.float32)
+    lib().orc_lmhead_argmax(E, h, ids, mx, M, V, K)
+    return ids, mx
+
+
+def lmhead_argmax_bf16(E_bits, h_bits):
+    E_bits = _c(E_bits, np.uint16); h_bits = _c(np.atleast_2d(h_bits), np.uint16)
+    V, K = E_bits.shape; M = h_bits.shape[0]
+    ids = np.empty(M, np.int32); mx = np.empty(M, np.float32)
+    lib().orc_lmhead_argmax_bf16(E_bits, h_bits, ids, mx, M, V, K)
+    return ids, mx
+
+
+def lmhead_argmax_int8(q, s, h):
+    q = _c(q, np.int8); s = _c(s, np.float32); h = _c(np.atleast_2d(h), np.float32)
+    V, K = q.shape; M = h.shape[0]
+    ids = np.empty(M, np.int32); mx = np.empty(M, np.float32)
+    lib().orc_lmhead_argmax_int8(q, s, h, ids, mx, M, V, K)
+    return ids, mx
+
+
+# ---- seeded generator ------------------------------------------------------
+def normal(shape, seed, mean=0.0, std=1.0):
+    out = np.empty(shape, np.float32)
+    lib().orc_fill_normal(out.reshape(-1), out.size, seed, mean, std)
+    return out
+
+
+def uniform(shape, seed, lo, hi):
+    out = np.empty(shape, np.float32)
+    lib().orc_fill_uniform(out.reshape(-1), out.size, seed, lo, hi)
+    return out
+
+
+def int8_uniform(shape, seed, lo=-127, hi=127):
+    out = np.empty(shape, np.int8)
+    lib().orc_fill_int8_uniform(out.reshape(-1), out.size, seed, lo, hi)
+    return out

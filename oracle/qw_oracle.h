@@ -1,0 +1,100 @@
+/*
+ * qw_oracle.h -- CPU oracle for the projection-matmul path (TEST INFRASTRUCTURE).
+ *
+ * This library is the checker, never the product: only tests/, the smoke()
+ * entry point and bench.py's cpu_baseline leg load it.  Every function is a
+ * scalar restatement of a reference CPU operator (file:line cited at each
+ * definition in qw_oracle.c), or an FP64 ground truth used to bound the error
+ * of the GPU kernels.
+ *
+ * Conventions (identical to the reference CPU operators):
+ *   - weights are row-major W[out][in]  (N rows of K elements);
+ *   - activations are row-major x[M][K], outputs y[M][N];
+ *   - y[m][o] = sum_k W[o][k] * x[m][k], FP32 accumulated in ascending k.
+ *
+ * Parity pins for each function are listed in oracle/README.md.
+ */
+#ifndef QW_ORACLE_H
+#define QW_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- number formats (round-to-nearest-even, as torch / HIP intrinsics) ---- */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+void orc_f32_to_bf16_n(const float* src, uint16_t* dst, int64_t n);
+void orc_bf16_to_f32_n(const uint16_t* src, float* dst, int64_t n);
+void orc_f32_to_f16_n(const float* src, uint16_t* dst, int64_t n);
+void orc_f16_to_f32_n(const uint16_t* src, float* dst, int64_t n);
+
+/* ---- projections ---- */
+/* FP32 sequential-k matvec over M rows: y[m][o] = sum_k W[o][k]*x[m][k]. */
+void orc_linear_f32(const float* W, const float* x, float* y, int M, int N, int K);
+/* FP64 ground truth on the same FP32 inputs. */
+void orc_linear_f64(const float* W, const float* x, double* y, int M, int N, int K);
+
+/* ---- INT8 weight-only ---- */
+/* Per-output-row symmetric quantization: s=max|w|/127 (1.0 if <=1e-8),
+ * q=clamp(roundf(w/s),-127,127). */
+void orc_quantize_rowscale(const float* W, int8_t* q, float* s, int N, int K);
+/* Dequant-then-matmul: y[m][o] = sum_k (q[o][k]*s[o]) * x[m][k]. */
+void orc_linear_int8_dequant(const int8_t* q, const float* s, const float* x, float* y,
+                             int M, int N, int K);
+/* FP64 ground truth: y = s[o] * sum_k q[o][k]*x[m][k]. */
+void orc_linear_int8_f64(const int8_t* q, const float* s, const float* x, double* y,
+                         int M, int N, int K);
+
+/* ---- epilogue pieces ---- */
+float orc_silu(float x);
+/* RMSNorm with the Qwen3.5 (1+w) convention, eps given. */
+void orc_rmsnorm(const float* x, const float* w, float* y, int M, int K, float eps);
+void orc_rmsnorm_f64(const float* x, const float* w, double* y, int M, int K, double eps);
+/* residual_out = residual_in + a ; normed = RMSNorm(residual_out). */
+void orc_residual_rmsnorm(const float* residual_in, const float* a, const float* w,
+                          float* residual_out, float* normed, int M, int K, float eps);
+
+/* ---- MLP block ---- */
+/* y[m] = Wd . (silu(Wg.x) * (Wu.x)), FP32, sequential k. */
+void orc_mlp(const float* Wg, const float* Wu, const float* Wd, const float* x, float* y,
+             int M, int H, int I);
+/* FP64 ground truth of the same. */
+void orc_mlp_f64(const float* Wg, const float* Wu, const float* Wd, const float* x, double* y,
+                 int M, int H, int I);
+/* Decoder-layer MLP half: h = residual; y = h + MLP(RMSNorm(h)). */
+void orc_mlp_block(const float* Wg, const float* Wu, const float* Wd, const float* gamma,
+                   const float* x, float* y, int M, int H, int I, float eps);
+void orc_mlp_block_f64(const float* Wg, const float* Wu, const float* Wd, const float* gamma,
+                       const float* x, double* y, int M, int H, int I, double eps);
+
+/* ---- full attention Q+gate de-interleave ---- */
+/* q_raw[m][H*2D] -> q[m][H*D], gate[m][H*D]: head h rows [h*2D,h*2D+D) are Q. */
+void orc_split_q_gate(const float* q_raw, float* q, float* gate, int M, int heads, int head_dim);
+
+/* ---- lm_head + greedy argmax ---- */
+/* index of the first maximum (std::max_element semantics). */
+int32_t orc_argmax_first(const float* v, int64_t n);
+/* logits = E . h (FP32 sequential k), ids[m] = first argmax, maxv[m] = its logit. */
+void orc_lmhead_argmax(const float* E, const float* h, int32_t* ids, float* maxv,
+                       int M, int V, int K);
+/* Same over bf16 inputs (E and h given as bf16 bits), FP32 accumulate. */
+void orc_lmhead_argmax_bf16(const uint16_t* E, const uint16_t* h, int32_t* ids, float* maxv,
+                            int M, int V, int K);
+/* INT8 per-row-scaled E: logits = s[v]*sum_k q[v][k]*h[m][k] (FP32). */
+void orc_lmhead_argmax_int8(const int8_t* q, const float* s, const float* h, int32_t* ids,
+                            float* maxv, int M, int V, int K);
+
+/* ---- seeded synthetic generator (mt19937-64 + Box-Muller) ---- */
+void orc_fill_normal(float* dst, int64_t n, uint64_t seed, float mean, float std);
+void orc_fill_uniform(float* dst, int64_t n, uint64_t seed, float lo, float hi);
+void orc_fill_int8_uniform(int8_t* dst, int64_t n, uint64_t seed, int lo, int hi);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

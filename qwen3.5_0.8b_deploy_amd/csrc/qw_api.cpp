@@ -1,0 +1,650 @@
+// qw_api.cpp -- C ABI of the projection library (declared in include/qw_linear.h).
+//
+// Host side only: argument validation, workspace carving, kernel choice and
+// launch.  Nothing here synchronizes the stream or allocates on the hot path;
+// device memory is reserved by qw_init (workspace) and qw_weight_pack
+// (weights) only.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/qw_linear.h"
+#include "qw_kernels.hpp"
+
+struct qw_ctx {
+    int device = 0;
+    int num_cus = 256;
+    uint8_t* ws = nullptr;
+    size_t ws_bytes = 0;
+    // carved regions
+    unsigned* counters = nullptr;          // split-K arrival counters
+    unsigned long long* keys = nullptr;    // argmax keys
+    unsigned* done = nullptr;              // argmax completion counter
+    float4* partials = nullptr;
+    size_t partials_bytes = 0;
+    uint8_t* scratch = nullptr;            // MLP intermediate
+    size_t scratch_bytes = 0;
+    std::string err;
+};
+
+struct qw_weight {
+    qw_ctx* ctx = nullptr;
+    uint8_t* packed = nullptr;
+    float* scales = nullptr;
+    int N = 0;        // logical output rows
+    int K = 0;
+    int wf = 0;       // qw_wfmt
+    int glu = 0;
+    int phys_tiles = 0;
+    int ksteps = 0;
+    size_t bytes = 0;
+    bool owns = true;
+};
+
+struct qw_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+constexpr size_t kCountersBytes = 64 * 1024;     // 16384 tiles
+constexpr size_t kKeysBytes = 64 * 1024;         // 8192 tokens
+constexpr size_t kDoneBytes = 256;
+constexpr size_t kPartialsBytes = 32u << 20;
+constexpr size_t kFixedBytes = kCountersBytes + kKeysBytes + kDoneBytes + kPartialsBytes;
+constexpr int kMaxCounters = (int)(kCountersBytes / 4);
+constexpr int kMaxKeys = (int)(kKeysBytes / 8);
+constexpr int kSkinnyMaxM = 32;
+
+qw_status fail(qw_ctx* c, qw_status s, const char* fmt, ...) {
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return s;
+}
+
+qw_status hip_fail(qw_ctx* c, hipError_t e, const char* what) {
+    return fail(c, QW_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int ke_of(int wf) { return wf == QW_WFMT_F32 ? 4 : (wf == QW_WFMT_BF16 ? 8 : 16); }
+int esize_of(int wf) { return wf == QW_WFMT_F32 ? 4 : (wf == QW_WFMT_BF16 ? 2 : 1); }
+int dsize(qw_dtype d) { return d == QW_F32 ? 4 : (d == QW_I8 ? 1 : 2); }
+bool valid_act(qw_dtype d) { return d == QW_F32 || d == QW_BF16 || d == QW_F16; }
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+size_t scratch_need(int M, int I) { return (size_t)M * I * 4; }
+
+}  // namespace
+
+extern "C" {
+
+int qw_abi_version(void) { return QW_ABI_VERSION; }
+
+const char* qw_status_string(qw_status s) {
+    switch (s) {
+        case QW_OK: return "ok";
+        case QW_ERR_INVALID: return "invalid argument";
+        case QW_ERR_NULL: return "null pointer";
+        case QW_ERR_SHAPE: return "unsupported shape";
+        case QW_ERR_DTYPE: return "unsupported dtype";
+        case QW_ERR_ALIGN: return "misaligned pointer or leading dimension";
+        case QW_ERR_WORKSPACE: return "workspace too small";
+        case QW_ERR_HIP: return "HIP runtime error";
+        case QW_ERR_NOMEM: return "out of device memory";
+        case QW_ERR_STATE: return "invalid state";
+    }
+    return "unknown status";
+}
+
+const char* qw_last_error(const qw_ctx* ctx) { return ctx ? ctx->err.c_str() : "null context"; }
+
+size_t qw_workspace_query(int max_M, int max_N, int max_K) {
+    (void)max_K;
+    if (max_M < 1) max_M = 1;
+    if (max_N < 1) max_N = 1;
+    size_t s = kFixedBytes + scratch_need(max_M, max_N);
+    return (s + 4095) & ~(size_t)4095;
+}
+
+qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
+    if (!out) return QW_ERR_NULL;
+    *out = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return QW_ERR_HIP;
+    if (device < 0 || device >= ndev) return QW_ERR_INVALID;
+    if (hipSetDevice(device) != hipSuccess) return QW_ERR_HIP;
+    qw_ctx* c = new qw_ctx();
+    c->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+        c->num_cus = prop.multiProcessorCount;
+    if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(128, 8224, 3584);
+    workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(1u << 20));
+    workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
+    if (hipMalloc(&c->ws, workspace_bytes) != hipSuccess) {
+        delete c;
+        return QW_ERR_NOMEM;
+    }
+    c->ws_bytes = workspace_bytes;
+    uint8_t* p = c->ws;
+    c->counters = reinterpret_cast<unsigned*>(p); p += kCountersBytes;
+    c->keys = reinterpret_cast<unsigned long long*>(p); p += kKeysBytes;
+    c->done = reinterpret_cast<unsigned*>(p); p += kDoneBytes;
+    c->partials = reinterpret_cast<float4*>(p); p += kPartialsBytes;
+    c->partials_bytes = kPartialsBytes;
+    c->scratch = p;
+    c->scratch_bytes = workspace_bytes - kFixedBytes;
+    // counters, keys and the completion counter start at zero; every kernel
+    // that uses them returns them to zero before it exits.
+    if (hipMemset(c->ws, 0, kCountersBytes + kKeysBytes + kDoneBytes) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        hipFree(c->ws);
+        delete c;
+        return QW_ERR_HIP;
+    }
+    *out = c;
+    return QW_OK;
+}
+
+qw_status qw_destroy(qw_ctx* ctx) {
+    if (!ctx) return QW_ERR_NULL;
+    hipSetDevice(ctx->device);
+    if (ctx->ws) hipFree(ctx->ws);
+    delete ctx;
+    return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// weights
+// ---------------------------------------------------------------------------
+
+static qw_status alloc_weight(qw_ctx* ctx, qw_wfmt dst, int N, int K, int glu, qw_weight** out) {
+    qw_weight* w = new qw_weight();
+    w->ctx = ctx;
+    w->N = N;
+    w->K = K;
+    w->wf = dst;
+    w->glu = glu;
+    const int tiles = (N + 15) / 16;
+    w->phys_tiles = tiles * (glu ? 2 : 1);
+    w->ksteps = K / (4 * ke_of(dst));
+    w->bytes = (size_t)w->phys_tiles * w->ksteps * 1024;
+    if (hipMalloc(&w->packed, w->bytes) != hipSuccess) {
+        delete w;
+        return fail(ctx, QW_ERR_NOMEM, "hipMalloc of %zu bytes for packed weight failed", w->bytes);
+    }
+    if (hipMemset(w->packed, 0, w->bytes) != hipSuccess) {
+        hipFree(w->packed);
+        delete w;
+        return fail(ctx, QW_ERR_HIP, "hipMemset of packed weight failed");
+    }
+    if (dst == QW_WFMT_INT8_ROWSCALE) {
+        const size_t sb = (size_t)w->phys_tiles * 16 * sizeof(float);
+        if (hipMalloc(&w->scales, sb) != hipSuccess) {
+            hipFree(w->packed);
+            delete w;
+            return fail(ctx, QW_ERR_NOMEM, "hipMalloc of scales failed");
+        }
+        hipMemset(w->scales, 0, sb);
+    }
+    *out = w;
+    return QW_OK;
+}
+
+static qw_status check_pack_args(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
+                                 const float* scales) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!w) return fail(ctx, QW_ERR_NULL, "weight pointer is NULL");
+    if (N < 1 || K < 64 || K % 64 != 0)
+        return fail(ctx, QW_ERR_SHAPE, "weight shape N=%d K=%d: need N>=1 and K a positive multiple of 64", N, K);
+    if ((size_t)N * K > (size_t)1 << 34) return fail(ctx, QW_ERR_SHAPE, "weight too large");
+    if (dst != QW_WFMT_F32 && dst != QW_WFMT_BF16 && dst != QW_WFMT_INT8_ROWSCALE)
+        return fail(ctx, QW_ERR_DTYPE, "unknown weight format %d", (int)dst);
+    if (src == QW_I8) {
+        if (dst != QW_WFMT_INT8_ROWSCALE)
+            return fail(ctx, QW_ERR_DTYPE, "INT8 source requires the INT8_ROWSCALE format");
+        if (!scales) return fail(ctx, QW_ERR_NULL, "INT8 source requires per-row scales");
+    } else if (!valid_act(src)) {
+        return fail(ctx, QW_ERR_DTYPE, "unknown source dtype %d", (int)src);
+    }
+    return QW_OK;
+}
+
+// Upload one host matrix and pack it into physical tiles t*tile_mul+tile_add.
+static qw_status pack_one(qw_ctx* ctx, qw_weight* W, const void* host, qw_dtype src,
+                          const float* host_scales, int tile_mul, int tile_add) {
+    const size_t bytes = (size_t)W->N * W->K * dsize(src);
+    void* dsrc = nullptr;
+    float* dscales = nullptr;
+    hipError_t e = hipMalloc(&dsrc, bytes);
+    if (e != hipSuccess) return fail(ctx, QW_ERR_NOMEM, "staging hipMalloc failed");
+    e = hipMemcpy(dsrc, host, bytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess && src == QW_I8) {
+        e = hipMalloc(&dscales, (size_t)W->N * sizeof(float));
+        if (e == hipSuccess)
+            e = hipMemcpy(dscales, host_scales, (size_t)W->N * sizeof(float), hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess)
+        e = qwk::launch_pack(dsrc, (int)src, W->wf, dscales, W->N, W->K, W->packed, W->scales,
+                             tile_mul, tile_add, 0);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    hipFree(dsrc);
+    if (dscales) hipFree(dscales);
+    if (e != hipSuccess) return hip_fail(ctx, e, "weight packing");
+    return QW_OK;
+}
+
+qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
+                         const float* scales, qw_weight** out) {
+    if (!out) return fail(ctx, QW_ERR_NULL, "out is NULL");
+    *out = nullptr;
+    qw_status s = check_pack_args(ctx, w, src, dst, N, K, scales);
+    if (s != QW_OK) return s;
+    hipSetDevice(ctx->device);
+    qw_weight* W = nullptr;
+    if ((s = alloc_weight(ctx, dst, N, K, 0, &W)) != QW_OK) return s;
+    if ((s = pack_one(ctx, W, w, src, scales, 1, 0)) != QW_OK) {
+        qw_weight_free(W);
+        return s;
+    }
+    *out = W;
+    return QW_OK;
+}
+
+qw_status qw_weight_pack_glu(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
+                             qw_wfmt dst, int N, int K, const float* gate_scales,
+                             const float* up_scales, qw_weight** out) {
+    if (!out) return fail(ctx, QW_ERR_NULL, "out is NULL");
+    *out = nullptr;
+    qw_status s = check_pack_args(ctx, gate, src, dst, N, K, gate_scales);
+    if (s != QW_OK) return s;
+    if ((s = check_pack_args(ctx, up, src, dst, N, K, up_scales)) != QW_OK) return s;
+    hipSetDevice(ctx->device);
+    qw_weight* W = nullptr;
+    if ((s = alloc_weight(ctx, dst, N, K, 1, &W)) != QW_OK) return s;
+    if ((s = pack_one(ctx, W, gate, src, gate_scales, 2, 0)) != QW_OK ||
+        (s = pack_one(ctx, W, up, src, up_scales, 2, 1)) != QW_OK) {
+        qw_weight_free(W);
+        return s;
+    }
+    *out = W;
+    return QW_OK;
+}
+
+qw_status qw_weight_wrap_packed(qw_ctx* ctx, void* packed, float* scales, qw_wfmt fmt, int N, int K,
+                                qw_weight** out) {
+    if (!ctx || !out) return QW_ERR_NULL;
+    *out = nullptr;
+    if (!packed) return fail(ctx, QW_ERR_NULL, "packed pointer is NULL");
+    if (N < 1 || K < 64 || K % 64 != 0) return fail(ctx, QW_ERR_SHAPE, "bad shape N=%d K=%d", N, K);
+    if (fmt == QW_WFMT_INT8_ROWSCALE && !scales) return fail(ctx, QW_ERR_NULL, "INT8 weight needs scales");
+    if (!aligned(packed, 16) || (scales && !aligned(scales, 16)))
+        return fail(ctx, QW_ERR_ALIGN, "packed data and scales must be 16-byte aligned");
+    qw_weight* W = new qw_weight();
+    W->ctx = ctx;
+    W->N = N;
+    W->K = K;
+    W->wf = fmt;
+    W->glu = 0;
+    W->phys_tiles = (N + 15) / 16;
+    W->ksteps = K / (4 * ke_of(fmt));
+    W->bytes = (size_t)W->phys_tiles * W->ksteps * 1024;
+    W->packed = static_cast<uint8_t*>(packed);
+    W->scales = fmt == QW_WFMT_INT8_ROWSCALE ? scales : nullptr;
+    W->owns = false;
+    *out = W;
+    return QW_OK;
+}
+
+qw_status qw_weight_free(qw_weight* w) {
+    if (!w) return QW_ERR_NULL;
+    if (w->owns) {
+        if (w->packed) hipFree(w->packed);
+        if (w->scales) hipFree(w->scales);
+    }
+    delete w;
+    return QW_OK;
+}
+
+qw_status qw_weight_info(const qw_weight* w, int* N, int* K, qw_wfmt* fmt, int* is_glu,
+                         size_t* packed_bytes) {
+    if (!w) return QW_ERR_NULL;
+    if (N) *N = w->N;
+    if (K) *K = w->K;
+    if (fmt) *fmt = (qw_wfmt)w->wf;
+    if (is_glu) *is_glu = w->glu;
+    if (packed_bytes) *packed_bytes = w->bytes;
+    return QW_OK;
+}
+
+qw_status qw_weight_device_ptrs(const qw_weight* w, const void** packed, const float** scales) {
+    if (!w) return QW_ERR_NULL;
+    if (packed) *packed = w->packed;
+    if (scales) *scales = w->scales;
+    return QW_OK;
+}
+
+qw_status qw_weight_unpack(qw_ctx* ctx, const qw_weight* w, void* dst, float* scales_dst) {
+    if (!ctx || !w) return QW_ERR_NULL;
+    if (!dst) return fail(ctx, QW_ERR_NULL, "dst is NULL");
+    if (w->wf == QW_WFMT_INT8_ROWSCALE && !scales_dst) return fail(ctx, QW_ERR_NULL, "scales_dst is NULL");
+    hipSetDevice(ctx->device);
+    const int parts = w->glu ? 2 : 1;
+    const size_t part_elems = (size_t)w->N * w->K;
+    const int es = esize_of(w->wf);
+    void* d = nullptr;
+    hipError_t e = hipMalloc(&d, part_elems * es);
+    if (e != hipSuccess) return fail(ctx, QW_ERR_NOMEM, "staging hipMalloc failed");
+    for (int p = 0; p < parts && e == hipSuccess; ++p) {
+        e = qwk::launch_unpack(w->packed, w->wf, w->N, w->K, d, parts, p, 0);
+        if (e == hipSuccess)
+            e = hipMemcpy(static_cast<uint8_t*>(dst) + p * part_elems * es, d, part_elems * es,
+                          hipMemcpyDeviceToHost);
+        if (e == hipSuccess && w->wf == QW_WFMT_INT8_ROWSCALE) {
+            // scales of logical tile t live at physical tile t*parts+p
+            const int tiles = (w->N + 15) / 16;
+            for (int t = 0; t < tiles && e == hipSuccess; ++t) {
+                const int rows = std::min(16, w->N - t * 16);
+                e = hipMemcpy(scales_dst + (size_t)p * w->N + t * 16,
+                              w->scales + (size_t)(t * parts + p) * 16, rows * sizeof(float),
+                              hipMemcpyDeviceToHost);
+            }
+        }
+    }
+    hipFree(d);
+    if (e != hipSuccess) return hip_fail(ctx, e, "weight unpack");
+    return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// projections
+// ---------------------------------------------------------------------------
+
+static qw_status check_xdt(qw_ctx* ctx, const qw_weight* W, qw_dtype xdt) {
+    if (!valid_act(xdt)) return fail(ctx, QW_ERR_DTYPE, "activation dtype %d unsupported", (int)xdt);
+    (void)W;
+    return QW_OK;
+}
+
+// Skinny launch for M <= 32 tokens (argmax: ids/maxv set, y ignored).
+static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx,
+                            int M, void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep,
+                            int32_t* ids, float* maxv, hipStream_t stream) {
+    const bool argmax = ids != nullptr;
+    qwk::SkinnyArgs a{};
+    a.w = W->packed;
+    a.scales = W->scales;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = M;
+    a.K = W->K;
+    a.N = W->N;
+    a.n_groups = (W->N + 15) / 16;
+    a.ksteps = W->ksteps;
+    const int target = ctx->num_cus * 8;
+    int S = 1;
+    if (!argmax && a.n_groups < target) {
+        S = (target + a.n_groups - 1) / a.n_groups;
+        S = std::min(S, std::max(1, W->ksteps / 2));
+        S = std::min(S, 64);
+        if (a.n_groups > kMaxCounters) S = 1;
+        const int RT = W->glu ? 2 : 1, CT = M <= 16 ? 1 : 2;
+        while (S > 1 && (size_t)a.n_groups * S * RT * CT * 1024 > ctx->partials_bytes) --S;
+    }
+    a.S = S;
+    a.n_items = a.n_groups * S;
+    a.flags = ep ? ep->flags : 0u;
+    if (ep && (ep->flags & QW_EP_RESIDUAL)) {
+        a.res = ep->residual;
+        a.res_dt = ep->residual_dtype;
+        a.ld_res = ep->ld_residual ? ep->ld_residual : W->N;
+    }
+    if (ep && (ep->flags & QW_EP_NORM_X)) {
+        a.gamma = ep->gamma;
+        a.eps = ep->eps;
+    }
+    a.y = y;
+    a.ydt = ydt;
+    a.ldy = ldy;
+    if (ep && (ep->flags & QW_EP_SPLIT)) {
+        a.y2 = ep->y2;
+        a.split_period = ep->split_period;
+    }
+    bool vec = (W->N % 4 == 0) && (ldy % 4 == 0) && aligned(y, 16);
+    if (a.flags & QW_EP_SPLIT) vec = vec && aligned(a.y2, 16);
+    if (a.flags & QW_EP_RESIDUAL) vec = vec && (a.ld_res % 4 == 0) && aligned(a.res, 16);
+    a.vec_store = vec ? 1 : 0;
+    a.partials = ctx->partials;
+    a.counters = ctx->counters;
+    a.keys = ctx->keys;
+    a.done = ctx->done;
+    a.ids = ids;
+    a.maxv = maxv;
+    const int waves = std::min(a.n_items, target);
+    const int grid = (waves + 3) / 4;
+    hipError_t e = qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, grid, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "skinny kernel launch");
+    return QW_OK;
+}
+
+static qw_status check_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx,
+                              int M, void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep,
+                              bool need_y) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!W) return fail(ctx, QW_ERR_NULL, "weight is NULL");
+    if (!x) return fail(ctx, QW_ERR_NULL, "x is NULL");
+    if (need_y && !y) return fail(ctx, QW_ERR_NULL, "y is NULL");
+    if (M < 1) return fail(ctx, QW_ERR_SHAPE, "M=%d must be >= 1", M);
+    qw_status s = check_xdt(ctx, W, xdt);
+    if (s != QW_OK) return s;
+    if (need_y && !valid_act(ydt)) return fail(ctx, QW_ERR_DTYPE, "output dtype %d unsupported", (int)ydt);
+    if (ldx < W->K) return fail(ctx, QW_ERR_SHAPE, "ldx=%d < K=%d", ldx, W->K);
+    if (!aligned(x, 16) || ((size_t)ldx * dsize(xdt)) % 16 != 0)
+        return fail(ctx, QW_ERR_ALIGN, "x must be 16-byte aligned with 16-byte aligned rows");
+    if (need_y) {
+        if (ldy < W->N && !(ep && (ep->flags & QW_EP_SPLIT)))
+            return fail(ctx, QW_ERR_SHAPE, "ldy=%d < N=%d", ldy, W->N);
+        if (!aligned(y, dsize(ydt))) return fail(ctx, QW_ERR_ALIGN, "y misaligned");
+    }
+    if (ep) {
+        if (ep->flags & ~(unsigned)(QW_EP_RESIDUAL | QW_EP_NORM_X | QW_EP_SPLIT))
+            return fail(ctx, QW_ERR_INVALID, "unknown epilogue flags 0x%x", ep->flags);
+        if (ep->flags & QW_EP_RESIDUAL) {
+            if (!ep->residual) return fail(ctx, QW_ERR_NULL, "residual is NULL");
+            if (!valid_act(ep->residual_dtype)) return fail(ctx, QW_ERR_DTYPE, "residual dtype unsupported");
+            if (!aligned(ep->residual, dsize(ep->residual_dtype))) return fail(ctx, QW_ERR_ALIGN, "residual misaligned");
+            if (ep->ld_residual != 0 && ep->ld_residual < W->N) return fail(ctx, QW_ERR_SHAPE, "ld_residual < N");
+        }
+        if (ep->flags & QW_EP_NORM_X) {
+            if (!ep->gamma) return fail(ctx, QW_ERR_NULL, "gamma is NULL");
+            if (!aligned(ep->gamma, 16)) return fail(ctx, QW_ERR_ALIGN, "gamma must be 16-byte aligned");
+            if (!(ep->eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
+        }
+        if (ep->flags & QW_EP_SPLIT) {
+            if (!ep->y2) return fail(ctx, QW_ERR_NULL, "y2 is NULL");
+            if (ep->split_period < 16 || ep->split_period % 16 != 0 || W->N % (2 * ep->split_period) != 0)
+                return fail(ctx, QW_ERR_SHAPE, "split_period must be a multiple of 16 dividing N/2");
+            if (W->glu) return fail(ctx, QW_ERR_INVALID, "split epilogue not available on GLU weights");
+            if (ldy < W->N / 2) return fail(ctx, QW_ERR_SHAPE, "ldy < N/2");
+        }
+    }
+    return QW_OK;
+}
+
+qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx, int M,
+                    void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep, hipStream_t stream) {
+    if (W && ldx == 0) ldx = W->K;
+    if (W && ldy == 0) ldy = (ep && (ep->flags & QW_EP_SPLIT)) ? W->N / 2 : W->N;
+    qw_status s = check_linear(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, true);
+    if (s != QW_OK) return s;
+    // token chunks of at most 32 for the skinny kernel
+    qw_epilogue e2;
+    if (ep) e2 = *ep;
+    for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {
+        const int mc = std::min(kSkinnyMaxM, M - m0);
+        const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * ldx * dsize(xdt);
+        void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * ldy * dsize(ydt);
+        if (ep) {
+            if (ep->flags & QW_EP_RESIDUAL) {
+                const int ldr = ep->ld_residual ? ep->ld_residual : W->N;
+                e2.residual = static_cast<const uint8_t*>(ep->residual) + (size_t)m0 * ldr * dsize(ep->residual_dtype);
+            }
+            if (ep->flags & QW_EP_SPLIT)
+                e2.y2 = static_cast<uint8_t*>(ep->y2) + (size_t)m0 * ldy * dsize(ydt);
+        }
+        s = run_skinny(ctx, W, xc, xdt, ldx, mc, yc, ydt, ldy, ep ? &e2 : nullptr, nullptr, nullptr, stream);
+        if (s != QW_OK) return s;
+    }
+    return QW_OK;
+}
+
+qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M,
+                           int32_t* token_ids, float* max_logit, hipStream_t stream) {
+    qw_status s = check_linear(ctx, E, h, hdt, E ? E->K : 0, M, nullptr, QW_F32, 0, nullptr, false);
+    if (s != QW_OK) return s;
+    if (!token_ids) return fail(ctx, QW_ERR_NULL, "token_ids is NULL");
+    if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
+    if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
+    for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {
+        const int mc = std::min(kSkinnyMaxM, M - m0);
+        const void* hc = static_cast<const uint8_t*>(h) + (size_t)m0 * E->K * dsize(hdt);
+        s = run_skinny(ctx, E, hc, hdt, E->K, mc, nullptr, QW_F32, 0, nullptr, token_ids + m0,
+                       max_logit ? max_logit + m0 : nullptr, stream);
+        if (s != QW_OK) return s;
+    }
+    return QW_OK;
+}
+
+qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,
+                       qw_dtype xdt, const float* gamma, float eps, const void* residual,
+                       qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!gateup || !down) return fail(ctx, QW_ERR_NULL, "weights are NULL");
+    if (!gateup->glu) return fail(ctx, QW_ERR_INVALID, "gateup must be a GLU weight");
+    if (down->glu) return fail(ctx, QW_ERR_INVALID, "down must not be a GLU weight");
+    const int H = gateup->K, I = gateup->N;
+    if (down->K != I || down->N != H)
+        return fail(ctx, QW_ERR_SHAPE, "down is [%d][%d], expected [%d][%d]", down->N, down->K, H, I);
+    if (M < 1) return fail(ctx, QW_ERR_SHAPE, "M=%d must be >= 1", M);
+    // intermediate h keeps the precision the down projection consumes
+    const qw_dtype hdt = gateup->wf == QW_WFMT_F32 ? QW_F32 : (gateup->wf == QW_WFMT_BF16 ? QW_BF16 : QW_F16);
+    const size_t per_tok = (size_t)I * dsize(hdt);
+    int chunk = (int)std::min<size_t>((size_t)M, ctx->scratch_bytes / per_tok);
+    if (chunk < 1) return fail(ctx, QW_ERR_WORKSPACE, "workspace too small for one token of the MLP");
+    qw_epilogue e1{};
+    if (gamma) {
+        e1.flags = QW_EP_NORM_X;
+        e1.gamma = gamma;
+        e1.eps = eps;
+    }
+    qw_epilogue e2{};
+    if (residual) {
+        e2.flags = QW_EP_RESIDUAL;
+        e2.residual_dtype = residual_dtype;
+    }
+    for (int m0 = 0; m0 < M; m0 += chunk) {
+        const int mc = std::min(chunk, M - m0);
+        const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * H * dsize(xdt);
+        void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * H * dsize(ydt);
+        qw_status s = qw_linear(ctx, gateup, xc, xdt, H, mc, ctx->scratch, hdt, I, gamma ? &e1 : nullptr, stream);
+        if (s != QW_OK) return s;
+        if (residual) e2.residual = static_cast<const uint8_t*>(residual) + (size_t)m0 * H * dsize(residual_dtype);
+        s = qw_linear(ctx, down, ctx->scratch, hdt, I, mc, yc, ydt, H, residual ? &e2 : nullptr, stream);
+        if (s != QW_OK) return s;
+    }
+    return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// norms
+// ---------------------------------------------------------------------------
+
+qw_status qw_rmsnorm(qw_ctx* ctx, const void* x, qw_dtype xdt, const float* gamma, float eps, void* y,
+                     qw_dtype ydt, int M, int K, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!x || !gamma || !y) return fail(ctx, QW_ERR_NULL, "x, gamma and y are required");
+    if (!valid_act(xdt) || !valid_act(ydt)) return fail(ctx, QW_ERR_DTYPE, "dtype unsupported");
+    if (M < 1 || K < 1 || K > 4096) return fail(ctx, QW_ERR_SHAPE, "M=%d K=%d (K <= 4096)", M, K);
+    if (!(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
+    hipError_t e = qwk::launch_rmsnorm(x, xdt, nullptr, nullptr, gamma, eps, y, ydt, M, K, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
+    return QW_OK;
+}
+
+qw_status qw_residual_rmsnorm(qw_ctx* ctx, const void* residual_in, const void* a, qw_dtype dt,
+                              void* residual_out, void* normed, qw_dtype normed_dt,
+                              const float* gamma, float eps, int M, int K, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!residual_in || !a || !residual_out || !normed || !gamma)
+        return fail(ctx, QW_ERR_NULL, "all pointers are required");
+    if (!valid_act(dt) || !valid_act(normed_dt)) return fail(ctx, QW_ERR_DTYPE, "dtype unsupported");
+    if (M < 1 || K < 1 || K > 4096) return fail(ctx, QW_ERR_SHAPE, "M=%d K=%d (K <= 4096)", M, K);
+    if (!(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
+    hipError_t e = qwk::launch_rmsnorm(residual_in, dt, a, residual_out, gamma, eps, normed,
+                                       normed_dt, M, K, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "residual rmsnorm launch");
+    return QW_OK;
+}
+
+qw_status qw_silu_mul(qw_ctx* ctx, const void* g, const void* u, void* h, qw_dtype dt, int64_t n,
+                      hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!g || !u || !h) return fail(ctx, QW_ERR_NULL, "g, u and h are required");
+    if (!valid_act(dt)) return fail(ctx, QW_ERR_DTYPE, "dtype unsupported");
+    if (n < 1) return fail(ctx, QW_ERR_SHAPE, "n must be >= 1");
+    hipError_t e = qwk::launch_silu_mul(g, u, h, dt, n, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "silu_mul launch");
+    return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// graphs
+// ---------------------------------------------------------------------------
+
+qw_status qw_graph_begin(qw_ctx* ctx, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    hipError_t e = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamBeginCapture");
+    return QW_OK;
+}
+
+qw_status qw_graph_end(qw_ctx* ctx, hipStream_t stream, qw_graph** out) {
+    if (!ctx || !out) return QW_ERR_NULL;
+    *out = nullptr;
+    qw_graph* g = new qw_graph();
+    hipError_t e = hipStreamEndCapture(stream, &g->graph);
+    if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        if (g->graph) hipGraphDestroy(g->graph);
+        delete g;
+        return hip_fail(ctx, e, "graph capture");
+    }
+    *out = g;
+    return QW_OK;
+}
+
+qw_status qw_graph_launch(qw_graph* g, hipStream_t stream) {
+    if (!g) return QW_ERR_NULL;
+    return hipGraphLaunch(g->exec, stream) == hipSuccess ? QW_OK : QW_ERR_HIP;
+}
+
+qw_status qw_graph_destroy(qw_graph* g) {
+    if (!g) return QW_ERR_NULL;
+    if (g->exec) hipGraphExecDestroy(g->exec);
+    if (g->graph) hipGraphDestroy(g->graph);
+    delete g;
+    return QW_OK;
+}
+
+}  // extern "C"

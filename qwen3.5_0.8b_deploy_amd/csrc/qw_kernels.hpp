@@ -1,0 +1,62 @@
+// qw_kernels.hpp -- host-visible launch descriptors of the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qwk {
+
+// One skinny (small-M) projection launch.  See qw_skinny.hip.
+struct SkinnyArgs {
+    const uint8_t* w;        // packed weight (tile order)
+    const float* scales;     // per physical row (INT8) or nullptr
+    const void* x;           // activations [M][ldx]
+    int ldx;
+    int M;                   // tokens
+    int K;                   // inputs (multiple of 64)
+    int N;                   // logical output rows (GLU: rows of the pair)
+    int n_groups;            // logical 16-row output tiles
+    int S;                   // k splits per tile
+    int ksteps;              // K / (4*KE)
+    int n_items;             // n_groups * S
+    unsigned flags;          // QW_EP_* bits
+    const void* res;         // residual [M][ld_res]
+    int res_dt;
+    int ld_res;
+    const float* gamma;      // RMSNorm weight [K]
+    float eps;
+    void* y;                 // output [M][ldy]
+    int ydt;
+    int ldy;
+    void* y2;                // split output
+    int split_period;
+    int vec_store;           // 1: 4-wide stores are aligned
+    float4* partials;        // split-K partial tiles
+    unsigned* counters;      // split-K arrival counters, one per tile (self-resetting)
+    unsigned long long* keys;  // argmax keys [M] (self-resetting)
+    unsigned* done;          // argmax completion counter (self-resetting)
+    int32_t* ids;            // argmax ids [M]
+    float* maxv;             // argmax values [M] or nullptr
+};
+
+// wf: 0 F32, 1 BF16, 2 INT8 ; xdt: 0 F32, 1 BF16, 2 F16
+hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int grid,
+                         hipStream_t stream);
+
+// Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
+// Output rows are written to physical tile `tile_of_row(o)` (GLU interleave
+// handled by the caller through tile_mul/tile_add: pt = t*tile_mul+tile_add).
+hipError_t launch_pack(const void* src, int src_dt, int wf, const float* src_scales, int N, int K,
+                       uint8_t* dst, float* dst_scales, int tile_mul, int tile_add,
+                       hipStream_t stream);
+hipError_t launch_unpack(const uint8_t* src, int wf, int n_rows, int K, void* dst,
+                         int tile_mul, int tile_add, hipStream_t stream);
+
+// RMSNorm family (qw_norm.hip)
+hipError_t launch_rmsnorm(const void* x, int xdt, const void* add, void* sum_out,
+                          const float* gamma, float eps, void* y, int ydt, int M, int K,
+                          hipStream_t stream);
+hipError_t launch_silu_mul(const void* g, const void* u, void* h, int dt, int64_t n,
+                           hipStream_t stream);
+
+}  // namespace qwk

@@ -1,0 +1,316 @@
+"""Python binding of the MI355X projection library (libqw_linear.so, C ABI in
+include/qw_linear.h).
+
+The library is the product; this module is a thin ctypes layer so tests,
+bench.py and Python callers can drive it.  Device memory and streams come from
+PyTorch (tensor.data_ptr(), torch.cuda.current_stream().cuda_stream); nothing
+here computes on the host.  If the library is not built the import of `lib()`
+raises -- there is no fallback path.
+
+Load this file by path (the package directory name contains dots):
+    spec = importlib.util.spec_from_file_location("qw", ".../qw.py")
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqw_linear.so")
+
+# enums (include/qw_linear.h)
+OK, ERR_INVALID, ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP, ERR_NOMEM, ERR_STATE = range(10)
+F32, BF16, F16, I8 = 0, 1, 2, 3
+WFMT_F32, WFMT_BF16, WFMT_INT8 = 0, 1, 2
+EP_RESIDUAL, EP_NORM_X, EP_SPLIT = 1, 2, 4
+
+# every symbol include/qw_linear.h declares
+EXPORTS = [
+    "qw_init", "qw_destroy", "qw_workspace_query", "qw_last_error", "qw_status_string",
+    "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_wrap_packed",
+    "qw_weight_free", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
+    "qw_linear", "qw_mlp_fused", "qw_lmhead_argmax", "qw_rmsnorm", "qw_residual_rmsnorm",
+    "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
+]
+
+
+class Epilogue(ctypes.Structure):
+    _fields_ = [
+        ("flags", ctypes.c_uint),
+        ("residual", ctypes.c_void_p),
+        ("residual_dtype", ctypes.c_int),
+        ("ld_residual", ctypes.c_int),
+        ("gamma", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("split_period", ctypes.c_int),
+        ("y2", ctypes.c_void_p),
+    ]
+
+
+class QwError(RuntimeError):
+    def __init__(self, status, msg):
+        super().__init__(f"qw status {status}: {msg}")
+        self.status = status
+
+
+_LIB = None
+_vp, _i, _sz, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+
+
+def lib():
+    """Load libqw_linear.so (raises if it was not built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built: run __graft_entry__.build() first")
+    L = ctypes.CDLL(LIB_PATH)
+    pp = ctypes.POINTER(ctypes.c_void_p)
+    sigs = {
+        "qw_init": ([pp, _i, _sz], _i),
+        "qw_destroy": ([_vp], _i),
+        "qw_workspace_query": ([_i, _i, _i], _sz),
+        "qw_last_error": ([_vp], ctypes.c_char_p),
+        "qw_status_string": ([_i], ctypes.c_char_p),
+        "qw_abi_version": ([], _i),
+        "qw_weight_pack": ([_vp, _vp, _i, _i, _i, _i, _vp, pp], _i),
+        "qw_weight_pack_glu": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, pp], _i),
+        "qw_weight_wrap_packed": ([_vp, _vp, _vp, _i, _i, _i, pp], _i),
+        "qw_weight_free": ([_vp], _i),
+        "qw_weight_info": ([_vp, _vp, _vp, _vp, _vp, _vp], _i),
+        "qw_weight_device_ptrs": ([_vp, _vp, _vp], _i),
+        "qw_weight_unpack": ([_vp, _vp, _vp, _vp], _i),
+        "qw_linear": ([_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, ctypes.POINTER(Epilogue), _vp], _i),
+        "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
+        "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+        "qw_rmsnorm": ([_vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _vp], _i),
+        "qw_residual_rmsnorm": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _f, _i, _i, _vp], _i),
+        "qw_silu_mul": ([_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp], _i),
+        "qw_graph_begin": ([_vp, _vp], _i),
+        "qw_graph_end": ([_vp, _vp, pp], _i),
+        "qw_graph_launch": ([_vp, _vp], _i),
+        "qw_graph_destroy": ([_vp], _i),
+    }
+    for name, (args, res) in sigs.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _LIB = L
+    return L
+
+
+def _np_dtype_code(a):
+    if a.dtype == np.float32:
+        return F32
+    if a.dtype == np.int8:
+        return I8
+    raise TypeError(f"unsupported host dtype {a.dtype}; pass float32, int8, or (bits, code)")
+
+
+def _torch_code(t):
+    import torch
+    return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}[t.dtype]
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if hasattr(stream, "cuda_stream"):
+        return ctypes.c_void_p(stream.cuda_stream)
+    return ctypes.c_void_p(stream)
+
+
+class Context:
+    """qw_ctx: one per stream; owns the workspace arena."""
+
+    def __init__(self, device=0, workspace_bytes=0):
+        self._h = ctypes.c_void_p()
+        st = lib().qw_init(ctypes.byref(self._h), device, workspace_bytes)
+        if st != OK:
+            raise QwError(st, lib().qw_status_string(st).decode())
+
+    @property
+    def handle(self):
+        return self._h
+
+    def check(self, st):
+        if st != OK:
+            raise QwError(st, lib().qw_last_error(self._h).decode())
+
+    def close(self):
+        if self._h:
+            lib().qw_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Weight:
+    """qw_weight: packed device weight owned by the library."""
+
+    def __init__(self, ctx, handle):
+        self.ctx = ctx
+        self._h = handle
+        N, K, fmt, glu, nbytes = _i(), _i(), _i(), _i(), _sz()
+        lib().qw_weight_info(handle, ctypes.byref(N), ctypes.byref(K), ctypes.byref(fmt),
+                             ctypes.byref(glu), ctypes.byref(nbytes))
+        self.N, self.K, self.fmt, self.glu, self.nbytes = N.value, K.value, fmt.value, glu.value, nbytes.value
+
+    @property
+    def handle(self):
+        return self._h
+
+    @staticmethod
+    def _src(w, src_code):
+        if src_code is None:
+            w = np.ascontiguousarray(w)
+            src_code = _np_dtype_code(w)
+        else:
+            w = np.ascontiguousarray(w)
+        return w, src_code
+
+    @classmethod
+    def pack(cls, ctx, w, fmt, scales=None, src_code=None):
+        """w: host W[N][K] float32 / int8 (with scales) / uint16 bits + src_code (BF16 or F16)."""
+        w, src = cls._src(w, src_code)
+        N, K = w.shape
+        sc = None if scales is None else np.ascontiguousarray(scales, dtype=np.float32)
+        h = ctypes.c_void_p()
+        ctx.check(lib().qw_weight_pack(ctx.handle, w.ctypes.data, src, fmt, N, K,
+                                       None if sc is None else sc.ctypes.data, ctypes.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def pack_glu(cls, ctx, gate, up, fmt, gate_scales=None, up_scales=None, src_code=None):
+        gate, src = cls._src(gate, src_code)
+        up, _ = cls._src(up, src_code)
+        N, K = gate.shape
+        gs = None if gate_scales is None else np.ascontiguousarray(gate_scales, dtype=np.float32)
+        us = None if up_scales is None else np.ascontiguousarray(up_scales, dtype=np.float32)
+        h = ctypes.c_void_p()
+        ctx.check(lib().qw_weight_pack_glu(ctx.handle, gate.ctypes.data, up.ctypes.data, src, fmt, N, K,
+                                           None if gs is None else gs.ctypes.data,
+                                           None if us is None else us.ctypes.data, ctypes.byref(h)))
+        return cls(ctx, h)
+
+    def unpack(self):
+        """Stored values as (W rows [parts*N][K] in stored dtype, scales or None)."""
+        parts = 2 if self.glu else 1
+        dt = {WFMT_F32: np.float32, WFMT_BF16: np.uint16, WFMT_INT8: np.int8}[self.fmt]
+        out = np.empty((parts * self.N, self.K), dt)
+        sc = np.empty(parts * self.N, np.float32) if self.fmt == WFMT_INT8 else None
+        self.ctx.check(lib().qw_weight_unpack(self.ctx.handle, self._h, out.ctypes.data,
+                                              None if sc is None else sc.ctypes.data))
+        return out, sc
+
+    def device_ptrs(self):
+        p, s = ctypes.c_void_p(), ctypes.c_void_p()
+        lib().qw_weight_device_ptrs(self._h, ctypes.byref(p), ctypes.byref(s))
+        return p.value, s.value
+
+    def free(self):
+        if self._h:
+            lib().qw_weight_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def linear(ctx, W, x, y, residual=None, gamma=None, eps=1e-6, y2=None, split_period=0,
+           ldx=0, ldy=0, stream=None):
+    """y = W.x (+ epilogue) on torch device tensors x [M][>=K], y [M][>=N]."""
+    ep = Epilogue()
+    use_ep = False
+    if residual is not None:
+        ep.flags |= EP_RESIDUAL
+        ep.residual = residual.data_ptr()
+        ep.residual_dtype = _torch_code(residual)
+        ep.ld_residual = residual.stride(0) if residual.dim() == 2 else 0
+        use_ep = True
+    if gamma is not None:
+        ep.flags |= EP_NORM_X
+        ep.gamma = gamma.data_ptr()
+        ep.eps = eps
+        use_ep = True
+    if y2 is not None:
+        ep.flags |= EP_SPLIT
+        ep.y2 = y2.data_ptr()
+        ep.split_period = split_period
+        use_ep = True
+    M = x.shape[0] if x.dim() == 2 else 1
+    ldx = ldx or (x.stride(0) if x.dim() == 2 else 0)
+    ldy = ldy or (y.stride(0) if y.dim() == 2 else 0)
+    ctx.check(lib().qw_linear(ctx.handle, W.handle, _ptr(x), _torch_code(x), ldx, M, _ptr(y),
+                              _torch_code(y), ldy, ctypes.byref(ep) if use_ep else None, _stream(stream)))
+
+
+def mlp_fused(ctx, gateup, down, x, y, gamma=None, eps=1e-6, residual=None, stream=None):
+    M = x.shape[0] if x.dim() == 2 else 1
+    ctx.check(lib().qw_mlp_fused(ctx.handle, gateup.handle, down.handle, _ptr(x), _torch_code(x),
+                                 _ptr(gamma), eps, _ptr(residual),
+                                 _torch_code(residual) if residual is not None else F32,
+                                 _ptr(y), _torch_code(y), M, _stream(stream)))
+
+
+def lmhead_argmax(ctx, E, h, ids, max_logit=None, stream=None):
+    M = h.shape[0] if h.dim() == 2 else 1
+    ctx.check(lib().qw_lmhead_argmax(ctx.handle, E.handle, _ptr(h), _torch_code(h), M, _ptr(ids),
+                                     _ptr(max_logit), _stream(stream)))
+
+
+def rmsnorm(ctx, x, gamma, y, eps=1e-6, stream=None):
+    M, K = x.shape
+    ctx.check(lib().qw_rmsnorm(ctx.handle, _ptr(x), _torch_code(x), _ptr(gamma), eps, _ptr(y),
+                               _torch_code(y), M, K, _stream(stream)))
+
+
+def residual_rmsnorm(ctx, residual_in, a, residual_out, normed, gamma, eps=1e-6, stream=None):
+    M, K = residual_in.shape
+    ctx.check(lib().qw_residual_rmsnorm(ctx.handle, _ptr(residual_in), _ptr(a), _torch_code(residual_in),
+                                        _ptr(residual_out), _ptr(normed), _torch_code(normed),
+                                        _ptr(gamma), eps, M, K, _stream(stream)))
+
+
+def silu_mul(ctx, g, u, h, stream=None):
+    ctx.check(lib().qw_silu_mul(ctx.handle, _ptr(g), _ptr(u), _ptr(h), _torch_code(g), g.numel(),
+                                _stream(stream)))
+
+
+class Graph:
+    """Capture qw_* calls on a stream and replay them."""
+
+    def __init__(self, ctx, stream):
+        self.ctx, self.stream, self._h = ctx, stream, ctypes.c_void_p()
+
+    def __enter__(self):
+        self.ctx.check(lib().qw_graph_begin(self.ctx.handle, _stream(self.stream)))
+        return self
+
+    def __exit__(self, *exc):
+        self.ctx.check(lib().qw_graph_end(self.ctx.handle, _stream(self.stream), ctypes.byref(self._h)))
+        return False
+
+    def launch(self, stream=None):
+        st = lib().qw_graph_launch(self._h, _stream(stream if stream is not None else self.stream))
+        if st != OK:
+            raise QwError(st, "graph launch failed")
+
+    def __del__(self):
+        try:
+            if self._h:
+                lib().qw_graph_destroy(self._h)
+        except Exception:
+            pass

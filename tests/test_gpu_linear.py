@@ -1,0 +1,323 @@
+"""GPU parity of the projection kernels (qw_linear, qw_weight_pack) against the
+CPU oracle.
+
+Bars (written next to each check):
+  * packing: bit-exact (BF16 bits, INT8 values and scales vs the oracle's
+    restatement of mlp_cuda.cu:22-39);
+  * FP32 weights x FP32 activations: <= 1e-5 normwise vs FP64;
+  * products on the exact stored operands (bf16/int8 weights, the activation
+    as stored): <= 2e-5 normwise vs FP64 for FP32 outputs (catches any
+    dropped/misplaced term: one wrong k is an O(1/sqrt(K)) error);
+  * BF16 paths <= 1e-2 vs FP64 on the unrounded FP32 weights,
+    INT8 paths <= 1e-3 vs the reference's dequant-then-matmul.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+XDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def stored_x(x, name):
+    """The activation values the GPU actually sees (rounded to its dtype)."""
+    return host(dev(x, XDT[name]))
+
+
+# ----------------------------------------------------------------------------
+# packing
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N,K", [(40, 128), (16, 64), (3584, 1024)])
+def test_pack_roundtrip(qw, ctx, oracle, N, K):
+    W = oracle.normal((N, K), 11, 0.0, 0.02)
+    w32 = qw.Weight.pack(ctx, W, qw.WFMT_F32)
+    got, _ = w32.unpack()
+    assert np.array_equal(got, W)
+    wbf = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    got, _ = wbf.unpack()
+    assert np.array_equal(got, oracle.to_bf16(W))          # bit-exact RNE
+    wi8 = qw.Weight.pack(ctx, W, qw.WFMT_INT8)
+    q, s = wi8.unpack()
+    q_ref, s_ref = oracle.quantize_rowscale(W)
+    assert np.array_equal(s, s_ref)                          # bit-exact scales
+    assert np.array_equal(q, q_ref)                          # bit-exact codes
+
+
+def test_pack_int8_edge_rows(qw, ctx, oracle):
+    """Zero row (scale 1.0), a row whose max is tiny (<= 1e-8*127), exact
+    .5 ties (roundf rounds half away from zero), and +-max clamping."""
+    K = 64
+    W = np.zeros((4, K), np.float32)
+    W[1, :] = 1e-9
+    W[2, :] = np.linspace(-127, 127, K).astype(np.float32)
+    W[2, 0] = 2.5; W[2, 1] = -2.5; W[2, 2] = 0.5; W[2, 3] = -0.5
+    W[3, :] = oracle.normal((K,), 5, 0.0, 3.0)
+    q, s = qw.Weight.pack(ctx, W, qw.WFMT_INT8).unpack()
+    q_ref, s_ref = oracle.quantize_rowscale(W)
+    assert s[0] == 1.0 and s[1] == 1.0
+    assert np.array_equal(q, q_ref) and np.array_equal(s, s_ref)
+    assert q[2, 0] == 3 and q[2, 1] == -3 and q[2, 2] == 1 and q[2, 3] == -1
+
+
+def test_pack_prequantized(qw, ctx, oracle):
+    N, K = 48, 192
+    q = oracle.int8_uniform((N, K), 3)
+    s = oracle.uniform((N,), 4, 1e-3, 2e-2)
+    q2, s2 = qw.Weight.pack(ctx, q, qw.WFMT_INT8, scales=s).unpack()
+    assert np.array_equal(q2, q) and np.array_equal(s2, s)
+
+
+def test_pack_glu_roundtrip(qw, ctx, oracle):
+    N, K = 48, 128
+    G = oracle.normal((N, K), 1, 0.0, 0.02)
+    U = oracle.normal((N, K), 2, 0.0, 0.02)
+    w = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_INT8)
+    q, s = w.unpack()
+    qg, sg = oracle.quantize_rowscale(G)
+    qu, su = oracle.quantize_rowscale(U)
+    assert np.array_equal(q[:N], qg) and np.array_equal(q[N:], qu)
+    assert np.array_equal(s[:N], sg) and np.array_equal(s[N:], su)
+
+
+# ----------------------------------------------------------------------------
+# closed forms: these fail for a transposed operand or a wrong k permutation
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", ["f32", "bf16", "int8"])
+def test_identity_and_onehot(qw, ctx, oracle, fmt):
+    K = 128
+    f = {"f32": qw.WFMT_F32, "bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
+    W = np.eye(K, dtype=np.float32)
+    w = qw.Weight.pack(ctx, W, f)
+    x = np.round(oracle.normal((3, K), 7) * 8) / 8          # exact in bf16/f16
+    xt = dev(x, torch.float32)
+    y = torch.empty(3, K, device="cuda")
+    qw.linear(ctx, w, xt, y)
+    torch.cuda.synchronize()
+    if fmt == "int8":                                        # q = 127*I, s = 1/127
+        q, s = w.unpack()
+        assert np.array_equal(host(y), (x * np.float32(127)) * s[None, :])
+    else:
+        assert np.array_equal(host(y), x)                    # W = I  =>  y = x
+    # one-hot x picks a column of W
+    N = 80
+    W2 = np.round(oracle.normal((N, K), 8) * 64) / 64
+    w2 = qw.Weight.pack(ctx, W2, f)
+    scale = w2.unpack()[1]
+    for k in (0, 1, 7, 8, 31, 32, 63, 64, 127):
+        e = np.zeros((1, K), np.float32)
+        e[0, k] = 1.0
+        y2 = torch.empty(1, N, device="cuda")
+        qw.linear(ctx, w2, dev(e), y2)
+        torch.cuda.synchronize()
+        if fmt == "int8":
+            qcol = w2.unpack()[0][:, k].astype(np.float32) * scale
+            assert np.array_equal(host(y2)[0], qcol)
+        else:
+            assert np.array_equal(host(y2)[0], W2[:, k])
+
+
+# ----------------------------------------------------------------------------
+# parity on random inputs
+# ----------------------------------------------------------------------------
+
+SHAPES = [(3584, 1024), (1024, 3584), (40, 128), (16, 1024)]
+
+
+def _exact_ref(oracle, fmt, W, wobj, xs):
+    """FP64 product on the exact operands the GPU uses."""
+    if fmt == "int8":
+        q, s = wobj.unpack()
+        return oracle.linear_int8_f64(q, s, xs)
+    if fmt == "bf16":
+        return oracle.linear_f64(oracle.round_bf16(W), xs)
+    return oracle.linear_f64(W, xs)
+
+
+@pytest.mark.parametrize("fmt,xname", [
+    ("f32", "f32"), ("f32", "bf16"),
+    ("bf16", "bf16"), ("bf16", "f32"), ("bf16", "f16"),
+    ("int8", "f16"), ("int8", "bf16"), ("int8", "f32"),
+])
+@pytest.mark.parametrize("M", [1, 7, 16, 32, 45])
+def test_linear_parity(qw, ctx, oracle, relerr, fmt, xname, M):
+    f = {"f32": qw.WFMT_F32, "bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
+    for si, (N, K) in enumerate(SHAPES):
+        if M > 16 and si == 0 and fmt == "f32":
+            continue  # keep the FP64 reference cheap
+        W = oracle.normal((N, K), 100 + si, 0.0, 0.02)
+        x = oracle.normal((M, K), 200 + si + M)
+        w = qw.Weight.pack(ctx, W, f)
+        xt = dev(x, XDT[xname])
+        y = torch.empty(M, N, device="cuda")
+        qw.linear(ctx, w, xt, y)
+        torch.cuda.synchronize()
+        got = host(y)
+        xs = stored_x(x, xname)
+        ref = _exact_ref(oracle, fmt, W, w, xs)
+        # exact operands: only FP32 accumulation error remains, except for the
+        # hi/lo bf16 split of an FP32 activation (16 of its 24 bits kept)
+        tol = 1e-4 if (fmt == "bf16" and xname == "f32") else 2e-5
+        assert relerr(got, ref) <= tol, (N, K, M, relerr(got, ref))
+        # north-star bars
+        if fmt == "bf16":
+            assert relerr(got, oracle.linear_f64(W, xs)) <= 1e-2
+        if fmt == "int8":
+            q, s = w.unpack()
+            assert relerr(got, oracle.linear_int8(q, s, xs)) <= 1e-3
+        if fmt == "f32" and xname == "f32":
+            assert relerr(got, oracle.linear_f64(W, x)) <= 1e-5
+
+
+@pytest.mark.parametrize("ydt", ["bf16", "f16"])
+def test_linear_output_dtypes(qw, ctx, oracle, relerr, ydt):
+    N, K, M = 1024, 2048, 4
+    W = oracle.normal((N, K), 31, 0.0, 0.02)
+    x = oracle.normal((M, K), 32)
+    w = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    y = torch.empty(M, N, device="cuda", dtype=XDT[ydt])
+    qw.linear(ctx, w, dev(x, torch.bfloat16), y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W), stored_x(x, "bf16"))
+    assert relerr(host(y), ref) <= 4e-3                     # one output rounding
+
+
+def test_linear_deterministic(qw, ctx, oracle):
+    """Split-K partials are summed in split order: bitwise repeatable."""
+    N, K, M = 1024, 3584, 3
+    w = qw.Weight.pack(ctx, oracle.normal((N, K), 41, 0.0, 0.02), qw.WFMT_BF16)
+    x = dev(oracle.normal((M, K), 42), torch.bfloat16)
+    outs = []
+    for _ in range(3):
+        y = torch.empty(M, N, device="cuda")
+        qw.linear(ctx, w, x, y)
+        torch.cuda.synchronize()
+        outs.append(host(y))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+
+
+# ----------------------------------------------------------------------------
+# epilogues
+# ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("M", [1, 20])
+@pytest.mark.parametrize("rdt", ["f32", "bf16"])
+def test_residual_epilogue(qw, ctx, oracle, relerr, M, rdt):
+    N, K = 1024, 2048                                        # out-proj shape
+    W = oracle.normal((N, K), 51, 0.0, 0.02)
+    x = oracle.normal((M, K), 52)
+    r = oracle.normal((M, N), 53)
+    w = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    res = dev(r, XDT[rdt])
+    y = res.clone() if rdt == "f32" else torch.empty(M, N, device="cuda")
+    # in place when the residual is FP32 (y aliases residual)
+    qw.linear(ctx, w, dev(x, torch.bfloat16), y, residual=(y if rdt == "f32" else res))
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W), stored_x(x, "bf16")) + host(res)
+    assert relerr(host(y), ref) <= 2e-5
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "f32"])
+@pytest.mark.parametrize("M", [1, 9, 32])
+def test_norm_prologue(qw, ctx, oracle, relerr, fmt, M):
+    """x := RMSNorm(x)*(1+gamma) folded into the projection."""
+    N, K = 512, 1024
+    f = {"f32": qw.WFMT_F32, "bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
+    W = oracle.normal((N, K), 61, 0.0, 0.02)
+    gamma = oracle.normal((K,), 62, 0.0, 0.02)
+    x = oracle.normal((M, K), 63) * 3.0
+    w = qw.Weight.pack(ctx, W, f)
+    xname = {"bf16": "bf16", "int8": "f16", "f32": "f32"}[fmt]
+    xt = dev(x, XDT[xname])
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(ctx, w, xt, y, gamma=dev(gamma), eps=1e-6)
+    torch.cuda.synchronize()
+    xs = stored_x(x, xname)
+    xn = oracle.rmsnorm_f64(xs, gamma)
+    if fmt == "int8":
+        q, s = w.unpack()
+        ref = (xn @ q.astype(np.float64).T) * s.astype(np.float64)
+        bar = 1e-3
+    elif fmt == "bf16":
+        ref = xn @ oracle.round_bf16(W).astype(np.float64).T
+        bar = 1e-2
+    else:
+        ref = xn @ W.astype(np.float64).T
+        bar = 1e-5
+    assert relerr(host(y), ref) <= bar
+
+
+def test_split_q_gate(qw, ctx, oracle):
+    """Full-attention q_proj [2*8*256][1024]: per head, rows [h*512, h*512+256)
+    are Q and the next 256 the output gate (language_full_attn.cpp:133-140)."""
+    heads, D, K, M = 8, 256, 1024, 3
+    W = oracle.normal((2 * heads * D, K), 71, 0.0, 0.02)
+    x = oracle.normal((M, K), 72)
+    w = qw.Weight.pack(ctx, W, qw.WFMT_F32)
+    q = torch.empty(M, heads * D, device="cuda")
+    g = torch.empty(M, heads * D, device="cuda")
+    qw.linear(ctx, w, dev(x), q, y2=g, split_period=D)
+    full = torch.empty(M, 2 * heads * D, device="cuda")
+    qw.linear(ctx, w, dev(x), full)
+    torch.cuda.synchronize()
+    q_ref, g_ref = oracle.split_q_gate(host(full), heads, D)
+    assert np.array_equal(host(q), q_ref) and np.array_equal(host(g), g_ref)
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "f32"])
+@pytest.mark.parametrize("M", [1, 16, 24])
+def test_glu_silu_mul(qw, ctx, oracle, relerr, fmt, M):
+    I, H = 3584, 1024
+    f = {"f32": qw.WFMT_F32, "bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
+    G = oracle.normal((I, H), 81, 0.0, 0.02)
+    U = oracle.normal((I, H), 82, 0.0, 0.02)
+    x = oracle.normal((M, H), 83)
+    w = qw.Weight.pack_glu(ctx, G, U, f)
+    xname = {"bf16": "bf16", "int8": "f16", "f32": "f32"}[fmt]
+    h = torch.empty(M, I, device="cuda")
+    qw.linear(ctx, w, dev(x, XDT[xname]), h)
+    torch.cuda.synchronize()
+    xs = stored_x(x, xname).astype(np.float64)
+    if fmt == "int8":
+        q, s = w.unpack()
+        g = (xs @ q[:I].astype(np.float64).T) * s[:I]
+        u = (xs @ q[I:].astype(np.float64).T) * s[I:]
+    elif fmt == "bf16":
+        g = xs @ oracle.round_bf16(G).astype(np.float64).T
+        u = xs @ oracle.round_bf16(U).astype(np.float64).T
+    else:
+        g = xs @ G.astype(np.float64).T
+        u = xs @ U.astype(np.float64).T
+    ref = g / (1.0 + np.exp(-g)) * u
+    assert relerr(host(h), ref) <= 1e-4
+
+
+def test_error_codes(qw, ctx, oracle):
+    W = oracle.normal((64, 128), 1, 0.0, 0.02)
+    w = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    x = torch.zeros(2, 128, device="cuda", dtype=torch.bfloat16)
+    y = torch.zeros(2, 64, device="cuda")
+    with pytest.raises(qw.QwError) as e:
+        qw.linear(ctx, w, x[:, 1:], y, ldx=128)             # misaligned x
+    assert e.value.status == qw.ERR_ALIGN
+    with pytest.raises(qw.QwError) as e:
+        qw.Weight.pack(ctx, oracle.normal((8, 100), 1), qw.WFMT_BF16)   # K % 64
+    assert e.value.status == qw.ERR_SHAPE
+    with pytest.raises(qw.QwError) as e:
+        qw.Weight.pack(ctx, oracle.int8_uniform((8, 64), 1), qw.WFMT_INT8)  # no scales
+    assert e.value.status == qw.ERR_NULL
+    with pytest.raises(qw.QwError) as e:
+        qw.linear(ctx, w, x, y, gamma=torch.zeros(128, device="cuda"), eps=0.0)
+    assert e.value.status == qw.ERR_INVALID
