@@ -1,0 +1,383 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X projection path (one GPU).
+
+Headline workload (decode M=1): one decode step of
+the fused MLP block -- RMSNorm(1+w) prologue, gate/up GEMV with SiLU*mul,
+down GEMV with residual add -- for all 24 layers of Qwen3.5-0.8B, BF16
+weights N(0,0.02) random-initialised per layer, BF16 activations, FP32
+accumulate.  24 distinct layers (528 MB of weights) exceed the 256 MB
+Infinity Cache, so every step streams the weights from HBM.  The step is
+captured once in a HIP graph and replayed.
+
+value = algorithmic bytes of the step / step time (GB/s), with
+  per layer: W 22,020,096 B + x M*1024*2 + y M*1024*2 + gamma 1024*4.
+roofline: the dominant kernel (the fused gate/up GEMV, 14.68 MB of weights
+per launch) timed with HIP events around each launch on its own stream.
+cpu_baseline: the reference's own MLP::forward_batch (oracle/_ref, compiled
+from the reference sources; FP32, 1 thread) on a bounded sample, expressed
+in the same algorithmic-bytes unit.  Falls back to the oracle port when
+oracle/_ref is absent.
+
+Sub-measurements for the other BASELINE configs are reported under "extra".
+"""
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "qwen3.5_0.8b_deploy_amd")
+HBM_PEAK = 8000.0        # GB/s, MI355X
+BF16_PEAK = 2500.0       # TFLOP/s dense
+H, I, V = 1024, 3584, 248320
+LAYERS = 24
+LINEAR_LAYERS = [i for i in range(24) if i % 4 != 3]   # 18 Gated-DeltaNet layers
+METRIC = "decode GEMV HBM GB/s (% of peak) at M=1; prefill GEMM TFLOPS (% MFMA peak)"
+
+
+def load_qw():
+    spec = importlib.util.spec_from_file_location("qw", os.path.join(PKG, "qw.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """HIP-event timing of a callable replayed `steps` times on `stream`."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(self.stream)
+            for _ in range(steps):
+                fn()
+            t1.record(self.stream)
+            torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps   # ms per step
+
+
+def graphed(qw, ctx, stream, body):
+    """Capture body() into a HIP graph (through the library's graph API)."""
+    import torch
+    with torch.cuda.stream(stream):
+        body()                               # one eager pass first
+        torch.cuda.synchronize()
+        g = qw.Graph(ctx, stream)
+        with g:
+            body()
+    return g
+
+
+def mlp_bytes(M):
+    return 3 * H * I * 2 + M * H * 2 * 2 + H * 4
+
+
+def gateup_bytes(M):
+    return 2 * H * I * 2 + M * H * 2 + M * I * 2 + H * 4
+
+
+def cpu_baseline(oracle):
+    """Reference CPU MLP (1 thread) on a bounded sample of the same workload."""
+    ref = oracle.ref_lib()
+    Wg = oracle.normal((I, H), 1, 0.0, 0.02)
+    Wu = oracle.normal((I, H), 2, 0.0, 0.02)
+    Wd = oracle.normal((H, I), 3, 0.0, 0.02)
+    x = oracle.normal((1, H), 4)
+    y = np.empty((1, H), np.float32)
+    if ref is not None:
+        t1 = ref.ref_mlp_time(Wg, Wu, Wd, x, y, 1, H, I, 1)
+        iters = max(1, min(2000, int(10.0 / max(t1, 1e-4))))
+        secs = ref.ref_mlp_time(Wg, Wu, Wd, x, y, 1, H, I, iters)
+        kind = "reference"
+        what = "qwen::MLP::forward_batch (reference language_mlp.cpp, built -O2 by oracle/Makefile)"
+    else:
+        t0 = time.perf_counter(); oracle.mlp(Wg, Wu, Wd, x); t1 = time.perf_counter() - t0
+        iters = max(1, min(2000, int(10.0 / max(t1, 1e-4))))
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            oracle.mlp(Wg, Wu, Wd, x)
+        secs = time.perf_counter() - t0
+        kind = "port"
+        what = "orc_mlp (oracle restatement of language_mlp.cpp:53-91)"
+    per = secs / iters
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(mlp_bytes(1) / per / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"{iters} MLP blocks at M=1 (H=1024, I=3584, FP32 weights) in {secs:.1f} s "
+                   f"= {per * 1e3:.2f} ms/block via {what}; RMSNorm+residual not included; "
+                   f"host {cpu_model!r}, nproc={os.cpu_count()}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(requested --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    qw = load_qw()
+    torch.cuda.set_device(0)
+    ctx = qw.Context(0)
+    stream = torch.cuda.Stream()
+    timer = Timer(torch, stream)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+
+    def randn(*shape, std=1.0, dtype=torch.bfloat16):
+        return (torch.randn(*shape, generator=gen, device="cuda") * std).to(dtype)
+
+    # ---------------- headline: 24-layer fused MLP decode step, BF16, M=1 ----
+    log("building 24 BF16 MLP layers ...")
+    gu, dn, gam = [], [], []
+    for _ in range(LAYERS):
+        g, u = randn(I, H, std=0.02), randn(I, H, std=0.02)
+        gu.append(qw.Weight.pack_glu_device(ctx, g, u, qw.WFMT_BF16))
+        d = randn(H, I, std=0.02)
+        dn.append(qw.Weight.pack_device(ctx, d, qw.WFMT_BF16))
+        gam.append(randn(H, std=0.02, dtype=torch.float32))
+        del g, u, d
+    torch.cuda.synchronize()
+
+    def mlp_step(hbuf, M):
+        def body():
+            for l in range(LAYERS):
+                qw.mlp_fused(ctx, gu[l], dn[l], hbuf, hbuf, gamma=gam[l], residual=hbuf)
+        return body
+
+    h1 = randn(1, H)
+    g_mlp = graphed(qw, ctx, stream, mlp_step(h1, 1))
+    ms = timer.run(g_mlp.launch, args.steps, args.warmup)
+    step_bytes = LAYERS * mlp_bytes(1)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    log(f"headline: {ms * 1e3:.1f} us/step, {value:.0f} GB/s")
+
+    # dominant kernel: gate/up GLU GEMV, events around each launch
+    hmid = torch.empty(1, I, device="cuda", dtype=torch.bfloat16)
+    evs = []
+    with torch.cuda.stream(stream):
+        for it in range(args.warmup + args.steps):
+            for l in range(LAYERS):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l])
+                e1.record(stream)
+                qw.linear(ctx, dn[l], hmid, h1, residual=h1)
+                if it >= args.warmup:
+                    evs.append((e0, e1))
+        torch.cuda.synchronize()
+    k_us = 1e3 * float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    k_bytes = gateup_bytes(1)
+    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
+    log(f"gate/up kernel: {k_us:.2f} us avg, {k_gbs:.0f} GB/s")
+
+    extra = {}
+    if not args.quick:
+        extra = run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args)
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        log("cpu baseline ...")
+        cpu = cpu_baseline(oracle)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations; random init, no checkpoint)",
+        "config": {
+            "workload": "fused MLP block decode step (RMSNorm+gate/up+SiLU*mul+down+residual), "
+                        "24 Qwen3.5-0.8B layers, BF16 weights, M=1 (BASELINE configs[1]); HIP graph replay",
+            "global_batch": 1, "seq_len": 1, "hidden": H, "intermediate": I, "layers": LAYERS,
+            "bytes_per_step": step_bytes, "pct_of_hbm_peak": round(100 * value / HBM_PEAK, 2),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "qwk::skinny_kernel<BF16 weights, BF16 x, CT=1, GLU> (fused RMSNorm+gate/up+SiLU*mul)",
+            "achieved": round(k_gbs, 2),
+            "peak": HBM_PEAK,
+            "unit": "GB/s",
+            "frac": round(k_gbs / HBM_PEAK, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": k_bytes,
+            "avg_launch_us": round(k_us, 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out), flush=True)
+    ctx.close()
+
+
+def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
+    extra = {}
+    steps = max(5, args.steps // 2)
+
+    # config 2: fused MLP at decode batches
+    for M in (8, 32, 128):
+        hb = randn(M, H)
+        g = graphed(qw, ctx, stream, lambda hb=hb: [qw.mlp_fused(ctx, gu[l], dn[l], hb, hb, gamma=gam[l], residual=hb)
+                                                   for l in range(LAYERS)])
+        ms = timer.run(g.launch, steps, 2)
+        b = LAYERS * mlp_bytes(M)
+        fl = LAYERS * 2.0 * M * 3 * H * I
+        extra[f"cfg2_mlp_bf16_M{M}"] = {"us_per_layer": round(ms * 1e3 / LAYERS, 2),
+                                        "GBps": round(b / ms / 1e6, 1),
+                                        "TFLOPs": round(fl / ms / 1e9, 2),
+                                        "tok_per_s_stack": round(M / (ms * 1e-3), 1)}
+        log("cfg2", M, extra[f"cfg2_mlp_bf16_M{M}"])
+
+    # config 1: FP32 GEMV x[1,1024] . W[1024->3584], 36 rotating copies (528 MB)
+    ws = []
+    for _ in range(36):
+        w = randn(I, H, std=0.02, dtype=torch.float32)
+        ws.append(qw.Weight.pack_device(ctx, w, qw.WFMT_F32))
+        del w
+    x1 = randn(1, H, dtype=torch.float32)
+    y1 = torch.empty(1, I, device="cuda")
+    g = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, w, x1, y1) for w in ws])
+    ms = timer.run(g.launch, steps, 2)
+    b = 36 * (I * H * 4 + H * 4 + I * 4)
+    extra["cfg1_gemv_f32_M1"] = {"us_per_gemv": round(ms * 1e3 / 36, 2), "GBps": round(b / ms / 1e6, 1),
+                                 "pct_hbm": round(100 * b / ms / 1e6 / HBM_PEAK, 1)}
+    log("cfg1", extra["cfg1_gemv_f32_M1"])
+    del ws, g
+
+    # config 3: INT8 weight-only projections of all 24 layers, FP16 activations
+    def i8(n, k):
+        q = torch.randint(-127, 128, (n, k), generator=torch.Generator(device="cuda").manual_seed(n * 7 + k),
+                          device="cuda", dtype=torch.int8)
+        s = torch.rand(n, generator=torch.Generator(device="cuda").manual_seed(n + k), device="cuda") * (2e-2 - 1e-3) + 1e-3
+        return q, s
+
+    layers = []
+    wbytes = 0
+    for li in range(LAYERS):
+        L = {}
+        if li in LINEAR_LAYERS:
+            shapes = {"qkv": (6144, 1024), "z": (2048, 1024), "out": (1024, 2048)}
+        else:
+            shapes = {"qg": (4096, 1024), "k": (512, 1024), "v": (512, 1024), "o": (1024, 2048)}
+        for name, (n, k) in shapes.items():
+            q, s = i8(n, k)
+            L[name] = qw.Weight.pack_device(ctx, q, qw.WFMT_INT8, scales=s)
+            wbytes += n * k + n * 4
+        qg_, sg_ = i8(I, H)
+        qu_, su_ = i8(I, H)
+        L["gu"] = qw.Weight.pack_glu_device(ctx, qg_, qu_, qw.WFMT_INT8, sg_, su_)
+        qd_, sd_ = i8(H, I)
+        L["down"] = qw.Weight.pack_device(ctx, qd_, qw.WFMT_INT8, scales=sd_)
+        wbytes += 3 * H * I + 2 * I * 4 + H * 4
+        layers.append(L)
+    torch.cuda.synchronize()
+    for M in (1, 32, 128):
+        xa = randn(M, H, dtype=torch.float16)
+        att = randn(M, 2048, dtype=torch.float16)            # attention-core stand-in
+        big = torch.empty(M, 6144, device="cuda", dtype=torch.float16)
+        z = torch.empty(M, 2048, device="cuda", dtype=torch.float16)
+        hmid = torch.empty(M, I, device="cuda", dtype=torch.float16)
+        kv = torch.empty(M, 512, device="cuda", dtype=torch.float16)
+        res = randn(M, H, dtype=torch.float16)
+
+        def body():
+            for li, L in enumerate(layers):
+                if "qkv" in L:
+                    qw.linear(ctx, L["qkv"], xa, big)
+                    qw.linear(ctx, L["z"], xa, z)
+                    qw.linear(ctx, L["out"], att, res, residual=res)
+                else:
+                    qw.linear(ctx, L["qg"], xa, big[:, :4096])
+                    qw.linear(ctx, L["k"], xa, kv)
+                    qw.linear(ctx, L["v"], xa, kv)
+                    qw.linear(ctx, L["o"], att, res, residual=res)
+                qw.linear(ctx, L["gu"], xa, hmid)
+                qw.linear(ctx, L["down"], hmid, res, residual=res)
+        g = graphed(qw, ctx, stream, body)
+        ms = timer.run(g.launch, steps, 2)
+        act = 0
+        for li in range(LAYERS):
+            if li in LINEAR_LAYERS:
+                act += M * 2 * (1024 * 3 + 6144 + 2048 + 2048 + 1024 * 3)
+            else:
+                act += M * 2 * (1024 * 3 + 4096 + 512 * 2 + 2048 + 1024 * 3)
+            act += M * 2 * (1024 + 2 * I + I + 1024)
+        b = wbytes + act
+        fl = 2.0 * M * (wbytes)  # one MAC per weight byte
+        extra[f"cfg3_int8_stack_M{M}"] = {"us_per_step": round(ms * 1e3, 1), "GBps": round(b / ms / 1e6, 1),
+                                          "pct_hbm": round(100 * b / ms / 1e6 / HBM_PEAK, 1),
+                                          "TFLOPs": round(fl / ms / 1e9, 2)}
+        log("cfg3", M, extra[f"cfg3_int8_stack_M{M}"])
+        del g
+    del layers
+
+    # config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each
+    for fmt, name in ((qw.WFMT_BF16, "bf16"), (qw.WFMT_INT8, "int8")):
+        Es = []
+        for c in range(2):
+            e = randn(V, H, std=0.02)
+            Es.append(qw.Weight.pack_device(ctx, e, fmt))
+            del e
+        torch.cuda.synchronize()
+        wb = V * H * (2 if fmt == qw.WFMT_BF16 else 1) + (V * 4 if fmt == qw.WFMT_INT8 else 0)
+        for M in (1, 32, 128):
+            hh = randn(M, H)
+            ids = torch.empty(M, dtype=torch.int32, device="cuda")
+            g = graphed(qw, ctx, stream, lambda hh=hh, ids=ids: [qw.lmhead_argmax(ctx, E, hh, ids) for E in Es])
+            ms = timer.run(g.launch, max(3, steps // 4), 1) / 2
+            b = wb + M * H * 2 + M * 4
+            extra[f"cfg5_lmhead_{name}_M{M}"] = {"us_per_call": round(ms * 1e3, 1), "GBps": round(b / ms / 1e6, 1),
+                                                 "pct_hbm": round(100 * b / ms / 1e6 / HBM_PEAK, 1),
+                                                 "tok_per_s": round(M / (ms * 1e-3), 1)}
+            log("cfg5", name, M, extra[f"cfg5_lmhead_{name}_M{M}"])
+            del g
+        del Es
+    torch.cuda.synchronize()
+    return extra
+
+
+if __name__ == "__main__":
+    main()

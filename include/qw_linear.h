@@ -90,6 +90,14 @@ qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, 
 qw_status qw_weight_pack_glu(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
                              qw_wfmt dst, int N, int K, const float* gate_scales,
                              const float* up_scales, qw_weight** out);
+/* Same as qw_weight_pack / qw_weight_pack_glu with `w`/`gate`/`up` and the
+ * optional scales given as DEVICE pointers (weights already resident in HBM,
+ * e.g. produced by another loader); nothing is copied through the host. */
+qw_status qw_weight_pack_device(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N,
+                                int K, const float* scales, qw_weight** out);
+qw_status qw_weight_pack_glu_device(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
+                                    qw_wfmt dst, int N, int K, const float* gate_scales,
+                                    const float* up_scales, qw_weight** out);
 /* Borrow: build a weight object over device memory already in packed order
  * (e.g. a tied embedding shared with the lm_head, as
  * CudaLMHead::set_weight_bf16_ptr borrows, lm_head_cuda.cu:189-196).  The

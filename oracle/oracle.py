@@ -89,6 +89,10 @@ def ref_lib():
         R.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, _i, _i, _fl]
         for fn in (R.ref_linear, R.ref_mlp, R.ref_greedy, R.ref_rmsnorm):
             fn.restype = ctypes.c_int
+        R.ref_mlp_time.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i]
+        R.ref_mlp_time.restype = ctypes.c_double
+        R.ref_lmhead_time.argtypes = [_f32p, _f32p, _i, _i, _i, ctypes.c_void_p]
+        R.ref_lmhead_time.restype = ctypes.c_double
         _REF = R
     return _REF
 

@@ -8,6 +8,7 @@
 //   qwen::MLP      src/backend/cpu/core/mlp/language_mlp.hpp:7-36
 //   qwen::Sampler  src/backend/cpu/core/heads/sampler.hpp        (GREEDY)
 //   qwen::RMSNorm  src/backend/cpu/core/common/language_common.hpp:9-33
+#include <chrono>
 #include <exception>
 #include <vector>
 
@@ -54,6 +55,42 @@ int ref_greedy(const float* logits, int n) {
         return s.sample(std::vector<float>(logits, logits + n));
     } catch (const std::exception&) {
         return -1;
+    }
+}
+
+// Timing leg of the CPU baseline: builds the reference MLP once and runs
+// MLP::forward_batch `iters` times; returns the elapsed seconds (or -1).
+double ref_mlp_time(const float* Wg, const float* Wu, const float* Wd, const float* x, float* y,
+                    int M, int H, int I, int iters) {
+    try {
+        qwen::MLP mlp(H, I);
+        mlp.set_weights(std::vector<float>(Wg, Wg + (size_t)I * H),
+                        std::vector<float>(Wu, Wu + (size_t)I * H),
+                        std::vector<float>(Wd, Wd + (size_t)H * I));
+        auto t0 = std::chrono::steady_clock::now();
+        for (int i = 0; i < iters; ++i) mlp.forward_batch(x, y, M);
+        auto t1 = std::chrono::steady_clock::now();
+        return std::chrono::duration<double>(t1 - t0).count();
+    } catch (const std::exception&) {
+        return -1.0;
+    }
+}
+
+// Timing leg for the lm_head: LMHead::forward + greedy Sampler, `iters` times.
+double ref_lmhead_time(const float* E, const float* h, int V, int K, int iters, int* id_out) {
+    try {
+        qwen::LMHead head(K, V);
+        head.set_weight(std::vector<float>(E, E + (size_t)V * K));
+        qwen::Sampler s(V, qwen::SamplingStrategy::GREEDY);
+        std::vector<float> in(h, h + K);
+        auto t0 = std::chrono::steady_clock::now();
+        int id = -1;
+        for (int i = 0; i < iters; ++i) id = s.sample(head.forward(in));
+        auto t1 = std::chrono::steady_clock::now();
+        if (id_out) *id_out = id;
+        return std::chrono::duration<double>(t1 - t0).count();
+    } catch (const std::exception&) {
+        return -1.0;
     }
 }
 

@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
@@ -18,6 +19,9 @@
 struct qw_ctx {
     int device = 0;
     int num_cus = 256;
+    int wg_per_cu = 2;       // resident skinny workgroups per CU (grid cap)
+    int min_items = 0;       // split K until a launch has this many items (0: never)
+    int force_nw = 0;        // waves per skinny workgroup (0: automatic)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -129,6 +133,9 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
         c->num_cus = prop.multiProcessorCount;
+    if (const char* v = getenv("QW_SKINNY_WG_PER_CU")) c->wg_per_cu = std::max(1, atoi(v));
+    if (const char* v = getenv("QW_SKINNY_MIN_ITEMS")) c->min_items = std::max(0, atoi(v));
+    if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = (atoi(v) == 16) ? 16 : (atoi(v) == 4 ? 4 : 0);
     if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(128, 8224, 3584);
     workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(1u << 20));
     workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
@@ -221,32 +228,39 @@ static qw_status check_pack_args(qw_ctx* ctx, const void* w, qw_dtype src, qw_wf
     return QW_OK;
 }
 
-// Upload one host matrix and pack it into physical tiles t*tile_mul+tile_add.
-static qw_status pack_one(qw_ctx* ctx, qw_weight* W, const void* host, qw_dtype src,
-                          const float* host_scales, int tile_mul, int tile_add) {
+// Pack one matrix (host or device source) into physical tiles t*tile_mul+tile_add.
+static qw_status pack_one(qw_ctx* ctx, qw_weight* W, const void* src_ptr, qw_dtype src,
+                          const float* src_scales, int tile_mul, int tile_add, bool on_device) {
     const size_t bytes = (size_t)W->N * W->K * dsize(src);
-    void* dsrc = nullptr;
-    float* dscales = nullptr;
-    hipError_t e = hipMalloc(&dsrc, bytes);
-    if (e != hipSuccess) return fail(ctx, QW_ERR_NOMEM, "staging hipMalloc failed");
-    e = hipMemcpy(dsrc, host, bytes, hipMemcpyHostToDevice);
-    if (e == hipSuccess && src == QW_I8) {
-        e = hipMalloc(&dscales, (size_t)W->N * sizeof(float));
-        if (e == hipSuccess)
-            e = hipMemcpy(dscales, host_scales, (size_t)W->N * sizeof(float), hipMemcpyHostToDevice);
+    const void* dsrc = src_ptr;
+    const float* dscales = src_scales;
+    void* stage = nullptr;
+    float* stage_s = nullptr;
+    hipError_t e = hipSuccess;
+    if (!on_device) {
+        e = hipMalloc(&stage, bytes);
+        if (e != hipSuccess) return fail(ctx, QW_ERR_NOMEM, "staging hipMalloc failed");
+        e = hipMemcpy(stage, src_ptr, bytes, hipMemcpyHostToDevice);
+        dsrc = stage;
+        if (e == hipSuccess && src == QW_I8) {
+            e = hipMalloc(&stage_s, (size_t)W->N * sizeof(float));
+            if (e == hipSuccess)
+                e = hipMemcpy(stage_s, src_scales, (size_t)W->N * sizeof(float), hipMemcpyHostToDevice);
+            dscales = stage_s;
+        }
     }
     if (e == hipSuccess)
         e = qwk::launch_pack(dsrc, (int)src, W->wf, dscales, W->N, W->K, W->packed, W->scales,
                              tile_mul, tile_add, 0);
     if (e == hipSuccess) e = hipDeviceSynchronize();
-    hipFree(dsrc);
-    if (dscales) hipFree(dscales);
+    if (stage) hipFree(stage);
+    if (stage_s) hipFree(stage_s);
     if (e != hipSuccess) return hip_fail(ctx, e, "weight packing");
     return QW_OK;
 }
 
-qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
-                         const float* scales, qw_weight** out) {
+static qw_status pack_impl(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
+                           const float* scales, qw_weight** out, bool on_device) {
     if (!out) return fail(ctx, QW_ERR_NULL, "out is NULL");
     *out = nullptr;
     qw_status s = check_pack_args(ctx, w, src, dst, N, K, scales);
@@ -254,7 +268,7 @@ qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, 
     hipSetDevice(ctx->device);
     qw_weight* W = nullptr;
     if ((s = alloc_weight(ctx, dst, N, K, 0, &W)) != QW_OK) return s;
-    if ((s = pack_one(ctx, W, w, src, scales, 1, 0)) != QW_OK) {
+    if ((s = pack_one(ctx, W, w, src, scales, 1, 0, on_device)) != QW_OK) {
         qw_weight_free(W);
         return s;
     }
@@ -262,9 +276,9 @@ qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, 
     return QW_OK;
 }
 
-qw_status qw_weight_pack_glu(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
-                             qw_wfmt dst, int N, int K, const float* gate_scales,
-                             const float* up_scales, qw_weight** out) {
+static qw_status pack_glu_impl(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
+                               qw_wfmt dst, int N, int K, const float* gate_scales,
+                               const float* up_scales, qw_weight** out, bool on_device) {
     if (!out) return fail(ctx, QW_ERR_NULL, "out is NULL");
     *out = nullptr;
     qw_status s = check_pack_args(ctx, gate, src, dst, N, K, gate_scales);
@@ -273,13 +287,35 @@ qw_status qw_weight_pack_glu(qw_ctx* ctx, const void* gate, const void* up, qw_d
     hipSetDevice(ctx->device);
     qw_weight* W = nullptr;
     if ((s = alloc_weight(ctx, dst, N, K, 1, &W)) != QW_OK) return s;
-    if ((s = pack_one(ctx, W, gate, src, gate_scales, 2, 0)) != QW_OK ||
-        (s = pack_one(ctx, W, up, src, up_scales, 2, 1)) != QW_OK) {
+    if ((s = pack_one(ctx, W, gate, src, gate_scales, 2, 0, on_device)) != QW_OK ||
+        (s = pack_one(ctx, W, up, src, up_scales, 2, 1, on_device)) != QW_OK) {
         qw_weight_free(W);
         return s;
     }
     *out = W;
     return QW_OK;
+}
+
+qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
+                         const float* scales, qw_weight** out) {
+    return pack_impl(ctx, w, src, dst, N, K, scales, out, false);
+}
+
+qw_status qw_weight_pack_device(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,
+                                const float* scales, qw_weight** out) {
+    return pack_impl(ctx, w, src, dst, N, K, scales, out, true);
+}
+
+qw_status qw_weight_pack_glu(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
+                             qw_wfmt dst, int N, int K, const float* gate_scales,
+                             const float* up_scales, qw_weight** out) {
+    return pack_glu_impl(ctx, gate, up, src, dst, N, K, gate_scales, up_scales, out, false);
+}
+
+qw_status qw_weight_pack_glu_device(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
+                                    qw_wfmt dst, int N, int K, const float* gate_scales,
+                                    const float* up_scales, qw_weight** out) {
+    return pack_glu_impl(ctx, gate, up, src, dst, N, K, gate_scales, up_scales, out, true);
 }
 
 qw_status qw_weight_wrap_packed(qw_ctx* ctx, void* packed, float* scales, qw_wfmt fmt, int N, int K,
@@ -392,15 +428,25 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     a.N = W->N;
     a.n_groups = (W->N + 15) / 16;
     a.ksteps = W->ksteps;
-    const int target = ctx->num_cus * 8;
+    const int CT = M <= 16 ? 1 : 2, RT = W->glu ? 2 : 1;
+    // Workgroup shape: tiles plentiful -> 4 waves per tile; few tiles (the
+    // 1024-row projections) -> 16 waves per tile so fewer CUs still keep
+    // enough loads in flight.  K is split across workgroups only on request
+    // (the split-K hand-off adds a device-coherent round trip).
+    const bool direct = (W->wf == QW_WFMT_BF16 && xdt == QW_BF16) || (W->wf == QW_WFMT_INT8_ROWSCALE && xdt == QW_F16) ||
+                        (W->wf == QW_WFMT_F32 && xdt == QW_F32);
+    const bool wide_ok = !argmax && !W->glu && M <= 16 && direct;
+    int nw = (wide_ok && a.n_groups * 4 < ctx->num_cus * 3) ? 16 : 4;
+    if (wide_ok && ctx->force_nw) nw = ctx->force_nw;
     int S = 1;
-    if (!argmax && a.n_groups < target) {
-        S = (target + a.n_groups - 1) / a.n_groups;
-        S = std::min(S, std::max(1, W->ksteps / 2));
-        S = std::min(S, 64);
-        if (a.n_groups > kMaxCounters) S = 1;
-        const int RT = W->glu ? 2 : 1, CT = M <= 16 ? 1 : 2;
-        while (S > 1 && (size_t)a.n_groups * S * RT * CT * 1024 > ctx->partials_bytes) --S;
+    if (!argmax && ctx->min_items > a.n_groups) {
+        const int want = (ctx->min_items + a.n_groups - 1) / a.n_groups;
+        S = std::max(1, std::min(want, W->ksteps / nw));
+    }
+    if (S > 1) {
+        if (a.n_groups > kMaxCounters) return fail(ctx, QW_ERR_WORKSPACE, "too many split-K tiles");
+        if ((size_t)a.n_groups * S * 64 * (RT * CT * 4 + CT) * 4 > ctx->partials_bytes)
+            return fail(ctx, QW_ERR_WORKSPACE, "split-K partials exceed the workspace");
     }
     a.S = S;
     a.n_items = a.n_groups * S;
@@ -431,9 +477,10 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     a.done = ctx->done;
     a.ids = ids;
     a.maxv = maxv;
-    const int waves = std::min(a.n_items, target);
-    const int grid = (waves + 3) / 4;
-    hipError_t e = qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, grid, stream);
+    const int grid = std::min(a.n_items, ctx->num_cus * ctx->wg_per_cu);
+    if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * dsize(xdt) >= (1ull << 32))
+        return fail(ctx, QW_ERR_SHAPE, "operands above 4 GiB are not supported");
+    hipError_t e = qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "skinny kernel launch");
     return QW_OK;
 }

@@ -39,8 +39,20 @@ struct SkinnyArgs {
     float* maxv;             // argmax values [M] or nullptr
 };
 
+// k-steps one wave holds in registers at a time (the loads of one chunk are
+// all issued together; the first chunk of the next item is issued before the
+// current item's reduction and epilogue).
+constexpr int skinny_unroll(int wf, int xdt, int ct, bool glu) {
+    const int ke = wf == 0 ? 4 : (wf == 1 ? 8 : 16);
+    const int xw = ke * (xdt == 0 ? 4 : 2) / 4;          // activation words per unit
+    const int per_unit = (glu ? 2 : 1) * 4 + ct * xw;
+    const int u = 96 / per_unit;
+    return u < 2 ? 2 : (u > 8 ? 8 : u);
+}
+
 // wf: 0 F32, 1 BF16, 2 INT8 ; xdt: 0 F32, 1 BF16, 2 F16
-hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int grid,
+// nw: waves per workgroup (4 or 16)
+hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream);
 
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.

@@ -174,118 +174,179 @@ __device__ __forceinline__ f32x4 unit_mfma(u32x4 a, const BOps<WF, XDT>& b, f32x
     return acc;
 }
 
-// 1/sqrt(mean(x[m]^2)+eps) for the token of this lane (lane & 15 within
-// token tile ct); all 64 lanes must call it.
-template <int XDT>
-__device__ __forceinline__ float lane_inv_rms(const SkinnyArgs& a, int m, int lane) {
-    const int g = lane >> 4;
-    const int kq = a.K >> 2;  // multiple of 16
-    float ss = 0.0f;
-    if (m < a.M) {
-        const uint8_t* base = reinterpret_cast<const uint8_t*>(a.x) +
-                              ((int64_t)m * a.ldx + (int64_t)g * kq) * XSize<XDT>::v;
-        constexpr int EPV = 16 / XSize<XDT>::v;  // elements per 16 B
-        for (int k = 0; k < kq; k += EPV) {
-            u32x4 v = *reinterpret_cast<const u32x4*>(base + (int64_t)k * XSize<XDT>::v);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    // raw (untyped) buffer: stride 0, num_records = bytes; loads past the end return 0
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+constexpr int AUX_NT = 2;  // non-temporal (streamed once)
+
+template <int XDT, int KE>
+__device__ __forceinline__ void buf_load_xraw(XRaw<XDT, KE>& r, __amdgpu_buffer_rsrc_t rs, uint32_t voff,
+                                              uint32_t soff) {
+    constexpr int B = XRaw<XDT, KE>::BYTES;
+    if constexpr (B >= 16) {
 #pragma unroll
-            for (int e = 0; e < EPV; ++e) {
-                float f;
-                if constexpr (XDT == DT_F32) f = __uint_as_float(v[e]);
-                else {
-                    uint32_t h = (v[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                    f = XDT == DT_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
-                }
-                ss += f * f;
+        for (int i = 0; i < B / 16; ++i) {
+            u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, 0));
+            r.w[4 * i + 0] = v[0]; r.w[4 * i + 1] = v[1];
+            r.w[4 * i + 2] = v[2]; r.w[4 * i + 3] = v[3];
+        }
+    } else {
+        u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0));
+        r.w[0] = v[0]; r.w[1] = v[1];
+    }
+}
+
+// Per-item epilogue operands, loaded before the item's weights so that they
+// never form a dependent memory round trip after the weight stream.
+template <int RT, int CT>
+struct EpiOps {
+    f32x4 sc[RT];
+    f32x4 res[CT];
+};
+
+template <int RT, int CT>
+__device__ __forceinline__ void load_epi(const SkinnyArgs& a, int grp, int lane, bool want_res,
+                                         EpiOps<RT, CT>& e) {
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+        e.sc[rt] = a.scales ? *reinterpret_cast<const f32x4*>(a.scales + (int64_t)(grp * RT + rt) * 16 + g * 4)
+                            : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        e.res[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int m = ct * 16 + r;
+        const int o = grp * 16 + g * 4;
+        if (want_res && m < a.M && o < a.N) {
+            if (a.vec_store) {
+                e.res[ct] = load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + o);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (o + i < a.N) e.res[ct][i] = load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + o + i);
             }
         }
     }
-    ss += __shfl_xor(ss, 16);
-    ss += __shfl_xor(ss, 32);
-    return 1.0f / sqrtf(ss / (float)a.K + a.eps);
 }
 
-template <int WF, int XDT, int CT, bool GLU, bool ARGMAX>
-__global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
+// This wave's k sub-range [kb, kend) of an item: the item's K split is cut
+// into NW contiguous pieces, one per wave of the workgroup.
+template <int NW>
+__device__ __forceinline__ void item_range(const SkinnyArgs& a, int item, int wave_id, int& kb, int& kend) {
+    const int grp = item / a.S;
+    const int s = item - grp * a.S;
+    const int ks0 = (int)(((int64_t)s * a.ksteps) / a.S);
+    const int ks1 = (int)(((int64_t)(s + 1) * a.ksteps) / a.S);
+    const int cnt = ks1 - ks0;
+    kb = ks0 + (wave_id * cnt) / NW;
+    kend = ks0 + ((wave_id + 1) * cnt) / NW;
+}
+
+// Issue the loads of k-steps [kb, kb+n) (n <= U) of tile group grp.
+template <int WF, int XDT, int CT, int RT, int U>
+__device__ __forceinline__ void issue_chunk(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t wrs,
+                                            __amdgpu_buffer_rsrc_t xrs, uint32_t xvoff[CT], int grp,
+                                            int kb, int n, int lane, u32x4 (&A)[U][RT],
+                                            XRaw<XDT, WTraits<WF>::KE> (&X)[U][CT]) {
+    constexpr int KE = WTraits<WF>::KE;
+    const uint32_t tile_bytes = (uint32_t)a.ksteps * 1024u;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        if (u < n) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                A[u][rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         wrs, lane * 16, (uint32_t)(grp * RT + rt) * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+                buf_load_xraw<XDT, KE>(X[u][ct], xrs, xvoff[ct], (uint32_t)(kb + u) * (4 * KE) * XSize<XDT>::v);
+        }
+    }
+}
+
+// Work decomposition (see the file header): a workgroup of NW waves owns one
+// item at a time -- a 16-row tile (two for GLU) over one K split -- and its
+// waves take contiguous pieces of that split; partial tiles meet in LDS.
+// Workgroups walk the items grid-stride, and the loads of the next item are
+// issued before the current item's reduction and epilogue.  The RMSNorm
+// statistics come from the activation fragments already in registers.
+template <int WF, int XDT, int CT, bool GLU, bool ARGMAX, int NW>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
+    constexpr int U = NW == 16 ? (WF == WF_I8 ? 2 : 4) : skinny_unroll(WF, XDT, CT, GLU);
     constexpr int KE = WTraits<WF>::KE;
     constexpr int RT = GLU ? 2 : 1;
+    constexpr int F = RT * CT;
     using XR = XRaw<XDT, KE>;
-    constexpr int PER_UNIT_REGS = RT * 4 + CT * XR::NW;
-    constexpr int U0 = 96 / PER_UNIT_REGS;
-    constexpr int U = U0 < 2 ? 2 : (U0 > 8 ? 8 : U0);
+    __shared__ f32x4 red[NW][F][64];
+    __shared__ float ssred[NW][CT][64];
+    extern __shared__ float gam_s[];  // K floats when the norm prologue is on
 
     const int lane = threadIdx.x & 63;
-    const int wave_id = threadIdx.x >> 6;
-    const int total_waves = gridDim.x * 4;
-    const int gw = blockIdx.x * 4 + wave_id;
+    const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15;
     const int g = lane >> 4;
     const bool norm = (a.flags & EP_NORM) != 0;
-    const int64_t tile_bytes = (int64_t)a.ksteps * 1024;
+    const bool want_res = !ARGMAX && (a.flags & EP_RESIDUAL);
 
-    float inv[CT];
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * RT * a.ksteps * 1024u));
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * XSize<XDT>::v));
+    uint32_t xvoff[CT];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) inv[ct] = 1.0f;
+    for (int ct = 0; ct < CT; ++ct)   // tokens >= M fall outside the buffer and read as 0
+        xvoff[ct] = (uint32_t)(((ct * 16 + r) * a.ldx + g * KE) * XSize<XDT>::v);
+
+    if (norm) {
+        for (int i = threadIdx.x; i < a.K / 4; i += NW * 64)
+            reinterpret_cast<f32x4*>(gam_s)[i] = reinterpret_cast<const f32x4*>(a.gamma)[i];
+    }
+
     unsigned long long best[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) best[ct] = 0ull;
-    if constexpr (ARGMAX) {
-        if (norm) {
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct) inv[ct] = lane_inv_rms<XDT>(a, ct * 16 + r, lane);
-        }
+
+    u32x4 A[U][RT];
+    XR X[U][CT];
+    EpiOps<RT, CT> epi, epi_next;
+    int kb = 0, kend = 0, n = 0;
+    int item = blockIdx.x;
+    if (item < a.n_items) {
+        if (wave_id == 0) load_epi<RT, CT>(a, item / a.S, lane, want_res, epi);
+        item_range<NW>(a, item, wave_id, kb, kend);
+        n = min(U, kend - kb);
+        issue_chunk<WF, XDT, CT, RT, U>(a, wrs, xrs, xvoff, item / a.S, kb, n, lane, A, X);
     }
+    __syncthreads();  // gamma staged
 
-    for (int item = gw; item < a.n_items; item += total_waves) {
-        const int grp = item / a.S;
-        const int s = item - grp * a.S;
-        const int ks0 = (int)(((int64_t)s * a.ksteps) / a.S);
-        const int ks1 = (int)(((int64_t)(s + 1) * a.ksteps) / a.S);
-
+    while (item < a.n_items) {
         f32x4 acc[RT][CT];
+        float ss[CT];
 #pragma unroll
-        for (int i = 0; i < RT; ++i)
+        for (int j = 0; j < CT; ++j) {
+            ss[j] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < CT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-        const uint8_t* wbase[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-            wbase[rt] = a.w + (int64_t)(grp * RT + rt) * tile_bytes + lane * 16;
-
-        for (int kb = ks0; kb < ks1; kb += U) {
-            const int n = ks1 - kb;
-            u32x4 A[U][RT];
-            XR X[U][CT];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (u < n) {
-#pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
-                        A[u][rt] = load_w16(wbase[rt] + (int64_t)(kb + u) * 1024);
-#pragma unroll
-                    for (int ct = 0; ct < CT; ++ct) {
-                        const int m = ct * 16 + r;
-                        if (m < a.M) {
-                            const int64_t k = (int64_t)(kb + u) * (4 * KE) + g * KE;
-                            load_xraw<XDT, KE>(X[u][ct], reinterpret_cast<const uint8_t*>(a.x) +
-                                                             ((int64_t)m * a.ldx + k) * XSize<XDT>::v);
-                        } else {
-                            zero_xraw<XDT, KE>(X[u][ct]);
-                        }
-                    }
-                }
-            }
+            for (int i = 0; i < RT; ++i) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        for (;;) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 if (u < n) {
                     float gam[KE];
                     if (norm) {
-                        const float* gp = a.gamma + (int64_t)(kb + u) * (4 * KE) + g * KE;
+                        const float* gp = gam_s + (kb + u) * (4 * KE) + g * KE;
 #pragma unroll
                         for (int e = 0; e < KE; e += 4) {
                             f32x4 gv = *reinterpret_cast<const f32x4*>(gp + e);
                             gam[e] = gv[0]; gam[e + 1] = gv[1]; gam[e + 2] = gv[2]; gam[e + 3] = gv[3];
                         }
+#pragma unroll
+                        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                            for (int e = 0; e < KE; ++e) {
+                                const float xv = xraw_elem(X[u][ct], e);
+                                ss[ct] += xv * xv;
+                            }
                     }
 #pragma unroll
                     for (int ct = 0; ct < CT; ++ct) {
@@ -296,69 +357,146 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
                     }
                 }
             }
+            kb += n;
+            if (kb >= kend) break;
+            n = min(U, kend - kb);
+            issue_chunk<WF, XDT, CT, RT, U>(a, wrs, xrs, xvoff, item / a.S, kb, n, lane, A, X);
+        }
+        const int cur = item;
+        item += gridDim.x;
+        if (item < a.n_items) {
+            if (wave_id == 0) load_epi<RT, CT>(a, item / a.S, lane, want_res, epi_next);
+            item_range<NW>(a, item, wave_id, kb, kend);
+            n = min(U, kend - kb);
+            issue_chunk<WF, XDT, CT, RT, U>(a, wrs, xrs, xvoff, item / a.S, kb, n, lane, A, X);
         }
 
-        if constexpr (!ARGMAX) {
-            if (a.S > 1) {
-                float4* P = a.partials + (int64_t)grp * a.S * (RT * CT) * 64 + lane;
-                float4* mine = P + (int64_t)s * (RT * CT) * 64;
+        // ---- reduce the NW pieces in LDS (fixed order) ----
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                    for (int ct = 0; ct < CT; ++ct) {
-                        f32x4 v = acc[rt][ct];
-                        mine[(rt * CT + ct) * 64] = make_float4(v[0], v[1], v[2], v[3]);
-                    }
-                __threadfence();
-                unsigned old = 0;
-                if (lane == 0) old = atomicAdd(&a.counters[grp], 1u);
-                old = __shfl(old, 0);
-                if (old != (unsigned)(a.S - 1)) continue;
-                __threadfence();
+            for (int ct = 0; ct < CT; ++ct) red[wave_id][rt * CT + ct][lane] = acc[rt][ct];
+        if (norm) {
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
+            for (int ct = 0; ct < CT; ++ct) ssred[wave_id][ct][lane] = ss[ct];
+        }
+        __syncthreads();
+        if (NW > 1) {
+            for (int t = threadIdx.x; t < F * 64; t += NW * 64) {
+                const int f = t >> 6, l = t & 63;
+                f32x4 sum = red[0][f][l];
 #pragma unroll
-                    for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-                for (int s2 = 0; s2 < a.S; ++s2) {
-                    const float4* q = P + (int64_t)s2 * (RT * CT) * 64;
-#pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                        for (int ct = 0; ct < CT; ++ct) {
-                            float4 v = q[(rt * CT + ct) * 64];
-                            acc[rt][ct] += f32x4{v.x, v.y, v.z, v.w};
-                        }
-                }
-                if (lane == 0) atomicExch(&a.counters[grp], 0u);
+                for (int w = 1; w < NW; ++w) sum += red[w][f][l];
+                red[0][f][l] = sum;
             }
             if (norm) {
+                for (int t = threadIdx.x; t < CT * 64; t += NW * 64) {
+                    const int c = t >> 6, l = t & 63;
+                    float sum = ssred[0][c][l];
 #pragma unroll
-                for (int ct = 0; ct < CT; ++ct) inv[ct] = lane_inv_rms<XDT>(a, ct * 16 + r, lane);
+                    for (int w = 1; w < NW; ++w) sum += ssred[w][c][l];
+                    ssred[0][c][l] = sum;
+                }
+            }
+            __syncthreads();
+        }
+        if (wave_id != 0) continue;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = red[0][rt * CT + ct][lane];
+        if (norm) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) ss[ct] = ssred[0][ct][lane];
+        }
+        EpiOps<RT, CT> e = epi;
+        epi = epi_next;
+
+        const int grp = cur / a.S;
+        bool finish = true;
+        if constexpr (!ARGMAX) {
+            if (a.S > 1) {
+                // Cross-workgroup split-K hand-off, no fence: the partial tile
+                // (and the partial sum of squares) go out as agent-scope atomic
+                // stores (written through to the device coherence point),
+                // s_waitcnt vmcnt(0) waits for their completion, then the
+                // agent-scope counter increment.  The last of the S workgroups
+                // reads the S partials back with agent-scope atomic loads, in
+                // split order (deterministic), and returns the counter to 0.
+                const int s = cur - grp * a.S;
+                constexpr int REC = F * 4 + CT;  // floats per lane per split
+                float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)grp * a.S * 64 + lane) * REC;
+                float* mine = P + (int64_t)s * 64 * REC;
+#pragma unroll
+                for (int f = 0; f < F; ++f)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        __hip_atomic_store(mine + f * 4 + i, acc[f / CT][f % CT][i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                if (norm) {
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct)
+                        __hip_atomic_store(mine + F * 4 + ct, ss[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                unsigned old = 0;
+                if (lane == 0)
+                    old = __hip_atomic_fetch_add(&a.counters[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                old = __shfl(old, 0);
+                finish = (old == (unsigned)(a.S - 1));
+                if (finish) {
+#pragma unroll
+                    for (int ct = 0; ct < CT; ++ct) {
+                        ss[ct] = 0.0f;
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                    for (int s2 = 0; s2 < a.S; ++s2) {
+                        const float* q = P + (int64_t)s2 * 64 * REC;
+#pragma unroll
+                        for (int f = 0; f < F; ++f)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                acc[f / CT][f % CT][i] += __hip_atomic_load(q + f * 4 + i, __ATOMIC_RELAXED,
+                                                                            __HIP_MEMORY_SCOPE_AGENT);
+                        if (norm) {
+#pragma unroll
+                            for (int ct = 0; ct < CT; ++ct)
+                                ss[ct] += __hip_atomic_load(q + F * 4 + ct, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                    }
+                    if (lane == 0)
+                        __hip_atomic_store(&a.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        if (!finish) continue;
+
+        float inv[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            inv[ct] = 1.0f;
+            if (norm) {
+                float t = ss[ct];
+                t += __shfl_xor(t, 16);
+                t += __shfl_xor(t, 32);
+                inv[ct] = 1.0f / sqrtf(t / (float)a.K + a.eps);
             }
         }
 
-        // ---- epilogue ----
+        // ---- epilogue (wave 0) ----
         const int o = grp * 16 + g * 4;  // first of this lane's 4 logical rows
-        f32x4 sc[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            if (a.scales) {
-                sc[rt] = *reinterpret_cast<const f32x4*>(a.scales + (int64_t)(grp * RT + rt) * 16 + g * 4);
-            } else {
-                sc[rt] = f32x4{1.f, 1.f, 1.f, 1.f};
-            }
-        }
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
             const int m = ct * 16 + r;
             f32x4 v;
             if constexpr (GLU) {
-                f32x4 gt = acc[0][ct] * sc[0] * inv[ct];
-                f32x4 up = acc[1][ct] * sc[1] * inv[ct];
+                f32x4 gt = acc[0][ct] * e.sc[0] * inv[ct];
+                f32x4 up = acc[1][ct] * e.sc[1] * inv[ct];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = silu_f(gt[i]) * up[i];
             } else {
-                v = acc[0][ct] * sc[0] * inv[ct];
+                v = acc[0][ct] * e.sc[0] * inv[ct];
             }
             if constexpr (ARGMAX) {
                 if (m < a.M) {
@@ -372,8 +510,8 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
                 }
             } else {
                 if (m >= a.M || o >= a.N) continue;
+                if (want_res) v += e.res[ct];
                 if (a.vec_store) {
-                    if (a.flags & EP_RESIDUAL) v += load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + o);
                     void* dst = a.y;
                     int col = o;
                     if (a.flags & EP_SPLIT) {
@@ -387,8 +525,6 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         const int oi = o + i;
                         if (oi >= a.N) break;
-                        float vi = v[i];
-                        if (a.flags & EP_RESIDUAL) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
                         void* dst = a.y;
                         int col = oi;
                         if (a.flags & EP_SPLIT) {
@@ -396,7 +532,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
                             dst = (blk & 1) ? a.y2 : a.y;
                             col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
                         }
-                        store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
+                        store_act(dst, a.ydt, (int64_t)m * a.ldy + col, v[i]);
                     }
                 }
             }
@@ -404,6 +540,7 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
     }
 
     if constexpr (ARGMAX) {
+        if (wave_id != 0) return;
         // merge the four row groups of each token column, then the grid
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
@@ -416,59 +553,78 @@ __global__ __launch_bounds__(256) void skinny_kernel(SkinnyArgs a) {
             if (g == 0 && m < a.M && best[ct] != 0ull)
                 __hip_atomic_fetch_max(&a.keys[m], best[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        __threadfence();
+        // The key updates are agent-scope read-modify-writes, performed at
+        // the device coherence point; waiting for their completion orders
+        // them before this workgroup's completion count.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned old = 0;
-        if (lane == 0) old = atomicAdd(a.done, 1u);
+        if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __shfl(old, 0);
-        if (old == (unsigned)(total_waves - 1)) {
-            __threadfence();
+        if (old == gridDim.x - 1) {
             for (int m = lane; m < a.M; m += 64) {
                 unsigned long long kk = __hip_atomic_exchange(&a.keys[m], 0ull, __ATOMIC_RELAXED,
                                                               __HIP_MEMORY_SCOPE_AGENT);
                 a.ids[m] = (int32_t)key_index(kk);
                 if (a.maxv) a.maxv[m] = key_value(kk);
             }
-            if (lane == 0) atomicExch(a.done, 0u);
+            if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
 
-template <int WF, int XDT, int CT>
-static hipError_t launch3(const SkinnyArgs& a, bool glu, bool argmax, int grid, hipStream_t st) {
+template <int WF, int XDT, int CT, int NW>
+static hipError_t launch4(const SkinnyArgs& a, bool glu, bool argmax, int grid, hipStream_t st) {
+    const size_t smem = (a.flags & EP_NORM) ? (size_t)a.K * sizeof(float) : 0;
     if (argmax) {
         if (glu) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, true>), dim3(grid), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, true, NW>), dim3(grid), dim3(NW * 64), smem, st, a);
     } else if (glu) {
-        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, true, false>), dim3(grid), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, true, false, NW>), dim3(grid), dim3(NW * 64), smem, st, a);
     } else {
-        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, false>), dim3(grid), dim3(256), 0, st, a);
+        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, false, NW>), dim3(grid), dim3(NW * 64), smem, st, a);
     }
     return hipGetLastError();
 }
 
+template <int WF, int XDT, int CT>
+static hipError_t launch3(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
+    // 16-wave workgroups serve plain (non-GLU) projections of up to 16
+    // tokens whose activation already has the MFMA input type
+    if constexpr (CT == 1 && ((WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16) ||
+                              (WF == WF_F32 && XDT == DT_F32))) {
+        if (nw == 16 && !glu && !argmax) {
+            const size_t smem = (a.flags & EP_NORM) ? (size_t)a.K * sizeof(float) : 0;
+            hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, false, 16>), dim3(grid), dim3(1024), smem, st, a);
+            return hipGetLastError();
+        }
+    }
+    return launch4<WF, XDT, CT, 4>(a, glu, argmax, grid, st);
+}
+
 template <int WF, int XDT>
-static hipError_t launch2(const SkinnyArgs& a, bool glu, bool argmax, int grid, hipStream_t st) {
-    if (a.M <= 16) return launch3<WF, XDT, 1>(a, glu, argmax, grid, st);
-    return launch3<WF, XDT, 2>(a, glu, argmax, grid, st);
+static hipError_t launch2(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
+    if (a.M <= 16) return launch3<WF, XDT, 1>(a, glu, argmax, nw, grid, st);
+    return launch3<WF, XDT, 2>(a, glu, argmax, nw, grid, st);
 }
 
 template <int WF>
-static hipError_t launch1(const SkinnyArgs& a, int xdt, bool glu, bool argmax, int grid, hipStream_t st) {
+static hipError_t launch1(const SkinnyArgs& a, int xdt, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
     switch (xdt) {
-        case DT_F32: return launch2<WF, DT_F32>(a, glu, argmax, grid, st);
-        case DT_BF16: return launch2<WF, DT_BF16>(a, glu, argmax, grid, st);
-        case DT_F16: return launch2<WF, DT_F16>(a, glu, argmax, grid, st);
+        case DT_F32: return launch2<WF, DT_F32>(a, glu, argmax, nw, grid, st);
+        case DT_BF16: return launch2<WF, DT_BF16>(a, glu, argmax, nw, grid, st);
+        case DT_F16: return launch2<WF, DT_F16>(a, glu, argmax, nw, grid, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int grid,
+hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream) {
     if (a.M < 1 || a.M > 32) return hipErrorInvalidValue;
+    if (nw != 4 && nw != 16) return hipErrorInvalidValue;
     switch (wf) {
-        case WF_F32: return launch1<WF_F32>(a, xdt, glu, argmax, grid, stream);
-        case WF_BF16: return launch1<WF_BF16>(a, xdt, glu, argmax, grid, stream);
-        case WF_I8: return launch1<WF_I8>(a, xdt, glu, argmax, grid, stream);
+        case WF_F32: return launch1<WF_F32>(a, xdt, glu, argmax, nw, grid, stream);
+        case WF_BF16: return launch1<WF_BF16>(a, xdt, glu, argmax, nw, grid, stream);
+        case WF_I8: return launch1<WF_I8>(a, xdt, glu, argmax, nw, grid, stream);
         default: return hipErrorInvalidValue;
     }
 }

@@ -27,7 +27,8 @@ EP_RESIDUAL, EP_NORM_X, EP_SPLIT = 1, 2, 4
 # every symbol include/qw_linear.h declares
 EXPORTS = [
     "qw_init", "qw_destroy", "qw_workspace_query", "qw_last_error", "qw_status_string",
-    "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_wrap_packed",
+    "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
+    "qw_weight_pack_glu_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_lmhead_argmax", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
@@ -75,6 +76,8 @@ def lib():
         "qw_abi_version": ([], _i),
         "qw_weight_pack": ([_vp, _vp, _i, _i, _i, _i, _vp, pp], _i),
         "qw_weight_pack_glu": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, pp], _i),
+        "qw_weight_pack_device": ([_vp, _vp, _i, _i, _i, _i, _vp, pp], _i),
+        "qw_weight_pack_glu_device": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, pp], _i),
         "qw_weight_wrap_packed": ([_vp, _vp, _vp, _i, _i, _i, pp], _i),
         "qw_weight_free": ([_vp], _i),
         "qw_weight_info": ([_vp, _vp, _vp, _vp, _vp, _vp], _i),
@@ -196,6 +199,30 @@ class Weight:
         ctx.check(lib().qw_weight_pack_glu(ctx.handle, gate.ctypes.data, up.ctypes.data, src, fmt, N, K,
                                            None if gs is None else gs.ctypes.data,
                                            None if us is None else us.ctypes.data, ctypes.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def pack_device(cls, ctx, w, fmt, scales=None):
+        """w: torch device tensor W[N][K] (float32/bfloat16/float16, or int8 with
+        device float32 scales)."""
+        import torch
+        code = I8 if w.dtype == torch.int8 else _torch_code(w)
+        N, K = w.shape
+        h = ctypes.c_void_p()
+        ctx.check(lib().qw_weight_pack_device(ctx.handle, w.data_ptr(), code, fmt, N, K,
+                                              None if scales is None else scales.data_ptr(), ctypes.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def pack_glu_device(cls, ctx, gate, up, fmt, gate_scales=None, up_scales=None):
+        import torch
+        code = I8 if gate.dtype == torch.int8 else _torch_code(gate)
+        N, K = gate.shape
+        h = ctypes.c_void_p()
+        ctx.check(lib().qw_weight_pack_glu_device(
+            ctx.handle, gate.data_ptr(), up.data_ptr(), code, fmt, N, K,
+            None if gate_scales is None else gate_scales.data_ptr(),
+            None if up_scales is None else up_scales.data_ptr(), ctypes.byref(h)))
         return cls(ctx, h)
 
     def unpack(self):

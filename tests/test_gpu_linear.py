@@ -321,3 +321,26 @@ def test_error_codes(qw, ctx, oracle):
     with pytest.raises(qw.QwError) as e:
         qw.linear(ctx, w, x, y, gamma=torch.zeros(128, device="cuda"), eps=0.0)
     assert e.value.status == qw.ERR_INVALID
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "int8"])
+def test_split_k_handoff_repeatable(qw, ctx, oracle, relerr, fmt):
+    """Split-K tiles (N=1024 over K=3584 is split across many waves): 200
+    back-to-back launches must all equal the first bitwise and the FP64
+    reference -- a partial read before its writer finished would show up as
+    a missing 1/S of the sum."""
+    f = {"bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
+    N, K, M = 1024, 3584, 2
+    W = oracle.normal((N, K), 91, 0.0, 0.02)
+    w = qw.Weight.pack(ctx, W, f)
+    x = oracle.normal((M, K), 92)
+    xt = dev(x, torch.float16 if fmt == "int8" else torch.bfloat16)
+    ys = torch.empty(200, M, N, device="cuda")
+    for i in range(200):
+        qw.linear(ctx, w, xt, ys[i])
+    torch.cuda.synchronize()
+    got = ys.cpu().numpy()
+    assert (got == got[0][None]).all()
+    xs = host(xt)
+    ref = oracle.linear_int8_f64(*w.unpack(), xs) if fmt == "int8" else oracle.linear_f64(oracle.round_bf16(W), xs)
+    assert relerr(got[0], ref) <= 2e-5
