@@ -22,6 +22,7 @@ struct qw_ctx {
     int wg_per_cu = 2;       // resident skinny workgroups per CU (grid cap)
     int min_items = 0;       // split K until a launch has this many items (0: never)
     int force_nw = 0;        // waves per skinny workgroup (0: automatic)
+    int force_nw_glu = 0;    // same, GLU weights only
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -32,6 +33,11 @@ struct qw_ctx {
     size_t partials_bytes = 0;
     uint8_t* scratch = nullptr;            // MLP intermediate
     size_t scratch_bytes = 0;
+    // optional weight arena: packed weights are carved from one large
+    // allocation (2 MiB aligned) instead of one hipMalloc each
+    uint8_t* arena = nullptr;
+    size_t arena_bytes = 0;
+    size_t arena_used = 0;
     std::string err;
 };
 
@@ -47,6 +53,7 @@ struct qw_weight {
     int ksteps = 0;
     size_t bytes = 0;
     bool owns = true;
+    bool in_arena = false;
 };
 
 struct qw_graph {
@@ -133,9 +140,15 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
         c->num_cus = prop.multiProcessorCount;
+    if (const char* v = getenv("QW_WEIGHT_ARENA_MB")) {
+        const size_t mb = (size_t)std::max(0, atoi(v));
+        if (mb && hipMalloc(&c->arena, mb << 20) == hipSuccess) c->arena_bytes = mb << 20;
+    }
     if (const char* v = getenv("QW_SKINNY_WG_PER_CU")) c->wg_per_cu = std::max(1, atoi(v));
     if (const char* v = getenv("QW_SKINNY_MIN_ITEMS")) c->min_items = std::max(0, atoi(v));
-    if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = (atoi(v) == 16) ? 16 : (atoi(v) == 4 ? 4 : 0);
+    auto nw_of = [](const char* v) { const int n = atoi(v); return (n == 4 || n == 8 || n == 16) ? n : 0; };
+    if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = nw_of(v);
+    if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(128, 8224, 3584);
     workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(1u << 20));
     workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
@@ -168,6 +181,7 @@ qw_status qw_destroy(qw_ctx* ctx) {
     if (!ctx) return QW_ERR_NULL;
     hipSetDevice(ctx->device);
     if (ctx->ws) hipFree(ctx->ws);
+    if (ctx->arena) hipFree(ctx->arena);
     delete ctx;
     return QW_OK;
 }
@@ -187,7 +201,12 @@ static qw_status alloc_weight(qw_ctx* ctx, qw_wfmt dst, int N, int K, int glu, q
     w->phys_tiles = tiles * (glu ? 2 : 1);
     w->ksteps = K / (4 * ke_of(dst));
     w->bytes = (size_t)w->phys_tiles * w->ksteps * 1024;
-    if (hipMalloc(&w->packed, w->bytes) != hipSuccess) {
+    const size_t need = (w->bytes + (2u << 20) - 1) & ~(size_t)((2u << 20) - 1);
+    if (ctx->arena && ctx->arena_used + need <= ctx->arena_bytes) {
+        w->packed = ctx->arena + ctx->arena_used;
+        ctx->arena_used += need;
+        w->in_arena = true;
+    } else if (hipMalloc(&w->packed, w->bytes) != hipSuccess) {
         delete w;
         return fail(ctx, QW_ERR_NOMEM, "hipMalloc of %zu bytes for packed weight failed", w->bytes);
     }
@@ -346,7 +365,7 @@ qw_status qw_weight_wrap_packed(qw_ctx* ctx, void* packed, float* scales, qw_wfm
 qw_status qw_weight_free(qw_weight* w) {
     if (!w) return QW_ERR_NULL;
     if (w->owns) {
-        if (w->packed) hipFree(w->packed);
+        if (w->packed && !w->in_arena) hipFree(w->packed);
         if (w->scales) hipFree(w->scales);
     }
     delete w;
@@ -433,15 +452,19 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     // 1024-row projections) -> 16 waves per tile so fewer CUs still keep
     // enough loads in flight.  K is split across workgroups only on request
     // (the split-K hand-off adds a device-coherent round trip).
-    const bool direct = (W->wf == QW_WFMT_BF16 && xdt == QW_BF16) || (W->wf == QW_WFMT_INT8_ROWSCALE && xdt == QW_F16) ||
-                        (W->wf == QW_WFMT_F32 && xdt == QW_F32);
-    const bool wide_ok = !argmax && !W->glu && M <= 16 && direct;
-    int nw = (wide_ok && a.n_groups * 4 < ctx->num_cus * 3) ? 16 : 4;
+    const bool wide_ok = !argmax && M <= 16;
+    int nw = (wide_ok && !W->glu && a.n_groups * 4 < ctx->num_cus * 3) ? 16 : 4;
     if (wide_ok && ctx->force_nw) nw = ctx->force_nw;
+    if (W->glu && ctx->force_nw_glu && wide_ok) nw = ctx->force_nw_glu;
     int S = 1;
     if (!argmax && ctx->min_items > a.n_groups) {
         const int want = (ctx->min_items + a.n_groups - 1) / a.n_groups;
         S = std::max(1, std::min(want, W->ksteps / nw));
+    }
+    // the activation slice of a split must fit the workgroup's LDS
+    while (qwk::skinny_lds_bytes(W->wf, (int)xdt, M, (W->ksteps + S - 1) / S) > qwk::kSkinnyMaxLds) {
+        if (argmax || S >= W->ksteps) return fail(ctx, QW_ERR_SHAPE, "K=%d too large for the skinny kernel", W->K);
+        ++S;
     }
     if (S > 1) {
         if (a.n_groups > kMaxCounters) return fail(ctx, QW_ERR_WORKSPACE, "too many split-K tiles");
@@ -477,7 +500,9 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     a.done = ctx->done;
     a.ids = ids;
     a.maxv = maxv;
-    const int grid = std::min(a.n_items, ctx->num_cus * ctx->wg_per_cu);
+    // a workgroup keeps one K split for its life: grid is a multiple of S
+    int grid = std::min(a.n_items, ctx->num_cus * ctx->wg_per_cu);
+    grid = std::max(S, grid - grid % S);
     if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * dsize(xdt) >= (1ull << 32))
         return fail(ctx, QW_ERR_SHAPE, "operands above 4 GiB are not supported");
     hipError_t e = qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream);

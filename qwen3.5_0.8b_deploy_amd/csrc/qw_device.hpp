@@ -38,11 +38,8 @@ template <> struct WTraits<WF_I8> { static constexpr int KE = 16; };
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    // round to nearest even (NaN stays NaN)
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    // round to nearest even; gfx950 converts in hardware (v_cvt_pk_bf16_f32)
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {

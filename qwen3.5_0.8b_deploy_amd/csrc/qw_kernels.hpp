@@ -39,18 +39,12 @@ struct SkinnyArgs {
     float* maxv;             // argmax values [M] or nullptr
 };
 
-// k-steps one wave holds in registers at a time (the loads of one chunk are
-// all issued together; the first chunk of the next item is issued before the
-// current item's reduction and epilogue).
-constexpr int skinny_unroll(int wf, int xdt, int ct, bool glu) {
-    const int ke = wf == 0 ? 4 : (wf == 1 ? 8 : 16);
-    const int xw = ke * (xdt == 0 ? 4 : 2) / 4;          // activation words per unit
-    const int per_unit = (glu ? 2 : 1) * 4 + ct * xw;
-    const int u = 96 / per_unit;
-    return u < 2 ? 2 : (u > 8 ? 8 : u);
-}
+// LDS the skinny kernel stages its activations in: (M+1) rows of the split's
+// K range in the MFMA input type (two planes when an FP32 activation feeds a
+// 16-bit MFMA), each row padded by 16 bytes.
+constexpr size_t kSkinnyMaxLds = 136 * 1024;
+size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split);
 
-// wf: 0 F32, 1 BF16, 2 INT8 ; xdt: 0 F32, 1 BF16, 2 F16
 // nw: waves per workgroup (4 or 16)
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream);

@@ -1,169 +1,265 @@
 // qw_skinny.hip -- small-M projection kernel for gfx950 (decode GEMV / skinny GEMM,
 // tied lm_head with fused greedy argmax).
 //
-// Work decomposition.  The unit of work is one wave64 "item": a 16-row output
-// tile (or a gate/up tile pair for GLU weights) over one slice of K.  Waves
-// are independent: a wave streams its weight k-steps straight from HBM into
-// MFMA A registers (1 KB fully coalesced non-temporal loads, see
-// qw_device.hpp), reads the matching activation fragment (L2 resident) as the
-// B operand, and accumulates 16 rows x 16 tokens per MFMA.  M <= 16 uses one
-// token column tile (CT=1), M <= 32 two.  When a tile has fewer rows than the
-// chip has waves to fill, K is split S ways; each split wave writes its FP32
-// partial tile to the workspace and the last of the S waves to arrive (an
-// agent-scope counter) sums the S partials in split order -- deterministic --
-// and runs the epilogue.  Counters are returned to zero by that wave, so the
-// kernel needs no memset and is safe to capture in a graph.
+// Data flow.  Weights stream once from HBM straight into MFMA A registers:
+// one k-step of a 16-row tile is a single fully coalesced 1 KB wave load in
+// the packed tile order of qw_device.hpp.  The activations of up to 32 tokens
+// are staged once per workgroup into LDS, already in the MFMA input type
+// (bf16, f16 or f32; an FP32 activation feeding a 16-bit MFMA is kept as a
+// hi + lo pair), with the RMSNorm weight (1 + gamma) folded in; the per-token
+// sums of squares for the RMSNorm are taken during the same staging pass.
+// Each k-step then costs one weight load, one or two ds_read_b128 and the
+// MFMAs (16 rows x 16 tokens each).  M <= 16 uses one token column tile
+// (CT = 1), M <= 32 two.
 //
-// Epilogue: per-row INT8 scale, RMSNorm of x (gamma folded into the B operand,
-// 1/rms applied to the accumulator), SiLU(gate)*up for GLU pairs, residual
-// add, Q/gate de-interleave, or -- for the lm_head -- a running (logit, index)
-// maximum per token that is merged across the grid with 64-bit atomic max on
-// an orderable key (ties resolve to the lowest index) and decoded by the last
-// wave of the grid.
+// Work decomposition.  An item is a 16-row output tile (a gate/up tile pair
+// for GLU weights) over one K split.  A workgroup of NW waves owns one item at
+// a time, its waves take contiguous pieces of the split, and their partial
+// tiles meet in LDS (fixed summation order).  Workgroups walk the items
+// grid-stride and keep one K split for their whole life, so the activation
+// staging happens once per workgroup; the weight loads of the next item are
+// issued before the current item's reduction and epilogue.  K is split across
+// workgroups only when the host asks for it (few output tiles, or an
+// activation slice too large for LDS); the last of the S workgroups of a tile
+// (agent-scope counter) sums the S partials in split order -- deterministic --
+// and runs the epilogue.  Counters return to zero, so no memset is needed and
+// the kernel can be captured in a graph.
+//
+// Epilogue: per-row INT8 scale, 1/rms of the RMSNorm, SiLU(gate)*up for GLU
+// pairs, residual add, Q/gate de-interleave, or -- for the lm_head -- a
+// running (logit, index) maximum per token merged across the grid with a
+// 64-bit atomic max on an orderable key (ties resolve to the lowest index)
+// and decoded by the last workgroup.
 //
 // Reference operators replaced: cutlass_style_gemv_kernel / _bf16 /
 // _fused_silu (cutlass_gemm_wrapper.cuh:41-200), int8_gemv_batch_kernel
 // (mlp_cuda.cu:158-180), lm_head_gemv_kernel_optimized (lm_head_cuda.cu:38-99)
 // + block_argmax_kernel (gpu_sampler_argmax.cu:14-43), and the thread-per-row
 // projection kernels of the attention operators.
+#include <type_traits>
+
 #include "qw_device.hpp"
 #include "qw_kernels.hpp"
 
 namespace qwk {
 
 constexpr unsigned EP_RESIDUAL = 1u, EP_NORM = 2u, EP_SPLIT = 4u;
+constexpr int AUX_NT = 2;  // buffer-load cache policy: non-temporal (streamed once)
 
 template <int XDT> struct XSize { static constexpr int v = (XDT == DT_F32) ? 4 : 2; };
 
-// Raw activation bits of one lane for one k-step unit (KE elements).
-template <int XDT, int KE> struct XRaw {
-    static constexpr int BYTES = KE * XSize<XDT>::v;
-    static constexpr int NW = BYTES / 4;
-    uint32_t w[NW];
-};
+// MFMA input type of a weight format: bf16 for BF16 weights, f16 for INT8
+// weights (exact for |q| <= 127), f32 for FP32 weights.
+template <int WF> struct OpSize { static constexpr int v = WF == WF_F32 ? 4 : 2; };
 
-template <int XDT, int KE>
-__device__ __forceinline__ void load_xraw(XRaw<XDT, KE>& r, const uint8_t* p) {
-    constexpr int B = XRaw<XDT, KE>::BYTES;
-    if constexpr (B >= 16) {
-#pragma unroll
-        for (int i = 0; i < B / 16; ++i) {
-            u32x4 v = reinterpret_cast<const u32x4*>(p)[i];
-            r.w[4 * i + 0] = v[0]; r.w[4 * i + 1] = v[1];
-            r.w[4 * i + 2] = v[2]; r.w[4 * i + 3] = v[3];
-        }
-    } else {
-        u32x2 v = *reinterpret_cast<const u32x2*>(p);
-        r.w[0] = v[0]; r.w[1] = v[1];
-    }
-}
-
-template <int XDT, int KE>
-__device__ __forceinline__ void zero_xraw(XRaw<XDT, KE>& r) {
-#pragma unroll
-    for (int i = 0; i < XRaw<XDT, KE>::NW; ++i) r.w[i] = 0u;
-}
-
-template <int XDT, int KE>
-__device__ __forceinline__ float xraw_elem(const XRaw<XDT, KE>& r, int e) {
-    if constexpr (XDT == DT_F32) {
-        return __uint_as_float(r.w[e]);
-    } else {
-        uint32_t h = (r.w[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-        return XDT == DT_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
-    }
-}
-
-// Whether x needs a hi/lo split to keep its precision through the MFMA input type.
+// Whether the activation needs a hi + lo pair to keep its precision through a
+// 16-bit MFMA input.
 template <int WF, int XDT> struct XSplit {
     static constexpr bool v = (WF == WF_BF16 && XDT != DT_BF16) || (WF == WF_I8 && XDT == DT_F32);
 };
-// Whether the raw x bits already are the MFMA input type.
-template <int WF, int XDT> struct XDirect {
-    static constexpr bool v = (WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16);
-};
 
-// B operands of one unit for one token tile.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    // raw (untyped) buffer: stride 0, num_records = bytes; loads past the end return 0
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// ---------------------------------------------------------------------------
+// LDS layout of the staged activations: nops planes (hi, lo) of (M + 1) rows
+// of `ls` op-elements; row M is all zero and serves tokens >= M.  The row
+// stride carries a 16-byte pad to spread the rows over the LDS banks.
+// ---------------------------------------------------------------------------
+template <int WF>
+__device__ __forceinline__ int lds_row_elems(int kr) { return kr + 16 / OpSize<WF>::v; }
+
+template <int WF>
+__device__ __forceinline__ uint32_t op_bits(float f) {
+    if constexpr (WF == WF_BF16) return f32_to_bf16_bits(f);
+    else if constexpr (WF == WF_I8) return f32_to_f16_bits(f);
+    else return __float_as_uint(f);
+}
+template <int WF>
+__device__ __forceinline__ float op_value(uint32_t h) {
+    if constexpr (WF == WF_BF16) return bf16_bits_to_f32(h);
+    else if constexpr (WF == WF_I8) return f16_bits_to_f32(h);
+    else return __uint_as_float(h);
+}
+
+// Activation staging, split in two so the small activation loads are issued
+// BEFORE the weight stream (vector-memory counters retire in order: a load
+// issued after the weights could only be consumed after all of them).
+// Thread t owns row t % RP (RP = M+1 rounded up to a power of two) and the
+// row's 8-element chunks j0, j0 + NT/RP, ...; the first SQ chunks are loaded
+// by stage_issue, stage_finish converts them (times 1 + gamma), writes them
+// to LDS and handles any further chunks.  Row M is all zero.
+template <int XDT, int SQ>
+struct XStage {
+    static constexpr int XB = 8 * XSize<XDT>::v;  // bytes of one raw chunk
+    u32x4 raw[SQ][XB / 16];
+    f32x4 gam[SQ][2];
+    int m, j0, tpr, nchunk;
+    float ss;
+};
+template <int XDT> struct XChunk { static constexpr int XB = 8 * XSize<XDT>::v; };
+
+// Buffer loads are range-checked on their VGPR offset only (the scalar
+// offset is not part of the check); a VGPR offset with the top bit set is out
+// of range and returns zeros without a memory access.  Loads that are not
+// wanted are issued that way instead of being skipped, so every path issues
+// the same number of loads and the compiler can wait for each one precisely.
+constexpr uint32_t OOB = 0x80000000u;
+
+template <int XDT, bool NORM>
+__device__ __forceinline__ void stage_load(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr,
+                                           int k0, int c, int m, bool valid, u32x4 (&raw)[XChunk<XDT>::XB / 16],
+                                           f32x4 (&gam)[2]) {
+    constexpr int XB = XChunk<XDT>::XB;
+    const uint32_t xo = valid && m < a.M ? (uint32_t)(((int64_t)m * a.ldx + k0 + c * 8) * XSize<XDT>::v) : OOB;
+#pragma unroll
+    for (int h = 0; h < XB / 16; ++h)
+        raw[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 16 * h, 0, 0));
+    if constexpr (NORM) {
+        const uint32_t go = valid ? (uint32_t)((k0 + c * 8) * 4) : OOB;
+        gam[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, go, 0, 0));
+        gam[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, go + 16, 0, 0));
+    }
+}
+
+template <int WF, int XDT, int NW, int SQ, bool NORM>
+__device__ __forceinline__ void stage_issue(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr,
+                                            int k0, int kr, XStage<XDT, SQ>& st) {
+    constexpr int NT = NW * 64;
+    int rp = 1;
+    while (rp < a.M + 1) rp <<= 1;  // <= 64
+    st.m = threadIdx.x & (rp - 1);
+    st.tpr = NT / rp;
+    st.j0 = threadIdx.x / rp;
+    st.nchunk = kr / 8;
+    st.ss = 0.0f;
+#pragma unroll
+    for (int q = 0; q < SQ; ++q) {
+        const int c = st.j0 + q * st.tpr;
+        stage_load<XDT, NORM>(a, xr, gr, k0, c, st.m, c < st.nchunk && st.m <= a.M, st.raw[q], st.gam[q]);
+    }
+}
+
+template <int WF, int XDT, bool NORM>
+__device__ __forceinline__ void stage_store(const SkinnyArgs& a, int c, int ls, int plane, uint8_t* xs,
+                                            const u32x4 (&raw)[XChunk<XDT>::XB / 16], const f32x4 (&gam)[2], int m,
+                                            float& ss) {
+    constexpr int OS = OpSize<WF>::v;
+    constexpr bool SPLIT = XSplit<WF, XDT>::v;
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        if constexpr (XDT == DT_F32) {
+            f[e] = __uint_as_float(raw[e >> 2][e & 3]);
+        } else {
+            const uint32_t hb = (raw[0][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+            f[e] = XDT == DT_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+        }
+    }
+    if constexpr (NORM) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] *= 1.0f + gam[e >> 2][e & 3];
+    }
+    uint8_t* dst = xs + ((int64_t)m * ls + c * 8) * OS;
+    if constexpr (OS == 4) {
+        reinterpret_cast<f32x4*>(dst)[0] = f32x4{f[0], f[1], f[2], f[3]};
+        reinterpret_cast<f32x4*>(dst)[1] = f32x4{f[4], f[5], f[6], f[7]};
+    } else {
+        u32x4 hi, lo;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t h0 = op_bits<WF>(f[2 * p]), h1 = op_bits<WF>(f[2 * p + 1]);
+            hi[p] = h0 | (h1 << 16);
+            if constexpr (SPLIT) {
+                const uint32_t l0 = op_bits<WF>(f[2 * p] - op_value<WF>(h0));
+                const uint32_t l1 = op_bits<WF>(f[2 * p + 1] - op_value<WF>(h1));
+                lo[p] = l0 | (l1 << 16);
+            }
+        }
+        *reinterpret_cast<u32x4*>(dst) = hi;
+        if constexpr (SPLIT) *reinterpret_cast<u32x4*>(dst + (int64_t)plane * OS) = lo;
+    }
+}
+
+// Finish the staging; per-token sums of squares of the raw activations over
+// the range go to ss_tok (LDS), reduced in a fixed order.
+template <int WF, int XDT, int CT, int NW, int SQ, bool NORM>
+__device__ void stage_finish(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, int k0,
+                             int kr, XStage<XDT, SQ>& st, uint8_t* xs, float* ss_tok, float* ss_scratch) {
+    constexpr int ROWS = CT * 16;
+    const int ls = lds_row_elems<WF>(kr);
+    const int plane = (a.M + 1) * ls;
+    if (st.m <= a.M) {
+#pragma unroll
+        for (int q = 0; q < SQ; ++q) {
+            const int c = st.j0 + q * st.tpr;
+            if (c < st.nchunk) stage_store<WF, XDT, NORM>(a, c, ls, plane, xs, st.raw[q], st.gam[q], st.m, st.ss);
+        }
+        for (int c = st.j0 + SQ * st.tpr; c < st.nchunk; c += st.tpr) {
+            u32x4 raw[XChunk<XDT>::XB / 16];
+            f32x4 gam[2];
+            stage_load<XDT, NORM>(a, xr, gr, k0, c, st.m, true, raw, gam);
+            stage_store<WF, XDT, NORM>(a, c, ls, plane, xs, raw, gam, st.m, st.ss);
+        }
+    }
+    if constexpr (NORM) {
+        int rp = 1;
+        while (rp < a.M + 1) rp <<= 1;
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        float ss = st.ss;
+        for (int off = rp; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
+        if (lane < rp && lane < ROWS) ss_scratch[wave * ROWS + lane] = ss;
+        __syncthreads();
+        if (threadIdx.x < ROWS) {
+            float t = 0.0f;
+            for (int w = 0; w < NW; ++w) t += (threadIdx.x < rp) ? ss_scratch[w * ROWS + threadIdx.x] : 0.0f;
+            ss_tok[threadIdx.x] = t;
+        }
+    }
+}
+
+// B operands of one k-step unit for one token tile, read from LDS.
 template <int WF, int XDT> struct BOps;
 template <int XDT> struct BOps<WF_BF16, XDT> { bf16x8 hi, lo; };
 template <int XDT> struct BOps<WF_I8, XDT> { f16x8 hi0, hi1, lo0, lo1; };
-template <int XDT> struct BOps<WF_F32, XDT> { float v[4]; };
+template <int XDT> struct BOps<WF_F32, XDT> { f32x4 v; };
 
-template <int WF, int XDT, int KE>
-__device__ __forceinline__ void make_bops(BOps<WF, XDT>& b, const XRaw<XDT, KE>& r, bool norm,
-                                          const float* gam) {
-    if constexpr (WF == WF_F32) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float f = xraw_elem(r, e);
-            b.v[e] = norm ? f * (1.0f + gam[e]) : f;
+template <int WF, int XDT>
+__device__ __forceinline__ void read_bops(BOps<WF, XDT>& b, const uint8_t* p, int plane_bytes) {
+    constexpr bool SPLIT = XSplit<WF, XDT>::v;
+    if constexpr (WF == WF_BF16) {
+        b.hi = *reinterpret_cast<const bf16x8*>(p);
+        if constexpr (SPLIT) b.lo = *reinterpret_cast<const bf16x8*>(p + plane_bytes);
+    } else if constexpr (WF == WF_I8) {
+        b.hi0 = reinterpret_cast<const f16x8*>(p)[0];
+        b.hi1 = reinterpret_cast<const f16x8*>(p)[1];
+        if constexpr (SPLIT) {
+            b.lo0 = reinterpret_cast<const f16x8*>(p + plane_bytes)[0];
+            b.lo1 = reinterpret_cast<const f16x8*>(p + plane_bytes)[1];
         }
-    } else if constexpr (WF == WF_BF16) {
-        if (XDirect<WF, XDT>::v && !norm) {
-            u32x4 t = {r.w[0], r.w[1], r.w[2], r.w[3]};
-            b.hi = __builtin_bit_cast(bf16x8, t);
-            return;
-        }
-        u32x4 th, tl;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            float f0 = xraw_elem(r, 2 * p), f1 = xraw_elem(r, 2 * p + 1);
-            if (norm) { f0 *= 1.0f + gam[2 * p]; f1 *= 1.0f + gam[2 * p + 1]; }
-            uint32_t h0 = f32_to_bf16_bits(f0), h1 = f32_to_bf16_bits(f1);
-            th[p] = h0 | (h1 << 16);
-            if constexpr (XSplit<WF, XDT>::v) {
-                uint32_t l0 = f32_to_bf16_bits(f0 - bf16_bits_to_f32(h0));
-                uint32_t l1 = f32_to_bf16_bits(f1 - bf16_bits_to_f32(h1));
-                tl[p] = l0 | (l1 << 16);
-            }
-        }
-        b.hi = __builtin_bit_cast(bf16x8, th);
-        if constexpr (XSplit<WF, XDT>::v) b.lo = __builtin_bit_cast(bf16x8, tl);
-    } else {  // WF_I8: f16 MFMA, 16 elements -> two operands
-        if (XDirect<WF, XDT>::v && !norm) {
-            u32x4 t0 = {r.w[0], r.w[1], r.w[2], r.w[3]};
-            u32x4 t1 = {r.w[4], r.w[5], r.w[6], r.w[7]};
-            b.hi0 = __builtin_bit_cast(f16x8, t0);
-            b.hi1 = __builtin_bit_cast(f16x8, t1);
-            return;
-        }
-        u32x4 th0, th1, tl0, tl1;
-#pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            float f0 = xraw_elem(r, 2 * p), f1 = xraw_elem(r, 2 * p + 1);
-            if (norm) { f0 *= 1.0f + gam[2 * p]; f1 *= 1.0f + gam[2 * p + 1]; }
-            uint32_t h0 = f32_to_f16_bits(f0), h1 = f32_to_f16_bits(f1);
-            uint32_t hv = h0 | (h1 << 16);
-            uint32_t lv = 0;
-            if constexpr (XSplit<WF, XDT>::v) {
-                uint32_t l0 = f32_to_f16_bits(f0 - f16_bits_to_f32(h0));
-                uint32_t l1 = f32_to_f16_bits(f1 - f16_bits_to_f32(h1));
-                lv = l0 | (l1 << 16);
-            }
-            if (p < 4) { th0[p] = hv; tl0[p] = lv; } else { th1[p - 4] = hv; tl1[p - 4] = lv; }
-        }
-        b.hi0 = __builtin_bit_cast(f16x8, th0);
-        b.hi1 = __builtin_bit_cast(f16x8, th1);
-        if constexpr (XSplit<WF, XDT>::v) {
-            b.lo0 = __builtin_bit_cast(f16x8, tl0);
-            b.lo1 = __builtin_bit_cast(f16x8, tl1);
-        }
+    } else {
+        b.v = *reinterpret_cast<const f32x4*>(p);
     }
 }
 
 // acc += A(unit) x B(unit)
 template <int WF, int XDT>
 __device__ __forceinline__ f32x4 unit_mfma(u32x4 a, const BOps<WF, XDT>& b, f32x4 acc) {
+    constexpr bool SPLIT = XSplit<WF, XDT>::v;
     if constexpr (WF == WF_BF16) {
         bf16x8 av = __builtin_bit_cast(bf16x8, a);
         acc = mfma_bf16(av, b.hi, acc);
-        if constexpr (XSplit<WF, XDT>::v) acc = mfma_bf16(av, b.lo, acc);
+        if constexpr (SPLIT) acc = mfma_bf16(av, b.lo, acc);
     } else if constexpr (WF == WF_I8) {
         f16x8 a0, a1;
         i8unit_to_f16(a, a0, a1);
         acc = mfma_f16(a0, b.hi0, acc);
         acc = mfma_f16(a1, b.hi1, acc);
-        if constexpr (XSplit<WF, XDT>::v) {
+        if constexpr (SPLIT) {
             acc = mfma_f16(a0, b.lo0, acc);
             acc = mfma_f16(a1, b.lo1, acc);
         }
@@ -174,114 +270,91 @@ __device__ __forceinline__ f32x4 unit_mfma(u32x4 a, const BOps<WF, XDT>& b, f32x
     return acc;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    // raw (untyped) buffer: stride 0, num_records = bytes; loads past the end return 0
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-constexpr int AUX_NT = 2;  // non-temporal (streamed once)
-
-template <int XDT, int KE>
-__device__ __forceinline__ void buf_load_xraw(XRaw<XDT, KE>& r, __amdgpu_buffer_rsrc_t rs, uint32_t voff,
-                                              uint32_t soff) {
-    constexpr int B = XRaw<XDT, KE>::BYTES;
-    if constexpr (B >= 16) {
-#pragma unroll
-        for (int i = 0; i < B / 16; ++i) {
-            u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 16 * i, soff, 0));
-            r.w[4 * i + 0] = v[0]; r.w[4 * i + 1] = v[1];
-            r.w[4 * i + 2] = v[2]; r.w[4 * i + 3] = v[3];
-        }
-    } else {
-        u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0));
-        r.w[0] = v[0]; r.w[1] = v[1];
-    }
-}
-
-// Per-item epilogue operands, loaded before the item's weights so that they
-// never form a dependent memory round trip after the weight stream.
+// ---------------------------------------------------------------------------
+// epilogue operands, issued with the weights and kept as raw bits until used
+// ---------------------------------------------------------------------------
 template <int RT, int CT>
 struct EpiOps {
-    f32x4 sc[RT];
-    f32x4 res[CT];
+    u32x4 sc[RT];     // 4 FP32 scales of this lane's rows
+    u32x4 res32[CT];  // residual, FP32 rows
+    u32x2 res16[CT];  // residual, 16-bit rows
 };
 
 template <int RT, int CT>
-__device__ __forceinline__ void load_epi(const SkinnyArgs& a, int grp, int lane, bool want_res,
-                                         EpiOps<RT, CT>& e) {
+__device__ __forceinline__ void load_epi(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t rr,
+                                         int grp, bool valid, int lane, EpiOps<RT, CT>& e) {
     const int r = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-        e.sc[rt] = a.scales ? *reinterpret_cast<const f32x4*>(a.scales + (int64_t)(grp * RT + rt) * 16 + g * 4)
-                            : f32x4{1.f, 1.f, 1.f, 1.f};
+    for (int rt = 0; rt < RT; ++rt) {  // the scale buffer is empty for non-INT8 weights
+        const uint32_t so = valid ? (uint32_t)(((grp * RT + rt) * 16 + g * 4) * 4) : OOB;
+        e.sc[rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, so, 0, 0));
+    }
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-        e.res[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int ct = 0; ct < CT; ++ct) {  // the residual buffer is empty without a residual
         const int m = ct * 16 + r;
         const int o = grp * 16 + g * 4;
-        if (want_res && m < a.M && o < a.N) {
-            if (a.vec_store) {
-                e.res[ct] = load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + o);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (o + i < a.N) e.res[ct][i] = load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + o + i);
-            }
-        }
+        const bool ok = valid && a.vec_store && m < a.M && o < a.N;
+        const uint32_t i = (uint32_t)((int64_t)m * a.ld_res + o);
+        const bool f32 = a.res_dt == DT_F32;
+        e.res32[ct] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, ok && f32 ? i * 4 : OOB, 0, 0));
+        e.res16[ct] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rr, ok && !f32 ? i * 2 : OOB, 0, 0));
     }
 }
 
-// This wave's k sub-range [kb, kend) of an item: the item's K split is cut
-// into NW contiguous pieces, one per wave of the workgroup.
+__device__ __forceinline__ f32x4 as_f32x4(u32x4 v) {
+    return f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+
+__device__ __forceinline__ f32x4 epi_res(int dt, u32x4 r32, u32x2 r16) {
+    if (dt == DT_F32) return as_f32x4(r32);
+    f32x4 v;
+    if (dt == DT_BF16) {
+        v[0] = bf16_bits_to_f32(r16[0] & 0xffffu); v[1] = bf16_bits_to_f32(r16[0] >> 16);
+        v[2] = bf16_bits_to_f32(r16[1] & 0xffffu); v[3] = bf16_bits_to_f32(r16[1] >> 16);
+    } else {
+        v[0] = f16_bits_to_f32(r16[0] & 0xffffu); v[1] = f16_bits_to_f32(r16[0] >> 16);
+        v[2] = f16_bits_to_f32(r16[1] & 0xffffu); v[3] = f16_bits_to_f32(r16[1] >> 16);
+    }
+    return v;
+}
+
+// This wave's k-step range [kb, kend) within the split [ks0, ks1).
 template <int NW>
-__device__ __forceinline__ void item_range(const SkinnyArgs& a, int item, int wave_id, int& kb, int& kend) {
-    const int grp = item / a.S;
-    const int s = item - grp * a.S;
-    const int ks0 = (int)(((int64_t)s * a.ksteps) / a.S);
-    const int ks1 = (int)(((int64_t)(s + 1) * a.ksteps) / a.S);
+__device__ __forceinline__ void wave_range(int ks0, int ks1, int wave_id, int& kb, int& kend) {
     const int cnt = ks1 - ks0;
     kb = ks0 + (wave_id * cnt) / NW;
     kend = ks0 + ((wave_id + 1) * cnt) / NW;
 }
 
-// Issue the loads of k-steps [kb, kb+n) (n <= U) of tile group grp.
-template <int WF, int XDT, int CT, int RT, int U>
-__device__ __forceinline__ void issue_chunk(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t wrs,
-                                            __amdgpu_buffer_rsrc_t xrs, uint32_t xvoff[CT], int grp,
-                                            int kb, int n, int lane, u32x4 (&A)[U][RT],
-                                            XRaw<XDT, WTraits<WF>::KE> (&X)[U][CT]) {
-    constexpr int KE = WTraits<WF>::KE;
+// Issue the weight loads of k-steps [kb, kb+n) (n <= U) of tile group grp.
+// Issue the weight loads of k-steps [kb, kb+n) (n <= U) of tile group grp;
+// the U - n unused slots are issued out of range (zeros, no traffic).
+template <int RT, int U>
+__device__ __forceinline__ void issue_weights(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t wrs, int grp, int kb,
+                                              int n, int lane, u32x4 (&A)[U][RT]) {
     const uint32_t tile_bytes = (uint32_t)a.ksteps * 1024u;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        if (u < n) {
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-                A[u][rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         wrs, lane * 16, (uint32_t)(grp * RT + rt) * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
-#pragma unroll
-            for (int ct = 0; ct < CT; ++ct)
-                buf_load_xraw<XDT, KE>(X[u][ct], xrs, xvoff[ct], (uint32_t)(kb + u) * (4 * KE) * XSize<XDT>::v);
-        }
-    }
+        for (int rt = 0; rt < RT; ++rt)
+            A[u][rt] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           wrs, u < n ? lane * 16 : OOB,
+                           (uint32_t)(grp * RT + rt) * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
 }
 
-// Work decomposition (see the file header): a workgroup of NW waves owns one
-// item at a time -- a 16-row tile (two for GLU) over one K split -- and its
-// waves take contiguous pieces of that split; partial tiles meet in LDS.
-// Workgroups walk the items grid-stride, and the loads of the next item are
-// issued before the current item's reduction and epilogue.  The RMSNorm
-// statistics come from the activation fragments already in registers.
 template <int WF, int XDT, int CT, bool GLU, bool ARGMAX, int NW>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
-    constexpr int U = NW == 16 ? (WF == WF_I8 ? 2 : 4) : skinny_unroll(WF, XDT, CT, GLU);
+    constexpr int U = (GLU && NW == 16) ? 4 : 8;
     constexpr int KE = WTraits<WF>::KE;
     constexpr int RT = GLU ? 2 : 1;
     constexpr int F = RT * CT;
-    using XR = XRaw<XDT, KE>;
+    constexpr int ROWS = CT * 16;
+    constexpr int OS = OpSize<WF>::v;
     __shared__ f32x4 red[NW][F][64];
-    __shared__ float ssred[NW][CT][64];
-    extern __shared__ float gam_s[];  // K floats when the norm prologue is on
+    __shared__ float ss_tok[ROWS];
+    __shared__ float ss_scratch[NW * ROWS];
+    extern __shared__ uint8_t xs[];  // staged activations
 
     const int lane = threadIdx.x & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -290,125 +363,138 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
     const bool norm = (a.flags & EP_NORM) != 0;
     const bool want_res = !ARGMAX && (a.flags & EP_RESIDUAL);
 
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * RT * a.ksteps * 1024u));
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * XSize<XDT>::v));
-    uint32_t xvoff[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)   // tokens >= M fall outside the buffer and read as 0
-        xvoff[ct] = (uint32_t)(((ct * 16 + r) * a.ldx + g * KE) * XSize<XDT>::v);
+    // this workgroup's K split (constant: the host makes gridDim.x % S == 0)
+    const int s = blockIdx.x % a.S;
+    const int ks0 = (int)(((int64_t)s * a.ksteps) / a.S);
+    const int ks1 = (int)(((int64_t)(s + 1) * a.ksteps) / a.S);
+    int kb, kend;
+    wave_range<NW>(ks0, ks1, wave_id, kb, kend);
+    const int kb0 = kb;
 
-    if (norm) {
-        for (int i = threadIdx.x; i < a.K / 4; i += NW * 64)
-            reinterpret_cast<f32x4*>(gam_s)[i] = reinterpret_cast<const f32x4*>(a.gamma)[i];
-    }
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * RT * a.ksteps * 1024u));
 
     unsigned long long best[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) best[ct] = 0ull;
 
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * XSize<XDT>::v));
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? (const void*)a.gamma : a.x, norm ? (uint32_t)a.K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)a.n_groups * RT * 64u : 0u);
+    const int res_size = a.res_dt == DT_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(want_res ? a.res : a.x, want_res ? (uint32_t)((uint64_t)a.M * a.ld_res * res_size) : 0u);
+
     u32x4 A[U][RT];
-    XR X[U][CT];
     EpiOps<RT, CT> epi, epi_next;
-    int kb = 0, kend = 0, n = 0;
     int item = blockIdx.x;
-    if (item < a.n_items) {
-        if (wave_id == 0) load_epi<RT, CT>(a, item / a.S, lane, want_res, epi);
-        item_range<NW>(a, item, wave_id, kb, kend);
-        n = min(U, kend - kb);
-        issue_chunk<WF, XDT, CT, RT, U>(a, wrs, xrs, xvoff, item / a.S, kb, n, lane, A, X);
+    int n = min(U, kend - kb);
+    // activation loads first, then the epilogue operands, then the weights;
+    // the activations are converted into LDS while the weights stream in
+    const int kr = (ks1 - ks0) * 4 * KE;
+    // chunks of 8 activations each thread stages (1, 2 or 4 up front)
+    int rp = 1;
+    while (rp < a.M + 1) rp <<= 1;
+    const int cpt = (kr / 8 + NW * 64 / rp - 1) / (NW * 64 / rp);
+    auto prologue = [&](auto sq_tag, auto norm_tag) {
+        constexpr int SQ = decltype(sq_tag)::value;
+        constexpr bool NORM = decltype(norm_tag)::value;
+        XStage<XDT, SQ> st;
+        stage_issue<WF, XDT, NW, SQ, NORM>(a, xr, gr, ks0 * 4 * KE, kr, st);
+        load_epi<RT, CT>(a, sr, rr, item / a.S, item < a.n_items, lane, epi);
+        __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the weight stream
+        issue_weights<RT, U>(a, wrs, item / a.S, kb, item < a.n_items ? n : 0, lane, A);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_finish<WF, XDT, CT, NW, SQ, NORM>(a, xr, gr, ks0 * 4 * KE, kr, st, xs, ss_tok, ss_scratch);
+    };
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I4 = std::integral_constant<int, 4>;
+    if (norm) {
+        if (cpt <= 1) prologue(I1{}, std::true_type{});
+        else if (cpt <= 2) prologue(I2{}, std::true_type{});
+        else prologue(I4{}, std::true_type{});
+    } else {
+        if (cpt <= 1) prologue(I1{}, std::false_type{});
+        else if (cpt <= 2) prologue(I2{}, std::false_type{});
+        else prologue(I4{}, std::false_type{});
     }
-    __syncthreads();  // gamma staged
+    __syncthreads();
+
+    const int ls = lds_row_elems<WF>(kr);
+    const int plane_bytes = (a.M + 1) * ls * OS;
+    int xrow[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) xrow[ct] = min(ct * 16 + r, a.M);
 
     while (item < a.n_items) {
         f32x4 acc[RT][CT];
-        float ss[CT];
 #pragma unroll
-        for (int j = 0; j < CT; ++j) {
-            ss[j] = 0.0f;
+        for (int j = 0; j < CT; ++j)
 #pragma unroll
             for (int i = 0; i < RT; ++i) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
         for (;;) {
+            if (n == U) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (u < n) {
-                    float gam[KE];
-                    if (norm) {
-                        const float* gp = gam_s + (kb + u) * (4 * KE) + g * KE;
-#pragma unroll
-                        for (int e = 0; e < KE; e += 4) {
-                            f32x4 gv = *reinterpret_cast<const f32x4*>(gp + e);
-                            gam[e] = gv[0]; gam[e + 1] = gv[1]; gam[e + 2] = gv[2]; gam[e + 3] = gv[3];
-                        }
-#pragma unroll
-                        for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-                            for (int e = 0; e < KE; ++e) {
-                                const float xv = xraw_elem(X[u][ct], e);
-                                ss[ct] += xv * xv;
-                            }
-                    }
+                for (int u = 0; u < U; ++u) {
+                    const int relk = (kb + u - ks0) * 4 * KE + g * KE;
 #pragma unroll
                     for (int ct = 0; ct < CT; ++ct) {
                         BOps<WF, XDT> b;
-                        make_bops<WF, XDT, KE>(b, X[u][ct], norm, gam);
+                        read_bops<WF, XDT>(b, xs + ((int64_t)xrow[ct] * ls + relk) * OS, plane_bytes);
 #pragma unroll
                         for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = unit_mfma<WF, XDT>(A[u][rt], b, acc[rt][ct]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    if (u < n) {
+                        const int relk = (kb + u - ks0) * 4 * KE + g * KE;
+#pragma unroll
+                        for (int ct = 0; ct < CT; ++ct) {
+                            BOps<WF, XDT> b;
+                            read_bops<WF, XDT>(b, xs + ((int64_t)xrow[ct] * ls + relk) * OS, plane_bytes);
+#pragma unroll
+                            for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = unit_mfma<WF, XDT>(A[u][rt], b, acc[rt][ct]);
+                        }
                     }
                 }
             }
             kb += n;
             if (kb >= kend) break;
             n = min(U, kend - kb);
-            issue_chunk<WF, XDT, CT, RT, U>(a, wrs, xrs, xvoff, item / a.S, kb, n, lane, A, X);
+            issue_weights<RT, U>(a, wrs, item / a.S, kb, n, lane, A);
         }
         const int cur = item;
         item += gridDim.x;
-        if (item < a.n_items) {
-            if (wave_id == 0) load_epi<RT, CT>(a, item / a.S, lane, want_res, epi_next);
-            item_range<NW>(a, item, wave_id, kb, kend);
-            n = min(U, kend - kb);
-            issue_chunk<WF, XDT, CT, RT, U>(a, wrs, xrs, xvoff, item / a.S, kb, n, lane, A, X);
-        }
+        kb = kb0;
+        n = min(U, kend - kb);
+        load_epi<RT, CT>(a, sr, rr, item / a.S, item < a.n_items, lane, epi_next);
+        issue_weights<RT, U>(a, wrs, item / a.S, kb, item < a.n_items ? n : 0, lane, A);
 
         // ---- reduce the NW pieces in LDS (fixed order) ----
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) red[wave_id][rt * CT + ct][lane] = acc[rt][ct];
-        if (norm) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < F * 64; t += NW * 64) {
+            const int f = t >> 6, l = t & 63;
+            f32x4 sum = red[0][f][l];
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct) ssred[wave_id][ct][lane] = ss[ct];
+            for (int w = 1; w < NW; ++w) sum += red[w][f][l];
+            red[0][f][l] = sum;
         }
         __syncthreads();
-        if (NW > 1) {
-            for (int t = threadIdx.x; t < F * 64; t += NW * 64) {
-                const int f = t >> 6, l = t & 63;
-                f32x4 sum = red[0][f][l];
-#pragma unroll
-                for (int w = 1; w < NW; ++w) sum += red[w][f][l];
-                red[0][f][l] = sum;
-            }
-            if (norm) {
-                for (int t = threadIdx.x; t < CT * 64; t += NW * 64) {
-                    const int c = t >> 6, l = t & 63;
-                    float sum = ssred[0][c][l];
-#pragma unroll
-                    for (int w = 1; w < NW; ++w) sum += ssred[w][c][l];
-                    ssred[0][c][l] = sum;
-                }
-            }
-            __syncthreads();
-        }
         if (wave_id != 0) continue;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = red[0][rt * CT + ct][lane];
-        if (norm) {
+        float ss[CT];
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct) ss[ct] = ssred[0][ct][lane];
-        }
+        for (int ct = 0; ct < CT; ++ct) ss[ct] = norm ? ss_tok[ct * 16 + r] : 0.0f;
         EpiOps<RT, CT> e = epi;
         epi = epi_next;
 
@@ -417,13 +503,13 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
         if constexpr (!ARGMAX) {
             if (a.S > 1) {
                 // Cross-workgroup split-K hand-off, no fence: the partial tile
-                // (and the partial sum of squares) go out as agent-scope atomic
-                // stores (written through to the device coherence point),
-                // s_waitcnt vmcnt(0) waits for their completion, then the
-                // agent-scope counter increment.  The last of the S workgroups
-                // reads the S partials back with agent-scope atomic loads, in
-                // split order (deterministic), and returns the counter to 0.
-                const int s = cur - grp * a.S;
+                // (and the partial sums of squares) go out as agent-scope
+                // atomic stores (written through to the device coherence
+                // point), s_waitcnt vmcnt(0) waits for their completion, then
+                // the agent-scope counter increment.  The last of the S
+                // workgroups reads the S partials back with agent-scope atomic
+                // loads, in split order (deterministic), and returns the
+                // counter to zero.
                 constexpr int REC = F * 4 + CT;  // floats per lane per split
                 float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)grp * a.S * 64 + lane) * REC;
                 float* mine = P + (int64_t)s * 64 * REC;
@@ -433,11 +519,9 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                     for (int i = 0; i < 4; ++i)
                         __hip_atomic_store(mine + f * 4 + i, acc[f / CT][f % CT][i], __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
-                if (norm) {
 #pragma unroll
-                    for (int ct = 0; ct < CT; ++ct)
-                        __hip_atomic_store(mine + F * 4 + ct, ss[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+                for (int ct = 0; ct < CT; ++ct)
+                    __hip_atomic_store(mine + F * 4 + ct, ss[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 unsigned old = 0;
                 if (lane == 0)
@@ -459,11 +543,9 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                             for (int i = 0; i < 4; ++i)
                                 acc[f / CT][f % CT][i] += __hip_atomic_load(q + f * 4 + i, __ATOMIC_RELAXED,
                                                                             __HIP_MEMORY_SCOPE_AGENT);
-                        if (norm) {
 #pragma unroll
-                            for (int ct = 0; ct < CT; ++ct)
-                                ss[ct] += __hip_atomic_load(q + F * 4 + ct, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        }
+                        for (int ct = 0; ct < CT; ++ct)
+                            ss[ct] += __hip_atomic_load(q + F * 4 + ct, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                     if (lane == 0)
                         __hip_atomic_store(&a.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -474,15 +556,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
 
         float inv[CT];
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-            inv[ct] = 1.0f;
-            if (norm) {
-                float t = ss[ct];
-                t += __shfl_xor(t, 16);
-                t += __shfl_xor(t, 32);
-                inv[ct] = 1.0f / sqrtf(t / (float)a.K + a.eps);
-            }
-        }
+        for (int ct = 0; ct < CT; ++ct) inv[ct] = norm ? 1.0f / sqrtf(ss[ct] / (float)a.K + a.eps) : 1.0f;
 
         // ---- epilogue (wave 0) ----
         const int o = grp * 16 + g * 4;  // first of this lane's 4 logical rows
@@ -491,12 +565,17 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
             const int m = ct * 16 + r;
             f32x4 v;
             if constexpr (GLU) {
-                f32x4 gt = acc[0][ct] * e.sc[0] * inv[ct];
-                f32x4 up = acc[1][ct] * e.sc[1] * inv[ct];
+                f32x4 gt = acc[0][ct] * inv[ct];
+                f32x4 up = acc[1][ct] * inv[ct];
+                if (a.scales) {
+                    gt *= as_f32x4(e.sc[0]);
+                    up *= as_f32x4(e.sc[1]);
+                }
 #pragma unroll
                 for (int i = 0; i < 4; ++i) v[i] = silu_f(gt[i]) * up[i];
             } else {
-                v = acc[0][ct] * e.sc[0] * inv[ct];
+                v = acc[0][ct] * inv[ct];
+                if (a.scales) v *= as_f32x4(e.sc[0]);
             }
             if constexpr (ARGMAX) {
                 if (m < a.M) {
@@ -510,8 +589,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                 }
             } else {
                 if (m >= a.M || o >= a.N) continue;
-                if (want_res) v += e.res[ct];
                 if (a.vec_store) {
+                    if (want_res) v += epi_res(a.res_dt, e.res32[ct], e.res16[ct]);
                     void* dst = a.y;
                     int col = o;
                     if (a.flags & EP_SPLIT) {
@@ -525,6 +604,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                     for (int i = 0; i < 4; ++i) {
                         const int oi = o + i;
                         if (oi >= a.N) break;
+                        float vi = v[i];
+                        if (want_res) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
                         void* dst = a.y;
                         int col = oi;
                         if (a.flags & EP_SPLIT) {
@@ -532,7 +613,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                             dst = (blk & 1) ? a.y2 : a.y;
                             col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
                         }
-                        store_act(dst, a.ydt, (int64_t)m * a.ldy + col, v[i]);
+                        store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
                     }
                 }
             }
@@ -572,47 +653,63 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
     }
 }
 
-template <int WF, int XDT, int CT, int NW>
-static hipError_t launch4(const SkinnyArgs& a, bool glu, bool argmax, int grid, hipStream_t st) {
-    const size_t smem = (a.flags & EP_NORM) ? (size_t)a.K * sizeof(float) : 0;
-    if (argmax) {
-        if (glu) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, true, NW>), dim3(grid), dim3(NW * 64), smem, st, a);
-    } else if (glu) {
-        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, true, false, NW>), dim3(grid), dim3(NW * 64), smem, st, a);
-    } else {
-        hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, false, NW>), dim3(grid), dim3(NW * 64), smem, st, a);
+// ---------------------------------------------------------------------------
+// host-side launch
+// ---------------------------------------------------------------------------
+size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split) {
+    const int os = wf == WF_F32 ? 4 : 2;
+    const int ke = wf == WF_F32 ? 4 : (wf == WF_BF16 ? 8 : 16);
+    const bool split = (wf == WF_BF16 && xdt != DT_BF16) || (wf == WF_I8 && xdt == DT_F32);
+    const size_t row = (size_t)ksteps_per_split * 4 * ke * os + 16;
+    return (split ? 2 : 1) * (size_t)(M + 1) * row;
+}
+
+template <typename Kern>
+static hipError_t launch_k(Kern k, const SkinnyArgs& a, int nw, int grid, size_t smem, hipStream_t st) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSkinnyMaxLds);
+        if (e != hipSuccess) return e;
+        configured = true;
     }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), smem, st, a);
     return hipGetLastError();
 }
 
 template <int WF, int XDT, int CT>
-static hipError_t launch3(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
-    // 16-wave workgroups serve plain (non-GLU) projections of up to 16
-    // tokens whose activation already has the MFMA input type
-    if constexpr (CT == 1 && ((WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16) ||
-                              (WF == WF_F32 && XDT == DT_F32))) {
-        if (nw == 16 && !glu && !argmax) {
-            const size_t smem = (a.flags & EP_NORM) ? (size_t)a.K * sizeof(float) : 0;
-            hipLaunchKernelGGL((skinny_kernel<WF, XDT, CT, false, false, 16>), dim3(grid), dim3(1024), smem, st, a);
-            return hipGetLastError();
+static hipError_t launch3(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, size_t smem, hipStream_t st) {
+    if constexpr (CT == 1) {
+        if (!argmax && nw == 16) {
+            if (glu) return launch_k(skinny_kernel<WF, XDT, CT, true, false, 16>, a, 16, grid, smem, st);
+            return launch_k(skinny_kernel<WF, XDT, CT, false, false, 16>, a, 16, grid, smem, st);
+        }
+        if (!argmax && nw == 8) {
+            if (glu) return launch_k(skinny_kernel<WF, XDT, CT, true, false, 8>, a, 8, grid, smem, st);
+            return launch_k(skinny_kernel<WF, XDT, CT, false, false, 8>, a, 8, grid, smem, st);
         }
     }
-    return launch4<WF, XDT, CT, 4>(a, glu, argmax, grid, st);
+    if (argmax) {
+        if (glu) return hipErrorInvalidValue;
+        return launch_k(skinny_kernel<WF, XDT, CT, false, true, 4>, a, 4, grid, smem, st);
+    }
+    if (glu) return launch_k(skinny_kernel<WF, XDT, CT, true, false, 4>, a, 4, grid, smem, st);
+    return launch_k(skinny_kernel<WF, XDT, CT, false, false, 4>, a, 4, grid, smem, st);
 }
 
 template <int WF, int XDT>
-static hipError_t launch2(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
-    if (a.M <= 16) return launch3<WF, XDT, 1>(a, glu, argmax, nw, grid, st);
-    return launch3<WF, XDT, 2>(a, glu, argmax, nw, grid, st);
+static hipError_t launch2(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, size_t smem, hipStream_t st) {
+    if (a.M <= 16) return launch3<WF, XDT, 1>(a, glu, argmax, nw, grid, smem, st);
+    return launch3<WF, XDT, 2>(a, glu, argmax, nw, grid, smem, st);
 }
 
 template <int WF>
-static hipError_t launch1(const SkinnyArgs& a, int xdt, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
+static hipError_t launch1(const SkinnyArgs& a, int xdt, bool glu, bool argmax, int nw, int grid, size_t smem,
+                          hipStream_t st) {
     switch (xdt) {
-        case DT_F32: return launch2<WF, DT_F32>(a, glu, argmax, nw, grid, st);
-        case DT_BF16: return launch2<WF, DT_BF16>(a, glu, argmax, nw, grid, st);
-        case DT_F16: return launch2<WF, DT_F16>(a, glu, argmax, nw, grid, st);
+        case DT_F32: return launch2<WF, DT_F32>(a, glu, argmax, nw, grid, smem, st);
+        case DT_BF16: return launch2<WF, DT_BF16>(a, glu, argmax, nw, grid, smem, st);
+        case DT_F16: return launch2<WF, DT_F16>(a, glu, argmax, nw, grid, smem, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -620,11 +717,14 @@ static hipError_t launch1(const SkinnyArgs& a, int xdt, bool glu, bool argmax, i
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream) {
     if (a.M < 1 || a.M > 32) return hipErrorInvalidValue;
-    if (nw != 4 && nw != 16) return hipErrorInvalidValue;
+    if (nw != 4 && nw != 8 && nw != 16) return hipErrorInvalidValue;
+    if (a.S < 1 || grid % a.S != 0) return hipErrorInvalidValue;
+    const size_t smem = skinny_lds_bytes(wf, xdt, a.M, (a.ksteps + a.S - 1) / a.S);
+    if (smem > kSkinnyMaxLds) return hipErrorInvalidValue;
     switch (wf) {
-        case WF_F32: return launch1<WF_F32>(a, xdt, glu, argmax, nw, grid, stream);
-        case WF_BF16: return launch1<WF_BF16>(a, xdt, glu, argmax, nw, grid, stream);
-        case WF_I8: return launch1<WF_I8>(a, xdt, glu, argmax, nw, grid, stream);
+        case WF_F32: return launch1<WF_F32>(a, xdt, glu, argmax, nw, grid, smem, stream);
+        case WF_BF16: return launch1<WF_BF16>(a, xdt, glu, argmax, nw, grid, smem, stream);
+        case WF_I8: return launch1<WF_I8>(a, xdt, glu, argmax, nw, grid, smem, stream);
         default: return hipErrorInvalidValue;
     }
 }
