@@ -187,21 +187,13 @@ def main():
     value = step_bytes / (ms * 1e-3) / 1e9
     log(f"headline: {ms * 1e3:.1f} us/step, {value:.0f} GB/s")
 
-    # dominant kernel: gate/up GLU GEMV, events around each launch
+    # Dominant kernel: the fused RMSNorm + gate/up + SiLU*mul GEMV.  Its
+    # average launch duration is timed with HIP events on its own stream over
+    # a graph of the 24 layers' launches back to back (so the figure includes
+    # the graph's inter-kernel gap and is an upper bound on the duration).
     hmid = torch.empty(1, I, device="cuda", dtype=torch.bfloat16)
-    evs = []
-    with torch.cuda.stream(stream):
-        for it in range(args.warmup + args.steps):
-            for l in range(LAYERS):
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l])
-                e1.record(stream)
-                qw.linear(ctx, dn[l], hmid, h1, residual=h1)
-                if it >= args.warmup:
-                    evs.append((e0, e1))
-        torch.cuda.synchronize()
-    k_us = 1e3 * float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    g_gu = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l]) for l in range(LAYERS)])
+    k_us = 1e3 * timer.run(g_gu.launch, args.steps, args.warmup) / LAYERS
     k_bytes = gateup_bytes(1)
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gate/up kernel: {k_us:.2f} us avg, {k_gbs:.0f} GB/s")

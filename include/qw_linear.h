@@ -161,6 +161,11 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
                        qw_dtype xdt, const float* gamma, float eps, const void* residual,
                        qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream);
 
+/* Reads and clears the context's device error flag: non-zero when a kernel
+ * gave up a bounded wait (a fused MLP down task whose gate/up inputs never
+ * completed); its outputs are then invalid.  Synchronizes the device. */
+qw_status qw_device_error(qw_ctx* ctx, int* flag);
+
 /* ---- lm_head + greedy argmax -------------------------------------------------
  * token_ids[m] = argmax_v sum_k E[v][k]*h[m][k]; ties go to the LOWEST index
  * (std::max_element, sampler.cpp:41-43).  max_logit (optional) receives the

@@ -23,12 +23,14 @@ struct qw_ctx {
     int min_items = 0;       // split K until a launch has this many items (0: never)
     int force_nw = 0;        // waves per skinny workgroup (0: automatic)
     int force_nw_glu = 0;    // same, GLU weights only
+    bool mlp_fused = false;  // one-launch MLP block (QW_MLP_FUSED=1)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
     unsigned* counters = nullptr;          // split-K arrival counters
     unsigned long long* keys = nullptr;    // argmax keys
     unsigned* done = nullptr;              // argmax completion counter
+    unsigned* mlp_ctl = nullptr;           // fused MLP: ticket, up done, exited, error flag
     float4* partials = nullptr;
     size_t partials_bytes = 0;
     uint8_t* scratch = nullptr;            // MLP intermediate
@@ -149,6 +151,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     auto nw_of = [](const char* v) { const int n = atoi(v); return (n == 4 || n == 8 || n == 16) ? n : 0; };
     if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = nw_of(v);
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
+    if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
     if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(128, 8224, 3584);
     workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(1u << 20));
     workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
@@ -160,7 +163,9 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     uint8_t* p = c->ws;
     c->counters = reinterpret_cast<unsigned*>(p); p += kCountersBytes;
     c->keys = reinterpret_cast<unsigned long long*>(p); p += kKeysBytes;
-    c->done = reinterpret_cast<unsigned*>(p); p += kDoneBytes;
+    c->done = reinterpret_cast<unsigned*>(p);
+    c->mlp_ctl = c->done + 16;
+    p += kDoneBytes;
     c->partials = reinterpret_cast<float4*>(p); p += kPartialsBytes;
     c->partials_bytes = kPartialsBytes;
     c->scratch = p;
@@ -454,7 +459,7 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     // (the split-K hand-off adds a device-coherent round trip).
     const bool wide_ok = !argmax && M <= 16;
     int nw = (wide_ok && !W->glu && a.n_groups * 4 < ctx->num_cus * 3) ? 16 : 4;
-    if (wide_ok && ctx->force_nw) nw = ctx->force_nw;
+    if (wide_ok && !W->glu && ctx->force_nw) nw = ctx->force_nw;
     if (W->glu && ctx->force_nw_glu && wide_ok) nw = ctx->force_nw_glu;
     int S = 1;
     if (!argmax && ctx->min_items > a.n_groups) {
@@ -614,6 +619,32 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
     const size_t per_tok = (size_t)I * dsize(hdt);
     int chunk = (int)std::min<size_t>((size_t)M, ctx->scratch_bytes / per_tok);
     if (chunk < 1) return fail(ctx, QW_ERR_WORKSPACE, "workspace too small for one token of the MLP");
+    // one launch for the whole block when the activations fit the LDS
+    if (ctx->mlp_fused && M <= 16 && (size_t)M * per_tok <= ctx->scratch_bytes &&
+        valid_act(xdt) && valid_act(ydt) && (!residual || valid_act(residual_dtype)) &&
+        aligned(x, 16) && (H * dsize(xdt)) % 16 == 0 && (!gamma || aligned(gamma, 16)) &&
+        qwk::mlp_fused_lds_bytes(gateup->wf, (int)xdt, M, H, I) <= qwk::kSkinnyMaxLds) {
+        if (gamma && !(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
+        qwk::MlpArgs p{};
+        qwk::SkinnyArgs& u = p.up;
+        u.w = gateup->packed; u.scales = gateup->scales; u.x = x; u.ldx = H; u.M = M; u.K = H; u.N = I;
+        u.n_groups = (I + 15) / 16; u.S = 1; u.ksteps = gateup->ksteps; u.n_items = u.n_groups;
+        u.flags = gamma ? QW_EP_NORM_X : 0u; u.gamma = gamma; u.eps = eps;
+        u.y = ctx->scratch; u.ydt = hdt; u.ldy = I;
+        qwk::SkinnyArgs& d = p.down;
+        d.w = down->packed; d.scales = down->scales; d.x = ctx->scratch; d.ldx = I; d.M = M; d.K = I; d.N = H;
+        d.n_groups = (H + 15) / 16; d.S = 1; d.ksteps = down->ksteps; d.n_items = d.n_groups;
+        d.flags = residual ? QW_EP_RESIDUAL : 0u; d.res = residual; d.res_dt = residual_dtype; d.ld_res = H;
+        d.y = y; d.ydt = ydt; d.ldy = H;
+        d.vec_store = (H % 4 == 0) && aligned(y, 16) && (!residual || aligned(residual, 16));
+        p.ctl = ctx->mlp_ctl;
+        p.n_up = u.n_groups;
+        p.n_down = d.n_groups;
+        const int grid = std::min(p.n_up + p.n_down, ctx->num_cus * 2);
+        hipError_t e = qwk::launch_mlp_fused(p, gateup->wf, (int)xdt, grid, stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "fused MLP launch");
+        return QW_OK;
+    }
     qw_epilogue e1{};
     if (gamma) {
         e1.flags = QW_EP_NORM_X;
@@ -635,6 +666,19 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         s = qw_linear(ctx, down, ctx->scratch, hdt, I, mc, yc, ydt, H, residual ? &e2 : nullptr, stream);
         if (s != QW_OK) return s;
     }
+    return QW_OK;
+}
+
+qw_status qw_device_error(qw_ctx* ctx, int* flag) {
+    if (!ctx || !flag) return QW_ERR_NULL;
+    unsigned v = 0;
+    hipError_t e = hipMemcpy(&v, ctx->mlp_ctl + 3, sizeof v, hipMemcpyDeviceToHost);
+    if (e == hipSuccess && v) {
+        const unsigned zero = 0;
+        e = hipMemcpy(ctx->mlp_ctl + 3, &zero, sizeof zero, hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "reading the device error flag");
+    *flag = (int)v;
     return QW_OK;
 }
 

@@ -49,6 +49,18 @@ size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split);
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream);
 
+// Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass
+// (x -> h, y = the h buffer), `down` the down pass (h -> y).
+struct MlpArgs {
+    SkinnyArgs up;
+    SkinnyArgs down;
+    unsigned* ctl;   // [0] ticket, [1] up tiles done, [2] workgroups exited, [3] error flag
+    int n_up;
+    int n_down;
+};
+size_t mlp_fused_lds_bytes(int wf, int xdt, int M, int H, int I);
+hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, int grid, hipStream_t stream);
+
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
 // Output rows are written to physical tile `tile_of_row(o)` (GLU interleave
 // handled by the caller through tile_mul/tile_add: pt = t*tile_mul+tile_add).

@@ -36,312 +36,9 @@
 // (mlp_cuda.cu:158-180), lm_head_gemv_kernel_optimized (lm_head_cuda.cu:38-99)
 // + block_argmax_kernel (gpu_sampler_argmax.cu:14-43), and the thread-per-row
 // projection kernels of the attention operators.
-#include <type_traits>
-
-#include "qw_device.hpp"
-#include "qw_kernels.hpp"
+#include "qw_stream.hpp"
 
 namespace qwk {
-
-constexpr unsigned EP_RESIDUAL = 1u, EP_NORM = 2u, EP_SPLIT = 4u;
-constexpr int AUX_NT = 2;  // buffer-load cache policy: non-temporal (streamed once)
-
-template <int XDT> struct XSize { static constexpr int v = (XDT == DT_F32) ? 4 : 2; };
-
-// MFMA input type of a weight format: bf16 for BF16 weights, f16 for INT8
-// weights (exact for |q| <= 127), f32 for FP32 weights.
-template <int WF> struct OpSize { static constexpr int v = WF == WF_F32 ? 4 : 2; };
-
-// Whether the activation needs a hi + lo pair to keep its precision through a
-// 16-bit MFMA input.
-template <int WF, int XDT> struct XSplit {
-    static constexpr bool v = (WF == WF_BF16 && XDT != DT_BF16) || (WF == WF_I8 && XDT == DT_F32);
-};
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    // raw (untyped) buffer: stride 0, num_records = bytes; loads past the end return 0
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-// ---------------------------------------------------------------------------
-// LDS layout of the staged activations: nops planes (hi, lo) of (M + 1) rows
-// of `ls` op-elements; row M is all zero and serves tokens >= M.  The row
-// stride carries a 16-byte pad to spread the rows over the LDS banks.
-// ---------------------------------------------------------------------------
-template <int WF>
-__device__ __forceinline__ int lds_row_elems(int kr) { return kr + 16 / OpSize<WF>::v; }
-
-template <int WF>
-__device__ __forceinline__ uint32_t op_bits(float f) {
-    if constexpr (WF == WF_BF16) return f32_to_bf16_bits(f);
-    else if constexpr (WF == WF_I8) return f32_to_f16_bits(f);
-    else return __float_as_uint(f);
-}
-template <int WF>
-__device__ __forceinline__ float op_value(uint32_t h) {
-    if constexpr (WF == WF_BF16) return bf16_bits_to_f32(h);
-    else if constexpr (WF == WF_I8) return f16_bits_to_f32(h);
-    else return __uint_as_float(h);
-}
-
-// Activation staging, split in two so the small activation loads are issued
-// BEFORE the weight stream (vector-memory counters retire in order: a load
-// issued after the weights could only be consumed after all of them).
-// Thread t owns row t % RP (RP = M+1 rounded up to a power of two) and the
-// row's 8-element chunks j0, j0 + NT/RP, ...; the first SQ chunks are loaded
-// by stage_issue, stage_finish converts them (times 1 + gamma), writes them
-// to LDS and handles any further chunks.  Row M is all zero.
-template <int XDT, int SQ>
-struct XStage {
-    static constexpr int XB = 8 * XSize<XDT>::v;  // bytes of one raw chunk
-    u32x4 raw[SQ][XB / 16];
-    f32x4 gam[SQ][2];
-    int m, j0, tpr, nchunk;
-    float ss;
-};
-template <int XDT> struct XChunk { static constexpr int XB = 8 * XSize<XDT>::v; };
-
-// Buffer loads are range-checked on their VGPR offset only (the scalar
-// offset is not part of the check); a VGPR offset with the top bit set is out
-// of range and returns zeros without a memory access.  Loads that are not
-// wanted are issued that way instead of being skipped, so every path issues
-// the same number of loads and the compiler can wait for each one precisely.
-constexpr uint32_t OOB = 0x80000000u;
-
-template <int XDT, bool NORM>
-__device__ __forceinline__ void stage_load(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr,
-                                           int k0, int c, int m, bool valid, u32x4 (&raw)[XChunk<XDT>::XB / 16],
-                                           f32x4 (&gam)[2]) {
-    constexpr int XB = XChunk<XDT>::XB;
-    const uint32_t xo = valid && m < a.M ? (uint32_t)(((int64_t)m * a.ldx + k0 + c * 8) * XSize<XDT>::v) : OOB;
-#pragma unroll
-    for (int h = 0; h < XB / 16; ++h)
-        raw[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xo + 16 * h, 0, 0));
-    if constexpr (NORM) {
-        const uint32_t go = valid ? (uint32_t)((k0 + c * 8) * 4) : OOB;
-        gam[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, go, 0, 0));
-        gam[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, go + 16, 0, 0));
-    }
-}
-
-template <int WF, int XDT, int NW, int SQ, bool NORM>
-__device__ __forceinline__ void stage_issue(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr,
-                                            int k0, int kr, XStage<XDT, SQ>& st) {
-    constexpr int NT = NW * 64;
-    int rp = 1;
-    while (rp < a.M + 1) rp <<= 1;  // <= 64
-    st.m = threadIdx.x & (rp - 1);
-    st.tpr = NT / rp;
-    st.j0 = threadIdx.x / rp;
-    st.nchunk = kr / 8;
-    st.ss = 0.0f;
-#pragma unroll
-    for (int q = 0; q < SQ; ++q) {
-        const int c = st.j0 + q * st.tpr;
-        stage_load<XDT, NORM>(a, xr, gr, k0, c, st.m, c < st.nchunk && st.m <= a.M, st.raw[q], st.gam[q]);
-    }
-}
-
-template <int WF, int XDT, bool NORM>
-__device__ __forceinline__ void stage_store(const SkinnyArgs& a, int c, int ls, int plane, uint8_t* xs,
-                                            const u32x4 (&raw)[XChunk<XDT>::XB / 16], const f32x4 (&gam)[2], int m,
-                                            float& ss) {
-    constexpr int OS = OpSize<WF>::v;
-    constexpr bool SPLIT = XSplit<WF, XDT>::v;
-    float f[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        if constexpr (XDT == DT_F32) {
-            f[e] = __uint_as_float(raw[e >> 2][e & 3]);
-        } else {
-            const uint32_t hb = (raw[0][e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-            f[e] = XDT == DT_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
-        }
-    }
-    if constexpr (NORM) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += f[e] * f[e];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] *= 1.0f + gam[e >> 2][e & 3];
-    }
-    uint8_t* dst = xs + ((int64_t)m * ls + c * 8) * OS;
-    if constexpr (OS == 4) {
-        reinterpret_cast<f32x4*>(dst)[0] = f32x4{f[0], f[1], f[2], f[3]};
-        reinterpret_cast<f32x4*>(dst)[1] = f32x4{f[4], f[5], f[6], f[7]};
-    } else {
-        u32x4 hi, lo;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint32_t h0 = op_bits<WF>(f[2 * p]), h1 = op_bits<WF>(f[2 * p + 1]);
-            hi[p] = h0 | (h1 << 16);
-            if constexpr (SPLIT) {
-                const uint32_t l0 = op_bits<WF>(f[2 * p] - op_value<WF>(h0));
-                const uint32_t l1 = op_bits<WF>(f[2 * p + 1] - op_value<WF>(h1));
-                lo[p] = l0 | (l1 << 16);
-            }
-        }
-        *reinterpret_cast<u32x4*>(dst) = hi;
-        if constexpr (SPLIT) *reinterpret_cast<u32x4*>(dst + (int64_t)plane * OS) = lo;
-    }
-}
-
-// Finish the staging; per-token sums of squares of the raw activations over
-// the range go to ss_tok (LDS), reduced in a fixed order.
-template <int WF, int XDT, int CT, int NW, int SQ, bool NORM>
-__device__ void stage_finish(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, int k0,
-                             int kr, XStage<XDT, SQ>& st, uint8_t* xs, float* ss_tok, float* ss_scratch) {
-    constexpr int ROWS = CT * 16;
-    const int ls = lds_row_elems<WF>(kr);
-    const int plane = (a.M + 1) * ls;
-    if (st.m <= a.M) {
-#pragma unroll
-        for (int q = 0; q < SQ; ++q) {
-            const int c = st.j0 + q * st.tpr;
-            if (c < st.nchunk) stage_store<WF, XDT, NORM>(a, c, ls, plane, xs, st.raw[q], st.gam[q], st.m, st.ss);
-        }
-        for (int c = st.j0 + SQ * st.tpr; c < st.nchunk; c += st.tpr) {
-            u32x4 raw[XChunk<XDT>::XB / 16];
-            f32x4 gam[2];
-            stage_load<XDT, NORM>(a, xr, gr, k0, c, st.m, true, raw, gam);
-            stage_store<WF, XDT, NORM>(a, c, ls, plane, xs, raw, gam, st.m, st.ss);
-        }
-    }
-    if constexpr (NORM) {
-        int rp = 1;
-        while (rp < a.M + 1) rp <<= 1;
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        float ss = st.ss;
-        for (int off = rp; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
-        if (lane < rp && lane < ROWS) ss_scratch[wave * ROWS + lane] = ss;
-        __syncthreads();
-        if (threadIdx.x < ROWS) {
-            float t = 0.0f;
-            for (int w = 0; w < NW; ++w) t += (threadIdx.x < rp) ? ss_scratch[w * ROWS + threadIdx.x] : 0.0f;
-            ss_tok[threadIdx.x] = t;
-        }
-    }
-}
-
-// B operands of one k-step unit for one token tile, read from LDS.
-template <int WF, int XDT> struct BOps;
-template <int XDT> struct BOps<WF_BF16, XDT> { bf16x8 hi, lo; };
-template <int XDT> struct BOps<WF_I8, XDT> { f16x8 hi0, hi1, lo0, lo1; };
-template <int XDT> struct BOps<WF_F32, XDT> { f32x4 v; };
-
-template <int WF, int XDT>
-__device__ __forceinline__ void read_bops(BOps<WF, XDT>& b, const uint8_t* p, int plane_bytes) {
-    constexpr bool SPLIT = XSplit<WF, XDT>::v;
-    if constexpr (WF == WF_BF16) {
-        b.hi = *reinterpret_cast<const bf16x8*>(p);
-        if constexpr (SPLIT) b.lo = *reinterpret_cast<const bf16x8*>(p + plane_bytes);
-    } else if constexpr (WF == WF_I8) {
-        b.hi0 = reinterpret_cast<const f16x8*>(p)[0];
-        b.hi1 = reinterpret_cast<const f16x8*>(p)[1];
-        if constexpr (SPLIT) {
-            b.lo0 = reinterpret_cast<const f16x8*>(p + plane_bytes)[0];
-            b.lo1 = reinterpret_cast<const f16x8*>(p + plane_bytes)[1];
-        }
-    } else {
-        b.v = *reinterpret_cast<const f32x4*>(p);
-    }
-}
-
-// acc += A(unit) x B(unit)
-template <int WF, int XDT>
-__device__ __forceinline__ f32x4 unit_mfma(u32x4 a, const BOps<WF, XDT>& b, f32x4 acc) {
-    constexpr bool SPLIT = XSplit<WF, XDT>::v;
-    if constexpr (WF == WF_BF16) {
-        bf16x8 av = __builtin_bit_cast(bf16x8, a);
-        acc = mfma_bf16(av, b.hi, acc);
-        if constexpr (SPLIT) acc = mfma_bf16(av, b.lo, acc);
-    } else if constexpr (WF == WF_I8) {
-        f16x8 a0, a1;
-        i8unit_to_f16(a, a0, a1);
-        acc = mfma_f16(a0, b.hi0, acc);
-        acc = mfma_f16(a1, b.hi1, acc);
-        if constexpr (SPLIT) {
-            acc = mfma_f16(a0, b.lo0, acc);
-            acc = mfma_f16(a1, b.lo1, acc);
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) acc = mfma_f32(__uint_as_float(a[e]), b.v[e], acc);
-    }
-    return acc;
-}
-
-// ---------------------------------------------------------------------------
-// epilogue operands, issued with the weights and kept as raw bits until used
-// ---------------------------------------------------------------------------
-template <int RT, int CT>
-struct EpiOps {
-    u32x4 sc[RT];     // 4 FP32 scales of this lane's rows
-    u32x4 res32[CT];  // residual, FP32 rows
-    u32x2 res16[CT];  // residual, 16-bit rows
-};
-
-template <int RT, int CT>
-__device__ __forceinline__ void load_epi(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t sr, __amdgpu_buffer_rsrc_t rr,
-                                         int grp, bool valid, int lane, EpiOps<RT, CT>& e) {
-    const int r = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {  // the scale buffer is empty for non-INT8 weights
-        const uint32_t so = valid ? (uint32_t)(((grp * RT + rt) * 16 + g * 4) * 4) : OOB;
-        e.sc[rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, so, 0, 0));
-    }
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {  // the residual buffer is empty without a residual
-        const int m = ct * 16 + r;
-        const int o = grp * 16 + g * 4;
-        const bool ok = valid && a.vec_store && m < a.M && o < a.N;
-        const uint32_t i = (uint32_t)((int64_t)m * a.ld_res + o);
-        const bool f32 = a.res_dt == DT_F32;
-        e.res32[ct] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, ok && f32 ? i * 4 : OOB, 0, 0));
-        e.res16[ct] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rr, ok && !f32 ? i * 2 : OOB, 0, 0));
-    }
-}
-
-__device__ __forceinline__ f32x4 as_f32x4(u32x4 v) {
-    return f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
-}
-
-__device__ __forceinline__ f32x4 epi_res(int dt, u32x4 r32, u32x2 r16) {
-    if (dt == DT_F32) return as_f32x4(r32);
-    f32x4 v;
-    if (dt == DT_BF16) {
-        v[0] = bf16_bits_to_f32(r16[0] & 0xffffu); v[1] = bf16_bits_to_f32(r16[0] >> 16);
-        v[2] = bf16_bits_to_f32(r16[1] & 0xffffu); v[3] = bf16_bits_to_f32(r16[1] >> 16);
-    } else {
-        v[0] = f16_bits_to_f32(r16[0] & 0xffffu); v[1] = f16_bits_to_f32(r16[0] >> 16);
-        v[2] = f16_bits_to_f32(r16[1] & 0xffffu); v[3] = f16_bits_to_f32(r16[1] >> 16);
-    }
-    return v;
-}
-
-// This wave's k-step range [kb, kend) within the split [ks0, ks1).
-template <int NW>
-__device__ __forceinline__ void wave_range(int ks0, int ks1, int wave_id, int& kb, int& kend) {
-    const int cnt = ks1 - ks0;
-    kb = ks0 + (wave_id * cnt) / NW;
-    kend = ks0 + ((wave_id + 1) * cnt) / NW;
-}
-
-// Issue the weight loads of k-steps [kb, kb+n) (n <= U) of tile group grp.
-// Issue the weight loads of k-steps [kb, kb+n) (n <= U) of tile group grp;
-// the U - n unused slots are issued out of range (zeros, no traffic).
-template <int RT, int U>
-__device__ __forceinline__ void issue_weights(const SkinnyArgs& a, __amdgpu_buffer_rsrc_t wrs, int grp, int kb,
-                                              int n, int lane, u32x4 (&A)[U][RT]) {
-    const uint32_t tile_bytes = (uint32_t)a.ksteps * 1024u;
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt)
-            A[u][rt] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           wrs, u < n ? lane * 16 : OOB,
-                           (uint32_t)(grp * RT + rt) * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
-}
 
 template <int WF, int XDT, int CT, bool GLU, bool ARGMAX, int NW>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
@@ -363,14 +60,19 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
     const bool norm = (a.flags & EP_NORM) != 0;
     const bool want_res = !ARGMAX && (a.flags & EP_RESIDUAL);
 
-    // this workgroup's K split (constant: the host makes gridDim.x % S == 0)
-    const int s = blockIdx.x % a.S;
-    const int ks0 = (int)(((int64_t)s * a.ksteps) / a.S);
-    const int ks1 = (int)(((int64_t)(s + 1) * a.ksteps) / a.S);
+    // This workgroup's K split is constant (the host makes gridDim.x % S == 0),
+    // so its tile group advances by gridDim.x / S per item: no division in
+    // the item loop.
+    int s = 0, ks0 = 0, ks1 = a.ksteps;
+    if (a.S > 1) {
+        s = blockIdx.x % a.S;
+        ks0 = (s * a.ksteps) / a.S;
+        ks1 = ((s + 1) * a.ksteps) / a.S;
+    }
+    const int grp_step = a.S > 1 ? gridDim.x / a.S : gridDim.x;
     int kb, kend;
     wave_range<NW>(ks0, ks1, wave_id, kb, kend);
     const int kb0 = kb;
-
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * RT * a.ksteps * 1024u));
 
     unsigned long long best[CT];
@@ -388,22 +90,22 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
     u32x4 A[U][RT];
     EpiOps<RT, CT> epi, epi_next;
     int item = blockIdx.x;
+    int grp = a.S > 1 ? blockIdx.x / a.S : blockIdx.x;
     int n = min(U, kend - kb);
     // activation loads first, then the epilogue operands, then the weights;
     // the activations are converted into LDS while the weights stream in
     const int kr = (ks1 - ks0) * 4 * KE;
     // chunks of 8 activations each thread stages (1, 2 or 4 up front)
-    int rp = 1;
-    while (rp < a.M + 1) rp <<= 1;
-    const int cpt = (kr / 8 + NW * 64 / rp - 1) / (NW * 64 / rp);
+    const int rp = 1 << (32 - __builtin_clz((unsigned)a.M));  // M+1 rounded up to a power of 2
+    const int cpt = ((kr / 8) * rp + NW * 64 - 1) / (NW * 64);
     auto prologue = [&](auto sq_tag, auto norm_tag) {
         constexpr int SQ = decltype(sq_tag)::value;
         constexpr bool NORM = decltype(norm_tag)::value;
         XStage<XDT, SQ> st;
         stage_issue<WF, XDT, NW, SQ, NORM>(a, xr, gr, ks0 * 4 * KE, kr, st);
-        load_epi<RT, CT>(a, sr, rr, item / a.S, item < a.n_items, lane, epi);
+        load_epi<RT, CT>(a, sr, rr, grp, item < a.n_items, lane, epi);
         __builtin_amdgcn_sched_barrier(0);  // keep the small loads ahead of the weight stream
-        issue_weights<RT, U>(a, wrs, item / a.S, kb, item < a.n_items ? n : 0, lane, A);
+        issue_weights<RT, U>(a, wrs, grp, kb, item < a.n_items ? n : 0, lane, A);
         __builtin_amdgcn_sched_barrier(0);
         stage_finish<WF, XDT, CT, NW, SQ, NORM>(a, xr, gr, ks0 * 4 * KE, kr, st, xs, ss_tok, ss_scratch);
     };
@@ -464,14 +166,18 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
             kb += n;
             if (kb >= kend) break;
             n = min(U, kend - kb);
-            issue_weights<RT, U>(a, wrs, item / a.S, kb, n, lane, A);
+            issue_weights<RT, U>(a, wrs, grp, kb, n, lane, A);
         }
-        const int cur = item;
+        const int cur_grp = grp;
         item += gridDim.x;
+        grp += grp_step;
         kb = kb0;
         n = min(U, kend - kb);
-        load_epi<RT, CT>(a, sr, rr, item / a.S, item < a.n_items, lane, epi_next);
-        issue_weights<RT, U>(a, wrs, item / a.S, kb, item < a.n_items ? n : 0, lane, A);
+        const bool more = item < a.n_items;
+        if (more) {  // uniform; the loop only comes back through this path
+            load_epi<RT, CT>(a, sr, rr, grp, true, lane, epi_next);
+            issue_weights<RT, U>(a, wrs, grp, kb, n, lane, A);
+        }
 
         // ---- reduce the NW pieces in LDS (fixed order) ----
 #pragma unroll
@@ -498,7 +204,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
         EpiOps<RT, CT> e = epi;
         epi = epi_next;
 
-        const int grp = cur / a.S;
+        const int grp = cur_grp;
         bool finish = true;
         if constexpr (!ARGMAX) {
             if (a.S > 1) {

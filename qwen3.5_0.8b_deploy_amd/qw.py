@@ -30,7 +30,7 @@ EXPORTS = [
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
     "qw_weight_pack_glu_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
-    "qw_linear", "qw_mlp_fused", "qw_lmhead_argmax", "qw_rmsnorm", "qw_residual_rmsnorm",
+    "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
 
@@ -85,6 +85,7 @@ def lib():
         "qw_weight_unpack": ([_vp, _vp, _vp, _vp], _i),
         "qw_linear": ([_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, ctypes.POINTER(Epilogue), _vp], _i),
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
+        "qw_device_error": ([_vp, _vp], _i),
         "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
         "qw_rmsnorm": ([_vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _vp], _i),
         "qw_residual_rmsnorm": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _f, _i, _i, _vp], _i),
@@ -140,6 +141,12 @@ class Context:
     def check(self, st):
         if st != OK:
             raise QwError(st, lib().qw_last_error(self._h).decode())
+
+    def device_error(self):
+        """Read (and clear) the device error flag (synchronizes)."""
+        v = ctypes.c_int()
+        self.check(lib().qw_device_error(self._h, ctypes.byref(v)))
+        return v.value
 
     def close(self):
         if self._h:

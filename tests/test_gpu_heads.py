@@ -113,6 +113,34 @@ def test_mlp_fused_bf16(qw, ctx, oracle, relerr, M):
     # against the bf16-rounded weights the error is far smaller
     ref_b = oracle.mlp_block_f64(oracle.round_bf16(G), oracle.round_bf16(U), oracle.round_bf16(D), gamma, xs)
     assert relerr(host(y), ref_b) <= 2e-3
+    assert ctx.device_error() == 0
+
+
+def test_mlp_fused_repeat_in_place(qw, ctx, oracle, relerr):
+    """Repeated launches must give identical results (device counters of the
+    one-launch path return to zero; split-K partials are summed in a fixed
+    order), and the in-place form (y aliases x and the residual) must match
+    the out-of-place one."""
+    H, I, M = 1024, 3584, 1
+    G, U, D = _mlp_weights(oracle, H, I, 431)
+    gamma = oracle.normal((H,), 434, 0.0, 0.02)
+    gu = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16)
+    dn = qw.Weight.pack(ctx, D, qw.WFMT_BF16)
+    x0 = oracle.normal((M, H), 435)
+    xt = dev(x0)
+    g = dev(gamma)
+    ys = torch.empty(50, M, H, device="cuda")
+    for i in range(50):
+        qw.mlp_fused(ctx, gu, dn, xt, ys[i], gamma=g, residual=xt)
+    torch.cuda.synchronize()
+    assert ctx.device_error() == 0
+    got = ys.cpu().numpy()
+    assert (got == got[0][None]).all()
+    ref = oracle.mlp_block_f64(oracle.round_bf16(G), oracle.round_bf16(U), oracle.round_bf16(D), gamma, x0)
+    assert relerr(got[0], ref) <= 2e-3
+    qw.mlp_fused(ctx, gu, dn, xt, xt, gamma=g, residual=xt)       # in place
+    torch.cuda.synchronize()
+    assert np.array_equal(host(xt), got[0])
 
 
 @pytest.mark.parametrize("M", [1, 32])
@@ -201,3 +229,48 @@ def test_silu_mul(qw, ctx, oracle, relerr):
     gd = g.astype(np.float64)
     ref = gd / (1 + np.exp(-gd)) * u
     assert relerr(host(h), ref) <= 1e-6
+
+
+@pytest.mark.parametrize("fmt,M", [("bf16", 1), ("bf16", 8), ("int8", 1), ("int8", 16), ("f32", 2)])
+def test_mlp_one_launch_path(qw, oracle, relerr, fmt, M):
+    """The single-launch MLP kernel (enabled with QW_MLP_FUSED=1 at context
+    creation) against the oracle, repeated to check its counters reset."""
+    import os
+    os.environ["QW_MLP_FUSED"] = "1"
+    try:
+        c = qw.Context(0)
+    finally:
+        del os.environ["QW_MLP_FUSED"]
+    H, I = 1024, 3584
+    f = {"bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8, "f32": qw.WFMT_F32}[fmt]
+    xdt = {"bf16": torch.bfloat16, "int8": torch.float16, "f32": torch.float32}[fmt]
+    G, U, D = _mlp_weights(oracle, H, I, 441)
+    gamma = oracle.normal((H,), 444, 0.0, 0.02)
+    x = oracle.normal((M, H), 445)
+    gu = qw.Weight.pack_glu(c, G, U, f)
+    dn = qw.Weight.pack(c, D, f)
+    xt = dev(x, xdt)
+    ys = [torch.empty(M, H, device="cuda") for _ in range(3)]
+    for y in ys:
+        qw.mlp_fused(c, gu, dn, xt, y, gamma=dev(gamma), residual=xt)
+    torch.cuda.synchronize()
+    assert c.device_error() == 0
+    assert all(torch.equal(ys[0], y) for y in ys[1:])
+    xs = host(xt)
+    if fmt == "int8":
+        qgu, sgu = gu.unpack()
+        qd, sd = dn.unpack()
+        Gd = qgu[:I].astype(np.float32) * sgu[:I, None]
+        Ud = qgu[I:].astype(np.float32) * sgu[I:, None]
+        Dd = qd.astype(np.float32) * sd[:, None]
+        ref = oracle.mlp_block(Gd, Ud, Dd, gamma, xs)
+        bar = 1e-3
+    elif fmt == "bf16":
+        ref = oracle.mlp_block_f64(G, U, D, gamma, xs)
+        bar = 1e-2
+    else:
+        ref = oracle.mlp_block_f64(G, U, D, gamma, xs)
+        bar = 1e-5
+    assert relerr(host(ys[0]), ref) <= bar
+    del gu, dn
+    c.close()
