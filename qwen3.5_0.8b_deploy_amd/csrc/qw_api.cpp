@@ -33,8 +33,10 @@ struct qw_ctx {
     unsigned* mlp_ctl = nullptr;           // fused MLP: ticket, up done, exited, error flag
     float4* partials = nullptr;
     size_t partials_bytes = 0;
-    uint8_t* scratch = nullptr;            // MLP intermediate
+    uint8_t* scratch = nullptr;            // MLP intermediate h
     size_t scratch_bytes = 0;
+    uint8_t* xnorm = nullptr;              // RMSNorm-ed activations for the GEMM path
+    size_t xnorm_bytes = 0;
     // optional weight arena: packed weights are carved from one large
     // allocation (2 MiB aligned) instead of one hipMalloc each
     uint8_t* arena = nullptr;
@@ -97,6 +99,8 @@ bool valid_act(qw_dtype d) { return d == QW_F32 || d == QW_BF16 || d == QW_F16; 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 size_t scratch_need(int M, int I) { return (size_t)M * I * 4; }
+size_t xnorm_need(int M, int K) { return (size_t)M * K * 2; }
+constexpr int kGemmMinM = 33;   // token count from which the MFMA GEMM is used
 
 }  // namespace
 
@@ -126,7 +130,8 @@ size_t qw_workspace_query(int max_M, int max_N, int max_K) {
     (void)max_K;
     if (max_M < 1) max_M = 1;
     if (max_N < 1) max_N = 1;
-    size_t s = kFixedBytes + scratch_need(max_M, max_N);
+    if (max_K < 1) max_K = 1;
+    size_t s = kFixedBytes + scratch_need(max_M, max_N) + xnorm_need(max_M, max_K) + 4096;
     return (s + 4095) & ~(size_t)4095;
 }
 
@@ -152,8 +157,8 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = nw_of(v);
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
-    if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(128, 8224, 3584);
-    workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(1u << 20));
+    if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(4096, 8224, 4096);
+    workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(3u << 20));
     workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
     if (hipMalloc(&c->ws, workspace_bytes) != hipSuccess) {
         delete c;
@@ -168,8 +173,15 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     p += kDoneBytes;
     c->partials = reinterpret_cast<float4*>(p); p += kPartialsBytes;
     c->partials_bytes = kPartialsBytes;
-    c->scratch = p;
-    c->scratch_bytes = workspace_bytes - kFixedBytes;
+    {
+        // the rest: normalized activations (about a third) and the MLP intermediate
+        const size_t rest = workspace_bytes - kFixedBytes;
+        c->xnorm_bytes = (rest / 3) & ~(size_t)4095;
+        c->xnorm = p;
+        p += c->xnorm_bytes;
+        c->scratch = p;
+        c->scratch_bytes = rest - c->xnorm_bytes;
+    }
     // counters, keys and the completion counter start at zero; every kernel
     // that uses them returns them to zero before it exits.
     if (hipMemset(c->ws, 0, kCountersBytes + kKeysBytes + kDoneBytes) != hipSuccess ||
@@ -515,6 +527,53 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     return QW_OK;
 }
 
+// MFMA GEMM launch for many tokens (BF16 weights and activations).
+static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
+    return W->wf == QW_WFMT_BF16 && xdt == QW_BF16 && W->ksteps % 2 == 0;
+}
+
+static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ldx, int M, void* y, qw_dtype ydt,
+                          int ldy, const qw_epilogue* ep, int32_t* ids, float* maxv, hipStream_t stream) {
+    qwk::GemmArgs a{};
+    a.w = W->packed;
+    a.scales = W->scales;
+    a.n_tiles = W->phys_tiles;
+    a.ksteps = W->ksteps;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = M;
+    a.K = W->K;
+    a.N = W->N;
+    a.nblk_n = (W->phys_tiles * 16 + 255) / 256;
+    a.nblk_m = (M + 255) / 256;
+    a.flags = ep ? (ep->flags & ~(unsigned)QW_EP_NORM_X) : 0u;
+    if (ep && (ep->flags & QW_EP_RESIDUAL)) {
+        a.res = ep->residual;
+        a.res_dt = ep->residual_dtype;
+        a.ld_res = ep->ld_residual ? ep->ld_residual : W->N;
+    }
+    a.y = y;
+    a.ydt = ydt;
+    a.ldy = ldy;
+    if (ep && (ep->flags & QW_EP_SPLIT)) {
+        a.y2 = ep->y2;
+        a.split_period = ep->split_period;
+    }
+    bool vec = (W->N % 4 == 0) && (ldy % 4 == 0) && aligned(y, 16);
+    if (a.flags & QW_EP_SPLIT) vec = vec && aligned(a.y2, 16);
+    if (a.flags & QW_EP_RESIDUAL) vec = vec && (a.ld_res % 4 == 0) && aligned(a.res, 16);
+    a.vec_store = vec ? 1 : 0;
+    a.keys = ctx->keys;
+    a.done = ctx->done;
+    a.ids = ids;
+    a.maxv = maxv;
+    if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * 2 >= (1ull << 31))
+        return fail(ctx, QW_ERR_SHAPE, "operands above 2 GiB are not supported");
+    hipError_t e = qwk::launch_gemm(a, W->wf, QW_BF16, W->glu != 0, ids != nullptr, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "GEMM launch");
+    return QW_OK;
+}
+
 static qw_status check_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx,
                               int M, void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep,
                               bool need_y) {
@@ -565,6 +624,30 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     if (W && ldy == 0) ldy = (ep && (ep->flags & QW_EP_SPLIT)) ? W->N / 2 : W->N;
     qw_status s = check_linear(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, true);
     if (s != QW_OK) return s;
+    if (M >= kGemmMinM && gemm_ok(W, xdt)) {
+        const bool norm = ep && (ep->flags & QW_EP_NORM_X);
+        if (!norm) return run_gemm(ctx, W, x, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);
+        // RMSNorm into the workspace, then the GEMM, in token chunks that fit
+        const int chunk = (int)std::min<size_t>((size_t)M, ctx->xnorm_bytes / ((size_t)W->K * 2));
+        if (chunk < 1) return fail(ctx, QW_ERR_WORKSPACE, "workspace too small for the RMSNorm-ed activations");
+        qw_epilogue e3 = *ep;
+        for (int m0 = 0; m0 < M; m0 += chunk) {
+            const int mc = std::min(chunk, M - m0);
+            const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * ldx * dsize(xdt);
+            hipError_t e = qwk::launch_rmsnorm_ld(xc, (int)xdt, ldx, ep->gamma, ep->eps, ctx->xnorm, (int)QW_BF16,
+                                                  W->K, mc, W->K, stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
+            void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * ldy * dsize(ydt);
+            if (ep->flags & QW_EP_RESIDUAL) {
+                const int ldr = ep->ld_residual ? ep->ld_residual : W->N;
+                e3.residual = static_cast<const uint8_t*>(ep->residual) + (size_t)m0 * ldr * dsize(ep->residual_dtype);
+            }
+            if (ep->flags & QW_EP_SPLIT) e3.y2 = static_cast<uint8_t*>(ep->y2) + (size_t)m0 * ldy * dsize(ydt);
+            s = run_gemm(ctx, W, ctx->xnorm, W->K, mc, yc, ydt, ldy, &e3, nullptr, nullptr, stream);
+            if (s != QW_OK) return s;
+        }
+        return QW_OK;
+    }
     // token chunks of at most 32 for the skinny kernel
     qw_epilogue e2;
     if (ep) e2 = *ep;
@@ -593,6 +676,7 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     if (!token_ids) return fail(ctx, QW_ERR_NULL, "token_ids is NULL");
     if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
     if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
+    if (M >= kGemmMinM && gemm_ok(E, hdt)) return run_gemm(ctx, E, h, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
     for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {
         const int mc = std::min(kSkinnyMaxM, M - m0);
         const void* hc = static_cast<const uint8_t*>(h) + (size_t)m0 * E->K * dsize(hdt);

@@ -49,6 +49,32 @@ size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split);
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream);
 
+// LDS double-buffered MFMA GEMM for many tokens (qw_gemm.hip).
+struct GemmArgs {
+    const uint8_t* w;        // packed weight
+    const float* scales;     // per physical row (INT8) or nullptr
+    int n_tiles;             // physical 16-row tiles
+    int ksteps;              // k-steps of the packed weight
+    const void* x;           // activations [M][ldx]
+    int ldx;
+    int M, K, N;             // N: logical output rows
+    int nblk_n, nblk_m;      // 256 x 256 block grid
+    unsigned flags;
+    const void* res;
+    int res_dt, ld_res;
+    void* y;
+    int ydt, ldy;
+    void* y2;
+    int split_period;
+    int vec_store;
+    unsigned long long* keys;
+    unsigned* done;
+    int32_t* ids;
+    float* maxv;
+};
+size_t gemm_lds_bytes();
+hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream);
+
 // Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass
 // (x -> h, y = the h buffer), `down` the down pass (h -> y).
 struct MlpArgs {
@@ -74,6 +100,8 @@ hipError_t launch_unpack(const uint8_t* src, int wf, int n_rows, int K, void* ds
 hipError_t launch_rmsnorm(const void* x, int xdt, const void* add, void* sum_out,
                           const float* gamma, float eps, void* y, int ydt, int M, int K,
                           hipStream_t stream);
+hipError_t launch_rmsnorm_ld(const void* x, int xdt, int ldx, const float* gamma, float eps, void* y, int ydt,
+                             int ldy, int M, int K, hipStream_t stream);
 hipError_t launch_silu_mul(const void* g, const void* u, void* h, int dt, int64_t n,
                            hipStream_t stream);
 

@@ -15,9 +15,10 @@ constexpr int NORM_MAX_PER_THREAD = 16;  // K <= 4096
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, int xdt, const void* add,
                                                       void* sum_out, const float* gamma, float eps,
-                                                      void* y, int ydt, int K) {
+                                                      void* y, int ydt, int K, int ldx, int ldy) {
     __shared__ float red[4];
-    const int64_t row = (int64_t)blockIdx.x * K;
+    const int64_t row = (int64_t)blockIdx.x * ldx;
+    const int64_t yrow = (int64_t)blockIdx.x * ldy;
     float v[NORM_MAX_PER_THREAD];
     float ss = 0.0f;
 #pragma unroll
@@ -45,7 +46,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, int xdt, co
 #pragma unroll
     for (int i = 0; i < NORM_MAX_PER_THREAD; ++i) {
         const int k = threadIdx.x + i * 256;
-        if (k < K) store_act(y, ydt, row + k, v[i] * inv * (1.0f + gamma[k]));
+        if (k < K) store_act(y, ydt, yrow + k, v[i] * inv * (1.0f + gamma[k]));
     }
 }
 
@@ -60,7 +61,15 @@ hipError_t launch_rmsnorm(const void* x, int xdt, const void* add, void* sum_out
                           hipStream_t stream) {
     if (K > NORM_MAX_PER_THREAD * 256) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, stream, x, xdt, add, sum_out, gamma,
-                       eps, y, ydt, K);
+                       eps, y, ydt, K, K, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_ld(const void* x, int xdt, int ldx, const float* gamma, float eps, void* y, int ydt,
+                             int ldy, int M, int K, hipStream_t stream) {
+    if (K > NORM_MAX_PER_THREAD * 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, stream, x, xdt, nullptr, nullptr, gamma, eps, y, ydt,
+                       K, ldx, ldy);
     return hipGetLastError();
 }
 

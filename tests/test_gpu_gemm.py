@@ -1,0 +1,131 @@
+"""GPU parity of the MFMA GEMM path (M >= 33 tokens, BF16 weights and
+activations) against the CPU oracle.
+
+Bars: <= 2e-5 normwise vs FP64 on the exact stored operands for FP32 outputs
+(one wrong k, row or token shows up as an O(1) error); BF16 outputs carry
+one rounding (<= 4e-3); argmax ids identical to the oracle.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("M,N,K", [(33, 40, 64), (64, 1024, 1024), (256, 256, 128), (300, 1024, 3584),
+                                   (1000, 2048, 1024), (517, 16, 1024), (256, 8224, 1024)])
+def test_gemm_parity(qw, ctx, oracle, relerr, M, N, K):
+    W = oracle.normal((N, K), 700 + N, 0.0, 0.02)
+    x = oracle.normal((M, K), 701 + M)
+    w = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(ctx, w, xt, y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W), host(xt))
+    assert relerr(host(y), ref) <= 2e-5
+    assert relerr(host(y), oracle.linear_f64(W, host(xt))) <= 1e-2
+
+
+def test_gemm_onehot_tokens_and_rows(qw, ctx, oracle):
+    """Token j = e_{k(j)} picks column k(j) of W: catches token/row swaps."""
+    M, N, K = 96, 512, 256
+    W = np.round(oracle.normal((N, K), 710, 0.0, 0.02) * 1024) / 1024
+    w = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    ks = (np.arange(M) * 37) % K
+    x = np.zeros((M, K), np.float32)
+    x[np.arange(M), ks] = 1.0
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(ctx, w, dev(x, torch.bfloat16), y)
+    torch.cuda.synchronize()
+    Wb = oracle.round_bf16(W)
+    assert np.array_equal(host(y), Wb[:, ks].T)
+
+
+@pytest.mark.parametrize("M", [64, 300])
+def test_gemm_glu(qw, ctx, oracle, relerr, M):
+    I, H = 3584, 1024
+    G = oracle.normal((I, H), 720, 0.0, 0.02)
+    U = oracle.normal((I, H), 721, 0.0, 0.02)
+    x = oracle.normal((M, H), 722)
+    w = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    h = torch.empty(M, I, device="cuda")
+    qw.linear(ctx, w, xt, h)
+    torch.cuda.synchronize()
+    xs = host(xt).astype(np.float64)
+    g = xs @ oracle.round_bf16(G).astype(np.float64).T
+    u = xs @ oracle.round_bf16(U).astype(np.float64).T
+    ref = g / (1.0 + np.exp(-g)) * u
+    assert relerr(host(h), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("ydt", ["bf16", "f32"])
+def test_gemm_residual_norm_split(qw, ctx, oracle, relerr, ydt):
+    """RMSNorm prologue (through the workspace), residual epilogue, and the
+    full-attention Q/gate split, all on the GEMM path."""
+    M, K = 130, 1024
+    heads, D = 8, 256
+    N = 2 * heads * D
+    W = oracle.normal((N, K), 730, 0.0, 0.02)
+    gamma = oracle.normal((K,), 731, 0.0, 0.02)
+    x = oracle.normal((M, K), 732) * 2.0
+    w = qw.Weight.pack(ctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
+    q = torch.empty(M, heads * D, device="cuda", dtype=ydtype)
+    g = torch.empty(M, heads * D, device="cuda", dtype=ydtype)
+    qw.linear(ctx, w, xt, q, y2=g, split_period=D, gamma=dev(gamma))
+    torch.cuda.synchronize()
+    xn = oracle.rmsnorm_f64(host(xt), gamma)
+    full = xn @ oracle.round_bf16(W).astype(np.float64).T
+    q_ref, g_ref = oracle.split_q_gate(full.astype(np.float32), heads, D)
+    bar = 1e-2
+    assert relerr(host(q), q_ref) <= bar and relerr(host(g), g_ref) <= bar
+    # residual
+    N2 = 1024
+    W2 = oracle.normal((N2, K), 733, 0.0, 0.02)
+    r = oracle.normal((M, N2), 734)
+    w2 = qw.Weight.pack(ctx, W2, qw.WFMT_BF16)
+    y = dev(r)
+    qw.linear(ctx, w2, xt, y, residual=y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W2), host(xt)) + r
+    assert relerr(host(y), ref) <= 2e-5
+
+
+@pytest.mark.parametrize("M", [33, 128, 300])
+def test_gemm_lmhead_argmax(qw, ctx, oracle, M):
+    V, K = 20000, 1024
+    E = oracle.normal((V, K), 740, 0.0, 0.02)
+    h = oracle.normal((M, K), 741 + M)
+    Eb, hb = oracle.to_bf16(E), oracle.to_bf16(h)
+    w = qw.Weight.pack(ctx, Eb, qw.WFMT_BF16, src_code=qw.BF16)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    mx = torch.empty(M, device="cuda")
+    qw.lmhead_argmax(ctx, w, dev(oracle.from_bf16(hb), torch.bfloat16), ids, mx)
+    torch.cuda.synchronize()
+    ref_ids, ref_max = oracle.lmhead_argmax_bf16(Eb, hb)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    np.testing.assert_allclose(mx.cpu().numpy(), ref_max, rtol=1e-4, atol=1e-5)
+
+
+def test_gemm_repeatable(qw, ctx, oracle):
+    M, N, K = 512, 1024, 1024
+    w = qw.Weight.pack(ctx, oracle.normal((N, K), 750, 0.0, 0.02), qw.WFMT_BF16)
+    xt = dev(oracle.normal((M, K), 751), torch.bfloat16)
+    ys = torch.empty(5, M, N, device="cuda")
+    for i in range(5):
+        qw.linear(ctx, w, xt, ys[i])
+    torch.cuda.synchronize()
+    got = ys.cpu().numpy()
+    assert (got == got[0][None]).all()
