@@ -133,7 +133,7 @@ typedef struct {
     int ld_residual;        /* 0 = N                                           */
     const float* gamma;     /* QW_EP_NORM_X: [K] RMSNorm weight, (1+gamma) form */
     float eps;              /* QW_EP_NORM_X epsilon (reference: 1e-6)           */
-    int split_period;       /* QW_EP_SPLIT: block length (multiple of 16)       */
+    int split_period;       /* QW_EP_SPLIT: block length (power of two >= 16)   */
     void* y2;               /* QW_EP_SPLIT: second output [M][ldy]              */
 } qw_epilogue;
 

@@ -567,7 +567,7 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ld
     a.done = ctx->done;
     a.ids = ids;
     a.maxv = maxv;
-    if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * 2 >= (1ull << 31))
+    if ((uint64_t)W->bytes >= (1ull << 31) || (uint64_t)M * ldx * 2 >= (1ull << 31))
         return fail(ctx, QW_ERR_SHAPE, "operands above 2 GiB are not supported");
     hipError_t e = qwk::launch_gemm(a, W->wf, QW_BF16, W->glu != 0, ids != nullptr, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "GEMM launch");
@@ -609,8 +609,9 @@ static qw_status check_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw
         }
         if (ep->flags & QW_EP_SPLIT) {
             if (!ep->y2) return fail(ctx, QW_ERR_NULL, "y2 is NULL");
-            if (ep->split_period < 16 || ep->split_period % 16 != 0 || W->N % (2 * ep->split_period) != 0)
-                return fail(ctx, QW_ERR_SHAPE, "split_period must be a multiple of 16 dividing N/2");
+            if (ep->split_period < 16 || (ep->split_period & (ep->split_period - 1)) != 0 ||
+                W->N % (2 * ep->split_period) != 0)
+                return fail(ctx, QW_ERR_SHAPE, "split_period must be a power of two >= 16 dividing N/2");
             if (W->glu) return fail(ctx, QW_ERR_INVALID, "split epilogue not available on GLU weights");
             if (ldy < W->N / 2) return fail(ctx, QW_ERR_SHAPE, "ldy < N/2");
         }

@@ -37,13 +37,33 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int GB_N = 256, GB_M = 256;      // block tile: weight rows x tokens
 constexpr int G_STAGE = 64 * 1024;         // bytes per LDS stage
 constexpr int G_XOFF = 32 * 1024;          // activation region within a stage
+constexpr int G_EPI_PITCH = 68;            // epilogue LDS row pitch (floats): 64 rows + pad
 
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds_unit, uint32_t voff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds_unit, 16, voff, 0, 0, 0);
 }
 
+// Element-wise store for outputs whose row count or alignment rules out the
+// 4-wide stores.
+__device__ __forceinline__ void gemm_store_slow(const GemmArgs& a, int m, int row, f32x4 o4) {
+    for (int e = 0; e < 4; ++e) {
+        const int oi = row + e;
+        if (oi >= a.N) break;
+        float vi = o4[e];
+        if (a.flags & EP_RESIDUAL) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
+        void* dst = a.y;
+        int col = oi;
+        if (a.flags & EP_SPLIT) {
+            const int blk = oi / a.split_period;
+            dst = (blk & 1) ? a.y2 : a.y;
+            col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
+        }
+        store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
+    }
+}
+
 template <bool GLU, bool ARGMAX>
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_bf16_kernel(GemmArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ unsigned long long best_s[2][GB_M];
 
@@ -65,26 +85,31 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
     const int nkb = a.ksteps / 2;
 
-    // the 16 units this wave moves per K-block: waves 0,1 weights, 2,3 activations
-    auto issue = [&](int kb, int stage) {
-        uint8_t* st = lds + stage * G_STAGE;
+    // The 16 units this wave moves per K-block: waves 0,1 the 32 weight units
+    // (16 tiles x 2 k-steps), waves 2,3 the 32 activation units (16 token
+    // groups x 2 k-steps); unit u lands at byte u*1024 of the stage either
+    // way.  Offsets for K-block 0 are computed once; K-block kb adds kb*kstep.
+    const bool wrole = wave < 2;
+    const __amdgpu_buffer_rsrc_t rs = wrole ? wrs : xrs;
+    const uint32_t kstep = wrole ? 2048u : 128u;
+    uint32_t vbase[16];
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int u = wave * 16 + q;
-            if (u < 32) {
-                const int t = u >> 1, ks = u & 1;
-                const int pt = nt0 + t;
-                const uint32_t vo = pt < a.n_tiles ? (uint32_t)(((pt * a.ksteps) + kb * 2 + ks) * 1024 + lane * 16) : OOB;
-                lds_dma16(wrs, st + u * 1024, vo);
-            } else {
-                const int v = u - 32;
-                const int tt = v >> 1, ks = v & 1;
-                const int row = m0 + tt * 16 + (lane & 15);
-                const uint32_t vo =
-                    row < a.M ? (uint32_t)((row * a.ldx + (kb * 2 + ks) * 32 + (lane >> 4) * 8) * 2) : OOB;
-                lds_dma16(xrs, st + G_XOFF + v * 1024, vo);
-            }
+    for (int q = 0; q < 16; ++q) {
+        const int v = (wave & 1) * 16 + q;  // unit within the role
+        const int t = v >> 1, ks = v & 1;
+        if (wrole) {
+            const int pt = nt0 + t;
+            vbase[q] = pt < a.n_tiles ? (uint32_t)((pt * a.ksteps + ks) * 1024 + lane * 16) : OOB;
+        } else {
+            const int row = m0 + t * 16 + (lane & 15);
+            vbase[q] = row < a.M ? (uint32_t)((row * a.ldx + ks * 32 + (lane >> 4) * 8) * 2) : OOB;
         }
+    }
+    auto issue = [&](int kb, int stage) {
+        uint8_t* st = lds + stage * G_STAGE + wave * 16 * 1024;
+        const uint32_t add = (uint32_t)kb * kstep;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) lds_dma16(rs, st + q * 1024, vbase[q] + add);
     };
 
     f32x16 acc[4][4];
@@ -98,33 +123,50 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
     const int frag_tile = (lane & 31) >> 4;
     const int frag_off = ((lane & 15) + 16 * (lane >> 5)) * 16;  // + 32*16*h
 
+    // fragments of sub-step s = 2*ks + h of a K-block
+    bf16x8 A[2][4], B[2][4];
+    auto read_frags = [&](const uint8_t* st, int sub, bf16x8 (&Ad)[4], bf16x8 (&Bd)[4]) {
+        const int ks = sub >> 1, h = sub & 1;
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+            const int t = wn * 8 + nb * 2 + frag_tile;
+            Ad[nb] = *reinterpret_cast<const bf16x8*>(st + (t * 2 + ks) * 1024 + frag_off + h * 512);
+        }
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+            const int t = wm * 8 + mb * 2 + frag_tile;
+            Bd[mb] = *reinterpret_cast<const bf16x8*>(st + G_XOFF + (t * 2 + ks) * 1024 + frag_off + h * 512);
+        }
+    };
+
+    // Software pipeline: the fragments of the next sub-step are read from LDS
+    // while the 16 MFMAs of the current one run; the global->LDS loads of
+    // K-block kb+1 are in flight during all of K-block kb.
     issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    read_frags(lds, 0, A[0], B[0]);
     for (int kb = 0; kb < nkb; ++kb) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
         const uint8_t* st = lds + (kb & 1) * G_STAGE;
+        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                bf16x8 A[4], B[4];
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb) {
-                    const int t = wn * 8 + nb * 2 + frag_tile;
-                    A[nb] = *reinterpret_cast<const bf16x8*>(st + (t * 2 + ks) * 1024 + frag_off + h * 512);
-                }
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    const int t = wm * 8 + mb * 2 + frag_tile;
-                    B[mb] = *reinterpret_cast<const bf16x8*>(st + G_XOFF + (t * 2 + ks) * 1024 + frag_off + h * 512);
-                }
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                    for (int mb = 0; mb < 4; ++mb)
-                        acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[nb], B[mb], acc[nb][mb], 0, 0, 0);
+        for (int sub = 0; sub < 4; ++sub) {
+            const int cur = sub & 1;
+            if (sub < 3) {
+                read_frags(st, sub + 1, A[cur ^ 1], B[cur ^ 1]);
+            } else {
+                // stage kb+1 complete and every wave done with stage kb
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (kb + 1 < nkb) read_frags(lds + ((kb + 1) & 1) * G_STAGE, 0, A[cur ^ 1], B[cur ^ 1]);
             }
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb)
+                    acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[cur][nb], B[cur][mb], acc[nb][mb], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
         }
     }
 
@@ -132,79 +174,25 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
     // accumulator item q of lane l: weight row i = 8*(q/4) + 4*(l/32) + q%4 of
     // the 32-row block, token j = l%32 of the 32-token block
     const int ihi = 4 * (lane >> 5);
-    unsigned long long best[4] = {0ull, 0ull, 0ull, 0ull};
+    if constexpr (ARGMAX) {
+        unsigned long long best[4] = {0ull, 0ull, 0ull, 0ull};
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-        const int pt0 = nt0 + wn * 8 + nb * 2;  // physical tile of rows 0..15 of this block
+        for (int nb = 0; nb < 4; ++nb) {
+            const int pt0 = nt0 + wn * 8 + nb * 2;
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            const int m = m0 + wm * 128 + mb * 32 + (lane & 31);
-            const f32x16 v = acc[nb][mb];
+            for (int qg = 0; qg < 4; ++qg) {
+                const int row = pt0 * 16 + 8 * qg + ihi;
+                f32x4 sc = {1.f, 1.f, 1.f, 1.f};
+                if (a.scales) sc = *reinterpret_cast<const f32x4*>(a.scales + row);
 #pragma unroll
-            for (int qg = 0; qg < (GLU ? 2 : 4); ++qg) {
-                // items 4qg .. 4qg+3: four consecutive rows starting at r0
-                const int r0 = 8 * qg + ihi;
-                f32x4 o4;
-                int row;  // logical output row of o4[0]
-                if constexpr (GLU) {
-                    row = (pt0 >> 1) * 16 + r0;   // rows 16.. of the block are the up tile
-                    f32x4 sg = {1.f, 1.f, 1.f, 1.f}, su = {1.f, 1.f, 1.f, 1.f};
-                    if (a.scales) {
-                        sg = *reinterpret_cast<const f32x4*>(a.scales + pt0 * 16 + r0);
-                        su = *reinterpret_cast<const f32x4*>(a.scales + (pt0 + 1) * 16 + r0);
-                    }
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o4[e] = silu_f(v[4 * qg + e] * sg[e]) * (v[4 * qg + 8 + e] * su[e]);
-                } else {
-                    row = pt0 * 16 + r0;
-                    f32x4 sc = {1.f, 1.f, 1.f, 1.f};
-                    if (a.scales) sc = *reinterpret_cast<const f32x4*>(a.scales + row);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o4[e] = v[4 * qg + e] * sc[e];
-                }
-                if constexpr (ARGMAX) {
+                for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        if (row + e < a.N) {
-                            const unsigned long long kk = argmax_key(o4[e], (uint32_t)(row + e));
-                            best[mb] = kk > best[mb] ? kk : best[mb];
-                        }
+                        const unsigned long long kk = argmax_key(acc[nb][mb][4 * qg + e] * sc[e], (uint32_t)(row + e));
+                        best[mb] = (row + e < a.N && kk > best[mb]) ? kk : best[mb];
                     }
-                } else {
-                    if (m >= a.M || row >= a.N) continue;
-                    if (a.vec_store) {
-                        if (a.flags & EP_RESIDUAL) o4 += load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + row);
-                        void* dst = a.y;
-                        int col = row;
-                        if (a.flags & EP_SPLIT) {
-                            const int blk = row / a.split_period;
-                            dst = (blk & 1) ? a.y2 : a.y;
-                            col = (blk >> 1) * a.split_period + (row - blk * a.split_period);
-                        }
-                        store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, o4);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int oi = row + e;
-                            if (oi >= a.N) break;
-                            float vi = o4[e];
-                            if (a.flags & EP_RESIDUAL) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
-                            void* dst = a.y;
-                            int col = oi;
-                            if (a.flags & EP_SPLIT) {
-                                const int blk = oi / a.split_period;
-                                dst = (blk & 1) ? a.y2 : a.y;
-                                col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
-                            }
-                            store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
-                        }
-                    }
-                }
             }
         }
-    }
-
-    if constexpr (ARGMAX) {
         // lanes l and l^32 hold the same token; then the two waves sharing a
         // token range (wn = 0, 1) meet in LDS; then the grid via atomic max
 #pragma unroll
@@ -239,10 +227,84 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmArgs a) {
             }
             if (threadIdx.x == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    } else {
+        // Results pass through LDS as [token][row] (row pitch G_EPI_PITCH
+        // floats) so that each token's output rows leave as one contiguous,
+        // coalesced store, and so that the accumulators are only ever indexed
+        // with constants.  GLU: the wave's 64 output rows in one pass; plain:
+        // its 128 rows in two passes of 64.
+        float* ep = reinterpret_cast<float*>(lds) + wave * (128 * G_EPI_PITCH);
+        const int row_base = GLU ? ((nt0 + wn * 8) >> 1) * 16 : (nt0 + wn * 8) * 16;
+        const int tok_base = m0 + wm * 128;
+        const bool has_res = (a.flags & EP_RESIDUAL) != 0;
+        const bool has_split = (a.flags & EP_SPLIT) != 0;
+        const int sp_log = a.split_period > 0 ? 31 - __builtin_clz((unsigned)a.split_period) : 0;
+        __syncthreads();  // every wave is done reading the K-loop stages
+#pragma unroll
+        for (int pass = 0; pass < (GLU ? 1 : 2); ++pass) {
+#pragma unroll
+            for (int nbl = 0; nbl < (GLU ? 4 : 2); ++nbl) {
+                const int nb = GLU ? nbl : pass * 2 + nbl;
+                const int pt0 = nt0 + wn * 8 + nb * 2;
+#pragma unroll
+                for (int qg = 0; qg < (GLU ? 2 : 4); ++qg) {
+                    const int r0 = 8 * qg + ihi;
+                    f32x4 sg = {1.f, 1.f, 1.f, 1.f}, su = {1.f, 1.f, 1.f, 1.f};
+                    if (a.scales) {
+                        sg = *reinterpret_cast<const f32x4*>(a.scales + pt0 * 16 + r0);
+                        if (GLU) su = *reinterpret_cast<const f32x4*>(a.scales + (pt0 + 1) * 16 + r0);
+                    }
+                    const int lrow = GLU ? nb * 16 + r0 : nbl * 32 + r0;
+#pragma unroll
+                    for (int mb = 0; mb < 4; ++mb) {
+                        f32x4 o4;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if constexpr (GLU)
+                                o4[e] = silu_f(acc[nb][mb][4 * qg + e] * sg[e]) * (acc[nb][mb][4 * qg + 8 + e] * su[e]);
+                            else
+                                o4[e] = acc[nb][mb][4 * qg + e] * sg[e];
+                        }
+                        *reinterpret_cast<f32x4*>(ep + (mb * 32 + (lane & 31)) * G_EPI_PITCH + lrow) = o4;
+                    }
+                }
+            }
+            // wave-local hand-off: each wave reads back only what it wrote
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            const int c = lane & 15;  // rows 4c .. 4c+3
+            const int row = row_base + pass * 64 + 4 * c;
+            for (int it = 0; it < 32; ++it) {
+                const int jj = it * 4 + (lane >> 4);
+                const int m = tok_base + jj;
+                if (m < a.M && row < a.N) {
+                    f32x4 o4 = *reinterpret_cast<const f32x4*>(ep + jj * G_EPI_PITCH + 4 * c);
+                    if (a.vec_store) {
+                        if (has_res) o4 += load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + row);
+                        void* dst = a.y;
+                        int col = row;
+                        if (has_split) {  // power-of-two period: shifts only
+                            dst = ((row >> sp_log) & 1) ? a.y2 : a.y;
+                            col = ((row >> (sp_log + 1)) << sp_log) + (row & (a.split_period - 1));
+                        }
+                        store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, o4);
+                    } else {
+                        gemm_store_slow(a, m, row, o4);
+                    }
+                }
+            }
+            if (!GLU && pass == 0) {
+                __builtin_amdgcn_s_waitcnt(0xc07f);
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
     }
 }
 
-size_t gemm_lds_bytes() { return 2 * (size_t)G_STAGE; }
+size_t gemm_lds_bytes() {
+    const size_t epi = 4 * 128 * G_EPI_PITCH * sizeof(float);
+    return epi > 2 * (size_t)G_STAGE ? epi : 2 * (size_t)G_STAGE;
+}
 
 template <typename Kern>
 static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, hipStream_t st) {
