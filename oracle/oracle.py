@@ -64,6 +64,7 @@ def lib():
             "orc_fill_uniform": [_f32p, _i64, ctypes.c_uint64, _fl, _fl],
             "orc_fill_int8_uniform": [_i8p, _i64, ctypes.c_uint64, _i, _i],
             "orc_silu": [_fl],
+            "orc_mt64_raw": [ctypes.c_uint64, np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"), _i64],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -297,4 +298,10 @@ def uniform(shape, seed, lo, hi):
 def int8_uniform(shape, seed, lo=-127, hi=127):
     out = np.empty(shape, np.int8)
     lib().orc_fill_int8_uniform(out.reshape(-1), out.size, seed, lo, hi)
+    return out
+
+
+def mt64_raw(seed, n):
+    out = np.empty(n, np.uint64)
+    lib().orc_mt64_raw(seed, out, n)
     return out

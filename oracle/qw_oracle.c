@@ -405,6 +405,12 @@ static uint64_t mt64_next(mt64* g) {
     return x;
 }
 
+void orc_mt64_raw(uint64_t seed, uint64_t* out, int64_t n) {
+    mt64 g;
+    mt64_seed(&g, seed);
+    for (int64_t i = 0; i < n; ++i) out[i] = mt64_next(&g);
+}
+
 /* uniform double in (0, 1): 53 random bits, offset by half an ulp */
 static double mt64_unit(mt64* g) {
     return ((double)(mt64_next(g) >> 11) + 0.5) * (1.0 / 9007199254740992.0);

@@ -12,7 +12,9 @@
  *   - activations are row-major x[M][K], outputs y[M][N];
  *   - y[m][o] = sum_k W[o][k] * x[m][k], FP32 accumulated in ascending k.
  *
- * Parity pins for each function are listed in oracle/README.md.
+ * Each function is pinned by tests/test_oracle.py: against the reference's
+ * own CPU operators (oracle/_ref), the committed golden vectors in
+ * tests/golden/, closed forms and FP64 brute force.
  */
 #ifndef QW_ORACLE_H
 #define QW_ORACLE_H
@@ -90,6 +92,8 @@ void orc_lmhead_argmax_int8(const int8_t* q, const float* s, const float* h, int
                             float* maxv, int M, int V, int K);
 
 /* ---- seeded synthetic generator (mt19937-64 + Box-Muller) ---- */
+/* raw MT19937-64 stream (first n outputs after seeding) */
+void orc_mt64_raw(uint64_t seed, uint64_t* out, int64_t n);
 void orc_fill_normal(float* dst, int64_t n, uint64_t seed, float mean, float std);
 void orc_fill_uniform(float* dst, int64_t n, uint64_t seed, float lo, float hi);
 void orc_fill_int8_uniform(int8_t* dst, int64_t n, uint64_t seed, int lo, int hi);

@@ -1,0 +1,278 @@
+"""CPU tests of the oracle (oracle/qw_oracle.c): it is pinned here before any
+GPU result is compared with it.
+
+Pins, by function:
+  number formats      numpy float16 (IEEE RNE), torch bfloat16 (RNE), hand-made
+                      bit patterns (ties, overflow, subnormals, NaN)
+  MT19937-64          the C++ standard's known answer (10000th output of the
+                      default seed) and the published first output
+  linear (FP32)       the reference's LMHead::forward compiled from its source
+                      (golden vectors + oracle/_ref), numpy float64, closed forms
+  quantize recipe     hand-worked golden rows (tests/golden/quant.npz)
+  INT8 dequant GEMV   exact integer arithmetic with power-of-two scales
+  RMSNorm (1+w)       constant-vector closed form, the reference unit test's
+                      uniform-input known answer, numpy float64
+  residual + RMSNorm  exact sum, then the RMSNorm pin
+  MLP                 reference MLP::forward_batch (golden + oracle/_ref),
+                      numpy float64 composition
+  Q/gate split        index identity on an arange input
+  argmax / lm_head    the reference Sampler (golden ties), planted maxima,
+                      numpy float64 argmax with a clear top-2 gap
+"""
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def np_silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+# ---- number formats --------------------------------------------------------
+def test_f16_matches_numpy(oracle):
+    x = np.concatenate([
+        oracle.normal(4096, 1, 0.0, 3.0),
+        np.array([0.0, -0.0, 1.0, 65504.0, 65519.0, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25,
+                  3 * 2.0 ** -26, 2.0 ** -14, 1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], np.float32),
+    ]).astype(np.float32)
+    got = oracle.to_f16(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+    assert np.array_equal(oracle.from_f16(ref), ref.view(np.float16).astype(np.float32))
+
+
+def test_bf16_bits(oracle):
+    torch = pytest.importorskip("torch")
+    x = np.concatenate([
+        oracle.normal(4096, 2, 0.0, 10.0),
+        np.array([1.0, -1.0, 3.3895314e38, -3.4e38], np.float32),
+    ]).astype(np.float32)
+    # exact ties: lower 16 bits 0x8000, with even and odd kept mantissa
+    ties = np.array([0x3F808000, 0x3F818000, 0xBF808000, 0x40490000 | 0x8000], np.uint32).view(np.float32)
+    x = np.concatenate([x, ties])
+    got = oracle.to_bf16(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    assert list(oracle.to_bf16(ties)) == [0x3F80, 0x3F82, 0xBF80, 0x404A]
+    back = oracle.from_bf16(got)
+    assert np.array_equal(back.view(np.uint32) >> 16, got.astype(np.uint32))
+    assert np.isnan(oracle.round_bf16(np.array([np.nan], np.float32))[0])
+
+
+# ---- generator ---------------------------------------------------------------
+def test_mt19937_64_known_answers(oracle):
+    r = oracle.mt64_raw(5489, 10000)
+    assert int(r[0]) == 14514284786278117030
+    assert int(r[-1]) == 9981545732273789042  # C++ [rand.predef]
+
+
+def test_normal_fill_moments(oracle):
+    v = oracle.normal(200000, 0, 0.0, 1.0).astype(np.float64)
+    assert abs(v.mean()) < 0.01 and abs(v.std() - 1.0) < 0.01
+    u = oracle.uniform(100000, 3, 1e-3, 2e-2)
+    assert u.min() >= 1e-3 and u.max() <= 2e-2
+    q = oracle.int8_uniform(100000, 4)
+    assert q.min() == -127 and q.max() == 127
+
+
+# ---- projections -----------------------------------------------------------
+def test_linear_matches_reference_golden(oracle):
+    g = np.load(os.path.join(GOLDEN, "ref_ops.npz"))
+    y = oracle.linear(g["lin_W"], g["lin_x"])
+    assert np.array_equal(y, g["lin_y"])  # same ascending-k FP32 loop
+
+
+def test_linear_fp64_and_closed_forms(oracle):
+    N, K = 40, 192
+    W = oracle.normal((N, K), 5, 0.0, 0.02)
+    x = oracle.normal((4, K), 6)
+    ref = x.astype(np.float64) @ W.astype(np.float64).T
+    assert np.abs(oracle.linear_f64(W, x) - ref).max() <= 1e-12
+    assert np.abs(oracle.linear(W, x) - ref).max() / np.abs(ref).max() < 1e-5
+    # one-hot token picks a column
+    e = np.zeros((1, K), np.float32); e[0, 77] = 1.0
+    assert np.array_equal(oracle.linear(W, e)[0], W[:, 77])
+    # identity weight
+    I = np.eye(K, dtype=np.float32)
+    assert np.array_equal(oracle.linear(I, x), x)
+    # all-ones: K * c exactly (c a power of two)
+    assert np.all(oracle.linear(np.ones((3, K), np.float32), np.full((1, K), 0.25, np.float32)) == K * 0.25)
+
+
+def test_quantize_recipe_golden(oracle):
+    g = np.load(os.path.join(GOLDEN, "quant.npz"))
+    q, s = oracle.quantize_rowscale(g["W"])
+    assert np.array_equal(q, g["q"])
+    assert np.array_equal(s, g["s"])
+
+
+def test_int8_exact_with_integer_inputs(oracle):
+    N, K = 24, 256
+    q = oracle.int8_uniform((N, K), 8)
+    s = np.ldexp(1.0, -np.arange(N) % 7).astype(np.float32)
+    x = oracle.int8_uniform((2, K), 9, -8, 8).astype(np.float32)
+    exact = (x.astype(np.int64) @ q.astype(np.int64).T) * s.astype(np.float64)
+    assert np.array_equal(oracle.linear_int8(q, s, x), exact.astype(np.float32))
+    assert np.array_equal(oracle.linear_int8_f64(q, s, x), exact)
+
+
+def test_int8_general_vs_fp64(oracle):
+    N, K = 64, 1024
+    q = oracle.int8_uniform((N, K), 10)
+    s = oracle.uniform(N, 11, 1e-3, 2e-2)
+    x = oracle.normal((3, K), 12)
+    ref = (x.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)
+    assert np.abs(oracle.linear_int8(q, s, x) - ref).max() / np.abs(ref).max() < 1e-5
+
+
+# ---- norms -----------------------------------------------------------------
+def test_rmsnorm_closed_forms(oracle):
+    K, eps = 1024, 1e-6
+    # reference unit test (tests/unit/test_rmsnorm.cu:54-115): all-ones input,
+    # unit effective weight -> 1/sqrt(1+eps); with the (1+w) form that is w=0
+    y = oracle.rmsnorm(np.ones((8, K), np.float32), np.zeros(K, np.float32), eps)
+    assert np.abs(y - 1.0 / np.sqrt(1.0 + eps)).max() < 1e-6
+    c = 3.0
+    w = oracle.normal(K, 13, 0.0, 0.02)
+    y = oracle.rmsnorm(np.full((1, K), c, np.float32), w, eps)[0]
+    exp = c / np.sqrt(c * c + eps) * (1.0 + w.astype(np.float64))
+    assert np.abs(y - exp).max() < 1e-6
+
+
+def test_rmsnorm_vs_fp64(oracle):
+    K = 1024
+    x = oracle.normal((5, K), 14)
+    w = oracle.normal(K, 15, 0.0, 0.02)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + 1e-6) * (1.0 + w.astype(np.float64))
+    assert np.abs(oracle.rmsnorm_f64(x, w) - ref).max() < 1e-12
+    assert np.abs(oracle.rmsnorm(x, w) - ref).max() < 1e-5
+
+
+def test_residual_rmsnorm(oracle):
+    K = 1024
+    r = oracle.normal((3, K), 16)
+    a = oracle.normal((3, K), 17)
+    w = oracle.normal(K, 18, 0.0, 0.02)
+    ro, no = oracle.residual_rmsnorm(r, a, w)
+    assert np.array_equal(ro, r + a)
+    assert np.array_equal(no, oracle.rmsnorm(r + a, w))
+
+
+# ---- MLP -------------------------------------------------------------------
+def test_mlp_matches_reference_golden(oracle):
+    g = np.load(os.path.join(GOLDEN, "ref_ops.npz"))
+    y = oracle.mlp(g["mlp_Wg"], g["mlp_Wu"], g["mlp_Wd"], g["mlp_x"])
+    assert np.array_equal(y, g["mlp_y"])
+
+
+def test_mlp_vs_numpy_fp64(oracle):
+    H, I = 128, 320
+    Wg = oracle.normal((I, H), 19, 0.0, 0.05)
+    Wu = oracle.normal((I, H), 20, 0.0, 0.05)
+    Wd = oracle.normal((H, I), 21, 0.0, 0.05)
+    x = oracle.normal((3, H), 22)
+    gate = x.astype(np.float64) @ Wg.astype(np.float64).T
+    up = x.astype(np.float64) @ Wu.astype(np.float64).T
+    ref = (np_silu(gate) * up) @ Wd.astype(np.float64).T
+    assert np.abs(oracle.mlp_f64(Wg, Wu, Wd, x) - ref).max() < 1e-12
+    assert np.abs(oracle.mlp(Wg, Wu, Wd, x) - ref).max() / np.abs(ref).max() < 1e-5
+    # block: x + MLP(RMSNorm(x))
+    gm = oracle.normal(H, 23, 0.0, 0.02)
+    xd = x.astype(np.float64)
+    n = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + 1e-6) * (1.0 + gm.astype(np.float64))
+    blk = xd + (np_silu(n @ Wg.astype(np.float64).T) * (n @ Wu.astype(np.float64).T)) @ Wd.astype(np.float64).T
+    assert np.abs(oracle.mlp_block_f64(Wg, Wu, Wd, gm, x) - blk).max() < 1e-10
+    assert np.abs(oracle.mlp_block(Wg, Wu, Wd, gm, x) - blk).max() / np.abs(blk).max() < 1e-5
+
+
+def test_silu_closed_forms(oracle):
+    assert oracle.silu(0.0) == 0.0
+    assert abs(oracle.silu(1.0) - 1.0 / (1.0 + np.exp(-1.0))) < 1e-7
+    assert abs(oracle.silu(-30.0)) < 1e-11
+    assert oracle.silu(30.0) == pytest.approx(30.0, rel=1e-7)
+
+
+def test_split_q_gate_indices(oracle):
+    heads, hd = 8, 256
+    raw = np.arange(2 * heads * hd * 2, dtype=np.float32).reshape(2, -1)
+    q, g = oracle.split_q_gate(raw, heads, hd)
+    r4 = raw.reshape(2, heads, 2, hd)
+    assert np.array_equal(q, r4[:, :, 0].reshape(2, -1))
+    assert np.array_equal(g, r4[:, :, 1].reshape(2, -1))
+
+
+# ---- argmax / lm_head ------------------------------------------------------
+def test_argmax_matches_reference_sampler(oracle):
+    g = np.load(os.path.join(GOLDEN, "ref_ops.npz"))
+    ids = [oracle.argmax_first(row) for row in g["greedy_logits"]]
+    assert ids == list(g["greedy_ids"])
+
+
+def test_lmhead_argmax_forms(oracle):
+    V, K, M = 3000, 256, 4
+    E = oracle.normal((V, K), 24, 0.0, 0.02)
+    h = oracle.normal((M, K), 25)
+    ids, mx = oracle.lmhead_argmax(E, h)
+    logits = h.astype(np.float64) @ E.astype(np.float64).T
+    top2 = np.sort(logits, axis=1)[:, -2:]
+    for m in range(M):
+        if top2[m, 1] - top2[m, 0] > 1e-4:
+            assert ids[m] == int(np.argmax(logits[m]))
+    assert np.array_equal(ids, [oracle.argmax_first(r) for r in oracle.linear(E, h)])
+    # planted ties: identical rows -> lowest index
+    E2 = E.copy(); E2[[5, 2000, 2999]] = 0.5
+    ids2, _ = oracle.lmhead_argmax(E2, np.abs(h))
+    assert np.all(ids2 == 5)
+    # bf16 / int8 forms agree with the FP32 form on the rounded / dequantized weight
+    Eb, hb = oracle.to_bf16(E), oracle.to_bf16(h)
+    ib, mb = oracle.lmhead_argmax_bf16(Eb, hb)
+    i32, m32 = oracle.lmhead_argmax(oracle.from_bf16(Eb), oracle.from_bf16(hb))
+    assert np.array_equal(ib, i32) and np.array_equal(mb, m32)
+    q, s = oracle.quantize_rowscale(E)
+    iq, mq = oracle.lmhead_argmax_int8(q, s, h)
+    lq = oracle.linear_int8(q, s, h)
+    assert np.array_equal(iq, [oracle.argmax_first(r) for r in lq])
+    assert np.array_equal(mq, lq.max(axis=1))
+
+
+# ---- oracle vs the reference's own operators at random shapes ---------------
+def _ref_or_skip(oracle):
+    R = oracle.ref_lib()
+    if R is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    return R
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 1024), (3, 130, 448)])
+def test_linear_vs_ref_lib(oracle, M, N, K):
+    R = _ref_or_skip(oracle)
+    W = oracle.normal((N, K), 40 + M, 0.0, 0.02)
+    x = oracle.normal((M, K), 50 + M)
+    y = np.empty((M, N), np.float32)
+    assert R.ref_linear(W, x, y, M, N, K) == 0
+    assert np.array_equal(oracle.linear(W, x), y)
+
+
+def test_mlp_vs_ref_lib(oracle):
+    R = _ref_or_skip(oracle)
+    M, H, I = 2, 128, 384
+    Wg = oracle.normal((I, H), 60, 0.0, 0.05)
+    Wu = oracle.normal((I, H), 61, 0.0, 0.05)
+    Wd = oracle.normal((H, I), 62, 0.0, 0.05)
+    x = oracle.normal((M, H), 63)
+    y = np.empty((M, H), np.float32)
+    assert R.ref_mlp(Wg, Wu, Wd, x, y, M, H, I) == 0
+    assert np.array_equal(oracle.mlp(Wg, Wu, Wd, x), y)
+
+
+def test_greedy_vs_ref_lib(oracle):
+    R = _ref_or_skip(oracle)
+    for seed in range(5):
+        v = oracle.normal(5000, 70 + seed)
+        v[[seed * 7, 4000]] = 10.0
+        assert oracle.argmax_first(v) == R.ref_greedy(v, v.size) == seed * 7
