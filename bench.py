@@ -36,6 +36,8 @@ BF16_PEAK = 2500.0       # TFLOP/s dense
 H, I, V = 1024, 3584, 248320
 LAYERS = 24
 LINEAR_LAYERS = [i for i in range(24) if i % 4 != 3]   # 18 Gated-DeltaNet layers
+COPY_BYTES = 64 << 20   # calibration copy for the HBM traffic counters
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gateup_glu_bf16_M1.txt")
 METRIC = "decode GEMV HBM GB/s (% of peak) at M=1; prefill GEMM TFLOPS (% MFMA peak)"
 
 
@@ -92,6 +94,25 @@ def gateup_bytes(M):
     return 2 * H * I * 2 + M * H * 2 + M * I * 2 + H * 4
 
 
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counter runs, each scaled by what the
+    same counter reads for a 64 MiB copy; None when the summary is absent."""
+    try:
+        vals = {}
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                k, sep, v = line.partition(":")
+                if sep and k.strip() in ("copy_bytes", "copy_fetch_kib", "copy_write_kib",
+                                         "kernel_fetch_kib", "kernel_write_kib"):
+                    vals[k.strip()] = float(v)
+        ff = vals["copy_bytes"] / (vals["copy_fetch_kib"] * 1024)
+        fw = vals["copy_bytes"] / (vals["copy_write_kib"] * 1024)
+        return int(vals["kernel_fetch_kib"] * 1024 * ff + vals["kernel_write_kib"] * 1024 * fw)
+    except (OSError, KeyError, ValueError, ZeroDivisionError):
+        return None
+
+
 def cpu_baseline(oracle):
     """Reference CPU MLP (1 thread) on a bounded sample of the same workload."""
     ref = oracle.ref_lib()
@@ -102,13 +123,13 @@ def cpu_baseline(oracle):
     y = np.empty((1, H), np.float32)
     if ref is not None:
         t1 = ref.ref_mlp_time(Wg, Wu, Wd, x, y, 1, H, I, 1)
-        iters = max(1, min(2000, int(10.0 / max(t1, 1e-4))))
+        iters = max(1, min(10000, int(12.0 / max(t1, 1e-4))))
         secs = ref.ref_mlp_time(Wg, Wu, Wd, x, y, 1, H, I, iters)
         kind = "reference"
         what = "qwen::MLP::forward_batch (reference language_mlp.cpp, built -O2 by oracle/Makefile)"
     else:
         t0 = time.perf_counter(); oracle.mlp(Wg, Wu, Wd, x); t1 = time.perf_counter() - t0
-        iters = max(1, min(2000, int(10.0 / max(t1, 1e-4))))
+        iters = max(1, min(10000, int(12.0 / max(t1, 1e-4))))
         t0 = time.perf_counter()
         for _ in range(iters):
             oracle.mlp(Wg, Wu, Wd, x)
@@ -143,6 +164,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="counter pass: only the dominant kernel (eager launches) and a 64 MiB "
+                         "calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -153,7 +177,8 @@ def main():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     qw = load_qw()
     torch.cuda.set_device(0)
-    ctx = qw.Context(0)
+    # workspace sized for the M=16384 prefill stack (RMSNorm-ed activations)
+    ctx = qw.Context(0, qw.lib().qw_workspace_query(16384, 8224, 4096))
     stream = torch.cuda.Stream()
     timer = Timer(torch, stream)
     gen = torch.Generator(device="cuda")
@@ -181,6 +206,20 @@ def main():
         return body
 
     h1 = randn(1, H)
+    if args.profile_kernel:
+        hmid = torch.empty(1, I, device="cuda", dtype=torch.bfloat16)
+        with torch.cuda.stream(stream):
+            for _ in range(4):
+                for l in range(LAYERS):
+                    qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l])
+            src = torch.empty(COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16).fill_(1.0)
+            dst = torch.empty_like(src)
+            for _ in range(4):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        log("profile pass done")
+        ctx.close()
+        return
     g_mlp = graphed(qw, ctx, stream, mlp_step(h1, 1))
     ms = timer.run(g_mlp.launch, args.steps, args.warmup)
     step_bytes = LAYERS * mlp_bytes(1)
@@ -234,7 +273,7 @@ def main():
             "peak": HBM_PEAK,
             "unit": "GB/s",
             "frac": round(k_gbs / HBM_PEAK, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": k_bytes,
             "avg_launch_us": round(k_us, 3),
         },
@@ -346,6 +385,8 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         del g
     del layers
 
+    extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
+
     # config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each
     for fmt, name in ((qw.WFMT_BF16, "bf16"), (qw.WFMT_INT8, "int8")):
         Es = []
@@ -369,6 +410,69 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         del Es
     torch.cuda.synchronize()
     return extra
+
+
+def run_prefill(qw, ctx, torch, timer, stream, randn, args, M=16384):
+    """Config 4: the 24-layer BF16 projection stack at M=16384 prefill tokens.
+
+    Per Gated-DeltaNet layer: QKV 1024->6144, Z 1024->2048, out 2048->1024
+    (+residual); per full-attention layer: Q+gate 1024->4096, K and V
+    1024->512, O 2048->1024 (+residual); every layer: RMSNorm + gate/up
+    1024->2x3584 with SiLU*mul, down 3584->1024 (+residual).  The attention
+    cores between the projections are outside this path; a fixed [M][2048]
+    tensor stands in for their output.  FLOPs = 2*M*sum(N*K) = 16.29 TFLOP."""
+    ws = []
+    nk = 0
+    for li in range(LAYERS):
+        L = {}
+        if li in LINEAR_LAYERS:
+            shapes = {"qkv": (6144, 1024), "z": (2048, 1024), "out": (1024, 2048)}
+        else:
+            shapes = {"qg": (4096, 1024), "k": (512, 1024), "v": (512, 1024), "o": (1024, 2048)}
+        for name, (n, k) in shapes.items():
+            w = randn(n, k, std=0.02)
+            L[name] = qw.Weight.pack_device(ctx, w, qw.WFMT_BF16)
+            nk += n * k
+            del w
+        g, u = randn(I, H, std=0.02), randn(I, H, std=0.02)
+        L["gu"] = qw.Weight.pack_glu_device(ctx, g, u, qw.WFMT_BF16)
+        d = randn(H, I, std=0.02)
+        L["down"] = qw.Weight.pack_device(ctx, d, qw.WFMT_BF16)
+        L["gamma"] = randn(H, std=0.02, dtype=torch.float32)
+        nk += 3 * H * I
+        del g, u, d
+        ws.append(L)
+    x = randn(M, H)
+    att = randn(M, 2048)
+    big = torch.empty(M, 6144, device="cuda", dtype=torch.bfloat16)
+    z = torch.empty(M, 2048, device="cuda", dtype=torch.bfloat16)
+    kv = torch.empty(M, 512, device="cuda", dtype=torch.bfloat16)
+    hmid = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
+    res = randn(M, H)
+    torch.cuda.synchronize()
+
+    def body():
+        for L in ws:
+            if "qkv" in L:
+                qw.linear(ctx, L["qkv"], x, big)
+                qw.linear(ctx, L["z"], x, z)
+                qw.linear(ctx, L["out"], att, res, residual=res)
+            else:
+                qw.linear(ctx, L["qg"], x, big[:, :4096])
+                qw.linear(ctx, L["k"], x, kv)
+                qw.linear(ctx, L["v"], x, kv)
+                qw.linear(ctx, L["o"], att, res, residual=res)
+            qw.linear(ctx, L["gu"], res, hmid, gamma=L["gamma"])
+            qw.linear(ctx, L["down"], hmid, res, residual=res)
+
+    ms = timer.run(body, max(3, args.steps // 10), 1)
+    fl = 2.0 * M * nk
+    out = {"cfg4_prefill_bf16_M16384": {"ms_per_stack": round(ms, 3), "TFLOPs": round(fl / ms / 1e9, 1),
+                                        "pct_mfma_peak": round(100 * fl / ms / 1e9 / BF16_PEAK, 1),
+                                        "tok_per_s": round(M / (ms * 1e-3), 1), "sum_NK": nk}}
+    log("cfg4", out)
+    del ws
+    return out
 
 
 if __name__ == "__main__":
