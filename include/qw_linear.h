@@ -61,7 +61,7 @@ typedef struct qw_graph qw_graph;
  * (CudaMLP::ensure_buffers, mlp_cuda.cu:229-259, and the per-call
  * cudaMalloc/cudaFree of CudaMLP::forward, mlp_cuda.cu:302-303,328-329)
  * with one arena reserved up front.  workspace_bytes = 0 picks the default
- * (qw_workspace_query(128, 8224, 3584)). */
+ * (qw_workspace_query(4096, 8224, 4096)). */
 qw_status qw_init(qw_ctx** ctx, int device, size_t workspace_bytes);
 qw_status qw_destroy(qw_ctx* ctx);
 /* Workspace needed for calls with up to max_M tokens, max_N output rows
@@ -174,6 +174,14 @@ qw_status qw_device_error(qw_ctx* ctx, int* flag);
  * and no host round trip. */
 qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M,
                            int32_t* token_ids, float* max_logit, hipStream_t stream);
+
+/* Greedy argmax of materialized logits [M][ld] (F32, BF16 or F16):
+ * token_ids[m] = lowest index of the row maximum.  Replaces
+ * GpuGreedyArgmaxSampler::sample (gpu_sampler_argmax.cu:69-93: block argmax +
+ * D2H + host scan) with one launch and no host round trip; for the lm_head
+ * prefer qw_lmhead_argmax, which never writes the logits.  ld 0 = V. */
+qw_status qw_argmax_rows(qw_ctx* ctx, const void* logits, qw_dtype dt, int M, int V, int ld,
+                         int32_t* token_ids, float* max_logit, hipStream_t stream);
 
 /* ---- RMSNorm -----------------------------------------------------------------
  * y = x / sqrt(mean(x^2) + eps) * (1 + gamma)  (language_common.cpp:21-78,

@@ -1,0 +1,389 @@
+// qw_ops.hpp -- C++ operator facade over the C ABI (qw_linear.h), shaped like
+// the reference engine's projection operators so that a caller written
+// against them (CudaLayer::forward, cuda_engine.cu:109-125) switches by
+// changing the class names.  Header-only; links against libqw_linear.so.
+//
+// Reference classes mirrored (zhils/Qwen3.5_0.8B_Deploy, src/backend/cuda/include):
+//   qwen::cuda::CudaMLP                 mlp_cuda.hpp:11-59       -> qwen::hip::HipMLP
+//   qwen::cuda::CudaLMHead              lm_head_cuda.hpp:10-38   -> qwen::hip::HipLMHead
+//   qwen::cuda::GpuGreedyArgmaxSampler  gpu_sampler_argmax.hpp:6-20 -> qwen::hip::HipGreedyArgmaxSampler
+//   qwen::cuda::CudaRMSNorm             rmsnorm_cuda.hpp:9-29    -> qwen::hip::HipRMSNorm
+//   projection parts of CudaLinearAttention (linear_attention_cuda.hpp:24-90) and
+//   CudaFullAttention (full_attention_cuda.hpp:35-90)
+//                                       -> HipLinearAttnProjections / HipFullAttnProjections
+//
+// Same argument meaning as the reference: weights arrive as host
+// std::vector<float> in row-major [out][in]; activations are caller-owned
+// device pointers (FP32); batch = number of tokens.  Differences:
+//   - every call takes an optional hipStream_t (the reference uses stream 0);
+//   - forward_add_residual ADDS the MLP output to the residual (the INT8
+//     CudaMLP overwrites it, mlp_cuda.cu:332-337);
+//   - errors throw qwen::hip::Error carrying the library's status and message
+//     (the reference mixes exceptions, printf and exit).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "qw_linear.h"
+
+namespace qwen {
+namespace hip {
+
+class Error : public std::runtime_error {
+  public:
+    Error(qw_status s, const std::string& what) : std::runtime_error(what), status(s) {}
+    qw_status status;
+};
+
+// One library context (workspace arena) per device, shared by the operators
+// created on it; use one Context per stream when streams run concurrently.
+class Context {
+  public:
+    explicit Context(int device = 0, size_t workspace_bytes = 0) {
+        check(qw_init(&ctx_, device, workspace_bytes), "qw_init");
+    }
+    ~Context() { qw_destroy(ctx_); }
+    Context(const Context&) = delete;
+    Context& operator=(const Context&) = delete;
+    qw_ctx* get() const { return ctx_; }
+
+    void check(qw_status s, const char* what) const {
+        if (s != QW_OK) {
+            std::string msg = std::string(what) + ": " + qw_status_string(s);
+            if (ctx_) msg += std::string(" (") + qw_last_error(ctx_) + ")";
+            throw Error(s, msg);
+        }
+    }
+
+    // process-wide default context of the current device
+    static std::shared_ptr<Context> default_for_current_device() {
+        static std::shared_ptr<Context> per_device[64];
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) throw Error(QW_ERR_HIP, "hipGetDevice");
+        if (!per_device[dev]) per_device[dev] = std::make_shared<Context>(dev);
+        return per_device[dev];
+    }
+
+  private:
+    qw_ctx* ctx_ = nullptr;
+};
+
+namespace detail {
+struct WeightDeleter {
+    void operator()(qw_weight* w) const { qw_weight_free(w); }
+};
+using WeightPtr = std::unique_ptr<qw_weight, WeightDeleter>;
+
+inline WeightPtr pack(const Context& c, const std::vector<float>& w, int N, int K, qw_wfmt fmt, const char* name) {
+    if ((int64_t)w.size() != (int64_t)N * K)
+        throw Error(QW_ERR_SHAPE, std::string(name) + ": expected " + std::to_string((int64_t)N * K) + " floats");
+    qw_weight* out = nullptr;
+    c.check(qw_weight_pack(c.get(), w.data(), QW_F32, fmt, N, K, nullptr, &out), name);
+    return WeightPtr(out);
+}
+
+inline void require(const void* p, const char* what) {
+    if (!p) throw Error(QW_ERR_STATE, std::string(what) + ": weights not set");
+}
+}  // namespace detail
+
+// ---------------------------------------------------------------------------
+// MLP: y = down(silu(gate.x) * up.x).  Default storage is INT8 with per-row
+// scales (the reference CudaMLP quantizes in set_weights, mlp_cuda.cu:261-293);
+// pass QW_WFMT_BF16 or QW_WFMT_F32 for the other formats.
+class HipMLP {
+  public:
+    explicit HipMLP(int hidden_size = 1024, int intermediate_size = 3584,
+                    qw_wfmt format = QW_WFMT_INT8_ROWSCALE,
+                    std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden_size), inter_(intermediate_size), fmt_(format),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {}
+
+    void set_weights(const std::vector<float>& gate_proj_weight, const std::vector<float>& up_proj_weight,
+                     const std::vector<float>& down_proj_weight) {
+        const int64_t n = (int64_t)inter_ * hidden_;
+        if ((int64_t)gate_proj_weight.size() != n || (int64_t)up_proj_weight.size() != n)
+            throw Error(QW_ERR_SHAPE, "HipMLP::set_weights: gate/up must be [intermediate][hidden]");
+        qw_weight* gu = nullptr;
+        ctx_->check(qw_weight_pack_glu(ctx_->get(), gate_proj_weight.data(), up_proj_weight.data(), QW_F32, fmt_,
+                                       inter_, hidden_, nullptr, nullptr, &gu),
+                    "HipMLP::set_weights gate/up");
+        gateup_.reset(gu);
+        down_ = detail::pack(*ctx_, down_proj_weight, hidden_, inter_, fmt_, "HipMLP::set_weights down");
+    }
+
+    void forward(const float* input, float* output, int batch_size = 1, hipStream_t stream = nullptr) const {
+        detail::require(down_.get(), "HipMLP::forward");
+        ctx_->check(qw_mlp_fused(ctx_->get(), gateup_.get(), down_.get(), input, QW_F32, nullptr, 1e-6f, nullptr,
+                                 QW_F32, output, QW_F32, batch_size, stream),
+                    "HipMLP::forward");
+    }
+
+    // residual[b] += MLP(input[b])
+    void forward_add_residual(const float* input, float* residual, int batch_size = 1,
+                              hipStream_t stream = nullptr) const {
+        detail::require(down_.get(), "HipMLP::forward_add_residual");
+        ctx_->check(qw_mlp_fused(ctx_->get(), gateup_.get(), down_.get(), input, QW_F32, nullptr, 1e-6f, residual,
+                                 QW_F32, residual, QW_F32, batch_size, stream),
+                    "HipMLP::forward_add_residual");
+    }
+
+    // residual[b] += MLP(RMSNorm(residual[b]) * (1 + gamma)): the post-attention
+    // norm, MLP and residual of one layer in two launches.
+    void forward_norm_add_residual(const float* gamma, float eps, float* residual, int batch_size = 1,
+                                   hipStream_t stream = nullptr) const {
+        detail::require(down_.get(), "HipMLP::forward_norm_add_residual");
+        ctx_->check(qw_mlp_fused(ctx_->get(), gateup_.get(), down_.get(), residual, QW_F32, gamma, eps, residual,
+                                 QW_F32, residual, QW_F32, batch_size, stream),
+                    "HipMLP::forward_norm_add_residual");
+    }
+
+    int hidden_size() const { return hidden_; }
+
+  private:
+    int hidden_, inter_;
+    qw_wfmt fmt_;
+    std::shared_ptr<Context> ctx_;
+    detail::WeightPtr gateup_, down_;
+};
+
+// ---------------------------------------------------------------------------
+// lm_head over the tied embedding E[vocab][hidden], stored BF16 (as
+// CudaLMHead::set_weight converts, lm_head_cuda.cu:163-187) or INT8.
+class HipLMHead {
+  public:
+    explicit HipLMHead(int hidden_size = 1024, int vocab_size = 248320, qw_wfmt format = QW_WFMT_BF16,
+                       std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden_size), vocab_(vocab_size), fmt_(format),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {}
+
+    void set_weight(const std::vector<float>& weight) {
+        E_ = detail::pack(*ctx_, weight, vocab_, hidden_, fmt_, "HipLMHead::set_weight");
+    }
+
+    // A resident row-major BF16 embedding (the tied token embedding).  The
+    // reference borrows it (lm_head_cuda.cu:189-196); the packed tile order
+    // needs its own copy, made on the device without a host round trip.
+    void set_weight_bf16_ptr(const void* d_weight_bf16) {
+        qw_weight* out = nullptr;
+        ctx_->check(qw_weight_pack_device(ctx_->get(), d_weight_bf16, QW_BF16, fmt_, vocab_, hidden_, nullptr, &out),
+                    "HipLMHead::set_weight_bf16_ptr");
+        E_.reset(out);
+    }
+
+    // logits[b][v] = E[v] . input[b]  (FP32 logits, as the reference writes)
+    void forward(const float* input, float* output, int batch_size = 1, hipStream_t stream = nullptr) const {
+        detail::require(E_.get(), "HipLMHead::forward");
+        ctx_->check(qw_linear(ctx_->get(), E_.get(), input, QW_F32, 0, batch_size, output, QW_F32, 0, nullptr, stream),
+                    "HipLMHead::forward");
+    }
+
+    // token_ids[b] = argmax_v logits[b][v] without writing the logits
+    void forward_argmax(const float* input, int32_t* d_token_ids, int batch_size = 1, float* d_max_logit = nullptr,
+                        hipStream_t stream = nullptr) const {
+        detail::require(E_.get(), "HipLMHead::forward_argmax");
+        ctx_->check(qw_lmhead_argmax(ctx_->get(), E_.get(), input, QW_F32, batch_size, d_token_ids, d_max_logit,
+                                     stream),
+                    "HipLMHead::forward_argmax");
+    }
+
+    int hidden_size() const { return hidden_; }
+    int vocab_size() const { return vocab_; }
+
+  private:
+    int hidden_, vocab_;
+    qw_wfmt fmt_;
+    std::shared_ptr<Context> ctx_;
+    detail::WeightPtr E_;
+};
+
+// ---------------------------------------------------------------------------
+// Greedy sampler over materialized FP32 logits: returns the lowest index of
+// the maximum (synchronous, like the reference's sample()).
+class HipGreedyArgmaxSampler {
+  public:
+    explicit HipGreedyArgmaxSampler(int vocab_size, std::shared_ptr<Context> ctx = nullptr)
+        : vocab_(vocab_size), ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {
+        if (hipMalloc(&d_id_, sizeof(int32_t)) != hipSuccess) throw Error(QW_ERR_NOMEM, "HipGreedyArgmaxSampler");
+    }
+    ~HipGreedyArgmaxSampler() { (void)hipFree(d_id_); }
+    HipGreedyArgmaxSampler(const HipGreedyArgmaxSampler&) = delete;
+    HipGreedyArgmaxSampler& operator=(const HipGreedyArgmaxSampler&) = delete;
+
+    int sample(const float* d_logits, hipStream_t stream = nullptr) {
+        ctx_->check(qw_argmax_rows(ctx_->get(), d_logits, QW_F32, 1, vocab_, 0, d_id_, nullptr, stream),
+                    "HipGreedyArgmaxSampler::sample");
+        int32_t id = -1;
+        if (hipMemcpyAsync(&id, d_id_, sizeof(id), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+            hipStreamSynchronize(stream) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipGreedyArgmaxSampler::sample copy");
+        return id;
+    }
+
+  private:
+    int vocab_;
+    std::shared_ptr<Context> ctx_;
+    int32_t* d_id_ = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+// RMSNorm, y = x / sqrt(mean(x^2) + eps) * (1 + w).
+class HipRMSNorm {
+  public:
+    explicit HipRMSNorm(int hidden_size = 1024, float eps = 1e-6f, std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden_size), eps_(eps), ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {}
+    ~HipRMSNorm() { (void)hipFree(d_w_); }
+    HipRMSNorm(const HipRMSNorm&) = delete;
+    HipRMSNorm& operator=(const HipRMSNorm&) = delete;
+
+    void set_weights(const std::vector<float>& weight) {
+        if ((int)weight.size() != hidden_) throw Error(QW_ERR_SHAPE, "HipRMSNorm::set_weights: size != hidden");
+        if (!d_w_ && hipMalloc(&d_w_, sizeof(float) * hidden_) != hipSuccess)
+            throw Error(QW_ERR_NOMEM, "HipRMSNorm::set_weights");
+        if (hipMemcpy(d_w_, weight.data(), sizeof(float) * hidden_, hipMemcpyHostToDevice) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipRMSNorm::set_weights copy");
+    }
+
+    void forward(const float* input, float* output, int batch_size = 1, hipStream_t stream = nullptr) const {
+        detail::require(d_w_, "HipRMSNorm::forward");
+        ctx_->check(qw_rmsnorm(ctx_->get(), input, QW_F32, d_w_, eps_, output, QW_F32, batch_size, hidden_, stream),
+                    "HipRMSNorm::forward");
+    }
+
+    // residual_out = residual_in + attn_out; normed_out = RMSNorm(residual_out)
+    void forward_with_residual(const float* residual_in, const float* attn_out, float* residual_out,
+                               float* normed_out, int batch_size = 1, hipStream_t stream = nullptr) const {
+        detail::require(d_w_, "HipRMSNorm::forward_with_residual");
+        ctx_->check(qw_residual_rmsnorm(ctx_->get(), residual_in, attn_out, QW_F32, residual_out, normed_out, QW_F32,
+                                        d_w_, eps_, batch_size, hidden_, stream),
+                    "HipRMSNorm::forward_with_residual");
+    }
+
+    const float* d_weight() const { return d_w_; }
+    int hidden_size() const { return hidden_; }
+
+  private:
+    int hidden_;
+    float eps_;
+    std::shared_ptr<Context> ctx_;
+    float* d_w_ = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+// Projections of a Gated-DeltaNet layer (language_linear_attn.cpp:136-168,
+// 258-263; linear_attention_cuda.cu:412-466): in_proj_qkv [6144][1024],
+// in_proj_z [2048][1024], in_proj_a / in_proj_b [16][1024],
+// out_proj [1024][2048].  Default storage BF16 (as CudaLinearAttention).
+class HipLinearAttnProjections {
+  public:
+    explicit HipLinearAttnProjections(int hidden = 1024, int qkv_dim = 6144, int z_dim = 2048, int num_v_heads = 16,
+                                      qw_wfmt format = QW_WFMT_BF16, std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden), qkv_(qkv_dim), z_(z_dim), nh_(num_v_heads), fmt_(format),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {}
+
+    void set_weights(const std::vector<float>& in_proj_qkv, const std::vector<float>& in_proj_z,
+                     const std::vector<float>& in_proj_a, const std::vector<float>& in_proj_b,
+                     const std::vector<float>& out_proj) {
+        Wqkv_ = detail::pack(*ctx_, in_proj_qkv, qkv_, hidden_, fmt_, "in_proj_qkv");
+        Wz_ = detail::pack(*ctx_, in_proj_z, z_, hidden_, fmt_, "in_proj_z");
+        Wa_ = detail::pack(*ctx_, in_proj_a, nh_, hidden_, fmt_, "in_proj_a");
+        Wb_ = detail::pack(*ctx_, in_proj_b, nh_, hidden_, fmt_, "in_proj_b");
+        Wo_ = detail::pack(*ctx_, out_proj, hidden_, z_, fmt_, "out_proj");
+    }
+
+    // qkv[b] = Wqkv.x[b], z[b] = Wz.x[b], a[b] = Wa.x[b], beta_raw[b] = Wb.x[b]
+    void project_in(const float* x, float* qkv, float* z, float* a, float* b, int batch_size = 1,
+                    hipStream_t stream = nullptr) const {
+        detail::require(Wo_.get(), "HipLinearAttnProjections::project_in");
+        lin(Wqkv_.get(), x, qkv, batch_size, nullptr, stream, "in_proj_qkv");
+        lin(Wz_.get(), x, z, batch_size, nullptr, stream, "in_proj_z");
+        lin(Wa_.get(), x, a, batch_size, nullptr, stream, "in_proj_a");
+        lin(Wb_.get(), x, b, batch_size, nullptr, stream, "in_proj_b");
+    }
+
+    // residual[b] += Wo.core[b]
+    void project_out_add_residual(const float* core, float* residual, int batch_size = 1,
+                                  hipStream_t stream = nullptr) const {
+        detail::require(Wo_.get(), "HipLinearAttnProjections::project_out_add_residual");
+        qw_epilogue ep{};
+        ep.flags = QW_EP_RESIDUAL;
+        ep.residual = residual;
+        ep.residual_dtype = QW_F32;
+        lin(Wo_.get(), core, residual, batch_size, &ep, stream, "out_proj");
+    }
+
+  private:
+    void lin(const qw_weight* W, const float* x, float* y, int M, const qw_epilogue* ep, hipStream_t st,
+             const char* what) const {
+        ctx_->check(qw_linear(ctx_->get(), W, x, QW_F32, 0, M, y, QW_F32, 0, ep, st), what);
+    }
+    int hidden_, qkv_, z_, nh_;
+    qw_wfmt fmt_;
+    std::shared_ptr<Context> ctx_;
+    detail::WeightPtr Wqkv_, Wz_, Wa_, Wb_, Wo_;
+};
+
+// ---------------------------------------------------------------------------
+// Projections of a gated full-attention layer (language_full_attn.cpp:127-156,
+// 218-223): q_proj [2*heads*head_dim][hidden] interleaved per head as
+// [Q(head_dim) | gate(head_dim)], k_proj / v_proj [kv_heads*head_dim][hidden],
+// o_proj [hidden][heads*head_dim].  project_in de-interleaves Q and gate in
+// the epilogue.
+class HipFullAttnProjections {
+  public:
+    explicit HipFullAttnProjections(int hidden = 1024, int heads = 8, int kv_heads = 2, int head_dim = 256,
+                                    qw_wfmt format = QW_WFMT_F32, std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden), heads_(heads), kvh_(kv_heads), hd_(head_dim), fmt_(format),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {}
+
+    void set_weights(const std::vector<float>& q_proj, const std::vector<float>& k_proj,
+                     const std::vector<float>& v_proj, const std::vector<float>& o_proj) {
+        Wq_ = detail::pack(*ctx_, q_proj, 2 * heads_ * hd_, hidden_, fmt_, "q_proj");
+        Wk_ = detail::pack(*ctx_, k_proj, kvh_ * hd_, hidden_, fmt_, "k_proj");
+        Wv_ = detail::pack(*ctx_, v_proj, kvh_ * hd_, hidden_, fmt_, "v_proj");
+        Wo_ = detail::pack(*ctx_, o_proj, hidden_, heads_ * hd_, fmt_, "o_proj");
+    }
+
+    // q[b] / gate[b]: [heads*head_dim] each; k[b], v[b]: [kv_heads*head_dim]
+    void project_in(const float* x, float* q, float* gate, float* k, float* v, int batch_size = 1,
+                    hipStream_t stream = nullptr) const {
+        detail::require(Wo_.get(), "HipFullAttnProjections::project_in");
+        qw_epilogue ep{};
+        ep.flags = QW_EP_SPLIT;
+        ep.split_period = hd_;
+        ep.y2 = gate;
+        ctx_->check(qw_linear(ctx_->get(), Wq_.get(), x, QW_F32, 0, batch_size, q, QW_F32, heads_ * hd_, &ep, stream),
+                    "q_proj");
+        ctx_->check(qw_linear(ctx_->get(), Wk_.get(), x, QW_F32, 0, batch_size, k, QW_F32, 0, nullptr, stream),
+                    "k_proj");
+        ctx_->check(qw_linear(ctx_->get(), Wv_.get(), x, QW_F32, 0, batch_size, v, QW_F32, 0, nullptr, stream),
+                    "v_proj");
+    }
+
+    // residual[b] += Wo.core[b]
+    void project_out_add_residual(const float* core, float* residual, int batch_size = 1,
+                                  hipStream_t stream = nullptr) const {
+        detail::require(Wo_.get(), "HipFullAttnProjections::project_out_add_residual");
+        qw_epilogue ep{};
+        ep.flags = QW_EP_RESIDUAL;
+        ep.residual = residual;
+        ep.residual_dtype = QW_F32;
+        ctx_->check(qw_linear(ctx_->get(), Wo_.get(), core, QW_F32, 0, batch_size, residual, QW_F32, 0, &ep, stream),
+                    "o_proj");
+    }
+
+  private:
+    int hidden_, heads_, kvh_, hd_;
+    qw_wfmt fmt_;
+    std::shared_ptr<Context> ctx_;
+    detail::WeightPtr Wq_, Wk_, Wv_, Wo_;
+};
+
+}  // namespace hip
+}  // namespace qwen

@@ -809,6 +809,21 @@ qw_status qw_silu_mul(qw_ctx* ctx, const void* g, const void* u, void* h, qw_dty
     return QW_OK;
 }
 
+qw_status qw_argmax_rows(qw_ctx* ctx, const void* logits, qw_dtype dt, int M, int V, int ld, int32_t* token_ids,
+                         float* max_logit, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!logits || !token_ids) return fail(ctx, QW_ERR_NULL, "logits and token_ids are required");
+    if (dt != QW_F32 && dt != QW_BF16 && dt != QW_F16) return fail(ctx, QW_ERR_DTYPE, "logits dtype unsupported");
+    if (M < 1 || V < 1) return fail(ctx, QW_ERR_SHAPE, "M and V must be >= 1");
+    if (ld == 0) ld = V;
+    if (ld < V) return fail(ctx, QW_ERR_SHAPE, "ld must be >= V");
+    if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
+    hipError_t e = qwk::launch_argmax_rows(logits, (int)dt, M, V, ld, ctx->keys, ctx->done, token_ids, max_logit,
+                                           stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "argmax launch");
+    return QW_OK;
+}
+
 // ---------------------------------------------------------------------------
 // graphs
 // ---------------------------------------------------------------------------

@@ -102,6 +102,8 @@ hipError_t launch_rmsnorm(const void* x, int xdt, const void* add, void* sum_out
                           hipStream_t stream);
 hipError_t launch_rmsnorm_ld(const void* x, int xdt, int ldx, const float* gamma, float eps, void* y, int ydt,
                              int ldy, int M, int K, hipStream_t stream);
+hipError_t launch_argmax_rows(const void* logits, int dt, int M, int V, int64_t ld, unsigned long long* keys,
+                              unsigned* done, int32_t* ids, float* maxv, hipStream_t stream);
 hipError_t launch_silu_mul(const void* g, const void* u, void* h, int dt, int64_t n,
                            hipStream_t stream);
 

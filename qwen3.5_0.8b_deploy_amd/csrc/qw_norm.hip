@@ -6,6 +6,8 @@
 // writes it back (rmsnorm_cuda.cu:103-170, fused_kernels.cu:23-65).
 // One 256-thread workgroup per token row; the row stays in registers between
 // the reduction and the scaling pass, so each element is read once.
+#include <algorithm>
+
 #include "qw_device.hpp"
 #include "qw_kernels.hpp"
 
@@ -54,6 +56,62 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const void* g, const void
                                                        int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) store_act(h, dt, i, silu_f(load_act(g, dt, i)) * load_act(u, dt, i));
+}
+
+// Row-wise greedy argmax over materialized logits (GpuGreedyArgmaxSampler,
+// gpu_sampler_argmax.cu:14-93, without its host-side second stage): grid
+// (nblk, M); each workgroup scans a contiguous slice of one row, reduces
+// (logit, index) keys across its waves and merges them into keys[m] with a
+// 64-bit atomic max (lowest index on ties, std::max_element's rule); the last
+// workgroup decodes every row and resets the keys and the counter.
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const void* logits, int dt, int V, int64_t ld,
+                                                          unsigned long long* keys, unsigned* done,
+                                                          int32_t* ids, float* maxv, int M) {
+    __shared__ unsigned long long wbest[4];
+    __shared__ int last;
+    const int m = blockIdx.y;
+    const int per = (V + gridDim.x - 1) / gridDim.x;
+    const int v0 = blockIdx.x * per;
+    const int v1 = min(V, v0 + per);
+    unsigned long long best = 0ull;
+    for (int v = v0 + threadIdx.x; v < v1; v += 256) {
+        const unsigned long long k = argmax_key(load_act(logits, dt, (int64_t)m * ld + v), (uint32_t)v);
+        best = k > best ? k : best;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(best, off);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = wbest[0];
+        for (int w = 1; w < 4; ++w) b = wbest[w] > b ? wbest[w] : b;
+        if (b) __hip_atomic_fetch_max(&keys[m], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const unsigned total = gridDim.x * gridDim.y;
+        const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = (old == total - 1) ? 1 : 0;
+    }
+    __syncthreads();
+    if (last) {
+        for (int r = threadIdx.x; r < M; r += 256) {
+            const unsigned long long k = __hip_atomic_exchange(&keys[r], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ids[r] = (int32_t)key_index(k);
+            if (maxv) maxv[r] = key_value(k);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+hipError_t launch_argmax_rows(const void* logits, int dt, int M, int V, int64_t ld, unsigned long long* keys,
+                              unsigned* done, int32_t* ids, float* maxv, hipStream_t stream) {
+    int nblk = (V + 2047) / 2048;
+    const int cap = std::max(1, 1024 / M);
+    nblk = std::max(1, std::min(nblk, cap));
+    hipLaunchKernelGGL(argmax_rows_kernel, dim3(nblk, M), dim3(256), 0, stream, logits, dt, V, ld, keys, done, ids,
+                       maxv, M);
+    return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(const void* x, int xdt, const void* add, void* sum_out,

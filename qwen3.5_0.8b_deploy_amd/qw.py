@@ -30,7 +30,7 @@ EXPORTS = [
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
     "qw_weight_pack_glu_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
-    "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_rmsnorm", "qw_residual_rmsnorm",
+    "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
 
@@ -87,6 +87,7 @@ def lib():
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
         "qw_device_error": ([_vp, _vp], _i),
         "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+        "qw_argmax_rows": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
         "qw_rmsnorm": ([_vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _vp], _i),
         "qw_residual_rmsnorm": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _f, _i, _i, _vp], _i),
         "qw_silu_mul": ([_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp], _i),
@@ -303,6 +304,13 @@ def lmhead_argmax(ctx, E, h, ids, max_logit=None, stream=None):
     M = h.shape[0] if h.dim() == 2 else 1
     ctx.check(lib().qw_lmhead_argmax(ctx.handle, E.handle, _ptr(h), _torch_code(h), M, _ptr(ids),
                                      _ptr(max_logit), _stream(stream)))
+
+
+def argmax_rows(ctx, logits, ids, max_logit=None, stream=None):
+    """Greedy argmax of each row of logits [M][V] (lowest index on ties)."""
+    M, V = logits.shape
+    ctx.check(lib().qw_argmax_rows(ctx.handle, _ptr(logits), _torch_code(logits), M, V, logits.stride(0),
+                                   _ptr(ids), _ptr(max_logit), _stream(stream)))
 
 
 def rmsnorm(ctx, x, gamma, y, eps=1e-6, stream=None):

@@ -1,0 +1,243 @@
+// test_facade.cpp -- GPU test of the C++ operator facade (include/qw_ops.hpp):
+// each reference-shaped operator is driven exactly as the reference's caller
+// drives it (host std::vector<float> weights, device FP32 activations) and
+// checked against the CPU oracle (oracle/qw_oracle.h).  Prints one line per
+// case and exits non-zero on the first failure.  Built by
+// __graft_entry__.build(); run by tests/test_gpu_facade.py.
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#include "qw_ops.hpp"
+#include "qw_oracle.h"
+
+using qwen::hip::HipFullAttnProjections;
+using qwen::hip::HipGreedyArgmaxSampler;
+using qwen::hip::HipLinearAttnProjections;
+using qwen::hip::HipLMHead;
+using qwen::hip::HipMLP;
+using qwen::hip::HipRMSNorm;
+
+static int g_fail = 0;
+
+static std::vector<float> normal(size_t n, uint64_t seed, float std = 1.0f) {
+    std::vector<float> v(n);
+    orc_fill_normal(v.data(), (int64_t)n, seed, 0.0f, std);
+    return v;
+}
+
+struct Dev {
+    float* p = nullptr;
+    size_t n = 0;
+    explicit Dev(size_t n_) : n(n_) {
+        if (hipMalloc(&p, n * sizeof(float)) != hipSuccess) { std::printf("hipMalloc failed\n"); std::exit(2); }
+    }
+    Dev(const std::vector<float>& h) : Dev(h.size()) { put(h); }
+    ~Dev() { (void)hipFree(p); }
+    void put(const std::vector<float>& h) { (void)hipMemcpy(p, h.data(), n * sizeof(float), hipMemcpyHostToDevice); }
+    std::vector<float> get() const {
+        std::vector<float> h(n);
+        (void)hipDeviceSynchronize();
+        (void)hipMemcpy(h.data(), p, n * sizeof(float), hipMemcpyDeviceToHost);
+        return h;
+    }
+};
+
+static double relerr(const std::vector<float>& got, const std::vector<float>& ref) {
+    double num = 0, den = 0;
+    for (size_t i = 0; i < ref.size(); ++i) {
+        num = std::fmax(num, std::fabs((double)got[i] - ref[i]));
+        den = std::fmax(den, std::fabs((double)ref[i]));
+    }
+    return num / (den > 0 ? den : 1.0);
+}
+
+static void report(const char* name, double err, double tol) {
+    const bool ok = err <= tol;
+    std::printf("%s %s relerr=%.3g tol=%.1g\n", ok ? "PASS" : "FAIL", name, err, tol);
+    std::fflush(stdout);
+    if (!ok) g_fail = 1;
+}
+
+// dequantize the oracle's INT8 recipe so the CPU reference sees the stored weights
+static std::vector<float> dequant(const std::vector<float>& W, int N, int K) {
+    std::vector<int8_t> q((size_t)N * K);
+    std::vector<float> s(N), out((size_t)N * K);
+    orc_quantize_rowscale(W.data(), q.data(), s.data(), N, K);
+    for (int o = 0; o < N; ++o)
+        for (int k = 0; k < K; ++k) out[(size_t)o * K + k] = (float)q[(size_t)o * K + k] * s[o];
+    return out;
+}
+
+static void test_mlp() {
+    const int H = 1024, I = 3584, B = 3;
+    auto Wg = normal((size_t)I * H, 1, 0.02f), Wu = normal((size_t)I * H, 2, 0.02f), Wd = normal((size_t)H * I, 3, 0.02f);
+    auto x = normal((size_t)B * H, 4);
+    auto r0 = normal((size_t)B * H, 5);
+    // FP32 storage: forward == reference MLP::forward_batch to FP32 rounding
+    {
+        HipMLP mlp(H, I, QW_WFMT_F32);
+        mlp.set_weights(Wg, Wu, Wd);
+        Dev dx(x), dy((size_t)B * H);
+        mlp.forward(dx.p, dy.p, B);
+        std::vector<float> ref((size_t)B * H);
+        orc_mlp(Wg.data(), Wu.data(), Wd.data(), x.data(), ref.data(), B, H, I);
+        report("HipMLP<f32>::forward", relerr(dy.get(), ref), 1e-5);
+    }
+    // INT8 storage (the reference CudaMLP default): forward_add_residual ADDS
+    {
+        HipMLP mlp(H, I);
+        mlp.set_weights(Wg, Wu, Wd);
+        Dev dx(x), dr(r0);
+        mlp.forward_add_residual(dx.p, dr.p, B);
+        auto qg = dequant(Wg, I, H), qu = dequant(Wu, I, H), qd = dequant(Wd, H, I);
+        std::vector<float> ref((size_t)B * H);
+        orc_mlp(qg.data(), qu.data(), qd.data(), x.data(), ref.data(), B, H, I);
+        for (size_t i = 0; i < ref.size(); ++i) ref[i] += r0[i];
+        report("HipMLP<int8>::forward_add_residual", relerr(dr.get(), ref), 1e-3);
+    }
+}
+
+static void test_rmsnorm() {
+    const int H = 1024, B = 4;
+    auto w = normal(H, 10, 0.02f), r = normal((size_t)B * H, 11), a = normal((size_t)B * H, 12);
+    HipRMSNorm norm(H, 1e-6f);
+    norm.set_weights(w);
+    Dev dr(r), da(a), dro((size_t)B * H), dno((size_t)B * H), dy((size_t)B * H);
+    norm.forward(dr.p, dy.p, B);
+    std::vector<float> ref((size_t)B * H), ro((size_t)B * H), no((size_t)B * H);
+    orc_rmsnorm(r.data(), w.data(), ref.data(), B, H, 1e-6f);
+    report("HipRMSNorm::forward", relerr(dy.get(), ref), 1e-5);
+    norm.forward_with_residual(dr.p, da.p, dro.p, dno.p, B);
+    orc_residual_rmsnorm(r.data(), a.data(), w.data(), ro.data(), no.data(), B, H, 1e-6f);
+    report("HipRMSNorm::forward_with_residual(residual)", relerr(dro.get(), ro), 0.0);
+    report("HipRMSNorm::forward_with_residual(normed)", relerr(dno.get(), no), 1e-5);
+}
+
+static void test_lmhead_and_sampler() {
+    const int H = 1024, V = 50000, B = 2;
+    auto E = normal((size_t)V * H, 20, 0.02f), x = normal((size_t)B * H, 21);
+    HipLMHead head(H, V);
+    head.set_weight(E);
+    Dev dx(x), dl((size_t)B * V);
+    head.forward(dx.p, dl.p, B);
+    // BF16 storage: the reference rounds E to BF16 as well (lm_head_cuda.cu:177-180)
+    std::vector<uint16_t> eb((size_t)V * H);
+    std::vector<float> Er((size_t)V * H), ref((size_t)B * V);
+    orc_f32_to_bf16_n(E.data(), eb.data(), (int64_t)E.size());
+    orc_bf16_to_f32_n(eb.data(), Er.data(), (int64_t)E.size());
+    orc_linear_f32(Er.data(), x.data(), ref.data(), B, V, H);
+    auto logits = dl.get();
+    report("HipLMHead::forward", relerr(logits, ref), 1e-5);
+
+    HipGreedyArgmaxSampler sampler(V);
+    const int id = sampler.sample(dl.p);
+    const int want = orc_argmax_first(logits.data(), V);
+    report("HipGreedyArgmaxSampler::sample", id == want ? 0.0 : 1.0, 0.0);
+
+    int32_t* d_ids = nullptr;
+    (void)hipMalloc(&d_ids, B * sizeof(int32_t));
+    head.forward_argmax(dx.p, d_ids, B);
+    int32_t ids[2];
+    (void)hipDeviceSynchronize();
+    (void)hipMemcpy(ids, d_ids, sizeof(ids), hipMemcpyDeviceToHost);
+    int32_t rids[2];
+    float rmax[2];
+    orc_lmhead_argmax(Er.data(), x.data(), rids, rmax, B, V, H);
+    // fused argmax vs the oracle: exact unless the top-2 gap is inside the error bound
+    bool ok = true;
+    for (int b = 0; b < B; ++b) {
+        if (ids[b] == rids[b]) continue;
+        const float* lr = ref.data() + (size_t)b * V;
+        if (std::fabs(lr[ids[b]] - lr[rids[b]]) > 1e-5f * std::fabs(rmax[b])) ok = false;
+    }
+    report("HipLMHead::forward_argmax", ok ? 0.0 : 1.0, 0.0);
+    (void)hipFree(d_ids);
+}
+
+static void test_attention_projections() {
+    const int H = 1024, B = 2;
+    {
+        auto qkv = normal((size_t)6144 * H, 30, 0.02f), z = normal((size_t)2048 * H, 31, 0.02f);
+        auto a = normal((size_t)16 * H, 32, 0.02f), b = normal((size_t)16 * H, 33, 0.02f);
+        auto o = normal((size_t)H * 2048, 34, 0.02f);
+        HipLinearAttnProjections p(H, 6144, 2048, 16, QW_WFMT_F32);
+        p.set_weights(qkv, z, a, b, o);
+        auto x = normal((size_t)B * H, 35), core = normal((size_t)B * 2048, 36), r = normal((size_t)B * H, 37);
+        Dev dx(x), dqkv((size_t)B * 6144), dz((size_t)B * 2048), da((size_t)B * 16), db((size_t)B * 16), dc(core),
+            dr(r);
+        p.project_in(dx.p, dqkv.p, dz.p, da.p, db.p, B);
+        p.project_out_add_residual(dc.p, dr.p, B);
+        std::vector<float> rq((size_t)B * 6144), rz((size_t)B * 2048), ra((size_t)B * 16), rb((size_t)B * 16),
+            ro((size_t)B * H);
+        orc_linear_f32(qkv.data(), x.data(), rq.data(), B, 6144, H);
+        orc_linear_f32(z.data(), x.data(), rz.data(), B, 2048, H);
+        orc_linear_f32(a.data(), x.data(), ra.data(), B, 16, H);
+        orc_linear_f32(b.data(), x.data(), rb.data(), B, 16, H);
+        orc_linear_f32(o.data(), core.data(), ro.data(), B, H, 2048);
+        for (size_t i = 0; i < ro.size(); ++i) ro[i] += r[i];
+        report("HipLinearAttnProjections qkv", relerr(dqkv.get(), rq), 1e-5);
+        report("HipLinearAttnProjections z", relerr(dz.get(), rz), 1e-5);
+        report("HipLinearAttnProjections a", relerr(da.get(), ra), 1e-5);
+        report("HipLinearAttnProjections b", relerr(db.get(), rb), 1e-5);
+        report("HipLinearAttnProjections out+residual", relerr(dr.get(), ro), 1e-5);
+    }
+    {
+        auto q = normal((size_t)4096 * H, 40, 0.02f), k = normal((size_t)512 * H, 41, 0.02f);
+        auto v = normal((size_t)512 * H, 42, 0.02f), o = normal((size_t)H * 2048, 43, 0.02f);
+        HipFullAttnProjections p(H, 8, 2, 256, QW_WFMT_F32);
+        p.set_weights(q, k, v, o);
+        auto x = normal((size_t)B * H, 44), core = normal((size_t)B * 2048, 45), r = normal((size_t)B * H, 46);
+        Dev dx(x), dq((size_t)B * 2048), dg((size_t)B * 2048), dk((size_t)B * 512), dv((size_t)B * 512), dc(core),
+            dr(r);
+        p.project_in(dx.p, dq.p, dg.p, dk.p, dv.p, B);
+        p.project_out_add_residual(dc.p, dr.p, B);
+        std::vector<float> raw((size_t)B * 4096), rq((size_t)B * 2048), rg((size_t)B * 2048), rk((size_t)B * 512),
+            rv((size_t)B * 512), ro((size_t)B * H);
+        orc_linear_f32(q.data(), x.data(), raw.data(), B, 4096, H);
+        orc_split_q_gate(raw.data(), rq.data(), rg.data(), B, 8, 256);
+        orc_linear_f32(k.data(), x.data(), rk.data(), B, 512, H);
+        orc_linear_f32(v.data(), x.data(), rv.data(), B, 512, H);
+        orc_linear_f32(o.data(), core.data(), ro.data(), B, H, 2048);
+        for (size_t i = 0; i < ro.size(); ++i) ro[i] += r[i];
+        report("HipFullAttnProjections q", relerr(dq.get(), rq), 1e-5);
+        report("HipFullAttnProjections gate", relerr(dg.get(), rg), 1e-5);
+        report("HipFullAttnProjections k", relerr(dk.get(), rk), 1e-5);
+        report("HipFullAttnProjections v", relerr(dv.get(), rv), 1e-5);
+        report("HipFullAttnProjections o+residual", relerr(dr.get(), ro), 1e-5);
+    }
+}
+
+static void test_errors() {
+    HipMLP mlp(1024, 3584);
+    bool threw = false;
+    try {
+        mlp.forward(nullptr, nullptr, 1);
+    } catch (const qwen::hip::Error& e) {
+        threw = e.status == QW_ERR_STATE;
+    }
+    report("HipMLP::forward before set_weights throws", threw ? 0.0 : 1.0, 0.0);
+    threw = false;
+    try {
+        mlp.set_weights(std::vector<float>(10), std::vector<float>(10), std::vector<float>(10));
+    } catch (const qwen::hip::Error& e) {
+        threw = e.status == QW_ERR_SHAPE;
+    }
+    report("HipMLP::set_weights shape check", threw ? 0.0 : 1.0, 0.0);
+}
+
+int main() {
+    try {
+        test_errors();
+        test_rmsnorm();
+        test_mlp();
+        test_attention_projections();
+        test_lmhead_and_sampler();
+    } catch (const std::exception& e) {
+        std::printf("FAIL exception: %s\n", e.what());
+        return 1;
+    }
+    std::printf(g_fail ? "FACADE FAILED\n" : "FACADE OK\n");
+    return g_fail;
+}

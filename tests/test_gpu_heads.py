@@ -274,3 +274,24 @@ def test_mlp_one_launch_path(qw, oracle, relerr, fmt, M):
     assert relerr(host(ys[0]), ref) <= bar
     del gu, dn
     c.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("M,V,dt", [(1, 248320, "f32"), (3, 5000, "f32"), (130, 4099, "bf16"), (1, 7, "f32")])
+def test_argmax_rows(qw, ctx, oracle, M, V, dt):
+    """Row argmax over materialized logits against the reference Sampler rule
+    (oracle argmax_first), with planted exact ties in every other row."""
+    L = oracle.normal((M, V), 600 + M)
+    for m in range(0, M, 2):
+        L[m, [V // 3, V - 1, V // 2]] = 7.5
+    if dt == "bf16":
+        L = oracle.round_bf16(L)
+    t = dev(L).to(torch.bfloat16 if dt == "bf16" else torch.float32)
+    ids = torch.empty(M, dtype=torch.int32, device="cuda")
+    mx = torch.empty(M, device="cuda")
+    for _ in range(2):  # second call checks the keys/counter were reset
+        qw.argmax_rows(ctx, t, ids, mx)
+        torch.cuda.synchronize()
+        ref = [oracle.argmax_first(r) for r in L]
+        assert list(ids.cpu().numpy()) == ref
+        assert np.array_equal(mx.cpu().numpy(), L.max(axis=1))
