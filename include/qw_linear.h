@@ -104,6 +104,17 @@ qw_status qw_weight_pack_glu_device(qw_ctx* ctx, const void* gate, const void* u
  * caller keeps ownership of `packed` and `scales`. */
 qw_status qw_weight_wrap_packed(qw_ctx* ctx, void* packed, float* scales, qw_wfmt fmt, int N,
                                 int K, qw_weight** out);
+/* Fold an RMSNorm weight into a BF16 or F32 weight: W[o][k] *= (1 + gamma[k])
+ * (device gamma[K], asynchronous on `stream`).  Afterwards the weight is used
+ * with QW_EP_NORM_X and gamma = NULL (qw_mlp_fused: gamma = NULL, the norm is
+ * implied), and the kernels only scale by 1/rms(x): no per-call gamma
+ * traffic.  Same math as RMSNorm(x)*(1+gamma) followed by the projection
+ * (rounding moves from the activation to the weight).  No reference
+ * counterpart: the reference applies the norm weight to the activation
+ * (language_common.cpp:21-36) before the MLP (language_mlp.cpp:53-91).
+ * INT8 weights are refused (QW_ERR_DTYPE): folding would change their
+ * quantization. */
+qw_status qw_weight_fold_norm(qw_ctx* ctx, qw_weight* w, const float* gamma, hipStream_t stream);
 qw_status qw_weight_free(qw_weight* w);
 /* Size, shape and format of a packed weight (any out pointer may be NULL). */
 qw_status qw_weight_info(const qw_weight* w, int* N, int* K, qw_wfmt* fmt, int* is_glu,
@@ -121,7 +132,8 @@ qw_status qw_weight_unpack(qw_ctx* ctx, const qw_weight* w, void* dst, float* sc
  * Fusions available on qw_linear / qw_gemm. */
 enum {
     QW_EP_RESIDUAL = 1u << 0, /* y = acc + residual[m][o] (residual may alias y) */
-    QW_EP_NORM_X = 1u << 1,   /* x := RMSNorm(x)*(1+gamma) before the product   */
+    QW_EP_NORM_X = 1u << 1,   /* x := RMSNorm(x)*(1+gamma) before the product
+                                 (gamma NULL: weight folded, qw_weight_fold_norm) */
     QW_EP_SPLIT = 1u << 2     /* rows alternate in blocks of split_period between
                                  y and y2 (full-attention Q / output gate) */
 };

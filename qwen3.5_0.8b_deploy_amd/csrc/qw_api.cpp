@@ -24,6 +24,7 @@ struct qw_ctx {
     int force_nw = 0;        // waves per skinny workgroup (0: automatic)
     int force_nw_glu = 0;    // same, GLU weights only
     bool mlp_fused = false;  // one-launch MLP block (QW_MLP_FUSED=1)
+    bool gemv = true;        // register-direct GEMV for M <= 16 (QW_GEMV=0: skinny kernel)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -58,6 +59,7 @@ struct qw_weight {
     size_t bytes = 0;
     bool owns = true;
     bool in_arena = false;
+    bool norm_folded = false;  // (1 + gamma) of an RMSNorm multiplied into the columns
 };
 
 struct qw_graph {
@@ -157,6 +159,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = nw_of(v);
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
+    if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(4096, 8224, 4096);
     workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(3u << 20));
     workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
@@ -407,6 +410,18 @@ qw_status qw_weight_device_ptrs(const qw_weight* w, const void** packed, const f
     return QW_OK;
 }
 
+qw_status qw_weight_fold_norm(qw_ctx* ctx, qw_weight* w, const float* gamma, hipStream_t stream) {
+    if (!ctx || !w) return QW_ERR_NULL;
+    if (!gamma) return fail(ctx, QW_ERR_NULL, "gamma is NULL");
+    if (w->wf == QW_WFMT_INT8_ROWSCALE)
+        return fail(ctx, QW_ERR_DTYPE, "folding into INT8 weights would change their quantization");
+    if (w->norm_folded) return fail(ctx, QW_ERR_STATE, "the weight already carries a norm weight");
+    hipError_t e = qwk::launch_fold_norm(w->packed, w->wf, w->phys_tiles, w->ksteps, gamma, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "fold launch");
+    w->norm_folded = true;
+    return QW_OK;
+}
+
 qw_status qw_weight_unpack(qw_ctx* ctx, const qw_weight* w, void* dst, float* scales_dst) {
     if (!ctx || !w) return QW_ERR_NULL;
     if (!dst) return fail(ctx, QW_ERR_NULL, "dst is NULL");
@@ -478,8 +493,16 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
         const int want = (ctx->min_items + a.n_groups - 1) / a.n_groups;
         S = std::max(1, std::min(want, W->ksteps / nw));
     }
+    // Register-direct GEMV wherever it measured faster than LDS staging; the
+    // one exception is a single BF16 token with a per-call gamma, where the
+    // gamma traffic of every lane outweighs the saved staging pass.
+    const bool gamma_call = ep && (ep->flags & QW_EP_NORM_X) && ep->gamma;
+    const bool direct = ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, M) &&
+                        !(M == 1 && gamma_call && W->wf == QW_WFMT_BF16);
+    if (direct)
+        nw = qwk::gemv_waves(W->wf, W->glu != 0, argmax, ep && (ep->flags & QW_EP_NORM_X), nw);
     // the activation slice of a split must fit the workgroup's LDS
-    while (qwk::skinny_lds_bytes(W->wf, (int)xdt, M, (W->ksteps + S - 1) / S) > qwk::kSkinnyMaxLds) {
+    while (!direct && qwk::skinny_lds_bytes(W->wf, (int)xdt, M, (W->ksteps + S - 1) / S) > qwk::kSkinnyMaxLds) {
         if (argmax || S >= W->ksteps) return fail(ctx, QW_ERR_SHAPE, "K=%d too large for the skinny kernel", W->K);
         ++S;
     }
@@ -522,7 +545,8 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     grid = std::max(S, grid - grid % S);
     if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * dsize(xdt) >= (1ull << 32))
         return fail(ctx, QW_ERR_SHAPE, "operands above 4 GiB are not supported");
-    hipError_t e = qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream);
+    hipError_t e = direct ? qwk::launch_gemv(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream)
+                          : qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "skinny kernel launch");
     return QW_OK;
 }
@@ -603,8 +627,11 @@ static qw_status check_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw
             if (ep->ld_residual != 0 && ep->ld_residual < W->N) return fail(ctx, QW_ERR_SHAPE, "ld_residual < N");
         }
         if (ep->flags & QW_EP_NORM_X) {
-            if (!ep->gamma) return fail(ctx, QW_ERR_NULL, "gamma is NULL");
-            if (!aligned(ep->gamma, 16)) return fail(ctx, QW_ERR_ALIGN, "gamma must be 16-byte aligned");
+            if (!ep->gamma && !W->norm_folded)
+                return fail(ctx, QW_ERR_NULL, "gamma is NULL and the weight carries no folded norm weight");
+            if (ep->gamma && W->norm_folded)
+                return fail(ctx, QW_ERR_INVALID, "the weight already carries the norm weight: pass gamma = NULL");
+            if (ep->gamma && !aligned(ep->gamma, 16)) return fail(ctx, QW_ERR_ALIGN, "gamma must be 16-byte aligned");
             if (!(ep->eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
         }
         if (ep->flags & QW_EP_SPLIT) {
@@ -699,6 +726,9 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
     if (down->K != I || down->N != H)
         return fail(ctx, QW_ERR_SHAPE, "down is [%d][%d], expected [%d][%d]", down->N, down->K, H, I);
     if (M < 1) return fail(ctx, QW_ERR_SHAPE, "M=%d must be >= 1", M);
+    if (gateup->norm_folded && gamma)
+        return fail(ctx, QW_ERR_INVALID, "gateup already carries the norm weight: pass gamma = NULL");
+    const bool norm = gamma != nullptr || gateup->norm_folded;
     // intermediate h keeps the precision the down projection consumes
     const qw_dtype hdt = gateup->wf == QW_WFMT_F32 ? QW_F32 : (gateup->wf == QW_WFMT_BF16 ? QW_BF16 : QW_F16);
     const size_t per_tok = (size_t)I * dsize(hdt);
@@ -709,12 +739,12 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         valid_act(xdt) && valid_act(ydt) && (!residual || valid_act(residual_dtype)) &&
         aligned(x, 16) && (H * dsize(xdt)) % 16 == 0 && (!gamma || aligned(gamma, 16)) &&
         qwk::mlp_fused_lds_bytes(gateup->wf, (int)xdt, M, H, I) <= qwk::kSkinnyMaxLds) {
-        if (gamma && !(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
+        if (norm && !(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
         qwk::MlpArgs p{};
         qwk::SkinnyArgs& u = p.up;
         u.w = gateup->packed; u.scales = gateup->scales; u.x = x; u.ldx = H; u.M = M; u.K = H; u.N = I;
         u.n_groups = (I + 15) / 16; u.S = 1; u.ksteps = gateup->ksteps; u.n_items = u.n_groups;
-        u.flags = gamma ? QW_EP_NORM_X : 0u; u.gamma = gamma; u.eps = eps;
+        u.flags = norm ? QW_EP_NORM_X : 0u; u.gamma = gamma; u.eps = eps;
         u.y = ctx->scratch; u.ydt = hdt; u.ldy = I;
         qwk::SkinnyArgs& d = p.down;
         d.w = down->packed; d.scales = down->scales; d.x = ctx->scratch; d.ldx = I; d.M = M; d.K = I; d.N = H;
@@ -731,7 +761,7 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         return QW_OK;
     }
     qw_epilogue e1{};
-    if (gamma) {
+    if (norm) {
         e1.flags = QW_EP_NORM_X;
         e1.gamma = gamma;
         e1.eps = eps;
@@ -745,7 +775,7 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         const int mc = std::min(chunk, M - m0);
         const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * H * dsize(xdt);
         void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * H * dsize(ydt);
-        qw_status s = qw_linear(ctx, gateup, xc, xdt, H, mc, ctx->scratch, hdt, I, gamma ? &e1 : nullptr, stream);
+        qw_status s = qw_linear(ctx, gateup, xc, xdt, H, mc, ctx->scratch, hdt, I, norm ? &e1 : nullptr, stream);
         if (s != QW_OK) return s;
         if (residual) e2.residual = static_cast<const uint8_t*>(residual) + (size_t)m0 * H * dsize(residual_dtype);
         s = qw_linear(ctx, down, ctx->scratch, hdt, I, mc, yc, ydt, H, residual ? &e2 : nullptr, stream);

@@ -1,0 +1,447 @@
+// qw_gemv.hip -- decode GEMV for gfx950 with register-direct activations
+// (M <= 16 tokens; BF16 weights with BF16 activations, INT8 weights with F16
+// or BF16 activations).
+//
+// Why a second small-M kernel.  The skinny kernel (qw_skinny.hip) stages the
+// activations of its K range into LDS before any MFMA can run: a global load
+// round trip, an LDS write pass and a workgroup barrier on the critical path
+// of every launch.  At decode the whole launch lasts a few microseconds, so
+// that prologue is a large share of it.  Here each lane loads its own MFMA B
+// operand straight from global memory (L2-resident: x is a few KB shared by
+// every workgroup), in the same instruction stream as the weights.  The
+// waves of a workgroup never wait for each other until their partial tiles
+// meet in LDS, and nothing precedes the first weight load but address math.
+//
+// B operand of k-step ks for lane l = r + 16g: token r, elements
+// [ks*4*KE + g*KE, +KE) -- exactly the A layout of the packed weight unit
+// (qw_device.hpp), so one MFMA per 16 B of weights (two for INT8).  Lanes of
+// tokens >= M issue their loads out of range (zeros, no memory traffic).
+// With the RMSNorm prologue the lane multiplies its values by (1 + gamma)
+// and accumulates their squares; the per-token sums of squares ride along
+// with the partial tiles through the reduction and any split-K hand-off, and
+// 1/rms scales the final tile (RMSNorm is linear in x once rms is known).
+//
+// Work decomposition, split-K hand-off, epilogue and fused argmax follow the
+// skinny kernel: an item is a 16-row tile (a gate/up pair for GLU weights)
+// over one K split; the NW waves of a workgroup take contiguous pieces of the
+// split; the loads of the next item are issued before the current item's
+// reduction.  The cross-wave reduction sums the NW partials with all threads
+// of the workgroup (independent LDS reads, fixed order).
+//
+// Reference operators replaced: cutlass_style_gemv_kernel / _bf16 /
+// _fused_silu (cutlass_gemm_wrapper.cuh:41-200), int8_gemv_batch_kernel
+// (mlp_cuda.cu:158-180), lm_head_gemv_kernel_optimized (lm_head_cuda.cu:38-99)
+// + block_argmax_kernel (gpu_sampler_argmax.cu:14-43), and the thread-per-row
+// decode projections of the attention operators (linear_attention_cuda.cu:
+// 33-45,174-187; full_attention_cuda.cu:31-76,78-148,161-172).
+#include "qw_stream.hpp"
+
+namespace qwk {
+
+// Activation fragment of one k-step as loaded: KE elements of XDT.
+template <int WF, int XDT> struct XFrag {
+    static constexpr int KE = WTraits<WF>::KE;
+    static constexpr int N16 = KE * 2 / 16;  // 16-byte loads per lane (XDT is 16-bit)
+    u32x4 v[N16];
+    f32x4 gam[KE / 4];
+};
+
+template <int WF, int XDT, bool GAM>
+__device__ __forceinline__ void load_xfrag(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, uint32_t xoff,
+                                           uint32_t goff, XFrag<WF, XDT>& f) {
+    constexpr int KE = WTraits<WF>::KE;
+#pragma unroll
+    for (int h = 0; h < XFrag<WF, XDT>::N16; ++h)
+        f.v[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 16 * h, 0, 0));
+    if constexpr (GAM) {
+#pragma unroll
+        for (int h = 0; h < KE / 4; ++h)
+            f.gam[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, goff + 16 * h, 0, 0));
+    }
+}
+
+// B operand of the unit from a loaded fragment (and the squares for RMSNorm).
+// NORM: accumulate the squares; GAM: multiply by (1 + gamma) (without GAM the
+// weight carries the norm weight and the activation bits pass through).
+template <int WF, int XDT, bool NORM, bool GAM>
+__device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT>& f, float& ss) {
+    constexpr int KE = WTraits<WF>::KE;
+    BOps<WF, XDT> b;
+    constexpr bool SAME = (WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16);
+    constexpr bool RAW = !GAM && SAME;
+    if constexpr (NORM && RAW) {
+#pragma unroll
+        for (int p = 0; p < KE / 2; ++p) {
+            const uint32_t w = f.v[p >> 2][p & 3];
+            const float e0 = XDT == DT_BF16 ? bf16_bits_to_f32(w & 0xffffu) : f16_bits_to_f32(w & 0xffffu);
+            const float e1 = XDT == DT_BF16 ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
+            ss += e0 * e0 + e1 * e1;
+        }
+    }
+    if constexpr (RAW) {
+        if constexpr (WF == WF_BF16) {
+            b.hi = __builtin_bit_cast(bf16x8, f.v[0]);
+        } else {
+            b.hi0 = __builtin_bit_cast(f16x8, f.v[0]);
+            b.hi1 = __builtin_bit_cast(f16x8, f.v[1]);
+        }
+    } else {
+        uint32_t out[KE / 2];
+#pragma unroll
+        for (int p = 0; p < KE / 2; ++p) {
+            const uint32_t w = f.v[p >> 2][p & 3];
+            float e0, e1;
+            if constexpr (XDT == DT_BF16) {
+                e0 = bf16_bits_to_f32(w & 0xffffu);
+                e1 = bf16_bits_to_f32(w >> 16);
+            } else {
+                e0 = f16_bits_to_f32(w & 0xffffu);
+                e1 = f16_bits_to_f32(w >> 16);
+            }
+            if constexpr (NORM) ss += e0 * e0 + e1 * e1;
+            if constexpr (GAM) {
+                e0 *= 1.0f + f.gam[(2 * p) >> 2][(2 * p) & 3];
+                e1 *= 1.0f + f.gam[(2 * p + 1) >> 2][(2 * p + 1) & 3];
+            }
+            out[p] = op_bits<WF>(e0) | (op_bits<WF>(e1) << 16);
+        }
+        if constexpr (WF == WF_BF16) {
+            b.hi = __builtin_bit_cast(bf16x8, u32x4{out[0], out[1], out[2], out[3]});
+        } else {
+            b.hi0 = __builtin_bit_cast(f16x8, u32x4{out[0], out[1], out[2], out[3]});
+            b.hi1 = __builtin_bit_cast(f16x8, u32x4{out[4], out[5], out[6], out[7]});
+        }
+    }
+    return b;
+}
+
+template <int WF, int XDT, bool GLU, bool ARGMAX, int NW, bool NORM, bool GAM>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemv_kernel(SkinnyArgs a) {
+    // k-steps per register buffer (two buffers in flight); fewer where the
+    // INT8 activation fragments and RMSNorm weights would crowd the registers
+    constexpr int U = (GAM && WF == WF_I8) ? 2 : 4;
+    constexpr int KE = WTraits<WF>::KE;
+    constexpr int RT = GLU ? 2 : 1;
+    __shared__ f32x4 red[NW][RT][64];
+    __shared__ float red_ss[NW][16];
+
+    const int lane = threadIdx.x & 63;
+    const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const bool want_res = !ARGMAX && (a.flags & EP_RESIDUAL);
+
+    int s = 0, ks0 = 0, ks1 = a.ksteps;
+    if (a.S > 1) {
+        s = blockIdx.x % a.S;
+        ks0 = (s * a.ksteps) / a.S;
+        ks1 = ((s + 1) * a.ksteps) / a.S;
+    }
+    const int grp_step = a.S > 1 ? gridDim.x / a.S : gridDim.x;
+    int kb, kend;
+    wave_range<NW>(ks0, ks1, wave_id, kb, kend);
+    const int kb0 = kb;
+
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * RT * a.ksteps * 1024u));
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(GAM ? (const void*)a.gamma : a.x, GAM ? (uint32_t)a.K * 4u : 0u);
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)a.n_groups * RT * 64u : 0u);
+    const int res_size = a.res_dt == DT_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t rr =
+        make_rsrc(want_res ? a.res : a.x, want_res ? (uint32_t)((uint64_t)a.M * a.ld_res * res_size) : 0u);
+
+    // this lane's activation row: token r (out of range past M)
+    const bool tok_ok = r < a.M;
+    const uint32_t xrow = tok_ok ? (uint32_t)(r * a.ldx + g * KE) * 2u : OOB;
+    const uint32_t grow = tok_ok ? (uint32_t)(g * KE) * 4u : OOB;
+
+    unsigned long long best = 0ull;
+    // two register buffers of U k-steps: the loads of chunk c+1 are in
+    // flight while chunk c is multiplied
+    u32x4 A0[U][RT], A1[U][RT];
+    XFrag<WF, XDT> X0[U], X1[U];
+    EpiOps<RT, 1> epi, epi_next;
+    int item = blockIdx.x;
+    int grp = a.S > 1 ? blockIdx.x / a.S : blockIdx.x;
+
+    auto issue = [&](int grp_, int kb_, int n_, u32x4 (&Ad)[U][RT], XFrag<WF, XDT> (&Xd)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t ko = (uint32_t)(kb_ + u) * 4u * KE;
+            load_xfrag<WF, XDT, GAM>(xr, gr, u < n_ ? xrow + ko * 2u : OOB, u < n_ ? grow + ko * 4u : OOB, Xd[u]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue_weights<RT, U>(a, wrs, grp_, kb_, n_, lane, Ad);
+    };
+    // slots u >= n were loaded out of range: zero operands, so every slot
+    // runs unconditionally (branch-free: each load is waited for on its own)
+    auto compute = [&](const u32x4 (&As)[U][RT], const XFrag<WF, XDT> (&Xs)[U], f32x4 (&acc)[RT], float& ss) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const BOps<WF, XDT> b = make_bops<WF, XDT, NORM, GAM>(Xs[u], ss);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) acc[rt] = unit_mfma<WF, XDT>(As[u][rt], b, acc[rt]);
+        }
+    };
+
+    // weights first: the epilogue operands (the residual may have just been
+    // written by the previous kernel: a slower, coherent fetch) are needed
+    // last, and loads retire in order
+    issue(grp, kb, item < a.n_items ? min(U, kend - kb) : 0, A0, X0);
+    load_epi<RT, 1>(a, sr, rr, grp, item < a.n_items, lane, epi);
+
+    while (item < a.n_items) {
+        f32x4 acc[RT];
+#pragma unroll
+        for (int i = 0; i < RT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float ss = 0.0f;
+        // buffer 0 holds the chunk at kb on entry
+        for (;;) {
+            if (kb + U < kend) issue(grp, kb + U, min(U, kend - kb - U), A1, X1);
+            compute(A0, X0, acc, ss);
+            kb += U;
+            if (kb >= kend) break;
+            if (kb + U < kend) issue(grp, kb + U, min(U, kend - kb - U), A0, X0);
+            compute(A1, X1, acc, ss);
+            kb += U;
+            if (kb >= kend) break;
+        }
+        const int cur_grp = grp;
+        item += gridDim.x;
+        grp += grp_step;
+        kb = kb0;
+        if (item < a.n_items) {  // next item's loads fly during this item's reduction
+            issue(grp, kb, min(U, kend - kb), A0, X0);
+            load_epi<RT, 1>(a, sr, rr, grp, true, lane, epi_next);
+        }
+
+        // ---- reduce the NW partial tiles (fixed order, all threads) ----
+        if constexpr (NORM) {
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (g == 0) red_ss[wave_id][r] = ss;
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) red[wave_id][rt][lane] = acc[rt];
+        __syncthreads();
+        {
+            float* redf = reinterpret_cast<float*>(&red[0][0][0]);
+            constexpr int PER_W = RT * 64 * 4;
+            for (int t = threadIdx.x; t < PER_W; t += NW * 64) {
+                float part[NW];
+#pragma unroll
+                for (int w = 0; w < NW; ++w) part[w] = redf[w * PER_W + t];
+                float sum = part[0];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) sum += part[w];
+                redf[t] = sum;
+            }
+            if constexpr (NORM) {
+                if (threadIdx.x < 16) {
+                    float t = red_ss[0][threadIdx.x];
+#pragma unroll
+                    for (int w = 1; w < NW; ++w) t += red_ss[w][threadIdx.x];
+                    red_ss[0][threadIdx.x] = t;
+                }
+            }
+        }
+        __syncthreads();
+        if (wave_id != 0) {
+            __syncthreads();  // wave 0 has read the sums before the next item overwrites them
+            continue;
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt] = red[0][rt][lane];
+        ss = NORM ? red_ss[0][r] : 0.0f;
+        __syncthreads();
+        EpiOps<RT, 1> e = epi;
+        epi = epi_next;
+
+        const int grp_c = cur_grp;
+        bool finish = true;
+        if constexpr (!ARGMAX) {
+            if (a.S > 1) {
+                // split-K hand-off without a fence: agent-scope stores of the
+                // partial tile and sum of squares, wait for their completion,
+                // then the agent-scope arrival count; the last arriver sums
+                // the S partials in split order and re-arms the counter
+                constexpr int REC = RT * 4 + 1;
+                float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)grp_c * a.S * 64 + lane) * REC;
+                float* mine = P + (int64_t)s * 64 * REC;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        __hip_atomic_store(mine + rt * 4 + i, acc[rt][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(mine + RT * 4, ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                unsigned old = 0;
+                if (lane == 0)
+                    old = __hip_atomic_fetch_add(&a.counters[grp_c], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                old = __shfl(old, 0);
+                finish = (old == (unsigned)(a.S - 1));
+                if (finish) {
+                    ss = 0.0f;
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int s2 = 0; s2 < a.S; ++s2) {
+                        const float* q = P + (int64_t)s2 * 64 * REC;
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                acc[rt][i] += __hip_atomic_load(q + rt * 4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        ss += __hip_atomic_load(q + RT * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                    if (lane == 0) __hip_atomic_store(&a.counters[grp_c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        if (!finish) continue;
+
+        const float inv = NORM ? 1.0f / sqrtf(ss / (float)a.K + a.eps) : 1.0f;
+        const int o = grp_c * 16 + g * 4;  // first of this lane's 4 logical rows
+        const int m = r;
+        f32x4 v;
+        if constexpr (GLU) {
+            f32x4 gt = acc[0] * inv;
+            f32x4 up = acc[1] * inv;
+            if (a.scales) {
+                gt *= as_f32x4(e.sc[0]);
+                up *= as_f32x4(e.sc[1]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = silu_f(gt[i]) * up[i];
+        } else {
+            v = acc[0] * inv;
+            if (a.scales) v *= as_f32x4(e.sc[0]);
+        }
+        if constexpr (ARGMAX) {
+            if (m < a.M) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (o + i < a.N) {
+                        const unsigned long long kk = argmax_key(v[i], (uint32_t)(o + i));
+                        best = kk > best ? kk : best;
+                    }
+                }
+            }
+        } else {
+            if (m >= a.M || o >= a.N) continue;
+            if (a.vec_store) {
+                if (want_res) v += epi_res(a.res_dt, e.res32[0], e.res16[0]);
+                void* dst = a.y;
+                int col = o;
+                if (a.flags & EP_SPLIT) {
+                    const int blk = o / a.split_period;
+                    dst = (blk & 1) ? a.y2 : a.y;
+                    col = (blk >> 1) * a.split_period + (o - blk * a.split_period);
+                }
+                store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, v);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int oi = o + i;
+                    if (oi >= a.N) break;
+                    float vi = v[i];
+                    if (want_res) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
+                    void* dst = a.y;
+                    int col = oi;
+                    if (a.flags & EP_SPLIT) {
+                        const int blk = oi / a.split_period;
+                        dst = (blk & 1) ? a.y2 : a.y;
+                        col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
+                    }
+                    store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
+                }
+            }
+        }
+    }
+
+    if constexpr (ARGMAX) {
+        if (wave_id != 0) return;
+#pragma unroll
+        for (int sh = 16; sh <= 32; sh <<= 1) {
+            const unsigned long long other = __shfl_xor(best, sh);
+            best = other > best ? other : best;
+        }
+        if (g == 0 && r < a.M && best != 0ull)
+            __hip_atomic_fetch_max(&a.keys[r], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the key updates are agent-scope read-modify-writes performed at the
+        // device coherence point; waiting for their completion orders them
+        // before this workgroup's completion count
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned old = 0;
+        if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        old = __shfl(old, 0);
+        if (old == gridDim.x - 1) {
+            for (int mm = lane; mm < a.M; mm += 64) {
+                const unsigned long long kk =
+                    __hip_atomic_exchange(&a.keys[mm], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                a.ids[mm] = (int32_t)key_index(kk);
+                if (a.maxv) a.maxv[mm] = key_value(kk);
+            }
+            if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host-side launch
+// ---------------------------------------------------------------------------
+int gemv_waves(int wf, bool glu, bool argmax, bool norm, int nw_wanted) {
+    if (glu || argmax) return 4;
+    if (nw_wanted >= 16) return (wf == WF_BF16 && !norm) ? 16 : (norm ? 4 : 8);
+    if (nw_wanted >= 8) return norm ? 4 : 8;
+    return 4;
+}
+
+bool gemv_supported(int wf, int xdt, int M) {
+    if (M < 1 || M > 16) return false;
+    return (wf == WF_BF16 && xdt == DT_BF16) || (wf == WF_I8 && (xdt == DT_F16 || xdt == DT_BF16));
+}
+
+template <int WF, int XDT, bool NORM, bool GAM>
+static hipError_t launch_n(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
+    const dim3 gd(grid), bd(nw * 64);
+    if (argmax) {
+        if (glu || NORM) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, true, 4, false, false>), gd, dim3(256), 0, st, a);
+    } else if (glu) {
+        if (nw != 4) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemv_kernel<WF, XDT, true, false, 4, NORM, GAM>), gd, dim3(256), 0, st, a);
+    } else if (nw == 16) {
+        // 16-wave workgroups fit their registers only without the RMSNorm
+        // prologue and with BF16 weights
+        if constexpr (NORM || WF != WF_BF16) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, false, 16, false, false>), gd, bd, 0, st, a);
+    } else if (nw == 8) {
+        if constexpr (NORM) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, false, 8, false, false>), gd, bd, 0, st, a);
+    } else {
+        hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, false, 4, NORM, GAM>), gd, dim3(256), 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <int WF, int XDT>
+static hipError_t launch_x(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
+    if (a.flags & EP_NORM) {
+        if (a.gamma) return launch_n<WF, XDT, true, true>(a, glu, argmax, nw, grid, st);
+        return launch_n<WF, XDT, true, false>(a, glu, argmax, nw, grid, st);
+    }
+    return launch_n<WF, XDT, false, false>(a, glu, argmax, nw, grid, st);
+}
+
+hipError_t launch_gemv(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
+                       hipStream_t stream) {
+    if (!gemv_supported(wf, xdt, a.M)) return hipErrorInvalidValue;
+    if (nw != 4 && nw != 8 && nw != 16) return hipErrorInvalidValue;
+    if (a.S < 1 || grid % a.S != 0) return hipErrorInvalidValue;
+    if (wf == WF_BF16) return launch_x<WF_BF16, DT_BF16>(a, glu, argmax, nw, grid, stream);
+    if (xdt == DT_F16) return launch_x<WF_I8, DT_F16>(a, glu, argmax, nw, grid, stream);
+    return launch_x<WF_I8, DT_BF16>(a, glu, argmax, nw, grid, stream);
+}
+
+}  // namespace qwk

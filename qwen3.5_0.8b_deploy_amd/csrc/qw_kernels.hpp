@@ -45,6 +45,14 @@ struct SkinnyArgs {
 constexpr size_t kSkinnyMaxLds = 136 * 1024;
 size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split);
 
+// Register-direct decode GEMV (qw_gemv.hip): M <= 16; BF16 weights with BF16
+// activations, INT8 weights with F16 or BF16 activations.
+bool gemv_supported(int wf, int xdt, int M);
+// workgroup size (waves) the GEMV instantiates closest to the one wanted
+int gemv_waves(int wf, bool glu, bool argmax, bool norm, int nw_wanted);
+hipError_t launch_gemv(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
+                       hipStream_t stream);
+
 // nw: waves per workgroup (4 or 16)
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream);
@@ -90,6 +98,7 @@ hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, int grid, hipStre
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
 // Output rows are written to physical tile `tile_of_row(o)` (GLU interleave
 // handled by the caller through tile_mul/tile_add: pt = t*tile_mul+tile_add).
+hipError_t launch_fold_norm(uint8_t* w, int wf, int phys_tiles, int ksteps, const float* gamma, hipStream_t stream);
 hipError_t launch_pack(const void* src, int src_dt, int wf, const float* src_scales, int N, int K,
                        uint8_t* dst, float* dst_scales, int tile_mul, int tile_add,
                        hipStream_t stream);

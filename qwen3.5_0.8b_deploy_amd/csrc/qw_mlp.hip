@@ -147,7 +147,7 @@ __global__ __launch_bounds__(MLP_NW * 64) void mlp_kernel(MlpArgs p) {
             const int n = min(UA, kend - kb);
             const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * 2 * a.ksteps * 1024u));
             const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * XSize<XDT>::v));
-            const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM ? (const void*)a.gamma : a.x, NORM ? (uint32_t)a.K * 4u : 0u);
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(NORM && a.gamma ? (const void*)a.gamma : a.x, NORM && a.gamma ? (uint32_t)a.K * 4u : 0u);
             const __amdgpu_buffer_rsrc_t sr =
                 make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)a.n_groups * 2 * 64u : 0u);
             const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.x, 0u);

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, int xdt, co
 #pragma unroll
     for (int i = 0; i < NORM_MAX_PER_THREAD; ++i) {
         const int k = threadIdx.x + i * 256;
-        if (k < K) store_act(y, ydt, yrow + k, v[i] * inv * (1.0f + gamma[k]));
+        if (k < K) store_act(y, ydt, yrow + k, v[i] * inv * (gamma ? 1.0f + gamma[k] : 1.0f));
     }
 }
 

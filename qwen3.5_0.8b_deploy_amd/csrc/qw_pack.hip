@@ -100,6 +100,43 @@ __global__ __launch_bounds__(256) void unpack_kernel(const uint8_t* src, int K, 
     }
 }
 
+// W[o][k] *= (1 + gamma[k]) in place on the packed tile order (the RMSNorm
+// weight folded into the consuming projection).  One thread per 16-byte lane
+// chunk: chunk c of k-step ks of any tile holds k = ks*4*KE + g*KE + e,
+// g = (c % 64) / 16.  BF16 results are rounded to nearest even.
+__global__ __launch_bounds__(256) void fold_norm_kernel(uint8_t* w, int wf, int ksteps, int64_t chunks,
+                                                        const float* gamma) {
+    const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (c >= chunks) return;
+    const int lane = (int)(c & 63);
+    const int ks = (int)((c >> 6) % ksteps);
+    const int g = lane >> 4;
+    u32x4* p = reinterpret_cast<u32x4*>(w) + c;
+    u32x4 v = *p;
+    if (wf == WF_BF16) {
+        const int k0 = ks * 32 + g * 8;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float lo = bf16_bits_to_f32(v[q] & 0xffffu) * (1.0f + gamma[k0 + 2 * q]);
+            const float hi = bf16_bits_to_f32(v[q] >> 16) * (1.0f + gamma[k0 + 2 * q + 1]);
+            v[q] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+        }
+    } else {
+        const int k0 = ks * 16 + g * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = __float_as_uint(__uint_as_float(v[q]) * (1.0f + gamma[k0 + q]));
+    }
+    *p = v;
+}
+
+hipError_t launch_fold_norm(uint8_t* w, int wf, int phys_tiles, int ksteps, const float* gamma, hipStream_t stream) {
+    if (wf != WF_BF16 && wf != WF_F32) return hipErrorInvalidValue;
+    const int64_t chunks = (int64_t)phys_tiles * ksteps * 64;
+    hipLaunchKernelGGL(fold_norm_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream, w, wf, ksteps,
+                       chunks, gamma);
+    return hipGetLastError();
+}
+
 hipError_t launch_pack(const void* src, int src_dt, int wf, const float* src_scales, int N, int K,
                        uint8_t* dst, float* dst_scales, int tile_mul, int tile_add,
                        hipStream_t stream) {

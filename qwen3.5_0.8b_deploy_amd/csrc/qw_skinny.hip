@@ -80,7 +80,9 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
     for (int ct = 0; ct < CT; ++ct) best[ct] = 0ull;
 
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * XSize<XDT>::v));
-    const __amdgpu_buffer_rsrc_t gr = make_rsrc(norm ? (const void*)a.gamma : a.x, norm ? (uint32_t)a.K * 4u : 0u);
+    // no gamma (the weight carries it): an empty buffer, every gamma load reads 0
+    const __amdgpu_buffer_rsrc_t gr =
+        make_rsrc(norm && a.gamma ? (const void*)a.gamma : a.x, norm && a.gamma ? (uint32_t)a.K * 4u : 0u);
     const __amdgpu_buffer_rsrc_t sr =
         make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)a.n_groups * RT * 64u : 0u);
     const int res_size = a.res_dt == DT_F32 ? 4 : 2;

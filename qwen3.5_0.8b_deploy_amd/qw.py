@@ -29,7 +29,7 @@ EXPORTS = [
     "qw_init", "qw_destroy", "qw_workspace_query", "qw_last_error", "qw_status_string",
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
     "qw_weight_pack_glu_device", "qw_weight_wrap_packed",
-    "qw_weight_free", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
+    "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
@@ -79,6 +79,7 @@ def lib():
         "qw_weight_pack_device": ([_vp, _vp, _i, _i, _i, _i, _vp, pp], _i),
         "qw_weight_pack_glu_device": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, pp], _i),
         "qw_weight_wrap_packed": ([_vp, _vp, _vp, _i, _i, _i, pp], _i),
+        "qw_weight_fold_norm": ([_vp, _vp, _vp, _vp], _i),
         "qw_weight_free": ([_vp], _i),
         "qw_weight_info": ([_vp, _vp, _vp, _vp, _vp, _vp], _i),
         "qw_weight_device_ptrs": ([_vp, _vp, _vp], _i),
@@ -233,6 +234,13 @@ class Weight:
             None if up_scales is None else up_scales.data_ptr(), ctypes.byref(h)))
         return cls(ctx, h)
 
+    def fold_norm(self, gamma, stream=None):
+        """Multiply (1 + gamma[k]) into the columns (BF16/F32 weights); use the
+        weight with gamma=None afterwards (the norm is then rms-only)."""
+        self.ctx.check(lib().qw_weight_fold_norm(self.ctx.handle, self._h, _ptr(gamma), _stream(stream)))
+        self.norm_folded = True
+        return self
+
     def unpack(self):
         """Stored values as (W rows [parts*N][K] in stored dtype, scales or None)."""
         parts = 2 if self.glu else 1
@@ -265,8 +273,9 @@ def _ptr(t):
 
 
 def linear(ctx, W, x, y, residual=None, gamma=None, eps=1e-6, y2=None, split_period=0,
-           ldx=0, ldy=0, stream=None):
-    """y = W.x (+ epilogue) on torch device tensors x [M][>=K], y [M][>=N]."""
+           ldx=0, ldy=0, stream=None, norm=False):
+    """y = W.x (+ epilogue) on torch device tensors x [M][>=K], y [M][>=N].
+    norm=True without gamma: RMSNorm of x for a weight with a folded norm."""
     ep = Epilogue()
     use_ep = False
     if residual is not None:
@@ -275,9 +284,9 @@ def linear(ctx, W, x, y, residual=None, gamma=None, eps=1e-6, y2=None, split_per
         ep.residual_dtype = _torch_code(residual)
         ep.ld_residual = residual.stride(0) if residual.dim() == 2 else 0
         use_ep = True
-    if gamma is not None:
+    if gamma is not None or norm:
         ep.flags |= EP_NORM_X
-        ep.gamma = gamma.data_ptr()
+        ep.gamma = gamma.data_ptr() if gamma is not None else None
         ep.eps = eps
         use_ep = True
     if y2 is not None:

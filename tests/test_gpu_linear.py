@@ -344,3 +344,62 @@ def test_split_k_handoff_repeatable(qw, ctx, oracle, relerr, fmt):
     xs = host(xt)
     ref = oracle.linear_int8_f64(*w.unpack(), xs) if fmt == "int8" else oracle.linear_f64(oracle.round_bf16(W), xs)
     assert relerr(got[0], ref) <= 2e-5
+
+
+# ----------------------------------------------------------------------------
+# RMSNorm weight folded into the projection (qw_weight_fold_norm)
+# ----------------------------------------------------------------------------
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt,M", [("bf16", 1), ("bf16", 8), ("bf16", 16), ("bf16", 40), ("f32", 3)])
+def test_fold_norm_linear(qw, ctx, oracle, relerr, fmt, M):
+    """W*(1+gamma) with rms-only scaling equals RMSNorm(x)*(1+gamma) then W,
+    against the FP64 oracle (GEMV, skinny and GEMM paths by M / dtype)."""
+    N, K = 3584, 1024
+    W = oracle.normal((N, K), 710, 0.0, 0.02)
+    gam = oracle.normal((K,), 711, 0.0, 0.1)
+    x = oracle.normal((M, K), 712)
+    f = qw.WFMT_BF16 if fmt == "bf16" else qw.WFMT_F32
+    xdt = torch.bfloat16 if fmt == "bf16" else torch.float32
+    w = qw.Weight.pack(ctx, W, f).fold_norm(torch.from_numpy(gam).cuda())
+    xt = torch.from_numpy(x).cuda().to(xdt)
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(ctx, w, xt, y, norm=True)
+    torch.cuda.synchronize()
+    xs = xt.float().cpu().numpy()
+    ref = oracle.linear_f64(W, oracle.rmsnorm_f64(xs, gam).astype(np.float32))
+    assert relerr(y.cpu().numpy(), ref) <= (1e-2 if fmt == "bf16" else 1e-5)
+
+
+@pytest.mark.gpu
+def test_fold_norm_mlp_and_errors(qw, ctx, oracle, relerr):
+    H, I, M = 1024, 3584, 2
+    G = oracle.normal((I, H), 720, 0.0, 0.02)
+    U = oracle.normal((I, H), 721, 0.0, 0.02)
+    D = oracle.normal((H, I), 722, 0.0, 0.02)
+    gam = oracle.normal((H,), 723, 0.0, 0.1)
+    x = oracle.normal((M, H), 724)
+    gt = torch.from_numpy(gam).cuda()
+    gu = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16).fold_norm(gt)
+    dn = qw.Weight.pack(ctx, D, qw.WFMT_BF16)
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    y = torch.empty(M, H, device="cuda")
+    qw.mlp_fused(ctx, gu, dn, xt, y, residual=xt)
+    torch.cuda.synchronize()
+    ref = oracle.mlp_block_f64(G, U, D, gam, xt.float().cpu().numpy())
+    assert relerr(y.cpu().numpy(), ref) <= 1e-2
+    # gamma given again, folding twice, INT8 weights: refused
+    with pytest.raises(qw.QwError) as e:
+        qw.mlp_fused(ctx, gu, dn, xt, y, gamma=gt, residual=xt)
+    assert e.value.status == qw.ERR_INVALID
+    with pytest.raises(qw.QwError) as e:
+        gu.fold_norm(gt)
+    assert e.value.status == qw.ERR_STATE
+    q8 = qw.Weight.pack(ctx, D, qw.WFMT_INT8)
+    with pytest.raises(qw.QwError) as e:
+        q8.fold_norm(torch.zeros(I, device="cuda"))
+    assert e.value.status == qw.ERR_DTYPE
+    # an unfolded weight still needs gamma for the norm
+    with pytest.raises(qw.QwError) as e:
+        qw.linear(ctx, dn, torch.empty(1, I, device="cuda", dtype=torch.bfloat16),
+                  torch.empty(1, H, device="cuda"), norm=True)
+    assert e.value.status == qw.ERR_NULL
