@@ -16,6 +16,8 @@
 #include "../../include/qw_linear.h"
 #include "qw_kernels.hpp"
 
+constexpr int kGemmMinM = 33;  // default token count from which the MFMA GEMM is used
+
 struct qw_ctx {
     int device = 0;
     int num_cus = 256;
@@ -24,7 +26,9 @@ struct qw_ctx {
     int force_nw = 0;        // waves per skinny workgroup (0: automatic)
     int force_nw_glu = 0;    // same, GLU weights only
     bool mlp_fused = false;  // one-launch MLP block (QW_MLP_FUSED=1)
-    bool gemv = true;        // register-direct GEMV for M <= 16 (QW_GEMV=0: skinny kernel)
+    bool gemv = true;        // register-direct GEMV for M <= 32 (QW_GEMV=0: skinny kernel)
+    int gemm_min_m = kGemmMinM;  // tokens from which BF16 calls may use the MFMA GEMM
+    bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -102,7 +106,6 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 size_t scratch_need(int M, int I) { return (size_t)M * I * 4; }
 size_t xnorm_need(int M, int K) { return (size_t)M * K * 2; }
-constexpr int kGemmMinM = 33;   // token count from which the MFMA GEMM is used
 
 }  // namespace
 
@@ -160,6 +163,10 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
+    if (const char* v = getenv("QW_GEMM_MIN_M")) {
+        c->gemm_min_m = std::max(1, atoi(v));
+        c->gemm_forced = true;
+    }
     if (workspace_bytes == 0) workspace_bytes = qw_workspace_query(4096, 8224, 4096);
     workspace_bytes = std::max(workspace_bytes, kFixedBytes + (size_t)(3u << 20));
     workspace_bytes = (workspace_bytes + 4095) & ~(size_t)4095;
@@ -497,10 +504,10 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     // one exception is a single BF16 token with a per-call gamma, where the
     // gamma traffic of every lane outweighs the saved staging pass.
     const bool gamma_call = ep && (ep->flags & QW_EP_NORM_X) && ep->gamma;
-    const bool direct = ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, M) &&
+    const bool direct = ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, M, ep && (ep->flags & QW_EP_NORM_X)) &&
                         !(M == 1 && gamma_call && W->wf == QW_WFMT_BF16);
     if (direct)
-        nw = qwk::gemv_waves(W->wf, W->glu != 0, argmax, ep && (ep->flags & QW_EP_NORM_X), nw);
+        nw = qwk::gemv_waves(W->wf, M, W->glu != 0, argmax, ep && (ep->flags & QW_EP_NORM_X), nw);
     // the activation slice of a split must fit the workgroup's LDS
     while (!direct && qwk::skinny_lds_bytes(W->wf, (int)xdt, M, (W->ksteps + S - 1) / S) > qwk::kSkinnyMaxLds) {
         if (argmax || S >= W->ksteps) return fail(ctx, QW_ERR_SHAPE, "K=%d too large for the skinny kernel", W->K);
@@ -554,6 +561,18 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
 // MFMA GEMM launch for many tokens (BF16 weights and activations).
 static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
     return W->wf == QW_WFMT_BF16 && xdt == QW_BF16 && W->ksteps % 2 == 0;
+}
+
+// GEMM or 32-token chunks of the small-M kernels.  The 256 x 256 GEMM tile
+// needs enough weight-row blocks to fill the chip: with few (the 1024-row
+// projections) the chunked weight-streaming kernels win up to a few hundred
+// tokens (measured on MI355X: M=128 down projection 45 us chunked vs 111 us
+// GEMM; gate/up with 28 row blocks: GEMM from M=128).
+static bool use_gemm(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M) {
+    if (!gemm_ok(W, xdt) || M < ctx->gemm_min_m) return false;
+    if (ctx->gemm_forced) return true;
+    const int nblk_n = (W->phys_tiles * 16 + 255) / 256;
+    return (nblk_n >= 16 && M >= 128) || M >= 384;
 }
 
 static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ldx, int M, void* y, qw_dtype ydt,
@@ -652,7 +671,7 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     if (W && ldy == 0) ldy = (ep && (ep->flags & QW_EP_SPLIT)) ? W->N / 2 : W->N;
     qw_status s = check_linear(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, true);
     if (s != QW_OK) return s;
-    if (M >= kGemmMinM && gemm_ok(W, xdt)) {
+    if (use_gemm(ctx, W, xdt, M)) {
         const bool norm = ep && (ep->flags & QW_EP_NORM_X);
         if (!norm) return run_gemm(ctx, W, x, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);
         // RMSNorm into the workspace, then the GEMM, in token chunks that fit
@@ -676,11 +695,14 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
         }
         return QW_OK;
     }
-    // token chunks of at most 32 for the skinny kernel
+    // token chunks of at most 32 for the small-M kernels (16 with the
+    // RMSNorm prologue, which the register-direct GEMV takes 16 at a time)
     qw_epilogue e2;
     if (ep) e2 = *ep;
-    for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {
-        const int mc = std::min(kSkinnyMaxM, M - m0);
+    const bool norm = ep && (ep->flags & QW_EP_NORM_X);
+    const int cmax = (norm && ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, 16, true)) ? 16 : kSkinnyMaxM;
+    for (int m0 = 0; m0 < M; m0 += cmax) {
+        const int mc = std::min(cmax, M - m0);
         const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * ldx * dsize(xdt);
         void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * ldy * dsize(ydt);
         if (ep) {
@@ -704,7 +726,7 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     if (!token_ids) return fail(ctx, QW_ERR_NULL, "token_ids is NULL");
     if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
     if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
-    if (M >= kGemmMinM && gemm_ok(E, hdt)) return run_gemm(ctx, E, h, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
+    if (use_gemm(ctx, E, hdt, M)) return run_gemm(ctx, E, h, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
     for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {
         const int mc = std::min(kSkinnyMaxM, M - m0);
         const void* hc = static_cast<const uint8_t*>(h) + (size_t)m0 * E->K * dsize(hdt);

@@ -1,5 +1,5 @@
 // qw_gemv.hip -- decode GEMV for gfx950 with register-direct activations
-// (M <= 16 tokens; BF16 weights with BF16 activations, INT8 weights with F16
+// (M <= 32 tokens; BF16 weights with BF16 activations, INT8 weights with F16
 // or BF16 activations).
 //
 // Why a second small-M kernel.  The skinny kernel (qw_skinny.hip) stages the
@@ -38,21 +38,25 @@
 
 namespace qwk {
 
-// Activation fragment of one k-step as loaded: KE elements of XDT.
-template <int WF, int XDT> struct XFrag {
+// Activation fragments of one k-step as loaded: KE elements of XDT for each
+// of the CT token tiles of the lane, and the matching (1 + gamma) weights
+// (shared by the tiles).
+template <int WF, int XDT, int CT> struct XFrag {
     static constexpr int KE = WTraits<WF>::KE;
-    static constexpr int N16 = KE * 2 / 16;  // 16-byte loads per lane (XDT is 16-bit)
-    u32x4 v[N16];
+    static constexpr int N16 = KE * 2 / 16;  // 16-byte loads per lane and tile (XDT is 16-bit)
+    u32x4 v[CT][N16];
     f32x4 gam[KE / 4];
 };
 
-template <int WF, int XDT, bool GAM>
-__device__ __forceinline__ void load_xfrag(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, uint32_t xoff,
-                                           uint32_t goff, XFrag<WF, XDT>& f) {
+template <int WF, int XDT, int CT, bool GAM>
+__device__ __forceinline__ void load_xfrag(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, const uint32_t (&xoff)[CT],
+                                           uint32_t goff, XFrag<WF, XDT, CT>& f) {
     constexpr int KE = WTraits<WF>::KE;
 #pragma unroll
-    for (int h = 0; h < XFrag<WF, XDT>::N16; ++h)
-        f.v[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff + 16 * h, 0, 0));
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int h = 0; h < XFrag<WF, XDT, CT>::N16; ++h)
+            f.v[ct][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[ct] + 16 * h, 0, 0));
     if constexpr (GAM) {
 #pragma unroll
         for (int h = 0; h < KE / 4; ++h)
@@ -60,11 +64,11 @@ __device__ __forceinline__ void load_xfrag(__amdgpu_buffer_rsrc_t xr, __amdgpu_b
     }
 }
 
-// B operand of the unit from a loaded fragment (and the squares for RMSNorm).
-// NORM: accumulate the squares; GAM: multiply by (1 + gamma) (without GAM the
-// weight carries the norm weight and the activation bits pass through).
-template <int WF, int XDT, bool NORM, bool GAM>
-__device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT>& f, float& ss) {
+// B operand of one token tile from a loaded fragment.  NORM: accumulate the
+// squares; GAM: multiply by (1 + gamma) (without GAM the weight carries the
+// norm weight and the activation bits pass through).
+template <int WF, int XDT, int CT, bool NORM, bool GAM>
+__device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT, CT>& f, int ct, float& ss) {
     constexpr int KE = WTraits<WF>::KE;
     BOps<WF, XDT> b;
     constexpr bool SAME = (WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16);
@@ -72,7 +76,7 @@ __device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT>& f, floa
     if constexpr (NORM && RAW) {
 #pragma unroll
         for (int p = 0; p < KE / 2; ++p) {
-            const uint32_t w = f.v[p >> 2][p & 3];
+            const uint32_t w = f.v[ct][p >> 2][p & 3];
             const float e0 = XDT == DT_BF16 ? bf16_bits_to_f32(w & 0xffffu) : f16_bits_to_f32(w & 0xffffu);
             const float e1 = XDT == DT_BF16 ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
             ss += e0 * e0 + e1 * e1;
@@ -80,16 +84,16 @@ __device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT>& f, floa
     }
     if constexpr (RAW) {
         if constexpr (WF == WF_BF16) {
-            b.hi = __builtin_bit_cast(bf16x8, f.v[0]);
+            b.hi = __builtin_bit_cast(bf16x8, f.v[ct][0]);
         } else {
-            b.hi0 = __builtin_bit_cast(f16x8, f.v[0]);
-            b.hi1 = __builtin_bit_cast(f16x8, f.v[1]);
+            b.hi0 = __builtin_bit_cast(f16x8, f.v[ct][0]);
+            b.hi1 = __builtin_bit_cast(f16x8, f.v[ct][1]);
         }
     } else {
         uint32_t out[KE / 2];
 #pragma unroll
         for (int p = 0; p < KE / 2; ++p) {
-            const uint32_t w = f.v[p >> 2][p & 3];
+            const uint32_t w = f.v[ct][p >> 2][p & 3];
             float e0, e1;
             if constexpr (XDT == DT_BF16) {
                 e0 = bf16_bits_to_f32(w & 0xffffu);
@@ -115,15 +119,16 @@ __device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT>& f, floa
     return b;
 }
 
-template <int WF, int XDT, bool GLU, bool ARGMAX, int NW, bool NORM, bool GAM>
+template <int WF, int XDT, int CT, bool GLU, bool ARGMAX, int NW, bool NORM, bool GAM>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemv_kernel(SkinnyArgs a) {
     // k-steps per register buffer (two buffers in flight); fewer where the
-    // INT8 activation fragments and RMSNorm weights would crowd the registers
-    constexpr int U = (GAM && WF == WF_I8) ? 2 : 4;
+    // activation fragments and RMSNorm weights would crowd the registers
+    constexpr int U = ((GAM && WF == WF_I8) || (CT == 2 && (GAM || WF == WF_I8))) ? 2 : 4;
     constexpr int KE = WTraits<WF>::KE;
     constexpr int RT = GLU ? 2 : 1;
-    __shared__ f32x4 red[NW][RT][64];
-    __shared__ float red_ss[NW][16];
+    constexpr int F = RT * CT;
+    __shared__ f32x4 red[NW][F][64];
+    __shared__ float red_ss[NW][16 * CT];
 
     const int lane = threadIdx.x & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -151,51 +156,65 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const __amdgpu_buffer_rsrc_t rr =
         make_rsrc(want_res ? a.res : a.x, want_res ? (uint32_t)((uint64_t)a.M * a.ld_res * res_size) : 0u);
 
-    // this lane's activation row: token r (out of range past M)
-    const bool tok_ok = r < a.M;
-    const uint32_t xrow = tok_ok ? (uint32_t)(r * a.ldx + g * KE) * 2u : OOB;
-    const uint32_t grow = tok_ok ? (uint32_t)(g * KE) * 4u : OOB;
+    // this lane's activation rows: token ct*16 + r of each tile (out of range past M)
+    uint32_t xrow[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+        xrow[ct] = ct * 16 + r < a.M ? (uint32_t)((ct * 16 + r) * a.ldx + g * KE) * 2u : OOB;
+    const uint32_t grow = r < a.M ? (uint32_t)(g * KE) * 4u : OOB;
 
-    unsigned long long best = 0ull;
+    unsigned long long best[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) best[ct] = 0ull;
     // two register buffers of U k-steps: the loads of chunk c+1 are in
     // flight while chunk c is multiplied
     u32x4 A0[U][RT], A1[U][RT];
-    XFrag<WF, XDT> X0[U], X1[U];
-    EpiOps<RT, 1> epi, epi_next;
+    XFrag<WF, XDT, CT> X0[U], X1[U];
+    EpiOps<RT, CT> epi, epi_next;
     int item = blockIdx.x;
     int grp = a.S > 1 ? blockIdx.x / a.S : blockIdx.x;
 
-    auto issue = [&](int grp_, int kb_, int n_, u32x4 (&Ad)[U][RT], XFrag<WF, XDT> (&Xd)[U]) {
+    auto issue = [&](int grp_, int kb_, int n_, u32x4 (&Ad)[U][RT], XFrag<WF, XDT, CT> (&Xd)[U]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t ko = (uint32_t)(kb_ + u) * 4u * KE;
-            load_xfrag<WF, XDT, GAM>(xr, gr, u < n_ ? xrow + ko * 2u : OOB, u < n_ ? grow + ko * 4u : OOB, Xd[u]);
+            uint32_t xo[CT];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) xo[ct] = u < n_ ? xrow[ct] + ko * 2u : OOB;
+            load_xfrag<WF, XDT, CT, GAM>(xr, gr, xo, u < n_ ? grow + ko * 4u : OOB, Xd[u]);
         }
         __builtin_amdgcn_sched_barrier(0);
         issue_weights<RT, U>(a, wrs, grp_, kb_, n_, lane, Ad);
     };
     // slots u >= n were loaded out of range: zero operands, so every slot
     // runs unconditionally (branch-free: each load is waited for on its own)
-    auto compute = [&](const u32x4 (&As)[U][RT], const XFrag<WF, XDT> (&Xs)[U], f32x4 (&acc)[RT], float& ss) {
+    auto compute = [&](const u32x4 (&As)[U][RT], const XFrag<WF, XDT, CT> (&Xs)[U], f32x4 (&acc)[RT][CT],
+                       float (&ss)[CT]) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const BOps<WF, XDT> b = make_bops<WF, XDT, NORM, GAM>(Xs[u], ss);
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) acc[rt] = unit_mfma<WF, XDT>(As[u][rt], b, acc[rt]);
-        }
+            for (int ct = 0; ct < CT; ++ct) {
+                const BOps<WF, XDT> b = make_bops<WF, XDT, CT, NORM, GAM>(Xs[u], ct, ss[ct]);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = unit_mfma<WF, XDT>(As[u][rt], b, acc[rt][ct]);
+            }
     };
 
     // weights first: the epilogue operands (the residual may have just been
     // written by the previous kernel: a slower, coherent fetch) are needed
     // last, and loads retire in order
     issue(grp, kb, item < a.n_items ? min(U, kend - kb) : 0, A0, X0);
-    load_epi<RT, 1>(a, sr, rr, grp, item < a.n_items, lane, epi);
+    load_epi<RT, CT>(a, sr, rr, grp, item < a.n_items, lane, epi);
 
     while (item < a.n_items) {
-        f32x4 acc[RT];
+        f32x4 acc[RT][CT];
+        float ss[CT];
 #pragma unroll
-        for (int i = 0; i < RT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        float ss = 0.0f;
+        for (int ct = 0; ct < CT; ++ct) {
+            ss[ct] = 0.0f;
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
         // buffer 0 holds the chunk at kb on entry
         for (;;) {
             if (kb + U < kend) issue(grp, kb + U, min(U, kend - kb - U), A1, X1);
@@ -213,21 +232,26 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         kb = kb0;
         if (item < a.n_items) {  // next item's loads fly during this item's reduction
             issue(grp, kb, min(U, kend - kb), A0, X0);
-            load_epi<RT, 1>(a, sr, rr, grp, true, lane, epi_next);
+            load_epi<RT, CT>(a, sr, rr, grp, true, lane, epi_next);
         }
 
         // ---- reduce the NW partial tiles (fixed order, all threads) ----
         if constexpr (NORM) {
-            ss += __shfl_xor(ss, 16);
-            ss += __shfl_xor(ss, 32);
-            if (g == 0) red_ss[wave_id][r] = ss;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                ss[ct] += __shfl_xor(ss[ct], 16);
+                ss[ct] += __shfl_xor(ss[ct], 32);
+                if (g == 0) red_ss[wave_id][ct * 16 + r] = ss[ct];
+            }
         }
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) red[wave_id][rt][lane] = acc[rt];
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) red[wave_id][rt * CT + ct][lane] = acc[rt][ct];
         __syncthreads();
         {
             float* redf = reinterpret_cast<float*>(&red[0][0][0]);
-            constexpr int PER_W = RT * 64 * 4;
+            constexpr int PER_W = F * 64 * 4;
             for (int t = threadIdx.x; t < PER_W; t += NW * 64) {
                 float part[NW];
 #pragma unroll
@@ -238,7 +262,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                 redf[t] = sum;
             }
             if constexpr (NORM) {
-                if (threadIdx.x < 16) {
+                if (threadIdx.x < 16 * CT) {
                     float t = red_ss[0][threadIdx.x];
 #pragma unroll
                     for (int w = 1; w < NW; ++w) t += red_ss[w][threadIdx.x];
@@ -252,10 +276,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
             continue;
         }
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt] = red[0][rt][lane];
-        ss = NORM ? red_ss[0][r] : 0.0f;
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = red[0][rt * CT + ct][lane];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) ss[ct] = NORM ? red_ss[0][ct * 16 + r] : 0.0f;
         __syncthreads();
-        EpiOps<RT, 1> e = epi;
+        EpiOps<RT, CT> e = epi;
         epi = epi_next;
 
         const int grp_c = cur_grp;
@@ -263,18 +290,21 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         if constexpr (!ARGMAX) {
             if (a.S > 1) {
                 // split-K hand-off without a fence: agent-scope stores of the
-                // partial tile and sum of squares, wait for their completion,
+                // partial tile and sums of squares, wait for their completion,
                 // then the agent-scope arrival count; the last arriver sums
                 // the S partials in split order and re-arms the counter
-                constexpr int REC = RT * 4 + 1;
+                constexpr int REC = F * 4 + CT;
                 float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)grp_c * a.S * 64 + lane) * REC;
                 float* mine = P + (int64_t)s * 64 * REC;
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
+                for (int f = 0; f < F; ++f)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        __hip_atomic_store(mine + rt * 4 + i, acc[rt][i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(mine + RT * 4, ss, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(mine + f * 4 + i, acc[f / CT][f % CT][i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct)
+                    __hip_atomic_store(mine + F * 4 + ct, ss[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 unsigned old = 0;
                 if (lane == 0)
@@ -282,17 +312,23 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                 old = __shfl(old, 0);
                 finish = (old == (unsigned)(a.S - 1));
                 if (finish) {
-                    ss = 0.0f;
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int ct = 0; ct < CT; ++ct) {
+                        ss[ct] = 0.0f;
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
                     for (int s2 = 0; s2 < a.S; ++s2) {
                         const float* q = P + (int64_t)s2 * 64 * REC;
 #pragma unroll
-                        for (int rt = 0; rt < RT; ++rt)
+                        for (int f = 0; f < F; ++f)
 #pragma unroll
                             for (int i = 0; i < 4; ++i)
-                                acc[rt][i] += __hip_atomic_load(q + rt * 4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        ss += __hip_atomic_load(q + RT * 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                acc[f / CT][f % CT][i] +=
+                                    __hip_atomic_load(q + f * 4 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                        for (int ct = 0; ct < CT; ++ct)
+                            ss[ct] += __hip_atomic_load(q + F * 4 + ct, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                     if (lane == 0) __hip_atomic_store(&a.counters[grp_c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
@@ -300,60 +336,63 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         }
         if (!finish) continue;
 
-        const float inv = NORM ? 1.0f / sqrtf(ss / (float)a.K + a.eps) : 1.0f;
         const int o = grp_c * 16 + g * 4;  // first of this lane's 4 logical rows
-        const int m = r;
-        f32x4 v;
-        if constexpr (GLU) {
-            f32x4 gt = acc[0] * inv;
-            f32x4 up = acc[1] * inv;
-            if (a.scales) {
-                gt *= as_f32x4(e.sc[0]);
-                up *= as_f32x4(e.sc[1]);
-            }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = silu_f(gt[i]) * up[i];
-        } else {
-            v = acc[0] * inv;
-            if (a.scales) v *= as_f32x4(e.sc[0]);
-        }
-        if constexpr (ARGMAX) {
-            if (m < a.M) {
+        for (int ct = 0; ct < CT; ++ct) {
+            const float inv = NORM ? 1.0f / sqrtf(ss[ct] / (float)a.K + a.eps) : 1.0f;
+            const int m = ct * 16 + r;
+            f32x4 v;
+            if constexpr (GLU) {
+                f32x4 gt = acc[0][ct] * inv;
+                f32x4 up = acc[1][ct] * inv;
+                if (a.scales) {
+                    gt *= as_f32x4(e.sc[0]);
+                    up *= as_f32x4(e.sc[1]);
+                }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (o + i < a.N) {
-                        const unsigned long long kk = argmax_key(v[i], (uint32_t)(o + i));
-                        best = kk > best ? kk : best;
-                    }
-                }
-            }
-        } else {
-            if (m >= a.M || o >= a.N) continue;
-            if (a.vec_store) {
-                if (want_res) v += epi_res(a.res_dt, e.res32[0], e.res16[0]);
-                void* dst = a.y;
-                int col = o;
-                if (a.flags & EP_SPLIT) {
-                    const int blk = o / a.split_period;
-                    dst = (blk & 1) ? a.y2 : a.y;
-                    col = (blk >> 1) * a.split_period + (o - blk * a.split_period);
-                }
-                store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, v);
+                for (int i = 0; i < 4; ++i) v[i] = silu_f(gt[i]) * up[i];
             } else {
+                v = acc[0][ct] * inv;
+                if (a.scales) v *= as_f32x4(e.sc[0]);
+            }
+            if constexpr (ARGMAX) {
+                if (m < a.M) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int oi = o + i;
-                    if (oi >= a.N) break;
-                    float vi = v[i];
-                    if (want_res) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
-                    void* dst = a.y;
-                    int col = oi;
-                    if (a.flags & EP_SPLIT) {
-                        const int blk = oi / a.split_period;
-                        dst = (blk & 1) ? a.y2 : a.y;
-                        col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
+                    for (int i = 0; i < 4; ++i) {
+                        if (o + i < a.N) {
+                            const unsigned long long kk = argmax_key(v[i], (uint32_t)(o + i));
+                            best[ct] = kk > best[ct] ? kk : best[ct];
+                        }
                     }
-                    store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
+                }
+            } else {
+                if (m >= a.M || o >= a.N) continue;
+                if (a.vec_store) {
+                    if (want_res) v += epi_res(a.res_dt, e.res32[ct], e.res16[ct]);
+                    void* dst = a.y;
+                    int col = o;
+                    if (a.flags & EP_SPLIT) {
+                        const int blk = o / a.split_period;
+                        dst = (blk & 1) ? a.y2 : a.y;
+                        col = (blk >> 1) * a.split_period + (o - blk * a.split_period);
+                    }
+                    store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, v);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int oi = o + i;
+                        if (oi >= a.N) break;
+                        float vi = v[i];
+                        if (want_res) vi += load_act(a.res, a.res_dt, (int64_t)m * a.ld_res + oi);
+                        void* dst = a.y;
+                        int col = oi;
+                        if (a.flags & EP_SPLIT) {
+                            const int blk = oi / a.split_period;
+                            dst = (blk & 1) ? a.y2 : a.y;
+                            col = (blk >> 1) * a.split_period + (oi - blk * a.split_period);
+                        }
+                        store_act(dst, a.ydt, (int64_t)m * a.ldy + col, vi);
+                    }
                 }
             }
         }
@@ -362,12 +401,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     if constexpr (ARGMAX) {
         if (wave_id != 0) return;
 #pragma unroll
-        for (int sh = 16; sh <= 32; sh <<= 1) {
-            const unsigned long long other = __shfl_xor(best, sh);
-            best = other > best ? other : best;
+        for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+            for (int sh = 16; sh <= 32; sh <<= 1) {
+                const unsigned long long other = __shfl_xor(best[ct], sh);
+                best[ct] = other > best[ct] ? other : best[ct];
+            }
+            const int m = ct * 16 + r;
+            if (g == 0 && m < a.M && best[ct] != 0ull)
+                __hip_atomic_fetch_max(&a.keys[m], best[ct], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (g == 0 && r < a.M && best != 0ull)
-            __hip_atomic_fetch_max(&a.keys[r], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // the key updates are agent-scope read-modify-writes performed at the
         // device coherence point; waiting for their completion orders them
         // before this workgroup's completion count
@@ -390,53 +433,63 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 // ---------------------------------------------------------------------------
 // host-side launch
 // ---------------------------------------------------------------------------
-int gemv_waves(int wf, bool glu, bool argmax, bool norm, int nw_wanted) {
-    if (glu || argmax) return 4;
+int gemv_waves(int wf, int M, bool glu, bool argmax, bool norm, int nw_wanted) {
+    if (glu || argmax || M > 16) return 4;
     if (nw_wanted >= 16) return (wf == WF_BF16 && !norm) ? 16 : (norm ? 4 : 8);
     if (nw_wanted >= 8) return norm ? 4 : 8;
     return 4;
 }
 
-bool gemv_supported(int wf, int xdt, int M) {
-    if (M < 1 || M > 16) return false;
+bool gemv_supported(int wf, int xdt, int M, bool norm) {
+    if (M < 1 || M > 32 || (M > 16 && norm)) return false;
     return (wf == WF_BF16 && xdt == DT_BF16) || (wf == WF_I8 && (xdt == DT_F16 || xdt == DT_BF16));
 }
 
-template <int WF, int XDT, bool NORM, bool GAM>
+template <int WF, int XDT, int CT, bool NORM, bool GAM>
 static hipError_t launch_n(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
     const dim3 gd(grid), bd(nw * 64);
     if (argmax) {
         if (glu || NORM) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, true, 4, false, false>), gd, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((gemv_kernel<WF, XDT, CT, false, true, 4, false, false>), gd, dim3(256), 0, st, a);
     } else if (glu) {
         if (nw != 4) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((gemv_kernel<WF, XDT, true, false, 4, NORM, GAM>), gd, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((gemv_kernel<WF, XDT, CT, true, false, 4, NORM, GAM>), gd, dim3(256), 0, st, a);
     } else if (nw == 16) {
         // 16-wave workgroups fit their registers only without the RMSNorm
         // prologue and with BF16 weights
-        if constexpr (NORM || WF != WF_BF16) return hipErrorInvalidValue;
-        else hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, false, 16, false, false>), gd, bd, 0, st, a);
+        if constexpr (NORM || WF != WF_BF16 || CT != 1) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((gemv_kernel<WF, XDT, CT, false, false, 16, false, false>), gd, bd, 0, st, a);
     } else if (nw == 8) {
-        if constexpr (NORM) return hipErrorInvalidValue;
-        else hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, false, 8, false, false>), gd, bd, 0, st, a);
+        if constexpr (NORM || CT != 1) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((gemv_kernel<WF, XDT, CT, false, false, 8, false, false>), gd, bd, 0, st, a);
     } else {
-        hipLaunchKernelGGL((gemv_kernel<WF, XDT, false, false, 4, NORM, GAM>), gd, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((gemv_kernel<WF, XDT, CT, false, false, 4, NORM, GAM>), gd, dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
 
+template <int WF, int XDT, int CT>
+static hipError_t launch_c(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
+    if constexpr (CT == 2) {  // two token tiles leave no registers for the RMSNorm operands
+        if (a.flags & EP_NORM) return hipErrorInvalidValue;
+        return launch_n<WF, XDT, CT, false, false>(a, glu, argmax, nw, grid, st);
+    }
+    if (a.flags & EP_NORM) {
+        if (a.gamma) return launch_n<WF, XDT, CT, true, true>(a, glu, argmax, nw, grid, st);
+        return launch_n<WF, XDT, CT, true, false>(a, glu, argmax, nw, grid, st);
+    }
+    return launch_n<WF, XDT, CT, false, false>(a, glu, argmax, nw, grid, st);
+}
+
 template <int WF, int XDT>
 static hipError_t launch_x(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
-    if (a.flags & EP_NORM) {
-        if (a.gamma) return launch_n<WF, XDT, true, true>(a, glu, argmax, nw, grid, st);
-        return launch_n<WF, XDT, true, false>(a, glu, argmax, nw, grid, st);
-    }
-    return launch_n<WF, XDT, false, false>(a, glu, argmax, nw, grid, st);
+    if (a.M <= 16) return launch_c<WF, XDT, 1>(a, glu, argmax, nw, grid, st);
+    return launch_c<WF, XDT, 2>(a, glu, argmax, nw, grid, st);
 }
 
 hipError_t launch_gemv(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                        hipStream_t stream) {
-    if (!gemv_supported(wf, xdt, a.M)) return hipErrorInvalidValue;
+    if (!gemv_supported(wf, xdt, a.M, (a.flags & EP_NORM) != 0)) return hipErrorInvalidValue;
     if (nw != 4 && nw != 8 && nw != 16) return hipErrorInvalidValue;
     if (a.S < 1 || grid % a.S != 0) return hipErrorInvalidValue;
     if (wf == WF_BF16) return launch_x<WF_BF16, DT_BF16>(a, glu, argmax, nw, grid, stream);

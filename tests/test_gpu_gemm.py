@@ -13,6 +13,21 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
+@pytest.fixture(scope="module")
+def ctx(qw):
+    """A context that takes the GEMM for every BF16 call from 33 tokens on
+    (the default routing sends small-N shapes to the chunked small-M kernels)."""
+    import os
+    os.environ["QW_GEMM_MIN_M"] = "33"
+    try:
+        c = qw.Context(0)
+    finally:
+        del os.environ["QW_GEMM_MIN_M"]
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
 def dev(a, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
 
