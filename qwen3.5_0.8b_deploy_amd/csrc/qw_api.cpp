@@ -29,6 +29,7 @@ struct qw_ctx {
     bool gemv = true;        // register-direct GEMV for M <= 32 (QW_GEMV=0: skinny kernel)
     int gemm_min_m = kGemmMinM;  // tokens from which BF16 calls may use the MFMA GEMM
     bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
+    int gemm_tile_m = 128;       // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -163,6 +164,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
+    if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;
@@ -500,12 +502,16 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
         const int want = (ctx->min_items + a.n_groups - 1) / a.n_groups;
         S = std::max(1, std::min(want, W->ksteps / nw));
     }
-    // Register-direct GEMV wherever it measured faster than LDS staging; the
-    // one exception is a single BF16 token with a per-call gamma, where the
-    // gamma traffic of every lane outweighs the saved staging pass.
+    // Register-direct GEMV where it measured faster than LDS staging: it saves
+    // the staging pass but reloads the activations for every tile, so it wins
+    // while a workgroup sees few tiles (or the tokens are few); the lm_head
+    // (thousands of tiles per launch) keeps the staged kernel from M = 5 on.
+    // A single BF16 token with a per-call gamma also stays staged (the gamma
+    // traffic of every lane outweighs the saved pass).
     const bool gamma_call = ep && (ep->flags & QW_EP_NORM_X) && ep->gamma;
+    const int tiles_per_wg = a.n_groups / std::max(1, ctx->num_cus * ctx->wg_per_cu);
     const bool direct = ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, M, ep && (ep->flags & QW_EP_NORM_X)) &&
-                        !(M == 1 && gamma_call && W->wf == QW_WFMT_BF16);
+                        !(M == 1 && gamma_call && W->wf == QW_WFMT_BF16) && (M <= 4 || tiles_per_wg <= 4);
     if (direct)
         nw = qwk::gemv_waves(W->wf, M, W->glu != 0, argmax, ep && (ep->flags & QW_EP_NORM_X), nw);
     // the activation slice of a split must fit the workgroup's LDS
@@ -560,7 +566,7 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
 
 // MFMA GEMM launch for many tokens (BF16 weights and activations).
 static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
-    return W->wf == QW_WFMT_BF16 && xdt == QW_BF16 && W->ksteps % 2 == 0;
+    return W->wf == QW_WFMT_BF16 && xdt == QW_BF16;
 }
 
 // GEMM or 32-token chunks of the small-M kernels.  The 256 x 256 GEMM tile
@@ -588,7 +594,8 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ld
     a.K = W->K;
     a.N = W->N;
     a.nblk_n = (W->phys_tiles * 16 + 255) / 256;
-    a.nblk_m = (M + 255) / 256;
+    a.tile_m = ctx->gemm_tile_m;
+    a.nblk_m = (M + a.tile_m - 1) / a.tile_m;
     a.flags = ep ? (ep->flags & ~(unsigned)QW_EP_NORM_X) : 0u;
     if (ep && (ep->flags & QW_EP_RESIDUAL)) {
         a.res = ep->residual;

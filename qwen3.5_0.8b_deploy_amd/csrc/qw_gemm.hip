@@ -1,10 +1,12 @@
 // qw_gemm.hip -- LDS double-buffered MFMA GEMM for gfx950 (prefill and
 // large-batch decode):  y[m][n] = sum_k W[n][k] * x[m][k]  (+ epilogue).
 //
-// Tiling.  A workgroup (4 waves) computes 256 weight rows x 256 tokens; each
-// wave a 128 x 128 quadrant as 4 x 4 blocks of v_mfma_f32_32x32x16_bf16
-// (weights are the A operand, tokens the B operand; FP32 accumulators).  K
-// advances in blocks of 64.
+// Tiling.  A workgroup (4 waves) computes 256 weight rows x BM tokens (BM =
+// 128 by default, 256 optional); each wave a 128 x BM/2 quadrant as 4 x BM/64
+// blocks of v_mfma_f32_32x32x16_bf16 (weights are the A operand, tokens the B
+// operand; FP32 accumulators).  K advances in blocks of one 32-deep k-step.
+// With BM = 128 two workgroups share a CU, so one wave's barrier and LDS
+// waits are covered by the other's MFMAs.
 //
 // Loads.  Both operands reach LDS through direct buffer->LDS loads
 // (buffer_load_dwordx4 ... lds): one wave instruction moves one 1 KB unit.
@@ -12,8 +14,11 @@
 // and the activations are fetched so that they land in the same order: lane
 // (r, g) of a unit carries x[token r][8 k starting at group g].  A 32 x 32 x 16
 // fragment of either operand is then one conflict-free ds_read_b128 per lane.
-// Two LDS stages (2 x 64 KB) let the loads of K-block i+1 fly while K-block i
-// is multiplied.
+// Three (BM = 128: 3 x 24 KB) or four (BM = 256: 4 x 32 KB) LDS stages keep
+// the next K-blocks' loads in flight while one is multiplied; a wave waits
+// only for its own loads of the block it is about to use, then one barrier
+// per block publishes them.  The loads of a block are issued one per MFMA
+// pair so the matrix pipe never waits on a burst of load issues.
 //
 // Epilogue.  In a 32-row weight block, rows i and i+16 of a token land in the
 // same lane (accumulator items q and q+8), so a GLU weight -- gate and up
@@ -34,13 +39,43 @@ namespace qwk {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int GB_N = 256, GB_M = 256;      // block tile: weight rows x tokens
-constexpr int G_STAGE = 64 * 1024;         // bytes per LDS stage
-constexpr int G_XOFF = 32 * 1024;          // activation region within a stage
+constexpr int GB_N = 256;                  // block tile: weight rows (x BM tokens, BM = 256 or 128)
+constexpr int G_GROUP_M = 8;               // token blocks per raster group
+constexpr int G_XOFF = 16 * 1024;          // activation region within a stage (after 16 weight units)
 constexpr int G_EPI_PITCH = 68;            // epilogue LDS row pitch (floats): 64 rows + pad
 
+// Per token-tile height BM: 1 KB units per stage (16 weight units + BM/16
+// activation units of one 32-deep k-step), units each of the 4 waves moves,
+// LDS pipeline depth (BM = 128 leaves room for two workgroups per CU).
+template <int BM> struct GTile {
+    static constexpr int MB = BM / 64;                // 32-token MFMA blocks per wave
+    static constexpr int UNITS = 16 + BM / 16;
+    static constexpr int UPW = UNITS / 4;
+    static constexpr int STAGE = UNITS * 1024;
+    static constexpr int NS = BM == 256 ? 4 : 3;
+    static constexpr size_t lds_bytes() {
+        const size_t epi = 4 * (size_t)(BM / 2) * G_EPI_PITCH * sizeof(float);
+        const size_t pipe = (size_t)NS * STAGE;
+        return epi > pipe ? epi : pipe;
+    }
+};
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
+// memory operations are outstanding, leaving the other counters alone
+constexpr unsigned vm_wait(int n) { return 0x0F70u | ((unsigned)n & 15u) | (((unsigned)n >> 4) << 14); }
+
+// One 1 KB unit global -> LDS (buffer_load_dwordx4 ... lds; M0 = LDS base of
+// the unit, lane l lands at +16*l).  Written as inline assembly so that the
+// compiler does not treat the asynchronous LDS write as a hazard for the
+// later LDS reads and wait for every load in flight: the K-loop waits for
+// exactly the stage it consumes (vector-memory counters retire in order)
+// and a barrier publishes it.
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds_unit, uint32_t voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds_unit, 16, voff, 0, 0, 0);
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds_unit;
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs)
+                 : "memory", "m0");
 }
 
 // Element-wise store for outputs whose row count or alignment rules out the
@@ -62,10 +97,13 @@ __device__ __forceinline__ void gemm_store_slow(const GemmArgs& a, int m, int ro
     }
 }
 
-template <bool GLU, bool ARGMAX>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_bf16_kernel(GemmArgs a) {
+template <bool GLU, bool ARGMAX, int BM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 256 ? 1 : 2, BM == 256 ? 1 : 2)))
+void gemm_bf16_kernel(GemmArgs a) {
+    using T = GTile<BM>;
+    constexpr int MB = T::MB, UPW = T::UPW, G_NS = T::NS, G_STAGE = T::STAGE;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ unsigned long long best_s[2][GB_M];
+    __shared__ unsigned long long best_s[2][BM];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -77,97 +115,110 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int nwg = gridDim.x;
     int b = blockIdx.x;
     if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
-    const int bm = b % a.nblk_m, bn = b / a.nblk_m;
+    // grouped raster: G_GROUP_M token blocks x all weight blocks per group,
+    // token block fastest, so the workgroups resident on one XCD at a time
+    // share both their activation blocks and their weight blocks in its L2
+    const int per_group = G_GROUP_M * a.nblk_n;
+    const int group = b / per_group;
+    const int first_m = group * G_GROUP_M;
+    const int gm = min(G_GROUP_M, a.nblk_m - first_m);
+    const int in_group = b - group * per_group;
+    const int bm = first_m + in_group % gm, bn = in_group / gm;
     const int nt0 = bn * (GB_N / 16);          // first physical 16-row tile
-    const int m0 = bm * GB_M;
+    const int m0 = bm * BM;
 
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_tiles * a.ksteps * 1024u));
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
-    const int nkb = a.ksteps / 2;
+    const int nkb = a.ksteps;  // K-blocks of one 32-deep k-step
 
-    // The 16 units this wave moves per K-block: waves 0,1 the 32 weight units
-    // (16 tiles x 2 k-steps), waves 2,3 the 32 activation units (16 token
-    // groups x 2 k-steps); unit u lands at byte u*1024 of the stage either
-    // way.  Offsets for K-block 0 are computed once; K-block kb adds kb*kstep.
-    const bool wrole = wave < 2;
-    const __amdgpu_buffer_rsrc_t rs = wrole ? wrs : xrs;
-    const uint32_t kstep = wrole ? 2048u : 128u;
-    uint32_t vbase[16];
+    // The UPW units this wave moves per K-block: unit u = wave*UPW + q of the
+    // stage is weight tile u (u < 16) or activation token group u - 16, and
+    // lands at byte u*1024.  Offsets for K-block 0 are computed once; K-block
+    // kb adds kb*1024 (weights) or kb*64 bytes (activations).
+    uint32_t vbase[UPW];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int v = (wave & 1) * 16 + q;  // unit within the role
-        const int t = v >> 1, ks = v & 1;
-        if (wrole) {
-            const int pt = nt0 + t;
-            vbase[q] = pt < a.n_tiles ? (uint32_t)((pt * a.ksteps + ks) * 1024 + lane * 16) : OOB;
+    for (int q = 0; q < UPW; ++q) {
+        const int u = wave * UPW + q;
+        if (u < 16) {
+            const int pt = nt0 + u;
+            vbase[q] = pt < a.n_tiles ? (uint32_t)(pt * a.ksteps * 1024 + lane * 16) : OOB;
         } else {
-            const int row = m0 + t * 16 + (lane & 15);
-            vbase[q] = row < a.M ? (uint32_t)((row * a.ldx + ks * 32 + (lane >> 4) * 8) * 2) : OOB;
+            const int row = m0 + (u - 16) * 16 + (lane & 15);
+            vbase[q] = row < a.M ? (uint32_t)((row * a.ldx + (lane >> 4) * 8) * 2) : OOB;
         }
     }
-    auto issue = [&](int kb, int stage) {
-        uint8_t* st = lds + stage * G_STAGE + wave * 16 * 1024;
-        const uint32_t add = (uint32_t)kb * kstep;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) lds_dma16(rs, st + q * 1024, vbase[q] + add);
+    auto dma = [&](int kb, int q) {
+        const int u = wave * UPW + q;
+        uint8_t* dst = lds + (kb % G_NS) * G_STAGE + u * 1024;
+        if (u < 16) lds_dma16(wrs, dst, vbase[q] + (uint32_t)kb * 1024u);
+        else lds_dma16(xrs, dst, vbase[q] + (uint32_t)kb * 64u);
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[4][MB];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+        for (int j = 0; j < MB; ++j) acc[i][j] = f32x16{};
 
     // lane -> fragment address within a (tile pair, k-step) unit: row l%32 of
     // a 32-row block = tile (l%32)/16, row l%16; k-group 2h + l/32
     const int frag_tile = (lane & 31) >> 4;
     const int frag_off = ((lane & 15) + 16 * (lane >> 5)) * 16;  // + 32*16*h
 
-    // fragments of sub-step s = 2*ks + h of a K-block
-    bf16x8 A[2][4], B[2][4];
-    auto read_frags = [&](const uint8_t* st, int sub, bf16x8 (&Ad)[4], bf16x8 (&Bd)[4]) {
-        const int ks = sub >> 1, h = sub & 1;
+    // fragments of half h (16 of the 32 k) of a K-block
+    bf16x8 A[2][4], B[2][MB];
+    auto read_frags = [&](const uint8_t* st, int h, bf16x8 (&Ad)[4], bf16x8 (&Bd)[MB]) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
             const int t = wn * 8 + nb * 2 + frag_tile;
-            Ad[nb] = *reinterpret_cast<const bf16x8*>(st + (t * 2 + ks) * 1024 + frag_off + h * 512);
+            Ad[nb] = *reinterpret_cast<const bf16x8*>(st + t * 1024 + frag_off + h * 512);
         }
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-            const int t = wm * 8 + mb * 2 + frag_tile;
-            Bd[mb] = *reinterpret_cast<const bf16x8*>(st + G_XOFF + (t * 2 + ks) * 1024 + frag_off + h * 512);
+        for (int mb = 0; mb < MB; ++mb) {
+            const int t = wm * 2 * MB + mb * 2 + frag_tile;
+            Bd[mb] = *reinterpret_cast<const bf16x8*>(st + G_XOFF + t * 1024 + frag_off + h * 512);
         }
     };
 
-    // Software pipeline: the fragments of the next sub-step are read from LDS
-    // while the 16 MFMAs of the current one run; the global->LDS loads of
-    // K-block kb+1 are in flight during all of K-block kb.
-    issue(0, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    read_frags(lds, 0, A[0], B[0]);
-    for (int kb = 0; kb < nkb; ++kb) {
-        const uint8_t* st = lds + (kb & 1) * G_STAGE;
-        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
+    // G_NS-stage pipeline over K-blocks: blocks kb+1 .. kb+G_NS-1 are loaded
+    // while kb is multiplied.  A wave waits only for its own loads of block
+    // kb (vector-memory counters retire in order), then one barrier publishes
+    // the block to all waves and frees the stage of block kb-1.  Inside a
+    // block the fragments of the next sub-step are read while the current
+    // sub-step's 16 MFMAs run, and the block's global->LDS loads are issued
+    // one per MFMA pair so the matrix pipe never waits on a burst of issues.
 #pragma unroll
-        for (int sub = 0; sub < 4; ++sub) {
-            const int cur = sub & 1;
-            if (sub < 3) {
-                read_frags(st, sub + 1, A[cur ^ 1], B[cur ^ 1]);
-            } else {
-                // stage kb+1 complete and every wave done with stage kb
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                if (kb + 1 < nkb) read_frags(lds + ((kb + 1) & 1) * G_STAGE, 0, A[cur ^ 1], B[cur ^ 1]);
-            }
-            __builtin_amdgcn_s_setprio(1);
+    for (int s0 = 0; s0 < G_NS - 1; ++s0)
+        if (s0 < nkb) {
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
-                    acc[nb][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[cur][nb], B[cur][mb], acc[nb][mb], 0, 0, 0);
-            __builtin_amdgcn_s_setprio(0);
+            for (int q = 0; q < UPW; ++q) dma(s0, q);
         }
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int later = min(G_NS - 2, nkb - 1 - kb);  // blocks issued after kb
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(2 * UPW));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_wait(UPW));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        __syncthreads();
+        const uint8_t* st = lds + (kb % G_NS) * G_STAGE;
+        const bool more = kb + G_NS - 1 < nkb;
+        read_frags(st, 0, A[0], B[0]);
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (h == 0) read_frags(st, 1, A[1], B[1]);
+#pragma unroll
+            for (int i = 0; i < 4 * MB; ++i) {
+                acc[i / MB][i % MB] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[h][i / MB], B[h][i % MB], acc[i / MB][i % MB], 0, 0, 0);
+                const int q = (h * 4 * MB + i) >> 1;
+                if ((i & 1) && q < UPW) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (more) dma(kb + G_NS - 1, q);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        __builtin_amdgcn_s_setprio(0);
     }
 
     // ---- epilogue ----
@@ -175,7 +226,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // the 32-row block, token j = l%32 of the 32-token block
     const int ihi = 4 * (lane >> 5);
     if constexpr (ARGMAX) {
-        unsigned long long best[4] = {0ull, 0ull, 0ull, 0ull};
+        unsigned long long best[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) best[mb] = 0ull;
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
             const int pt0 = nt0 + wn * 8 + nb * 2;
@@ -185,7 +238,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 f32x4 sc = {1.f, 1.f, 1.f, 1.f};
                 if (a.scales) sc = *reinterpret_cast<const f32x4*>(a.scales + row);
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb)
+                for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const unsigned long long kk = argmax_key(acc[nb][mb][4 * qg + e] * sc[e], (uint32_t)(row + e));
@@ -196,13 +249,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // lanes l and l^32 hold the same token; then the two waves sharing a
         // token range (wn = 0, 1) meet in LDS; then the grid via atomic max
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
+        for (int mb = 0; mb < MB; ++mb) {
             const unsigned long long o = __shfl_xor(best[mb], 32);
             best[mb] = o > best[mb] ? o : best[mb];
-            if (lane < 32) best_s[wn][wm * 128 + mb * 32 + lane] = best[mb];
+            if (lane < 32) best_s[wn][wm * (BM / 2) + mb * 32 + lane] = best[mb];
         }
         __syncthreads();
-        if (threadIdx.x < GB_M) {
+        if (threadIdx.x < BM) {
             const int j = threadIdx.x;
             unsigned long long k0 = best_s[0][j], k1 = best_s[1][j];
             const unsigned long long kk = k0 > k1 ? k0 : k1;
@@ -233,9 +286,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         // coalesced store, and so that the accumulators are only ever indexed
         // with constants.  GLU: the wave's 64 output rows in one pass; plain:
         // its 128 rows in two passes of 64.
-        float* ep = reinterpret_cast<float*>(lds) + wave * (128 * G_EPI_PITCH);
+        float* ep = reinterpret_cast<float*>(lds) + wave * ((BM / 2) * G_EPI_PITCH);
         const int row_base = GLU ? ((nt0 + wn * 8) >> 1) * 16 : (nt0 + wn * 8) * 16;
-        const int tok_base = m0 + wm * 128;
+        const int tok_base = m0 + wm * (BM / 2);
         const bool has_res = (a.flags & EP_RESIDUAL) != 0;
         const bool has_split = (a.flags & EP_SPLIT) != 0;
         const int sp_log = a.split_period > 0 ? 31 - __builtin_clz((unsigned)a.split_period) : 0;
@@ -256,7 +309,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                     }
                     const int lrow = GLU ? nb * 16 + r0 : nbl * 32 + r0;
 #pragma unroll
-                    for (int mb = 0; mb < 4; ++mb) {
+                    for (int mb = 0; mb < MB; ++mb) {
                         f32x4 o4;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
@@ -274,7 +327,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             __builtin_amdgcn_wave_barrier();
             const int c = lane & 15;  // rows 4c .. 4c+3
             const int row = row_base + pass * 64 + 4 * c;
-            for (int it = 0; it < 32; ++it) {
+            for (int it = 0; it < BM / 8; ++it) {
                 const int jj = it * 4 + (lane >> 4);
                 const int m = tok_base + jj;
                 if (m < a.M && row < a.N) {
@@ -301,32 +354,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-size_t gemm_lds_bytes() {
-    const size_t epi = 4 * 128 * G_EPI_PITCH * sizeof(float);
-    return epi > 2 * (size_t)G_STAGE ? epi : 2 * (size_t)G_STAGE;
-}
-
 template <typename Kern>
-static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, hipStream_t st) {
-    static bool configured = false;
+static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, size_t lds, hipStream_t st) {
+    static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemm_lds_bytes());
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), gemm_lds_bytes(), st, a);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, a);
     return hipGetLastError();
+}
+
+template <int BM>
+static hipError_t launch_bm(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
+    const int grid = a.nblk_n * a.nblk_m;
+    const size_t lds = GTile<BM>::lds_bytes();
+    if (argmax) return launch_gemm_k(gemm_bf16_kernel<false, true, BM>, a, grid, lds, stream);
+    if (glu) return launch_gemm_k(gemm_bf16_kernel<true, false, BM>, a, grid, lds, stream);
+    return launch_gemm_k(gemm_bf16_kernel<false, false, BM>, a, grid, lds, stream);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream) {
     if (wf != WF_BF16 || xdt != DT_BF16) return hipErrorInvalidValue;
-    if (a.ksteps % 2 != 0) return hipErrorInvalidValue;
     if (argmax && glu) return hipErrorInvalidValue;
-    const int grid = a.nblk_n * a.nblk_m;
-    if (argmax) return launch_gemm_k(gemm_bf16_kernel<false, true>, a, grid, stream);
-    if (glu) return launch_gemm_k(gemm_bf16_kernel<true, false>, a, grid, stream);
-    return launch_gemm_k(gemm_bf16_kernel<false, false>, a, grid, stream);
+    if (a.tile_m == 256 && a.nblk_m == (a.M + 255) / 256) return launch_bm<256>(a, glu, argmax, stream);
+    if (a.tile_m == 128 && a.nblk_m == (a.M + 127) / 128) return launch_bm<128>(a, glu, argmax, stream);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace qwk

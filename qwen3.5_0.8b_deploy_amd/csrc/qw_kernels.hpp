@@ -66,7 +66,8 @@ struct GemmArgs {
     const void* x;           // activations [M][ldx]
     int ldx;
     int M, K, N;             // N: logical output rows
-    int nblk_n, nblk_m;      // 256 x 256 block grid
+    int nblk_n, nblk_m;      // block grid: 256 weight rows x tile_m tokens
+    int tile_m;              // tokens per block: 256 or 128
     unsigned flags;
     const void* res;
     int res_dt, ld_res;
@@ -80,7 +81,6 @@ struct GemmArgs {
     int32_t* ids;
     float* maxv;
 };
-size_t gemm_lds_bytes();
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream);
 
 // Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass
