@@ -474,16 +474,19 @@ static qw_status check_xdt(qw_ctx* ctx, const qw_weight* W, qw_dtype xdt) {
 }
 
 // Skinny launch for M <= 32 tokens (argmax: ids/maxv set, y ignored).
+// tg_size > 0 and M > tg_size: one launch over token groups of tg_size.
 static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx,
-                            int M, void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep,
-                            int32_t* ids, float* maxv, hipStream_t stream) {
+                            int M_total, void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep,
+                            int32_t* ids, float* maxv, hipStream_t stream, int tg_size = 0) {
     const bool argmax = ids != nullptr;
+    const int groups = (tg_size > 0 && M_total > tg_size) ? (M_total + tg_size - 1) / tg_size : 1;
+    const int M = groups > 1 ? tg_size : M_total;  // tokens one workgroup sees
     qwk::SkinnyArgs a{};
     a.w = W->packed;
     a.scales = W->scales;
     a.x = x;
     a.ldx = ldx;
-    a.M = M;
+    a.M = M_total;
     a.K = W->K;
     a.N = W->N;
     a.n_groups = (W->N + 15) / 16;
@@ -520,8 +523,8 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
         ++S;
     }
     if (S > 1) {
-        if (a.n_groups > kMaxCounters) return fail(ctx, QW_ERR_WORKSPACE, "too many split-K tiles");
-        if ((size_t)a.n_groups * S * 64 * (RT * CT * 4 + CT) * 4 > ctx->partials_bytes)
+        if ((int64_t)a.n_groups * groups > kMaxCounters) return fail(ctx, QW_ERR_WORKSPACE, "too many split-K tiles");
+        if ((size_t)a.n_groups * groups * S * 64 * (RT * CT * 4 + CT) * 4 > ctx->partials_bytes)
             return fail(ctx, QW_ERR_WORKSPACE, "split-K partials exceed the workspace");
     }
     a.S = S;
@@ -556,7 +559,19 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     // a workgroup keeps one K split for its life: grid is a multiple of S
     int grid = std::min(a.n_items, ctx->num_cus * ctx->wg_per_cu);
     grid = std::max(S, grid - grid % S);
-    if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * dsize(xdt) >= (1ull << 32))
+    if (groups > 1) {
+        // the groups share the device's workgroup slots; a multiple of 8 per
+        // group puts the workgroups of one tile (one per group) on one XCD,
+        // where the later ones find its weights in L2
+        int per = (ctx->num_cus * ctx->wg_per_cu + groups - 1) / groups;
+        per = std::min(per, a.n_items);
+        per = (per + 7) / 8 * 8;
+        per = (per + S - 1) / S * S;
+        a.tg_size = tg_size;
+        a.tg_grid = per;
+        grid = per * groups;
+    }
+    if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M_total * ldx * dsize(xdt) >= (1ull << 32))
         return fail(ctx, QW_ERR_SHAPE, "operands above 4 GiB are not supported");
     hipError_t e = direct ? qwk::launch_gemv(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream)
                           : qwk::launch_skinny(a, W->wf, (int)xdt, W->glu != 0, argmax, nw, grid, stream);
@@ -702,28 +717,12 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
         }
         return QW_OK;
     }
-    // token chunks of at most 32 for the small-M kernels (16 with the
-    // RMSNorm prologue, which the register-direct GEMV takes 16 at a time)
-    qw_epilogue e2;
-    if (ep) e2 = *ep;
+    // small-M kernels: up to 32 tokens per workgroup (16 with the RMSNorm
+    // prologue, which the register-direct GEMV takes 16 at a time); more
+    // tokens run as token groups of one launch
     const bool norm = ep && (ep->flags & QW_EP_NORM_X);
-    const int cmax = (norm && ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, 16, true)) ? 16 : kSkinnyMaxM;
-    for (int m0 = 0; m0 < M; m0 += cmax) {
-        const int mc = std::min(cmax, M - m0);
-        const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * ldx * dsize(xdt);
-        void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * ldy * dsize(ydt);
-        if (ep) {
-            if (ep->flags & QW_EP_RESIDUAL) {
-                const int ldr = ep->ld_residual ? ep->ld_residual : W->N;
-                e2.residual = static_cast<const uint8_t*>(ep->residual) + (size_t)m0 * ldr * dsize(ep->residual_dtype);
-            }
-            if (ep->flags & QW_EP_SPLIT)
-                e2.y2 = static_cast<uint8_t*>(ep->y2) + (size_t)m0 * ldy * dsize(ydt);
-        }
-        s = run_skinny(ctx, W, xc, xdt, ldx, mc, yc, ydt, ldy, ep ? &e2 : nullptr, nullptr, nullptr, stream);
-        if (s != QW_OK) return s;
-    }
-    return QW_OK;
+    const int tg = (norm && ctx->gemv && qwk::gemv_supported(W->wf, (int)xdt, 16, true)) ? 16 : kSkinnyMaxM;
+    return run_skinny(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream, tg);
 }
 
 qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M,
@@ -734,14 +733,8 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
     if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
     if (use_gemm(ctx, E, hdt, M)) return run_gemm(ctx, E, h, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
-    for (int m0 = 0; m0 < M; m0 += kSkinnyMaxM) {
-        const int mc = std::min(kSkinnyMaxM, M - m0);
-        const void* hc = static_cast<const uint8_t*>(h) + (size_t)m0 * E->K * dsize(hdt);
-        s = run_skinny(ctx, E, hc, hdt, E->K, mc, nullptr, QW_F32, 0, nullptr, token_ids + m0,
-                       max_logit ? max_logit + m0 : nullptr, stream);
-        if (s != QW_OK) return s;
-    }
-    return QW_OK;
+    return run_skinny(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream,
+                      kSkinnyMaxM);
 }
 
 qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,

@@ -120,7 +120,26 @@ __device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT, CT>& f, 
 }
 
 template <int WF, int XDT, int CT, bool GLU, bool ARGMAX, int NW, bool NORM, bool GAM>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemv_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void gemv_kernel(SkinnyArgs ain) {
+    // Token groups (tg_grid > 0): the grid is tg_grid workgroups per group of
+    // tg_size tokens, all groups of a launch streaming the same weights
+    // concurrently (workgroup w: group w / tg_grid); each workgroup sees its
+    // group as a small-M problem of its own.
+    const int tgi = ain.tg_grid ? (int)(blockIdx.x / (unsigned)ain.tg_grid) : 0;
+    const int bid = (int)blockIdx.x - tgi * ain.tg_grid;
+    const int gdim = ain.tg_grid ? ain.tg_grid : (int)gridDim.x;
+    const int gofs = tgi * ain.n_groups;  // this group's split-K counters / partials
+    SkinnyArgs a = ain;
+    if (ain.tg_grid) {
+        const int tok0 = tgi * ain.tg_size;
+        a.M = min(ain.tg_size, ain.M - tok0);
+        a.x = static_cast<const uint8_t*>(ain.x) + (int64_t)tok0 * ain.ldx * 2;
+        const int ys = ain.ydt == DT_F32 ? 4 : 2;
+        if (ain.y) a.y = static_cast<uint8_t*>(ain.y) + (int64_t)tok0 * ain.ldy * ys;
+        if (ain.y2) a.y2 = static_cast<uint8_t*>(ain.y2) + (int64_t)tok0 * ain.ldy * ys;
+        if (ain.res) a.res = static_cast<const uint8_t*>(ain.res) + (int64_t)tok0 * ain.ld_res * (ain.res_dt == DT_F32 ? 4 : 2);
+        a.keys = ain.keys + tok0;
+    }
     // k-steps per register buffer (two buffers in flight); fewer where the
     // activation fragments and RMSNorm weights would crowd the registers
     constexpr int U = ((GAM && WF == WF_I8) || (CT == 2 && (GAM || WF == WF_I8))) ? 2 : 4;
@@ -138,11 +157,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 
     int s = 0, ks0 = 0, ks1 = a.ksteps;
     if (a.S > 1) {
-        s = blockIdx.x % a.S;
+        s = bid % a.S;
         ks0 = (s * a.ksteps) / a.S;
         ks1 = ((s + 1) * a.ksteps) / a.S;
     }
-    const int grp_step = a.S > 1 ? gridDim.x / a.S : gridDim.x;
+    const int grp_step = a.S > 1 ? gdim / a.S : gdim;
     int kb, kend;
     wave_range<NW>(ks0, ks1, wave_id, kb, kend);
     const int kb0 = kb;
@@ -171,8 +190,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     u32x4 A0[U][RT], A1[U][RT];
     XFrag<WF, XDT, CT> X0[U], X1[U];
     EpiOps<RT, CT> epi, epi_next;
-    int item = blockIdx.x;
-    int grp = a.S > 1 ? blockIdx.x / a.S : blockIdx.x;
+    int item = bid;
+    int grp = a.S > 1 ? bid / a.S : bid;
 
     auto issue = [&](int grp_, int kb_, int n_, u32x4 (&Ad)[U][RT], XFrag<WF, XDT, CT> (&Xd)[U]) {
 #pragma unroll
@@ -227,7 +246,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
             if (kb >= kend) break;
         }
         const int cur_grp = grp;
-        item += gridDim.x;
+        item += gdim;
         grp += grp_step;
         kb = kb0;
         if (item < a.n_items) {  // next item's loads fly during this item's reduction
@@ -294,7 +313,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                 // then the agent-scope arrival count; the last arriver sums
                 // the S partials in split order and re-arms the counter
                 constexpr int REC = F * 4 + CT;
-                float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)grp_c * a.S * 64 + lane) * REC;
+                float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)(grp_c + gofs) * a.S * 64 + lane) * REC;
                 float* mine = P + (int64_t)s * 64 * REC;
 #pragma unroll
                 for (int f = 0; f < F; ++f)
@@ -308,7 +327,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 unsigned old = 0;
                 if (lane == 0)
-                    old = __hip_atomic_fetch_add(&a.counters[grp_c], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    old = __hip_atomic_fetch_add(&a.counters[grp_c + gofs], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 old = __shfl(old, 0);
                 finish = (old == (unsigned)(a.S - 1));
                 if (finish) {
@@ -330,7 +349,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                         for (int ct = 0; ct < CT; ++ct)
                             ss[ct] += __hip_atomic_load(q + F * 4 + ct, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    if (lane == 0) __hip_atomic_store(&a.counters[grp_c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (lane == 0) __hip_atomic_store(&a.counters[grp_c + gofs], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
         }
@@ -419,11 +438,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __shfl(old, 0);
         if (old == gridDim.x - 1) {
-            for (int mm = lane; mm < a.M; mm += 64) {
+            for (int mm = lane; mm < ain.M; mm += 64) {
                 const unsigned long long kk =
-                    __hip_atomic_exchange(&a.keys[mm], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                a.ids[mm] = (int32_t)key_index(kk);
-                if (a.maxv) a.maxv[mm] = key_value(kk);
+                    __hip_atomic_exchange(&ain.keys[mm], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ain.ids[mm] = (int32_t)key_index(kk);
+                if (ain.maxv) ain.maxv[mm] = key_value(kk);
             }
             if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -473,25 +492,29 @@ static hipError_t launch_c(const SkinnyArgs& a, bool glu, bool argmax, int nw, i
     if constexpr (CT == 2) {  // two token tiles leave no registers for the RMSNorm operands
         if (a.flags & EP_NORM) return hipErrorInvalidValue;
         return launch_n<WF, XDT, CT, false, false>(a, glu, argmax, nw, grid, st);
+    } else {
+        if (a.flags & EP_NORM) {
+            if (a.gamma) return launch_n<WF, XDT, CT, true, true>(a, glu, argmax, nw, grid, st);
+            return launch_n<WF, XDT, CT, true, false>(a, glu, argmax, nw, grid, st);
+        }
+        return launch_n<WF, XDT, CT, false, false>(a, glu, argmax, nw, grid, st);
     }
-    if (a.flags & EP_NORM) {
-        if (a.gamma) return launch_n<WF, XDT, CT, true, true>(a, glu, argmax, nw, grid, st);
-        return launch_n<WF, XDT, CT, true, false>(a, glu, argmax, nw, grid, st);
-    }
-    return launch_n<WF, XDT, CT, false, false>(a, glu, argmax, nw, grid, st);
 }
 
 template <int WF, int XDT>
 static hipError_t launch_x(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, hipStream_t st) {
-    if (a.M <= 16) return launch_c<WF, XDT, 1>(a, glu, argmax, nw, grid, st);
+    if ((a.tg_grid ? a.tg_size : a.M) <= 16) return launch_c<WF, XDT, 1>(a, glu, argmax, nw, grid, st);
     return launch_c<WF, XDT, 2>(a, glu, argmax, nw, grid, st);
 }
 
 hipError_t launch_gemv(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                        hipStream_t stream) {
-    if (!gemv_supported(wf, xdt, a.M, (a.flags & EP_NORM) != 0)) return hipErrorInvalidValue;
+    const int mg = a.tg_grid ? a.tg_size : a.M;  // tokens one workgroup sees
+    if (!gemv_supported(wf, xdt, mg, (a.flags & EP_NORM) != 0)) return hipErrorInvalidValue;
+    if (a.tg_grid && (grid % a.tg_grid != 0 || (int64_t)(grid / a.tg_grid) * a.tg_size < a.M))
+        return hipErrorInvalidValue;
     if (nw != 4 && nw != 8 && nw != 16) return hipErrorInvalidValue;
-    if (a.S < 1 || grid % a.S != 0) return hipErrorInvalidValue;
+    if (a.S < 1 || (a.tg_grid ? a.tg_grid : grid) % a.S != 0) return hipErrorInvalidValue;
     if (wf == WF_BF16) return launch_x<WF_BF16, DT_BF16>(a, glu, argmax, nw, grid, stream);
     if (xdt == DT_F16) return launch_x<WF_I8, DT_F16>(a, glu, argmax, nw, grid, stream);
     return launch_x<WF_I8, DT_BF16>(a, glu, argmax, nw, grid, stream);

@@ -37,6 +37,8 @@ struct SkinnyArgs {
     unsigned* done;          // argmax completion counter (self-resetting)
     int32_t* ids;            // argmax ids [M]
     float* maxv;             // argmax values [M] or nullptr
+    int tg_size;             // token-group height (tokens per group); 0: one group
+    int tg_grid;             // workgroups per token group; 0: one group
 };
 
 // LDS the skinny kernel stages its activations in: (M+1) rows of the split's

@@ -41,7 +41,26 @@
 namespace qwk {
 
 template <int WF, int XDT, int CT, bool GLU, bool ARGMAX, int NW>
-__global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs ain) {
+    // Token groups (tg_grid > 0): the grid is tg_grid workgroups per group of
+    // tg_size tokens, all groups of a launch streaming the same weights
+    // concurrently (workgroup w: group w / tg_grid); each workgroup sees its
+    // group as a small-M problem of its own.
+    const int tgi = ain.tg_grid ? (int)(blockIdx.x / (unsigned)ain.tg_grid) : 0;
+    const int bid = (int)blockIdx.x - tgi * ain.tg_grid;
+    const int gdim = ain.tg_grid ? ain.tg_grid : (int)gridDim.x;
+    const int gofs = tgi * ain.n_groups;  // this group's split-K counters / partials
+    SkinnyArgs a = ain;
+    if (ain.tg_grid) {
+        const int tok0 = tgi * ain.tg_size;
+        a.M = min(ain.tg_size, ain.M - tok0);
+        a.x = static_cast<const uint8_t*>(ain.x) + (int64_t)tok0 * ain.ldx * XSize<XDT>::v;
+        const int ys = ain.ydt == DT_F32 ? 4 : 2;
+        if (ain.y) a.y = static_cast<uint8_t*>(ain.y) + (int64_t)tok0 * ain.ldy * ys;
+        if (ain.y2) a.y2 = static_cast<uint8_t*>(ain.y2) + (int64_t)tok0 * ain.ldy * ys;
+        if (ain.res) a.res = static_cast<const uint8_t*>(ain.res) + (int64_t)tok0 * ain.ld_res * (ain.res_dt == DT_F32 ? 4 : 2);
+        a.keys = ain.keys + tok0;
+    }
     constexpr int U = (GLU && NW == 16) ? 4 : 8;
     constexpr int KE = WTraits<WF>::KE;
     constexpr int RT = GLU ? 2 : 1;
@@ -60,16 +79,16 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
     const bool norm = (a.flags & EP_NORM) != 0;
     const bool want_res = !ARGMAX && (a.flags & EP_RESIDUAL);
 
-    // This workgroup's K split is constant (the host makes gridDim.x % S == 0),
-    // so its tile group advances by gridDim.x / S per item: no division in
+    // This workgroup's K split is constant (the host makes gdim % S == 0),
+    // so its tile group advances by gdim / S per item: no division in
     // the item loop.
     int s = 0, ks0 = 0, ks1 = a.ksteps;
     if (a.S > 1) {
-        s = blockIdx.x % a.S;
+        s = bid % a.S;
         ks0 = (s * a.ksteps) / a.S;
         ks1 = ((s + 1) * a.ksteps) / a.S;
     }
-    const int grp_step = a.S > 1 ? gridDim.x / a.S : gridDim.x;
+    const int grp_step = a.S > 1 ? gdim / a.S : gdim;
     int kb, kend;
     wave_range<NW>(ks0, ks1, wave_id, kb, kend);
     const int kb0 = kb;
@@ -91,8 +110,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
 
     u32x4 A[U][RT];
     EpiOps<RT, CT> epi, epi_next;
-    int item = blockIdx.x;
-    int grp = a.S > 1 ? blockIdx.x / a.S : blockIdx.x;
+    int item = bid;
+    int grp = a.S > 1 ? bid / a.S : bid;
     int n = min(U, kend - kb);
     // activation loads first, then the epilogue operands, then the weights;
     // the activations are converted into LDS while the weights stream in
@@ -171,7 +190,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
             issue_weights<RT, U>(a, wrs, grp, kb, n, lane, A);
         }
         const int cur_grp = grp;
-        item += gridDim.x;
+        item += gdim;
         grp += grp_step;
         kb = kb0;
         n = min(U, kend - kb);
@@ -219,7 +238,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                 // loads, in split order (deterministic), and returns the
                 // counter to zero.
                 constexpr int REC = F * 4 + CT;  // floats per lane per split
-                float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)grp * a.S * 64 + lane) * REC;
+                float* P = reinterpret_cast<float*>(a.partials) + ((int64_t)(grp + gofs) * a.S * 64 + lane) * REC;
                 float* mine = P + (int64_t)s * 64 * REC;
 #pragma unroll
                 for (int f = 0; f < F; ++f)
@@ -233,7 +252,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                 asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 unsigned old = 0;
                 if (lane == 0)
-                    old = __hip_atomic_fetch_add(&a.counters[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    old = __hip_atomic_fetch_add(&a.counters[grp + gofs], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 old = __shfl(old, 0);
                 finish = (old == (unsigned)(a.S - 1));
                 if (finish) {
@@ -256,7 +275,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
                             ss[ct] += __hip_atomic_load(q + F * 4 + ct, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                     if (lane == 0)
-                        __hip_atomic_store(&a.counters[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&a.counters[grp + gofs], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
         }
@@ -350,11 +369,11 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs a) {
         if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __shfl(old, 0);
         if (old == gridDim.x - 1) {
-            for (int m = lane; m < a.M; m += 64) {
-                unsigned long long kk = __hip_atomic_exchange(&a.keys[m], 0ull, __ATOMIC_RELAXED,
+            for (int m = lane; m < ain.M; m += 64) {
+                unsigned long long kk = __hip_atomic_exchange(&ain.keys[m], 0ull, __ATOMIC_RELAXED,
                                                               __HIP_MEMORY_SCOPE_AGENT);
-                a.ids[m] = (int32_t)key_index(kk);
-                if (a.maxv) a.maxv[m] = key_value(kk);
+                ain.ids[m] = (int32_t)key_index(kk);
+                if (ain.maxv) ain.maxv[m] = key_value(kk);
             }
             if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -407,7 +426,7 @@ static hipError_t launch3(const SkinnyArgs& a, bool glu, bool argmax, int nw, in
 
 template <int WF, int XDT>
 static hipError_t launch2(const SkinnyArgs& a, bool glu, bool argmax, int nw, int grid, size_t smem, hipStream_t st) {
-    if (a.M <= 16) return launch3<WF, XDT, 1>(a, glu, argmax, nw, grid, smem, st);
+    if ((a.tg_grid ? a.tg_size : a.M) <= 16) return launch3<WF, XDT, 1>(a, glu, argmax, nw, grid, smem, st);
     return launch3<WF, XDT, 2>(a, glu, argmax, nw, grid, smem, st);
 }
 
@@ -424,10 +443,13 @@ static hipError_t launch1(const SkinnyArgs& a, int xdt, bool glu, bool argmax, i
 
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream) {
-    if (a.M < 1 || a.M > 32) return hipErrorInvalidValue;
+    const int mg = a.tg_grid ? a.tg_size : a.M;  // tokens one workgroup sees
+    if (a.M < 1 || mg < 1 || mg > 32) return hipErrorInvalidValue;
+    if (a.tg_grid && (grid % a.tg_grid != 0 || (int64_t)(grid / a.tg_grid) * a.tg_size < a.M))
+        return hipErrorInvalidValue;
     if (nw != 4 && nw != 8 && nw != 16) return hipErrorInvalidValue;
-    if (a.S < 1 || grid % a.S != 0) return hipErrorInvalidValue;
-    const size_t smem = skinny_lds_bytes(wf, xdt, a.M, (a.ksteps + a.S - 1) / a.S);
+    if (a.S < 1 || (a.tg_grid ? a.tg_grid : grid) % a.S != 0) return hipErrorInvalidValue;
+    const size_t smem = skinny_lds_bytes(wf, xdt, mg, (a.ksteps + a.S - 1) / a.S);
     if (smem > kSkinnyMaxLds) return hipErrorInvalidValue;
     switch (wf) {
         case WF_F32: return launch1<WF_F32>(a, xdt, glu, argmax, nw, grid, smem, stream);

@@ -25,7 +25,7 @@ def host(t):
 # lm_head + argmax
 # ----------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M", [1, 5, 32, 37])
+@pytest.mark.parametrize("M", [1, 5, 32, 37, 100])
 def test_lmhead_argmax_bf16(qw, ctx, oracle, M):
     V, K = 20000, 1024
     E = oracle.normal((V, K), 301, 0.0, 0.02)
@@ -47,7 +47,7 @@ def test_lmhead_argmax_bf16(qw, ctx, oracle, M):
     assert np.array_equal(ids2.cpu().numpy(), ref_ids)
 
 
-@pytest.mark.parametrize("M", [1, 8])
+@pytest.mark.parametrize("M", [1, 8, 70])
 def test_lmhead_argmax_int8(qw, ctx, oracle, M):
     V, K = 12000, 1024
     E = oracle.normal((V, K), 311, 0.0, 0.02)
@@ -95,7 +95,7 @@ def _mlp_weights(oracle, H, I, seed):
     return G, U, D
 
 
-@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("M", [1, 8, 32, 128])
 def test_mlp_fused_bf16(qw, ctx, oracle, relerr, M):
     H, I = 1024, 3584
     G, U, D = _mlp_weights(oracle, H, I, 401)
@@ -143,7 +143,7 @@ def test_mlp_fused_repeat_in_place(qw, ctx, oracle, relerr):
     assert np.array_equal(host(xt), got[0])
 
 
-@pytest.mark.parametrize("M", [1, 32])
+@pytest.mark.parametrize("M", [1, 32, 128])
 def test_mlp_fused_int8(qw, ctx, oracle, relerr, M):
     H, I = 1024, 3584
     G, U, D = _mlp_weights(oracle, H, I, 411)

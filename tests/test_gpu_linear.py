@@ -151,7 +151,7 @@ def _exact_ref(oracle, fmt, W, wobj, xs):
     ("bf16", "bf16"), ("bf16", "f32"), ("bf16", "f16"),
     ("int8", "f16"), ("int8", "bf16"), ("int8", "f32"),
 ])
-@pytest.mark.parametrize("M", [1, 7, 16, 32, 45])
+@pytest.mark.parametrize("M", [1, 7, 16, 32, 45, 100])
 def test_linear_parity(qw, ctx, oracle, relerr, fmt, xname, M):
     f = {"f32": qw.WFMT_F32, "bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
     for si, (N, K) in enumerate(SHAPES):
@@ -212,7 +212,7 @@ def test_linear_deterministic(qw, ctx, oracle):
 # epilogues
 # ----------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M", [1, 20])
+@pytest.mark.parametrize("M", [1, 20, 50])
 @pytest.mark.parametrize("rdt", ["f32", "bf16"])
 def test_residual_epilogue(qw, ctx, oracle, relerr, M, rdt):
     N, K = 1024, 2048                                        # out-proj shape
@@ -230,7 +230,7 @@ def test_residual_epilogue(qw, ctx, oracle, relerr, M, rdt):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "int8", "f32"])
-@pytest.mark.parametrize("M", [1, 9, 32])
+@pytest.mark.parametrize("M", [1, 9, 32, 70])
 def test_norm_prologue(qw, ctx, oracle, relerr, fmt, M):
     """x := RMSNorm(x)*(1+gamma) folded into the projection."""
     N, K = 512, 1024
@@ -277,7 +277,7 @@ def test_split_q_gate(qw, ctx, oracle):
 
 
 @pytest.mark.parametrize("fmt", ["bf16", "int8", "f32"])
-@pytest.mark.parametrize("M", [1, 16, 24])
+@pytest.mark.parametrize("M", [1, 16, 24, 80])
 def test_glu_silu_mul(qw, ctx, oracle, relerr, fmt, M):
     I, H = 3584, 1024
     f = {"f32": qw.WFMT_F32, "bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8}[fmt]
@@ -344,6 +344,44 @@ def test_split_k_handoff_repeatable(qw, ctx, oracle, relerr, fmt):
     xs = host(xt)
     ref = oracle.linear_int8_f64(*w.unpack(), xs) if fmt == "int8" else oracle.linear_f64(oracle.round_bf16(W), xs)
     assert relerr(got[0], ref) <= 2e-5
+
+
+@pytest.mark.parametrize("kernel", ["gemv", "skinny"])
+@pytest.mark.parametrize("M", [2, 70])
+def test_forced_split_k(qw, oracle, relerr, kernel, M):
+    """Cross-workgroup split-K (forced with QW_SKINNY_MIN_ITEMS) on both
+    small-M kernels, with and without token groups, with the RMSNorm sums of
+    squares and a residual riding along: repeated calls bit-identical and
+    equal to the FP64 reference (counters and partials of each group and
+    tile kept apart and re-armed)."""
+    import os
+    os.environ["QW_SKINNY_MIN_ITEMS"] = "1024"
+    os.environ["QW_GEMV"] = "1" if kernel == "gemv" else "0"
+    try:
+        c = qw.Context(0)
+    finally:
+        del os.environ["QW_SKINNY_MIN_ITEMS"]
+        del os.environ["QW_GEMV"]
+    N, K = 1024, 3584
+    W = oracle.normal((N, K), 95, 0.0, 0.02)
+    gam = oracle.normal((K,), 96, 0.0, 0.1)
+    x = oracle.normal((M, K), 97)
+    r = oracle.normal((M, N), 98)
+    w = qw.Weight.pack(c, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    rt = dev(r)
+    ys = torch.empty(5, M, N, device="cuda")
+    for i in range(5):
+        qw.linear(c, w, xt, ys[i], residual=rt, gamma=dev(gam) if M <= 16 else None)
+    torch.cuda.synchronize()
+    got = ys.cpu().numpy()
+    assert (got == got[0][None]).all()
+    xs = host(xt)
+    xin = oracle.rmsnorm_f64(xs, gam) if M <= 16 else xs
+    ref = xin @ oracle.round_bf16(W).astype(np.float64).T + r
+    assert relerr(got[0], ref) <= (1e-2 if M <= 16 else 2e-5)
+    torch.cuda.synchronize()
+    c.close()
 
 
 # ----------------------------------------------------------------------------
