@@ -517,6 +517,10 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
                         !(M == 1 && gamma_call && W->wf == QW_WFMT_BF16) && (M <= 4 || tiles_per_wg <= 4);
     if (direct)
         nw = qwk::gemv_waves(W->wf, M, W->glu != 0, argmax, ep && (ep->flags & QW_EP_NORM_X), nw);
+    if (direct && argmax) {  // the GEMV's argmax items may be runs of consecutive tiles
+        const int rows = 16 * qwk::gemv_argmax_tiles(W->wf);
+        a.n_groups = (W->N + rows - 1) / rows;
+    }
     // the activation slice of a split must fit the workgroup's LDS
     while (!direct && qwk::skinny_lds_bytes(W->wf, (int)xdt, M, (W->ksteps + S - 1) / S) > qwk::kSkinnyMaxLds) {
         if (argmax || S >= W->ksteps) return fail(ctx, QW_ERR_SHAPE, "K=%d too large for the skinny kernel", W->K);

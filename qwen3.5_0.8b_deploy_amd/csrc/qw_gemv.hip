@@ -38,6 +38,10 @@
 
 namespace qwk {
 
+// consecutive 16-row tiles per argmax item: two for INT8 (a 16 KB tile is
+// too little work per cross-wave reduction), one for BF16 (measured)
+template <int WF> struct ArgmaxTiles { static constexpr int v = WF == WF_I8 ? 2 : 1; };
+
 // Activation fragments of one k-step as loaded: KE elements of XDT for each
 // of the CT token tiles of the lane, and the matching (1 + gamma) weights
 // (shared by the tiles).
@@ -144,7 +148,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // activation fragments and RMSNorm weights would crowd the registers
     constexpr int U = ((GAM && WF == WF_I8) || (CT == 2 && (GAM || WF == WF_I8))) ? 2 : 4;
     constexpr int KE = WTraits<WF>::KE;
-    constexpr int RT = GLU ? 2 : 1;
+    // tiles per item: a gate/up pair (GLU), or ArgmaxTiles consecutive tiles
+    // for the argmax (fewer per-item reductions for the many-tile lm_head)
+    constexpr int RT = GLU ? 2 : (ARGMAX ? ArgmaxTiles<WF>::v : 1);
     constexpr int F = RT * CT;
     __shared__ f32x4 red[NW][F][64];
     __shared__ float red_ss[NW][16 * CT];
@@ -166,11 +172,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     wave_range<NW>(ks0, ks1, wave_id, kb, kend);
     const int kb0 = kb;
 
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * RT * a.ksteps * 1024u));
+    // weight tiles that exist (the last argmax pair may have only one)
+    const int n_tiles = ARGMAX ? (a.N + 15) / 16 : a.n_groups * RT;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)n_tiles * a.ksteps * 1024u));
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(GAM ? (const void*)a.gamma : a.x, GAM ? (uint32_t)a.K * 4u : 0u);
     const __amdgpu_buffer_rsrc_t sr =
-        make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)a.n_groups * RT * 64u : 0u);
+        make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)n_tiles * 64u : 0u);
     const int res_size = a.res_dt == DT_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t rr =
         make_rsrc(want_res ? a.res : a.x, want_res ? (uint32_t)((uint64_t)a.M * a.ld_res * res_size) : 0u);
@@ -355,6 +363,27 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         }
         if (!finish) continue;
 
+        if constexpr (ARGMAX) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const int m = ct * 16 + r;
+                if (m >= a.M) continue;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int o = (grp_c * RT + rt) * 16 + g * 4;  // first of this lane's 4 rows
+                    f32x4 v = acc[rt][ct];
+                    if (a.scales) v *= as_f32x4(e.sc[rt]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (o + i < a.N) {
+                            const unsigned long long kk = argmax_key(v[i], (uint32_t)(o + i));
+                            best[ct] = kk > best[ct] ? kk : best[ct];
+                        }
+                    }
+                }
+            }
+            continue;
+        }
         const int o = grp_c * 16 + g * 4;  // first of this lane's 4 logical rows
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) {
@@ -374,17 +403,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                 v = acc[0][ct] * inv;
                 if (a.scales) v *= as_f32x4(e.sc[0]);
             }
-            if constexpr (ARGMAX) {
-                if (m < a.M) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (o + i < a.N) {
-                            const unsigned long long kk = argmax_key(v[i], (uint32_t)(o + i));
-                            best[ct] = kk > best[ct] ? kk : best[ct];
-                        }
-                    }
-                }
-            } else {
+            {
                 if (m >= a.M || o >= a.N) continue;
                 if (a.vec_store) {
                     if (want_res) v += epi_res(a.res_dt, e.res32[ct], e.res16[ct]);
@@ -458,6 +477,8 @@ int gemv_waves(int wf, int M, bool glu, bool argmax, bool norm, int nw_wanted) {
     if (nw_wanted >= 8) return norm ? 4 : 8;
     return 4;
 }
+
+int gemv_argmax_tiles(int wf) { return wf == WF_I8 ? ArgmaxTiles<WF_I8>::v : ArgmaxTiles<WF_BF16>::v; }
 
 bool gemv_supported(int wf, int xdt, int M, bool norm) {
     if (M < 1 || M > 32 || (M > 16 && norm)) return false;

@@ -50,6 +50,8 @@ size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split);
 // Register-direct decode GEMV (qw_gemv.hip): M <= 32; BF16 weights with BF16
 // activations, INT8 weights with F16 or BF16 activations.
 bool gemv_supported(int wf, int xdt, int M, bool norm);
+// consecutive 16-row tiles per argmax item of the GEMV
+int gemv_argmax_tiles(int wf);
 // workgroup size (waves) the GEMV instantiates closest to the one wanted
 int gemv_waves(int wf, int M, bool glu, bool argmax, bool norm, int nw_wanted);
 hipError_t launch_gemv(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
