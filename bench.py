@@ -325,18 +325,25 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         s = torch.rand(n, generator=torch.Generator(device="cuda").manual_seed(n + k), device="cuda") * (2e-2 - 1e-3) + 1e-3
         return q, s
 
+    # Projections that read the same activation are stacked into one weight
+    # (qw_weight_pack_concat): QKV+Z of a Gated-DeltaNet layer, Q+gate/K/V of
+    # a full-attention layer -- one launch each.
     layers = []
     wbytes = 0
     for li in range(LAYERS):
         L = {}
         if li in LINEAR_LAYERS:
-            shapes = {"qkv": (6144, 1024), "z": (2048, 1024), "out": (1024, 2048)}
+            ins = [(6144, 1024), (2048, 1024)]
         else:
-            shapes = {"qg": (4096, 1024), "k": (512, 1024), "v": (512, 1024), "o": (1024, 2048)}
-        for name, (n, k) in shapes.items():
-            q, s = i8(n, k)
-            L[name] = qw.Weight.pack_device(ctx, q, qw.WFMT_INT8, scales=s)
-            wbytes += n * k + n * 4
+            ins = [(4096, 1024), (512, 1024), (512, 1024)]
+        qs, ss = zip(*[i8(n, k) for n, k in ins])
+        L["in"] = qw.Weight.pack_concat_device(ctx, list(qs), qw.WFMT_INT8, scales=list(ss))
+        L["n_in"] = sum(n for n, _ in ins)
+        wbytes += sum(n * k + n * 4 for n, k in ins)
+        q, s_ = i8(1024, 2048)
+        L["out"] = qw.Weight.pack_device(ctx, q, qw.WFMT_INT8, scales=s_)
+        wbytes += 1024 * 2048 + 1024 * 4
+        del qs, ss
         qg_, sg_ = i8(I, H)
         qu_, su_ = i8(I, H)
         L["gu"] = qw.Weight.pack_glu_device(ctx, qg_, qu_, qw.WFMT_INT8, sg_, su_)
@@ -348,23 +355,14 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
     for M in (1, 32, 128):
         xa = randn(M, H, dtype=torch.float16)
         att = randn(M, 2048, dtype=torch.float16)            # attention-core stand-in
-        big = torch.empty(M, 6144, device="cuda", dtype=torch.float16)
-        z = torch.empty(M, 2048, device="cuda", dtype=torch.float16)
+        big = torch.empty(M, 8192, device="cuda", dtype=torch.float16)
         hmid = torch.empty(M, I, device="cuda", dtype=torch.float16)
-        kv = torch.empty(M, 512, device="cuda", dtype=torch.float16)
         res = randn(M, H, dtype=torch.float16)
 
         def body():
-            for li, L in enumerate(layers):
-                if "qkv" in L:
-                    qw.linear(ctx, L["qkv"], xa, big)
-                    qw.linear(ctx, L["z"], xa, z)
-                    qw.linear(ctx, L["out"], att, res, residual=res)
-                else:
-                    qw.linear(ctx, L["qg"], xa, big[:, :4096])
-                    qw.linear(ctx, L["k"], xa, kv)
-                    qw.linear(ctx, L["v"], xa, kv)
-                    qw.linear(ctx, L["o"], att, res, residual=res)
+            for L in layers:
+                qw.linear(ctx, L["in"], xa, big[:, :L["n_in"]])
+                qw.linear(ctx, L["out"], att, res, residual=res)
                 qw.linear(ctx, L["gu"], xa, hmid)
                 qw.linear(ctx, L["down"], hmid, res, residual=res)
         g = graphed(qw, ctx, stream, body)

@@ -98,6 +98,18 @@ qw_status qw_weight_pack_device(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfm
 qw_status qw_weight_pack_glu_device(qw_ctx* ctx, const void* gate, const void* up, qw_dtype src,
                                     qw_wfmt dst, int N, int K, const float* gate_scales,
                                     const float* up_scales, qw_weight** out);
+/* Several projections of the same input stacked into one weight: part i
+ * (W_i[N_i][K], host or device source, optional per-row INT8 scales) takes
+ * output rows [N_0 + ... + N_{i-1}, +N_i) of W[sum N_i][K].  One qw_linear
+ * then computes all parts in one launch (e.g. the Gated-DeltaNet in_proj_qkv,
+ * in_proj_z, in_proj_a and in_proj_b of language_linear_attn.cpp:136-168, or
+ * the full-attention q/k/v projections of language_full_attn.cpp:127-156);
+ * the caller reads part i at column offset N_0 + ... + N_{i-1} of y.  Every
+ * part but the last must have a multiple of 16 rows. */
+qw_status qw_weight_pack_concat(qw_ctx* ctx, int parts, const void* const* ws, const int* Ns, qw_dtype src,
+                                qw_wfmt dst, int K, const float* const* scales, qw_weight** out);
+qw_status qw_weight_pack_concat_device(qw_ctx* ctx, int parts, const void* const* ws, const int* Ns, qw_dtype src,
+                                       qw_wfmt dst, int K, const float* const* scales, qw_weight** out);
 /* Borrow: build a weight object over device memory already in packed order
  * (e.g. a tied embedding shared with the lm_head, as
  * CudaLMHead::set_weight_bf16_ptr borrows, lm_head_cuda.cu:189-196).  The

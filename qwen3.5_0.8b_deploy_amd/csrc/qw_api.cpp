@@ -276,10 +276,13 @@ static qw_status check_pack_args(qw_ctx* ctx, const void* w, qw_dtype src, qw_wf
     return QW_OK;
 }
 
-// Pack one matrix (host or device source) into physical tiles t*tile_mul+tile_add.
+// Pack one matrix of `rows` rows (host or device source) into physical tiles
+// tile_off + t*tile_mul + tile_add (rows 0 = all of W).
 static qw_status pack_one(qw_ctx* ctx, qw_weight* W, const void* src_ptr, qw_dtype src,
-                          const float* src_scales, int tile_mul, int tile_add, bool on_device) {
-    const size_t bytes = (size_t)W->N * W->K * dsize(src);
+                          const float* src_scales, int tile_mul, int tile_add, bool on_device,
+                          int rows = 0, int tile_off = 0) {
+    if (rows == 0) rows = W->N;
+    const size_t bytes = (size_t)rows * W->K * dsize(src);
     const void* dsrc = src_ptr;
     const float* dscales = src_scales;
     void* stage = nullptr;
@@ -291,15 +294,16 @@ static qw_status pack_one(qw_ctx* ctx, qw_weight* W, const void* src_ptr, qw_dty
         e = hipMemcpy(stage, src_ptr, bytes, hipMemcpyHostToDevice);
         dsrc = stage;
         if (e == hipSuccess && src == QW_I8) {
-            e = hipMalloc(&stage_s, (size_t)W->N * sizeof(float));
+            e = hipMalloc(&stage_s, (size_t)rows * sizeof(float));
             if (e == hipSuccess)
-                e = hipMemcpy(stage_s, src_scales, (size_t)W->N * sizeof(float), hipMemcpyHostToDevice);
+                e = hipMemcpy(stage_s, src_scales, (size_t)rows * sizeof(float), hipMemcpyHostToDevice);
             dscales = stage_s;
         }
     }
     if (e == hipSuccess)
-        e = qwk::launch_pack(dsrc, (int)src, W->wf, dscales, W->N, W->K, W->packed, W->scales,
-                             tile_mul, tile_add, 0);
+        e = qwk::launch_pack(dsrc, (int)src, W->wf, dscales, rows, W->K,
+                             W->packed + (size_t)tile_off * W->ksteps * 1024,
+                             W->scales ? W->scales + (size_t)tile_off * 16 : nullptr, tile_mul, tile_add, 0);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (stage) hipFree(stage);
     if (stage_s) hipFree(stage_s);
@@ -342,6 +346,47 @@ static qw_status pack_glu_impl(qw_ctx* ctx, const void* gate, const void* up, qw
     }
     *out = W;
     return QW_OK;
+}
+
+static qw_status pack_concat_impl(qw_ctx* ctx, int parts, const void* const* ws, const int* Ns, qw_dtype src,
+                                  qw_wfmt dst, int K, const float* const* scales, qw_weight** out, bool on_device) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!out) return fail(ctx, QW_ERR_NULL, "out is NULL");
+    *out = nullptr;
+    if (parts < 1 || !ws || !Ns) return fail(ctx, QW_ERR_NULL, "parts, ws and Ns are required");
+    int64_t N = 0;
+    for (int i = 0; i < parts; ++i) {
+        qw_status s = check_pack_args(ctx, ws[i], src, dst, Ns[i], K, scales ? scales[i] : nullptr);
+        if (s != QW_OK) return s;
+        if (i + 1 < parts && Ns[i] % 16 != 0)
+            return fail(ctx, QW_ERR_SHAPE, "part %d has %d rows: all parts but the last need a multiple of 16", i, Ns[i]);
+        N += Ns[i];
+    }
+    if (N > (1 << 30)) return fail(ctx, QW_ERR_SHAPE, "too many rows");
+    hipSetDevice(ctx->device);
+    qw_weight* W = nullptr;
+    qw_status s = alloc_weight(ctx, dst, (int)N, K, 0, &W);
+    if (s != QW_OK) return s;
+    int tile = 0;
+    for (int i = 0; i < parts; ++i) {
+        if ((s = pack_one(ctx, W, ws[i], src, scales ? scales[i] : nullptr, 1, 0, on_device, Ns[i], tile)) != QW_OK) {
+            qw_weight_free(W);
+            return s;
+        }
+        tile += (Ns[i] + 15) / 16;
+    }
+    *out = W;
+    return QW_OK;
+}
+
+qw_status qw_weight_pack_concat(qw_ctx* ctx, int parts, const void* const* ws, const int* Ns, qw_dtype src,
+                                qw_wfmt dst, int K, const float* const* scales, qw_weight** out) {
+    return pack_concat_impl(ctx, parts, ws, Ns, src, dst, K, scales, out, false);
+}
+
+qw_status qw_weight_pack_concat_device(qw_ctx* ctx, int parts, const void* const* ws, const int* Ns, qw_dtype src,
+                                       qw_wfmt dst, int K, const float* const* scales, qw_weight** out) {
+    return pack_concat_impl(ctx, parts, ws, Ns, src, dst, K, scales, out, true);
 }
 
 qw_status qw_weight_pack(qw_ctx* ctx, const void* w, qw_dtype src, qw_wfmt dst, int N, int K,

@@ -28,7 +28,7 @@ EP_RESIDUAL, EP_NORM_X, EP_SPLIT = 1, 2, 4
 EXPORTS = [
     "qw_init", "qw_destroy", "qw_workspace_query", "qw_last_error", "qw_status_string",
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
-    "qw_weight_pack_glu_device", "qw_weight_wrap_packed",
+    "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
@@ -78,6 +78,8 @@ def lib():
         "qw_weight_pack_glu": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, pp], _i),
         "qw_weight_pack_device": ([_vp, _vp, _i, _i, _i, _i, _vp, pp], _i),
         "qw_weight_pack_glu_device": ([_vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, pp], _i),
+        "qw_weight_pack_concat": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp, pp], _i),
+        "qw_weight_pack_concat_device": ([_vp, _i, _vp, _vp, _i, _i, _i, _vp, pp], _i),
         "qw_weight_wrap_packed": ([_vp, _vp, _vp, _i, _i, _i, pp], _i),
         "qw_weight_fold_norm": ([_vp, _vp, _vp, _vp], _i),
         "qw_weight_free": ([_vp], _i),
@@ -232,6 +234,38 @@ class Weight:
             ctx.handle, gate.data_ptr(), up.data_ptr(), code, fmt, N, K,
             None if gate_scales is None else gate_scales.data_ptr(),
             None if up_scales is None else up_scales.data_ptr(), ctypes.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def pack_concat(cls, ctx, parts, fmt, scales=None, src_code=None):
+        """Stack host matrices W_i[N_i][K] (same dtype) into one weight."""
+        arrs, src = [], None
+        for w in parts:
+            w, src = cls._src(w, src_code)
+            arrs.append(w)
+        K = arrs[0].shape[1]
+        ptrs = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+        Ns = (ctypes.c_int * len(arrs))(*[a.shape[0] for a in arrs])
+        scs = None
+        if scales is not None:
+            keep = [np.ascontiguousarray(v, dtype=np.float32) for v in scales]
+            scs = (ctypes.c_void_p * len(keep))(*[v.ctypes.data for v in keep])
+        h = ctypes.c_void_p()
+        ctx.check(lib().qw_weight_pack_concat(ctx.handle, len(arrs), ptrs, Ns, src, fmt, K, scs, ctypes.byref(h)))
+        return cls(ctx, h)
+
+    @classmethod
+    def pack_concat_device(cls, ctx, parts, fmt, scales=None):
+        """Stack torch device matrices W_i[N_i][K] (scales: device float32 per part, INT8)."""
+        import torch
+        code = I8 if parts[0].dtype == torch.int8 else _torch_code(parts[0])
+        K = parts[0].shape[1]
+        ptrs = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
+        Ns = (ctypes.c_int * len(parts))(*[p.shape[0] for p in parts])
+        scs = None if scales is None else (ctypes.c_void_p * len(scales))(*[v.data_ptr() for v in scales])
+        h = ctypes.c_void_p()
+        ctx.check(lib().qw_weight_pack_concat_device(ctx.handle, len(parts), ptrs, Ns, code, fmt, K, scs,
+                                                     ctypes.byref(h)))
         return cls(ctx, h)
 
     def fold_norm(self, gamma, stream=None):

@@ -441,3 +441,41 @@ def test_fold_norm_mlp_and_errors(qw, ctx, oracle, relerr):
         qw.linear(ctx, dn, torch.empty(1, I, device="cuda", dtype=torch.bfloat16),
                   torch.empty(1, H, device="cuda"), norm=True)
     assert e.value.status == qw.ERR_NULL
+
+
+# ----------------------------------------------------------------------------
+# stacked projections (qw_weight_pack_concat)
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize("fmt", ["bf16", "int8"])
+@pytest.mark.parametrize("M", [1, 40])
+def test_pack_concat(qw, ctx, oracle, relerr, fmt, M):
+    """in_proj_qkv + in_proj_z + in_proj_a + in_proj_b of a Gated-DeltaNet
+    layer stacked into one weight: one launch, each part equal to its own
+    projection (bitwise for the same kernel path) and to the FP64 reference."""
+    K = 1024
+    Ns = [6144, 2048, 16, 16]
+    Ws = [oracle.normal((n, K), 900 + i, 0.0, 0.02) for i, n in enumerate(Ns)]
+    f = qw.WFMT_BF16 if fmt == "bf16" else qw.WFMT_INT8
+    xt = dev(oracle.normal((M, K), 910), torch.bfloat16 if fmt == "bf16" else torch.float16)
+    cat = qw.Weight.pack_concat(ctx, Ws, f)
+    y = torch.empty(M, sum(Ns), device="cuda")
+    qw.linear(ctx, cat, xt, y)
+    torch.cuda.synchronize()
+    xs = host(xt)
+    o = 0
+    for i, (n, W) in enumerate(zip(Ns, Ws)):
+        w1 = qw.Weight.pack(ctx, W, f)
+        yi = torch.empty(M, n, device="cuda")
+        qw.linear(ctx, w1, xt, yi)
+        torch.cuda.synchronize()
+        part = host(y)[:, o:o + n]
+        if fmt == "bf16":
+            ref = oracle.linear_f64(oracle.round_bf16(W), xs)
+            assert relerr(part, ref) <= 2e-5
+        else:
+            ref = oracle.linear_int8_f64(*w1.unpack(), xs)
+            assert relerr(part, ref) <= 1e-3
+        o += n
+    with pytest.raises(qw.QwError) as e:
+        qw.Weight.pack_concat(ctx, [Ws[2][:10], Ws[3]], f)   # 10 rows: not a multiple of 16
+    assert e.value.status == qw.ERR_SHAPE
