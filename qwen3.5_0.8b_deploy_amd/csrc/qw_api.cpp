@@ -29,7 +29,9 @@ struct qw_ctx {
     bool gemv = true;        // register-direct GEMV for M <= 32 (QW_GEMV=0: skinny kernel)
     int gemm_min_m = kGemmMinM;  // tokens from which BF16 calls may use the MFMA GEMM
     bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
-    int gemm_tile_m = 128;       // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256)
+    int gemm_tile_m = 0;         // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256; 0 = by shape)
+    int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
+    int gemm_pingpong = 0;       // 8-wave blocks: ping-pong schedule (QW_GEMM_PINGPONG=1)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -164,7 +166,9 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
-    if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;
+    if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
+    if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
+    if (const char* v = getenv("QW_GEMM_PINGPONG")) c->gemm_pingpong = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;
@@ -658,8 +662,13 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ld
     a.K = W->K;
     a.N = W->N;
     a.nblk_n = (W->phys_tiles * 16 + 255) / 256;
-    a.tile_m = ctx->gemm_tile_m;
+    // 256-token blocks (8 waves, half the L2->LDS traffic per FLOP of the
+    // 128-token block) once they alone fill the 256 CUs; 128-token blocks
+    // (two workgroups per CU) for fewer tokens
+    a.tile_m = ctx->gemm_tile_m ? ctx->gemm_tile_m : (a.nblk_n * ((M + 255) / 256) >= 256 ? 256 : 128);
     a.nblk_m = (M + a.tile_m - 1) / a.tile_m;
+    a.waves = a.tile_m == 256 ? ctx->gemm_waves : 4;
+    a.pingpong = ctx->gemm_pingpong;
     a.flags = ep ? (ep->flags & ~(unsigned)QW_EP_NORM_X) : 0u;
     if (ep && (ep->flags & QW_EP_RESIDUAL)) {
         a.res = ep->residual;

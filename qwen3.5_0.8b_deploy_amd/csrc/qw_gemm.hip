@@ -1,12 +1,19 @@
 // qw_gemm.hip -- LDS double-buffered MFMA GEMM for gfx950 (prefill and
 // large-batch decode):  y[m][n] = sum_k W[n][k] * x[m][k]  (+ epilogue).
 //
-// Tiling.  A workgroup (4 waves) computes 256 weight rows x BM tokens (BM =
-// 128 by default, 256 optional); each wave a 128 x BM/2 quadrant as 4 x BM/64
-// blocks of v_mfma_f32_32x32x16_bf16 (weights are the A operand, tokens the B
-// operand; FP32 accumulators).  K advances in blocks of one 32-deep k-step.
-// With BM = 128 two workgroups share a CU, so one wave's barrier and LDS
-// waits are covered by the other's MFMAs.
+// Tiling.  A workgroup computes 256 weight rows x BM tokens with
+// v_mfma_f32_32x32x16_bf16 (weights are the A operand, tokens the B operand;
+// FP32 accumulators); K advances in blocks of one 32-deep k-step.  Shapes:
+//   - BM = 256, 8 waves (default once the 256-token blocks fill the chip):
+//     each wave 128 rows x 64 tokens, two waves per SIMD, half the
+//     L2->LDS bytes per FLOP of the 128-token block;
+//   - BM = 128, 4 waves (fewer tokens): each wave 128 x 64; two workgroups
+//     share a CU, so one's barrier and LDS waits are covered by the other;
+//   - BM = 256, 4 waves: each wave 128 x 128 (one wave per SIMD).
+// The 8-wave block also has a ping-pong schedule (PP): the two waves of a
+// SIMD alternate between a run of MFMAs and the memory work of the next
+// block.  Measured on MI355X (M = 16384, random BF16 operands) the plain
+// 8-wave schedule is as fast or faster, so PP is opt-in.
 //
 // Loads.  Both operands reach LDS through direct buffer->LDS loads
 // (buffer_load_dwordx4 ... lds): one wave instruction moves one 1 KB unit.
@@ -17,7 +24,8 @@
 // Three (BM = 128: 3 x 24 KB) or four (BM = 256: 4 x 32 KB) LDS stages keep
 // the next K-blocks' loads in flight while one is multiplied; a wave waits
 // only for its own loads of the block it is about to use, then one barrier
-// per block publishes them.  The loads of a block are issued one per MFMA
+// per block publishes them, placed mid-block so that no barrier sits between
+// a fragment read and its MFMAs.  The loads of a block are issued one per MFMA
 // pair so the matrix pipe never waits on a burst of load issues.
 //
 // Epilogue.  In a 32-row weight block, rows i and i+16 of a token land in the
@@ -47,14 +55,17 @@ constexpr int G_EPI_PITCH = 68;            // epilogue LDS row pitch (floats): 6
 // Per token-tile height BM: 1 KB units per stage (16 weight units + BM/16
 // activation units of one 32-deep k-step), units each of the 4 waves moves,
 // LDS pipeline depth (BM = 128 leaves room for two workgroups per CU).
-template <int BM> struct GTile {
-    static constexpr int MB = BM / 64;                // 32-token MFMA blocks per wave
+template <int BM, int NW> struct GTile {
+    static constexpr int WM = NW / 2;                 // waves along the tokens (2 along the rows)
+    static constexpr int WT = BM / WM;                // tokens per wave
+    static constexpr int MB = WT / 32;                // 32-token MFMA blocks per wave
     static constexpr int UNITS = 16 + BM / 16;
-    static constexpr int UPW = UNITS / 4;
+    static constexpr int UPW = UNITS / NW;
     static constexpr int STAGE = UNITS * 1024;
     static constexpr int NS = BM == 256 ? 4 : 3;
+    static_assert(MB >= 1 && UPW >= 1 && UNITS % NW == 0, "tile shape");
     static constexpr size_t lds_bytes() {
-        const size_t epi = 4 * (size_t)(BM / 2) * G_EPI_PITCH * sizeof(float);
+        const size_t epi = (size_t)NW * WT * G_EPI_PITCH * sizeof(float);
         const size_t pipe = (size_t)NS * STAGE;
         return epi > pipe ? epi : pipe;
     }
@@ -97,17 +108,22 @@ __device__ __forceinline__ void gemm_store_slow(const GemmArgs& a, int m, int ro
     }
 }
 
-template <bool GLU, bool ARGMAX, int BM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BM == 256 ? 1 : 2, BM == 256 ? 1 : 2)))
+template <bool GLU, bool ARGMAX, int BM, int NW, bool PP>
+__global__ __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(BM == 256 && NW == 4 ? 1 : 2, BM == 256 && NW == 4 ? 1 : 2)))
 void gemm_bf16_kernel(GemmArgs a) {
-    using T = GTile<BM>;
-    constexpr int MB = T::MB, UPW = T::UPW, G_NS = T::NS, G_STAGE = T::STAGE;
+    using T = GTile<BM, NW>;
+    constexpr int MB = T::MB, UPW = T::UPW, G_NS = T::NS, G_STAGE = T::STAGE, WM = T::WM, WT = T::WT;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ unsigned long long best_s[2][BM];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wn = wave >> 1, wm = wave & 1;   // quadrant of this wave
+    // 128 rows x WT tokens of this wave.  Ping-pong: waves w and w + 4 share a
+    // SIMD (and a row half); group g = w / 4 selects the token quarters.
+    const int pg = wave >> 2;
+    const int wn = PP ? (wave & 3) >> 1 : wave / WM;
+    const int wm = PP ? ((wave & 1) | (pg << 1)) : wave % WM;
 
     // XCD-aware order: consecutive workgroup ids go to different XCDs; give
     // each XCD a contiguous range of tiles (M fastest) so the tiles that
@@ -135,23 +151,25 @@ void gemm_bf16_kernel(GemmArgs a) {
     // stage is weight tile u (u < 16) or activation token group u - 16, and
     // lands at byte u*1024.  Offsets for K-block 0 are computed once; K-block
     // kb adds kb*1024 (weights) or kb*64 bytes (activations).
-    uint32_t vbase[UPW];
+    // The buffer and per-block stride of each unit are chosen once (wave-
+    // uniform selects), so issuing a load inside the K-loop is branch-free.
+    uint32_t vbase[UPW], vstep[UPW];
+    __amdgpu_buffer_rsrc_t rsq[UPW];
 #pragma unroll
     for (int q = 0; q < UPW; ++q) {
         const int u = wave * UPW + q;
-        if (u < 16) {
-            const int pt = nt0 + u;
-            vbase[q] = pt < a.n_tiles ? (uint32_t)(pt * a.ksteps * 1024 + lane * 16) : OOB;
-        } else {
-            const int row = m0 + (u - 16) * 16 + (lane & 15);
-            vbase[q] = row < a.M ? (uint32_t)((row * a.ldx + (lane >> 4) * 8) * 2) : OOB;
-        }
+        const bool isw = u < 16;
+        const int pt = nt0 + u;
+        const int row = m0 + (u - 16) * 16 + (lane & 15);
+        const uint32_t wo = pt < a.n_tiles ? (uint32_t)(pt * a.ksteps * 1024 + lane * 16) : OOB;
+        const uint32_t xo = row < a.M ? (uint32_t)((row * a.ldx + (lane >> 4) * 8) * 2) : OOB;
+        vbase[q] = isw ? wo : xo;
+        vstep[q] = isw ? 1024u : 64u;
+        rsq[q] = isw ? wrs : xrs;
     }
     auto dma = [&](int kb, int q) {
-        const int u = wave * UPW + q;
-        uint8_t* dst = lds + (kb % G_NS) * G_STAGE + u * 1024;
-        if (u < 16) lds_dma16(wrs, dst, vbase[q] + (uint32_t)kb * 1024u);
-        else lds_dma16(xrs, dst, vbase[q] + (uint32_t)kb * 64u);
+        uint8_t* dst = lds + (kb % G_NS) * G_STAGE + (wave * UPW + q) * 1024;
+        lds_dma16(rsq[q], dst, vbase[q] + (uint32_t)kb * vstep[q]);
     };
 
     f32x16 acc[4][MB];
@@ -180,45 +198,134 @@ void gemm_bf16_kernel(GemmArgs a) {
         }
     };
 
-    // G_NS-stage pipeline over K-blocks: blocks kb+1 .. kb+G_NS-1 are loaded
-    // while kb is multiplied.  A wave waits only for its own loads of block
-    // kb (vector-memory counters retire in order), then one barrier publishes
-    // the block to all waves and frees the stage of block kb-1.  Inside a
-    // block the fragments of the next sub-step are read while the current
-    // sub-step's 16 MFMAs run, and the block's global->LDS loads are issued
-    // one per MFMA pair so the matrix pipe never waits on a burst of issues.
+    // G_NS-stage pipeline over K-blocks (two 16-deep halves each).  Block kb
+    // runs as: read the fragments of half 1; MFMAs of half 0; wait for this
+    // wave's loads of block kb+1 and one barrier, which publishes kb+1 and
+    // proves every wave has consumed block kb-1 (its half-1 MFMAs were
+    // issued); read the fragments of kb+1 half 0; MFMAs of half 1, with the
+    // global->LDS loads of block kb+G_NS-1 (into the stage of kb-1) issued one
+    // per MFMA pair.  LDS read latency is covered by the other half's MFMAs
+    // and the barrier never sits between a fragment read and its use.
+    auto wait_loads = [&](int later) {  // at most `later` blocks of loads may stay in flight
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(2 * UPW));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_wait(UPW));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    };
 #pragma unroll
     for (int s0 = 0; s0 < G_NS - 1; ++s0)
         if (s0 < nkb) {
 #pragma unroll
             for (int q = 0; q < UPW; ++q) dma(s0, q);
         }
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int later = min(G_NS - 2, nkb - 1 - kb);  // blocks issued after kb
-        if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(2 * UPW));
-        else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_wait(UPW));
-        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    if constexpr (PP) {
+        // Ping-pong over K-blocks.  Each block j takes two phases separated
+        // by barriers: in phase 2j group 0 multiplies block j (fragments in
+        // registers) while group 1 reads block j's fragments and issues its
+        // loads of block j+NS-1; in phase 2j+1 group 1 multiplies block j
+        // while group 0 reads block j+1 and issues its loads of block j+NS.
+        // The two waves of a SIMD thus alternate between an uninterrupted
+        // run of 16 MFMAs and the memory work, so load issue and LDS read
+        // latency never sit inside an MFMA run.  Stage reuse: block j+NS-1
+        // (group 1, phase 2j) and j+NS (group 0, phase 2j+1) land in stages
+        // whose last reader finished before the barrier that ends phase
+        // 2j-1 resp. 2j.  Before the barrier ending phase 2j every wave has
+        // its own loads of block j+1 complete, so group 0 may read it next.
+        auto issue = [&](int blk) {
+            if (blk < nkb) {
+#pragma unroll
+                for (int q = 0; q < UPW; ++q) dma(blk, q);
+            }
+        };
+        auto compute = [&]() {
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4 * MB; ++i)
+                    acc[i / MB][i % MB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[h][i / MB], B[h][i % MB],
+                                                                                acc[i / MB][i % MB], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+        };
+        auto read_block = [&](int blk) {
+            const uint8_t* st = lds + (blk % G_NS) * G_STAGE;
+            read_frags(st, 0, A[0], B[0]);
+            read_frags(st, 1, A[1], B[1]);
+        };
+        // prologue: group 0 issues blocks 0..NS-1, group 1 blocks 0..NS-2
+#pragma unroll
+        for (int s0 = 0; s0 < G_NS - 1; ++s0) issue(s0);
+        if (pg == 0) issue(G_NS - 1);
+        if (pg == 0) wait_loads(min(G_NS - 1, nkb - 1));
+        else wait_loads(min(G_NS - 2, nkb - 1));
         __syncthreads();
-        const uint8_t* st = lds + (kb % G_NS) * G_STAGE;
-        const bool more = kb + G_NS - 1 < nkb;
-        read_frags(st, 0, A[0], B[0]);
-        __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (h == 0) read_frags(st, 1, A[1], B[1]);
-#pragma unroll
+        if (pg == 0) read_block(0);
+        for (int j = 0; j < nkb; ++j) {
+            // phase 2j
+            if (pg == 0) {
+                compute();
+            } else {
+                read_block(j);
+                issue(j + G_NS - 1);
+            }
+            // own loads of block j+1 complete (blocks j+2 .. j+NS-1 may remain)
+            wait_loads(min(G_NS - 2, nkb - j - 2));
+            __syncthreads();
+            // phase 2j+1
+            if (pg == 1) {
+                compute();
+            } else if (j + 1 < nkb) {
+                read_block(j + 1);
+                issue(j + G_NS);
+            }
+            __syncthreads();
+        }
+    } else {
+        wait_loads(min(G_NS - 2, nkb - 1));
+        __syncthreads();
+        read_frags(lds, 0, A[0], B[0]);
+        // one K-block; LAST (the final block) has no successor to publish.  The
+        // final block is peeled off so the loop body has a single path: at a
+        // control-flow join the compiler's wait counting would make the half-1
+        // MFMAs wait for the next block's fragment reads.
+        auto kblock = [&](int kb, auto last) {
+            constexpr bool LAST = decltype(last)::value;
+            const uint8_t* st = lds + (kb % G_NS) * G_STAGE;
+            read_frags(st, 1, A[1], B[1]);
+            __builtin_amdgcn_s_setprio(1);
+    #pragma unroll
+            for (int i = 0; i < 4 * MB; ++i)
+                acc[i / MB][i % MB] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0][i / MB], B[0][i % MB], acc[i / MB][i % MB], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+            if constexpr (!LAST) {
+                wait_loads(min(G_NS - 3, nkb - kb - 2));
+                __syncthreads();
+                read_frags(lds + ((kb + 1) % G_NS) * G_STAGE, 0, A[0], B[0]);
+            }
+            const bool more = kb + G_NS - 1 < nkb;
+            __builtin_amdgcn_s_setprio(1);
+    #pragma unroll
             for (int i = 0; i < 4 * MB; ++i) {
                 acc[i / MB][i % MB] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[h][i / MB], B[h][i % MB], acc[i / MB][i % MB], 0, 0, 0);
-                const int q = (h * 4 * MB + i) >> 1;
-                if ((i & 1) && q < UPW) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (more) dma(kb + G_NS - 1, q);
-                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[1][i / MB], B[1][i % MB], acc[i / MB][i % MB], 0, 0, 0);
+                constexpr int per = (4 * MB) / UPW > 0 ? (4 * MB) / UPW : 1;  // MFMAs per load issue
+                if constexpr (!LAST) {
+                    if (i % per == per - 1 && i / per < UPW) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (more) dma(kb + G_NS - 1, i / per);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
                 }
             }
-        }
-        __builtin_amdgcn_s_setprio(0);
+            if constexpr (!LAST && (4 * MB) / UPW == 0) {  // more units than MFMAs: the rest after them
+    #pragma unroll
+                for (int q = 4 * MB; q < UPW; ++q)
+                    if (more) dma(kb + G_NS - 1, q);
+            }
+            __builtin_amdgcn_s_setprio(0);
+        };
+        for (int kb = 0; kb < nkb - 1; ++kb) kblock(kb, std::false_type{});
+        kblock(nkb - 1, std::true_type{});
     }
 
     // ---- epilogue ----
@@ -252,7 +359,7 @@ void gemm_bf16_kernel(GemmArgs a) {
         for (int mb = 0; mb < MB; ++mb) {
             const unsigned long long o = __shfl_xor(best[mb], 32);
             best[mb] = o > best[mb] ? o : best[mb];
-            if (lane < 32) best_s[wn][wm * (BM / 2) + mb * 32 + lane] = best[mb];
+            if (lane < 32) best_s[wn][wm * WT + mb * 32 + lane] = best[mb];
         }
         __syncthreads();
         if (threadIdx.x < BM) {
@@ -272,7 +379,7 @@ void gemm_bf16_kernel(GemmArgs a) {
         }
         __syncthreads();
         if (best_s[0][0] == 1ull) {
-            for (int m = threadIdx.x; m < a.M; m += 256) {
+            for (int m = threadIdx.x; m < a.M; m += NW * 64) {
                 const unsigned long long kk =
                     __hip_atomic_exchange(&a.keys[m], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 a.ids[m] = (int32_t)key_index(kk);
@@ -286,9 +393,9 @@ void gemm_bf16_kernel(GemmArgs a) {
         // coalesced store, and so that the accumulators are only ever indexed
         // with constants.  GLU: the wave's 64 output rows in one pass; plain:
         // its 128 rows in two passes of 64.
-        float* ep = reinterpret_cast<float*>(lds) + wave * ((BM / 2) * G_EPI_PITCH);
+        float* ep = reinterpret_cast<float*>(lds) + wave * (WT * G_EPI_PITCH);
         const int row_base = GLU ? ((nt0 + wn * 8) >> 1) * 16 : (nt0 + wn * 8) * 16;
-        const int tok_base = m0 + wm * (BM / 2);
+        const int tok_base = m0 + wm * WT;
         const bool has_res = (a.flags & EP_RESIDUAL) != 0;
         const bool has_split = (a.flags & EP_SPLIT) != 0;
         const int sp_log = a.split_period > 0 ? 31 - __builtin_clz((unsigned)a.split_period) : 0;
@@ -327,7 +434,7 @@ void gemm_bf16_kernel(GemmArgs a) {
             __builtin_amdgcn_wave_barrier();
             const int c = lane & 15;  // rows 4c .. 4c+3
             const int row = row_base + pass * 64 + 4 * c;
-            for (int it = 0; it < BM / 8; ++it) {
+            for (int it = 0; it < WT / 4; ++it) {
                 const int jj = it * 4 + (lane >> 4);
                 const int m = tok_base + jj;
                 if (m < a.M && row < a.N) {
@@ -355,7 +462,7 @@ void gemm_bf16_kernel(GemmArgs a) {
 }
 
 template <typename Kern>
-static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, size_t lds, hipStream_t st) {
+static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, int threads, size_t lds, hipStream_t st) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
@@ -363,24 +470,27 @@ static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, size_t lds,
         if (e != hipSuccess) return e;
         configured = true;
     }
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, st, a);
+    hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, st, a);
     return hipGetLastError();
 }
 
-template <int BM>
+template <int BM, int NW, bool PP = false>
 static hipError_t launch_bm(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
     const int grid = a.nblk_n * a.nblk_m;
-    const size_t lds = GTile<BM>::lds_bytes();
-    if (argmax) return launch_gemm_k(gemm_bf16_kernel<false, true, BM>, a, grid, lds, stream);
-    if (glu) return launch_gemm_k(gemm_bf16_kernel<true, false, BM>, a, grid, lds, stream);
-    return launch_gemm_k(gemm_bf16_kernel<false, false, BM>, a, grid, lds, stream);
+    const size_t lds = GTile<BM, NW>::lds_bytes();
+    if (argmax) return launch_gemm_k(gemm_bf16_kernel<false, true, BM, NW, PP>, a, grid, NW * 64, lds, stream);
+    if (glu) return launch_gemm_k(gemm_bf16_kernel<true, false, BM, NW, PP>, a, grid, NW * 64, lds, stream);
+    return launch_gemm_k(gemm_bf16_kernel<false, false, BM, NW, PP>, a, grid, NW * 64, lds, stream);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream) {
     if (wf != WF_BF16 || xdt != DT_BF16) return hipErrorInvalidValue;
     if (argmax && glu) return hipErrorInvalidValue;
-    if (a.tile_m == 256 && a.nblk_m == (a.M + 255) / 256) return launch_bm<256>(a, glu, argmax, stream);
-    if (a.tile_m == 128 && a.nblk_m == (a.M + 127) / 128) return launch_bm<128>(a, glu, argmax, stream);
+    if (a.tile_m == 256 && a.nblk_m == (a.M + 255) / 256)
+        return a.waves == 8   ? (a.pingpong ? launch_bm<256, 8, true>(a, glu, argmax, stream)
+                                            : launch_bm<256, 8>(a, glu, argmax, stream))
+                              : launch_bm<256, 4>(a, glu, argmax, stream);
+    if (a.tile_m == 128 && a.nblk_m == (a.M + 127) / 128) return launch_bm<128, 4>(a, glu, argmax, stream);
     return hipErrorInvalidValue;
 }
 

@@ -72,6 +72,8 @@ struct GemmArgs {
     int M, K, N;             // N: logical output rows
     int nblk_n, nblk_m;      // block grid: 256 weight rows x tile_m tokens
     int tile_m;              // tokens per block: 256 or 128
+    int waves;               // waves per workgroup: 4, or 8 (tile_m 256 only)
+    int pingpong;            // 8 waves: alternate MFMA and memory phases between wave pairs
     unsigned flags;
     const void* res;
     int res_dt, ld_res;

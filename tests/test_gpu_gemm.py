@@ -13,16 +13,23 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module")
-def ctx(qw):
+@pytest.fixture(scope="module", params=["128x4", "256x4", "256x8", "256x8pp"])
+def ctx(qw, request):
     """A context that takes the GEMM for every BF16 call from 33 tokens on
-    (the default routing sends small-N shapes to the chunked small-M kernels)."""
+    (the default routing sends small-N shapes to the chunked small-M kernels),
+    with each token-block shape: 128 tokens x 4 waves, 256 x 4, 256 x 8, and
+    256 x 8 with the ping-pong schedule."""
     import os
-    os.environ["QW_GEMM_MIN_M"] = "33"
+    tile, waves = request.param.split("x")
+    pp = waves.endswith("pp")
+    env = {"QW_GEMM_MIN_M": "33", "QW_GEMM_TILE_M": tile, "QW_GEMM_WAVES": waves.rstrip("p"),
+           "QW_GEMM_PINGPONG": "1" if pp else "0"}
+    os.environ.update(env)
     try:
         c = qw.Context(0)
     finally:
-        del os.environ["QW_GEMM_MIN_M"]
+        for k in env:
+            del os.environ[k]
     yield c
     torch.cuda.synchronize()
     c.close()
