@@ -31,7 +31,6 @@ struct qw_ctx {
     bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
     int gemm_tile_m = 0;         // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256; 0 = by shape)
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
-    int gemm_pingpong = 0;       // 8-wave blocks: ping-pong schedule (QW_GEMM_PINGPONG=1)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -168,7 +167,6 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
-    if (const char* v = getenv("QW_GEMM_PINGPONG")) c->gemm_pingpong = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;
@@ -632,9 +630,10 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     return QW_OK;
 }
 
-// MFMA GEMM launch for many tokens (BF16 weights and activations).
+// MFMA GEMM launch for many tokens: BF16 weights with BF16 activations, INT8
+// weights with F16 or BF16 activations.
 static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
-    return W->wf == QW_WFMT_BF16 && xdt == QW_BF16;
+    return qwk::gemm_supported(W->wf, (int)xdt);
 }
 
 // GEMM or 32-token chunks of the small-M kernels.  The 256 x 256 GEMM tile
@@ -649,8 +648,9 @@ static bool use_gemm(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M)
     return (nblk_n >= 16 && M >= 128) || M >= 384;
 }
 
-static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ldx, int M, void* y, qw_dtype ydt,
-                          int ldy, const qw_epilogue* ep, int32_t* ids, float* maxv, hipStream_t stream) {
+static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx, int M, void* y,
+                          qw_dtype ydt, int ldy, const qw_epilogue* ep, int32_t* ids, float* maxv,
+                          hipStream_t stream) {
     qwk::GemmArgs a{};
     a.w = W->packed;
     a.scales = W->scales;
@@ -667,8 +667,7 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ld
     // (two workgroups per CU) for fewer tokens
     a.tile_m = ctx->gemm_tile_m ? ctx->gemm_tile_m : (a.nblk_n * ((M + 255) / 256) >= 256 ? 256 : 128);
     a.nblk_m = (M + a.tile_m - 1) / a.tile_m;
-    a.waves = a.tile_m == 256 ? ctx->gemm_waves : 4;
-    a.pingpong = ctx->gemm_pingpong;
+    a.waves = W->wf == QW_WFMT_INT8_ROWSCALE ? 8 : (a.tile_m == 256 ? ctx->gemm_waves : 4);
     a.flags = ep ? (ep->flags & ~(unsigned)QW_EP_NORM_X) : 0u;
     if (ep && (ep->flags & QW_EP_RESIDUAL)) {
         a.res = ep->residual;
@@ -692,7 +691,7 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, int ld
     a.maxv = maxv;
     if ((uint64_t)W->bytes >= (1ull << 31) || (uint64_t)M * ldx * 2 >= (1ull << 31))
         return fail(ctx, QW_ERR_SHAPE, "operands above 2 GiB are not supported");
-    hipError_t e = qwk::launch_gemm(a, W->wf, QW_BF16, W->glu != 0, ids != nullptr, stream);
+    hipError_t e = qwk::launch_gemm(a, W->wf, (int)xdt, W->glu != 0, ids != nullptr, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "GEMM launch");
     return QW_OK;
 }
@@ -753,15 +752,18 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     if (s != QW_OK) return s;
     if (use_gemm(ctx, W, xdt, M)) {
         const bool norm = ep && (ep->flags & QW_EP_NORM_X);
-        if (!norm) return run_gemm(ctx, W, x, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);
-        // RMSNorm into the workspace, then the GEMM, in token chunks that fit
+        if (!norm) return run_gemm(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);
+        // RMSNorm into the workspace, then the GEMM, in token chunks that fit.
+        // INT8 weights take F16 (their MFMA type: a BF16 copy would add ~1e-3
+        // of rounding error, the whole INT8 tolerance).
+        const qw_dtype ndt = W->wf == QW_WFMT_INT8_ROWSCALE ? QW_F16 : QW_BF16;
         const int chunk = (int)std::min<size_t>((size_t)M, ctx->xnorm_bytes / ((size_t)W->K * 2));
         if (chunk < 1) return fail(ctx, QW_ERR_WORKSPACE, "workspace too small for the RMSNorm-ed activations");
         qw_epilogue e3 = *ep;
         for (int m0 = 0; m0 < M; m0 += chunk) {
             const int mc = std::min(chunk, M - m0);
             const void* xc = static_cast<const uint8_t*>(x) + (size_t)m0 * ldx * dsize(xdt);
-            hipError_t e = qwk::launch_rmsnorm_ld(xc, (int)xdt, ldx, ep->gamma, ep->eps, ctx->xnorm, (int)QW_BF16,
+            hipError_t e = qwk::launch_rmsnorm_ld(xc, (int)xdt, ldx, ep->gamma, ep->eps, ctx->xnorm, (int)ndt,
                                                   W->K, mc, W->K, stream);
             if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
             void* yc = static_cast<uint8_t*>(y) + (size_t)m0 * ldy * dsize(ydt);
@@ -770,7 +772,7 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
                 e3.residual = static_cast<const uint8_t*>(ep->residual) + (size_t)m0 * ldr * dsize(ep->residual_dtype);
             }
             if (ep->flags & QW_EP_SPLIT) e3.y2 = static_cast<uint8_t*>(ep->y2) + (size_t)m0 * ldy * dsize(ydt);
-            s = run_gemm(ctx, W, ctx->xnorm, W->K, mc, yc, ydt, ldy, &e3, nullptr, nullptr, stream);
+            s = run_gemm(ctx, W, ctx->xnorm, ndt, W->K, mc, yc, ydt, ldy, &e3, nullptr, nullptr, stream);
             if (s != QW_OK) return s;
         }
         return QW_OK;
@@ -790,7 +792,8 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     if (!token_ids) return fail(ctx, QW_ERR_NULL, "token_ids is NULL");
     if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
     if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
-    if (use_gemm(ctx, E, hdt, M)) return run_gemm(ctx, E, h, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
+    if (use_gemm(ctx, E, hdt, M))
+        return run_gemm(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
     return run_skinny(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream,
                       kSkinnyMaxM);
 }

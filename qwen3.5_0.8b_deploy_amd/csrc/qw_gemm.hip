@@ -1,19 +1,23 @@
 // qw_gemm.hip -- LDS double-buffered MFMA GEMM for gfx950 (prefill and
 // large-batch decode):  y[m][n] = sum_k W[n][k] * x[m][k]  (+ epilogue).
 //
-// Tiling.  A workgroup computes 256 weight rows x BM tokens with
-// v_mfma_f32_32x32x16_bf16 (weights are the A operand, tokens the B operand;
-// FP32 accumulators); K advances in blocks of one 32-deep k-step.  Shapes:
-//   - BM = 256, 8 waves (default once the 256-token blocks fill the chip):
-//     each wave 128 rows x 64 tokens, two waves per SIMD, half the
-//     L2->LDS bytes per FLOP of the 128-token block;
-//   - BM = 128, 4 waves (fewer tokens): each wave 128 x 64; two workgroups
-//     share a CU, so one's barrier and LDS waits are covered by the other;
-//   - BM = 256, 4 waves: each wave 128 x 128 (one wave per SIMD).
-// The 8-wave block also has a ping-pong schedule (PP): the two waves of a
-// SIMD alternate between a run of MFMAs and the memory work of the next
-// block.  Measured on MI355X (M = 16384, random BF16 operands) the plain
-// 8-wave schedule is as fast or faster, so PP is opt-in.
+// Tiling.  A workgroup computes 256 weight rows x BM tokens with 32 x 32 x 16
+// MFMAs (weights are the A operand, tokens the B operand; FP32
+// accumulators); K advances in blocks of one k-step of the packed weight
+// (32 deep for BF16, 64 for INT8).  Shapes:
+//   - BM = 256, 8 waves (once the 256-token blocks fill the chip): each wave
+//     128 rows x 64 tokens, two waves per SIMD, half the L2->LDS bytes per
+//     FLOP of the 128-token block;
+//   - BM = 128: BF16 with 4 waves (each 128 x 64; two workgroups share a CU,
+//     so one's barrier and LDS waits are covered by the other), INT8 with 8
+//     waves (each 128 x 32);
+//   - BM = 256, 4 waves (BF16): each wave 128 x 128 (one wave per SIMD).
+// Weight formats: BF16 weights use the bf16 MFMA on BF16 activations.  INT8
+// weights (per-row scales) reach LDS as INT8, half the bytes; each lane
+// converts its 8-byte fragment exactly to f16 (qw_device.hpp i8x4_to_f16)
+// for the f16 MFMA, BF16 activations are converted to f16 when read, and the
+// row scale is applied in the epilogue -- y = s * sum q*x, the reference's
+// dequantize-then-multiply.
 //
 // Loads.  Both operands reach LDS through direct buffer->LDS loads
 // (buffer_load_dwordx4 ... lds): one wave instruction moves one 1 KB unit.
@@ -52,17 +56,23 @@ constexpr int G_GROUP_M = 8;               // token blocks per raster group
 constexpr int G_XOFF = 16 * 1024;          // activation region within a stage (after 16 weight units)
 constexpr int G_EPI_PITCH = 68;            // epilogue LDS row pitch (floats): 64 rows + pad
 
-// Per token-tile height BM: 1 KB units per stage (16 weight units + BM/16
-// activation units of one 32-deep k-step), units each of the 4 waves moves,
-// LDS pipeline depth (BM = 128 leaves room for two workgroups per CU).
-template <int BM, int NW> struct GTile {
+// Stage geometry for token-tile height BM, NW waves and weight format WF.  A
+// K-block is one k-step of the packed weight: 32 deep for BF16, 64 for INT8
+// (KSUB 32-deep activation sub-steps).  A stage holds the block's 16 weight
+// units (256 rows) and KSUB * BM/16 activation units; UPW units per wave;
+// NS stages in flight (fewer where the stage is larger or two workgroups
+// share a CU).
+template <int BM, int NW, int WF> struct GTile {
     static constexpr int WM = NW / 2;                 // waves along the tokens (2 along the rows)
     static constexpr int WT = BM / WM;                // tokens per wave
     static constexpr int MB = WT / 32;                // 32-token MFMA blocks per wave
-    static constexpr int UNITS = 16 + BM / 16;
+    static constexpr int KSUB = WF == WF_I8 ? 2 : 1;
+    static constexpr int KSL = 2 * KSUB;              // 16-deep MFMA slices per K-block
+    static constexpr int XU = BM / 16;                // activation units per sub-step
+    static constexpr int UNITS = 16 + KSUB * XU;
     static constexpr int UPW = UNITS / NW;
     static constexpr int STAGE = UNITS * 1024;
-    static constexpr int NS = BM == 256 ? 4 : 3;
+    static constexpr int NS = (BM == 256 && WF != WF_I8) ? 4 : 3;
     static_assert(MB >= 1 && UPW >= 1 && UNITS % NW == 0, "tile shape");
     static constexpr size_t lds_bytes() {
         const size_t epi = (size_t)NW * WT * G_EPI_PITCH * sizeof(float);
@@ -108,22 +118,26 @@ __device__ __forceinline__ void gemm_store_slow(const GemmArgs& a, int m, int ro
     }
 }
 
-template <bool GLU, bool ARGMAX, int BM, int NW, bool PP>
+// Fragment registers: 8 halves (bf16 or f16) as raw bits.
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// WF: BF16 (bf16 MFMA) or INT8 (weights converted exactly to f16 in registers,
+// f16 MFMA; BF16 activations are converted to f16 as well).  XDT: activation
+// type (BF16, or F16 with INT8 weights).
+template <int WF, int XDT, bool GLU, bool ARGMAX, int BM, int NW>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(BM == 256 && NW == 4 ? 1 : 2, BM == 256 && NW == 4 ? 1 : 2)))
-void gemm_bf16_kernel(GemmArgs a) {
-    using T = GTile<BM, NW>;
+void gemm_kernel(GemmArgs a) {
+    using T = GTile<BM, NW, WF>;
     constexpr int MB = T::MB, UPW = T::UPW, G_NS = T::NS, G_STAGE = T::STAGE, WM = T::WM, WT = T::WT;
+    constexpr int KSUB = T::KSUB, KSL = T::KSL, XU = T::XU;
+    constexpr bool I8 = WF == WF_I8;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ unsigned long long best_s[2][BM];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // 128 rows x WT tokens of this wave.  Ping-pong: waves w and w + 4 share a
-    // SIMD (and a row half); group g = w / 4 selects the token quarters.
-    const int pg = wave >> 2;
-    const int wn = PP ? (wave & 3) >> 1 : wave / WM;
-    const int wm = PP ? ((wave & 1) | (pg << 1)) : wave % WM;
+    const int wn = wave / WM, wm = wave % WM;   // 128 rows x WT tokens of this wave
 
     // XCD-aware order: consecutive workgroup ids go to different XCDs; give
     // each XCD a contiguous range of tiles (M fastest) so the tiles that
@@ -148,11 +162,10 @@ void gemm_bf16_kernel(GemmArgs a) {
     const int nkb = a.ksteps;  // K-blocks of one 32-deep k-step
 
     // The UPW units this wave moves per K-block: unit u = wave*UPW + q of the
-    // stage is weight tile u (u < 16) or activation token group u - 16, and
-    // lands at byte u*1024.  Offsets for K-block 0 are computed once; K-block
-    // kb adds kb*1024 (weights) or kb*64 bytes (activations).
-    // The buffer and per-block stride of each unit are chosen once (wave-
-    // uniform selects), so issuing a load inside the K-loop is branch-free.
+    // stage is weight tile u (u < 16) or activation unit v = u - 16 (sub-step
+    // v / XU, token group v % XU), and lands at byte u*1024.  The buffer and
+    // per-block stride of each unit are chosen once (wave-uniform selects),
+    // so issuing a load inside the K-loop is branch-free.
     uint32_t vbase[UPW], vstep[UPW];
     __amdgpu_buffer_rsrc_t rsq[UPW];
 #pragma unroll
@@ -160,11 +173,12 @@ void gemm_bf16_kernel(GemmArgs a) {
         const int u = wave * UPW + q;
         const bool isw = u < 16;
         const int pt = nt0 + u;
-        const int row = m0 + (u - 16) * 16 + (lane & 15);
+        const int v = u - 16;
+        const int row = m0 + (v % XU) * 16 + (lane & 15);
         const uint32_t wo = pt < a.n_tiles ? (uint32_t)(pt * a.ksteps * 1024 + lane * 16) : OOB;
-        const uint32_t xo = row < a.M ? (uint32_t)((row * a.ldx + (lane >> 4) * 8) * 2) : OOB;
+        const uint32_t xo = row < a.M ? (uint32_t)((row * a.ldx + (lane >> 4) * 8) * 2 + (v / XU) * 64) : OOB;
         vbase[q] = isw ? wo : xo;
-        vstep[q] = isw ? 1024u : 64u;
+        vstep[q] = isw ? 1024u : (uint32_t)(KSUB * 64);
         rsq[q] = isw ? wrs : xrs;
     }
     auto dma = [&](int kb, int q) {
@@ -178,34 +192,63 @@ void gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < MB; ++j) acc[i][j] = f32x16{};
 
-    // lane -> fragment address within a (tile pair, k-step) unit: row l%32 of
-    // a 32-row block = tile (l%32)/16, row l%16; k-group 2h + l/32
+    // lane -> fragment address: row l%32 of a 32-row block = tile (l%32)/16,
+    // row l%16.  BF16 unit (32 k): k-group 2*slice + l/32 of 8 -> 16 bytes at
+    // ((l%16) + 16*(l/32))*16 + slice*512.  INT8 unit (64 k): lane group g of
+    // the unit holds 16 k from 16g, so slice s, half l/32 is the 8 bytes at
+    // ((l%16) + 16*s)*16 + 8*(l/32).  Activation units as BF16 weight units.
     const int frag_tile = (lane & 31) >> 4;
-    const int frag_off = ((lane & 15) + 16 * (lane >> 5)) * 16;  // + 32*16*h
+    const int frag_off = ((lane & 15) + 16 * (lane >> 5)) * 16;
+    const int frag_off8 = (lane & 15) * 16 + 8 * (lane >> 5);
 
-    // fragments of half h (16 of the 32 k) of a K-block
-    bf16x8 A[2][4], B[2][MB];
-    auto read_frags = [&](const uint8_t* st, int h, bf16x8 (&Ad)[4], bf16x8 (&Bd)[MB]) {
+    // fragments of one 16-deep slice (raw 16-bit bits)
+    u32x4v A[2][4], B[2][MB];
+    auto read_frags = [&](const uint8_t* st, int sl, u32x4v (&Ad)[4], u32x4v (&Bd)[MB]) {
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
             const int t = wn * 8 + nb * 2 + frag_tile;
-            Ad[nb] = *reinterpret_cast<const bf16x8*>(st + t * 1024 + frag_off + h * 512);
+            if constexpr (I8) {
+                const uint2 w8 = *reinterpret_cast<const uint2*>(st + t * 1024 + frag_off8 + sl * 256);
+                uint32_t l0, h0, l1, h1;
+                i8x4_to_f16(w8.x, l0, h0);
+                i8x4_to_f16(w8.y, l1, h1);
+                Ad[nb] = u32x4v{l0, h0, l1, h1};
+            } else {
+                Ad[nb] = *reinterpret_cast<const u32x4v*>(st + t * 1024 + frag_off + sl * 512);
+            }
         }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-            const int t = wm * 2 * MB + mb * 2 + frag_tile;
-            Bd[mb] = *reinterpret_cast<const bf16x8*>(st + G_XOFF + t * 1024 + frag_off + h * 512);
+            const int t = (sl >> 1) * XU + wm * 2 * MB + mb * 2 + frag_tile;
+            u32x4v xv = *reinterpret_cast<const u32x4v*>(st + G_XOFF + t * 1024 + frag_off + (sl & 1) * 512);
+            if constexpr (I8 && XDT == DT_BF16) {  // exact for |x| in the f16 normal range
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    xv[e] = f32_to_f16_bits(bf16_bits_to_f32(xv[e] & 0xffffu)) |
+                            (f32_to_f16_bits(bf16_bits_to_f32(xv[e] >> 16)) << 16);
+            }
+            Bd[mb] = xv;
         }
     };
+    auto mfma = [&](const u32x4v& av, const u32x4v& bv, f32x16& c) {
+        if constexpr (I8)
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, bv),
+                                                       c, 0, 0, 0);
+        else
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv),
+                                                        c, 0, 0, 0);
+    };
 
-    // G_NS-stage pipeline over K-blocks (two 16-deep halves each).  Block kb
-    // runs as: read the fragments of half 1; MFMAs of half 0; wait for this
-    // wave's loads of block kb+1 and one barrier, which publishes kb+1 and
-    // proves every wave has consumed block kb-1 (its half-1 MFMAs were
-    // issued); read the fragments of kb+1 half 0; MFMAs of half 1, with the
-    // global->LDS loads of block kb+G_NS-1 (into the stage of kb-1) issued one
-    // per MFMA pair.  LDS read latency is covered by the other half's MFMAs
-    // and the barrier never sits between a fragment read and its use.
+    // G_NS-stage pipeline over K-blocks of KSL 16-deep slices.  Block kb runs
+    // its slices with a one-slice fragment lookahead (slice s+1 is read while
+    // slice s is multiplied, two register buffers).  Before the last slice's
+    // MFMAs: wait for this wave's loads of block kb+1 and one barrier, which
+    // publishes kb+1 and proves every wave has consumed block kb-1 (its last
+    // slice was multiplied); then slice 0 of kb+1 is read and the last slice
+    // is multiplied with the global->LDS loads of block kb+G_NS-1 (into the
+    // stage of kb-1) issued between MFMAs.  LDS read latency is covered by the
+    // previous slice's MFMAs and no barrier sits between a fragment read and
+    // its use.
     auto wait_loads = [&](int later) {  // at most `later` blocks of loads may stay in flight
         if (later >= 2) __builtin_amdgcn_s_waitcnt(vm_wait(2 * UPW));
         else if (later == 1) __builtin_amdgcn_s_waitcnt(vm_wait(UPW));
@@ -217,116 +260,52 @@ void gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
             for (int q = 0; q < UPW; ++q) dma(s0, q);
         }
-    if constexpr (PP) {
-        // Ping-pong over K-blocks.  Each block j takes two phases separated
-        // by barriers: in phase 2j group 0 multiplies block j (fragments in
-        // registers) while group 1 reads block j's fragments and issues its
-        // loads of block j+NS-1; in phase 2j+1 group 1 multiplies block j
-        // while group 0 reads block j+1 and issues its loads of block j+NS.
-        // The two waves of a SIMD thus alternate between an uninterrupted
-        // run of 16 MFMAs and the memory work, so load issue and LDS read
-        // latency never sit inside an MFMA run.  Stage reuse: block j+NS-1
-        // (group 1, phase 2j) and j+NS (group 0, phase 2j+1) land in stages
-        // whose last reader finished before the barrier that ends phase
-        // 2j-1 resp. 2j.  Before the barrier ending phase 2j every wave has
-        // its own loads of block j+1 complete, so group 0 may read it next.
-        auto issue = [&](int blk) {
-            if (blk < nkb) {
+    wait_loads(min(G_NS - 2, nkb - 1));
+    __syncthreads();
+    read_frags(lds, 0, A[0], B[0]);
+    // The final block is peeled off so the loop body has a single path: at a
+    // control-flow join the compiler's wait counting would make the last
+    // slice's MFMAs wait for the next block's fragment reads.
+    auto kblock = [&](int kb, auto last) {
+        constexpr bool LAST = decltype(last)::value;
+        const uint8_t* st = lds + (kb % G_NS) * G_STAGE;
 #pragma unroll
-                for (int q = 0; q < UPW; ++q) dma(blk, q);
-            }
-        };
-        auto compute = [&]() {
+        for (int sl = 0; sl < KSL - 1; ++sl) {
+            read_frags(st, sl + 1, A[(sl + 1) & 1], B[(sl + 1) & 1]);
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int i = 0; i < 4 * MB; ++i)
-                    acc[i / MB][i % MB] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[h][i / MB], B[h][i % MB],
-                                                                                acc[i / MB][i % MB], 0, 0, 0);
+            for (int i = 0; i < 4 * MB; ++i) mfma(A[sl & 1][i / MB], B[sl & 1][i % MB], acc[i / MB][i % MB]);
             __builtin_amdgcn_s_setprio(0);
-        };
-        auto read_block = [&](int blk) {
-            const uint8_t* st = lds + (blk % G_NS) * G_STAGE;
-            read_frags(st, 0, A[0], B[0]);
-            read_frags(st, 1, A[1], B[1]);
-        };
-        // prologue: group 0 issues blocks 0..NS-1, group 1 blocks 0..NS-2
-#pragma unroll
-        for (int s0 = 0; s0 < G_NS - 1; ++s0) issue(s0);
-        if (pg == 0) issue(G_NS - 1);
-        if (pg == 0) wait_loads(min(G_NS - 1, nkb - 1));
-        else wait_loads(min(G_NS - 2, nkb - 1));
-        __syncthreads();
-        if (pg == 0) read_block(0);
-        for (int j = 0; j < nkb; ++j) {
-            // phase 2j
-            if (pg == 0) {
-                compute();
-            } else {
-                read_block(j);
-                issue(j + G_NS - 1);
-            }
-            // own loads of block j+1 complete (blocks j+2 .. j+NS-1 may remain)
-            wait_loads(min(G_NS - 2, nkb - j - 2));
-            __syncthreads();
-            // phase 2j+1
-            if (pg == 1) {
-                compute();
-            } else if (j + 1 < nkb) {
-                read_block(j + 1);
-                issue(j + G_NS);
-            }
-            __syncthreads();
         }
-    } else {
-        wait_loads(min(G_NS - 2, nkb - 1));
-        __syncthreads();
-        read_frags(lds, 0, A[0], B[0]);
-        // one K-block; LAST (the final block) has no successor to publish.  The
-        // final block is peeled off so the loop body has a single path: at a
-        // control-flow join the compiler's wait counting would make the half-1
-        // MFMAs wait for the next block's fragment reads.
-        auto kblock = [&](int kb, auto last) {
-            constexpr bool LAST = decltype(last)::value;
-            const uint8_t* st = lds + (kb % G_NS) * G_STAGE;
-            read_frags(st, 1, A[1], B[1]);
-            __builtin_amdgcn_s_setprio(1);
-    #pragma unroll
-            for (int i = 0; i < 4 * MB; ++i)
-                acc[i / MB][i % MB] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0][i / MB], B[0][i % MB], acc[i / MB][i % MB], 0, 0, 0);
-            __builtin_amdgcn_s_setprio(0);
+        constexpr int LB = (KSL - 1) & 1;  // register buffer of the last slice
+        if constexpr (!LAST) {
+            wait_loads(min(G_NS - 3, nkb - kb - 2));
+            __syncthreads();
+            read_frags(lds + ((kb + 1) % G_NS) * G_STAGE, 0, A[LB ^ 1], B[LB ^ 1]);
+        }
+        const bool more = kb + G_NS - 1 < nkb;
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int i = 0; i < 4 * MB; ++i) {
+            mfma(A[LB][i / MB], B[LB][i % MB], acc[i / MB][i % MB]);
+            constexpr int per = (4 * MB) / UPW > 0 ? (4 * MB) / UPW : 1;  // MFMAs per load issue
             if constexpr (!LAST) {
-                wait_loads(min(G_NS - 3, nkb - kb - 2));
-                __syncthreads();
-                read_frags(lds + ((kb + 1) % G_NS) * G_STAGE, 0, A[0], B[0]);
-            }
-            const bool more = kb + G_NS - 1 < nkb;
-            __builtin_amdgcn_s_setprio(1);
-    #pragma unroll
-            for (int i = 0; i < 4 * MB; ++i) {
-                acc[i / MB][i % MB] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[1][i / MB], B[1][i % MB], acc[i / MB][i % MB], 0, 0, 0);
-                constexpr int per = (4 * MB) / UPW > 0 ? (4 * MB) / UPW : 1;  // MFMAs per load issue
-                if constexpr (!LAST) {
-                    if (i % per == per - 1 && i / per < UPW) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        if (more) dma(kb + G_NS - 1, i / per);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
+                if (i % per == per - 1 && i / per < UPW) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (more) dma(kb + G_NS - 1, i / per);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            if constexpr (!LAST && (4 * MB) / UPW == 0) {  // more units than MFMAs: the rest after them
-    #pragma unroll
-                for (int q = 4 * MB; q < UPW; ++q)
-                    if (more) dma(kb + G_NS - 1, q);
-            }
-            __builtin_amdgcn_s_setprio(0);
-        };
-        for (int kb = 0; kb < nkb - 1; ++kb) kblock(kb, std::false_type{});
-        kblock(nkb - 1, std::true_type{});
-    }
+        }
+        if constexpr (!LAST && (4 * MB) / UPW == 0) {  // more units than MFMAs: the rest after them
+#pragma unroll
+            for (int q = 4 * MB; q < UPW; ++q)
+                if (more) dma(kb + G_NS - 1, q);
+        }
+        __builtin_amdgcn_s_setprio(0);
+    };
+    for (int kb = 0; kb < nkb - 1; ++kb) kblock(kb, std::false_type{});
+    kblock(nkb - 1, std::true_type{});
 
     // ---- epilogue ----
     // accumulator item q of lane l: weight row i = 8*(q/4) + 4*(l/32) + q%4 of
@@ -474,24 +453,41 @@ static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, int threads
     return hipGetLastError();
 }
 
-template <int BM, int NW, bool PP = false>
+template <int WF, int XDT, int BM, int NW>
 static hipError_t launch_bm(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
     const int grid = a.nblk_n * a.nblk_m;
-    const size_t lds = GTile<BM, NW>::lds_bytes();
-    if (argmax) return launch_gemm_k(gemm_bf16_kernel<false, true, BM, NW, PP>, a, grid, NW * 64, lds, stream);
-    if (glu) return launch_gemm_k(gemm_bf16_kernel<true, false, BM, NW, PP>, a, grid, NW * 64, lds, stream);
-    return launch_gemm_k(gemm_bf16_kernel<false, false, BM, NW, PP>, a, grid, NW * 64, lds, stream);
+    const size_t lds = GTile<BM, NW, WF>::lds_bytes();
+    if (argmax) return launch_gemm_k(gemm_kernel<WF, XDT, false, true, BM, NW>, a, grid, NW * 64, lds, stream);
+    if (glu) return launch_gemm_k(gemm_kernel<WF, XDT, true, false, BM, NW>, a, grid, NW * 64, lds, stream);
+    return launch_gemm_k(gemm_kernel<WF, XDT, false, false, BM, NW>, a, grid, NW * 64, lds, stream);
+}
+
+// Block shapes: BF16 weights 256 x 256 (8 or 4 waves) or 256 x 128 (4 waves,
+// two workgroups per CU); INT8 weights 256 x 256 or 256 x 128, 8 waves.
+template <int WF, int XDT>
+static hipError_t launch_wf(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
+    if (a.tile_m == 256 && a.nblk_m == (a.M + 255) / 256) {
+        if (a.waves == 8) return launch_bm<WF, XDT, 256, 8>(a, glu, argmax, stream);
+        if constexpr (WF == WF_BF16) return launch_bm<WF, XDT, 256, 4>(a, glu, argmax, stream);
+        return hipErrorInvalidValue;
+    }
+    if (a.tile_m == 128 && a.nblk_m == (a.M + 127) / 128) {
+        if constexpr (WF == WF_I8) return launch_bm<WF, XDT, 128, 8>(a, glu, argmax, stream);
+        else return launch_bm<WF, XDT, 128, 4>(a, glu, argmax, stream);
+    }
+    return hipErrorInvalidValue;
+}
+
+bool gemm_supported(int wf, int xdt) {
+    return (wf == WF_BF16 && xdt == DT_BF16) || (wf == WF_I8 && (xdt == DT_BF16 || xdt == DT_F16));
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream) {
-    if (wf != WF_BF16 || xdt != DT_BF16) return hipErrorInvalidValue;
+    if (!gemm_supported(wf, xdt)) return hipErrorInvalidValue;
     if (argmax && glu) return hipErrorInvalidValue;
-    if (a.tile_m == 256 && a.nblk_m == (a.M + 255) / 256)
-        return a.waves == 8   ? (a.pingpong ? launch_bm<256, 8, true>(a, glu, argmax, stream)
-                                            : launch_bm<256, 8>(a, glu, argmax, stream))
-                              : launch_bm<256, 4>(a, glu, argmax, stream);
-    if (a.tile_m == 128 && a.nblk_m == (a.M + 127) / 128) return launch_bm<128, 4>(a, glu, argmax, stream);
-    return hipErrorInvalidValue;
+    if (wf == WF_BF16) return launch_wf<WF_BF16, DT_BF16>(a, glu, argmax, stream);
+    if (xdt == DT_F16) return launch_wf<WF_I8, DT_F16>(a, glu, argmax, stream);
+    return launch_wf<WF_I8, DT_BF16>(a, glu, argmax, stream);
 }
 
 }  // namespace qwk

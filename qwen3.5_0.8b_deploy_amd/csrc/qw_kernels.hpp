@@ -73,7 +73,6 @@ struct GemmArgs {
     int nblk_n, nblk_m;      // block grid: 256 weight rows x tile_m tokens
     int tile_m;              // tokens per block: 256 or 128
     int waves;               // waves per workgroup: 4, or 8 (tile_m 256 only)
-    int pingpong;            // 8 waves: alternate MFMA and memory phases between wave pairs
     unsigned flags;
     const void* res;
     int res_dt, ld_res;
@@ -87,6 +86,7 @@ struct GemmArgs {
     int32_t* ids;
     float* maxv;
 };
+bool gemm_supported(int wf, int xdt);
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream);
 
 // Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass

@@ -13,17 +13,15 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module", params=["128x4", "256x4", "256x8", "256x8pp"])
+@pytest.fixture(scope="module", params=["128x4", "256x4", "256x8"])
 def ctx(qw, request):
-    """A context that takes the GEMM for every BF16 call from 33 tokens on
-    (the default routing sends small-N shapes to the chunked small-M kernels),
-    with each token-block shape: 128 tokens x 4 waves, 256 x 4, 256 x 8, and
-    256 x 8 with the ping-pong schedule."""
+    """A context that takes the GEMM for every BF16 / INT8 call from 33 tokens
+    on (the default routing sends small-N shapes to the chunked small-M
+    kernels), with each token-block shape: 128 tokens x 4 waves, 256 x 4,
+    256 x 8 (INT8 weights always run 8 waves: 128 x 8, 256 x 8)."""
     import os
     tile, waves = request.param.split("x")
-    pp = waves.endswith("pp")
-    env = {"QW_GEMM_MIN_M": "33", "QW_GEMM_TILE_M": tile, "QW_GEMM_WAVES": waves.rstrip("p"),
-           "QW_GEMM_PINGPONG": "1" if pp else "0"}
+    env = {"QW_GEMM_MIN_M": "33", "QW_GEMM_TILE_M": tile, "QW_GEMM_WAVES": waves}
     os.environ.update(env)
     try:
         c = qw.Context(0)
@@ -151,3 +149,108 @@ def test_gemm_repeatable(qw, ctx, oracle):
     torch.cuda.synchronize()
     got = ys.cpu().numpy()
     assert (got == got[0][None]).all()
+
+
+# ---------------------------------------------------------------------------
+# INT8 weights (per-row scales): INT8 units in LDS, exact f16 conversion in
+# registers, f16 MFMA, scale in the epilogue.  Bar: <= 1e-3 normwise against
+# dequantize-then-multiply of the same q, s and activations (FP64 here, so
+# only FP32 accumulation error remains: <= 2e-5 in practice).
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("xname", ["f16", "bf16"])
+@pytest.mark.parametrize("M,N,K", [(33, 40, 64), (130, 1024, 1024), (300, 1032, 2048), (517, 4096, 1024)])
+def test_gemm_int8_parity(qw, ctx, oracle, relerr, xname, M, N, K):
+    W = oracle.normal((N, K), 800 + N, 0.0, 0.02)
+    x = oracle.normal((M, K), 801 + M)
+    w = qw.Weight.pack(ctx, W, qw.WFMT_INT8)
+    q, sc = w.unpack()
+    xt = dev(x, torch.float16 if xname == "f16" else torch.bfloat16)
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(ctx, w, xt, y)
+    torch.cuda.synchronize()
+    xs = host(xt)
+    assert relerr(host(y), oracle.linear_int8_f64(q, sc, xs)) <= 2e-5
+    assert relerr(host(y), oracle.linear_int8(q, sc, xs)) <= 1e-3
+
+
+def test_gemm_int8_exact(qw, ctx, oracle):
+    """Integer activations and power-of-two scales: every product and partial
+    sum is an exactly representable FP32 integer, so the GEMM must equal the
+    FP64 result bit for bit (a dropped k, a wrong row or a mis-converted byte
+    shows up as an integer error)."""
+    M, N, K = 200, 512, 1024
+    q = oracle.int8_uniform((N, K), 810)
+    sc = np.float32(2.0) ** (-(np.arange(N) % 7)).astype(np.float32)
+    x = np.round(oracle.normal((M, K), 811) * 2.0).clip(-4, 4).astype(np.float32)
+    w = qw.Weight.pack(ctx, q, qw.WFMT_INT8, scales=sc)
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(ctx, w, dev(x, torch.float16), y)
+    torch.cuda.synchronize()
+    ref = (x.astype(np.float64) @ q.astype(np.float64).T) * sc.astype(np.float64)[None, :]
+    assert np.array_equal(host(y), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("ydt", ["bf16", "f32"])
+def test_gemm_int8_epilogues(qw, ctx, oracle, relerr, ydt):
+    """GLU (gate/up pairs with their own scales), RMSNorm prologue (F16 copy
+    in the workspace), residual add and the Q/gate split on INT8 weights."""
+    ydtype = torch.bfloat16 if ydt == "bf16" else torch.float32
+    # FP32 outputs: the north-star INT8 bar (the RMSNorm prologue feeds the
+    # GEMM an F16 copy of the normalized activations, ~2.5e-4 normwise);
+    # BF16 outputs add one output rounding
+    bar_y = 4e-3 if ydt == "bf16" else 1e-3
+    M, H, I = 150, 1024, 1024
+    G = oracle.normal((I, H), 820, 0.0, 0.02)
+    U = oracle.normal((I, H), 821, 0.0, 0.02)
+    gamma = oracle.normal((H,), 822, 0.0, 0.02)
+    x = oracle.normal((M, H), 823)
+    gu = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_INT8)
+    qgu, sgu = gu.unpack()
+    xt = dev(x, torch.float16)
+    h = torch.empty(M, I, device="cuda", dtype=ydtype)
+    qw.linear(ctx, gu, xt, h, gamma=dev(gamma))
+    torch.cuda.synchronize()
+    xn = oracle.rmsnorm_f64(host(xt), gamma)
+    g = oracle.linear_int8_f64(qgu[:I], sgu[:I], xn)
+    u = oracle.linear_int8_f64(qgu[I:], sgu[I:], xn)
+    assert relerr(host(h), g / (1.0 + np.exp(-g)) * u) <= bar_y
+    # residual
+    W2 = oracle.normal((H, I), 824, 0.0, 0.02)
+    r = oracle.normal((M, H), 825)
+    w2 = qw.Weight.pack(ctx, W2, qw.WFMT_INT8)
+    q2, s2 = w2.unpack()
+    hin = dev(oracle.normal((M, I), 826), torch.float16)
+    y = dev(r, ydtype)
+    ref = oracle.linear_int8_f64(q2, s2, host(hin)) + host(y)
+    qw.linear(ctx, w2, hin, y, residual=y)
+    torch.cuda.synchronize()
+    assert relerr(host(y), ref) <= bar_y
+    # Q/gate split
+    heads, D = 4, 256
+    W3 = oracle.normal((2 * heads * D, H), 827, 0.0, 0.02)
+    w3 = qw.Weight.pack(ctx, W3, qw.WFMT_INT8)
+    q3, s3 = w3.unpack()
+    qo = torch.empty(M, heads * D, device="cuda", dtype=ydtype)
+    go = torch.empty(M, heads * D, device="cuda", dtype=ydtype)
+    qw.linear(ctx, w3, xt, qo, y2=go, split_period=D)
+    torch.cuda.synchronize()
+    full = oracle.linear_int8_f64(q3, s3, host(xt))
+    q_ref, g_ref = oracle.split_q_gate(full.astype(np.float32), heads, D)
+    assert relerr(host(qo), q_ref) <= bar_y and relerr(host(go), g_ref) <= bar_y
+
+
+@pytest.mark.parametrize("M", [33, 128, 300])
+def test_gemm_int8_lmhead_argmax(qw, ctx, oracle, M):
+    V, K = 20000, 1024
+    E = oracle.normal((V, K), 830, 0.0, 0.02)
+    h = oracle.normal((M, K), 831 + M)
+    w = qw.Weight.pack(ctx, E, qw.WFMT_INT8)
+    q, sc = w.unpack()
+    ht = dev(h, torch.float16)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    qw.lmhead_argmax(ctx, w, ht, ids)
+    torch.cuda.synchronize()
+    ref_ids, _ = oracle.lmhead_argmax_int8(q, sc, host(ht))
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
