@@ -413,25 +413,32 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
 def run_prefill(qw, ctx, torch, timer, stream, randn, args, M=16384):
     """Config 4: the 24-layer BF16 projection stack at M=16384 prefill tokens.
 
-    Per Gated-DeltaNet layer: QKV 1024->6144, Z 1024->2048, out 2048->1024
-    (+residual); per full-attention layer: Q+gate 1024->4096, K and V
-    1024->512, O 2048->1024 (+residual); every layer: RMSNorm + gate/up
-    1024->2x3584 with SiLU*mul, down 3584->1024 (+residual).  The attention
+    Per Gated-DeltaNet layer: QKV 1024->6144 and Z 1024->2048 (one stacked
+    weight), out 2048->1024 (+residual); per full-attention layer: Q+gate
+    1024->4096, K and V 1024->512 (one stacked weight), O 2048->1024
+    (+residual); every layer: RMSNorm + gate/up 1024->2x3584 with SiLU*mul,
+    down 3584->1024 (+residual).  The attention
     cores between the projections are outside this path; a fixed [M][2048]
     tensor stands in for their output.  FLOPs = 2*M*sum(N*K) = 16.29 TFLOP."""
     ws = []
     nk = 0
     for li in range(LAYERS):
         L = {}
+        # the input projections of a layer share x: one stacked weight per
+        # layer (qw_weight_pack_concat), as the loader packs them
         if li in LINEAR_LAYERS:
-            shapes = {"qkv": (6144, 1024), "z": (2048, 1024), "out": (1024, 2048)}
+            ins, out_k = [(6144, 1024), (2048, 1024)], 2048
         else:
-            shapes = {"qg": (4096, 1024), "k": (512, 1024), "v": (512, 1024), "o": (1024, 2048)}
-        for name, (n, k) in shapes.items():
-            w = randn(n, k, std=0.02)
-            L[name] = qw.Weight.pack_device(ctx, w, qw.WFMT_BF16)
-            nk += n * k
-            del w
+            ins, out_k = [(4096, 1024), (512, 1024), (512, 1024)], 2048
+        parts = [randn(n, k, std=0.02) for n, k in ins]
+        L["in"] = qw.Weight.pack_concat_device(ctx, parts, qw.WFMT_BF16)
+        L["n_in"] = sum(n for n, _ in ins)
+        nk += sum(n * k for n, k in ins)
+        del parts
+        o = randn(1024, out_k, std=0.02)
+        L["out"] = qw.Weight.pack_device(ctx, o, qw.WFMT_BF16)
+        nk += 1024 * out_k
+        del o
         g, u = randn(I, H, std=0.02), randn(I, H, std=0.02)
         L["gu"] = qw.Weight.pack_glu_device(ctx, g, u, qw.WFMT_BF16)
         d = randn(H, I, std=0.02)
@@ -442,24 +449,15 @@ def run_prefill(qw, ctx, torch, timer, stream, randn, args, M=16384):
         ws.append(L)
     x = randn(M, H)
     att = randn(M, 2048)
-    big = torch.empty(M, 6144, device="cuda", dtype=torch.bfloat16)
-    z = torch.empty(M, 2048, device="cuda", dtype=torch.bfloat16)
-    kv = torch.empty(M, 512, device="cuda", dtype=torch.bfloat16)
+    big = torch.empty(M, 8192, device="cuda", dtype=torch.bfloat16)
     hmid = torch.empty(M, I, device="cuda", dtype=torch.bfloat16)
     res = randn(M, H)
     torch.cuda.synchronize()
 
     def body():
         for L in ws:
-            if "qkv" in L:
-                qw.linear(ctx, L["qkv"], x, big)
-                qw.linear(ctx, L["z"], x, z)
-                qw.linear(ctx, L["out"], att, res, residual=res)
-            else:
-                qw.linear(ctx, L["qg"], x, big[:, :4096])
-                qw.linear(ctx, L["k"], x, kv)
-                qw.linear(ctx, L["v"], x, kv)
-                qw.linear(ctx, L["o"], att, res, residual=res)
+            qw.linear(ctx, L["in"], x, big[:, :L["n_in"]], ldy=8192)
+            qw.linear(ctx, L["out"], att, res, residual=res)
             qw.linear(ctx, L["gu"], res, hmid, gamma=L["gamma"])
             qw.linear(ctx, L["down"], hmid, res, residual=res)
 

@@ -31,6 +31,7 @@ struct qw_ctx {
     bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
     int gemm_tile_m = 0;         // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256; 0 = by shape)
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
+    int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -167,6 +168,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
+    if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;
@@ -636,20 +638,32 @@ static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
     return qwk::gemm_supported(W->wf, (int)xdt);
 }
 
-// GEMM or 32-token chunks of the small-M kernels.  The 256 x 256 GEMM tile
-// needs enough weight-row blocks to fill the chip: with few (the 1024-row
-// projections) the chunked weight-streaming kernels win up to a few hundred
-// tokens (measured on MI355X: M=128 down projection 45 us chunked vs 111 us
-// GEMM; gate/up with 28 row blocks: GEMM from M=128).
-static bool use_gemm(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M) {
-    if (!gemm_ok(W, xdt) || M < ctx->gemm_min_m) return false;
-    if (ctx->gemm_forced) return true;
-    const int nblk_n = (W->phys_tiles * 16 + 255) / 256;
-    return (nblk_n >= 16 && M >= 128) || M >= 384;
+// Route of a call with M tokens: 0 = the small-M kernels (32-token groups
+// streaming the weights), else the GEMM with 64- or 256-row blocks.
+// Measured on MI355X with the weights streamed from HBM (distinct copies
+// replayed from a graph, as in a decode step), BF16 and INT8 alike:
+//   - up to ~128-192 tokens the small-M kernels win on every shape (gate/up
+//     M=128: 15.5 us vs 26.2 us with 64-row blocks);
+//   - 1024-row weights (out, down): small-M kernels up to at least 512 tokens
+//     (down M=512: 33 us vs 82 us for the best GEMM);
+//   - 4096..8192-row weights at 256..512 tokens: 64-row blocks (QKV+Z M=256:
+//     26 us vs 38 us with 256-row blocks vs 42 us small-M);
+//   - lm_head-size weights (>= 128 row blocks): 256-row blocks from 128.
+static int gemm_route(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M) {
+    if (!gemm_ok(W, xdt) || M < ctx->gemm_min_m) return 0;
+    const int nb256 = (W->phys_tiles * 16 + 255) / 256;
+    if (ctx->gemm_forced) return ctx->gemm_rows ? ctx->gemm_rows : (M <= 1024 && nb256 < 128 ? 64 : 256);
+    int rows;
+    if (nb256 < 16) rows = M >= 1536 ? 256 : 0;
+    else if (nb256 >= 128) rows = M >= 128 ? 256 : 0;
+    else if (M <= 192) rows = 0;
+    else rows = M <= 1024 ? 64 : 256;
+    if (rows && ctx->gemm_rows) rows = ctx->gemm_rows;
+    return rows;
 }
 
-static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx, int M, void* y,
-                          qw_dtype ydt, int ldy, const qw_epilogue* ep, int32_t* ids, float* maxv,
+static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, int rows, const void* x, qw_dtype xdt, int ldx, int M,
+                          void* y, qw_dtype ydt, int ldy, const qw_epilogue* ep, int32_t* ids, float* maxv,
                           hipStream_t stream) {
     qwk::GemmArgs a{};
     a.w = W->packed;
@@ -663,9 +677,15 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dty
     a.N = W->N;
     a.nblk_n = (W->phys_tiles * 16 + 255) / 256;
     // 256-token blocks (8 waves, half the L2->LDS traffic per FLOP of the
-    // 128-token block) once they alone fill the 256 CUs; 128-token blocks
-    // (two workgroups per CU) for fewer tokens
-    a.tile_m = ctx->gemm_tile_m ? ctx->gemm_tile_m : (a.nblk_n * ((M + 255) / 256) >= 256 ? 256 : 128);
+    // 128-token block) once they alone fill the 256 CUs and more than 128
+    // tokens exist; 128-token blocks (two workgroups per CU) otherwise;
+    // 64-row blocks (always 128 tokens) where gemm_route chose them
+    a.tile_m = ctx->gemm_tile_m ? ctx->gemm_tile_m : (M > 128 && a.nblk_n * ((M + 255) / 256) >= 256 ? 256 : 128);
+    a.rows = rows;
+    if (rows == 64) {
+        a.tile_m = 128;
+        a.nblk_n = (W->phys_tiles * 16 + 63) / 64;
+    }
     a.nblk_m = (M + a.tile_m - 1) / a.tile_m;
     a.waves = W->wf == QW_WFMT_INT8_ROWSCALE ? 8 : (a.tile_m == 256 ? ctx->gemm_waves : 4);
     a.flags = ep ? (ep->flags & ~(unsigned)QW_EP_NORM_X) : 0u;
@@ -750,9 +770,9 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     if (W && ldy == 0) ldy = (ep && (ep->flags & QW_EP_SPLIT)) ? W->N / 2 : W->N;
     qw_status s = check_linear(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, true);
     if (s != QW_OK) return s;
-    if (use_gemm(ctx, W, xdt, M)) {
+    if (const int rows = gemm_route(ctx, W, xdt, M)) {
         const bool norm = ep && (ep->flags & QW_EP_NORM_X);
-        if (!norm) return run_gemm(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);
+        if (!norm) return run_gemm(ctx, W, rows, x, xdt, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);
         // RMSNorm into the workspace, then the GEMM, in token chunks that fit.
         // INT8 weights take F16 (their MFMA type: a BF16 copy would add ~1e-3
         // of rounding error, the whole INT8 tolerance).
@@ -772,7 +792,7 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
                 e3.residual = static_cast<const uint8_t*>(ep->residual) + (size_t)m0 * ldr * dsize(ep->residual_dtype);
             }
             if (ep->flags & QW_EP_SPLIT) e3.y2 = static_cast<uint8_t*>(ep->y2) + (size_t)m0 * ldy * dsize(ydt);
-            s = run_gemm(ctx, W, ctx->xnorm, ndt, W->K, mc, yc, ydt, ldy, &e3, nullptr, nullptr, stream);
+            s = run_gemm(ctx, W, rows, ctx->xnorm, ndt, W->K, mc, yc, ydt, ldy, &e3, nullptr, nullptr, stream);
             if (s != QW_OK) return s;
         }
         return QW_OK;
@@ -792,8 +812,8 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     if (!token_ids) return fail(ctx, QW_ERR_NULL, "token_ids is NULL");
     if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
     if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
-    if (use_gemm(ctx, E, hdt, M))
-        return run_gemm(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
+    if (const int rows = gemm_route(ctx, E, hdt, M))
+        return run_gemm(ctx, E, rows, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
     return run_skinny(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream,
                       kSkinnyMaxM);
 }

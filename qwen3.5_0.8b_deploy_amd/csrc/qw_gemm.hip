@@ -1,7 +1,7 @@
 // qw_gemm.hip -- LDS double-buffered MFMA GEMM for gfx950 (prefill and
 // large-batch decode):  y[m][n] = sum_k W[n][k] * x[m][k]  (+ epilogue).
 //
-// Tiling.  A workgroup computes 256 weight rows x BM tokens with 32 x 32 x 16
+// Tiling.  A workgroup computes RW = 256 (or 64) weight rows x BM tokens with 32 x 32 x 16
 // MFMAs (weights are the A operand, tokens the B operand; FP32
 // accumulators); K advances in blocks of one k-step of the packed weight
 // (32 deep for BF16, 64 for INT8).  Shapes:
@@ -11,7 +11,9 @@
 //   - BM = 128: BF16 with 4 waves (each 128 x 64; two workgroups share a CU,
 //     so one's barrier and LDS waits are covered by the other), INT8 with 8
 //     waves (each 128 x 32);
-//   - BM = 256, 4 waves (BF16): each wave 128 x 128 (one wave per SIMD).
+//   - BM = 256, 4 waves (BF16): each wave 128 x 128 (one wave per SIMD);
+//   - RW = 64, BM = 128, 4 waves (both formats): each wave 64 x 32, for few
+//     tokens on few weight rows, where 256-row blocks leave CUs idle.
 // Weight formats: BF16 weights use the bf16 MFMA on BF16 activations.  INT8
 // weights (per-row scales) reach LDS as INT8, half the bytes; each lane
 // converts its 8-byte fragment exactly to f16 (qw_device.hpp i8x4_to_f16)
@@ -51,25 +53,27 @@ namespace qwk {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int GB_N = 256;                  // block tile: weight rows (x BM tokens, BM = 256 or 128)
 constexpr int G_GROUP_M = 8;               // token blocks per raster group
-constexpr int G_XOFF = 16 * 1024;          // activation region within a stage (after 16 weight units)
 constexpr int G_EPI_PITCH = 68;            // epilogue LDS row pitch (floats): 64 rows + pad
 
-// Stage geometry for token-tile height BM, NW waves and weight format WF.  A
-// K-block is one k-step of the packed weight: 32 deep for BF16, 64 for INT8
-// (KSUB 32-deep activation sub-steps).  A stage holds the block's 16 weight
-// units (256 rows) and KSUB * BM/16 activation units; UPW units per wave;
+// Stage geometry for a block of RW weight rows x BM tokens, NW waves and
+// weight format WF.  A K-block is one k-step of the packed weight: 32 deep
+// for BF16, 64 for INT8 (KSUB 32-deep activation sub-steps).  A stage holds
+// the block's RW/16 weight units and KSUB * BM/16 activation units (after the
+// weight units); UPW units per wave;
 // NS stages in flight (fewer where the stage is larger or two workgroups
 // share a CU).
-template <int BM, int NW, int WF> struct GTile {
-    static constexpr int WM = NW / 2;                 // waves along the tokens (2 along the rows)
+template <int BM, int NW, int WF, int RW> struct GTile {
+    static constexpr int WR = RW == 256 ? 2 : 1;      // waves along the rows
+    static constexpr int WM = NW / WR;                // waves along the tokens
     static constexpr int WT = BM / WM;                // tokens per wave
     static constexpr int MB = WT / 32;                // 32-token MFMA blocks per wave
+    static constexpr int NBW = RW / WR / 32;          // 32-row MFMA blocks per wave
+    static constexpr int WU = RW / 16;                // weight units (16-row tiles) per stage
     static constexpr int KSUB = WF == WF_I8 ? 2 : 1;
     static constexpr int KSL = 2 * KSUB;              // 16-deep MFMA slices per K-block
     static constexpr int XU = BM / 16;                // activation units per sub-step
-    static constexpr int UNITS = 16 + KSUB * XU;
+    static constexpr int UNITS = WU + KSUB * XU;
     static constexpr int UPW = UNITS / NW;
     static constexpr int STAGE = UNITS * 1024;
     static constexpr int NS = (BM == 256 && WF != WF_I8) ? 4 : 3;
@@ -124,20 +128,21 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 // WF: BF16 (bf16 MFMA) or INT8 (weights converted exactly to f16 in registers,
 // f16 MFMA; BF16 activations are converted to f16 as well).  XDT: activation
 // type (BF16, or F16 with INT8 weights).
-template <int WF, int XDT, bool GLU, bool ARGMAX, int BM, int NW>
+template <int WF, int XDT, bool GLU, bool ARGMAX, int BM, int NW, int RW>
 __global__ __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(BM == 256 && NW == 4 ? 1 : 2, BM == 256 && NW == 4 ? 1 : 2)))
 void gemm_kernel(GemmArgs a) {
-    using T = GTile<BM, NW, WF>;
+    using T = GTile<BM, NW, WF, RW>;
     constexpr int MB = T::MB, UPW = T::UPW, G_NS = T::NS, G_STAGE = T::STAGE, WM = T::WM, WT = T::WT;
-    constexpr int KSUB = T::KSUB, KSL = T::KSL, XU = T::XU;
+    constexpr int KSUB = T::KSUB, KSL = T::KSL, XU = T::XU, NBW = T::NBW, WU = T::WU, WR = T::WR;
+    constexpr int G_XOFF = WU * 1024;       // activation units follow the weight units
     constexpr bool I8 = WF == WF_I8;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ unsigned long long best_s[2][BM];
+    __shared__ unsigned long long best_s[WR][BM];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wn = wave / WM, wm = wave % WM;   // 128 rows x WT tokens of this wave
+    const int wn = wave / WM, wm = wave % WM;   // 32*NBW rows x WT tokens of this wave
 
     // XCD-aware order: consecutive workgroup ids go to different XCDs; give
     // each XCD a contiguous range of tiles (M fastest) so the tiles that
@@ -154,7 +159,7 @@ void gemm_kernel(GemmArgs a) {
     const int gm = min(G_GROUP_M, a.nblk_m - first_m);
     const int in_group = b - group * per_group;
     const int bm = first_m + in_group % gm, bn = in_group / gm;
-    const int nt0 = bn * (GB_N / 16);          // first physical 16-row tile
+    const int nt0 = bn * WU;                   // first physical 16-row tile
     const int m0 = bm * BM;
 
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_tiles * a.ksteps * 1024u));
@@ -162,7 +167,7 @@ void gemm_kernel(GemmArgs a) {
     const int nkb = a.ksteps;  // K-blocks of one 32-deep k-step
 
     // The UPW units this wave moves per K-block: unit u = wave*UPW + q of the
-    // stage is weight tile u (u < 16) or activation unit v = u - 16 (sub-step
+    // stage is weight tile u (u < WU) or activation unit v = u - WU (sub-step
     // v / XU, token group v % XU), and lands at byte u*1024.  The buffer and
     // per-block stride of each unit are chosen once (wave-uniform selects),
     // so issuing a load inside the K-loop is branch-free.
@@ -171,9 +176,9 @@ void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int q = 0; q < UPW; ++q) {
         const int u = wave * UPW + q;
-        const bool isw = u < 16;
+        const bool isw = u < WU;
         const int pt = nt0 + u;
-        const int v = u - 16;
+        const int v = u - WU;
         const int row = m0 + (v % XU) * 16 + (lane & 15);
         const uint32_t wo = pt < a.n_tiles ? (uint32_t)(pt * a.ksteps * 1024 + lane * 16) : OOB;
         const uint32_t xo = row < a.M ? (uint32_t)((row * a.ldx + (lane >> 4) * 8) * 2 + (v / XU) * 64) : OOB;
@@ -186,9 +191,9 @@ void gemm_kernel(GemmArgs a) {
         lds_dma16(rsq[q], dst, vbase[q] + (uint32_t)kb * vstep[q]);
     };
 
-    f32x16 acc[4][MB];
+    f32x16 acc[NBW][MB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NBW; ++i)
 #pragma unroll
         for (int j = 0; j < MB; ++j) acc[i][j] = f32x16{};
 
@@ -202,11 +207,11 @@ void gemm_kernel(GemmArgs a) {
     const int frag_off8 = (lane & 15) * 16 + 8 * (lane >> 5);
 
     // fragments of one 16-deep slice (raw 16-bit bits)
-    u32x4v A[2][4], B[2][MB];
-    auto read_frags = [&](const uint8_t* st, int sl, u32x4v (&Ad)[4], u32x4v (&Bd)[MB]) {
+    u32x4v A[2][NBW], B[2][MB];
+    auto read_frags = [&](const uint8_t* st, int sl, u32x4v (&Ad)[NBW], u32x4v (&Bd)[MB]) {
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-            const int t = wn * 8 + nb * 2 + frag_tile;
+        for (int nb = 0; nb < NBW; ++nb) {
+            const int t = wn * 2 * NBW + nb * 2 + frag_tile;
             if constexpr (I8) {
                 const uint2 w8 = *reinterpret_cast<const uint2*>(st + t * 1024 + frag_off8 + sl * 256);
                 uint32_t l0, h0, l1, h1;
@@ -274,7 +279,7 @@ void gemm_kernel(GemmArgs a) {
             read_frags(st, sl + 1, A[(sl + 1) & 1], B[(sl + 1) & 1]);
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int i = 0; i < 4 * MB; ++i) mfma(A[sl & 1][i / MB], B[sl & 1][i % MB], acc[i / MB][i % MB]);
+            for (int i = 0; i < NBW * MB; ++i) mfma(A[sl & 1][i / MB], B[sl & 1][i % MB], acc[i / MB][i % MB]);
             __builtin_amdgcn_s_setprio(0);
         }
         constexpr int LB = (KSL - 1) & 1;  // register buffer of the last slice
@@ -286,9 +291,9 @@ void gemm_kernel(GemmArgs a) {
         const bool more = kb + G_NS - 1 < nkb;
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-        for (int i = 0; i < 4 * MB; ++i) {
+        for (int i = 0; i < NBW * MB; ++i) {
             mfma(A[LB][i / MB], B[LB][i % MB], acc[i / MB][i % MB]);
-            constexpr int per = (4 * MB) / UPW > 0 ? (4 * MB) / UPW : 1;  // MFMAs per load issue
+            constexpr int per = (NBW * MB) / UPW > 0 ? (NBW * MB) / UPW : 1;  // MFMAs per load issue
             if constexpr (!LAST) {
                 if (i % per == per - 1 && i / per < UPW) {
                     __builtin_amdgcn_sched_barrier(0);
@@ -297,9 +302,9 @@ void gemm_kernel(GemmArgs a) {
                 }
             }
         }
-        if constexpr (!LAST && (4 * MB) / UPW == 0) {  // more units than MFMAs: the rest after them
+        if constexpr (!LAST && (NBW * MB) / UPW == 0) {  // more units than MFMAs: the rest after them
 #pragma unroll
-            for (int q = 4 * MB; q < UPW; ++q)
+            for (int q = NBW * MB; q < UPW; ++q)
                 if (more) dma(kb + G_NS - 1, q);
         }
         __builtin_amdgcn_s_setprio(0);
@@ -316,8 +321,8 @@ void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) best[mb] = 0ull;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) {
-            const int pt0 = nt0 + wn * 8 + nb * 2;
+        for (int nb = 0; nb < NBW; ++nb) {
+            const int pt0 = nt0 + wn * 2 * NBW + nb * 2;
 #pragma unroll
             for (int qg = 0; qg < 4; ++qg) {
                 const int row = pt0 * 16 + 8 * qg + ihi;
@@ -343,8 +348,9 @@ void gemm_kernel(GemmArgs a) {
         __syncthreads();
         if (threadIdx.x < BM) {
             const int j = threadIdx.x;
-            unsigned long long k0 = best_s[0][j], k1 = best_s[1][j];
-            const unsigned long long kk = k0 > k1 ? k0 : k1;
+            unsigned long long kk = best_s[0][j];
+#pragma unroll
+            for (int r = 1; r < WR; ++r) kk = best_s[r][j] > kk ? best_s[r][j] : kk;
             if (m0 + j < a.M && kk != 0ull)
                 __hip_atomic_fetch_max(&a.keys[m0 + j], kk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -370,21 +376,24 @@ void gemm_kernel(GemmArgs a) {
         // Results pass through LDS as [token][row] (row pitch G_EPI_PITCH
         // floats) so that each token's output rows leave as one contiguous,
         // coalesced store, and so that the accumulators are only ever indexed
-        // with constants.  GLU: the wave's 64 output rows in one pass; plain:
-        // its 128 rows in two passes of 64.
+        // with constants.  GLU: the wave's 16*NBW output rows in one pass;
+        // plain: its 32*NBW rows in passes of 64.
         float* ep = reinterpret_cast<float*>(lds) + wave * (WT * G_EPI_PITCH);
-        const int row_base = GLU ? ((nt0 + wn * 8) >> 1) * 16 : (nt0 + wn * 8) * 16;
+        const int row_base = GLU ? ((nt0 + wn * 2 * NBW) >> 1) * 16 : (nt0 + wn * 2 * NBW) * 16;
+        constexpr int PASSES = GLU ? 1 : NBW / 2;   // passes of (up to) 64 rows
+        constexpr int NBP = GLU ? NBW : 2;          // 32-row blocks per pass
+        constexpr int PROWS = GLU ? 16 * NBW : 64;  // output rows per pass
         const int tok_base = m0 + wm * WT;
         const bool has_res = (a.flags & EP_RESIDUAL) != 0;
         const bool has_split = (a.flags & EP_SPLIT) != 0;
         const int sp_log = a.split_period > 0 ? 31 - __builtin_clz((unsigned)a.split_period) : 0;
         __syncthreads();  // every wave is done reading the K-loop stages
 #pragma unroll
-        for (int pass = 0; pass < (GLU ? 1 : 2); ++pass) {
+        for (int pass = 0; pass < PASSES; ++pass) {
 #pragma unroll
-            for (int nbl = 0; nbl < (GLU ? 4 : 2); ++nbl) {
+            for (int nbl = 0; nbl < NBP; ++nbl) {
                 const int nb = GLU ? nbl : pass * 2 + nbl;
-                const int pt0 = nt0 + wn * 8 + nb * 2;
+                const int pt0 = nt0 + wn * 2 * NBW + nb * 2;
 #pragma unroll
                 for (int qg = 0; qg < (GLU ? 2 : 4); ++qg) {
                     const int r0 = 8 * qg + ihi;
@@ -411,12 +420,12 @@ void gemm_kernel(GemmArgs a) {
             // wave-local hand-off: each wave reads back only what it wrote
             __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
             __builtin_amdgcn_wave_barrier();
-            const int c = lane & 15;  // rows 4c .. 4c+3
+            const int c = lane & 15;  // rows 4c .. 4c+3 (PROWS of them exist)
             const int row = row_base + pass * 64 + 4 * c;
             for (int it = 0; it < WT / 4; ++it) {
                 const int jj = it * 4 + (lane >> 4);
                 const int m = tok_base + jj;
-                if (m < a.M && row < a.N) {
+                if (m < a.M && row < a.N && 4 * c < PROWS) {
                     f32x4 o4 = *reinterpret_cast<const f32x4*>(ep + jj * G_EPI_PITCH + 4 * c);
                     if (a.vec_store) {
                         if (has_res) o4 += load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + row);
@@ -432,7 +441,7 @@ void gemm_kernel(GemmArgs a) {
                     }
                 }
             }
-            if (!GLU && pass == 0) {
+            if (!GLU && pass + 1 < PASSES) {
                 __builtin_amdgcn_s_waitcnt(0xc07f);
                 __builtin_amdgcn_wave_barrier();
             }
@@ -453,27 +462,34 @@ static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, int threads
     return hipGetLastError();
 }
 
-template <int WF, int XDT, int BM, int NW>
+template <int WF, int XDT, int BM, int NW, int RW>
 static hipError_t launch_bm(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
     const int grid = a.nblk_n * a.nblk_m;
-    const size_t lds = GTile<BM, NW, WF>::lds_bytes();
-    if (argmax) return launch_gemm_k(gemm_kernel<WF, XDT, false, true, BM, NW>, a, grid, NW * 64, lds, stream);
-    if (glu) return launch_gemm_k(gemm_kernel<WF, XDT, true, false, BM, NW>, a, grid, NW * 64, lds, stream);
-    return launch_gemm_k(gemm_kernel<WF, XDT, false, false, BM, NW>, a, grid, NW * 64, lds, stream);
+    const size_t lds = GTile<BM, NW, WF, RW>::lds_bytes();
+    if (argmax) return launch_gemm_k(gemm_kernel<WF, XDT, false, true, BM, NW, RW>, a, grid, NW * 64, lds, stream);
+    if (glu) return launch_gemm_k(gemm_kernel<WF, XDT, true, false, BM, NW, RW>, a, grid, NW * 64, lds, stream);
+    return launch_gemm_k(gemm_kernel<WF, XDT, false, false, BM, NW, RW>, a, grid, NW * 64, lds, stream);
 }
 
-// Block shapes: BF16 weights 256 x 256 (8 or 4 waves) or 256 x 128 (4 waves,
-// two workgroups per CU); INT8 weights 256 x 256 or 256 x 128, 8 waves.
+// Block shapes (rows x tokens, waves): BF16 weights 256 x 256 (8 or 4 waves),
+// 256 x 128 (4 waves, two workgroups per CU); INT8 weights 256 x 256 and
+// 256 x 128 (8 waves); both formats 64 x 128 (4 waves, each 64 x 32) for
+// few tokens on few weight rows, where 256-row blocks leave CUs idle.
 template <int WF, int XDT>
 static hipError_t launch_wf(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
+    if (a.rows == 64) {
+        if (a.tile_m != 128 || a.nblk_m != (a.M + 127) / 128) return hipErrorInvalidValue;
+        return launch_bm<WF, XDT, 128, 4, 64>(a, glu, argmax, stream);
+    }
+    if (a.rows != 256) return hipErrorInvalidValue;
     if (a.tile_m == 256 && a.nblk_m == (a.M + 255) / 256) {
-        if (a.waves == 8) return launch_bm<WF, XDT, 256, 8>(a, glu, argmax, stream);
-        if constexpr (WF == WF_BF16) return launch_bm<WF, XDT, 256, 4>(a, glu, argmax, stream);
+        if (a.waves == 8) return launch_bm<WF, XDT, 256, 8, 256>(a, glu, argmax, stream);
+        if constexpr (WF == WF_BF16) return launch_bm<WF, XDT, 256, 4, 256>(a, glu, argmax, stream);
         return hipErrorInvalidValue;
     }
     if (a.tile_m == 128 && a.nblk_m == (a.M + 127) / 128) {
-        if constexpr (WF == WF_I8) return launch_bm<WF, XDT, 128, 8>(a, glu, argmax, stream);
-        else return launch_bm<WF, XDT, 128, 4>(a, glu, argmax, stream);
+        if constexpr (WF == WF_I8) return launch_bm<WF, XDT, 128, 8, 256>(a, glu, argmax, stream);
+        else return launch_bm<WF, XDT, 128, 4, 256>(a, glu, argmax, stream);
     }
     return hipErrorInvalidValue;
 }

@@ -70,7 +70,8 @@ struct GemmArgs {
     const void* x;           // activations [M][ldx]
     int ldx;
     int M, K, N;             // N: logical output rows
-    int nblk_n, nblk_m;      // block grid: 256 weight rows x tile_m tokens
+    int nblk_n, nblk_m;      // block grid: `rows` weight rows x tile_m tokens
+    int rows;                // weight rows per block: 256, or 64 (tile_m 128)
     int tile_m;              // tokens per block: 256 or 128
     int waves;               // waves per workgroup: 4, or 8 (tile_m 256 only)
     unsigned flags;
