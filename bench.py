@@ -385,6 +385,8 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
 
     extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
 
+    extra.update(run_gdn(qw, ctx, torch, timer, stream, randn, args))
+
     # config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each
     for fmt, name in ((qw.WFMT_BF16, "bf16"), (qw.WFMT_INT8, "int8")):
         Es = []
@@ -408,6 +410,70 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         del Es
     torch.cuda.synchronize()
     return extra
+
+
+def run_gdn(qw, ctx, torch, timer, stream, randn, args):
+    """Gated-DeltaNet decode (the next row after the projections): one token
+    of each of B sequences through the 18 linear-attention layers, (a) the
+    step between the projections alone (conv1d, gates, delta rule on the FP32
+    state, norm-gate), and (b) the whole layer: the stacked QKV+Z+a+b
+    projection (FP32 out), the step (BF16 out), the out projection with the
+    residual add.  BF16 weights.  Bytes: the state is read and written
+    (2 x 16 x 128 x 128 x 4 per sequence) plus the conv state; the layer adds
+    its weights (8224 x 1024 + 1024 x 2048, BF16)."""
+    NH, KD, VD, K = 16, 128, 128, 4
+    CD = 2 * NH * KD + NH * VD
+    NIN = CD + NH * VD + 2 * NH
+    layers = []
+    for li in range(len(LINEAR_LAYERS)):
+        parts = [randn(n, H, std=0.02) for n in (CD, NH * VD, NH, NH)]
+        L = {"in": qw.Weight.pack_concat_device(ctx, parts, qw.WFMT_BF16)}
+        del parts
+        o = randn(H, NH * VD, std=0.02)
+        L["out"] = qw.Weight.pack_device(ctx, o, qw.WFMT_BF16)
+        del o
+        L["conv_w"] = randn(CD, K, std=0.5, dtype=torch.float32)
+        L["A_log"] = randn(NH, std=0.5, dtype=torch.float32)
+        L["dt_bias"] = randn(NH, std=0.5, dtype=torch.float32)
+        L["norm_w"] = 1.0 + randn(VD, std=0.1, dtype=torch.float32)
+        layers.append(L)
+    out = {}
+    for B in (1, 32):
+        x = randn(B, H)
+        res = randn(B, H)
+        row = torch.empty(B, NIN, device="cuda", dtype=torch.float32)
+        core = torch.empty(B, NH * VD, device="cuda", dtype=torch.bfloat16)
+        for L in layers:
+            L["cs"] = torch.zeros(B, CD, K - 1, device="cuda")
+            L["rs"] = randn(B, NH, KD * VD, std=0.1, dtype=torch.float32)
+        qw.linear(ctx, layers[0]["in"], x, row)
+        torch.cuda.synchronize()
+
+        def step(L):
+            qw.gdn_decode(ctx, L["conv_w"], L["A_log"], L["dt_bias"], L["norm_w"], row[:, :CD],
+                          row[:, CD:CD + NH * VD], row[:, CD + NH * VD:CD + NH * VD + NH],
+                          row[:, CD + NH * VD + NH:], L["cs"], L["rs"], core, NH)
+
+        def layer_body():
+            for L in layers:
+                qw.linear(ctx, L["in"], x, row)
+                step(L)
+                qw.linear(ctx, L["out"], core, res, residual=res)
+
+        g1 = graphed(qw, ctx, stream, lambda: [step(L) for L in layers])
+        us = 1e3 * timer.run(g1.launch, max(3, args.steps // 5), 1) / len(layers)
+        sb = B * (NH * KD * VD * 4 * 2 + CD * (K - 1) * 4 * 2)
+        out[f"gdn_step_B{B}"] = {"us_per_layer": round(us, 2), "GBps": round(sb / us / 1e3, 1),
+                                 "pct_hbm": round(100 * sb / us / 1e3 / HBM_PEAK, 1)}
+        g2 = graphed(qw, ctx, stream, layer_body)
+        us2 = 1e3 * timer.run(g2.launch, max(3, args.steps // 5), 1) / len(layers)
+        lb = sb + (NIN * H + H * NH * VD) * 2
+        out[f"gdn_layer_decode_B{B}"] = {"us_per_layer": round(us2, 2), "GBps": round(lb / us2 / 1e3, 1),
+                                         "tok_per_s_18_layers": round(B / (us2 * len(layers) * 1e-6), 1)}
+        log("gdn", B, out[f"gdn_step_B{B}"], out[f"gdn_layer_decode_B{B}"])
+        del g1, g2
+    del layers
+    return out
 
 
 def run_prefill(qw, ctx, torch, timer, stream, randn, args, M=16384):

@@ -224,6 +224,42 @@ qw_status qw_residual_rmsnorm(qw_ctx* ctx, const void* residual_in, const void* 
 qw_status qw_silu_mul(qw_ctx* ctx, const void* g, const void* u, void* h, qw_dtype dt, int64_t n,
                       hipStream_t stream);
 
+/* ---- Gated-DeltaNet decode step ---------------------------------------------------
+ * Everything between the input projections and the out projection of a
+ * linear-attention layer, one token for each of `batch` sequences:
+ * causal conv1d (+SiLU) over the QKV channels with the conv-state shift,
+ * per-head L2 norm of q (times 1/sqrt(key_dim)) and k, beta = sigmoid(b),
+ * g = -exp(A_log) * softplus(a + dt_bias), the delta rule on the FP32
+ * recurrent state (S *= exp(g); S += beta * k (v - S^T k)^T; o = S^T q), and
+ * the per-head RMSNorm (eps 1e-6) times norm_weight times SiLU(z).
+ * Replaces the core of LinearAttention::forward (language_linear_attn.cpp:
+ * 143-256) and the kernel chain of CudaLinearAttention::forward
+ * (conv1d_update_fused / l2norm_qk_fused / gated_delta / norm_gate_fused,
+ * linear_attention_cuda.cu:47-172, launched at :486-530).
+ * Inputs, one row per sequence with stride ld_in elements (typically the rows
+ * of one stacked [QKV | Z | a | b] projection output): mixed_qkv
+ * [2*nh*kd + nh*vd] (all q, then all k, then all v), z [nh*vd], a [nh],
+ * b [nh], all in in_dtype (F32, BF16 or F16).  Parameters (FP32, device):
+ * conv_weight [conv_dim][conv_kernel], A_log [nh], dt_bias [nh],
+ * norm_weight [vd].  States (FP32, device, updated in place, the reference
+ * layouts): conv_state [batch][conv_dim][conv_kernel-1] (index 0 the newest
+ * input; may be NULL when conv_kernel is 1), recurrent_state [batch][nh][kd][vd].  out [batch][ld_out] receives
+ * nh*vd values.  key_dim = value_dim = 128, 1 <= conv_kernel <= 8. */
+typedef struct {
+    int num_heads;
+    int key_dim;
+    int value_dim;
+    int conv_kernel;
+    const float* conv_weight;
+    const float* A_log;
+    const float* dt_bias;
+    const float* norm_weight;
+} qw_gdn_params;
+qw_status qw_gdn_decode(qw_ctx* ctx, const qw_gdn_params* p, int batch, const void* mixed_qkv,
+                        const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
+                        float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype,
+                        int ld_out, hipStream_t stream);
+
 /* ---- graphs --------------------------------------------------------------------
  * Capture a sequence of qw_* calls on `stream` into a replayable HIP graph
  * (the role of cudaStreamBeginCapture/cudaGraphLaunch in

@@ -64,6 +64,8 @@ def lib():
             "orc_fill_uniform": [_f32p, _i64, ctypes.c_uint64, _fl, _fl],
             "orc_fill_int8_uniform": [_i8p, _i64, ctypes.c_uint64, _i, _i],
             "orc_silu": [_fl],
+            "orc_gdn_step": [_i, _i, _i, _i, _i, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                             _f32p, _f32p, _f32p],
             "orc_mt64_raw": [ctypes.c_uint64, np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"), _i64],
         }
         for name, args in sig.items():
@@ -94,6 +96,8 @@ def ref_lib():
         R.ref_mlp_time.restype = ctypes.c_double
         R.ref_lmhead_time.argtypes = [_f32p, _f32p, _i, _i, _i, ctypes.c_void_p]
         R.ref_lmhead_time.restype = ctypes.c_double
+        R.ref_linear_attn.argtypes = [_f32p, _f32p] + [_i] * 6 + [_f32p] * 11
+        R.ref_linear_attn.restype = ctypes.c_int
         _REF = R
     return _REF
 
@@ -305,3 +309,38 @@ def mt64_raw(seed, n):
     out = np.empty(n, np.uint64)
     lib().orc_mt64_raw(seed, out, n)
     return out
+
+
+# ---- Gated-DeltaNet decode step --------------------------------------------
+def gdn_step(mixed, a, b, z, conv_w, A_log, dt_bias, norm_w, conv_state, rec_state, nh, kd, vd):
+    """One token per sequence through the step between the projections of
+    LinearAttention::forward (language_linear_attn.cpp:143-256).  Returns
+    (out [B][nh*vd], conv_state, rec_state), the states as new arrays."""
+    mixed = _c(np.atleast_2d(mixed), np.float32)
+    B = mixed.shape[0]
+    K = conv_w.shape[1]
+    cs = _c(conv_state, np.float32).copy()
+    rs = _c(rec_state, np.float32).copy()
+    out = np.empty((B, nh * vd), np.float32)
+    lib().orc_gdn_step(B, nh, kd, vd, K, mixed, _c(a, np.float32), _c(b, np.float32), _c(z, np.float32),
+                       _c(conv_w, np.float32), _c(A_log, np.float32), _c(dt_bias, np.float32),
+                       _c(norm_w, np.float32), cs, rs, out)
+    return out, cs, rs
+
+
+def ref_linear_attn(x, Wqkv, Wa, Wb, Wz, conv_w, A_log, dt_bias, norm_w, Wout, conv_state, rec_state,
+                    nh, kd, vd):
+    """The reference's own LinearAttention::forward over the T rows of x (one
+    sequence); (y [T][H], conv_state, rec_state)."""
+    R = ref_lib()
+    x = _c(np.atleast_2d(x), np.float32)
+    T, H = x.shape
+    y = np.empty((T, H), np.float32)
+    cs = _c(conv_state, np.float32).copy()
+    rs = _c(rec_state, np.float32).copy()
+    rc = R.ref_linear_attn(x, y, T, H, nh, kd, vd, conv_w.shape[1], _c(Wqkv, np.float32), _c(Wa, np.float32),
+                           _c(Wb, np.float32), _c(Wz, np.float32), _c(conv_w, np.float32), _c(A_log, np.float32),
+                           _c(dt_bias, np.float32), _c(norm_w, np.float32), _c(Wout, np.float32), cs, rs)
+    if rc != 0:
+        raise RuntimeError("reference LinearAttention raised")
+    return y, cs, rs

@@ -440,3 +440,94 @@ void orc_fill_int8_uniform(int8_t* dst, int64_t n, uint64_t seed, int lo, int hi
     uint64_t span = (uint64_t)(hi - lo + 1);
     for (int64_t i = 0; i < n; ++i) dst[i] = (int8_t)(lo + (int)(mt64_next(&g) % span));
 }
+
+/* ------------------------------------------------------------------------
+ * Gated-DeltaNet decode step: everything between the input projections and
+ * the out projection of LinearAttention::forward
+ * (src/backend/cpu/core/attention/language_linear_attn.cpp:143-256), in that
+ * file's operation order, one token per sequence for B sequences:
+ *   1. causal conv1d over the conv_dim = 2*nh*kd + nh*vd QKV channels with
+ *      the reference's tap order (w[d][K-1] on the current input, w[d][j] on
+ *      conv_state[d][j], j < K-1, state[d][0] the newest), SiLU; then the
+ *      state shift (:144-157);
+ *   2. beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias) (:166-174);
+ *   3. per head: q /= sqrt(sum q^2 + 1e-6) then * 1/sqrt(kd); k likewise
+ *      without the scale (:176-200);
+ *   4. per head the delta rule on S[kd][vd]: S *= exp(g); kv = S^T k;
+ *      delta = (v - kv) * beta; S += k delta^T; o = S^T q (:202-234);
+ *   5. per head RMSNorm of o (eps 1e-6) times norm_w, times SiLU(z) (:236-251).
+ * Layouts: mixed [B][conv_dim], a/b [B][nh], z [B][nh*vd], conv_w
+ * [conv_dim][K], conv_state [B][conv_dim][K-1], rec_state [B][nh][kd][vd],
+ * out [B][nh*vd].  The states are updated in place.
+ * ------------------------------------------------------------------------ */
+static float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+static float orc_softplus(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+void orc_gdn_step(int B, int nh, int kd, int vd, int K, const float* mixed, const float* a, const float* b,
+                  const float* z, const float* conv_w, const float* A_log, const float* dt_bias,
+                  const float* norm_w, float* conv_state, float* rec_state, float* out) {
+    const int conv_dim = 2 * nh * kd + nh * vd;
+    const int sl = K - 1;
+    float* co = (float*)malloc(sizeof(float) * (size_t)conv_dim);
+    float* kv = (float*)malloc(sizeof(float) * (size_t)vd);
+    float* de = (float*)malloc(sizeof(float) * (size_t)vd);
+    const float q_scale = 1.0f / sqrtf((float)kd);
+    for (int bi = 0; bi < B; ++bi) {
+        const float* mx = mixed + (size_t)bi * conv_dim;
+        float* cs = conv_state + (size_t)bi * conv_dim * sl;
+        for (int d = 0; d < conv_dim; ++d) {
+            float sum = conv_w[(size_t)d * K + (K - 1)] * mx[d];
+            for (int j = 0; j < sl; ++j) sum += conv_w[(size_t)d * K + j] * cs[(size_t)d * sl + j];
+            co[d] = orc_silu(sum);
+        }
+        for (int d = 0; d < conv_dim; ++d) {
+            for (int j = sl - 1; j > 0; --j) cs[(size_t)d * sl + j] = cs[(size_t)d * sl + j - 1];
+            if (sl > 0) cs[(size_t)d * sl] = mx[d];
+        }
+        float* q = co;
+        float* k = co + nh * kd;
+        const float* v = co + 2 * nh * kd;
+        float* o = out + (size_t)bi * nh * vd;
+        const float* zz = z + (size_t)bi * nh * vd;
+        for (int h = 0; h < nh; ++h) {
+            float ql = 0.0f, kl = 0.0f;
+            for (int d = 0; d < kd; ++d) ql += q[h * kd + d] * q[h * kd + d];
+            ql = sqrtf(ql + 1e-6f);
+            for (int d = 0; d < kd; ++d) q[h * kd + d] = q[h * kd + d] / ql * q_scale;
+            for (int d = 0; d < kd; ++d) kl += k[h * kd + d] * k[h * kd + d];
+            kl = sqrtf(kl + 1e-6f);
+            for (int d = 0; d < kd; ++d) k[h * kd + d] = k[h * kd + d] / kl;
+        }
+        for (int h = 0; h < nh; ++h) {
+            const float beta = orc_sigmoid(b[(size_t)bi * nh + h]);
+            const float g = -expf(A_log[h]) * orc_softplus(a[(size_t)bi * nh + h] + dt_bias[h]);
+            const float gt = expf(g);
+            float* S = rec_state + ((size_t)bi * nh + h) * kd * vd;
+            for (int i = 0; i < kd * vd; ++i) S[i] *= gt;
+            for (int c = 0; c < vd; ++c) {
+                float acc = 0.0f;
+                for (int r = 0; r < kd; ++r) acc += S[r * vd + c] * k[h * kd + r];
+                kv[c] = acc;
+            }
+            for (int c = 0; c < vd; ++c) de[c] = (v[h * vd + c] - kv[c]) * beta;
+            for (int r = 0; r < kd; ++r)
+                for (int c = 0; c < vd; ++c) S[r * vd + c] += k[h * kd + r] * de[c];
+            for (int c = 0; c < vd; ++c) {
+                float acc = 0.0f;
+                for (int r = 0; r < kd; ++r) acc += S[r * vd + c] * q[h * kd + r];
+                o[h * vd + c] = acc;
+            }
+        }
+        for (int h = 0; h < nh; ++h) {
+            float var = 0.0f;
+            for (int c = 0; c < vd; ++c) var += o[h * vd + c] * o[h * vd + c];
+            var /= (float)vd;
+            const float inv = 1.0f / sqrtf(var + 1e-6f);
+            for (int c = 0; c < vd; ++c) o[h * vd + c] = o[h * vd + c] * inv * norm_w[c];
+        }
+        for (int i = 0; i < nh * vd; ++i) o[i] = o[i] * orc_silu(zz[i]);
+    }
+    free(co);
+    free(kv);
+    free(de);
+}

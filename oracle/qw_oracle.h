@@ -98,7 +98,15 @@ void orc_fill_normal(float* dst, int64_t n, uint64_t seed, float mean, float std
 void orc_fill_uniform(float* dst, int64_t n, uint64_t seed, float lo, float hi);
 void orc_fill_int8_uniform(int8_t* dst, int64_t n, uint64_t seed, int lo, int hi);
 
+/* Gated-DeltaNet decode step between the projections
+ * (language_linear_attn.cpp:143-256); see qw_oracle.c. */
+void orc_gdn_step(int B, int nh, int kd, int vd, int K, const float* mixed, const float* a, const float* b,
+                  const float* z, const float* conv_w, const float* A_log, const float* dt_bias,
+                  const float* norm_w, float* conv_state, float* rec_state, float* out);
+
+
 #ifdef __cplusplus
 }
 #endif
 #endif
+

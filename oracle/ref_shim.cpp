@@ -8,10 +8,12 @@
 //   qwen::MLP      src/backend/cpu/core/mlp/language_mlp.hpp:7-36
 //   qwen::Sampler  src/backend/cpu/core/heads/sampler.hpp        (GREEDY)
 //   qwen::RMSNorm  src/backend/cpu/core/common/language_common.hpp:9-33
+//   qwen::LinearAttention  src/backend/cpu/core/attention/language_linear_attn.hpp:7-90
 #include <chrono>
 #include <exception>
 #include <vector>
 
+#include "language_linear_attn.hpp"
 #include "language_mlp.hpp"
 #include "language_common.hpp"
 #include "lm_head.hpp"
@@ -100,6 +102,45 @@ int ref_rmsnorm(const float* x, const float* w, float* y, int M, int K, float ep
         qwen::RMSNorm norm(K, eps);
         norm.set_weight(std::vector<float>(w, w + K));
         norm.forward_batch(x, y, M);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+// T tokens of one sequence through LinearAttention::forward (the whole
+// Gated-DeltaNet layer: projections, conv, gates, delta rule, norm-gate, out
+// projection), starting from the given conv state [conv_dim][K-1] and
+// recurrent state [nh][kd*vd]; both are returned updated.
+int ref_linear_attn(const float* x, float* y, int T, int H, int nh, int kd, int vd, int K,
+                    const float* Wqkv, const float* Wa, const float* Wb, const float* Wz,
+                    const float* conv_w, const float* A_log, const float* dt_bias, const float* norm_w,
+                    const float* Wout, float* conv_state, float* rec_state) {
+    try {
+        const int conv_dim = 2 * nh * kd + nh * vd;
+        qwen::LinearAttention la(H, nh, kd, vd, K);
+        la.set_weights(std::vector<float>(Wqkv, Wqkv + (size_t)conv_dim * H),
+                       std::vector<float>(Wa, Wa + (size_t)nh * H), std::vector<float>(Wb, Wb + (size_t)nh * H),
+                       std::vector<float>(Wz, Wz + (size_t)nh * vd * H),
+                       std::vector<float>(conv_w, conv_w + (size_t)conv_dim * K),
+                       std::vector<float>(A_log, A_log + nh), std::vector<float>(dt_bias, dt_bias + nh),
+                       std::vector<float>(norm_w, norm_w + vd),
+                       std::vector<float>(Wout, Wout + (size_t)H * nh * vd));
+        qwen::LinearAttnState st;
+        st.reset(nh, kd, vd, K);
+        for (int d = 0; d < conv_dim; ++d)
+            for (int j = 0; j < K - 1; ++j) st.conv_state[d][j] = conv_state[(size_t)d * (K - 1) + j];
+        for (int h = 0; h < nh; ++h)
+            for (int i = 0; i < kd * vd; ++i) st.recurrent_state[h][i] = rec_state[(size_t)h * kd * vd + i];
+        for (int t = 0; t < T; ++t) {
+            std::vector<float> in(x + (size_t)t * H, x + (size_t)(t + 1) * H);
+            std::vector<float> out = la.forward(in, st);
+            for (int i = 0; i < H; ++i) y[(size_t)t * H + i] = out[i];
+        }
+        for (int d = 0; d < conv_dim; ++d)
+            for (int j = 0; j < K - 1; ++j) conv_state[(size_t)d * (K - 1) + j] = st.conv_state[d][j];
+        for (int h = 0; h < nh; ++h)
+            for (int i = 0; i < kd * vd; ++i) rec_state[(size_t)h * kd * vd + i] = st.recurrent_state[h][i];
         return 0;
     } catch (const std::exception&) {
         return -1;

@@ -818,6 +818,47 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
                       kSkinnyMaxM);
 }
 
+qw_status qw_gdn_decode(qw_ctx* ctx, const qw_gdn_params* p, int batch, const void* mixed_qkv,
+                        const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
+                        float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype,
+                        int ld_out, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!p || !mixed_qkv || !z || !a || !b || !recurrent_state || !out || !p->conv_weight || !p->A_log ||
+        !p->dt_bias || !p->norm_weight || (!conv_state && p->conv_kernel > 1))
+        return fail(ctx, QW_ERR_NULL, "gdn: NULL argument");
+    if (batch < 1) return fail(ctx, QW_ERR_SHAPE, "gdn: batch=%d must be >= 1", batch);
+    if (p->num_heads < 1 || p->key_dim != 128 || p->value_dim != 128 || p->conv_kernel < 1 || p->conv_kernel > 8)
+        return fail(ctx, QW_ERR_SHAPE, "gdn: needs key_dim = value_dim = 128, 1 <= conv_kernel <= 8 (got %d, %d, %d)",
+                    p->key_dim, p->value_dim, p->conv_kernel);
+    if (!valid_act(in_dtype) || !valid_act(out_dtype)) return fail(ctx, QW_ERR_DTYPE, "gdn: dtype unsupported");
+    const int vdim = p->num_heads * p->value_dim;
+    if (ld_in < 1 || ld_out < vdim) return fail(ctx, QW_ERR_SHAPE, "gdn: ld_in=%d, ld_out=%d < %d", ld_in, ld_out, vdim);
+    qwk::GdnArgs g{};
+    g.B = batch;
+    g.nh = p->num_heads;
+    g.kd = p->key_dim;
+    g.vd = p->value_dim;
+    g.K = p->conv_kernel;
+    g.mixed = mixed_qkv;
+    g.z = z;
+    g.a = a;
+    g.b = b;
+    g.in_dt = (int)in_dtype;
+    g.ld_in = ld_in;
+    g.conv_w = p->conv_weight;
+    g.A_log = p->A_log;
+    g.dt_bias = p->dt_bias;
+    g.norm_w = p->norm_weight;
+    g.conv_state = conv_state;
+    g.rec_state = recurrent_state;
+    g.out = out;
+    g.out_dt = (int)out_dtype;
+    g.ld_out = ld_out;
+    hipError_t e = qwk::launch_gdn_decode(g, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gdn decode launch");
+    return QW_OK;
+}
+
 qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,
                        qw_dtype xdt, const float* gamma, float eps, const void* residual,
                        qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream) {

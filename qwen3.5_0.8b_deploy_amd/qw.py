@@ -31,8 +31,21 @@ EXPORTS = [
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
-    "qw_silu_mul", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
+    "qw_silu_mul", "qw_gdn_decode", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
+
+
+class GdnParams(ctypes.Structure):
+    _fields_ = [
+        ("num_heads", ctypes.c_int),
+        ("key_dim", ctypes.c_int),
+        ("value_dim", ctypes.c_int),
+        ("conv_kernel", ctypes.c_int),
+        ("conv_weight", ctypes.c_void_p),
+        ("A_log", ctypes.c_void_p),
+        ("dt_bias", ctypes.c_void_p),
+        ("norm_weight", ctypes.c_void_p),
+    ]
 
 
 class Epilogue(ctypes.Structure):
@@ -88,6 +101,8 @@ def lib():
         "qw_weight_unpack": ([_vp, _vp, _vp, _vp], _i),
         "qw_linear": ([_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, ctypes.POINTER(Epilogue), _vp], _i),
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
+        "qw_gdn_decode": ([_vp, ctypes.POINTER(GdnParams), _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i,
+                           _vp], _i),
         "qw_device_error": ([_vp, _vp], _i),
         "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
         "qw_argmax_rows": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
@@ -399,3 +414,18 @@ class Graph:
                 lib().qw_graph_destroy(self._h)
         except Exception:
             pass
+
+
+def gdn_decode(ctx, conv_weight, A_log, dt_bias, norm_weight, mixed, z, a, b, conv_state, recurrent_state, out,
+               num_heads, key_dim=128, value_dim=128, ld_in=0, ld_out=0, stream=None):
+    """Gated-DeltaNet decode step for the rows (sequences) of mixed/z/a/b
+    (views into one projection output share its row stride); the FP32
+    states are updated in place; out [B][>= num_heads*value_dim]."""
+    p = GdnParams(num_heads, key_dim, value_dim, conv_weight.shape[1], conv_weight.data_ptr(), A_log.data_ptr(),
+                  dt_bias.data_ptr(), norm_weight.data_ptr())
+    B = mixed.shape[0]
+    ld_in = ld_in or mixed.stride(0)
+    ld_out = ld_out or out.stride(0)
+    ctx.check(lib().qw_gdn_decode(ctx.handle, ctypes.byref(p), B, _ptr(mixed), _ptr(z), _ptr(a), _ptr(b),
+                                  _torch_code(mixed), ld_in, _ptr(conv_state), _ptr(recurrent_state), _ptr(out),
+                                  _torch_code(out), ld_out, _stream(stream)))

@@ -10,6 +10,9 @@ Vectors:
                     (src/backend/cpu/core/mlp/language_mlp.cpp:93-127)
                   - Sampler::sample greedy (src/backend/cpu/core/heads/sampler.cpp:41-43)
                     on logits with planted exact ties
+                  - LinearAttention::forward, 3 tokens of one sequence from
+                    non-zero conv / recurrent states
+                    (src/backend/cpu/core/attention/language_linear_attn.cpp:125-257)
   quant.npz     the INT8 per-row quantize recipe
                 (src/backend/cuda/kernels/mlp_cuda.cu:22-39) worked by hand
                 on rows that hit each of its cases; no code computes these
@@ -57,6 +60,21 @@ def ref_ops():
             L[r, s] = 9.5
         ids.append(R.ref_greedy(np.ascontiguousarray(L[r]), L.shape[1]))
     out.update(greedy_logits=L, greedy_ids=np.array(ids, np.int32))
+    # Gated-DeltaNet layer (small dims): projections, conv, gates, delta rule,
+    # norm-gate and out projection of the reference, over 3 tokens
+    H, nh, kd, vd, K, T = 64, 2, 8, 8, 4, 3
+    cd = 2 * nh * kd + nh * vd
+    g = dict(Wqkv=oracle.normal((cd, H), 41, 0.0, 0.2), Wa=oracle.normal((nh, H), 42, 0.0, 0.2),
+             Wb=oracle.normal((nh, H), 43, 0.0, 0.2), Wz=oracle.normal((nh * vd, H), 44, 0.0, 0.2),
+             conv_w=oracle.normal((cd, K), 45, 0.0, 0.5), A_log=oracle.normal((nh,), 46, 0.0, 0.5),
+             dt_bias=oracle.normal((nh,), 47, 0.0, 0.5), norm_w=1.0 + oracle.normal((vd,), 48, 0.0, 0.1),
+             Wout=oracle.normal((H, nh * vd), 49, 0.0, 0.2), conv_state=oracle.normal((cd, K - 1), 50),
+             rec_state=oracle.normal((nh, kd * vd), 51, 0.0, 0.3), x=oracle.normal((T, H), 52))
+    y, cs, rs = oracle.ref_linear_attn(g["x"], g["Wqkv"], g["Wa"], g["Wb"], g["Wz"], g["conv_w"], g["A_log"],
+                                       g["dt_bias"], g["norm_w"], g["Wout"], g["conv_state"], g["rec_state"],
+                                       nh, kd, vd)
+    out.update({"gdn_" + k: v for k, v in g.items()})
+    out.update(gdn_y=y, gdn_conv_state_out=cs, gdn_rec_state_out=rs)
     np.savez_compressed(os.path.join(HERE, "ref_ops.npz"), **out)
 
 

@@ -1,0 +1,100 @@
+"""GPU parity of the Gated-DeltaNet decode step (qw_gdn_decode) against the
+CPU oracle (orc_gdn_step, pinned bit-exactly to the reference's own
+LinearAttention::forward in tests/test_oracle.py).
+
+Shapes: Qwen3.5-0.8B linear attention, 16 heads, key_dim = value_dim = 128,
+conv kernel 4 (also 1 and 2).  Several consecutive tokens run on the GPU
+with the states carried in place, and on the oracle with its own states.
+
+Bars: FP32 outputs and states <= 1e-5 normwise against the oracle (only the
+summation order of the column dot products and norms differs; the carried
+state accumulates that over the steps); the conv state is a pure copy, so it
+must match bit for bit; BF16 inputs/outputs: the oracle runs on the same
+rounded inputs and the output carries one BF16 rounding (<= 4e-3).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+NH, KD, VD = 16, 128, 128
+CD = 2 * NH * KD + NH * VD
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def _params(oracle, K, seed):
+    return dict(conv_w=oracle.normal((CD, K), seed, 0.0, 0.5), A_log=oracle.normal((NH,), seed + 1, 0.0, 0.5),
+                dt_bias=oracle.normal((NH,), seed + 2, 0.0, 0.5),
+                norm_w=1.0 + oracle.normal((VD,), seed + 3, 0.0, 0.1))
+
+
+@pytest.mark.parametrize("B,K,io", [(1, 4, "f32"), (3, 4, "f32"), (2, 1, "f32"), (2, 2, "f32"), (4, 4, "bf16")])
+def test_gdn_decode_parity(qw, ctx, oracle, relerr, B, K, io):
+    P = _params(oracle, K, 900 + K)
+    dP = {k: dev(v) for k, v in P.items()}
+    cs = oracle.normal((B, CD, max(K - 1, 0)), 910)
+    rs = oracle.normal((B, NH, KD * VD), 911, 0.0, 0.3)
+    dcs, drs = dev(cs), dev(rs)
+    tdt = torch.float32 if io == "f32" else torch.bfloat16
+    # one stacked projection output row per sequence: [mixed | z | a | b | pad]
+    ld = CD + NH * VD + 2 * NH + 8
+    for step in range(4):
+        row = oracle.normal((B, ld), 920 + step)
+        drow = dev(row, tdt)
+        mixed, z = drow[:, :CD], drow[:, CD:CD + NH * VD]
+        a, b = drow[:, CD + NH * VD:CD + NH * VD + NH], drow[:, CD + NH * VD + NH:CD + NH * VD + 2 * NH]
+        out = torch.empty(B, NH * VD, device="cuda", dtype=tdt)
+        qw.gdn_decode(ctx, dP["conv_w"], dP["A_log"], dP["dt_bias"], dP["norm_w"], mixed, z, a, b, dcs, drs, out,
+                      NH)
+        torch.cuda.synchronize()
+        r = host(drow)
+        o_ref, cs, rs = oracle.gdn_step(r[:, :CD], r[:, CD + NH * VD:CD + NH * VD + NH],
+                                        r[:, CD + NH * VD + NH:CD + NH * VD + 2 * NH], r[:, CD:CD + NH * VD],
+                                        P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], cs, rs, NH, KD, VD)
+        bar = 1e-5 if io == "f32" else 4e-3
+        assert relerr(host(out), o_ref) <= bar, (step, relerr(host(out), o_ref))
+        assert relerr(host(drs), rs) <= 1e-5, (step, relerr(host(drs), rs))
+        assert np.array_equal(host(dcs), cs)
+
+
+def test_gdn_decode_repeatable(qw, ctx, oracle):
+    """Fixed reduction orders: the same inputs and states give the same bits."""
+    B, K = 2, 4
+    P = {k: dev(v) for k, v in _params(oracle, K, 930).items()}
+    cs0 = dev(oracle.normal((B, CD, K - 1), 931))
+    rs0 = dev(oracle.normal((B, NH, KD * VD), 932, 0.0, 0.3))
+    row = dev(oracle.normal((B, CD + NH * VD + 2 * NH), 933))
+    outs, states = [], []
+    for _ in range(3):
+        cs, rs = cs0.clone(), rs0.clone()
+        out = torch.empty(B, NH * VD, device="cuda")
+        qw.gdn_decode(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], row[:, :CD],
+                      row[:, CD:CD + NH * VD], row[:, CD + NH * VD:CD + NH * VD + NH],
+                      row[:, CD + NH * VD + NH:], cs, rs, out, NH)
+        outs.append(out)
+        states.append(rs)
+    torch.cuda.synchronize()
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    assert all(torch.equal(states[0], s) for s in states[1:])
+
+
+def test_gdn_decode_errors(qw, ctx):
+    """Shapes the kernel does not cover are refused with a status, not run."""
+    P = {"conv_w": torch.zeros(2 * 4 * 64 + 4 * 64, 4, device="cuda"), "A_log": torch.zeros(4, device="cuda"),
+         "dt_bias": torch.zeros(4, device="cuda"), "norm_w": torch.ones(64, device="cuda")}
+    x = torch.zeros(1, 2048, device="cuda")
+    cs = torch.zeros(1, 768 * 3, device="cuda")
+    rs = torch.zeros(1, 4 * 64 * 64, device="cuda")
+    out = torch.empty(1, 256, device="cuda")
+    with pytest.raises(qw.QwError):
+        qw.gdn_decode(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], x, x, x, x, cs, rs, out,
+                      4, key_dim=64, value_dim=64)

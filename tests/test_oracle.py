@@ -276,3 +276,130 @@ def test_greedy_vs_ref_lib(oracle):
         v = oracle.normal(5000, 70 + seed)
         v[[seed * 7, 4000]] = 10.0
         assert oracle.argmax_first(v) == R.ref_greedy(v, v.size) == seed * 7
+
+
+# ---------------------------------------------------------------------------
+# Gated-DeltaNet decode step (language_linear_attn.cpp:143-256)
+# ---------------------------------------------------------------------------
+def gdn_f64(mixed, a, b, z, conv_w, A_log, dt_bias, norm_w, conv_state, rec_state, nh, kd, vd):
+    """Independent float64 restatement in matrix form (einsum per head), for
+    one token of each sequence: catches transposed state indices, a wrong
+    conv tap order or a missing gate -- the loop-order restatement in
+    qw_oracle.c shares none of this code."""
+    mixed, a, b, z = (np.atleast_2d(np.asarray(t, np.float64)) for t in (mixed, a, b, z))
+    B = mixed.shape[0]
+    K = conv_w.shape[1]
+    cs = np.asarray(conv_state, np.float64).reshape(B, -1, K - 1).copy()
+    rs = np.asarray(rec_state, np.float64).reshape(B, nh, kd, vd).copy()
+    w = np.asarray(conv_w, np.float64)
+    pre = w[:, K - 1][None, :] * mixed + np.einsum("dj,bdj->bd", w[:, :K - 1], cs)
+    co = pre / (1.0 + np.exp(-pre))
+    cs = np.concatenate([mixed[:, :, None], cs[:, :, :K - 2]], axis=2) if K > 1 else cs
+    q = co[:, :nh * kd].reshape(B, nh, kd)
+    k = co[:, nh * kd:2 * nh * kd].reshape(B, nh, kd)
+    v = co[:, 2 * nh * kd:].reshape(B, nh, vd)
+    q = q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6) / np.sqrt(kd)
+    k = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+    beta = 1.0 / (1.0 + np.exp(-b))
+    sp = np.log1p(np.exp(a + np.asarray(dt_bias, np.float64)))
+    g = -np.exp(np.asarray(A_log, np.float64)) * sp                     # [B][nh]
+    rs = rs * np.exp(g)[:, :, None, None]
+    kvm = np.einsum("bhkv,bhk->bhv", rs, k)
+    rs = rs + np.einsum("bhk,bhv->bhkv", k, (v - kvm) * beta[:, :, None])
+    o = np.einsum("bhkv,bhk->bhv", rs, q)
+    o = o / np.sqrt((o * o).mean(-1, keepdims=True) + 1e-6) * np.asarray(norm_w, np.float64)
+    o = o.reshape(B, nh * vd) * (z / (1.0 + np.exp(-z)))
+    return o, cs, rs.reshape(B, nh, kd * vd)
+
+
+def _gdn_case(oracle, B, nh, kd, vd, K, seed):
+    cd = 2 * nh * kd + nh * vd
+    return dict(mixed=oracle.normal((B, cd), seed), a=oracle.normal((B, nh), seed + 1),
+                b=oracle.normal((B, nh), seed + 2), z=oracle.normal((B, nh * vd), seed + 3),
+                conv_w=oracle.normal((cd, K), seed + 4, 0.0, 0.5), A_log=oracle.normal((nh,), seed + 5, 0.0, 0.5),
+                dt_bias=oracle.normal((nh,), seed + 6, 0.0, 0.5), norm_w=1.0 + oracle.normal((vd,), seed + 7, 0.0, 0.1),
+                conv_state=oracle.normal((B, cd, K - 1), seed + 8), rec_state=oracle.normal((B, nh, kd * vd), seed + 9, 0.0, 0.3))
+
+
+def test_gdn_matches_reference_golden(oracle):
+    """Projections (oracle linear) + the step + out projection reproduce the
+    reference's own LinearAttention::forward bit for bit over 3 tokens,
+    including both updated states (tests/golden/ref_ops.npz)."""
+    g = np.load(os.path.join(GOLDEN, "ref_ops.npz"))
+    nh, kd, vd = 2, 8, 8
+    cs, rs = g["gdn_conv_state"], g["gdn_rec_state"]
+    ys = []
+    for t in range(g["gdn_x"].shape[0]):
+        x = g["gdn_x"][t:t + 1]
+        mixed, a, b, z = (oracle.linear(g[n], x) for n in ("gdn_Wqkv", "gdn_Wa", "gdn_Wb", "gdn_Wz"))
+        o, cs, rs = oracle.gdn_step(mixed, a, b, z, g["gdn_conv_w"], g["gdn_A_log"], g["gdn_dt_bias"],
+                                    g["gdn_norm_w"], cs, rs, nh, kd, vd)
+        ys.append(oracle.linear(g["gdn_Wout"], o))
+    assert np.array_equal(np.concatenate(ys), g["gdn_y"])
+    assert np.array_equal(cs, g["gdn_conv_state_out"])
+    assert np.array_equal(rs.reshape(g["gdn_rec_state_out"].shape), g["gdn_rec_state_out"])
+
+
+def test_gdn_vs_ref_lib(oracle):
+    """Live reference build, Qwen3.5-0.8B head shape (nh 16, kd = vd = 128)."""
+    if oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    H, nh, kd, vd, K, T = 256, 16, 128, 128, 4, 2
+    cd = 2 * nh * kd + nh * vd
+    W = {n: oracle.normal(sh, 60 + i, 0.0, 0.05) for i, (n, sh) in enumerate(
+        [("Wqkv", (cd, H)), ("Wa", (nh, H)), ("Wb", (nh, H)), ("Wz", (nh * vd, H)), ("Wout", (H, nh * vd))])}
+    c = _gdn_case(oracle, 1, nh, kd, vd, K, 70)
+    x = oracle.normal((T, H), 80)
+    y_ref, cs_ref, rs_ref = oracle.ref_linear_attn(x, W["Wqkv"], W["Wa"], W["Wb"], W["Wz"], c["conv_w"], c["A_log"],
+                                                   c["dt_bias"], c["norm_w"], W["Wout"], c["conv_state"][0],
+                                                   c["rec_state"][0], nh, kd, vd)
+    cs, rs = c["conv_state"], c["rec_state"]
+    for t in range(T):
+        xt = x[t:t + 1]
+        o, cs, rs = oracle.gdn_step(oracle.linear(W["Wqkv"], xt), oracle.linear(W["Wa"], xt),
+                                    oracle.linear(W["Wb"], xt), oracle.linear(W["Wz"], xt), c["conv_w"],
+                                    c["A_log"], c["dt_bias"], c["norm_w"], cs, rs, nh, kd, vd)
+        assert np.array_equal(oracle.linear(W["Wout"], o)[0], y_ref[t])
+    assert np.array_equal(cs[0], cs_ref) and np.array_equal(rs[0], rs_ref)
+
+
+@pytest.mark.parametrize("B,nh,kd,vd,K", [(1, 2, 8, 8, 4), (3, 4, 16, 8, 4), (2, 16, 128, 128, 4), (2, 2, 8, 8, 2)])
+def test_gdn_vs_float64_matrix_form(oracle, relerr, B, nh, kd, vd, K):
+    c = _gdn_case(oracle, B, nh, kd, vd, K, 90 + K)
+    cs, rs, cs64, rs64 = c["conv_state"], c["rec_state"], c["conv_state"], c["rec_state"]
+    for step in range(3):
+        mixed = oracle.normal(c["mixed"].shape, 100 + step)
+        o, cs, rs = oracle.gdn_step(mixed, c["a"], c["b"], c["z"], c["conv_w"], c["A_log"], c["dt_bias"],
+                                    c["norm_w"], cs, rs, nh, kd, vd)
+        o64, cs64, rs64 = gdn_f64(mixed, c["a"], c["b"], c["z"], c["conv_w"], c["A_log"], c["dt_bias"],
+                                  c["norm_w"], cs64, rs64, nh, kd, vd)
+        assert relerr(o, o64) <= 1e-5
+        assert relerr(rs.reshape(rs64.shape), rs64) <= 1e-5
+        assert np.array_equal(cs.reshape(cs64.shape), cs64.astype(np.float32))   # pure copies
+
+
+def test_gdn_closed_forms(oracle):
+    """beta -> 0 (b = -80): the state only decays, S' = exp(g) S, and o is
+    S'^T q; a single last conv tap of 1: the conv output is silu(x)."""
+    B, nh, kd, vd, K = 1, 2, 8, 8, 4
+    c = _gdn_case(oracle, B, nh, kd, vd, K, 120)
+    c["b"][:] = -80.0
+    c["conv_w"][:] = 0.0
+    c["conv_w"][:, K - 1] = 1.0
+    c["norm_w"][:] = 1.0
+    c["z"][:] = 40.0                                   # silu(z) = z
+    o, cs, rs = oracle.gdn_step(c["mixed"], c["a"], c["b"], c["z"], c["conv_w"], c["A_log"], c["dt_bias"],
+                                c["norm_w"], c["conv_state"], c["rec_state"], nh, kd, vd)
+    x = c["mixed"][0].astype(np.float64)
+    co = x / (1 + np.exp(-x))
+    q = co[:nh * kd].reshape(nh, kd)
+    q = q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6) / np.sqrt(kd)
+    g = -np.exp(c["A_log"].astype(np.float64)) * np.log1p(np.exp(c["a"][0] + c["dt_bias"]))
+    S = c["rec_state"][0].reshape(nh, kd, vd).astype(np.float64) * np.exp(g)[:, None, None]
+    np.testing.assert_allclose(rs[0].reshape(nh, kd, vd), S, rtol=1e-5, atol=1e-7)
+    oo = np.einsum("hkv,hk->hv", S, q)
+    oo = oo / np.sqrt((oo * oo).mean(-1, keepdims=True) + 1e-6) * 40.0
+    np.testing.assert_allclose(o[0].reshape(nh, vd), oo, rtol=1e-4, atol=1e-5)
+    # conv state: newest first, the oldest tap dropped
+    assert np.array_equal(cs[0][:, 0], c["mixed"][0])
+    assert np.array_equal(cs[0][:, 1:], c["conv_state"][0][:, :K - 2])
