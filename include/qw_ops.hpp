@@ -11,6 +11,8 @@
 //   projection parts of CudaLinearAttention (linear_attention_cuda.hpp:24-90) and
 //   CudaFullAttention (full_attention_cuda.hpp:35-90)
 //                                       -> HipLinearAttnProjections / HipFullAttnProjections
+//   qwen::cuda::CudaLinearAttention / CudaLinearAttnState (whole decode layer,
+//   linear_attention_cuda.hpp:11-90)   -> HipLinearAttention / HipLinearAttnState
 //
 // Same argument meaning as the reference: weights arrive as host
 // std::vector<float> in row-major [out][in]; activations are caller-owned
@@ -327,6 +329,161 @@ class HipLinearAttnProjections {
     qw_wfmt fmt_;
     std::shared_ptr<Context> ctx_;
     detail::WeightPtr Wqkv_, Wz_, Wa_, Wb_, Wo_;
+};
+
+// ---------------------------------------------------------------------------
+// Recurrent and conv state of a Gated-DeltaNet layer (CudaLinearAttnState,
+// linear_attention_cuda.hpp:11-22): device FP32, recurrent state
+// [batch][nh][kd][vd], conv state [batch][conv_dim][conv_kernel-1]
+// (index 0 the newest input), conv_dim = 2*nh*kd + nh*vd.
+struct HipLinearAttnState {
+    float* d_recurrent_state = nullptr;
+    float* d_conv_state = nullptr;
+    int num_heads = 0, key_dim = 0, value_dim = 0, conv_dim = 0, conv_kernel = 0, batch = 0;
+
+    HipLinearAttnState() = default;
+    HipLinearAttnState(const HipLinearAttnState&) = delete;
+    HipLinearAttnState& operator=(const HipLinearAttnState&) = delete;
+    ~HipLinearAttnState() { release(); }
+
+    // (re)allocate for `batch_size` sequences and zero
+    void reset(int nh, int kd, int vd, int conv_k = 4, int batch_size = 1) {
+        release();
+        num_heads = nh;
+        key_dim = kd;
+        value_dim = vd;
+        conv_kernel = conv_k;
+        conv_dim = nh * (2 * kd + vd);
+        batch = batch_size;
+        if (hipMalloc(&d_recurrent_state, rec_bytes()) != hipSuccess ||
+            (conv_bytes() && hipMalloc(&d_conv_state, conv_bytes()) != hipSuccess))
+            throw Error(QW_ERR_HIP, "HipLinearAttnState::reset: hipMalloc");
+        clear();
+    }
+    void clear() {
+        if (hipMemset(d_recurrent_state, 0, rec_bytes()) != hipSuccess ||
+            (d_conv_state && hipMemset(d_conv_state, 0, conv_bytes()) != hipSuccess))
+            throw Error(QW_ERR_HIP, "HipLinearAttnState::clear: hipMemset");
+    }
+    size_t rec_bytes() const { return (size_t)batch * num_heads * key_dim * value_dim * sizeof(float); }
+    size_t conv_bytes() const { return (size_t)batch * conv_dim * (conv_kernel - 1) * sizeof(float); }
+
+  private:
+    void release() {
+        if (d_recurrent_state) (void)hipFree(d_recurrent_state);
+        if (d_conv_state) (void)hipFree(d_conv_state);
+        d_recurrent_state = d_conv_state = nullptr;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// A whole Gated-DeltaNet layer for decode (CudaLinearAttention,
+// linear_attention_cuda.hpp:24-90; CPU LinearAttention::forward,
+// language_linear_attn.cpp:125-257): one token per sequence,
+//   [qkv | z | a | b] = W_in . x      one stacked projection
+//   core = gated delta step(...)     qw_gdn_decode (conv, gates, state, norm-gate)
+//   output = W_out . core
+// set_weights takes the reference's arguments in the reference's order;
+// empty a_log / dt_bias / norm_weight default to 0 / 0 / 1 as there
+// (linear_attention_cuda.cu:450-464).  Default storage BF16.  The projection
+// and core buffers grow with the batch on first use (as the reference's
+// ensure_batch_buffers); the step itself allocates nothing.
+class HipLinearAttention {
+  public:
+    explicit HipLinearAttention(int hidden = 1024, int num_heads = 16, int key_dim = 128, int value_dim = 128,
+                                int conv_kernel = 4, qw_wfmt format = QW_WFMT_BF16,
+                                std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden), nh_(num_heads), kd_(key_dim), vd_(value_dim), K_(conv_kernel), fmt_(format),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {
+        conv_dim_ = nh_ * (2 * kd_ + vd_);
+        nin_ = conv_dim_ + nh_ * vd_ + 2 * nh_;
+    }
+    ~HipLinearAttention() {
+        for (float* p : {d_conv_w_, d_A_log_, d_dt_bias_, d_norm_w_, d_row_, d_core_})
+            if (p) (void)hipFree(p);
+    }
+    HipLinearAttention(const HipLinearAttention&) = delete;
+    HipLinearAttention& operator=(const HipLinearAttention&) = delete;
+
+    void set_weights(const std::vector<float>& in_proj_qkv_weight, const std::vector<float>& in_proj_a_weight,
+                     const std::vector<float>& in_proj_b_weight, const std::vector<float>& in_proj_z_weight,
+                     const std::vector<float>& conv1d_weight, const std::vector<float>& out_proj_weight,
+                     const std::vector<float>& a_log = {}, const std::vector<float>& dt_bias = {},
+                     const std::vector<float>& norm_weight = {}) {
+        const int H = hidden_;
+        check_size(in_proj_qkv_weight, (size_t)conv_dim_ * H, "in_proj_qkv");
+        check_size(in_proj_z_weight, (size_t)nh_ * vd_ * H, "in_proj_z");
+        check_size(in_proj_a_weight, (size_t)nh_ * H, "in_proj_a");
+        check_size(in_proj_b_weight, (size_t)nh_ * H, "in_proj_b");
+        check_size(conv1d_weight, (size_t)conv_dim_ * K_, "conv1d");
+        check_size(out_proj_weight, (size_t)H * nh_ * vd_, "out_proj");
+        const float* parts[4] = {in_proj_qkv_weight.data(), in_proj_z_weight.data(), in_proj_a_weight.data(),
+                                 in_proj_b_weight.data()};
+        const int Ns[4] = {conv_dim_, nh_ * vd_, nh_, nh_};
+        qw_weight* w = nullptr;
+        ctx_->check(qw_weight_pack_concat(ctx_->get(), 4, reinterpret_cast<const void* const*>(parts), Ns, QW_F32,
+                                          fmt_, H, nullptr, &w),
+                    "HipLinearAttention in_proj");
+        Win_.reset(w);
+        Wout_ = detail::pack(*ctx_, out_proj_weight, H, nh_ * vd_, fmt_, "out_proj");
+        upload(d_conv_w_, conv1d_weight, conv1d_weight.size());
+        upload(d_A_log_, a_log.empty() ? std::vector<float>(nh_, 0.0f) : a_log, nh_);
+        upload(d_dt_bias_, dt_bias.empty() ? std::vector<float>(nh_, 0.0f) : dt_bias, nh_);
+        upload(d_norm_w_, norm_weight.empty() ? std::vector<float>(vd_, 1.0f) : norm_weight, vd_);
+    }
+
+    void forward(const float* input, float* output, HipLinearAttnState& state, hipStream_t stream = nullptr) const {
+        forward_batch(input, output, state, 1, stream);
+    }
+
+    // input/output [batch][hidden] FP32 device; state sized for >= batch sequences
+    void forward_batch(const float* input, float* output, HipLinearAttnState& state, int batch_size,
+                       hipStream_t stream = nullptr) const {
+        detail::require(Wout_.get(), "HipLinearAttention::forward");
+        if (state.num_heads != nh_ || state.key_dim != kd_ || state.value_dim != vd_ || state.conv_kernel != K_ ||
+            state.batch < batch_size)
+            throw Error(QW_ERR_SHAPE, "HipLinearAttention::forward: state shape does not match");
+        ensure(batch_size);
+        ctx_->check(qw_linear(ctx_->get(), Win_.get(), input, QW_F32, 0, batch_size, d_row_, QW_F32, nin_, nullptr,
+                              stream),
+                    "HipLinearAttention in_proj");
+        qw_gdn_params p{nh_, kd_, vd_, K_, d_conv_w_, d_A_log_, d_dt_bias_, d_norm_w_};
+        const float* z = d_row_ + conv_dim_;
+        const float* a = z + nh_ * vd_;
+        const float* b = a + nh_;
+        ctx_->check(qw_gdn_decode(ctx_->get(), &p, batch_size, d_row_, z, a, b, QW_F32, nin_, state.d_conv_state,
+                                  state.d_recurrent_state, d_core_, QW_F32, nh_ * vd_, stream),
+                    "HipLinearAttention step");
+        ctx_->check(qw_linear(ctx_->get(), Wout_.get(), d_core_, QW_F32, 0, batch_size, output, QW_F32, 0, nullptr,
+                              stream),
+                    "HipLinearAttention out_proj");
+    }
+
+  private:
+    static void check_size(const std::vector<float>& v, size_t n, const char* name) {
+        if (v.size() != n) throw Error(QW_ERR_SHAPE, std::string(name) + ": expected " + std::to_string(n) + " floats");
+    }
+    static void upload(float*& d, const std::vector<float>& h, size_t n) {
+        if (!d && hipMalloc(&d, n * sizeof(float)) != hipSuccess) throw Error(QW_ERR_HIP, "hipMalloc");
+        if (hipMemcpy(d, h.data(), n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            throw Error(QW_ERR_HIP, "hipMemcpy");
+    }
+    void ensure(int batch) const {
+        if (batch <= cap_) return;
+        if (d_row_) (void)hipFree(d_row_);
+        if (d_core_) (void)hipFree(d_core_);
+        if (hipMalloc(&d_row_, (size_t)batch * nin_ * sizeof(float)) != hipSuccess ||
+            hipMalloc(&d_core_, (size_t)batch * nh_ * vd_ * sizeof(float)) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipLinearAttention: hipMalloc");
+        cap_ = batch;
+    }
+    int hidden_, nh_, kd_, vd_, K_, conv_dim_, nin_;
+    qw_wfmt fmt_;
+    std::shared_ptr<Context> ctx_;
+    detail::WeightPtr Win_, Wout_;
+    float *d_conv_w_ = nullptr, *d_A_log_ = nullptr, *d_dt_bias_ = nullptr, *d_norm_w_ = nullptr;
+    mutable float *d_row_ = nullptr, *d_core_ = nullptr;
+    mutable int cap_ = 0;
 };
 
 // ---------------------------------------------------------------------------

@@ -14,7 +14,9 @@
 
 using qwen::hip::HipFullAttnProjections;
 using qwen::hip::HipGreedyArgmaxSampler;
+using qwen::hip::HipLinearAttention;
 using qwen::hip::HipLinearAttnProjections;
+using qwen::hip::HipLinearAttnState;
 using qwen::hip::HipLMHead;
 using qwen::hip::HipMLP;
 using qwen::hip::HipRMSNorm;
@@ -209,6 +211,80 @@ static void test_attention_projections() {
     }
 }
 
+// Whole Gated-DeltaNet decode layer over several tokens: stacked in-projection,
+// conv + gated delta step, out-projection; oracle = FP32 projections +
+// orc_gdn_step carrying the same conv and recurrent state.
+static void test_linear_attention() {
+    const int H = 1024, nh = 16, kd = 128, vd = 128, K = 4, B = 3, T = 4;
+    const int CD = nh * (2 * kd + vd), V = nh * vd;
+    auto qkv = normal((size_t)CD * H, 60, 0.03f), a = normal((size_t)nh * H, 61, 0.03f);
+    auto b = normal((size_t)nh * H, 62, 0.03f), z = normal((size_t)V * H, 63, 0.03f);
+    auto conv = normal((size_t)CD * K, 64, 0.5f), o = normal((size_t)H * V, 65, 0.02f);
+    auto alog = normal(nh, 66, 0.5f), dtb = normal(nh, 67, 0.5f), nw = normal(vd, 68, 0.2f);
+    for (auto& w : nw) w += 1.0f;
+    for (int defaults = 0; defaults < 2; ++defaults) {
+        HipLinearAttention la(H, nh, kd, vd, K, QW_WFMT_F32);
+        if (defaults)
+            la.set_weights(qkv, a, b, z, conv, o);
+        else
+            la.set_weights(qkv, a, b, z, conv, o, alog, dtb, nw);
+        std::vector<float> ra = defaults ? std::vector<float>(nh, 0.0f) : alog;
+        std::vector<float> rd = defaults ? std::vector<float>(nh, 0.0f) : dtb;
+        std::vector<float> rn = defaults ? std::vector<float>(vd, 1.0f) : nw;
+        HipLinearAttnState st;
+        st.reset(nh, kd, vd, K, B);
+        std::vector<float> cs((size_t)B * CD * (K - 1), 0.0f), rs((size_t)B * nh * kd * vd, 0.0f);
+        double worst = 0;
+        for (int t = 0; t < T; ++t) {
+            auto x = normal((size_t)B * H, 70 + t);
+            Dev dx(x), dy((size_t)B * H);
+            la.forward_batch(dx.p, dy.p, st, B);
+            std::vector<float> mx((size_t)B * CD), rz((size_t)B * V), rA((size_t)B * nh), rB((size_t)B * nh),
+                core((size_t)B * V), ry((size_t)B * H);
+            orc_linear_f32(qkv.data(), x.data(), mx.data(), B, CD, H);
+            orc_linear_f32(z.data(), x.data(), rz.data(), B, V, H);
+            orc_linear_f32(a.data(), x.data(), rA.data(), B, nh, H);
+            orc_linear_f32(b.data(), x.data(), rB.data(), B, nh, H);
+            orc_gdn_step(B, nh, kd, vd, K, mx.data(), rA.data(), rB.data(), rz.data(), conv.data(), ra.data(),
+                         rd.data(), rn.data(), cs.data(), rs.data(), core.data());
+            orc_linear_f32(o.data(), core.data(), ry.data(), B, H, V);
+            worst = std::fmax(worst, relerr(dy.get(), ry));
+        }
+        Dev drs(rs.size());
+        (void)hipMemcpy(drs.p, st.d_recurrent_state, rs.size() * sizeof(float), hipMemcpyDeviceToDevice);
+        report(defaults ? "HipLinearAttention forward_batch (default A_log/dt_bias/norm)"
+                        : "HipLinearAttention forward_batch",
+               worst, 1e-4);
+        report("HipLinearAttention recurrent state", relerr(drs.get(), rs), 1e-4);
+        if (!defaults) {  // single-sequence forward on a fresh state == first row of a batch step
+            HipLinearAttnState s1;
+            s1.reset(nh, kd, vd, K, 1);
+            auto x = normal((size_t)H, 80);
+            Dev dx(x), dy((size_t)H);
+            la.forward(dx.p, dy.p, s1);
+            std::vector<float> c1((size_t)CD * (K - 1), 0.0f), r1((size_t)nh * kd * vd, 0.0f), mx(CD), rz(V),
+                rA(nh), rB(nh), core(V), ry(H);
+            orc_linear_f32(qkv.data(), x.data(), mx.data(), 1, CD, H);
+            orc_linear_f32(z.data(), x.data(), rz.data(), 1, V, H);
+            orc_linear_f32(a.data(), x.data(), rA.data(), 1, nh, H);
+            orc_linear_f32(b.data(), x.data(), rB.data(), 1, nh, H);
+            orc_gdn_step(1, nh, kd, vd, K, mx.data(), rA.data(), rB.data(), rz.data(), conv.data(), ra.data(),
+                         rd.data(), rn.data(), c1.data(), r1.data(), core.data());
+            orc_linear_f32(o.data(), core.data(), ry.data(), 1, H, V);
+            report("HipLinearAttention forward", relerr(dy.get(), ry), 1e-4);
+            bool threw = false;
+            try {
+                HipLinearAttnState bad;
+                bad.reset(nh, kd, vd, K, 1);
+                la.forward_batch(dx.p, dy.p, bad, 2);
+            } catch (const qwen::hip::Error& e) {
+                threw = e.status == QW_ERR_SHAPE;
+            }
+            report("HipLinearAttention state too small throws", threw ? 0.0 : 1.0, 0.0);
+        }
+    }
+}
+
 static void test_errors() {
     HipMLP mlp(1024, 3584);
     bool threw = false;
@@ -233,6 +309,7 @@ int main() {
         test_rmsnorm();
         test_mlp();
         test_attention_projections();
+        test_linear_attention();
         test_lmhead_and_sampler();
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
