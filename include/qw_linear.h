@@ -243,8 +243,8 @@ qw_status qw_silu_mul(qw_ctx* ctx, const void* g, const void* u, void* h, qw_dty
  * conv_weight [conv_dim][conv_kernel], A_log [nh], dt_bias [nh],
  * norm_weight [vd].  States (FP32, device, updated in place, the reference
  * layouts): conv_state [batch][conv_dim][conv_kernel-1] (index 0 the newest
- * input; may be NULL when conv_kernel is 1), recurrent_state [batch][nh][kd][vd].  out [batch][ld_out] receives
- * nh*vd values.  key_dim = value_dim = 128, 1 <= conv_kernel <= 8. */
+ * input; may be NULL when conv_kernel is 1), recurrent_state
+ * [batch][nh][kd][vd].  out [batch][ld_out] receives nh*vd values.  key_dim = value_dim = 128, 1 <= conv_kernel <= 8. */
 typedef struct {
     int num_heads;
     int key_dim;
@@ -259,6 +259,20 @@ qw_status qw_gdn_decode(qw_ctx* ctx, const qw_gdn_params* p, int batch, const vo
                         const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
                         float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype,
                         int ld_out, hipStream_t stream);
+/* The same step over `tokens` consecutive tokens of each of `batch`
+ * sequences, serially in token order: input and output row b*tokens + t
+ * holds token t of sequence b; the states carry from one token to the next
+ * and hold the state after the last token on return.  Equal to `tokens`
+ * calls of qw_gdn_decode, in one launch that reads and writes each state
+ * once.  Replaces the state chain of CudaLinearAttention::forward_batch
+ * (linear_attention_cuda.cu:529-680; its contract, equality with serial
+ * single-token steps, is verify_linear_attn_batch.cu:68-112) and
+ * LinearAttention::forward over several tokens (language_linear_attn.cpp:
+ * 125-257). */
+qw_status qw_gdn_prefill(qw_ctx* ctx, const qw_gdn_params* p, int batch, int tokens, const void* mixed_qkv,
+                         const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
+                         float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype, int ld_out,
+                         hipStream_t stream);
 
 /* ---- graphs --------------------------------------------------------------------
  * Capture a sequence of qw_* calls on `stream` into a replayable HIP graph

@@ -334,27 +334,29 @@ class HipLinearAttnProjections {
 // ---------------------------------------------------------------------------
 // Recurrent and conv state of a Gated-DeltaNet layer (CudaLinearAttnState,
 // linear_attention_cuda.hpp:11-22): device FP32, recurrent state
-// [batch][nh][kd][vd], conv state [batch][conv_dim][conv_kernel-1]
-// (index 0 the newest input), conv_dim = 2*nh*kd + nh*vd.
+// [sequences][nh][kd][vd], conv state [sequences][conv_dim][conv_kernel-1]
+// (index 0 the newest input), conv_dim = 2*nh*kd + nh*vd.  The reference
+// state holds one sequence; `sequences` > 1 (an extension) backs
+// HipLinearAttention::forward_decode_sequences.
 struct HipLinearAttnState {
     float* d_recurrent_state = nullptr;
     float* d_conv_state = nullptr;
-    int num_heads = 0, key_dim = 0, value_dim = 0, conv_dim = 0, conv_kernel = 0, batch = 0;
+    int num_heads = 0, key_dim = 0, value_dim = 0, conv_dim = 0, conv_kernel = 0, sequences = 0;
 
     HipLinearAttnState() = default;
     HipLinearAttnState(const HipLinearAttnState&) = delete;
     HipLinearAttnState& operator=(const HipLinearAttnState&) = delete;
     ~HipLinearAttnState() { release(); }
 
-    // (re)allocate for `batch_size` sequences and zero
-    void reset(int nh, int kd, int vd, int conv_k = 4, int batch_size = 1) {
+    // (re)allocate for `seqs` sequences and zero
+    void reset(int nh, int kd, int vd, int conv_k = 4, int seqs = 1) {
         release();
         num_heads = nh;
         key_dim = kd;
         value_dim = vd;
         conv_kernel = conv_k;
         conv_dim = nh * (2 * kd + vd);
-        batch = batch_size;
+        sequences = seqs;
         if (hipMalloc(&d_recurrent_state, rec_bytes()) != hipSuccess ||
             (conv_bytes() && hipMalloc(&d_conv_state, conv_bytes()) != hipSuccess))
             throw Error(QW_ERR_HIP, "HipLinearAttnState::reset: hipMalloc");
@@ -365,8 +367,8 @@ struct HipLinearAttnState {
             (d_conv_state && hipMemset(d_conv_state, 0, conv_bytes()) != hipSuccess))
             throw Error(QW_ERR_HIP, "HipLinearAttnState::clear: hipMemset");
     }
-    size_t rec_bytes() const { return (size_t)batch * num_heads * key_dim * value_dim * sizeof(float); }
-    size_t conv_bytes() const { return (size_t)batch * conv_dim * (conv_kernel - 1) * sizeof(float); }
+    size_t rec_bytes() const { return (size_t)sequences * num_heads * key_dim * value_dim * sizeof(float); }
+    size_t conv_bytes() const { return (size_t)sequences * conv_dim * (conv_kernel - 1) * sizeof(float); }
 
   private:
     void release() {
@@ -377,12 +379,17 @@ struct HipLinearAttnState {
 };
 
 // ---------------------------------------------------------------------------
-// A whole Gated-DeltaNet layer for decode (CudaLinearAttention,
+// A whole Gated-DeltaNet layer (CudaLinearAttention,
 // linear_attention_cuda.hpp:24-90; CPU LinearAttention::forward,
-// language_linear_attn.cpp:125-257): one token per sequence,
-//   [qkv | z | a | b] = W_in . x      one stacked projection
-//   core = gated delta step(...)     qw_gdn_decode (conv, gates, state, norm-gate)
-//   output = W_out . core
+// language_linear_attn.cpp:125-257):
+//   [qkv | z | a | b] = W_in . x      one stacked projection (all tokens)
+//   core = gated delta steps(...)    qw_gdn_prefill (conv, gates, state, norm-gate)
+//   output = W_out . core            (all tokens)
+// forward_batch(input, output, state, n) runs n consecutive tokens of the
+// state's one sequence, serially, as the reference forward_batch is
+// specified (equal to n single-token forward calls,
+// verify_linear_attn_batch.cu:68-112); forward_decode_sequences (an
+// extension) runs one token for each of n sequences with their own states.
 // set_weights takes the reference's arguments in the reference's order;
 // empty a_log / dt_bias / norm_weight default to 0 / 0 / 1 as there
 // (linear_attention_cuda.cu:450-464).  Default storage BF16.  The projection
@@ -436,30 +443,47 @@ class HipLinearAttention {
         forward_batch(input, output, state, 1, stream);
     }
 
-    // input/output [batch][hidden] FP32 device; state sized for >= batch sequences
+    // input/output [batch_size][hidden] FP32 device: batch_size consecutive
+    // tokens of sequence 0 of `state`
     void forward_batch(const float* input, float* output, HipLinearAttnState& state, int batch_size,
                        hipStream_t stream = nullptr) const {
-        detail::require(Wout_.get(), "HipLinearAttention::forward");
-        if (state.num_heads != nh_ || state.key_dim != kd_ || state.value_dim != vd_ || state.conv_kernel != K_ ||
-            state.batch < batch_size)
-            throw Error(QW_ERR_SHAPE, "HipLinearAttention::forward: state shape does not match");
-        ensure(batch_size);
-        ctx_->check(qw_linear(ctx_->get(), Win_.get(), input, QW_F32, 0, batch_size, d_row_, QW_F32, nin_, nullptr,
-                              stream),
-                    "HipLinearAttention in_proj");
+        run(input, output, state, 1, batch_size, "HipLinearAttention::forward_batch", stream);
+    }
+
+    // input/output [n][hidden]: one token for each of sequences 0..n-1 of `state`
+    void forward_decode_sequences(const float* input, float* output, HipLinearAttnState& state, int n,
+                                  hipStream_t stream = nullptr) const {
+        run(input, output, state, n, 1, "HipLinearAttention::forward_decode_sequences", stream);
+    }
+
+    // CudaLinearAttention::forward_fused (linear_attention_cuda.cu:686-689) is forward
+    void forward_fused(const float* input, float* output, HipLinearAttnState& state,
+                       hipStream_t stream = nullptr) const {
+        forward_batch(input, output, state, 1, stream);
+    }
+
+  private:
+    void run(const float* input, float* output, HipLinearAttnState& state, int seqs, int tokens, const char* what,
+             hipStream_t stream) const {
+        detail::require(Wout_.get(), what);
+        if (state.num_heads != nh_ || state.key_dim != kd_ || state.value_dim != vd_ ||
+            state.conv_kernel != K_ || state.sequences < seqs)
+            throw Error(QW_ERR_SHAPE, std::string(what) + ": state shape does not match");
+        if (seqs < 1 || tokens < 1) throw Error(QW_ERR_SHAPE, std::string(what) + ": empty batch");
+        const int rows = seqs * tokens;
+        ensure(rows);
+        ctx_->check(qw_linear(ctx_->get(), Win_.get(), input, QW_F32, 0, rows, d_row_, QW_F32, nin_, nullptr, stream),
+                    what);
         qw_gdn_params p{nh_, kd_, vd_, K_, d_conv_w_, d_A_log_, d_dt_bias_, d_norm_w_};
         const float* z = d_row_ + conv_dim_;
         const float* a = z + nh_ * vd_;
         const float* b = a + nh_;
-        ctx_->check(qw_gdn_decode(ctx_->get(), &p, batch_size, d_row_, z, a, b, QW_F32, nin_, state.d_conv_state,
-                                  state.d_recurrent_state, d_core_, QW_F32, nh_ * vd_, stream),
-                    "HipLinearAttention step");
-        ctx_->check(qw_linear(ctx_->get(), Wout_.get(), d_core_, QW_F32, 0, batch_size, output, QW_F32, 0, nullptr,
-                              stream),
-                    "HipLinearAttention out_proj");
+        ctx_->check(qw_gdn_prefill(ctx_->get(), &p, seqs, tokens, d_row_, z, a, b, QW_F32, nin_, state.d_conv_state,
+                                   state.d_recurrent_state, d_core_, QW_F32, nh_ * vd_, stream),
+                    what);
+        ctx_->check(
+            qw_linear(ctx_->get(), Wout_.get(), d_core_, QW_F32, 0, rows, output, QW_F32, 0, nullptr, stream), what);
     }
-
-  private:
     static void check_size(const std::vector<float>& v, size_t n, const char* name) {
         if (v.size() != n) throw Error(QW_ERR_SHAPE, std::string(name) + ": expected " + std::to_string(n) + " floats");
     }

@@ -818,23 +818,27 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
                       kSkinnyMaxM);
 }
 
-qw_status qw_gdn_decode(qw_ctx* ctx, const qw_gdn_params* p, int batch, const void* mixed_qkv,
-                        const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
-                        float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype,
-                        int ld_out, hipStream_t stream) {
+static qw_status gdn_run(qw_ctx* ctx, const qw_gdn_params* p, int batch, int tokens, const void* mixed_qkv,
+                         const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
+                         float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype, int ld_out,
+                         hipStream_t stream) {
     if (!ctx) return QW_ERR_NULL;
     if (!p || !mixed_qkv || !z || !a || !b || !recurrent_state || !out || !p->conv_weight || !p->A_log ||
         !p->dt_bias || !p->norm_weight || (!conv_state && p->conv_kernel > 1))
         return fail(ctx, QW_ERR_NULL, "gdn: NULL argument");
-    if (batch < 1) return fail(ctx, QW_ERR_SHAPE, "gdn: batch=%d must be >= 1", batch);
+    if (batch < 1 || tokens < 1)
+        return fail(ctx, QW_ERR_SHAPE, "gdn: batch=%d, tokens=%d must be >= 1", batch, tokens);
     if (p->num_heads < 1 || p->key_dim != 128 || p->value_dim != 128 || p->conv_kernel < 1 || p->conv_kernel > 8)
         return fail(ctx, QW_ERR_SHAPE, "gdn: needs key_dim = value_dim = 128, 1 <= conv_kernel <= 8 (got %d, %d, %d)",
                     p->key_dim, p->value_dim, p->conv_kernel);
     if (!valid_act(in_dtype) || !valid_act(out_dtype)) return fail(ctx, QW_ERR_DTYPE, "gdn: dtype unsupported");
     const int vdim = p->num_heads * p->value_dim;
     if (ld_in < 1 || ld_out < vdim) return fail(ctx, QW_ERR_SHAPE, "gdn: ld_in=%d, ld_out=%d < %d", ld_in, ld_out, vdim);
+    if ((int64_t)batch * p->num_heads > 65535 * 64 || batch > 65535)
+        return fail(ctx, QW_ERR_SHAPE, "gdn: batch=%d too large", batch);
     qwk::GdnArgs g{};
     g.B = batch;
+    g.T = tokens;
     g.nh = p->num_heads;
     g.kd = p->key_dim;
     g.vd = p->value_dim;
@@ -854,9 +858,25 @@ qw_status qw_gdn_decode(qw_ctx* ctx, const qw_gdn_params* p, int batch, const vo
     g.out = out;
     g.out_dt = (int)out_dtype;
     g.ld_out = ld_out;
-    hipError_t e = qwk::launch_gdn_decode(g, stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "gdn decode launch");
+    hipError_t e = qwk::launch_gdn(g, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "gdn launch");
     return QW_OK;
+}
+
+qw_status qw_gdn_decode(qw_ctx* ctx, const qw_gdn_params* p, int batch, const void* mixed_qkv,
+                        const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
+                        float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype,
+                        int ld_out, hipStream_t stream) {
+    return gdn_run(ctx, p, batch, 1, mixed_qkv, z, a, b, in_dtype, ld_in, conv_state, recurrent_state, out,
+                   out_dtype, ld_out, stream);
+}
+
+qw_status qw_gdn_prefill(qw_ctx* ctx, const qw_gdn_params* p, int batch, int tokens, const void* mixed_qkv,
+                         const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,
+                         float* conv_state, float* recurrent_state, void* out, qw_dtype out_dtype, int ld_out,
+                         hipStream_t stream) {
+    return gdn_run(ctx, p, batch, tokens, mixed_qkv, z, a, b, in_dtype, ld_in, conv_state, recurrent_state, out,
+                   out_dtype, ld_out, stream);
 }
 
 qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,

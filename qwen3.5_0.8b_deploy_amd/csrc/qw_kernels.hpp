@@ -104,11 +104,11 @@ hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, int grid, hipStre
 
 // Gated-DeltaNet decode step (qw_gdn.hip): one token of each of B sequences.
 struct GdnArgs {
-    int B, nh, kd, vd, K;
-    const void* mixed;     // [B][ld_in] rows: q | k | v channels
-    const void* z;         // [B][ld_in]: nh*vd
-    const void* a;         // [B][ld_in]: nh
-    const void* b;         // [B][ld_in]: nh
+    int B, T, nh, kd, vd, K;  // B sequences of T consecutive tokens; row = b*T + t
+    const void* mixed;     // [B*T][ld_in] rows: q | k | v channels
+    const void* z;         // [B*T][ld_in]: nh*vd
+    const void* a;         // [B*T][ld_in]: nh
+    const void* b;         // [B*T][ld_in]: nh
     int in_dt, ld_in;
     const float* conv_w;   // [conv_dim][K]
     const float* A_log;    // [nh]
@@ -116,10 +116,10 @@ struct GdnArgs {
     const float* norm_w;   // [vd]
     float* conv_state;     // [B][conv_dim][K-1]
     float* rec_state;      // [B][nh][kd][vd]
-    void* out;             // [B][ld_out]: nh*vd
+    void* out;             // [B*T][ld_out]: nh*vd
     int out_dt, ld_out;
 };
-hipError_t launch_gdn_decode(const GdnArgs& a, hipStream_t stream);
+hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream);
 
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
 // Output rows are written to physical tile `tile_of_row(o)` (GLU interleave

@@ -31,7 +31,7 @@ EXPORTS = [
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
-    "qw_silu_mul", "qw_gdn_decode", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
+    "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
 
 
@@ -103,6 +103,8 @@ def lib():
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
         "qw_gdn_decode": ([_vp, ctypes.POINTER(GdnParams), _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i,
                            _vp], _i),
+        "qw_gdn_prefill": ([_vp, ctypes.POINTER(GdnParams), _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i,
+                            _i, _vp], _i),
         "qw_device_error": ([_vp, _vp], _i),
         "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
         "qw_argmax_rows": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
@@ -429,3 +431,21 @@ def gdn_decode(ctx, conv_weight, A_log, dt_bias, norm_weight, mixed, z, a, b, co
     ctx.check(lib().qw_gdn_decode(ctx.handle, ctypes.byref(p), B, _ptr(mixed), _ptr(z), _ptr(a), _ptr(b),
                                   _torch_code(mixed), ld_in, _ptr(conv_state), _ptr(recurrent_state), _ptr(out),
                                   _torch_code(out), ld_out, _stream(stream)))
+
+
+def gdn_prefill(ctx, conv_weight, A_log, dt_bias, norm_weight, mixed, z, a, b, conv_state, recurrent_state, out,
+                num_heads, tokens, key_dim=128, value_dim=128, ld_in=0, ld_out=0, stream=None):
+    """Gated-DeltaNet step over `tokens` consecutive tokens of each sequence:
+    row s*tokens + t of mixed/z/a/b/out is token t of sequence s; the FP32
+    states (one per sequence) carry across the tokens and are updated in
+    place."""
+    p = GdnParams(num_heads, key_dim, value_dim, conv_weight.shape[1], conv_weight.data_ptr(), A_log.data_ptr(),
+                  dt_bias.data_ptr(), norm_weight.data_ptr())
+    rows = mixed.shape[0]
+    if tokens < 1 or rows % tokens:
+        raise QwError(ERR_SHAPE, f"{rows} rows are not a whole number of {tokens}-token sequences")
+    ld_in = ld_in or mixed.stride(0)
+    ld_out = ld_out or out.stride(0)
+    ctx.check(lib().qw_gdn_prefill(ctx.handle, ctypes.byref(p), rows // tokens, tokens, _ptr(mixed), _ptr(z),
+                                   _ptr(a), _ptr(b), _torch_code(mixed), ld_in, _ptr(conv_state),
+                                   _ptr(recurrent_state), _ptr(out), _torch_code(out), ld_out, _stream(stream)))

@@ -238,7 +238,7 @@ static void test_linear_attention() {
         for (int t = 0; t < T; ++t) {
             auto x = normal((size_t)B * H, 70 + t);
             Dev dx(x), dy((size_t)B * H);
-            la.forward_batch(dx.p, dy.p, st, B);
+            la.forward_decode_sequences(dx.p, dy.p, st, B);
             std::vector<float> mx((size_t)B * CD), rz((size_t)B * V), rA((size_t)B * nh), rB((size_t)B * nh),
                 core((size_t)B * V), ry((size_t)B * H);
             orc_linear_f32(qkv.data(), x.data(), mx.data(), B, CD, H);
@@ -252,8 +252,8 @@ static void test_linear_attention() {
         }
         Dev drs(rs.size());
         (void)hipMemcpy(drs.p, st.d_recurrent_state, rs.size() * sizeof(float), hipMemcpyDeviceToDevice);
-        report(defaults ? "HipLinearAttention forward_batch (default A_log/dt_bias/norm)"
-                        : "HipLinearAttention forward_batch",
+        report(defaults ? "HipLinearAttention forward_decode_sequences (default A_log/dt_bias/norm)"
+                        : "HipLinearAttention forward_decode_sequences",
                worst, 1e-4);
         report("HipLinearAttention recurrent state", relerr(drs.get(), rs), 1e-4);
         if (!defaults) {  // single-sequence forward on a fresh state == first row of a batch step
@@ -276,11 +276,39 @@ static void test_linear_attention() {
             try {
                 HipLinearAttnState bad;
                 bad.reset(nh, kd, vd, K, 1);
-                la.forward_batch(dx.p, dy.p, bad, 2);
+                la.forward_decode_sequences(dx.p, dy.p, bad, 2);  // throws before any launch
             } catch (const qwen::hip::Error& e) {
                 threw = e.status == QW_ERR_SHAPE;
             }
             report("HipLinearAttention state too small throws", threw ? 0.0 : 1.0, 0.0);
+
+            // forward_batch: P consecutive tokens of one sequence == P forward calls (the
+            // reference's own contract) and == P oracle steps
+            const int P = 5;
+            auto xs = normal((size_t)P * H, 90);
+            Dev dxs(xs), dys((size_t)P * H), dys2((size_t)P * H);
+            HipLinearAttnState sp, ss;
+            sp.reset(nh, kd, vd, K);
+            ss.reset(nh, kd, vd, K);
+            la.forward_batch(dxs.p, dys.p, sp, P);
+            for (int t = 0; t < P; ++t) la.forward(dxs.p + (size_t)t * H, dys2.p + (size_t)t * H, ss);
+            std::vector<float> cp((size_t)CD * (K - 1), 0.0f), rp((size_t)nh * kd * vd, 0.0f), ref((size_t)P * H);
+            for (int t = 0; t < P; ++t) {
+                const float* xt = xs.data() + (size_t)t * H;
+                orc_linear_f32(qkv.data(), xt, mx.data(), 1, CD, H);
+                orc_linear_f32(z.data(), xt, rz.data(), 1, V, H);
+                orc_linear_f32(a.data(), xt, rA.data(), 1, nh, H);
+                orc_linear_f32(b.data(), xt, rB.data(), 1, nh, H);
+                orc_gdn_step(1, nh, kd, vd, K, mx.data(), rA.data(), rB.data(), rz.data(), conv.data(), ra.data(),
+                             rd.data(), rn.data(), cp.data(), rp.data(), core.data());
+                orc_linear_f32(o.data(), core.data(), ref.data() + (size_t)t * H, 1, H, V);
+            }
+            report("HipLinearAttention forward_batch (5 tokens, one sequence)", relerr(dys.get(), ref), 1e-4);
+            report("HipLinearAttention forward_batch == 5 x forward", relerr(dys.get(), dys2.get()), 1e-5);
+            Dev dcs(cp.size());
+            (void)hipMemcpy(dcs.p, sp.d_conv_state, cp.size() * sizeof(float), hipMemcpyDeviceToDevice);
+            // the conv taps are copies of the projection outputs (GPU vs CPU dot products)
+            report("HipLinearAttention forward_batch conv state", relerr(dcs.get(), cp), 1e-5);
         }
     }
 }

@@ -98,3 +98,76 @@ def test_gdn_decode_errors(qw, ctx):
     with pytest.raises(qw.QwError):
         qw.gdn_decode(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], x, x, x, x, cs, rs, out,
                       4, key_dim=64, value_dim=64)
+
+
+@pytest.mark.parametrize("B,T,K,io", [(1, 7, 4, "f32"), (2, 33, 4, "f32"), (3, 5, 1, "f32"), (2, 9, 4, "bf16")])
+def test_gdn_prefill_parity(qw, ctx, oracle, relerr, B, T, K, io):
+    """qw_gdn_prefill over T tokens of B sequences against T oracle steps
+    (the serial semantics of the reference forward_batch)."""
+    P = _params(oracle, K, 940 + K)
+    dP = {k: dev(v) for k, v in P.items()}
+    cs = oracle.normal((B, CD, max(K - 1, 0)), 941)
+    rs = oracle.normal((B, NH, KD * VD), 942, 0.0, 0.3)
+    dcs, drs = dev(cs), dev(rs)
+    tdt = torch.float32 if io == "f32" else torch.bfloat16
+    ld = CD + NH * VD + 2 * NH
+    rows = dev(oracle.normal((B * T, ld), 943), tdt)
+    out = torch.empty(B * T, NH * VD, device="cuda", dtype=tdt)
+    qw.gdn_prefill(ctx, dP["conv_w"], dP["A_log"], dP["dt_bias"], dP["norm_w"], rows[:, :CD],
+                   rows[:, CD:CD + NH * VD], rows[:, CD + NH * VD:CD + NH * VD + NH], rows[:, CD + NH * VD + NH:],
+                   dcs, drs, out, NH, T)
+    torch.cuda.synchronize()
+    r = host(rows).reshape(B, T, ld)
+    o_ref = np.empty((B, T, NH * VD), np.float32)
+    for t in range(T):
+        rt = np.ascontiguousarray(r[:, t])
+        o_ref[:, t], cs, rs = oracle.gdn_step(rt[:, :CD], rt[:, CD + NH * VD:CD + NH * VD + NH],
+                                              rt[:, CD + NH * VD + NH:], rt[:, CD:CD + NH * VD], P["conv_w"],
+                                              P["A_log"], P["dt_bias"], P["norm_w"], cs, rs, NH, KD, VD)
+    bar = 1e-5 if io == "f32" else 4e-3
+    # the carried state adds a little summation-order difference per token
+    sbar = 1e-5 * max(1, T // 8)
+    assert relerr(host(out).reshape(B, T, -1), o_ref) <= bar
+    assert relerr(host(drs), rs) <= sbar, relerr(host(drs), rs)
+    assert np.array_equal(host(dcs), cs)
+
+
+def test_gdn_prefill_equals_decode_steps(qw, ctx, oracle):
+    """One T-token launch and T one-token launches run the same arithmetic:
+    outputs and both states agree bit for bit."""
+    B, T, K = 2, 6, 4
+    P = {k: dev(v) for k, v in _params(oracle, K, 950).items()}
+    cs0 = dev(oracle.normal((B, CD, K - 1), 951))
+    rs0 = dev(oracle.normal((B, NH, KD * VD), 952, 0.0, 0.3))
+    ld = CD + NH * VD + 2 * NH
+    rows = dev(oracle.normal((B, T, ld), 953))
+
+    def parts(x):
+        return x[:, :CD], x[:, CD:CD + NH * VD], x[:, CD + NH * VD:CD + NH * VD + NH], x[:, CD + NH * VD + NH:]
+
+    cs1, rs1 = cs0.clone(), rs0.clone()
+    out1 = torch.empty(B * T, NH * VD, device="cuda")
+    qw.gdn_prefill(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], *parts(rows.reshape(B * T, ld)), cs1,
+                   rs1, out1, NH, T)
+    cs2, rs2 = cs0.clone(), rs0.clone()
+    out2 = torch.empty(B, T, NH * VD, device="cuda")
+    for t in range(T):
+        o = torch.empty(B, NH * VD, device="cuda")
+        qw.gdn_decode(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], *parts(rows[:, t]), cs2, rs2, o, NH)
+        out2[:, t] = o
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2.reshape(B * T, -1))
+    assert torch.equal(rs1, rs2) and torch.equal(cs1, cs2)
+
+
+def test_gdn_prefill_errors(qw, ctx):
+    P = {"conv_w": torch.zeros(CD, 4, device="cuda"), "A_log": torch.zeros(NH, device="cuda"),
+         "dt_bias": torch.zeros(NH, device="cuda"), "norm_w": torch.ones(VD, device="cuda")}
+    x = torch.zeros(6, CD, device="cuda")
+    out = torch.empty(6, NH * VD, device="cuda")
+    cs = torch.zeros(1, CD * 3, device="cuda")
+    rs = torch.zeros(1, NH * KD * VD, device="cuda")
+    with pytest.raises(qw.QwError):  # 6 rows are not whole 4-token sequences
+        qw.gdn_prefill(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], x, x, x, x, cs, rs, out, NH, 4)
+    with pytest.raises(qw.QwError):  # zero tokens
+        qw.gdn_prefill(ctx, P["conv_w"], P["A_log"], P["dt_bias"], P["norm_w"], x, x, x, x, cs, rs, out, NH, 0)
