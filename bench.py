@@ -472,6 +472,21 @@ def run_gdn(qw, ctx, torch, timer, stream, randn, args):
                                          "tok_per_s_18_layers": round(B / (us2 * len(layers) * 1e-6), 1)}
         log("gdn", B, out[f"gdn_step_B{B}"], out[f"gdn_layer_decode_B{B}"])
         del g1, g2
+    # prefill of one sequence: T tokens serially through the recurrence (one launch per layer)
+    T = 1024
+    rows = randn(T, NIN, dtype=torch.float32)
+    core = torch.empty(T, NH * VD, device="cuda", dtype=torch.bfloat16)
+    L = layers[0]
+    cs = torch.zeros(1, CD, K - 1, device="cuda")
+    rs = torch.zeros(1, NH, KD * VD, device="cuda")
+
+    def pre():
+        qw.gdn_prefill(ctx, L["conv_w"], L["A_log"], L["dt_bias"], L["norm_w"], rows[:, :CD],
+                       rows[:, CD:CD + NH * VD], rows[:, CD + NH * VD:CD + NH * VD + NH], rows[:, CD + NH * VD + NH:],
+                       cs, rs, core, NH, T)
+    ms = timer.run(pre, 3, 1)
+    out[f"gdn_prefill_T{T}"] = {"us_per_layer": round(1e3 * ms, 1), "tok_per_s_per_layer": round(T / (ms * 1e-3), 0)}
+    log("gdn prefill", out[f"gdn_prefill_T{T}"])
     del layers
     return out
 

@@ -17,6 +17,7 @@
 #include "qw_kernels.hpp"
 
 constexpr int kGemmMinM = 33;  // default token count from which the MFMA GEMM is used
+constexpr int kGdnChunkMin = 32;  // tokens per sequence from which the chunked Gated-DeltaNet form runs
 
 struct qw_ctx {
     int device = 0;
@@ -32,6 +33,7 @@ struct qw_ctx {
     int gemm_tile_m = 0;         // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256; 0 = by shape)
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
+    int gdn_chunk_min = kGdnChunkMin;  // tokens per sequence from which the chunked GDN form runs (QW_GDN_CHUNK_MIN)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -169,6 +171,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
+    if (const char* v = getenv("QW_GDN_CHUNK_MIN")) c->gdn_chunk_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;
@@ -858,7 +861,12 @@ static qw_status gdn_run(qw_ctx* ctx, const qw_gdn_params* p, int batch, int tok
     g.out = out;
     g.out_dt = (int)out_dtype;
     g.ld_out = ld_out;
-    hipError_t e = qwk::launch_gdn(g, stream);
+    // long runs: the chunked form, when the workspace (normalized-activation and
+    // intermediate regions, unused by this call) holds at least one chunk per sequence
+    const size_t ws_free = ctx->xnorm_bytes + ctx->scratch_bytes;
+    const bool chunked = tokens >= ctx->gdn_chunk_min &&
+                         ws_free >= (size_t)batch * 64 * qwk::gdn_chunked_bytes_per_token(p->num_heads);
+    hipError_t e = chunked ? qwk::launch_gdn_chunked(g, ctx->xnorm, ws_free, stream) : qwk::launch_gdn(g, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "gdn launch");
     return QW_OK;
 }

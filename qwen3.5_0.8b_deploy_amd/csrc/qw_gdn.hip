@@ -197,4 +197,490 @@ hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// ===========================================================================
+// Chunked form for long token runs.  The serial recurrence above costs one
+// barrier chain per token; here the tokens of a sequence are cut into chunks
+// of C = 64 and the delta rule is rewritten per chunk (the WY form of the
+// delta rule, Yang et al. 2024, "Parallelizing Linear Transformers with the
+// Delta Rule over Sequence Length", with the per-token decay of Gated
+// DeltaNet).  For a chunk with start state S0, per-token decays gamma_i,
+// G_i = sum_{m<=i} log gamma_m (so Gamma_i = exp(G_i)), the serial steps
+//   S_i = gamma_i S_{i-1} + k_i u_i^T,  u_i = beta_i (v_i - gamma_i S_{i-1}^T k_i),
+//   o_i = S_i^T q_i
+// unroll to
+//   (I + A) U = diag(beta) V - diag(beta Gamma) K S0,
+//       A_ij = beta_i exp(G_i - G_j) k_i.k_j  (j < i, else 0)
+//   U = Ut - W S0,  Ut = (I+A)^-1 diag(beta) V,  W = (I+A)^-1 diag(beta Gamma) K
+//   O = diag(Gamma) Q S0 + Aq U,  Aq_ij = exp(G_i - G_j) q_i.k_j  (j <= i)
+//   S_C = Gamma_C S0 + K^T diag(exp(G_C - G_i)) U.
+// Every decay ratio is exp of a non-positive number, so nothing overflows.
+// Three launches per segment of tokens:
+//   gdn_chunk_prep   (chunk, head, sequence): conv + SiLU, L2 norms, gates,
+//                    the two Gram matrices, the unit-triangular solve for Ut
+//                    and W (one column of [W | Ut] per thread, in registers),
+//                    and the decayed Q and K, written to a chunk record;
+//   gdn_chunk_state  (8-column slice of the state, head, sequence): the only
+//                    serial pass, S_{c+1} = Gamma_C S_c + Kd^T (Ut - W S_c);
+//                    it records each chunk's start state S_c and U = Ut - W S_c,
+//                    with the next chunk's W and Kd prefetched into registers
+//                    while the current one is computed;
+//   gdn_chunk_out    (chunk, head, sequence), in parallel over the chunks:
+//                    O = Qd S_c + Aq U, then RMSNorm x norm_w x SiLU(z).
+// The state update is column-separable (column j of S only needs column j of
+// V), which is what lets the state pass split the state over 16 workgroups.
+constexpr int GC_C = 64;     // tokens per chunk
+constexpr int GC_D = 128;    // key_dim = value_dim
+constexpr int GC_P = GC_D + 4;  // LDS row stride (floats) of the [C][D] tiles
+constexpr int GC_VS = 8;     // state columns per state-pass workgroup
+// chunk record (floats): W[C][D] | Ut[C][D] (U after the state pass) | Qd[C][D] | Kd[C][D] |
+// Aq[C][C] | Gamma_C, padding | S_c[D][D] (start state, written by the state pass)
+constexpr int GR_W = 0, GR_U = GC_C * GC_D, GR_Q = 2 * GC_C * GC_D, GR_K = 3 * GC_C * GC_D,
+              GR_AQ = 4 * GC_C * GC_D, GR_G = GR_AQ + GC_C * GC_C, GR_S = GR_G + 64, GR_SIZE = GR_S + GC_D * GC_D;
+
+__device__ __forceinline__ float gdn_x(const GdnArgs& a, int b, int conv_dim, int d, int tau) {
+    // conv input of channel d at token tau of sequence b; tau < 0 reads the conv state
+    // (state[0] is token -1), tau >= T is padding
+    if (tau >= a.T) return 0.0f;
+    if (tau >= 0) return gdn_load(a.mixed, a.in_dt, ((int64_t)b * a.T + tau) * a.ld_in + d);
+    return a.conv_state[((int64_t)b * conv_dim + d) * (a.K - 1) + (-tau - 1)];
+}
+
+__global__ __launch_bounds__(256) void gdn_chunk_prep(GdnArgs a, int t0, int nchunk, float* rec) {
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int nh = a.nh, K = a.K;
+    const int conv_dim = 3 * nh * GC_D;
+    const int tc = t0 + c * GC_C;  // first token of the chunk
+
+    __shared__ __attribute__((aligned(16))) float qkv_s[3 * GC_C * GC_P];  // q | k | v tiles [C][P]
+    float* const qs = qkv_s;
+    float* const ks = qkv_s + GC_C * GC_P;
+    float* const vs = qkv_s + 2 * GC_C * GC_P;
+    __shared__ __attribute__((aligned(16))) float As[GC_C * GC_C];
+    __shared__ float hx[7 * 3 * GC_D];  // the K-1 inputs before the chunk: hx[j][channel] = x_{-1-j}
+    __shared__ double Gs[GC_C];  // decay prefix sums in FP64: their differences stay exact to ~1e-16
+    __shared__ float bs[GC_C];
+
+    // ---- conv1d + SiLU.  Raw inputs of the chunk go to LDS first (coalesced
+    // rows); then one thread per channel convolves in place from the last
+    // token backwards, so the inputs it still needs are not yet overwritten;
+    // the K-1 inputs before the chunk come from the rows or the conv state ----
+    {
+        // 4 consecutive channels per item, all 24 loads of a thread in flight
+        // together (vector loads when the rows allow; element loads otherwise)
+        const int esz = a.in_dt == DT_F32 ? 4 : 2;
+        const bool vec = ((uintptr_t)a.mixed % (4 * esz)) == 0 && (a.ld_in % 4) == 0;
+        f32x4 xv[GC_C * 3 * GC_D / 4 / 256];
+#pragma unroll
+        for (int v = 0; v < GC_C * 3 * GC_D / 4 / 256; ++v) {
+            const int e = t + 256 * v, i = e / (3 * GC_D / 4), cl = (e % (3 * GC_D / 4)) * 4;
+            const int g3 = cl / GC_D, ch = cl % GC_D;
+            const int d = g3 * nh * GC_D + h * GC_D + ch;
+            const int tau = tc + i;
+            f32x4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (tau < a.T) {
+                const int64_t o = ((int64_t)b * a.T + tau) * a.ld_in + d;
+                if (vec) {
+                    x = load_act4(a.mixed, a.in_dt, o);
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) x[q] = load_act(a.mixed, a.in_dt, o + q);
+                }
+            }
+            xv[v] = x;
+        }
+#pragma unroll
+        for (int v = 0; v < GC_C * 3 * GC_D / 4 / 256; ++v) {
+            const int e = t + 256 * v, i = e / (3 * GC_D / 4), cl = (e % (3 * GC_D / 4)) * 4;
+            const int g3 = cl / GC_D, ch = cl % GC_D;
+            *reinterpret_cast<f32x4*>(&qkv_s[g3 * GC_C * GC_P + i * GC_P + ch]) = xv[v];
+        }
+    }
+    for (int e = t; e < (K - 1) * 3 * GC_D; e += 256) {
+        const int j = e / (3 * GC_D), cl = e % (3 * GC_D), g3 = cl / GC_D, ch = cl % GC_D;
+        hx[e] = gdn_x(a, b, conv_dim, g3 * nh * GC_D + h * GC_D + ch, tc - 1 - j);
+        (void)j;
+    }
+    __syncthreads();
+    {
+        // thread = (channel, 32-token half): 384 x 2 = 3 x 256 work items; the
+        // K-1 inputs before a block are read into registers before any output
+        // is written (barrier), then each thread convolves its 32 tokens in place
+        float hist[3][7], wv[3][8];
+        int colo[3];
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int item = t + 256 * u, cl = item % (3 * GC_D), i0 = (item / (3 * GC_D)) * (GC_C / 2);
+            const int g3 = cl / GC_D, ch = cl % GC_D;
+            const int d = g3 * nh * GC_D + h * GC_D + ch;
+            colo[u] = g3 * GC_C * GC_P + i0 * GC_P + ch;  // offset of token i0 in qs|ks|vs
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wv[u][j] = j < K ? a.conv_w[(int64_t)d * K + j] : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 7; ++j) {
+                const int src = i0 - 1 - j;
+                hist[u][j] = j < K - 1 ? (src >= 0 ? qs[colo[u] - (1 + j) * GC_P] : hx[(-src - 1) * 3 * GC_D + cl]) : 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            const int item = t + 256 * u, i0 = (item / (3 * GC_D)) * (GC_C / 2);
+            const float wl = a.conv_w[(int64_t)((item % (3 * GC_D)) / GC_D * nh * GC_D + h * GC_D + item % GC_D) * K + K - 1];
+#pragma unroll 8
+            for (int i = 0; i < GC_C / 2; ++i) {
+                const float x = qs[colo[u] + i * GC_P];
+                float sum = wl * x;
+#pragma unroll
+                for (int j = 0; j < 7; ++j)
+                    if (j < K - 1) sum += wv[u][j] * hist[u][j];
+#pragma unroll
+                for (int j = 6; j > 0; --j) hist[u][j] = hist[u][j - 1];
+                hist[u][0] = x;
+                qs[colo[u] + i * GC_P] = tc + i0 + i < a.T ? silu_f(sum) : 0.0f;
+            }
+        }
+    }
+    // ---- gates and the decay prefix sum (wave 0, one token per lane) ----
+    if (wave == 0) {
+        const int tau = tc + lane;
+        double g = 0.0;
+        float beta = 0.0f;
+        if (tau < a.T) {
+            const int64_t row = ((int64_t)b * a.T + tau) * a.ld_in;
+            const float av = gdn_load(a.a, a.in_dt, row + h) + a.dt_bias[h];
+            const float bv = gdn_load(a.b, a.in_dt, row + h);
+            const float sp = av > 20.0f ? av : logf(1.0f + __expf(av));
+            beta = 1.0f / (1.0f + __expf(-bv));
+            g = (double)(-__expf(a.A_log[h]) * sp);
+        }
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double o = __shfl_up(g, off);
+            if (lane >= off) g += o;
+        }
+        Gs[lane] = g;
+        bs[lane] = beta;
+    }
+    __syncthreads();
+    // ---- per-token L2 norms of q (times 1/sqrt(D)) and k: a lane pair per
+    // (token, vector), each lane summing 64 squares ----
+    {
+        const int item = t >> 1, half = t & 1;          // 128 items: token item/2, q or k
+        float* v = (item & 1 ? ks : qs) + (item >> 1) * GC_P + half * 64;
+        float ss = 0.0f;
+#pragma unroll
+        for (int d = 0; d < 64; d += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(&v[d]);
+            ss += x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w;
+        }
+        ss += __shfl_xor(ss, 1);
+        const float sc = 1.0f / sqrtf(ss + 1e-6f) * (item & 1 ? 1.0f : 1.0f / sqrtf((float)GC_D));
+        __syncthreads();  // every lane has read its row
+#pragma unroll
+        for (int d = 0; d < 64; d += 4) {
+            float4 x = *reinterpret_cast<const float4*>(&v[d]);
+            x.x *= sc; x.y *= sc; x.z *= sc; x.w *= sc;
+            *reinterpret_cast<float4*>(&v[d]) = x;
+        }
+    }
+    __syncthreads();
+    // ---- Gram tiles: thread = 4x4 tile (ti, tj) of the 64x64 lower triangle ----
+    float* R = rec + ((int64_t)(b * nh + h) * nchunk + c) * GR_SIZE;
+    {
+        const int ti = t >> 4, tj = t & 15;
+        float kk[4][4] = {}, qk[4][4] = {};
+        if (tj <= ti) {
+#pragma unroll 2
+            for (int d = 0; d < GC_D; d += 4) {
+                float4 ki[4], kj[4], qi[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    ki[r] = *reinterpret_cast<const float4*>(&ks[(4 * ti + r) * GC_P + d]);
+                    kj[r] = *reinterpret_cast<const float4*>(&ks[(4 * tj + r) * GC_P + d]);
+                    qi[r] = *reinterpret_cast<const float4*>(&qs[(4 * ti + r) * GC_P + d]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        kk[r][s] += ki[r].x * kj[s].x + ki[r].y * kj[s].y + ki[r].z * kj[s].z + ki[r].w * kj[s].w;
+                        qk[r][s] += qi[r].x * kj[s].x + qi[r].y * kj[s].y + qi[r].z * kj[s].z + qi[r].w * kj[s].w;
+                    }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 4 * ti + r;
+            float4 arow, qrow;
+            float* ap = &arow.x;
+            float* qp = &qrow.x;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const int j = 4 * tj + s;
+                const float dec = j <= i ? __expf((float)(Gs[i] - Gs[j])) : 0.0f;
+                ap[s] = j < i ? bs[i] * dec * kk[r][s] : 0.0f;
+                qp[s] = j <= i ? dec * qk[r][s] : 0.0f;
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < 4; ++s2) As[(4 * tj + s2) * GC_C + i] = ap[s2];  // transposed: As[j][i]
+            *reinterpret_cast<float4*>(&R[GR_AQ + i * GC_C + 4 * tj]) = qrow;
+        }
+    }
+    __syncthreads();
+    // ---- (I + A) X = [diag(beta Gamma) K | diag(beta) V], one column per thread,
+    // column-oriented: once x_j is final it updates every later row, so the
+    // 63 - j updates of step j are independent (A is held transposed) ----
+    {
+        const bool isw = t < GC_D;
+        const int col = t & (GC_D - 1);
+        const float* src = isw ? ks : vs;
+        float x[GC_C];
+#pragma unroll
+        for (int i = 0; i < GC_C; ++i) x[i] = bs[i] * (isw ? __expf((float)Gs[i]) : 1.0f) * src[i * GC_P + col];
+#pragma unroll
+        for (int j = 0; j < GC_C - 1; ++j) {
+            const float xj = x[j];
+#pragma unroll
+            for (int i4 = (j + 1) & ~3; i4 < GC_C; i4 += 4) {
+                const float4 ac = *reinterpret_cast<const float4*>(&As[j * GC_C + i4]);
+                if (i4 + 0 > j) x[i4 + 0] -= ac.x * xj;
+                if (i4 + 1 > j) x[i4 + 1] -= ac.y * xj;
+                if (i4 + 2 > j) x[i4 + 2] -= ac.z * xj;
+                if (i4 + 3 > j) x[i4 + 3] -= ac.w * xj;
+            }
+        }
+        float* dstp = R + (isw ? GR_W : GR_U) + col;
+#pragma unroll
+        for (int i = 0; i < GC_C; ++i) dstp[i * GC_D] = x[i];
+    }
+    // ---- decayed q and k for the scan ----
+    const double GC = Gs[GC_C - 1];
+    for (int e = t; e < GC_C * GC_D / 4; e += 256) {
+        const int i = e / (GC_D / 4), d = (e % (GC_D / 4)) * 4;
+        const float gq = __expf((float)Gs[i]), gk = __expf((float)(GC - Gs[i]));
+        float4 qv = *reinterpret_cast<const float4*>(&qs[i * GC_P + d]);
+        float4 kv = *reinterpret_cast<const float4*>(&ks[i * GC_P + d]);
+        qv.x *= gq; qv.y *= gq; qv.z *= gq; qv.w *= gq;
+        kv.x *= gk; kv.y *= gk; kv.z *= gk; kv.w *= gk;
+        *reinterpret_cast<float4*>(&R[GR_Q + i * GC_D + d]) = qv;
+        *reinterpret_cast<float4*>(&R[GR_K + i * GC_D + d]) = kv;
+    }
+    if (t == 0) R[GR_G] = __expf((float)GC);
+}
+
+// The serial pass over the chunks of one segment for an 8-column slice of one
+// head's state.  Per chunk: record S_c, U = Ut - W S_c (written over Ut), and
+// S_{c+1} = Gamma_C S_c + Kd^T U.  On the last segment the workgroup also
+// moves the conv state of 24 of the head's 384 channels (the prep kernel of
+// this segment has finished reading it).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_chunk_state(GdnArgs a, int nchunk, float* rec, int last_segment) {
+    const int sl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x;
+    const int nh = a.nh;
+    const int c0 = sl * GC_VS;  // first state column of the slice
+    constexpr int NV = GC_C * GC_D / 4 / 256;  // float4 of W (and of Kd) per thread: 8
+
+    __shared__ __attribute__((aligned(16))) float Wl[GC_C * GC_P], Kl[GC_C * GC_P];
+    __shared__ float Ss[GC_D * GC_VS], Us[GC_C * GC_VS];
+
+    float* Sg = a.rec_state + ((int64_t)b * nh + h) * GC_D * GC_D;
+    for (int e = t; e < GC_D * GC_VS; e += 256) Ss[e] = Sg[(e / GC_VS) * GC_D + c0 + e % GC_VS];
+
+    float* R0 = rec + (int64_t)(b * nh + h) * nchunk * GR_SIZE;
+    const int col = t % GC_VS, rg = t / GC_VS;  // 32 row groups
+    float4 wn[NV], kn[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int e = (t + 256 * v) * 4;
+        wn[v] = *reinterpret_cast<const float4*>(&R0[GR_W + e]);
+        kn[v] = *reinterpret_cast<const float4*>(&R0[GR_K + e]);
+    }
+    float utn0 = R0[GR_U + rg * GC_D + c0 + col], utn1 = R0[GR_U + (rg + 32) * GC_D + c0 + col];
+    float gCn = R0[GR_G];
+    for (int c = 0; c < nchunk; ++c) {
+        float* R = R0 + (int64_t)c * GR_SIZE;
+        __syncthreads();  // the previous chunk is done with Wl, Kl, Us; Ss holds S_c
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int e = (t + 256 * v) * 4, i = e / GC_D, d = e % GC_D;
+            *reinterpret_cast<float4*>(&Wl[i * GC_P + d]) = wn[v];
+            *reinterpret_cast<float4*>(&Kl[i * GC_P + d]) = kn[v];
+        }
+        const float ut0 = utn0, ut1 = utn1, gC = gCn;
+        if (c + 1 < nchunk) {  // prefetch the next chunk; consumed after this one's compute
+            const float* Rn = R + GR_SIZE;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int e = (t + 256 * v) * 4;
+                wn[v] = *reinterpret_cast<const float4*>(&Rn[GR_W + e]);
+                kn[v] = *reinterpret_cast<const float4*>(&Rn[GR_K + e]);
+            }
+            utn0 = Rn[GR_U + rg * GC_D + c0 + col];
+            utn1 = Rn[GR_U + (rg + 32) * GC_D + c0 + col];
+            gCn = Rn[GR_G];
+        }
+        // record the start state of this chunk
+        for (int e = t; e < GC_D * GC_VS; e += 256) R[GR_S + (e / GC_VS) * GC_D + c0 + e % GC_VS] = Ss[e];
+        __syncthreads();
+        // U = Ut - W S_c   (rows rg and rg + 32)
+        float p0[4] = {}, p1[4] = {};  // four partial sums per row: short dependency chains
+#pragma unroll 8
+        for (int d = 0; d < GC_D; d += 4) {
+            const float4 w0 = *reinterpret_cast<const float4*>(&Wl[rg * GC_P + d]);
+            const float4 w1 = *reinterpret_cast<const float4*>(&Wl[(rg + 32) * GC_P + d]);
+            const float s0 = Ss[(d + 0) * GC_VS + col], s1 = Ss[(d + 1) * GC_VS + col];
+            const float s2 = Ss[(d + 2) * GC_VS + col], s3 = Ss[(d + 3) * GC_VS + col];
+            p0[0] += w0.x * s0; p0[1] += w0.y * s1; p0[2] += w0.z * s2; p0[3] += w0.w * s3;
+            p1[0] += w1.x * s0; p1[1] += w1.y * s1; p1[2] += w1.z * s2; p1[3] += w1.w * s3;
+        }
+        const float u0 = ut0 - ((p0[0] + p0[1]) + (p0[2] + p0[3]));
+        const float u1 = ut1 - ((p1[0] + p1[1]) + (p1[2] + p1[3]));
+        Us[rg * GC_VS + col] = u0;
+        Us[(rg + 32) * GC_VS + col] = u1;
+        R[GR_U + rg * GC_D + c0 + col] = u0;
+        R[GR_U + (rg + 32) * GC_D + c0 + col] = u1;
+        __syncthreads();
+        // S_{c+1} = Gamma_C S_c + Kd^T U   (state rows rg + 32m)
+        float acc[4][2] = {};
+#pragma unroll 8
+        for (int i = 0; i < GC_C; i += 2) {
+            const float ua = Us[i * GC_VS + col], ub = Us[(i + 1) * GC_VS + col];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                acc[m][0] += Kl[i * GC_P + rg + 32 * m] * ua;
+                acc[m][1] += Kl[(i + 1) * GC_P + rg + 32 * m] * ub;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int d = rg + 32 * m;
+            Ss[d * GC_VS + col] = gC * Ss[d * GC_VS + col] + (acc[m][0] + acc[m][1]);
+        }
+    }
+    __syncthreads();
+    for (int e = t; e < GC_D * GC_VS; e += 256) Sg[(e / GC_VS) * GC_D + c0 + e % GC_VS] = Ss[e];
+
+    constexpr int CPS = 3 * GC_D / (GC_D / GC_VS);  // conv channels per slice: 24
+    if (last_segment && a.K > 1 && t < CPS) {
+        const int conv_dim = 3 * nh * GC_D;
+        const int cl = sl * CPS + t;  // 0 .. 383 within the head
+        const int d = cl < GC_D ? h * GC_D + cl
+                                : (cl < 2 * GC_D ? nh * GC_D + h * GC_D + cl - GC_D : 2 * nh * GC_D + h * GC_D + cl - 2 * GC_D);
+        float nv[7];
+#pragma unroll
+        for (int j = 0; j < 7; ++j) nv[j] = j < a.K - 1 ? gdn_x(a, b, conv_dim, d, a.T - 1 - j) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 7; ++j)
+            if (j < a.K - 1) a.conv_state[((int64_t)b * conv_dim + d) * (a.K - 1) + j] = nv[j];
+    }
+}
+
+// Outputs of one chunk of one head: O = Qd S_c + Aq U, then per token
+// RMSNorm x norm_w x SiLU(z).  Thread = 4 tokens x 8 columns; the 16 threads
+// of a token row are 16 consecutive lanes (row sums by xor-shuffle).
+__global__ __launch_bounds__(256) void gdn_chunk_out(GdnArgs a, int t0, int nchunk, const float* rec) {
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int t = threadIdx.x;
+    const int nh = a.nh;
+    constexpr int SP = GC_D + 4;
+    __shared__ __attribute__((aligned(16))) float Ql[GC_C * GC_P], Ul[GC_C * GC_P], Al[GC_C * GC_C], Sl[GC_D * SP];
+    const float* R = rec + ((int64_t)(b * nh + h) * nchunk + c) * GR_SIZE;
+    for (int e = t; e < GC_C * GC_D / 4; e += 256) {
+        const int i = e / (GC_D / 4), d = (e % (GC_D / 4)) * 4;
+        *reinterpret_cast<float4*>(&Ql[i * GC_P + d]) = *reinterpret_cast<const float4*>(&R[GR_Q + i * GC_D + d]);
+        *reinterpret_cast<float4*>(&Ul[i * GC_P + d]) = *reinterpret_cast<const float4*>(&R[GR_U + i * GC_D + d]);
+    }
+    for (int e = t; e < GC_C * GC_C / 4; e += 256)
+        *reinterpret_cast<float4*>(&Al[e * 4]) = *reinterpret_cast<const float4*>(&R[GR_AQ + e * 4]);
+    for (int e = t; e < GC_D * GC_D / 4; e += 256) {
+        const int i = e / (GC_D / 4), d = (e % (GC_D / 4)) * 4;
+        *reinterpret_cast<float4*>(&Sl[i * SP + d]) = *reinterpret_cast<const float4*>(&R[GR_S + i * GC_D + d]);
+    }
+    __syncthreads();
+    const int rg = t >> 4, cg = t & 15;  // rows 4rg .. 4rg+3, columns 8cg .. 8cg+7
+    float o[4][8] = {};
+    for (int d = 0; d < GC_D; d += 4) {
+        float4 q[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = *reinterpret_cast<const float4*>(&Ql[(4 * rg + r) * GC_P + d]);
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+            const float4 s0 = *reinterpret_cast<const float4*>(&Sl[(d + dd) * SP + 8 * cg]);
+            const float4 s1 = *reinterpret_cast<const float4*>(&Sl[(d + dd) * SP + 8 * cg + 4]);
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float qv = dd == 0 ? q[r].x : dd == 1 ? q[r].y : dd == 2 ? q[r].z : q[r].w;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[r][j] += qv * sv[j];
+            }
+        }
+    }
+    for (int jj = 0; jj < GC_C; jj += 4) {
+        float4 q[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) q[r] = *reinterpret_cast<const float4*>(&Al[(4 * rg + r) * GC_C + jj]);
+#pragma unroll
+        for (int dd = 0; dd < 4; ++dd) {
+            const float4 s0 = *reinterpret_cast<const float4*>(&Ul[(jj + dd) * GC_P + 8 * cg]);
+            const float4 s1 = *reinterpret_cast<const float4*>(&Ul[(jj + dd) * GC_P + 8 * cg + 4]);
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float qv = dd == 0 ? q[r].x : dd == 1 ? q[r].y : dd == 2 ? q[r].z : q[r].w;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[r][j] += qv * sv[j];
+            }
+        }
+    }
+    // ---- RMSNorm x norm_w x SiLU(z) per token row ----
+    float nw[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) nw[j] = a.norm_w[8 * cg + j];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += o[r][j] * o[r][j];
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        const int tau = t0 + c * GC_C + 4 * rg + r;
+        if (tau >= a.T) continue;
+        const float inv = 1.0f / sqrtf(ss / (float)GC_D + 1e-6f);
+        const int64_t row = (int64_t)b * a.T + tau;
+        const int64_t zi = row * a.ld_in + h * GC_D + 8 * cg;
+        const int64_t oi = row * a.ld_out + h * GC_D + 8 * cg;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float y = o[r][j] * inv * nw[j] * silu_f(gdn_load(a.z, a.in_dt, zi + j));
+            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + j] = y;
+            else store_act(a.out, a.out_dt, oi + j, y);
+        }
+    }
+}
+
+size_t gdn_chunked_bytes_per_token(int nh) { return (size_t)nh * GR_SIZE * 4 / GC_C; }
+
+hipError_t launch_gdn_chunked(const GdnArgs& a, void* ws, size_t ws_bytes, hipStream_t stream) {
+    if (a.kd != GC_D || a.vd != GC_D || a.K < 1 || a.K > 8 || a.T < 1) return hipErrorInvalidValue;
+    // tokens per segment: whole chunks whose records fit the workspace
+    const size_t per_tok = (size_t)a.B * gdn_chunked_bytes_per_token(a.nh);
+    int64_t seg = (int64_t)(ws_bytes / per_tok) / GC_C * GC_C;
+    if (seg < GC_C) return hipErrorInvalidValue;
+    seg = std::min<int64_t>(seg, ((int64_t)a.T + GC_C - 1) / GC_C * GC_C);
+    float* rec = reinterpret_cast<float*>(ws);
+    for (int t0 = 0; t0 < a.T; t0 += (int)seg) {
+        const int len = (int)std::min<int64_t>(seg, a.T - t0);
+        const int nchunk = (len + GC_C - 1) / GC_C;
+        const bool last = t0 + len >= a.T;
+        hipLaunchKernelGGL(gdn_chunk_prep, dim3(nchunk, a.nh, a.B), dim3(256), 0, stream, a, t0, nchunk, rec);
+        hipLaunchKernelGGL(gdn_chunk_state, dim3(GC_D / GC_VS, a.nh, a.B), dim3(256), 0, stream, a, nchunk, rec,
+                           last ? 1 : 0);
+        hipLaunchKernelGGL(gdn_chunk_out, dim3(nchunk, a.nh, a.B), dim3(256), 0, stream, a, t0, nchunk,
+                           (const float*)rec);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace qwk

@@ -120,6 +120,10 @@ struct GdnArgs {
     int out_dt, ld_out;
 };
 hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream);
+// chunked form for long token runs: workspace bytes per token of each sequence
+size_t gdn_chunked_bytes_per_token(int nh);
+// hipErrorInvalidValue when the workspace does not hold one 64-token chunk per sequence
+hipError_t launch_gdn_chunked(const GdnArgs& a, void* ws, size_t ws_bytes, hipStream_t stream);
 
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
 // Output rows are written to physical tile `tile_of_row(o)` (GLU interleave
