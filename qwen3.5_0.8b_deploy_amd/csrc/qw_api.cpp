@@ -17,7 +17,7 @@
 #include "qw_kernels.hpp"
 
 constexpr int kGemmMinM = 33;  // default token count from which the MFMA GEMM is used
-constexpr int kGdnChunkMin = 32;  // tokens per sequence from which the chunked Gated-DeltaNet form runs
+constexpr int kGdnChunkMin = 24;  // tokens per sequence from which the chunked Gated-DeltaNet form runs (measured crossover 20-26)
 
 struct qw_ctx {
     int device = 0;

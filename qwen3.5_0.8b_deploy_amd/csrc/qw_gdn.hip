@@ -219,7 +219,7 @@ hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
 //                    the two Gram matrices, the unit-triangular solve for Ut
 //                    and W (one column of [W | Ut] per thread, in registers),
 //                    and the decayed Q and K, written to a chunk record;
-//   gdn_chunk_state  (8-column slice of the state, head, sequence): the only
+//   gdn_chunk_state  (16-column slice of the state, head, sequence): the only
 //                    serial pass, S_{c+1} = Gamma_C S_c + Kd^T (Ut - W S_c);
 //                    it records each chunk's start state S_c and U = Ut - W S_c,
 //                    with the next chunk's W and Kd prefetched into registers
@@ -227,15 +227,25 @@ hipError_t launch_gdn(const GdnArgs& a, hipStream_t stream) {
 //   gdn_chunk_out    (chunk, head, sequence), in parallel over the chunks:
 //                    O = Qd S_c + Aq U, then RMSNorm x norm_w x SiLU(z).
 // The state update is column-separable (column j of S only needs column j of
-// V), which is what lets the state pass split the state over 16 workgroups.
+// V), which is what lets the state pass split the state over 8 workgroups.
+// Every product runs on FP32 MFMA (exact FP32 products, FP32 accumulation).
 constexpr int GC_C = 64;     // tokens per chunk
 constexpr int GC_D = 128;    // key_dim = value_dim
 constexpr int GC_P = GC_D + 4;  // LDS row stride (floats) of the [C][D] tiles
-constexpr int GC_VS = 8;     // state columns per state-pass workgroup
+constexpr int GC_VS = 16;    // state columns per state-pass workgroup
 // chunk record (floats): W[C][D] | Ut[C][D] (U after the state pass) | Qd[C][D] | Kd[C][D] |
 // Aq[C][C] | Gamma_C, padding | S_c[D][D] (start state, written by the state pass)
 constexpr int GR_W = 0, GR_U = GC_C * GC_D, GR_Q = 2 * GC_C * GC_D, GR_K = 3 * GC_C * GC_D,
               GR_AQ = 4 * GC_C * GC_D, GR_G = GR_AQ + GC_C * GC_C, GR_S = GR_G + 64, GR_SIZE = GR_S + GC_D * GC_D;
+
+// FP32 MFMA 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
+// D[4*(l/16) + r][l%16] in element r.  The k index of a product only has to be
+// the same permutation on both sides, so a 16-deep k block is fed as four
+// steps q with k = 4*(l/16) + q: a float4 along k per lane and operand, and a
+// D tile is directly the B operand of a following product.
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 __device__ __forceinline__ float gdn_x(const GdnArgs& a, int b, int conv_dim, int d, int tau) {
     // conv input of channel d at token tau of sequence b; tau < 0 reads the conv state
@@ -271,23 +281,25 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnArgs a, int t0, int nch
         const int esz = a.in_dt == DT_F32 ? 4 : 2;
         const bool vec = ((uintptr_t)a.mixed % (4 * esz)) == 0 && (a.ld_in % 4) == 0;
         f32x4 xv[GC_C * 3 * GC_D / 4 / 256];
+        if (vec) {  // branch-free: rows past T are read clamped and zeroed
 #pragma unroll
-        for (int v = 0; v < GC_C * 3 * GC_D / 4 / 256; ++v) {
-            const int e = t + 256 * v, i = e / (3 * GC_D / 4), cl = (e % (3 * GC_D / 4)) * 4;
-            const int g3 = cl / GC_D, ch = cl % GC_D;
-            const int d = g3 * nh * GC_D + h * GC_D + ch;
-            const int tau = tc + i;
-            f32x4 x = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (tau < a.T) {
-                const int64_t o = ((int64_t)b * a.T + tau) * a.ld_in + d;
-                if (vec) {
-                    x = load_act4(a.mixed, a.in_dt, o);
-                } else {
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) x[q] = load_act(a.mixed, a.in_dt, o + q);
-                }
+            for (int v = 0; v < GC_C * 3 * GC_D / 4 / 256; ++v) {
+                const int e = t + 256 * v, i = e / (3 * GC_D / 4), cl = (e % (3 * GC_D / 4)) * 4;
+                const int d = (cl / GC_D) * nh * GC_D + h * GC_D + cl % GC_D;
+                const int tau = tc + i;
+                const int64_t o = ((int64_t)b * a.T + min(tau, a.T - 1)) * a.ld_in + d;
+                const f32x4 x = a.in_dt == DT_F32 ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.mixed) + o)
+                                                  : load_act4(a.mixed, a.in_dt, o);
+                xv[v] = tau < a.T ? x : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-            xv[v] = x;
+        } else {
+#pragma unroll
+            for (int v = 0; v < GC_C * 3 * GC_D / 4 / 256; ++v) {
+                const int e = t + 256 * v, i = e / (3 * GC_D / 4), cl = (e % (3 * GC_D / 4)) * 4;
+                const int d = (cl / GC_D) * nh * GC_D + h * GC_D + cl % GC_D;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[v][q] = gdn_x(a, b, conv_dim, d + q, tc + i);
+            }
         }
 #pragma unroll
         for (int v = 0; v < GC_C * 3 * GC_D / 4 / 256; ++v) {
@@ -385,74 +397,107 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnArgs a, int t0, int nch
         }
     }
     __syncthreads();
-    // ---- Gram tiles: thread = 4x4 tile (ti, tj) of the 64x64 lower triangle ----
+    // ---- Gram tiles on MFMA: the 10 lower 16x16 tiles (ti >= tj) of K K^T and
+    // Q K^T; A = beta_i exp(G_i - G_j) k_i.k_j (j < i) into LDS transposed
+    // (As[j][i]); Aq = exp(G_i - G_j) q_i.k_j (j <= i) to the record ----
     float* R = rec + ((int64_t)(b * nh + h) * nchunk + c) * GR_SIZE;
-    {
-        const int ti = t >> 4, tj = t & 15;
-        float kk[4][4] = {}, qk[4][4] = {};
-        if (tj <= ti) {
+    const int li = lane & 15, lg = lane >> 4;
+    for (int job = wave; job < 10; job += 4) {
+        const int ti = job < 1 ? 0 : job < 3 ? 1 : job < 6 ? 2 : 3;
+        const int tj = job - ti * (ti + 1) / 2;
+        f32x4 kk = {0.0f, 0.0f, 0.0f, 0.0f}, qk = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 2
-            for (int d = 0; d < GC_D; d += 4) {
-                float4 ki[4], kj[4], qi[4];
+        for (int kb = 0; kb < GC_D; kb += 16) {
+            const f32x4 ka = *reinterpret_cast<const f32x4*>(&ks[(16 * ti + li) * GC_P + kb + 4 * lg]);
+            const f32x4 qa = *reinterpret_cast<const f32x4*>(&qs[(16 * ti + li) * GC_P + kb + 4 * lg]);
+            const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&ks[(16 * tj + li) * GC_P + kb + 4 * lg]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    ki[r] = *reinterpret_cast<const float4*>(&ks[(4 * ti + r) * GC_P + d]);
-                    kj[r] = *reinterpret_cast<const float4*>(&ks[(4 * tj + r) * GC_P + d]);
-                    qi[r] = *reinterpret_cast<const float4*>(&qs[(4 * ti + r) * GC_P + d]);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        kk[r][s] += ki[r].x * kj[s].x + ki[r].y * kj[s].y + ki[r].z * kj[s].z + ki[r].w * kj[s].w;
-                        qk[r][s] += qi[r].x * kj[s].x + qi[r].y * kj[s].y + qi[r].z * kj[s].z + qi[r].w * kj[s].w;
-                    }
+            for (int q = 0; q < 4; ++q) {
+                kk = mfma16(ka[q], kb4[q], kk);
+                qk = mfma16(qa[q], kb4[q], qk);
             }
         }
+        const int j = 16 * tj + li;
+        f32x4 av;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int i = 4 * ti + r;
-            float4 arow, qrow;
-            float* ap = &arow.x;
-            float* qp = &qrow.x;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int j = 4 * tj + s;
-                const float dec = j <= i ? __expf((float)(Gs[i] - Gs[j])) : 0.0f;
-                ap[s] = j < i ? bs[i] * dec * kk[r][s] : 0.0f;
-                qp[s] = j <= i ? dec * qk[r][s] : 0.0f;
-            }
-#pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) As[(4 * tj + s2) * GC_C + i] = ap[s2];  // transposed: As[j][i]
-            *reinterpret_cast<float4*>(&R[GR_AQ + i * GC_C + 4 * tj]) = qrow;
+            const int i = 16 * ti + 4 * lg + r;
+            const float dec = j <= i ? __expf((float)(Gs[i] - Gs[j])) : 0.0f;
+            av[r] = j < i ? bs[i] * dec * kk[r] : 0.0f;
+            R[GR_AQ + i * GC_C + j] = j <= i ? dec * qk[r] : 0.0f;
         }
+        *reinterpret_cast<f32x4*>(&As[j * GC_C + 16 * ti + 4 * lg]) = av;
+    }
+    // upper tiles of Aq are zero
+    for (int e = t; e < 6 * 256; e += 256) {
+        const int tile = e >> 8, w = e & 255;
+        const int ti = tile < 3 ? 0 : tile < 5 ? 1 : 2;
+        const int tj = ti + 1 + (tile - (ti == 0 ? 0 : ti == 1 ? 3 : 5));
+        R[GR_AQ + (16 * ti + (w >> 4)) * GC_C + 16 * tj + (w & 15)] = 0.0f;
     }
     __syncthreads();
-    // ---- (I + A) X = [diag(beta Gamma) K | diag(beta) V], one column per thread,
-    // column-oriented: once x_j is final it updates every later row, so the
-    // 63 - j updates of step j are independent (A is held transposed) ----
+    // ---- (I + A) X = [diag(beta Gamma) K | diag(beta) V] by 16-row blocks:
+    // the four diagonal blocks are inverted by substitution (wave 0, one lane
+    // per column of a block), then each wave runs the block substitution
+    //   X_b = T_bb (R_b - sum_{c<b} A_bc X_c)
+    // on MFMA for its 64 of the 256 right-hand-side columns, X in registers ----
+    __shared__ __attribute__((aligned(16))) float Tl[4 * 256];  // T_bb[m][j]
+    if (wave == 0) {
+        const int bb = lg, jc = li;
+        float x[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            float v = m == jc ? 1.0f : 0.0f;
+#pragma unroll
+            for (int n = 0; n < m; ++n) v -= As[(16 * bb + n) * GC_C + 16 * bb + m] * x[n];
+            x[m] = v;
+        }
+#pragma unroll
+        for (int m = 0; m < 16; ++m) Tl[bb * 256 + m * 16 + jc] = x[m];
+    }
+    __syncthreads();
     {
-        const bool isw = t < GC_D;
-        const int col = t & (GC_D - 1);
+        const bool isw = wave < 2;
         const float* src = isw ? ks : vs;
-        float x[GC_C];
+        const int cbase = (wave & 1) * 64;  // column base within K (waves 0, 1) or V (waves 2, 3)
+        f32x4 X[4][4];
 #pragma unroll
-        for (int i = 0; i < GC_C; ++i) x[i] = bs[i] * (isw ? __expf((float)Gs[i]) : 1.0f) * src[i * GC_P + col];
+        for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-        for (int j = 0; j < GC_C - 1; ++j) {
-            const float xj = x[j];
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * rb + 4 * lg + r;
+                const float sc = bs[i] * (isw ? __expf((float)Gs[i]) : 1.0f);
 #pragma unroll
-            for (int i4 = (j + 1) & ~3; i4 < GC_C; i4 += 4) {
-                const float4 ac = *reinterpret_cast<const float4*>(&As[j * GC_C + i4]);
-                if (i4 + 0 > j) x[i4 + 0] -= ac.x * xj;
-                if (i4 + 1 > j) x[i4 + 1] -= ac.y * xj;
-                if (i4 + 2 > j) x[i4 + 2] -= ac.z * xj;
-                if (i4 + 3 > j) x[i4 + 3] -= ac.w * xj;
+                for (int ct = 0; ct < 4; ++ct) X[rb][ct][r] = sc * src[i * GC_P + cbase + 16 * ct + li];
+            }
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+            for (int cb = 0; cb < rb; ++cb) {
+                float na[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) na[q] = -As[(16 * cb + 4 * lg + q) * GC_C + 16 * rb + li];
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) X[rb][ct] = mfma16(na[q], X[cb][ct][q], X[rb][ct]);
+            }
+            const f32x4 ta = *reinterpret_cast<const f32x4*>(&Tl[rb * 256 + li * 16 + 4 * lg]);
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                f32x4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) y = mfma16(ta[q], X[rb][ct][q], y);
+                X[rb][ct] = y;
             }
         }
-        float* dstp = R + (isw ? GR_W : GR_U) + col;
+        float* dstp = R + (isw ? GR_W : GR_U) + cbase;
 #pragma unroll
-        for (int i = 0; i < GC_C; ++i) dstp[i * GC_D] = x[i];
+        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dstp[(16 * rb + 4 * lg + r) * GC_D + 16 * ct + li] = X[rb][ct][r];
     }
     // ---- decayed q and k for the scan ----
     const double GC = Gs[GC_C - 1];
@@ -469,104 +514,102 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep(GdnArgs a, int t0, int nch
     if (t == 0) R[GR_G] = __expf((float)GC);
 }
 
-// The serial pass over the chunks of one segment for an 8-column slice of one
-// head's state.  Per chunk: record S_c, U = Ut - W S_c (written over Ut), and
-// S_{c+1} = Gamma_C S_c + Kd^T U.  On the last segment the workgroup also
-// moves the conv state of 24 of the head's 384 channels (the prep kernel of
-// this segment has finished reading it).
+// The serial pass over the chunks of one segment for a 16-column slice of
+// one head's state, on MFMA.  Per chunk: record S_c, U = Ut - W S_c (wave w:
+// rows 16w..16w+15, written over Ut), S_{c+1} = Gamma_C S_c + Kd^T U (wave w:
+// state rows 32w..32w+31).  The state slice lives in LDS transposed
+// (St[j][d]); the next chunk's W, Kd, Ut tile and Gamma_C are prefetched into
+// registers while the current one is computed.  On the last segment the
+// workgroup also moves the conv state of 48 of the head's 384 channels (the
+// prep kernel of this segment has finished reading it).
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_chunk_state(GdnArgs a, int nchunk, float* rec, int last_segment) {
     const int sl = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, li = lane & 15, lg = lane >> 4;
     const int nh = a.nh;
     const int c0 = sl * GC_VS;  // first state column of the slice
     constexpr int NV = GC_C * GC_D / 4 / 256;  // float4 of W (and of Kd) per thread: 8
+    constexpr int UP = GC_C + 4;               // row stride of the transposed U tile
 
     __shared__ __attribute__((aligned(16))) float Wl[GC_C * GC_P], Kl[GC_C * GC_P];
-    __shared__ float Ss[GC_D * GC_VS], Us[GC_C * GC_VS];
+    __shared__ __attribute__((aligned(16))) float St[GC_VS * GC_P], Ut[GC_VS * UP];
 
     float* Sg = a.rec_state + ((int64_t)b * nh + h) * GC_D * GC_D;
-    for (int e = t; e < GC_D * GC_VS; e += 256) Ss[e] = Sg[(e / GC_VS) * GC_D + c0 + e % GC_VS];
+    for (int e = t; e < GC_D * GC_VS; e += 256) {
+        const int d = e / GC_VS, j = e % GC_VS;
+        St[j * GC_P + d] = Sg[d * GC_D + c0 + j];
+    }
 
     float* R0 = rec + (int64_t)(b * nh + h) * nchunk * GR_SIZE;
-    const int col = t % GC_VS, rg = t / GC_VS;  // 32 row groups
-    float4 wn[NV], kn[NV];
+    f32x4 wn[NV], kn[NV], un;
+    float gCn;
+    auto prefetch = [&](const float* Rc) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-        const int e = (t + 256 * v) * 4;
-        wn[v] = *reinterpret_cast<const float4*>(&R0[GR_W + e]);
-        kn[v] = *reinterpret_cast<const float4*>(&R0[GR_K + e]);
-    }
-    float utn0 = R0[GR_U + rg * GC_D + c0 + col], utn1 = R0[GR_U + (rg + 32) * GC_D + c0 + col];
-    float gCn = R0[GR_G];
+        for (int v = 0; v < NV; ++v) {
+            const int e = (t + 256 * v) * 4;
+            wn[v] = *reinterpret_cast<const f32x4*>(&Rc[GR_W + e]);
+            kn[v] = *reinterpret_cast<const f32x4*>(&Rc[GR_K + e]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) un[r] = Rc[GR_U + (16 * wave + 4 * lg + r) * GC_D + c0 + li];
+        gCn = Rc[GR_G];
+    };
+    prefetch(R0);
     for (int c = 0; c < nchunk; ++c) {
         float* R = R0 + (int64_t)c * GR_SIZE;
-        __syncthreads();  // the previous chunk is done with Wl, Kl, Us; Ss holds S_c
+        __syncthreads();  // the previous chunk is done with Wl, Kl, Ut; St holds S_c
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int e = (t + 256 * v) * 4, i = e / GC_D, d = e % GC_D;
-            *reinterpret_cast<float4*>(&Wl[i * GC_P + d]) = wn[v];
-            *reinterpret_cast<float4*>(&Kl[i * GC_P + d]) = kn[v];
+            *reinterpret_cast<f32x4*>(&Wl[i * GC_P + d]) = wn[v];
+            *reinterpret_cast<f32x4*>(&Kl[i * GC_P + d]) = kn[v];
         }
-        const float ut0 = utn0, ut1 = utn1, gC = gCn;
-        if (c + 1 < nchunk) {  // prefetch the next chunk; consumed after this one's compute
-            const float* Rn = R + GR_SIZE;
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                const int e = (t + 256 * v) * 4;
-                wn[v] = *reinterpret_cast<const float4*>(&Rn[GR_W + e]);
-                kn[v] = *reinterpret_cast<const float4*>(&Rn[GR_K + e]);
-            }
-            utn0 = Rn[GR_U + rg * GC_D + c0 + col];
-            utn1 = Rn[GR_U + (rg + 32) * GC_D + c0 + col];
-            gCn = Rn[GR_G];
-        }
+        f32x4 u = un;
+        const float gC = gCn;
+        if (c + 1 < nchunk) prefetch(R + GR_SIZE);  // consumed after this chunk's compute
         // record the start state of this chunk
-        for (int e = t; e < GC_D * GC_VS; e += 256) R[GR_S + (e / GC_VS) * GC_D + c0 + e % GC_VS] = Ss[e];
-        __syncthreads();
-        // U = Ut - W S_c   (rows rg and rg + 32)
-        float p0[4] = {}, p1[4] = {};  // four partial sums per row: short dependency chains
-#pragma unroll 8
-        for (int d = 0; d < GC_D; d += 4) {
-            const float4 w0 = *reinterpret_cast<const float4*>(&Wl[rg * GC_P + d]);
-            const float4 w1 = *reinterpret_cast<const float4*>(&Wl[(rg + 32) * GC_P + d]);
-            const float s0 = Ss[(d + 0) * GC_VS + col], s1 = Ss[(d + 1) * GC_VS + col];
-            const float s2 = Ss[(d + 2) * GC_VS + col], s3 = Ss[(d + 3) * GC_VS + col];
-            p0[0] += w0.x * s0; p0[1] += w0.y * s1; p0[2] += w0.z * s2; p0[3] += w0.w * s3;
-            p1[0] += w1.x * s0; p1[1] += w1.y * s1; p1[2] += w1.z * s2; p1[3] += w1.w * s3;
+        for (int e = t; e < GC_D * GC_VS; e += 256) {
+            const int d = e / GC_VS, j = e % GC_VS;
+            R[GR_S + d * GC_D + c0 + j] = St[j * GC_P + d];
         }
-        const float u0 = ut0 - ((p0[0] + p0[1]) + (p0[2] + p0[3]));
-        const float u1 = ut1 - ((p1[0] + p1[1]) + (p1[2] + p1[3]));
-        Us[rg * GC_VS + col] = u0;
-        Us[(rg + 32) * GC_VS + col] = u1;
-        R[GR_U + rg * GC_D + c0 + col] = u0;
-        R[GR_U + (rg + 32) * GC_D + c0 + col] = u1;
         __syncthreads();
-        // S_{c+1} = Gamma_C S_c + Kd^T U   (state rows rg + 32m)
-        float acc[4][2] = {};
-#pragma unroll 8
-        for (int i = 0; i < GC_C; i += 2) {
-            const float ua = Us[i * GC_VS + col], ub = Us[(i + 1) * GC_VS + col];
+        // U = Ut - W S_c   (wave w: rows 16w .. 16w+15)
+#pragma unroll 4
+        for (int kb = 0; kb < GC_D; kb += 16) {
+            const f32x4 wa = *reinterpret_cast<const f32x4*>(&Wl[(16 * wave + li) * GC_P + kb + 4 * lg]);
+            const f32x4 sb = *reinterpret_cast<const f32x4*>(&St[li * GC_P + kb + 4 * lg]);
 #pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                acc[m][0] += Kl[i * GC_P + rg + 32 * m] * ua;
-                acc[m][1] += Kl[(i + 1) * GC_P + rg + 32 * m] * ub;
+            for (int q = 0; q < 4; ++q) u = mfma16(-wa[q], sb[q], u);
+        }
+        *reinterpret_cast<f32x4*>(&Ut[li * UP + 16 * wave + 4 * lg]) = u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) R[GR_U + (16 * wave + 4 * lg + r) * GC_D + c0 + li] = u[r];
+        __syncthreads();
+        // S_{c+1} = Gamma_C S_c + Kd^T U   (wave w: state rows 32w .. 32w+31)
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+            const int d0 = 32 * wave + 16 * dt;
+            f32x4 acc = *reinterpret_cast<const f32x4*>(&St[li * GC_P + d0 + 4 * lg]);
+            acc = acc * gC;
+#pragma unroll
+            for (int ib = 0; ib < GC_C; ib += 16) {
+                const f32x4 ub = *reinterpret_cast<const f32x4*>(&Ut[li * UP + ib + 4 * lg]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc = mfma16(Kl[(ib + 4 * lg + q) * GC_P + d0 + li], ub[q], acc);
             }
-        }
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int d = rg + 32 * m;
-            Ss[d * GC_VS + col] = gC * Ss[d * GC_VS + col] + (acc[m][0] + acc[m][1]);
+            *reinterpret_cast<f32x4*>(&St[li * GC_P + d0 + 4 * lg]) = acc;
         }
     }
     __syncthreads();
-    for (int e = t; e < GC_D * GC_VS; e += 256) Sg[(e / GC_VS) * GC_D + c0 + e % GC_VS] = Ss[e];
+    for (int e = t; e < GC_D * GC_VS; e += 256) {
+        const int d = e / GC_VS, j = e % GC_VS;
+        Sg[d * GC_D + c0 + j] = St[j * GC_P + d];
+    }
 
-    constexpr int CPS = 3 * GC_D / (GC_D / GC_VS);  // conv channels per slice: 24
+    constexpr int CPS = 3 * GC_D / (GC_D / GC_VS);  // conv channels per slice: 48
     if (last_segment && a.K > 1 && t < CPS) {
         const int conv_dim = 3 * nh * GC_D;
         const int cl = sl * CPS + t;  // 0 .. 383 within the head
-        const int d = cl < GC_D ? h * GC_D + cl
-                                : (cl < 2 * GC_D ? nh * GC_D + h * GC_D + cl - GC_D : 2 * nh * GC_D + h * GC_D + cl - 2 * GC_D);
+        const int d = (cl / GC_D) * nh * GC_D + h * GC_D + cl % GC_D;
         float nv[7];
 #pragma unroll
         for (int j = 0; j < 7; ++j) nv[j] = j < a.K - 1 ? gdn_x(a, b, conv_dim, d, a.T - 1 - j) : 0.0f;
@@ -576,88 +619,103 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
 }
 
-// Outputs of one chunk of one head: O = Qd S_c + Aq U, then per token
-// RMSNorm x norm_w x SiLU(z).  Thread = 4 tokens x 8 columns; the 16 threads
-// of a token row are 16 consecutive lanes (row sums by xor-shuffle).
+// Outputs of one chunk of one head on MFMA: O = Qd S_c + Aq U (wave w: output
+// columns 32w .. 32w+31, all 64 rows), then per token RMSNorm x norm_w x
+// SiLU(z), the row sums combined across the waves in LDS.
 __global__ __launch_bounds__(256) void gdn_chunk_out(GdnArgs a, int t0, int nchunk, const float* rec) {
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int t = threadIdx.x;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, li = lane & 15, lg = lane >> 4;
     const int nh = a.nh;
-    constexpr int SP = GC_D + 4;
-    __shared__ __attribute__((aligned(16))) float Ql[GC_C * GC_P], Ul[GC_C * GC_P], Al[GC_C * GC_C], Sl[GC_D * SP];
+    constexpr int AP = GC_C + 4;  // row stride of Aq and of the transposed U
+    __shared__ __attribute__((aligned(16))) float Ql[GC_C * GC_P], STl[GC_D * GC_P], Al[GC_C * AP], UTl[GC_D * AP];
+    __shared__ float red[4][GC_C];
     const float* R = rec + ((int64_t)(b * nh + h) * nchunk + c) * GR_SIZE;
     for (int e = t; e < GC_C * GC_D / 4; e += 256) {
         const int i = e / (GC_D / 4), d = (e % (GC_D / 4)) * 4;
-        *reinterpret_cast<float4*>(&Ql[i * GC_P + d]) = *reinterpret_cast<const float4*>(&R[GR_Q + i * GC_D + d]);
-        *reinterpret_cast<float4*>(&Ul[i * GC_P + d]) = *reinterpret_cast<const float4*>(&R[GR_U + i * GC_D + d]);
+        *reinterpret_cast<f32x4*>(&Ql[i * GC_P + d]) = *reinterpret_cast<const f32x4*>(&R[GR_Q + i * GC_D + d]);
+        const f32x4 uv = *reinterpret_cast<const f32x4*>(&R[GR_U + i * GC_D + d]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) UTl[(d + q) * AP + i] = uv[q];
     }
-    for (int e = t; e < GC_C * GC_C / 4; e += 256)
-        *reinterpret_cast<float4*>(&Al[e * 4]) = *reinterpret_cast<const float4*>(&R[GR_AQ + e * 4]);
+    for (int e = t; e < GC_C * GC_C / 4; e += 256) {
+        const int i = e / (GC_C / 4), j = (e % (GC_C / 4)) * 4;
+        *reinterpret_cast<f32x4*>(&Al[i * AP + j]) = *reinterpret_cast<const f32x4*>(&R[GR_AQ + i * GC_C + j]);
+    }
     for (int e = t; e < GC_D * GC_D / 4; e += 256) {
-        const int i = e / (GC_D / 4), d = (e % (GC_D / 4)) * 4;
-        *reinterpret_cast<float4*>(&Sl[i * SP + d]) = *reinterpret_cast<const float4*>(&R[GR_S + i * GC_D + d]);
+        const int k = e / (GC_D / 4), j = (e % (GC_D / 4)) * 4;
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(&R[GR_S + k * GC_D + j]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) STl[(j + q) * GC_P + k] = sv[q];
     }
     __syncthreads();
-    const int rg = t >> 4, cg = t & 15;  // rows 4rg .. 4rg+3, columns 8cg .. 8cg+7
-    float o[4][8] = {};
-    for (int d = 0; d < GC_D; d += 4) {
-        float4 q[4];
+    f32x4 o[4][2];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) q[r] = *reinterpret_cast<const float4*>(&Ql[(4 * rg + r) * GC_P + d]);
+    for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-            const float4 s0 = *reinterpret_cast<const float4*>(&Sl[(d + dd) * SP + 8 * cg]);
-            const float4 s1 = *reinterpret_cast<const float4*>(&Sl[(d + dd) * SP + 8 * cg + 4]);
-            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        for (int ct = 0; ct < 2; ++ct) o[rt][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int cb = 32 * wave;
+#pragma unroll 2
+    for (int kb = 0; kb < GC_D; kb += 16) {
+        f32x4 qa[4], sb[2];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float qv = dd == 0 ? q[r].x : dd == 1 ? q[r].y : dd == 2 ? q[r].z : q[r].w;
+        for (int rt = 0; rt < 4; ++rt) qa[rt] = *reinterpret_cast<const f32x4*>(&Ql[(16 * rt + li) * GC_P + kb + 4 * lg]);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) o[r][j] += qv * sv[j];
+        for (int ct = 0; ct < 2; ++ct) sb[ct] = *reinterpret_cast<const f32x4*>(&STl[(cb + 16 * ct + li) * GC_P + kb + 4 * lg]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) o[rt][ct] = mfma16(qa[rt][q], sb[ct][q], o[rt][ct]);
+    }
+#pragma unroll
+    for (int kb = 0; kb < GC_C; kb += 16) {
+        f32x4 qa[4], sb[2];
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) qa[rt] = *reinterpret_cast<const f32x4*>(&Al[(16 * rt + li) * AP + kb + 4 * lg]);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) sb[ct] = *reinterpret_cast<const f32x4*>(&UTl[(cb + 16 * ct + li) * AP + kb + 4 * lg]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) o[rt][ct] = mfma16(qa[rt][q], sb[ct][q], o[rt][ct]);
+    }
+    // ---- RMSNorm x norm_w x SiLU(z) per token row: partial sums per wave ----
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float ss = o[rt][0][r] * o[rt][0][r] + o[rt][1][r] * o[rt][1][r];
+#pragma unroll
+            for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+            if (li == 0) red[wave][16 * rt + 4 * lg + r] = ss;
+        }
+    __syncthreads();
+    const float nw0 = a.norm_w[cb + li], nw1 = a.norm_w[cb + 16 + li];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * rt + 4 * lg + r;
+            const int tau = t0 + c * GC_C + i;
+            if (tau >= a.T) continue;
+            const float tot = red[0][i] + red[1][i] + red[2][i] + red[3][i];
+            const float inv = 1.0f / sqrtf(tot / (float)GC_D + 1e-6f);
+            const int64_t row = (int64_t)b * a.T + tau;
+            const int64_t zi = row * a.ld_in + h * GC_D + cb + li;
+            const int64_t oi = row * a.ld_out + h * GC_D + cb + li;
+            const float y0 = o[rt][0][r] * inv * nw0 * silu_f(gdn_load(a.z, a.in_dt, zi));
+            const float y1 = o[rt][1][r] * inv * nw1 * silu_f(gdn_load(a.z, a.in_dt, zi + 16));
+            if (a.out_dt == DT_F32) {
+                reinterpret_cast<float*>(a.out)[oi] = y0;
+                reinterpret_cast<float*>(a.out)[oi + 16] = y1;
+            } else {
+                store_act(a.out, a.out_dt, oi, y0);
+                store_act(a.out, a.out_dt, oi + 16, y1);
             }
         }
-    }
-    for (int jj = 0; jj < GC_C; jj += 4) {
-        float4 q[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) q[r] = *reinterpret_cast<const float4*>(&Al[(4 * rg + r) * GC_C + jj]);
-#pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-            const float4 s0 = *reinterpret_cast<const float4*>(&Ul[(jj + dd) * GC_P + 8 * cg]);
-            const float4 s1 = *reinterpret_cast<const float4*>(&Ul[(jj + dd) * GC_P + 8 * cg + 4]);
-            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float qv = dd == 0 ? q[r].x : dd == 1 ? q[r].y : dd == 2 ? q[r].z : q[r].w;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o[r][j] += qv * sv[j];
-            }
-        }
-    }
-    // ---- RMSNorm x norm_w x SiLU(z) per token row ----
-    float nw[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) nw[j] = a.norm_w[8 * cg + j];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss += o[r][j] * o[r][j];
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-        const int tau = t0 + c * GC_C + 4 * rg + r;
-        if (tau >= a.T) continue;
-        const float inv = 1.0f / sqrtf(ss / (float)GC_D + 1e-6f);
-        const int64_t row = (int64_t)b * a.T + tau;
-        const int64_t zi = row * a.ld_in + h * GC_D + 8 * cg;
-        const int64_t oi = row * a.ld_out + h * GC_D + 8 * cg;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float y = o[r][j] * inv * nw[j] * silu_f(gdn_load(a.z, a.in_dt, zi + j));
-            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + j] = y;
-            else store_act(a.out, a.out_dt, oi + j, y);
-        }
-    }
 }
 
 size_t gdn_chunked_bytes_per_token(int nh) { return (size_t)nh * GR_SIZE * 4 / GC_C; }
