@@ -67,6 +67,11 @@ def lib():
             "orc_gdn_step": [_i, _i, _i, _i, _i, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                              _f32p, _f32p, _f32p],
             "orc_mt64_raw": [ctypes.c_uint64, np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS"), _i64],
+            "orc_attn_norm_rope": [_f32p, _f32p, _i, _i, _i, _i, _fl, _f32p, _f32p, _i],
+            "orc_kv_quant_int8": [_f32p, _i, _i8p, _f32p],
+            "orc_attn_token": [_f32p, _f32p, _f32p, _f32p, _i, _i, _i, _i, _f32p],
+            "orc_full_attn_seq": [_i, _i, _i, _i, _i, _i, _fl, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _i,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, _f32p],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -98,6 +103,8 @@ def ref_lib():
         R.ref_lmhead_time.restype = ctypes.c_double
         R.ref_linear_attn.argtypes = [_f32p, _f32p] + [_i] * 6 + [_f32p] * 11
         R.ref_linear_attn.restype = ctypes.c_int
+        R.ref_full_attn.argtypes = [_f32p, _f32p] + [_i] * 6 + [_fl, _fl] + [_f32p] * 6
+        R.ref_full_attn.restype = ctypes.c_int
         _REF = R
     return _REF
 
@@ -344,3 +351,70 @@ def ref_linear_attn(x, Wqkv, Wa, Wb, Wz, conv_w, A_log, dt_bias, norm_w, Wout, c
     if rc != 0:
         raise RuntimeError("reference LinearAttention raised")
     return y, cs, rs
+
+
+# ---- gated full attention ----------------------------------------------------
+def attn_norm_rope(q, k, q_norm_w, k_norm_w, position, nh, nkv, hd, rotary_dim, theta):
+    """Per-head RMSNorm (1 + w) and RoPE of one token's q [nh*hd], k [nkv*hd]
+    (language_full_attn.cpp:77-108,156-163); returns new arrays."""
+    q = _c(q, np.float32).copy()
+    k = _c(k, np.float32).copy()
+    lib().orc_attn_norm_rope(q, k, nh, nkv, hd, rotary_dim, theta, _c(q_norm_w, np.float32),
+                             _c(k_norm_w, np.float32), int(position))
+    return q, k
+
+
+def kv_quant_int8(x):
+    """INT8 of one head vector with its scale (full_attention_cuda.cu:130-150)."""
+    x = _c(x, np.float32)
+    q = np.empty(x.shape[0], np.int8)
+    s = np.empty(1, np.float32)
+    lib().orc_kv_quant_int8(x, x.shape[0], q, s)
+    return q, float(s[0])
+
+
+def attn_token(q, gate, kc, vc, nh, nkv, hd):
+    """One query token over an FP32 cache [len][nkv][hd], then the sigmoid gate
+    (language_full_attn.cpp:165-207)."""
+    kc = _c(kc, np.float32)
+    out = np.empty(nh * hd, np.float32)
+    lib().orc_attn_token(_c(q, np.float32), _c(gate, np.float32), kc, _c(vc, np.float32), kc.shape[0], nh, nkv,
+                         hd, out)
+    return out
+
+
+def full_attn_seq(q, gate, k, v, q_norm_w, k_norm_w, nh, nkv, hd, rotary_dim=64, theta=1.0e7, pos0=0,
+                  cache=None, int8=False, capacity=None):
+    """T tokens of one sequence between the projections: q, gate [T][nh*hd],
+    k, v [T][nkv*hd] raw projections.  `cache` = (kc, vc, ks, vs) arrays of
+    `capacity` tokens, updated in place (created empty when None).  Returns
+    (out [T][nh*hd], cache)."""
+    q = _c(np.atleast_2d(q), np.float32)
+    T = q.shape[0]
+    if cache is None:
+        cap = capacity or (pos0 + T)
+        kd = np.int8 if int8 else np.float32
+        cache = (np.zeros((cap, nkv, hd), kd), np.zeros((cap, nkv, hd), kd), np.zeros((cap, nkv), np.float32),
+                 np.zeros((cap, nkv), np.float32))
+    kc, vc, ks, vs = cache
+    assert kc.shape[0] >= pos0 + T
+    out = np.empty((T, nh * hd), np.float32)
+    lib().orc_full_attn_seq(T, pos0, nh, nkv, hd, rotary_dim, theta, _c(q_norm_w, np.float32),
+                            _c(k_norm_w, np.float32), q, _c(gate, np.float32), _c(k, np.float32),
+                            _c(v, np.float32), 1 if int8 else 0, kc.ctypes.data, vc.ctypes.data, ks.ctypes.data,
+                            vs.ctypes.data, out)
+    return out, cache
+
+
+def ref_full_attn(x, Wq, Wk, Wv, qn, kn, Wo, nh, nkv, qhd, kvhd, theta=1.0e7, partial=0.25):
+    """The reference's own FullAttention::forward over the T rows of x, token t
+    at position t from an empty cache; y [T][H]."""
+    R = ref_lib()
+    x = _c(np.atleast_2d(x), np.float32)
+    T, H = x.shape
+    y = np.empty((T, H), np.float32)
+    rc = R.ref_full_attn(x, y, T, H, nh, nkv, qhd, kvhd, theta, partial, _c(Wq, np.float32), _c(Wk, np.float32),
+                         _c(Wv, np.float32), _c(qn, np.float32), _c(kn, np.float32), _c(Wo, np.float32))
+    if rc != 0:
+        raise RuntimeError("reference FullAttention raised")
+    return y

@@ -531,3 +531,129 @@ void orc_gdn_step(int B, int nh, int kd, int vd, int K, const float* mixed, cons
     free(kv);
     free(de);
 }
+
+/* ===== gated full attention (language_full_attn.cpp:117-216) ===== */
+
+/* FullAttention::rms_normalize (language_full_attn.cpp:77-86) */
+static void orc_attn_rmsnorm(float* x, int n, const float* w) {
+    float sum_sq = 0.0f;
+    for (int i = 0; i < n; ++i) sum_sq += x[i] * x[i];
+    const float rms = sqrtf(sum_sq / n + 1e-6f);
+    for (int i = 0; i < n; ++i) x[i] = x[i] / rms * (1.0f + w[i]);
+}
+
+/* per-head norms (language_full_attn.cpp:156-161) and FullAttention::apply_rope
+ * (language_full_attn.cpp:88-108) */
+void orc_attn_norm_rope(float* q, float* k, int nh, int nkv, int hd, int rotary_dim, float theta,
+                        const float* q_norm_w, const float* k_norm_w, int position) {
+    for (int h = 0; h < nh; ++h) orc_attn_rmsnorm(q + (size_t)h * hd, hd, q_norm_w);
+    for (int h = 0; h < nkv; ++h) orc_attn_rmsnorm(k + (size_t)h * hd, hd, k_norm_w);
+    for (int d = 0; d < rotary_dim; d += 2) {
+        const float freq = 1.0f / powf(theta, (float)d / rotary_dim);
+        const float angle = position * freq;
+        const float c = cosf(angle), s = sinf(angle);
+        for (int h = 0; h < nh; ++h) {
+            const float q0 = q[h * hd + d], q1 = q[h * hd + d + 1];
+            q[h * hd + d] = q0 * c - q1 * s;
+            q[h * hd + d + 1] = q0 * s + q1 * c;
+        }
+        for (int h = 0; h < nkv; ++h) {
+            const float k0 = k[h * hd + d], k1 = k[h * hd + d + 1];
+            k[h * hd + d] = k0 * c - k1 * s;
+            k[h * hd + d + 1] = k0 * s + k1 * c;
+        }
+    }
+}
+
+/* the INT8 KV-cache write of fused_kv_cache_int8_kernel
+ * (full_attention_cuda.cu:130-150): absmax / 127 per head, 1 when tiny,
+ * roundf (half away from zero), clamp to +-127 */
+void orc_kv_quant_int8(const float* x, int hd, int8_t* q, float* scale) {
+    float m = 0.0f;
+    for (int d = 0; d < hd; ++d) m = fmaxf(m, fabsf(x[d]));
+    float s = m / 127.0f;
+    s = s > 1e-8f ? s : 1.0f;
+    for (int d = 0; d < hd; ++d) q[d] = (int8_t)fmaxf(-127.0f, fminf(127.0f, roundf(x[d] / s)));
+    *scale = s;
+}
+
+/* the attention and gate of FullAttention::forward (language_full_attn.cpp:165-207) */
+void orc_attn_token(const float* q, const float* gate, const float* kc, const float* vc, int len, int nh,
+                    int nkv, int hd, float* out) {
+    const int group = nh / nkv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* w = (float*)malloc(sizeof(float) * (size_t)(len > 0 ? len : 1));
+    for (int h = 0; h < nh; ++h) {
+        const int g = h / group;
+        float* o = out + (size_t)h * hd;
+        for (int d = 0; d < hd; ++d) o[d] = 0.0f;
+        for (int t = 0; t < len; ++t) {
+            const float* kp = kc + ((size_t)t * nkv + g) * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; ++d) dot += q[(size_t)h * hd + d] * kp[d];
+            w[t] = dot * scale;
+        }
+        float mx = w[0];
+        for (int t = 1; t < len; ++t) mx = fmaxf(mx, w[t]);
+        float sum = 0.0f;
+        for (int t = 0; t < len; ++t) {
+            w[t] = expf(w[t] - mx);
+            sum += w[t];
+        }
+        for (int t = 0; t < len; ++t) w[t] /= sum;
+        for (int t = 0; t < len; ++t) {
+            const float* vp = vc + ((size_t)t * nkv + g) * hd;
+            for (int d = 0; d < hd; ++d) o[d] += w[t] * vp[d];
+        }
+        for (int d = 0; d < hd; ++d) o[d] *= 1.0f / (1.0f + expf(-gate[(size_t)h * hd + d]));
+    }
+    free(w);
+}
+
+/* FullAttention::forward over consecutive positions (forward_sequence,
+ * language_full_attn.cpp:219-250), between the projections; the INT8 cache
+ * variant stores what fused_kv_cache_int8_kernel stores and reads each token
+ * back with its own scale */
+void orc_full_attn_seq(int T, int pos0, int nh, int nkv, int hd, int rotary_dim, float theta,
+                       const float* q_norm_w, const float* k_norm_w, const float* q, const float* gate,
+                       const float* k, const float* v, int cache_int8, void* kc, void* vc, float* ks, float* vs,
+                       float* out) {
+    const size_t qn = (size_t)nh * hd, kn = (size_t)nkv * hd;
+    float* qb = (float*)malloc(sizeof(float) * qn);
+    float* kb = (float*)malloc(sizeof(float) * kn);
+    const int len_max = pos0 + T;
+    float* kf = cache_int8 ? (float*)malloc(sizeof(float) * (size_t)len_max * kn) : NULL;
+    float* vf = cache_int8 ? (float*)malloc(sizeof(float) * (size_t)len_max * kn) : NULL;
+    for (int t = 0; t < T; ++t) {
+        const int pos = pos0 + t;
+        memcpy(qb, q + (size_t)t * qn, sizeof(float) * qn);
+        memcpy(kb, k + (size_t)t * kn, sizeof(float) * kn);
+        orc_attn_norm_rope(qb, kb, nh, nkv, hd, rotary_dim, theta, q_norm_w, k_norm_w, pos);
+        const float* vt = v + (size_t)t * kn;
+        if (cache_int8) {
+            int8_t* kq = (int8_t*)kc;
+            int8_t* vq = (int8_t*)vc;
+            for (int h = 0; h < nkv; ++h) {
+                orc_kv_quant_int8(kb + (size_t)h * hd, hd, kq + ((size_t)pos * nkv + h) * hd, ks + (size_t)pos * nkv + h);
+                orc_kv_quant_int8(vt + (size_t)h * hd, hd, vq + ((size_t)pos * nkv + h) * hd, vs + (size_t)pos * nkv + h);
+            }
+            for (int p = 0; p <= pos; ++p)
+                for (int h = 0; h < nkv; ++h)
+                    for (int d = 0; d < hd; ++d) {
+                        const size_t i = ((size_t)p * nkv + h) * hd + d;
+                        kf[i] = (float)kq[i] * ks[(size_t)p * nkv + h];
+                        vf[i] = (float)vq[i] * vs[(size_t)p * nkv + h];
+                    }
+            orc_attn_token(qb, gate + (size_t)t * qn, kf, vf, pos + 1, nh, nkv, hd, out + (size_t)t * qn);
+        } else {
+            memcpy((float*)kc + (size_t)pos * kn, kb, sizeof(float) * kn);
+            memcpy((float*)vc + (size_t)pos * kn, vt, sizeof(float) * kn);
+            orc_attn_token(qb, gate + (size_t)t * qn, (const float*)kc, (const float*)vc, pos + 1, nh, nkv, hd,
+                           out + (size_t)t * qn);
+        }
+    }
+    free(qb);
+    free(kb);
+    free(kf);
+    free(vf);
+}

@@ -104,6 +104,30 @@ void orc_gdn_step(int B, int nh, int kd, int vd, int K, const float* mixed, cons
                   const float* z, const float* conv_w, const float* A_log, const float* dt_bias,
                   const float* norm_w, float* conv_state, float* rec_state, float* out);
 
+/* ---- gated full attention between the projections
+ * (language_full_attn.cpp:117-216; INT8 KV recipe full_attention_cuda.cu:75-155) ---- */
+/* Per-head RMSNorm (1 + w) of q [nh][hd] and k [nkv][hd] in place, then RoPE on
+ * the first rotary_dim dims (interleaved pairs) at `position`. */
+void orc_attn_norm_rope(float* q, float* k, int nh, int nkv, int hd, int rotary_dim, float theta,
+                        const float* q_norm_w, const float* k_norm_w, int position);
+/* Symmetric INT8 of one head vector: scale = max|x| / 127 (1 when <= 1e-8),
+ * q = clamp(round_half_away(x / scale), -127, 127). */
+void orc_kv_quant_int8(const float* x, int hd, int8_t* q, float* scale);
+/* One query token over a cache of `len` tokens (FP32, [len][nkv][hd]), GQA
+ * head h -> kv head h / (nh / nkv), scale 1/sqrt(hd), exact softmax, then
+ * out *= sigmoid(gate).  q, gate, out: [nh][hd]. */
+void orc_attn_token(const float* q, const float* gate, const float* kc, const float* vc, int len, int nh,
+                    int nkv, int hd, float* out);
+/* T tokens of one sequence at positions pos0 .. pos0+T-1: norm + RoPE, append
+ * to the cache (cache_int8: INT8 with per-(token, kv head) scales, else FP32),
+ * attention over positions 0 .. p (causal), gate.  q, gate: [T][nh][hd] raw
+ * projections (after the Q/gate split); k, v: [T][nkv][hd].  Caches are
+ * [capacity][nkv][hd] (kc/vc FP32 or int8_t), scales [capacity][nkv]. */
+void orc_full_attn_seq(int T, int pos0, int nh, int nkv, int hd, int rotary_dim, float theta,
+                       const float* q_norm_w, const float* k_norm_w, const float* q, const float* gate,
+                       const float* k, const float* v, int cache_int8, void* kc, void* vc, float* ks, float* vs,
+                       float* out);
+
 
 #ifdef __cplusplus
 }

@@ -9,10 +9,12 @@
 //   qwen::Sampler  src/backend/cpu/core/heads/sampler.hpp        (GREEDY)
 //   qwen::RMSNorm  src/backend/cpu/core/common/language_common.hpp:9-33
 //   qwen::LinearAttention  src/backend/cpu/core/attention/language_linear_attn.hpp:7-90
+//   qwen::FullAttention, qwen::KVCache  src/backend/cpu/core/attention/language_full_attn.hpp:8-124
 #include <chrono>
 #include <exception>
 #include <vector>
 
+#include "language_full_attn.hpp"
 #include "language_linear_attn.hpp"
 #include "language_mlp.hpp"
 #include "language_common.hpp"
@@ -141,6 +143,30 @@ int ref_linear_attn(const float* x, float* y, int T, int H, int nh, int kd, int 
             for (int j = 0; j < K - 1; ++j) conv_state[(size_t)d * (K - 1) + j] = st.conv_state[d][j];
         for (int h = 0; h < nh; ++h)
             for (int i = 0; i < kd * vd; ++i) rec_state[(size_t)h * kd * vd + i] = st.recurrent_state[h][i];
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+/* FullAttention::forward_sequence-style run from an empty cache: token t at
+ * position t (language_full_attn.cpp:117-216).  x [T][H] -> y [T][H]. */
+int ref_full_attn(const float* x, float* y, int T, int H, int nh, int nkv, int qhd, int kvhd, float theta,
+                  float partial, const float* Wq, const float* Wk, const float* Wv, const float* qn,
+                  const float* kn, const float* Wo) {
+    try {
+        qwen::FullAttention fa(H, nh, nkv, qhd, kvhd, theta, partial);
+        fa.set_weights(std::vector<float>(Wq, Wq + (size_t)nh * qhd * 2 * H),
+                       std::vector<float>(Wk, Wk + (size_t)nkv * kvhd * H),
+                       std::vector<float>(Wv, Wv + (size_t)nkv * kvhd * H), std::vector<float>(qn, qn + kvhd),
+                       std::vector<float>(kn, kn + kvhd), std::vector<float>(Wo, Wo + (size_t)H * nh * kvhd));
+        qwen::KVCache cache;
+        cache.reset(1, nkv, kvhd, T);
+        for (int t = 0; t < T; ++t) {
+            std::vector<float> in(x + (size_t)t * H, x + (size_t)(t + 1) * H);
+            std::vector<float> out = fa.forward(in, cache, 0, t);
+            for (int i = 0; i < H; ++i) y[(size_t)t * H + i] = out[i];
+        }
         return 0;
     } catch (const std::exception&) {
         return -1;

@@ -13,6 +13,8 @@ Vectors:
                   - LinearAttention::forward, 3 tokens of one sequence from
                     non-zero conv / recurrent states
                     (src/backend/cpu/core/attention/language_linear_attn.cpp:125-257)
+                  - FullAttention::forward, 6 tokens from an empty KV cache
+                    (src/backend/cpu/core/attention/language_full_attn.cpp:117-216)
   quant.npz     the INT8 per-row quantize recipe
                 (src/backend/cuda/kernels/mlp_cuda.cu:22-39) worked by hand
                 on rows that hit each of its cases; no code computes these
@@ -75,6 +77,17 @@ def ref_ops():
                                        nh, kd, vd)
     out.update({"gdn_" + k: v for k, v in g.items()})
     out.update(gdn_y=y, gdn_conv_state_out=cs, gdn_rec_state_out=rs)
+    # gated full attention (small dims, GQA 4:2, head dim 16, rotary 4 dims,
+    # theta 100 so the rotations are large): 6 tokens from an empty cache
+    H, nh, nkv, hd, T = 64, 4, 2, 16, 6
+    f = dict(Wq=oracle.normal((nh * hd * 2, H), 61, 0.0, 0.2), Wk=oracle.normal((nkv * hd, H), 62, 0.0, 0.2),
+             Wv=oracle.normal((nkv * hd, H), 63, 0.0, 0.2), qn=oracle.normal((hd,), 64, 0.0, 0.1),
+             kn=oracle.normal((hd,), 65, 0.0, 0.1), Wo=oracle.normal((H, nh * hd), 66, 0.0, 0.2),
+             x=oracle.normal((T, H), 67))
+    y = oracle.ref_full_attn(f["x"], f["Wq"], f["Wk"], f["Wv"], f["qn"], f["kn"], f["Wo"], nh, nkv, hd, hd,
+                             theta=100.0, partial=0.25)
+    out.update({"fa_" + k: v for k, v in f.items()})
+    out.update(fa_y=y)
     np.savez_compressed(os.path.join(HERE, "ref_ops.npz"), **out)
 
 

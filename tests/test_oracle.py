@@ -18,6 +18,13 @@ Pins, by function:
   Q/gate split        index identity on an arange input
   argmax / lm_head    the reference Sampler (golden ties), planted maxima,
                       numpy float64 argmax with a clear top-2 gap
+  Gated-DeltaNet      reference LinearAttention::forward (golden + oracle/_ref),
+                      numpy float64 matrix form, closed forms (beta -> 0, unit tap)
+  full attention      reference FullAttention::forward (golden + oracle/_ref),
+                      numpy float64 statement, closed forms (position 0, a
+                      single cached token, constant input, rotation norms)
+  INT8 KV recipe      vectors worked by hand (ties away from zero, +-127, tiny
+                      and zero heads)
 """
 import os
 
@@ -403,3 +410,135 @@ def test_gdn_closed_forms(oracle):
     # conv state: newest first, the oldest tap dropped
     assert np.array_equal(cs[0][:, 0], c["mixed"][0])
     assert np.array_equal(cs[0][:, 1:], c["conv_state"][0][:, :K - 2])
+
+
+# ---- gated full attention ------------------------------------------------------
+def _split_qg(qraw, nh, hd):
+    """The per-head Q/gate interleave of the reference (language_full_attn.cpp:133-140)."""
+    r = qraw.reshape(qraw.shape[0], nh, 2, hd)
+    return np.ascontiguousarray(r[:, :, 0].reshape(qraw.shape[0], -1)), \
+        np.ascontiguousarray(r[:, :, 1].reshape(qraw.shape[0], -1))
+
+
+def test_full_attn_matches_reference_golden(oracle):
+    """Projections (oracle linear) + norm/RoPE/cache/attention/gate + o_proj
+    reproduce the reference's own FullAttention::forward bit for bit over 6
+    tokens from an empty cache (tests/golden/ref_ops.npz; theta 100)."""
+    g = np.load(os.path.join(GOLDEN, "ref_ops.npz"))
+    nh, nkv, hd = 4, 2, 16
+    x = g["fa_x"]
+    q, gate = _split_qg(oracle.linear(g["fa_Wq"], x), nh, hd)
+    k, v = oracle.linear(g["fa_Wk"], x), oracle.linear(g["fa_Wv"], x)
+    out, _ = oracle.full_attn_seq(q, gate, k, v, g["fa_qn"], g["fa_kn"], nh, nkv, hd, rotary_dim=4, theta=100.0)
+    assert np.array_equal(oracle.linear(g["fa_Wo"], out), g["fa_y"])
+
+
+def test_full_attn_vs_ref_lib(oracle):
+    """Live reference build at the Qwen3.5-0.8B shape (8 heads, 2 KV heads,
+    head dim 256, rotary 64, theta 1e7), 3 tokens."""
+    if oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    H, nh, nkv, hd, T = 128, 8, 2, 256, 3
+    Wq = oracle.normal((nh * hd * 2, H), 130, 0.0, 0.05)
+    Wk, Wv = oracle.normal((nkv * hd, H), 131, 0.0, 0.05), oracle.normal((nkv * hd, H), 132, 0.0, 0.05)
+    qn, kn = oracle.normal((hd,), 133, 0.0, 0.1), oracle.normal((hd,), 134, 0.0, 0.1)
+    Wo = oracle.normal((H, nh * hd), 135, 0.0, 0.05)
+    x = oracle.normal((T, H), 136)
+    y_ref = oracle.ref_full_attn(x, Wq, Wk, Wv, qn, kn, Wo, nh, nkv, hd, hd)
+    q, gate = _split_qg(oracle.linear(Wq, x), nh, hd)
+    out, _ = oracle.full_attn_seq(q, gate, oracle.linear(Wk, x), oracle.linear(Wv, x), qn, kn, nh, nkv, hd)
+    assert np.array_equal(oracle.linear(Wo, out), y_ref)
+
+
+def full_attn_f64(q, gate, k, v, qn, kn, nh, nkv, hd, rotary_dim, theta):
+    """numpy float64 statement of the same T tokens from an empty cache."""
+    T = q.shape[0]
+    q = q.astype(np.float64).reshape(T, nh, hd)
+    k = k.astype(np.float64).reshape(T, nkv, hd)
+    v = v.astype(np.float64).reshape(T, nkv, hd)
+    q = q / np.sqrt((q * q).mean(-1, keepdims=True) + 1e-6) * (1.0 + qn)
+    k = k / np.sqrt((k * k).mean(-1, keepdims=True) + 1e-6) * (1.0 + kn)
+    d = np.arange(0, rotary_dim, 2)
+    ang = np.arange(T)[:, None] * (1.0 / theta ** (d / rotary_dim))[None, :]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    for x in (q, k):
+        x0, x1 = x[..., d].copy(), x[..., d + 1].copy()
+        x[..., d], x[..., d + 1] = x0 * c - x1 * s, x0 * s + x1 * c
+    out = np.zeros((T, nh, hd))
+    for t in range(T):
+        for h in range(nh):
+            g = h // (nh // nkv)
+            sc = k[:t + 1, g] @ q[t, h] / np.sqrt(hd)
+            w = np.exp(sc - sc.max())
+            w /= w.sum()
+            out[t, h] = (w @ v[:t + 1, g]) / (1.0 + np.exp(-gate.reshape(T, nh, hd)[t, h]))
+    return out.reshape(T, -1)
+
+
+def test_full_attn_vs_float64(oracle, relerr):
+    nh, nkv, hd, T = 8, 2, 256, 7
+    q, gate = oracle.normal((T, nh * hd), 140), oracle.normal((T, nh * hd), 141)
+    k, v = oracle.normal((T, nkv * hd), 142), oracle.normal((T, nkv * hd), 143)
+    qn, kn = oracle.normal((hd,), 144, 0.0, 0.1), oracle.normal((hd,), 145, 0.0, 0.1)
+    out, _ = oracle.full_attn_seq(q, gate, k, v, qn, kn, nh, nkv, hd, rotary_dim=64, theta=1000.0)
+    ref = full_attn_f64(q, gate, k, v, qn, kn, nh, nkv, hd, 64, 1000.0)
+    assert relerr(out, ref) <= 1e-5
+
+
+def test_full_attn_closed_forms(oracle):
+    """Position 0 leaves q, k unrotated; the first token attends only to itself,
+    so its output is v * sigmoid(gate) whatever q and k are; a constant input
+    normalizes to (1 + w)."""
+    nh, nkv, hd = 4, 2, 16
+    q, k = oracle.normal(nh * hd, 150), oracle.normal(nkv * hd, 151)
+    w0 = np.zeros(hd, np.float32)
+    q1, k1 = oracle.attn_norm_rope(q, k, w0, w0, 0, nh, nkv, hd, 8, 1.0e4)
+    qr = q.reshape(nh, hd).astype(np.float64)
+    np.testing.assert_allclose(q1.reshape(nh, hd), qr / np.sqrt((qr * qr).mean(-1, keepdims=True) + 1e-6),
+                               rtol=1e-6, atol=1e-6)
+    const = np.full(nh * hd, 3.0, np.float32)
+    w = oracle.normal(hd, 152, 0.0, 0.1)
+    qc, _ = oracle.attn_norm_rope(const, np.full(nkv * hd, 3.0, np.float32), w, w, 0, nh, nkv, hd, 8, 1.0e4)
+    np.testing.assert_allclose(qc.reshape(nh, hd), np.tile(3.0 / np.sqrt(9.0 + 1e-6) * (1.0 + w), (nh, 1)),
+                               rtol=1e-6)
+    gate, v = oracle.normal((1, nh * hd), 153), oracle.normal((1, nkv * hd), 154)
+    out, _ = oracle.full_attn_seq(q[None], gate, k[None], v, w0, w0, nh, nkv, hd, rotary_dim=8)
+    vv = v.reshape(nkv, hd)[np.arange(nh) // 2].reshape(-1)
+    np.testing.assert_allclose(out[0], vv / (1.0 + np.exp(-gate[0].astype(np.float64))), rtol=1e-6, atol=1e-7)
+    # RoPE is a rotation: each rotated pair keeps its norm (position 5, unit norm weights)
+    q5, _ = oracle.attn_norm_rope(q, k, w0, w0, 5, nh, nkv, hd, 8, 1.0)
+    n0 = q1.reshape(nh, hd // 2, 2)[:, :4]
+    n5 = q5.reshape(nh, hd // 2, 2)[:, :4]
+    np.testing.assert_allclose((n5 ** 2).sum(-1), (n0 ** 2).sum(-1), rtol=1e-5)
+    assert np.array_equal(q5.reshape(nh, hd)[:, 8:], q1.reshape(nh, hd)[:, 8:])
+
+
+def test_kv_quant_int8_hand_worked(oracle):
+    """The INT8 KV recipe on vectors worked by hand: scale = max|x|/127, ties
+    of x/scale round away from zero, the maximum maps to +-127, an all-zero
+    (or tiny) head gets scale 1."""
+    x = np.zeros(8, np.float32)
+    x[:5] = [127.0, -63.5, 2.5, -0.5, 1.49]   # scale exactly 1.0
+    q, s = oracle.kv_quant_int8(x)
+    assert s == 1.0 and list(q) == [127, -64, 3, -1, 1, 0, 0, 0]
+    q, s = oracle.kv_quant_int8(np.array([0.0, -254.0, 1.0, 3.0], np.float32))   # scale 2
+    assert s == 2.0 and list(q) == [0, -127, 1, 2]                                # 0.5 -> 1, 1.5 -> 2
+    q, s = oracle.kv_quant_int8(np.zeros(4, np.float32))
+    assert s == 1.0 and not q.any()
+    q, s = oracle.kv_quant_int8(np.array([1e-7, -1e-7], np.float32))             # max/127 < 1e-8
+    assert s == 1.0 and not q.any()
+
+
+def test_full_attn_int8_cache_reads_each_token_scale(oracle, relerr):
+    """The INT8 cache keeps per-(token, head) scales and the oracle reads each
+    token back with its own: with tokens of very different magnitudes the
+    result stays within INT8 rounding of the FP32-cache result."""
+    nh, nkv, hd, T = 8, 2, 256, 5
+    q, gate = oracle.normal((T, nh * hd), 160), oracle.normal((T, nh * hd), 161)
+    k = oracle.normal((T, nkv * hd), 162)
+    v = oracle.normal((T, nkv * hd), 163) * np.array([1, 100, 0.01, 10, 1], np.float32)[:, None]
+    qn = kn = np.zeros(hd, np.float32)
+    o32, _ = oracle.full_attn_seq(q, gate, k, v, qn, kn, nh, nkv, hd)
+    o8, (kc, vc, ks, vs) = oracle.full_attn_seq(q, gate, k, v, qn, kn, nh, nkv, hd, int8=True)
+    assert relerr(o8, o32) <= 2e-2
+    assert ks.shape == (T, nkv) and len(set(np.round(vs[:, 0], 6))) == T
