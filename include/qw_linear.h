@@ -190,6 +190,62 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
  * completed); its outputs are then invalid.  Synchronizes the device. */
 qw_status qw_device_error(qw_ctx* ctx, int* flag);
 
+/* ---- gated full attention (between the projections) -------------------------
+ * One call runs, for `tokens` new tokens of each of `batch` sequences (row
+ * b*tokens + t is token t of sequence b, at cache position positions[b] + t):
+ *   q_h = RMSNorm(q_h) * (1 + q_norm_weight), k_g likewise (eps 1e-6, per head);
+ *   RoPE on the first rotary_dim dims (interleaved pairs (d, d+1), angle
+ *   position / rope_theta^(d / rotary_dim)) of q and k;
+ *   the K/V cache write at that position;
+ *   o_h = softmax(q_h . K_g^T / sqrt(head_dim)) V_g over positions
+ *   0 .. position (causal), g = h / (num_heads / num_kv_heads);
+ *   out = o * sigmoid(gate).
+ * Replaces the attention core of FullAttention::forward
+ * (language_full_attn.cpp:117-216) and of CudaFullAttention::forward /
+ * forward_batch_prefill (fused_q_path_kernel, fused_kv_cache_int8_kernel,
+ * flash attention, gate_sigmoid_kernel: full_attention_cuda.cu:31-166,
+ * 353-449, 640-714).  Differences from that CUDA chain, both deliberate: the
+ * INT8 cache is read back with each token's own scale (its dequant kernels
+ * index the scale by head only, fused_kernels.cu:400-412), and a batch of
+ * tokens attends causally (its prefill attends to every cached position up to
+ * the batch's maximum, fused_kernels.cu:175-200); both follow the CPU operator.
+ * Inputs (in_dtype F32, BF16 or F16, row stride ld_in elements): q and gate,
+ * element (row r, head h, dim d) at r*ld_in + h*q_head_stride + d (512 for the
+ * interleaved Q|gate projection output with gate = q + 256, 256 for split
+ * buffers); k and v at r*ld_in + g*head_dim + d.  positions: device int
+ * [batch].  max_len: an upper bound of positions[b] + tokens used to size the
+ * launch (0: the cache capacity).  A token whose position falls outside the
+ * cache writes nothing, outputs zeros and sets the device error flag
+ * (qw_device_error).  head_dim 128 or 256, num_heads / num_kv_heads <= 4. */
+typedef struct {
+    int num_heads;              /* query heads (8) */
+    int num_kv_heads;           /* key/value heads (2) */
+    int head_dim;               /* q and kv head dim (256) */
+    int rotary_dim;             /* leading dims rotated (64 = head_dim * 0.25) */
+    float rope_theta;           /* 1e7 */
+    const float* q_norm_weight; /* [head_dim], device */
+    const float* k_norm_weight; /* [head_dim], device */
+} qw_attn_params;
+
+/* KV cache of one layer, the CudaKVCache layout (full_attention_cuda.hpp:
+ * 11-33) with a sequence dimension: k, v [sequences][capacity][num_kv_heads]
+ * [head_dim] of dtype QW_I8 (symmetric, one FP32 scale per token and KV head
+ * in k_scale / v_scale [sequences][capacity][num_kv_heads]) or QW_F32 (the CPU
+ * KVCache, language_full_attn.hpp:8-54; scales unused). */
+typedef struct {
+    qw_dtype dtype;
+    void* k;
+    void* v;
+    float* k_scale;
+    float* v_scale;
+    int capacity;  /* tokens per sequence */
+} qw_kv_cache;
+
+qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cache* cache, int batch, int tokens,
+                          const int* positions, int max_len, const void* q, const void* gate, int q_head_stride,
+                          const void* k, const void* v, qw_dtype in_dtype, int ld_in, void* out,
+                          qw_dtype out_dtype, int ld_out, hipStream_t stream);
+
 /* ---- lm_head + greedy argmax -------------------------------------------------
  * token_ids[m] = argmax_v sum_k E[v][k]*h[m][k]; ties go to the LOWEST index
  * (std::max_element, sampler.cpp:41-43).  max_logit (optional) receives the

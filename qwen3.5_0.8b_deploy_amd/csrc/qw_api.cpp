@@ -887,6 +887,77 @@ qw_status qw_gdn_prefill(qw_ctx* ctx, const qw_gdn_params* p, int batch, int tok
                    out_dtype, ld_out, stream);
 }
 
+qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cache* cache, int batch, int tokens,
+                          const int* positions, int max_len, const void* q, const void* gate, int q_head_stride,
+                          const void* k, const void* v, qw_dtype in_dtype, int ld_in, void* out,
+                          qw_dtype out_dtype, int ld_out, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!p || !cache || !positions || !q || !gate || !k || !v || !out || !p->q_norm_weight || !p->k_norm_weight ||
+        !cache->k || !cache->v || (cache->dtype == QW_I8 && (!cache->k_scale || !cache->v_scale)))
+        return fail(ctx, QW_ERR_NULL, "attn: NULL argument");
+    if (batch < 1 || tokens < 1) return fail(ctx, QW_ERR_SHAPE, "attn: batch=%d, tokens=%d must be >= 1", batch, tokens);
+    const int nh = p->num_heads, nkv = p->num_kv_heads, hd = p->head_dim;
+    if (nkv < 1 || nh < nkv || nh % nkv || nh / nkv > 4 || (hd != 128 && hd != 256) || p->rotary_dim < 0 ||
+        p->rotary_dim % 2 || p->rotary_dim > hd || !(p->rope_theta > 0.0f))
+        return fail(ctx, QW_ERR_SHAPE, "attn: unsupported shape (heads %d/%d, head_dim %d, rotary %d)", nh, nkv, hd,
+                    p->rotary_dim);
+    if (cache->dtype != QW_I8 && cache->dtype != QW_F32) return fail(ctx, QW_ERR_DTYPE, "attn: cache dtype must be I8 or F32");
+    if (cache->capacity < 1) return fail(ctx, QW_ERR_SHAPE, "attn: cache capacity %d", cache->capacity);
+    if (!valid_act(in_dtype) || !valid_act(out_dtype)) return fail(ctx, QW_ERR_DTYPE, "attn: dtype unsupported");
+    if (q_head_stride < hd || ld_in < 1 || ld_out < nh * hd)
+        return fail(ctx, QW_ERR_SHAPE, "attn: q_head_stride=%d, ld_in=%d, ld_out=%d", q_head_stride, ld_in, ld_out);
+    const int64_t rows_all = (int64_t)batch * tokens;
+    int len = max_len > 0 ? std::min(max_len, cache->capacity) : cache->capacity;
+    // keys per split: enough workgroups to fill the chip, at most 1024 keys each
+    const int64_t want = (int64_t)len * rows_all * nkv / (4LL * ctx->num_cus);
+    int split = (int)std::min<int64_t>(1024, std::max<int64_t>(32, want)) / 32 * 32;
+    const int nsplit = (len + split - 1) / split;
+    const size_t per_row = qwk::attn_bytes_per_row(nh, hd, nsplit);
+    const size_t ws = ctx->xnorm_bytes + ctx->scratch_bytes;
+    const int64_t seg = std::min<int64_t>({rows_all, (int64_t)(ws / per_row), (int64_t)65535});
+    if (seg < 1) return fail(ctx, QW_ERR_WORKSPACE, "attn: workspace too small for one row");
+    qwk::AttnArgs a{};
+    a.B = batch;
+    a.T = tokens;
+    a.nh = nh;
+    a.nkv = nkv;
+    a.hd = hd;
+    a.rot = p->rotary_dim;
+    a.theta = p->rope_theta;
+    a.qn_w = p->q_norm_weight;
+    a.kn_w = p->k_norm_weight;
+    a.q = q;
+    a.gate = gate;
+    a.k = k;
+    a.v = v;
+    a.q_hs = q_head_stride;
+    a.in_dt = (int)in_dtype;
+    a.ld_in = ld_in;
+    a.kv_dt = (int)cache->dtype;  // qw_dtype codes are the kernels' DType codes
+    a.kc = cache->k;
+    a.vc = cache->v;
+    a.ks = cache->k_scale;
+    a.vs = cache->v_scale;
+    a.cap = cache->capacity;
+    a.pos = positions;
+    a.out = out;
+    a.out_dt = (int)out_dtype;
+    a.ld_out = ld_out;
+    a.err = ctx->mlp_ctl + 3;
+    a.split = split;
+    a.nsplit = nsplit;
+    // rows in order, so every row finds the keys of the rows before it in the cache
+    for (int64_t r0 = 0; r0 < rows_all; r0 += seg) {
+        a.row0 = (int)r0;
+        a.rows = (int)std::min<int64_t>(seg, rows_all - r0);
+        a.qn = reinterpret_cast<float*>(ctx->xnorm);
+        a.part = a.qn + (size_t)a.rows * nh * hd;
+        hipError_t e = qwk::launch_attn(a, stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "attn launch");
+    }
+    return QW_OK;
+}
+
 qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,
                        qw_dtype xdt, const float* gamma, float eps, const void* residual,
                        qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream) {

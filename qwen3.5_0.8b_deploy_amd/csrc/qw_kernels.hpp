@@ -125,6 +125,37 @@ size_t gdn_chunked_bytes_per_token(int nh);
 // hipErrorInvalidValue when the workspace does not hold one 64-token chunk per sequence
 hipError_t launch_gdn_chunked(const GdnArgs& a, void* ws, size_t ws_bytes, hipStream_t stream);
 
+// Gated full attention between the projections (qw_attn.hip): B sequences of
+// T new tokens each; row r = b*T + t is at cache position pos[b] + t.
+struct AttnArgs {
+    int B, T, nh, nkv, hd, rot;
+    float theta;
+    const float* qn_w;     // [hd] RMSNorm (1 + w) of q
+    const float* kn_w;     // [hd] of k
+    const void* q;         // row r, head h, dim d at r*ld_in + h*q_hs + d
+    const void* gate;      // same indexing as q
+    const void* k;         // r*ld_in + g*hd + d
+    const void* v;
+    int q_hs, in_dt, ld_in;
+    int kv_dt;             // DT_F32 or DT_I8 (per-(token, head) scales)
+    void* kc;              // [B][cap][nkv][hd]
+    void* vc;
+    float* ks;             // [B][cap][nkv] (INT8)
+    float* vs;
+    int cap;
+    const int* pos;        // device [B]
+    void* out;             // r*ld_out + h*hd + d
+    int out_dt, ld_out;
+    unsigned* err;         // device error flag (position out of the cache)
+    int row0, rows;        // the segment of rows of this launch
+    float* qn;             // workspace [rows][nh][hd]: normalized, rotated q
+    float* part;           // workspace [rows][nh][nsplit][hd + 2]: split partials
+    int split, nsplit;     // keys per split, splits per row (upper bound)
+};
+// workspace bytes per row for a given split count
+size_t attn_bytes_per_row(int nh, int hd, int nsplit);
+hipError_t launch_attn(const AttnArgs& a, hipStream_t stream);
+
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
 // Output rows are written to physical tile `tile_of_row(o)` (GLU interleave
 // handled by the caller through tile_mul/tile_add: pt = t*tile_mul+tile_add).

@@ -31,8 +31,31 @@ EXPORTS = [
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
-    "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
+    "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
+
+
+class AttnParams(ctypes.Structure):
+    _fields_ = [
+        ("num_heads", ctypes.c_int),
+        ("num_kv_heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("rotary_dim", ctypes.c_int),
+        ("rope_theta", ctypes.c_float),
+        ("q_norm_weight", ctypes.c_void_p),
+        ("k_norm_weight", ctypes.c_void_p),
+    ]
+
+
+class KVCache(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("k_scale", ctypes.c_void_p),
+        ("v_scale", ctypes.c_void_p),
+        ("capacity", ctypes.c_int),
+    ]
 
 
 class GdnParams(ctypes.Structure):
@@ -103,6 +126,8 @@ def lib():
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
         "qw_gdn_decode": ([_vp, ctypes.POINTER(GdnParams), _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i,
                            _vp], _i),
+        "qw_attn_forward": ([_vp, ctypes.POINTER(AttnParams), ctypes.POINTER(KVCache), _i, _i, _vp, _i, _vp, _vp,
+                             _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp], _i),
         "qw_gdn_prefill": ([_vp, ctypes.POINTER(GdnParams), _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i,
                             _i, _vp], _i),
         "qw_device_error": ([_vp, _vp], _i),
@@ -449,3 +474,38 @@ def gdn_prefill(ctx, conv_weight, A_log, dt_bias, norm_weight, mixed, z, a, b, c
     ctx.check(lib().qw_gdn_prefill(ctx.handle, ctypes.byref(p), rows // tokens, tokens, _ptr(mixed), _ptr(z),
                                    _ptr(a), _ptr(b), _torch_code(mixed), ld_in, _ptr(conv_state),
                                    _ptr(recurrent_state), _ptr(out), _torch_code(out), ld_out, _stream(stream)))
+
+
+def kv_cache(sequences, capacity, num_kv_heads=2, head_dim=256, int8=True, device="cuda"):
+    """Zeroed device KV cache of one layer: (k, v, k_scale, v_scale) tensors in
+    the qw_kv_cache layout [sequences][capacity][num_kv_heads][head_dim]."""
+    import torch
+    dt = torch.int8 if int8 else torch.float32
+    shape = (sequences, capacity, num_kv_heads, head_dim)
+    return (torch.zeros(shape, dtype=dt, device=device), torch.zeros(shape, dtype=dt, device=device),
+            torch.zeros(shape[:3], dtype=torch.float32, device=device),
+            torch.zeros(shape[:3], dtype=torch.float32, device=device))
+
+
+def attn_forward(ctx, q_norm_weight, k_norm_weight, cache, positions, q, gate, k, v, out, num_heads=8,
+                 num_kv_heads=2, head_dim=256, rotary_dim=64, rope_theta=1.0e7, tokens=1, q_head_stride=0,
+                 ld_in=0, ld_out=0, max_len=0, stream=None):
+    """Gated full attention between the projections for rows = batch*tokens
+    (row b*tokens + t is token t of sequence b at position positions[b] + t);
+    q/gate/k/v are views into the projection output(s) sharing one row stride;
+    `cache` is kv_cache(...)'s tuple, updated in place."""
+    kc, vc, ks, vs = cache
+    p = AttnParams(num_heads, num_kv_heads, head_dim, rotary_dim, rope_theta, q_norm_weight.data_ptr(),
+                   k_norm_weight.data_ptr())
+    int8 = kc.element_size() == 1
+    c = KVCache(I8 if int8 else F32, kc.data_ptr(), vc.data_ptr(), ks.data_ptr() if int8 else None,
+                vs.data_ptr() if int8 else None, kc.shape[1])
+    rows = q.shape[0]
+    if tokens < 1 or rows % tokens:
+        raise QwError(ERR_SHAPE, f"{rows} rows are not a whole number of {tokens}-token sequences")
+    ld_in = ld_in or q.stride(0)
+    ld_out = ld_out or out.stride(0)
+    q_head_stride = q_head_stride or head_dim
+    ctx.check(lib().qw_attn_forward(ctx.handle, ctypes.byref(p), ctypes.byref(c), rows // tokens, tokens,
+                                    _ptr(positions), max_len, _ptr(q), _ptr(gate), q_head_stride, _ptr(k), _ptr(v),
+                                    _torch_code(q), ld_in, _ptr(out), _torch_code(out), ld_out, _stream(stream)))
