@@ -386,6 +386,7 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
     extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
 
     extra.update(run_gdn(qw, ctx, torch, timer, stream, randn, args))
+    extra.update(run_attn(qw, ctx, torch, timer, stream, randn, args))
 
     # config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each
     for fmt, name in ((qw.WFMT_BF16, "bf16"), (qw.WFMT_INT8, "int8")):
@@ -410,6 +411,51 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         del Es
     torch.cuda.synchronize()
     return extra
+
+
+def run_attn(qw, ctx, torch, timer, stream, randn, args):
+    """Gated full attention between the projections (6 of the 24 layers): the
+    norm/RoPE/cache-write prep, causal attention over the INT8 KV cache and
+    the gate, for (a) decode steps of B sequences at a context of L tokens and
+    (b) a T-token prefill of one sequence.  Decode bytes: the K and V codes
+    and scales of the context (2 x L x 2 heads x (256 + 4) per sequence)."""
+    NH, NKV, HD = 8, 2, 256
+    LD = NH * 2 * HD + 2 * NKV * HD
+    qn = 0.1 * randn(HD, dtype=torch.float32)
+    kn = 0.1 * randn(HD, dtype=torch.float32)
+    out = {}
+
+    def call(cache, rows, pos, tokens, o, max_len):
+        qw.attn_forward(ctx, qn, kn, cache, pos, rows[:, 0:], rows[:, HD:], rows[:, NH * 2 * HD:],
+                        rows[:, NH * 2 * HD + NKV * HD:], o, tokens=tokens, q_head_stride=2 * HD, max_len=max_len)
+
+    for B, L in ((1, 512), (1, 4096), (1, 32768), (32, 4096)):
+        cache = qw.kv_cache(B, L + 1)
+        cache[0].random_(-127, 128)
+        cache[1].random_(-127, 128)
+        cache[2].uniform_(0.001, 0.01)
+        cache[3].uniform_(0.001, 0.01)
+        rows = randn(B, LD, dtype=torch.float32)
+        pos = torch.full((B,), L, dtype=torch.int32, device="cuda")
+        o = torch.empty(B, NH * HD, device="cuda", dtype=torch.bfloat16)
+        g = graphed(qw, ctx, stream, lambda: call(cache, rows, pos, 1, o, L + 1))
+        us = 1e3 * timer.run(g.launch, max(5, args.steps // 2), 2)
+        by = B * 2 * (L + 1) * NKV * (HD + 4)
+        out[f"attn_decode_B{B}_L{L}"] = {"us_per_layer": round(us, 2), "GBps": round(by / us / 1e3, 1),
+                                         "pct_hbm": round(100 * by / us / 1e3 / HBM_PEAK, 1)}
+        log("attn decode", B, L, out[f"attn_decode_B{B}_L{L}"])
+        del cache, g
+    for T in (1024, 4096):
+        cache = qw.kv_cache(1, T)
+        rows = randn(T, LD, dtype=torch.float32)
+        pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+        o = torch.empty(T, NH * HD, device="cuda", dtype=torch.bfloat16)
+        ms = timer.run(lambda: call(cache, rows, pos, T, o, T), 3, 1)
+        flops = 2 * 2 * NH * HD * T * (T + 1) / 2  # QK^T and PV over the causal triangle
+        out[f"attn_prefill_T{T}"] = {"us_per_layer": round(1e3 * ms, 1), "TFLOPs": round(flops / ms / 1e9, 1)}
+        log("attn prefill", T, out[f"attn_prefill_T{T}"])
+        del cache
+    return out
 
 
 def run_gdn(qw, ctx, torch, timer, stream, randn, args):

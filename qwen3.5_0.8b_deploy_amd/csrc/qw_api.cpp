@@ -33,7 +33,8 @@ struct qw_ctx {
     int gemm_tile_m = 0;         // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256; 0 = by shape)
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
-    int gdn_chunk_min = kGdnChunkMin;  // tokens per sequence from which the chunked GDN form runs (QW_GDN_CHUNK_MIN)
+    int gdn_chunk_min = kGdnChunkMin;
+    int attn_prefill_min = 16;   // tokens per sequence from which the query-block attention kernel runs (QW_ATTN_PREFILL_MIN)  // tokens per sequence from which the chunked GDN form runs (QW_GDN_CHUNK_MIN)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
     // carved regions
@@ -171,6 +172,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
+    if (const char* v = getenv("QW_ATTN_PREFILL_MIN")) c->attn_prefill_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GDN_CHUNK_MIN")) c->gdn_chunk_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
@@ -908,14 +910,6 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
         return fail(ctx, QW_ERR_SHAPE, "attn: q_head_stride=%d, ld_in=%d, ld_out=%d", q_head_stride, ld_in, ld_out);
     const int64_t rows_all = (int64_t)batch * tokens;
     int len = max_len > 0 ? std::min(max_len, cache->capacity) : cache->capacity;
-    // keys per split: enough workgroups to fill the chip, at most 1024 keys each
-    const int64_t want = (int64_t)len * rows_all * nkv / (4LL * ctx->num_cus);
-    int split = (int)std::min<int64_t>(1024, std::max<int64_t>(32, want)) / 32 * 32;
-    const int nsplit = (len + split - 1) / split;
-    const size_t per_row = qwk::attn_bytes_per_row(nh, hd, nsplit);
-    const size_t ws = ctx->xnorm_bytes + ctx->scratch_bytes;
-    const int64_t seg = std::min<int64_t>({rows_all, (int64_t)(ws / per_row), (int64_t)65535});
-    if (seg < 1) return fail(ctx, QW_ERR_WORKSPACE, "attn: workspace too small for one row");
     qwk::AttnArgs a{};
     a.B = batch;
     a.T = tokens;
@@ -944,13 +938,69 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
     a.out_dt = (int)out_dtype;
     a.ld_out = ld_out;
     a.err = ctx->mlp_ctl + 3;
+    const size_t ws = ctx->xnorm_bytes + ctx->scratch_bytes;
+    a.qn = reinterpret_cast<float*>(ctx->xnorm);
+    if (tokens >= ctx->attn_prefill_min) {
+        // query blocks of 16 tokens; segments of whole sequences, or of 16-token
+        // chunks of one sequence, whose normalized q fit the workspace
+        a.prefill = 1;
+        if (cache->dtype == QW_I8) {
+            // key splits of >= 256 keys, at most 8 per query block (the longest
+            // block's chain is then <= 1/8 of the context)
+            const int s8 = (len + 7) / 8;
+            a.split = std::max(256, (s8 + 31) / 32 * 32);
+            a.nsplit = (len + a.split - 1) / a.split;
+        } else {
+            a.split = len;
+            a.nsplit = 1;
+        }
+        const size_t per_row = (size_t)nh * hd * 4 + (a.nsplit > 1 ? (size_t)nh * a.nsplit * (hd + 2) * 4 : 0);
+        const int64_t seq_fit = (int64_t)(ws / (per_row * (size_t)tokens));
+        if (seq_fit >= 1) {
+            const int64_t nbseg = std::min<int64_t>({(int64_t)batch, seq_fit, (int64_t)65535});
+            for (int b0 = 0; b0 < batch; b0 += (int)nbseg) {
+                a.b0 = b0;
+                a.nb = (int)std::min<int64_t>(nbseg, batch - b0);
+                a.tb = 0;
+                a.ntok = tokens;
+                a.row0 = b0 * tokens;
+                a.rows = a.nb * tokens;
+                a.part = a.qn + (size_t)a.rows * nh * hd;
+                hipError_t e = qwk::launch_attn(a, stream);
+                if (e != hipSuccess) return hip_fail(ctx, e, "attn launch");
+            }
+        } else {
+            const int chunk = (int)(ws / per_row) / 16 * 16;
+            if (chunk < 16) return fail(ctx, QW_ERR_WORKSPACE, "attn: workspace too small for 16 tokens");
+            for (int b0 = 0; b0 < batch; ++b0)
+                for (int tb = 0; tb < tokens; tb += chunk) {
+                    a.b0 = b0;
+                    a.nb = 1;
+                    a.tb = tb;
+                    a.ntok = std::min(chunk, tokens - tb);
+                    a.row0 = b0 * tokens + tb;
+                    a.rows = a.ntok;
+                    a.part = a.qn + (size_t)a.rows * nh * hd;
+                    hipError_t e = qwk::launch_attn(a, stream);
+                    if (e != hipSuccess) return hip_fail(ctx, e, "attn launch");
+                }
+        }
+        return QW_OK;
+    }
+    // few tokens per sequence: key-split rows; keys per split about two
+    // workgroups per CU, 128 .. 1024 keys each
+    const int64_t want = (int64_t)len * rows_all * nkv / (2LL * ctx->num_cus);
+    const int split = (int)std::min<int64_t>(1024, std::max<int64_t>(128, want)) / 32 * 32;
+    const int nsplit = (len + split - 1) / split;
+    const size_t per_row = qwk::attn_bytes_per_row(nh, hd, nsplit);
+    const int64_t seg = std::min<int64_t>({rows_all, (int64_t)(ws / per_row), (int64_t)65535});
+    if (seg < 1) return fail(ctx, QW_ERR_WORKSPACE, "attn: workspace too small for one row");
     a.split = split;
     a.nsplit = nsplit;
     // rows in order, so every row finds the keys of the rows before it in the cache
     for (int64_t r0 = 0; r0 < rows_all; r0 += seg) {
         a.row0 = (int)r0;
         a.rows = (int)std::min<int64_t>(seg, rows_all - r0);
-        a.qn = reinterpret_cast<float*>(ctx->xnorm);
         a.part = a.qn + (size_t)a.rows * nh * hd;
         hipError_t e = qwk::launch_attn(a, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "attn launch");

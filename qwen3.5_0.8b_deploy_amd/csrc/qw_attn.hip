@@ -30,6 +30,12 @@ namespace qwk {
 
 constexpr int AT_KT = 32;  // keys per LDS tile
 
+// FP32 MFMA 16x16x4: lane l supplies A[l%16][l/16] and B[l/16][l%16] and holds
+// D[4*(l/16) + r][l%16] in element r.
+__device__ __forceinline__ f32x4 at_mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float at_load(const void* p, int dt, int64_t i) {
     return dt == DT_F32 ? reinterpret_cast<const float*>(p)[i] : load_act(p, dt, i);
 }
@@ -47,10 +53,10 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// prep: one workgroup (4 waves) per row; work items = nh q heads, nkv k
-// heads, nkv v heads, one wave each; lane l holds dims [l*E, l*E + E).
+// prep: one workgroup per row with one wave per work item (nh q heads, nkv k
+// heads, nkv v heads; 64 x items threads); lane l holds dims [l*E, l*E + E).
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prep(AttnArgs a) {
+__global__ __launch_bounds__(1024) void attn_prep(AttnArgs a) {
     constexpr int E = HD / 64;
     const int rl = blockIdx.x, r = a.row0 + rl;
     const int b = r / a.T, t = r % a.T;
@@ -59,9 +65,18 @@ __global__ __launch_bounds__(256) void attn_prep(AttnArgs a) {
     const bool ok = P >= 0 && P < a.cap && P < a.nsplit * a.split;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (!ok && threadIdx.x == 0) *a.err = 1u;
+    // the rotation of this position, shared by every q and k head
+    __shared__ float rc[HD / 2], rs[HD / 2];
+    if ((int)threadIdx.x < a.rot / 2) {
+        const float freq = 1.0f / powf(a.theta, (float)(2 * threadIdx.x) / (float)a.rot);
+        const float ang = (float)P * freq;
+        rc[threadIdx.x] = cosf(ang);
+        rs[threadIdx.x] = sinf(ang);
+    }
+    __syncthreads();
     const int items = a.nh + 2 * a.nkv;
     const int64_t row = (int64_t)r * a.ld_in;
-    for (int it = wave; it < items; it += 4) {
+    for (int it = wave; it < items; it += blockDim.x >> 6) {
         const bool isq = it < a.nh, isk = !isq && it < a.nh + a.nkv;
         const int h = isq ? it : (isk ? it - a.nh : it - a.nh - a.nkv);
         const void* src = isq ? a.q : (isk ? a.k : a.v);
@@ -82,9 +97,7 @@ __global__ __launch_bounds__(256) void attn_prep(AttnArgs a) {
             for (int e = 0; e < E; e += 2) {
                 const int d = lane * E + e;
                 if (d < a.rot) {
-                    const float freq = 1.0f / powf(a.theta, (float)d / (float)a.rot);
-                    const float ang = (float)P * freq;
-                    const float c = cosf(ang), s = sinf(ang);
+                    const float c = rc[d / 2], s = rs[d / 2];
                     const float x0 = x[e], x1 = x[e + 1];
                     x[e] = x0 * c - x1 * s;
                     x[e + 1] = x0 * s + x1 * c;
@@ -120,22 +133,68 @@ __global__ __launch_bounds__(256) void attn_prep(AttnArgs a) {
 
 // ---------------------------------------------------------------------------
 // split: (key split s, KV head g, row rl); wave w < G handles query head g*G + w.
-template <int HD>
+// The K and V tiles of 32 keys are staged in LDS once for the whole KV group:
+// INT8 codes as they are (the scales multiply the score and the probability),
+// FP32 values as they are; every thread issues its share of the next tile's
+// loads before the current tile is computed.
+template <int HD, bool I8>
+struct AtTile {
+    static constexpr int KROW = I8 ? HD + 4 : (HD + 4) * 4;   // K row stride, bytes (bank spread)
+    static constexpr int VROW = I8 ? HD : HD * 4;             // V row stride, bytes
+    static constexpr int CH = AT_KT * (I8 ? HD : HD * 4) / 16; // 16-byte chunks per K (or V) tile
+    static constexpr int PER = 2 * CH / 256;                   // chunks per thread (K and V)
+};
+
+template <int HD, bool I8>
 __global__ __launch_bounds__(256) void attn_split(AttnArgs a) {
-    constexpr int E = HD / 64, KP = HD + 4;
+    using Tl = AtTile<HD, I8>;
+    constexpr int E = HD / 64, ESZ = I8 ? 1 : 4, CPR = HD * ESZ / 16;  // chunks per row
     const int s = blockIdx.x, g = blockIdx.y, rl = blockIdx.z, r = a.row0 + rl;
     const int b = r / a.T, t = r % a.T;
     const int P = a.pos[b] + t;
     const int L = (P >= 0 && P < a.cap && P < a.nsplit * a.split) ? P + 1 : 0;  // causal: keys 0 .. P
     const int k0 = s * a.split, k1 = min(k0 + a.split, L);
-    if (k0 >= k1) return;  // uniform over the workgroup
     const int G = a.nh / a.nkv;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int h = g * G + wave;
+    if (k0 >= k1) {  // uniform over the workgroup
+        if (L == 0 && a.nsplit == 1 && wave < G) {  // a flagged token without a combine step: zeros
+            const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = 0.0f;
+                else store_act(a.out, a.out_dt, oi + e, 0.0f);
+            }
+        }
+        return;
+    }
 
     __shared__ __attribute__((aligned(16))) float qs[4][HD];
-    __shared__ __attribute__((aligned(16))) float Ks[AT_KT][KP], Vs[AT_KT][KP];
+    __shared__ __attribute__((aligned(16))) uint8_t Kt[AT_KT * Tl::KROW];
+    __shared__ __attribute__((aligned(16))) uint8_t Vt[AT_KT * Tl::VROW];
+    __shared__ float ksc[AT_KT], vsc[AT_KT];
 
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.kc);
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.vc);
+    const int64_t slot0 = (int64_t)b * a.cap * a.nkv + g;  // slot of key j: slot0 + j * nkv
+    u32x4 pre[Tl::PER];
+    float psc = 0.0f;
+    auto issue = [&](int kt) {  // the loads of the tile starting at key kt
+        const int n = min(AT_KT, k1 - kt);
+#pragma unroll
+        for (int i = 0; i < Tl::PER; ++i) {
+            const int c = threadIdx.x + 256 * i, isv = c >= Tl::CH, cc = c - isv * Tl::CH;
+            const int j = cc / CPR, part = cc % CPR;
+            const int64_t slot = slot0 + (int64_t)(kt + j) * a.nkv;
+            if (j < n) pre[i] = *reinterpret_cast<const u32x4*>((isv ? vbase : kbase) + slot * (HD * ESZ) + part * 16);
+            else pre[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+        if (I8 && threadIdx.x < 2 * AT_KT) {
+            const int j = threadIdx.x & (AT_KT - 1);
+            psc = j < n ? (threadIdx.x < AT_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + j) * a.nkv] : 0.0f;
+        }
+    };
+    issue(k0);
     for (int e = threadIdx.x; e < G * HD; e += 256) qs[e / HD][e % HD] = a.qn[((int64_t)rl * a.nh + g * G) * HD + e];
     const float scale = 1.0f / sqrtf((float)HD);
     float m = -INFINITY, l = 0.0f, o[E];
@@ -146,35 +205,42 @@ __global__ __launch_bounds__(256) void attn_split(AttnArgs a) {
     for (int kt = k0; kt < k1; kt += AT_KT) {
         const int n = min(AT_KT, k1 - kt);
         __syncthreads();  // the previous tile is consumed; qs is in place
-        // K and V rows of the tile: 2 x n rows, 64 lanes x E dims per row
-        for (int rr = threadIdx.x >> 6; rr < 2 * n; rr += 4) {
-            const int j = rr >> 1;
-            const bool isv = rr & 1;
-            const int64_t slot = ((int64_t)b * a.cap + kt + j) * a.nkv + g;
-            float* dst = (isv ? &Vs[j][0] : &Ks[j][0]) + lane * E;
-            if (a.kv_dt == DT_I8) {
-                const float sc = (isv ? a.vs : a.ks)[slot];
-                const int8_t* src = reinterpret_cast<const int8_t*>(isv ? a.vc : a.kc) + slot * HD + lane * E;
 #pragma unroll
-                for (int e = 0; e < E; ++e) dst[e] = (float)src[e] * sc;
+        for (int i = 0; i < Tl::PER; ++i) {
+            const int c = threadIdx.x + 256 * i, isv = c >= Tl::CH, cc = c - isv * Tl::CH;
+            const int j = cc / CPR, part = cc % CPR;
+            if (isv) {
+                *reinterpret_cast<u32x4*>(&Vt[j * Tl::VROW + part * 16]) = pre[i];
             } else {
-                const float* src = reinterpret_cast<const float*>(isv ? a.vc : a.kc) + slot * HD + lane * E;
-#pragma unroll
-                for (int e = 0; e < E; ++e) dst[e] = src[e];
+                uint32_t* d32 = reinterpret_cast<uint32_t*>(&Kt[j * Tl::KROW + part * 16]);
+                d32[0] = pre[i][0]; d32[1] = pre[i][1]; d32[2] = pre[i][2]; d32[3] = pre[i][3];
             }
         }
+        if (I8 && threadIdx.x < 2 * AT_KT) (threadIdx.x < AT_KT ? ksc : vsc)[threadIdx.x & (AT_KT - 1)] = psc;
+        if (kt + AT_KT < k1) issue(kt + AT_KT);
         __syncthreads();
         if (wave < G) {
-            // scores: lane pair (kj, half) covers key kj
             float dot = 0.0f;
             if (kj < n) {
-                const float* kr = &Ks[kj][half * (HD / 2)];
                 const float* qr = &qs[wave][half * (HD / 2)];
+                if (I8) {
+                    const uint32_t* kr = reinterpret_cast<const uint32_t*>(&Kt[kj * Tl::KROW + half * (HD / 2)]);
 #pragma unroll 8
-                for (int d = 0; d < HD / 2; d += 4) {
-                    const float4 kv = *reinterpret_cast<const float4*>(kr + d);
-                    const float4 qv = *reinterpret_cast<const float4*>(qr + d);
-                    dot += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+                    for (int w = 0; w < HD / 8; ++w) {
+                        const uint32_t c4 = kr[w];
+                        const float4 qv = *reinterpret_cast<const float4*>(qr + 4 * w);
+                        dot += qv.x * (float)(int8_t)(c4 & 0xff) + qv.y * (float)(int8_t)((c4 >> 8) & 0xff) +
+                               qv.z * (float)(int8_t)((c4 >> 16) & 0xff) + qv.w * (float)(int8_t)(c4 >> 24);
+                    }
+                    dot *= ksc[kj];
+                } else {
+                    const float* kr = reinterpret_cast<const float*>(&Kt[kj * Tl::KROW]) + half * (HD / 2);
+#pragma unroll 8
+                    for (int d = 0; d < HD / 2; d += 4) {
+                        const float4 kv = *reinterpret_cast<const float4*>(kr + d);
+                        const float4 qv = *reinterpret_cast<const float4*>(qr + d);
+                        dot += qv.x * kv.x + qv.y * kv.y + qv.z * kv.z + qv.w * kv.w;
+                    }
                 }
             }
             dot += __shfl_xor(dot, 1);
@@ -184,59 +250,498 @@ __global__ __launch_bounds__(256) void attn_split(AttnArgs a) {
             const float corr = __expf(m - mn);  // m = -inf on the first tile: 0
             const float p = kj < n ? __expf(sc - mn) : 0.0f;
             l = l * corr + wave_sum(half == 0 ? p : 0.0f);
+            const float pv = I8 ? p * vsc[kj < n ? kj : 0] : p;  // probability times the V row's scale
 #pragma unroll
             for (int e = 0; e < E; ++e) o[e] *= corr;
             for (int j = 0; j < n; ++j) {
-                const float pj = __shfl(p, 2 * j);
+                const float pj = __shfl(pv, 2 * j);
+                if (I8 && E == 4) {
+                    const uint32_t c4 = reinterpret_cast<const uint32_t*>(&Vt[j * Tl::VROW])[lane];
 #pragma unroll
-                for (int e = 0; e < E; ++e) o[e] += pj * Vs[j][lane * E + e];
+                    for (int e = 0; e < E; ++e) o[e] += pj * (float)(int8_t)((c4 >> (8 * e)) & 0xff);
+                } else if (I8) {
+#pragma unroll
+                    for (int e = 0; e < E; ++e) o[e] += pj * (float)(int8_t)Vt[j * Tl::VROW + lane * E + e];
+                } else {
+                    const float* vr = reinterpret_cast<const float*>(&Vt[j * Tl::VROW]) + lane * E;
+#pragma unroll
+                    for (int e = 0; e < E; ++e) o[e] += pj * vr[e];
+                }
             }
             m = mn;
         }
     }
-    if (wave < G) {
-        float* dst = a.part + (((int64_t)rl * a.nh + h) * a.nsplit + s) * (HD + 2);
+    if (wave >= G) return;
+    if (a.nsplit == 1) {  // the only split: finish the row here
+        const float inv = 1.0f / l;
+        const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + lane * E;
+        const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
 #pragma unroll
-        for (int e = 0; e < E; ++e) dst[lane * E + e] = o[e];
-        if (lane == 0) {
-            dst[HD] = m;
-            dst[HD + 1] = l;
+        for (int e = 0; e < E; ++e) {
+            const float y = o[e] * inv * (1.0f / (1.0f + __expf(-at_load(a.gate, a.in_dt, gi + e))));
+            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = y;
+            else store_act(a.out, a.out_dt, oi + e, y);
         }
+        return;
+    }
+    float* dst = a.part + (((int64_t)rl * a.nh + h) * a.nsplit + s) * (HD + 2);
+#pragma unroll
+    for (int e = 0; e < E; ++e) dst[lane * E + e] = o[e];
+    if (lane == 0) {
+        dst[HD] = m;
+        dst[HD + 1] = l;
     }
 }
 
 // ---------------------------------------------------------------------------
-// combine: one wave per (row, head); merges the used splits, gate, output.
-template <int HD>
-__global__ __launch_bounds__(64) void attn_combine(AttnArgs a) {
+// combine: one workgroup of NW waves per (row, head) (NW = 1 for up to 16
+// splits, else 4).  The split maxima are reduced over all threads; each wave
+// then sums the partial outputs of every NW-th split, eight splits' loads in
+// flight; the wave sums are merged in LDS.
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
     constexpr int E = HD / 64;
     const int rl = blockIdx.x, h = blockIdx.y, r = a.row0 + rl;
     const int b = r / a.T, t = r % a.T;
     const int P = a.pos[b] + t;
     const int L = (P >= 0 && P < a.cap && P < a.nsplit * a.split) ? P + 1 : 0;
-    const int lane = threadIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ns = (L + a.split - 1) / a.split;
     const float* pp = a.part + ((int64_t)rl * a.nh + h) * a.nsplit * (HD + 2);
+    __shared__ float red[2][NW];
+    __shared__ __attribute__((aligned(16))) float osum[NW][HD];
     float M = -INFINITY;
-    for (int s = 0; s < ns; ++s) M = fmaxf(M, pp[s * (HD + 2) + HD]);
-    float l = 0.0f, o[E];
+    for (int s = threadIdx.x; s < ns; s += 64 * NW) M = fmaxf(M, pp[s * (HD + 2) + HD]);
+    M = wave_max(M);
+    if (NW > 1) {
+        if (lane == 0) red[0][wave] = M;
+        __syncthreads();
+        M = red[0][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) M = fmaxf(M, red[0][w]);
+    }
+    float l = 0.0f;
+    for (int s = threadIdx.x; s < ns; s += 64 * NW) l += __expf(pp[s * (HD + 2) + HD] - M) * pp[s * (HD + 2) + HD + 1];
+    l = wave_sum(l);
+    if (NW > 1 && lane == 0) red[1][wave] = l;
+    float o[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) o[e] = 0.0f;
-    for (int s = 0; s < ns; ++s) {
-        const float w = __expf(pp[s * (HD + 2) + HD] - M);
-        l += w * pp[s * (HD + 2) + HD + 1];
+    int s = wave;
+    for (; s + 7 * NW < ns; s += 8 * NW) {  // splits s, s+NW, ..., s+7NW
+        float w[8], v[8][E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[e] += w * pp[s * (HD + 2) + lane * E + e];
+        for (int u = 0; u < 8; ++u) {
+            w[u] = pp[(s + NW * u) * (HD + 2) + HD];
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[u][e] = pp[(s + NW * u) * (HD + 2) + lane * E + e];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float wu = __expf(w[u] - M);
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[e] += wu * v[u][e];
+        }
+    }
+    for (; s < ns; s += NW) {
+        const float wu = __expf(pp[s * (HD + 2) + HD] - M);
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] += wu * pp[s * (HD + 2) + lane * E + e];
+    }
+    if (NW > 1) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) osum[wave][lane * E + e] = o[e];
+        __syncthreads();
+        if (wave != 0) return;
+        l = red[1][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) l += red[1][w];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) t += osum[w][lane * E + e];
+            o[e] = t;
+        }
     }
     const float inv = L > 0 ? 1.0f / l : 0.0f;
     const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + lane * E;
     const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
+        const int d = lane * E + e;
         const float y = o[e] * inv * (1.0f / (1.0f + __expf(-at_load(a.gate, a.in_dt, gi + e))));
         if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = y;
         else store_act(a.out, a.out_dt, oi + e, y);
     }
+}
+
+// ---------------------------------------------------------------------------
+// prefill: (16-token query block, KV head g, sequence b); wave w handles query
+// head g*G + w for the 16 tokens of the block, all on FP32 MFMA (16x16x4):
+//   S^T = K Q^T (32 keys x 16 queries per tile; Q in registers as the B
+//   operand), causal mask, online softmax per query column, O^T += V^T P^T
+//   (P^T is the score tile's own D layout: the B operand needs no shuffle).
+// K and V tiles of 32 keys are staged in LDS once for the KV group (INT8
+// codes with their scales folded into the scores and probabilities, or FP32).
+template <int HD, bool I8>
+__global__ __launch_bounds__(256) void attn_prefill(AttnArgs a) {
+    using Tl = AtTile<HD, I8>;
+    constexpr int ESZ = I8 ? 1 : 4, CPR = HD * ESZ / 16, KB = HD / 16, DT = HD / 16;
+    const int qb = blockIdx.x, g = blockIdx.y, b = a.b0 + blockIdx.z;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const int G = a.nh / a.nkv;
+    const int h = g * G + min(wave, G - 1);
+    const int tok0 = a.tb + qb * 16;
+    const int P0 = a.pos[b];
+    const int nq = min(16, a.tb + a.ntok - tok0);          // valid queries of the block
+    const int plast = P0 + tok0 + nq - 1;                  // last query position
+    const int pend = min(a.cap, a.nsplit * a.split);       // positions must stay below this
+    const int L = P0 >= 0 ? min(plast, pend - 1) + 1 : 0;  // keys 0 .. last valid query position
+    const int qpos = P0 + tok0 + li;                       // this lane's query position
+    const bool qvalid = li < nq && P0 >= 0 && qpos < pend; // an invalid query outputs zeros
+
+    __shared__ __attribute__((aligned(16))) uint8_t Kt[AT_KT * Tl::KROW];
+    __shared__ __attribute__((aligned(16))) uint8_t Vt[AT_KT * Tl::VROW];
+    __shared__ float ksc[AT_KT], vsc[AT_KT];
+
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.kc);
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.vc);
+    const int64_t slot0 = (int64_t)b * a.cap * a.nkv + g;
+    u32x4 pre[Tl::PER];
+    float psc = 0.0f;
+    auto issue = [&](int kt) {
+        const int n = min(AT_KT, L - kt);
+#pragma unroll
+        for (int i = 0; i < Tl::PER; ++i) {
+            const int c = threadIdx.x + 256 * i, isv = c >= Tl::CH, cc = c - isv * Tl::CH;
+            const int j = cc / CPR, part = cc % CPR;
+            const int64_t slot = slot0 + (int64_t)(kt + j) * a.nkv;
+            if (j < n) pre[i] = *reinterpret_cast<const u32x4*>((isv ? vbase : kbase) + slot * (HD * ESZ) + part * 16);
+            else pre[i] = u32x4{0u, 0u, 0u, 0u};
+        }
+        if (I8 && threadIdx.x < 2 * AT_KT) {
+            const int j = threadIdx.x & (AT_KT - 1);
+            psc = j < n ? (threadIdx.x < AT_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + j) * a.nkv] : 0.0f;
+        }
+    };
+    if (L > 0) issue(0);
+
+    // Q block of this wave's head in registers: lane (lg, li) holds Q[li][16kb + 4lg + q]
+    f32x4 qr[KB];
+    {
+        const int64_t row = (int64_t)b * a.T + tok0 + li - a.row0;  // segment-local row
+        const float* qp = a.qn + (row * a.nh + h) * HD + 4 * lg;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) qr[kb] = li < nq ? *reinterpret_cast<const f32x4*>(qp + 16 * kb) : f32x4{0, 0, 0, 0};
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    for (int kt = 0; kt < L; kt += AT_KT) {
+        __syncthreads();  // the previous tile is consumed
+#pragma unroll
+        for (int i = 0; i < Tl::PER; ++i) {
+            const int c = threadIdx.x + 256 * i, isv = c >= Tl::CH, cc = c - isv * Tl::CH;
+            const int j = cc / CPR, part = cc % CPR;
+            if (isv) {
+                *reinterpret_cast<u32x4*>(&Vt[j * Tl::VROW + part * 16]) = pre[i];
+            } else {
+                uint32_t* d32 = reinterpret_cast<uint32_t*>(&Kt[j * Tl::KROW + part * 16]);
+                d32[0] = pre[i][0]; d32[1] = pre[i][1]; d32[2] = pre[i][2]; d32[3] = pre[i][3];
+            }
+        }
+        if (I8 && threadIdx.x < 2 * AT_KT) (threadIdx.x < AT_KT ? ksc : vsc)[threadIdx.x & (AT_KT - 1)] = psc;
+        if (kt + AT_KT < L) issue(kt + AT_KT);
+        __syncthreads();
+        if (wave >= G) continue;
+        // S^T for keys kt + 16*sub + (4lg + r), queries li
+        f32x4 sc[2];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+            const int key = 16 * sub + li;  // A operand row: key, k = dim
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                float k4[4];
+                if (I8) {
+                    const uint32_t c4 = *reinterpret_cast<const uint32_t*>(&Kt[key * Tl::KROW + 16 * kb + 4 * lg]);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) k4[q] = (float)(int8_t)((c4 >> (8 * q)) & 0xff);
+                } else {
+                    const f32x4 kv = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(&Kt[key * Tl::KROW]) + 16 * kb + 4 * lg);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) k4[q] = kv[q];
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sacc = at_mfma16(k4[q], qr[kb][q], sacc);
+            }
+            sc[sub] = sacc;
+        }
+        // scale, mask, running max per query column li
+        float mt = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kl = 16 * sub + 4 * lg + r, kp = kt + kl;
+                float v = sc[sub][r] * scale * (I8 ? ksc[kl] : 1.0f);
+                v = (qvalid && kp <= qpos && kp < L) ? v : -INFINITY;
+                sc[sub][r] = v;
+                mt = fmaxf(mt, v);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float corr = mn == -INFINITY ? 1.0f : __expf(m - mn);
+        float ps = 0.0f;
+        f32x4 pb[2];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kl = 16 * sub + 4 * lg + r;
+                const float p = mn == -INFINITY ? 0.0f : __expf(sc[sub][r] - mn);
+                ps += p;
+                pb[sub][r] = I8 ? p * vsc[kl] : p;  // B operand of P V: (key 4lg+r, query li)
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = acc[dt] * corr;
+        // O^T[d][query] += V^T[d][key] P^T[key][query]
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int key = 16 * sub + 4 * lg + q, d = 16 * dt + li;
+                    const float va = I8 ? (float)(int8_t)Vt[key * Tl::VROW + d]
+                                        : reinterpret_cast<const float*>(&Vt[key * Tl::VROW])[d];
+                    acc[dt] = at_mfma16(va, pb[sub][q], acc[dt]);
+                }
+    }
+    if (wave >= G || li >= nq) return;
+    // acc[dt] lane (lg, li) element r: O^T[16dt + 4lg + r][query li]
+    const int64_t r = (int64_t)b * a.T + tok0 + li;
+    const float inv = L > 0 && l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int d = 16 * dt + 4 * lg + rr;
+            const float gt = at_load(a.gate, a.in_dt, r * a.ld_in + (int64_t)h * a.q_hs + d);
+            const float y = acc[dt][rr] * inv * (1.0f / (1.0f + __expf(-gt)));
+            const int64_t oi = r * a.ld_out + (int64_t)h * HD + d;
+            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi] = y;
+            else store_act(a.out, a.out_dt, oi, y);
+        }
+}
+
+// ---------------------------------------------------------------------------
+// prefill over an INT8 cache on f16 MFMA (16x16x16): the cached codes are
+// integers of at most 127 in magnitude, exact in f16, and their scales are
+// applied in FP32 (to the scores, and to the probabilities before P V), so
+// only q and p are rounded to f16 (relative 2^-11).  Same work decomposition
+// as attn_prefill; each tile is converted to f16 once as it is staged (K by
+// rows, V transposed, VhT[d][key], built from 4-key x 4-dim blocks), so the
+// MFMA operands are single 64-bit LDS reads.
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f16x4 i8x4_to_h4(uint32_t c4) {
+    f16x4 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r[q] = (_Float16)(float)(int8_t)((c4 >> (8 * q)) & 0xff);
+    return r;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
+    constexpr int KB = HD / 16, DT = HD / 16;
+    constexpr int KHP = HD + 8;           // f16 K row stride (elements)
+    constexpr int VHP = AT_KT + 4;        // f16 V^T row stride (elements)
+    constexpr int KCH = AT_KT * HD / 16;  // 16-code chunks of the K tile
+    constexpr int KPER = KCH / 256;       // per thread
+    constexpr int VBL = AT_KT * HD / 16;  // 4-key x 4-dim blocks of the V tile
+    constexpr int VPER = VBL / 256;
+    const int qb = blockIdx.x / a.nsplit, sp = blockIdx.x % a.nsplit, g = blockIdx.y, b = a.b0 + blockIdx.z;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    const int G = a.nh / a.nkv;
+    const int h = g * G + min(wave, G - 1);
+    const int tok0 = a.tb + qb * 16;
+    const int P0 = a.pos[b];
+    const int nq = min(16, a.tb + a.ntok - tok0);
+    const int plast = P0 + tok0 + nq - 1;
+    const int pend = min(a.cap, a.nsplit * a.split);
+    const int L = P0 >= 0 ? min(plast, pend - 1) + 1 : 0;
+    const int qpos = P0 + tok0 + li;
+    const bool qvalid = li < nq && P0 >= 0 && qpos < pend;
+    // this workgroup's keys: [k0, k1) of the block's causal range
+    const int k0 = sp * a.split, k1 = min(k0 + a.split, L);
+    if (k0 >= k1 && !(k0 == 0 && a.nsplit == 1)) return;  // uniform; a lone split still writes zeros
+
+    __shared__ __attribute__((aligned(16))) _Float16 Kh[AT_KT * KHP];
+    __shared__ __attribute__((aligned(16))) _Float16 VhT[HD * VHP];
+    __shared__ float ksc[AT_KT], vsc[AT_KT];
+
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.kc);
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.vc);
+    const int64_t slot0 = (int64_t)b * a.cap * a.nkv + g;
+    u32x4 kpre[KPER];
+    uint32_t vpre[VPER][4];
+    float psc = 0.0f;
+    auto issue = [&](int kt) {
+        const int n = min(AT_KT, k1 - kt);
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) {  // K: 16 consecutive codes of one key
+            const int c = threadIdx.x + 256 * i, j = c / (HD / 16), part = c % (HD / 16);
+            kpre[i] = j < n ? *reinterpret_cast<const u32x4*>(kbase + (slot0 + (int64_t)(kt + j) * a.nkv) * HD + part * 16)
+                            : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {  // V: 4 dims of 4 consecutive keys
+            const int blk = threadIdx.x + 256 * i, d4 = blk % (HD / 4), k4 = blk / (HD / 4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = 4 * k4 + q;
+                vpre[i][q] = j < n ? *reinterpret_cast<const uint32_t*>(vbase + (slot0 + (int64_t)(kt + j) * a.nkv) * HD + 4 * d4) : 0u;
+            }
+        }
+        if (threadIdx.x < 2 * AT_KT) {
+            const int j = threadIdx.x & (AT_KT - 1);
+            psc = j < n ? (threadIdx.x < AT_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + j) * a.nkv] : 0.0f;
+        }
+    };
+    if (k0 < k1) issue(k0);
+
+    f16x4 qh[KB];
+    {
+        const int64_t row = (int64_t)b * a.T + tok0 + li - a.row0;
+        const float* qp = a.qn + (row * a.nh + h) * HD + 4 * lg;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const f32x4 v = li < nq ? *reinterpret_cast<const f32x4*>(qp + 16 * kb) : f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) qh[kb][q] = (_Float16)v[q];
+        }
+    }
+    const float scale = 1.0f / sqrtf((float)HD);
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    for (int kt = k0; kt < k1; kt += AT_KT) {
+        __syncthreads();
+        // stage the tile as f16, converting every code once
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) {
+            const int c = threadIdx.x + 256 * i, j = c / (HD / 16), part = c % (HD / 16);
+            f16x4 hv[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) hv[w] = i8x4_to_h4(kpre[i][w]);
+            f16x4* dst = reinterpret_cast<f16x4*>(&Kh[j * KHP + part * 16]);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) dst[w] = hv[w];
+        }
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {
+            const int blk = threadIdx.x + 256 * i, d4 = blk % (HD / 4), k4 = blk / (HD / 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {  // dim 4*d4 + e of keys 4*k4 .. 4*k4+3
+                f16x4 hv;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) hv[q] = (_Float16)(float)(int8_t)((vpre[i][q] >> (8 * e)) & 0xff);
+                *reinterpret_cast<f16x4*>(&VhT[(4 * d4 + e) * VHP + 4 * k4]) = hv;
+            }
+        }
+        if (threadIdx.x < 2 * AT_KT) (threadIdx.x < AT_KT ? ksc : vsc)[threadIdx.x & (AT_KT - 1)] = psc;
+        if (kt + AT_KT < k1) issue(kt + AT_KT);
+        __syncthreads();
+        if (wave >= G) continue;
+        f32x4 sc[2];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) {
+            f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+            const _Float16* kr = &Kh[(16 * sub + li) * KHP + 4 * lg];
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(*reinterpret_cast<const f16x4*>(kr + 16 * kb), qh[kb], sacc, 0, 0, 0);
+            sc[sub] = sacc;
+        }
+        float mt = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kl = 16 * sub + 4 * lg + r, kp = kt + kl;
+                float v = sc[sub][r] * scale * ksc[kl];
+                v = (qvalid && kp <= qpos && kp < k1) ? v : -INFINITY;
+                sc[sub][r] = v;
+                mt = fmaxf(mt, v);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float corr = mn == -INFINITY ? 1.0f : __expf(m - mn);
+        float ps = 0.0f;
+        f16x4 pb[2];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kl = 16 * sub + 4 * lg + r;
+                const float p = mn == -INFINITY ? 0.0f : __expf(sc[sub][r] - mn);
+                ps += p;
+                pb[sub][r] = (_Float16)(p * vsc[kl]);
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = acc[dt] * corr;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    *reinterpret_cast<const f16x4*>(&VhT[(16 * dt + li) * VHP + 16 * sub + 4 * lg]), pb[sub], acc[dt],
+                    0, 0, 0);
+    }
+    if (wave >= G || li >= nq) return;
+    const int64_t r = (int64_t)b * a.T + tok0 + li;
+    if (a.nsplit > 1) {  // a partial (o, max, sum) for the combine kernel
+        if (!qvalid || qpos < k0) return;  // never read for this query
+        float* dst = a.part + (((r - a.row0) * a.nh + h) * a.nsplit + sp) * (HD + 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) dst[16 * dt + 4 * lg + rr] = acc[dt][rr];
+        if (lg == 0) {
+            dst[HD] = m;
+            dst[HD + 1] = l;
+        }
+        return;
+    }
+    const float inv = L > 0 && l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int d = 16 * dt + 4 * lg + rr;
+            const float gt = at_load(a.gate, a.in_dt, r * a.ld_in + (int64_t)h * a.q_hs + d);
+            const float y = acc[dt][rr] * inv * (1.0f / (1.0f + __expf(-gt)));
+            const int64_t oi = r * a.ld_out + (int64_t)h * HD + d;
+            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi] = y;
+            else store_act(a.out, a.out_dt, oi, y);
+        }
 }
 
 size_t attn_bytes_per_row(int nh, int hd, int nsplit) {
@@ -244,10 +749,30 @@ size_t attn_bytes_per_row(int nh, int hd, int nsplit) {
 }
 
 template <int HD>
+static void launch_combine(const AttnArgs& a, hipStream_t stream) {
+    if (a.nsplit <= 1) return;
+    if (a.nsplit <= 16) hipLaunchKernelGGL((attn_combine<HD, 1>), dim3(a.rows, a.nh), dim3(64), 0, stream, a);
+    else hipLaunchKernelGGL((attn_combine<HD, 4>), dim3(a.rows, a.nh), dim3(256), 0, stream, a);
+}
+
+template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_prep<HD>, dim3(a.rows), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(attn_split<HD>, dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(attn_combine<HD>, dim3(a.rows, a.nh), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL(attn_prep<HD>, dim3(a.rows), dim3(64 * std::min(16, a.nh + 2 * a.nkv)), 0, stream, a);
+    if (a.prefill) {
+        // INT8: query blocks x key splits (f16 MFMA), merged by attn_combine;
+        // FP32: one workgroup per query block over all its keys (FP32 MFMA)
+        if (a.kv_dt == DT_I8) {
+            hipLaunchKernelGGL(attn_prefill_i8h<HD>, dim3((a.ntok + 15) / 16 * a.nsplit, a.nkv, a.nb), dim3(256), 0,
+                               stream, a);
+            launch_combine<HD>(a, stream);
+        } else {
+            hipLaunchKernelGGL((attn_prefill<HD, false>), dim3((a.ntok + 15) / 16, a.nkv, a.nb), dim3(256), 0, stream, a);
+        }
+        return hipGetLastError();
+    }
+    if (a.kv_dt == DT_I8) hipLaunchKernelGGL((attn_split<HD, true>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((attn_split<HD, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+    launch_combine<HD>(a, stream);
     return hipGetLastError();
 }
 

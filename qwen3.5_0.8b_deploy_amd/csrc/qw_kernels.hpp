@@ -151,6 +151,8 @@ struct AttnArgs {
     float* qn;             // workspace [rows][nh][hd]: normalized, rotated q
     float* part;           // workspace [rows][nh][nsplit][hd + 2]: split partials
     int split, nsplit;     // keys per split, splits per row (upper bound)
+    int prefill;           // query-block kernel: tokens [tb, tb + ntok) of sequences [b0, b0 + nb)
+    int b0, nb, tb, ntok;  // (the rows of the segment are then contiguous: row0 = b0*T + tb)
 };
 // workspace bytes per row for a given split count
 size_t attn_bytes_per_row(int nh, int hd, int nsplit);

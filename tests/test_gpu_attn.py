@@ -11,7 +11,9 @@ Bars (normwise relative error against the oracle):
   FP32 cache, FP32 io      2e-5: only reduction orders (norms, dot products,
                            online softmax), __expf and the device cosf/sinf
                            differ; measured ~1e-6.
-  INT8 cache               5e-3: the same, plus INT8 rounding flips where the
+  INT8 cache               5e-3: the same, plus (prefill runs of 16+ tokens)
+                           f16 MFMA operands for q and p (2^-11), plus INT8
+                           rounding flips where the
                            GPU's and the oracle's normalized k or v land on
                            either side of a .5 step (one step = 1/127 of the
                            head's max); the cached codes are checked to differ
@@ -193,3 +195,42 @@ def test_attn_errors(qw, ctx, oracle):
                 [0], 1, 1.0e7, ROT)
     with pytest.raises(qw.QwError):  # odd rotary dim
         run_gpu(qw, ctx, st, cache, dev(st.rows[:, 0]), [0], 1, 1.0e7, 63)
+
+
+def _ctx_with(qw, env, **kw):
+    import os
+    os.environ.update(env)
+    try:
+        return qw.Context(0, **kw)
+    finally:
+        for k in env:
+            del os.environ[k]
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_attn_prefill_kernel_matches_split_path(qw, oracle, relerr, int8):
+    """The query-block prefill kernel, the key-split kernel (a context that
+    sends every run to it) and, with a 6 MB workspace, the prefill kernel in
+    768-token chunks of one sequence give the same result: 2 sequences of
+    1000 tokens, the second starting at position 7 after a 7-token prefix.
+    Over an INT8 cache the prefill kernel runs f16 MFMAs (q and p rounded to
+    f16, 2^-11), so it meets the split path within the INT8 bar (5e-3); over
+    an FP32 cache both are FP32 (2e-5); the chunked run is the same kernel."""
+    B, T, cap = 2, 1000, 1024
+    st = Stream(oracle, B, T + 7, 800)
+    outs = []
+    ctxs = [_ctx_with(qw, {}), _ctx_with(qw, {"QW_ATTN_PREFILL_MIN": "100000"}),
+            _ctx_with(qw, {}, workspace_bytes=qw.lib().qw_workspace_query(1, 1, 1) + (6 << 20))]
+    for c in ctxs:
+        cache = qw.kv_cache(B, cap, int8=int8)
+        sub = tuple(x[1:2] for x in cache)
+        run_gpu(qw, c, st, sub, dev(st.rows[1, :7]), [0], 7, 1.0e7, ROT)
+        rows = np.stack([st.rows[0, :T], st.rows[1, 7:T + 7]]).reshape(B * T, -1)
+        outs.append(host(run_gpu(qw, c, st, cache, dev(rows), [0, 7], T, 1.0e7, ROT)))
+        torch.cuda.synchronize()
+    for c in ctxs:
+        c.close()
+    print("prefill vs split", int8, relerr(outs[1], outs[0]), relerr(outs[2], outs[0]))
+    assert relerr(outs[1], outs[0]) <= (5e-3 if int8 else 2e-5) and relerr(outs[2], outs[0]) <= 2e-5
+    ref0, _ = oracle_stream(oracle, st, st.rows[0, :200], int8, 1.0e7, ROT, cap)
+    assert relerr(outs[0][:200], ref0) <= (5e-3 if int8 else 2e-5)
