@@ -13,6 +13,8 @@
 //                                       -> HipLinearAttnProjections / HipFullAttnProjections
 //   qwen::cuda::CudaLinearAttention / CudaLinearAttnState (whole decode layer,
 //   linear_attention_cuda.hpp:11-90)   -> HipLinearAttention / HipLinearAttnState
+//   qwen::cuda::CudaFullAttention / CudaKVCache (whole layer,
+//   full_attention_cuda.hpp:11-90)     -> HipFullAttention / HipKVCache
 //
 // Same argument meaning as the reference: weights arrive as host
 // std::vector<float> in row-major [out][in]; activations are caller-owned
@@ -26,6 +28,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <memory>
 #include <stdexcept>
@@ -564,6 +567,241 @@ class HipFullAttnProjections {
     qw_wfmt fmt_;
     std::shared_ptr<Context> ctx_;
     detail::WeightPtr Wq_, Wk_, Wv_, Wo_;
+};
+
+
+// ---------------------------------------------------------------------------
+// KV cache of all full-attention layers (CudaKVCache, full_attention_cuda.hpp:
+// 11-33; grow/ensure_capacity full_attention_cuda.cu:255-330): per layer
+// [capacity][kv_heads][head_dim], INT8 with one FP32 scale per token and KV
+// head (the reference format) or FP32 (the CPU KVCache format); capacity
+// doubles on demand, keeping the contents.  layer_lengths is host-side
+// bookkeeping, as in the reference.
+struct HipKVCache {
+    void* d_k_cache = nullptr;
+    void* d_v_cache = nullptr;
+    float* d_k_scale = nullptr;
+    float* d_v_scale = nullptr;
+    std::vector<int> layer_lengths;
+    int num_layers = 0, num_kv_heads = 0, head_dim = 0, capacity_seq_len = 0, max_seq_len = 0;
+    bool int8 = true;
+
+    HipKVCache() = default;
+    HipKVCache(const HipKVCache&) = delete;
+    HipKVCache& operator=(const HipKVCache&) = delete;
+    ~HipKVCache() { release(); }
+
+    void reset(int nl, int nkh, int hd, int init_capacity = 1024, bool int8_cache = true) {
+        release();
+        num_layers = nl;
+        num_kv_heads = nkh;
+        head_dim = hd;
+        int8 = int8_cache;
+        max_seq_len = 0;
+        layer_lengths.assign(nl, 0);
+        allocate(init_capacity, &d_k_cache, &d_v_cache, &d_k_scale, &d_v_scale);
+        capacity_seq_len = init_capacity;
+    }
+    void clear() {
+        zero(d_k_cache, d_v_cache, d_k_scale, d_v_scale, capacity_seq_len);
+        std::fill(layer_lengths.begin(), layer_lengths.end(), 0);
+        max_seq_len = 0;
+    }
+    int length(int layer_idx) const { return layer_lengths[layer_idx]; }
+    void ensure_capacity(int required) {
+        if (required <= capacity_seq_len) return;
+        int cap = capacity_seq_len * 2;
+        while (cap < required) cap *= 2;
+        void *k, *v;
+        float *ks, *vs;
+        allocate(cap, &k, &v, &ks, &vs);
+        for (int l = 0; l < num_layers; ++l) {  // copy each layer's slice into the larger stride
+            copy_layer(k, d_k_cache, cap, l, (size_t)num_kv_heads * head_dim * esize());
+            copy_layer(v, d_v_cache, cap, l, (size_t)num_kv_heads * head_dim * esize());
+            if (int8) {
+                copy_layer(ks, d_k_scale, cap, l, (size_t)num_kv_heads * sizeof(float));
+                copy_layer(vs, d_v_scale, cap, l, (size_t)num_kv_heads * sizeof(float));
+            }
+        }
+        release_buffers();
+        d_k_cache = k;
+        d_v_cache = v;
+        d_k_scale = ks;
+        d_v_scale = vs;
+        capacity_seq_len = cap;
+    }
+    // the C-ABI view of one layer (one sequence)
+    qw_kv_cache layer(int l) const {
+        const size_t per = (size_t)capacity_seq_len * num_kv_heads;
+        qw_kv_cache c{};
+        c.dtype = int8 ? QW_I8 : QW_F32;
+        c.k = static_cast<uint8_t*>(d_k_cache) + (size_t)l * per * head_dim * esize();
+        c.v = static_cast<uint8_t*>(d_v_cache) + (size_t)l * per * head_dim * esize();
+        c.k_scale = int8 ? d_k_scale + (size_t)l * per : nullptr;
+        c.v_scale = int8 ? d_v_scale + (size_t)l * per : nullptr;
+        c.capacity = capacity_seq_len;
+        return c;
+    }
+
+  private:
+    size_t esize() const { return int8 ? 1 : 4; }
+    void allocate(int cap, void** k, void** v, float** ks, float** vs) const {
+        const size_t n = (size_t)num_layers * cap * num_kv_heads * head_dim * esize();
+        const size_t ns = (size_t)num_layers * cap * num_kv_heads * sizeof(float);
+        *ks = *vs = nullptr;
+        if (hipMalloc(k, n) != hipSuccess || hipMalloc(v, n) != hipSuccess ||
+            (int8 && (hipMalloc(reinterpret_cast<void**>(ks), ns) != hipSuccess ||
+                      hipMalloc(reinterpret_cast<void**>(vs), ns) != hipSuccess)))
+            throw Error(QW_ERR_HIP, "HipKVCache: hipMalloc");
+        zero(*k, *v, *ks, *vs, cap);
+    }
+    void zero(void* k, void* v, float* ks, float* vs, int cap) const {
+        const size_t n = (size_t)num_layers * cap * num_kv_heads * head_dim * esize();
+        const size_t ns = (size_t)num_layers * cap * num_kv_heads * sizeof(float);
+        if (hipMemset(k, 0, n) != hipSuccess || hipMemset(v, 0, n) != hipSuccess ||
+            (ks && hipMemset(ks, 0, ns) != hipSuccess) || (vs && hipMemset(vs, 0, ns) != hipSuccess))
+            throw Error(QW_ERR_HIP, "HipKVCache: hipMemset");
+    }
+    void copy_layer(void* dst, const void* src, int new_cap, int l, size_t token_bytes) const {
+        if (hipMemcpy(static_cast<uint8_t*>(dst) + (size_t)l * new_cap * token_bytes,
+                      static_cast<const uint8_t*>(src) + (size_t)l * capacity_seq_len * token_bytes,
+                      (size_t)capacity_seq_len * token_bytes, hipMemcpyDeviceToDevice) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipKVCache: hipMemcpy");
+    }
+    void release_buffers() {
+        for (void* p : {d_k_cache, d_v_cache, static_cast<void*>(d_k_scale), static_cast<void*>(d_v_scale)})
+            if (p) (void)hipFree(p);
+        d_k_cache = d_v_cache = nullptr;
+        d_k_scale = d_v_scale = nullptr;
+    }
+    void release() { release_buffers(); }
+};
+
+// ---------------------------------------------------------------------------
+// A whole gated full-attention layer (CudaFullAttention,
+// full_attention_cuda.hpp:35-90; CPU FullAttention::forward,
+// language_full_attn.cpp:117-216):
+//   [q|gate interleaved per head | k | v] = W_in . x   one stacked projection
+//   core = qw_attn_forward(...)   norms, RoPE, cache write, causal attention, gate
+//   output = W_o . core
+// forward(input, output, cache, layer, position) runs one token;
+// forward_batch_prefill(..., positions, batch_size, max_seq) runs batch_size
+// consecutive tokens of one sequence starting at positions[0] (device), the
+// way the reference engine calls it (positions 0 .. n-1 of a prompt).
+// Rotary: 64 of 256 dims, theta 1e7 (the reference's constants).
+class HipFullAttention {
+  public:
+    explicit HipFullAttention(int hidden = 1024, int num_heads = 8, int num_kv_heads = 2, int q_head_dim = 256,
+                              int kv_head_dim = 256, qw_wfmt format = QW_WFMT_BF16,
+                              std::shared_ptr<Context> ctx = nullptr)
+        : hidden_(hidden), nh_(num_heads), nkv_(num_kv_heads), hd_(kv_head_dim), fmt_(format),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {
+        if (q_head_dim != kv_head_dim) throw Error(QW_ERR_SHAPE, "HipFullAttention: q_head_dim must equal kv_head_dim");
+        nin_ = nh_ * 2 * hd_ + 2 * nkv_ * hd_;
+    }
+    ~HipFullAttention() {
+        for (void* p : {static_cast<void*>(d_qn_), static_cast<void*>(d_kn_), static_cast<void*>(d_row_),
+                        static_cast<void*>(d_core_), static_cast<void*>(d_pos_)})
+            if (p) (void)hipFree(p);
+    }
+    HipFullAttention(const HipFullAttention&) = delete;
+    HipFullAttention& operator=(const HipFullAttention&) = delete;
+
+    void set_weights(const std::vector<float>& q_proj_weight, const std::vector<float>& k_proj_weight,
+                     const std::vector<float>& v_proj_weight, const std::vector<float>& q_norm_weight,
+                     const std::vector<float>& k_norm_weight, const std::vector<float>& o_proj_weight) {
+        const int H = hidden_;
+        check(q_proj_weight, (size_t)nh_ * 2 * hd_ * H, "q_proj");
+        check(k_proj_weight, (size_t)nkv_ * hd_ * H, "k_proj");
+        check(v_proj_weight, (size_t)nkv_ * hd_ * H, "v_proj");
+        check(q_norm_weight, (size_t)hd_, "q_norm");
+        check(k_norm_weight, (size_t)hd_, "k_norm");
+        check(o_proj_weight, (size_t)H * nh_ * hd_, "o_proj");
+        const float* parts[3] = {q_proj_weight.data(), k_proj_weight.data(), v_proj_weight.data()};
+        const int Ns[3] = {nh_ * 2 * hd_, nkv_ * hd_, nkv_ * hd_};
+        qw_weight* w = nullptr;
+        ctx_->check(qw_weight_pack_concat(ctx_->get(), 3, reinterpret_cast<const void* const*>(parts), Ns, QW_F32,
+                                          fmt_, H, nullptr, &w),
+                    "HipFullAttention in_proj");
+        Win_.reset(w);
+        Wo_ = detail::pack(*ctx_, o_proj_weight, H, nh_ * hd_, fmt_, "o_proj");
+        upload(d_qn_, q_norm_weight);
+        upload(d_kn_, k_norm_weight);
+        if (!d_pos_ && hipMalloc(&d_pos_, sizeof(int)) != hipSuccess) throw Error(QW_ERR_HIP, "hipMalloc");
+    }
+
+    void forward(const float* input, float* output, HipKVCache& kv_cache, int layer_idx, int position,
+                 hipStream_t stream = nullptr) const {
+        kv_cache.ensure_capacity(position + 1);
+        kv_cache.max_seq_len = std::max(kv_cache.max_seq_len, position + 1);
+        if (hipMemcpyAsync(d_pos_, &position, sizeof(int), hipMemcpyHostToDevice, stream) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipFullAttention: position upload");
+        run(input, output, kv_cache, layer_idx, d_pos_, 1, position + 1, stream);
+        if (hipStreamSynchronize(stream) != hipSuccess) throw Error(QW_ERR_HIP, "HipFullAttention: sync");
+        kv_cache.layer_lengths[layer_idx] = std::max(kv_cache.layer_lengths[layer_idx], position + 1);
+    }
+
+    // batch_size consecutive tokens of one sequence from positions[0] (device int)
+    void forward_batch_prefill(const float* input, float* output, HipKVCache& kv_cache, int layer_idx,
+                               const int* positions, int batch_size, int max_seq = 0,
+                               hipStream_t stream = nullptr) const {
+        int end = max_seq;
+        if (end == 0) {  // as the reference: read the positions back to size the cache
+            int p0 = 0;
+            if (hipMemcpy(&p0, positions, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+                throw Error(QW_ERR_HIP, "HipFullAttention: positions read");
+            end = p0 + batch_size;
+        }
+        kv_cache.ensure_capacity(end);
+        kv_cache.max_seq_len = std::max(kv_cache.max_seq_len, end);
+        run(input, output, kv_cache, layer_idx, positions, batch_size, end, stream);
+        kv_cache.layer_lengths[layer_idx] = std::max(kv_cache.layer_lengths[layer_idx], end);
+    }
+
+  private:
+    void run(const float* input, float* output, HipKVCache& kv, int layer, const int* pos, int T, int max_len,
+             hipStream_t stream) const {
+        detail::require(Wo_.get(), "HipFullAttention::forward");
+        if (kv.num_kv_heads != nkv_ || kv.head_dim != hd_ || layer < 0 || layer >= kv.num_layers)
+            throw Error(QW_ERR_SHAPE, "HipFullAttention: cache shape does not match");
+        ensure(T);
+        ctx_->check(qw_linear(ctx_->get(), Win_.get(), input, QW_F32, 0, T, d_row_, QW_F32, nin_, nullptr, stream),
+                    "HipFullAttention in_proj");
+        qw_attn_params p{nh_, nkv_, hd_, hd_ / 4, 1.0e7f, d_qn_, d_kn_};
+        const qw_kv_cache c = kv.layer(layer);
+        const float* q = d_row_;
+        ctx_->check(qw_attn_forward(ctx_->get(), &p, &c, 1, T, pos, max_len, q, q + hd_, 2 * hd_,
+                                    q + nh_ * 2 * hd_, q + nh_ * 2 * hd_ + nkv_ * hd_, QW_F32, nin_, d_core_, QW_F32,
+                                    nh_ * hd_, stream),
+                    "HipFullAttention core");
+        ctx_->check(qw_linear(ctx_->get(), Wo_.get(), d_core_, QW_F32, 0, T, output, QW_F32, 0, nullptr, stream),
+                    "HipFullAttention o_proj");
+    }
+    static void check(const std::vector<float>& v, size_t n, const char* name) {
+        if (v.size() != n) throw Error(QW_ERR_SHAPE, std::string(name) + ": expected " + std::to_string(n) + " floats");
+    }
+    static void upload(float*& d, const std::vector<float>& h) {
+        if (!d && hipMalloc(&d, h.size() * sizeof(float)) != hipSuccess) throw Error(QW_ERR_HIP, "hipMalloc");
+        if (hipMemcpy(d, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            throw Error(QW_ERR_HIP, "hipMemcpy");
+    }
+    void ensure(int T) const {
+        if (T <= cap_) return;
+        if (d_row_) (void)hipFree(d_row_);
+        if (d_core_) (void)hipFree(d_core_);
+        if (hipMalloc(&d_row_, (size_t)T * nin_ * sizeof(float)) != hipSuccess ||
+            hipMalloc(&d_core_, (size_t)T * nh_ * hd_ * sizeof(float)) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipFullAttention: hipMalloc");
+        cap_ = T;
+    }
+    int hidden_, nh_, nkv_, hd_, nin_;
+    qw_wfmt fmt_;
+    std::shared_ptr<Context> ctx_;
+    detail::WeightPtr Win_, Wo_;
+    float *d_qn_ = nullptr, *d_kn_ = nullptr;
+    int* d_pos_ = nullptr;
+    mutable float *d_row_ = nullptr, *d_core_ = nullptr;
+    mutable int cap_ = 0;
 };
 
 }  // namespace hip

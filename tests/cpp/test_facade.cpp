@@ -12,7 +12,9 @@
 #include "qw_ops.hpp"
 #include "qw_oracle.h"
 
+using qwen::hip::HipFullAttention;
 using qwen::hip::HipFullAttnProjections;
+using qwen::hip::HipKVCache;
 using qwen::hip::HipGreedyArgmaxSampler;
 using qwen::hip::HipLinearAttention;
 using qwen::hip::HipLinearAttnProjections;
@@ -313,6 +315,51 @@ static void test_linear_attention() {
     }
 }
 
+// Whole gated full-attention layer: a 5-token prefill then 3 single-token
+// steps through a cache that starts at capacity 4 (so it grows twice), against
+// FP32 projections + orc_full_attn_seq + o_proj.  INT8 cache: the kernels
+// round q and p to f16 in the prefill and may flip INT8 roundings, bar 5e-3;
+// FP32 cache: 1e-4.
+static void test_full_attention() {
+    const int H = 1024, nh = 8, nkv = 2, hd = 256, T0 = 5, T = 8;
+    auto Wq = normal((size_t)nh * 2 * hd * H, 170, 0.03f), Wk = normal((size_t)nkv * hd * H, 171, 0.03f);
+    auto Wv = normal((size_t)nkv * hd * H, 172, 0.03f), Wo = normal((size_t)H * nh * hd, 173, 0.02f);
+    auto qn = normal(hd, 174, 0.1f), kn = normal(hd, 175, 0.1f);
+    auto x = normal((size_t)T * H, 176);
+    // oracle: projections, the core over all T tokens from position 0, o_proj
+    std::vector<float> qraw((size_t)T * nh * 2 * hd), q((size_t)T * nh * hd), g((size_t)T * nh * hd),
+        k((size_t)T * nkv * hd), v((size_t)T * nkv * hd), core((size_t)T * nh * hd), ref((size_t)T * H);
+    orc_linear_f32(Wq.data(), x.data(), qraw.data(), T, nh * 2 * hd, H);
+    orc_split_q_gate(qraw.data(), q.data(), g.data(), T, nh, hd);
+    orc_linear_f32(Wk.data(), x.data(), k.data(), T, nkv * hd, H);
+    orc_linear_f32(Wv.data(), x.data(), v.data(), T, nkv * hd, H);
+    for (int int8 = 1; int8 >= 0; --int8) {
+        std::vector<int8_t> kc8((size_t)T * nkv * hd), vc8((size_t)T * nkv * hd);
+        std::vector<float> kc((size_t)T * nkv * hd), vc((size_t)T * nkv * hd), ks((size_t)T * nkv), vs((size_t)T * nkv);
+        orc_full_attn_seq(T, 0, nh, nkv, hd, hd / 4, 1.0e7f, qn.data(), kn.data(), q.data(), g.data(), k.data(),
+                          v.data(), int8, int8 ? (void*)kc8.data() : (void*)kc.data(),
+                          int8 ? (void*)vc8.data() : (void*)vc.data(), ks.data(), vs.data(), core.data());
+        orc_linear_f32(Wo.data(), core.data(), ref.data(), T, H, nh * hd);
+        HipFullAttention fa(H, nh, nkv, hd, hd, QW_WFMT_F32);
+        fa.set_weights(Wq, Wk, Wv, qn, kn, Wo);
+        HipKVCache cache;
+        cache.reset(2, nkv, hd, 4, int8 == 1);
+        const int layer = 1;
+        Dev dx(x), dy((size_t)T * H);
+        int* dpos = nullptr;
+        (void)hipMalloc(&dpos, sizeof(int));
+        (void)hipMemset(dpos, 0, sizeof(int));
+        fa.forward_batch_prefill(dx.p, dy.p, cache, layer, dpos, T0);
+        for (int t = T0; t < T; ++t) fa.forward(dx.p + (size_t)t * H, dy.p + (size_t)t * H, cache, layer, t);
+        (void)hipFree(dpos);
+        const double tol = int8 ? 5e-3 : 1e-4;
+        report(int8 ? "HipFullAttention prefill + decode (INT8 cache)" : "HipFullAttention prefill + decode (FP32 cache)",
+               relerr(dy.get(), ref), tol);
+        report("HipKVCache grew and kept its lengths",
+               (cache.capacity_seq_len == 8 && cache.length(layer) == T && cache.length(0) == 0) ? 0.0 : 1.0, 0.0);
+    }
+}
+
 static void test_errors() {
     HipMLP mlp(1024, 3584);
     bool threw = false;
@@ -338,6 +385,7 @@ int main() {
         test_mlp();
         test_attention_projections();
         test_linear_attention();
+        test_full_attention();
         test_lmhead_and_sampler();
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
