@@ -990,7 +990,7 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
     // few tokens per sequence: key-split rows; keys per split about two
     // workgroups per CU, 128 .. 1024 keys each
     const int64_t want = (int64_t)len * rows_all * nkv / (2LL * ctx->num_cus);
-    const int split = (int)std::min<int64_t>(1024, std::max<int64_t>(128, want)) / 32 * 32;
+    const int split = (int)std::min<int64_t>(1024, std::max<int64_t>(128, want)) / 64 * 64;
     const int nsplit = (len + split - 1) / split;
     const size_t per_row = qwk::attn_bytes_per_row(nh, hd, nsplit);
     const int64_t seg = std::min<int64_t>({rows_all, (int64_t)(ws / per_row), (int64_t)65535});

@@ -554,11 +554,31 @@ __global__ __launch_bounds__(256) void attn_prefill(AttnArgs a) {
 // MFMA operands are single 64-bit LDS reads.
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
+// Four signed INT8 codes to f16 without conversions: each byte u = c + 128
+// is placed under the f16 exponent of 1024 (bits 0x6400 | u = 1024 + u) by a
+// byte permute, then one packed f16 subtraction of 1152 leaves c (exact).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ f16x4 i8x4_to_h4(uint32_t c4) {
-    f16x4 r;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r[q] = (_Float16)(float)(int8_t)((c4 >> (8 * q)) & 0xff);
-    return r;
+    const uint32_t u = c4 ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const f16x2 x = __builtin_bit_cast(f16x2, lo) - off, y = __builtin_bit_cast(f16x2, hi) - off;
+    return f16x4{x[0], x[1], y[0], y[1]};
+}
+
+// 4x4 byte transpose: byte q of o[e] = byte e of w[q] (four keys' codes of one
+// dim from four keys' rows of four dims)
+__device__ __forceinline__ void transpose4x4(const uint32_t w[4], uint32_t o[4]) {
+    const uint32_t t0 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+    const uint32_t t2 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
+    const uint32_t t3 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+    o[0] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+    o[1] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+    o[2] = __builtin_amdgcn_perm(t3, t2, 0x05040100u);
+    o[3] = __builtin_amdgcn_perm(t3, t2, 0x07060302u);
 }
 
 template <int HD>
@@ -570,6 +590,7 @@ __global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
     constexpr int KPER = KCH / 256;       // per thread
     constexpr int VBL = AT_KT * HD / 16;  // 4-key x 4-dim blocks of the V tile
     constexpr int VPER = VBL / 256;
+    constexpr int KT4 = AT_KT / 4;        // lanes take consecutive 4-key groups: conflict-free V^T stores
     const int qb = blockIdx.x / a.nsplit, sp = blockIdx.x % a.nsplit, g = blockIdx.y, b = a.b0 + blockIdx.z;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
     const int G = a.nh / a.nkv;
@@ -601,24 +622,23 @@ __global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < KPER; ++i) {  // K: 16 consecutive codes of one key
             const int c = threadIdx.x + 256 * i, j = c / (HD / 16), part = c % (HD / 16);
-            kpre[i] = j < n ? *reinterpret_cast<const u32x4*>(kbase + (slot0 + (int64_t)(kt + j) * a.nkv) * HD + part * 16)
-                            : u32x4{0u, 0u, 0u, 0u};
+            // keys past the range read the range's last key: finite, masked out later
+            kpre[i] = *reinterpret_cast<const u32x4*>(kbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + part * 16);
         }
 #pragma unroll
         for (int i = 0; i < VPER; ++i) {  // V: 4 dims of 4 consecutive keys
-            const int blk = threadIdx.x + 256 * i, d4 = blk % (HD / 4), k4 = blk / (HD / 4);
+            const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int j = 4 * k4 + q;
-                vpre[i][q] = j < n ? *reinterpret_cast<const uint32_t*>(vbase + (slot0 + (int64_t)(kt + j) * a.nkv) * HD + 4 * d4) : 0u;
+                vpre[i][q] = *reinterpret_cast<const uint32_t*>(vbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + 4 * d4);
             }
         }
         if (threadIdx.x < 2 * AT_KT) {
             const int j = threadIdx.x & (AT_KT - 1);
-            psc = j < n ? (threadIdx.x < AT_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + j) * a.nkv] : 0.0f;
+            psc = (threadIdx.x < AT_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv];
         }
     };
-    if (k0 < k1) issue(k0);
 
     f16x4 qh[KB];
     {
@@ -631,6 +651,7 @@ __global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
             for (int q = 0; q < 4; ++q) qh[kb][q] = (_Float16)v[q];
         }
     }
+    if (k0 < k1) issue(k0);  // after the q loads, so that waiting for q does not wait for the tile
     const float scale = 1.0f / sqrtf((float)HD);
     f32x4 acc[DT];
 #pragma unroll
@@ -646,20 +667,17 @@ __global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
             f16x4 hv[4];
 #pragma unroll
             for (int w = 0; w < 4; ++w) hv[w] = i8x4_to_h4(kpre[i][w]);
-            f16x4* dst = reinterpret_cast<f16x4*>(&Kh[j * KHP + part * 16]);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) dst[w] = hv[w];
+            u32x4* dst = reinterpret_cast<u32x4*>(&Kh[j * KHP + part * 16]);
+            dst[0] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+            dst[1] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hv[2], hv[3], 0, 1, 2, 3, 4, 5, 6, 7));
         }
 #pragma unroll
         for (int i = 0; i < VPER; ++i) {
-            const int blk = threadIdx.x + 256 * i, d4 = blk % (HD / 4), k4 = blk / (HD / 4);
+            const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
+            uint32_t tw[4];
+            transpose4x4(vpre[i], tw);  // tw[e]: dim 4*d4 + e of keys 4*k4 .. 4*k4+3
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {  // dim 4*d4 + e of keys 4*k4 .. 4*k4+3
-                f16x4 hv;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) hv[q] = (_Float16)(float)(int8_t)((vpre[i][q] >> (8 * e)) & 0xff);
-                *reinterpret_cast<f16x4*>(&VhT[(4 * d4 + e) * VHP + 4 * k4]) = hv;
-            }
+            for (int e = 0; e < 4; ++e) *reinterpret_cast<f16x4*>(&VhT[(4 * d4 + e) * VHP + 4 * k4]) = i8x4_to_h4(tw[e]);
         }
         if (threadIdx.x < 2 * AT_KT) (threadIdx.x < AT_KT ? ksc : vsc)[threadIdx.x & (AT_KT - 1)] = psc;
         if (kt + AT_KT < k1) issue(kt + AT_KT);
@@ -744,6 +762,206 @@ __global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// decode over an INT8 cache on f16 MFMA: (key split, KV head g, row).  The
+// group's query heads are the MFMA columns (B = Q^T, 16 columns of which G
+// are used); a 64-key tile is staged as f16 once (K rows, V transposed) and
+// wave w takes its 16-key quarter: S^T = K Q^T, an online softmax of its own
+// per column, O^T += V^T P^T.  The four waves' (max, sum, O) are merged in LDS
+// at the end; a lone split writes the output, otherwise a partial.
+constexpr int AD_KT = 64;  // keys per tile
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
+    constexpr int KB = HD / 16, DT = HD / 16, E = HD / 64;
+    constexpr int KHP = HD + 8, VHP = AD_KT + 4;
+    constexpr int KPER = AD_KT * HD / 16 / 256;  // 16-code K chunks per thread
+    constexpr int VPER = AD_KT * HD / 16 / 256;  // 4x4 V blocks per thread
+    constexpr int KT4 = AD_KT / 4;               // lanes take consecutive 4-key groups: conflict-free V^T stores
+    const int s = blockIdx.x, g = blockIdx.y, rl = blockIdx.z, r = a.row0 + rl;
+    const int b = r / a.T, t = r % a.T;
+    const int P = a.pos[b] + t;
+    const int L = (P >= 0 && P < a.cap && P < a.nsplit * a.split) ? P + 1 : 0;
+    const int k0 = s * a.split, k1 = min(k0 + a.split, L);
+    const int G = a.nh / a.nkv;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+    if (k0 >= k1) {  // uniform over the workgroup
+        if (L == 0 && a.nsplit == 1 && wave < G) {
+            const int64_t oi = (int64_t)r * a.ld_out + (int64_t)(g * G + wave) * HD + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = 0.0f;
+                else store_act(a.out, a.out_dt, oi + e, 0.0f);
+            }
+        }
+        return;
+    }
+
+    __shared__ __attribute__((aligned(16))) _Float16 Kh[AD_KT * KHP];
+    __shared__ __attribute__((aligned(16))) _Float16 VhT[HD * VHP];
+    __shared__ float ksc[AD_KT], vsc[AD_KT];
+    __shared__ float wm[4][16], wl[4][16];
+
+    const uint8_t* kbase = reinterpret_cast<const uint8_t*>(a.kc);
+    const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.vc);
+    const int64_t slot0 = (int64_t)b * a.cap * a.nkv + g;
+    u32x4 kpre[KPER];
+    uint32_t vpre[VPER][4];
+    float psc = 0.0f;
+    auto issue = [&](int kt) {
+        const int n = min(AD_KT, k1 - kt);
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) {
+            const int c = threadIdx.x + 256 * i, j = c / (HD / 16), part = c % (HD / 16);
+            // keys past the range read the range's last key: finite, masked out later
+            kpre[i] = *reinterpret_cast<const u32x4*>(kbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + part * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {
+            const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = 4 * k4 + q;
+                vpre[i][q] = *reinterpret_cast<const uint32_t*>(vbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + 4 * d4);
+            }
+        }
+        if (threadIdx.x < 2 * AD_KT) {
+            const int j = threadIdx.x & (AD_KT - 1);
+            psc = (threadIdx.x < AD_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv];
+        }
+    };
+    // B operand: column li = query head g*G + li of this row (zero for li >= G)
+    f16x4 qh[KB];
+    {
+        const float* qp = a.qn + ((int64_t)rl * a.nh + g * G + min(li, G - 1)) * HD + 4 * lg;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const f32x4 v = li < G ? *reinterpret_cast<const f32x4*>(qp + 16 * kb) : f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) qh[kb][q] = (_Float16)v[q];
+        }
+    }
+    issue(k0);  // after the q loads, so that waiting for q does not wait for the tile
+    const float scale = 1.0f / sqrtf((float)HD);
+    f32x4 acc[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+
+    for (int kt = k0; kt < k1; kt += AD_KT) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < KPER; ++i) {
+            const int c = threadIdx.x + 256 * i, j = c / (HD / 16), part = c % (HD / 16);
+            f16x4 hv[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) hv[w] = i8x4_to_h4(kpre[i][w]);
+            u32x4* dst = reinterpret_cast<u32x4*>(&Kh[j * KHP + part * 16]);
+            dst[0] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
+            dst[1] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hv[2], hv[3], 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+#pragma unroll
+        for (int i = 0; i < VPER; ++i) {
+            const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
+            uint32_t tw[4];
+            transpose4x4(vpre[i], tw);  // tw[e]: dim 4*d4 + e of keys 4*k4 .. 4*k4+3
+#pragma unroll
+            for (int e = 0; e < 4; ++e) *reinterpret_cast<f16x4*>(&VhT[(4 * d4 + e) * VHP + 4 * k4]) = i8x4_to_h4(tw[e]);
+        }
+        if (threadIdx.x < 2 * AD_KT) (threadIdx.x < AD_KT ? ksc : vsc)[threadIdx.x & (AD_KT - 1)] = psc;
+        if (kt + AD_KT < k1) issue(kt + AD_KT);
+        __syncthreads();
+        const int kw = 16 * wave;  // this wave's quarter of the tile
+        if (kt + kw >= k1) continue;
+        f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+        const _Float16* kr = &Kh[(kw + li) * KHP + 4 * lg];
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+            sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(*reinterpret_cast<const f16x4*>(kr + 16 * kb), qh[kb], sacc, 0, 0, 0);
+        float mt = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int kl = kw + 4 * lg + q;
+            const float v = kt + kl < k1 ? sacc[q] * scale * ksc[kl] : -INFINITY;
+            sacc[q] = v;
+            mt = fmaxf(mt, v);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);  // finite: the quarter has at least one key
+        const float corr = __expf(m - mn);
+        float ps = 0.0f;
+        f16x4 pb;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float p = __expf(sacc[q] - mn);
+            ps += p;
+            pb[q] = (_Float16)(p * vsc[kw + 4 * lg + q]);
+        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            acc[dt] = acc[dt] * corr;
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                *reinterpret_cast<const f16x4*>(&VhT[(16 * dt + li) * VHP + kw + 4 * lg]), pb, acc[dt], 0, 0, 0);
+        }
+    }
+    // merge the four waves: column li of each wave's (m, l, O^T)
+    __syncthreads();  // the tiles are no longer read; reuse VhT for the wave outputs
+    float* ow = reinterpret_cast<float*>(VhT);  // [4 waves][G cols][HD]
+    if (lg == 0) {
+        wm[wave][li] = m;
+        wl[wave][li] = l;
+    }
+    if (li < G) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(&ow[(wave * 4 + li) * HD + 16 * dt + 4 * lg]) = acc[dt];
+    }
+    __syncthreads();
+    if (wave >= G) return;
+    const int col = wave, h = g * G + col;  // wave w now finishes query head g*G + w
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][col]);
+    float wsc[4], lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        wsc[w] = wm[w][col] == -INFINITY ? 0.0f : __expf(wm[w][col] - M);
+        lt += wsc[w] * wl[w][col];
+    }
+    float o[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int d = lane * E + e;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) v += wsc[w] * ow[(w * 4 + col) * HD + d];
+        o[e] = v;
+    }
+    if (a.nsplit == 1) {
+        const float inv = 1.0f / lt;
+        const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + lane * E;
+        const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float y = o[e] * inv * (1.0f / (1.0f + __expf(-at_load(a.gate, a.in_dt, gi + e))));
+            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = y;
+            else store_act(a.out, a.out_dt, oi + e, y);
+        }
+        return;
+    }
+    float* dst = a.part + (((int64_t)rl * a.nh + h) * a.nsplit + s) * (HD + 2);
+#pragma unroll
+    for (int e = 0; e < E; ++e) dst[lane * E + e] = o[e];
+    if (lane == 0) {
+        dst[HD] = M;
+        dst[HD + 1] = lt;
+    }
+}
+
 size_t attn_bytes_per_row(int nh, int hd, int nsplit) {
     return (size_t)nh * hd * 4 + (size_t)nh * nsplit * (hd + 2) * 4;
 }
@@ -770,7 +988,7 @@ static hipError_t launch_attn_hd(const AttnArgs& a, hipStream_t stream) {
         }
         return hipGetLastError();
     }
-    if (a.kv_dt == DT_I8) hipLaunchKernelGGL((attn_split<HD, true>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+    if (a.kv_dt == DT_I8) hipLaunchKernelGGL(attn_decode_i8h<HD>, dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((attn_split<HD, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
     launch_combine<HD>(a, stream);
     return hipGetLastError();

@@ -11,8 +11,8 @@ Bars (normwise relative error against the oracle):
   FP32 cache, FP32 io      2e-5: only reduction orders (norms, dot products,
                            online softmax), __expf and the device cosf/sinf
                            differ; measured ~1e-6.
-  INT8 cache               5e-3: the same, plus (prefill runs of 16+ tokens)
-                           f16 MFMA operands for q and p (2^-11), plus INT8
+  INT8 cache               5e-3: the same, plus f16 MFMA operands for q and
+                           p (2^-11; measured ~2.5e-4), plus INT8
                            rounding flips where the
                            GPU's and the oracle's normalized k or v land on
                            either side of a .5 step (one step = 1/127 of the
@@ -160,7 +160,8 @@ def test_attn_long_context_decode(qw, ctx, oracle, relerr, int8):
         kc = kc * host(cache[2][0, :L + 1])[..., None]
         vc = vc * host(cache[3][0, :L + 1])[..., None]
     ref = oracle.attn_token(qn, g[0], kc, vc, NH, NKV, HD)
-    assert relerr(host(out)[0], ref) <= 2e-5
+    # INT8 cache: f16 MFMA operands for q and p (2^-11); FP32 cache: FP32 throughout
+    assert relerr(host(out)[0], ref) <= (5e-3 if int8 else 2e-5)
 
 
 def test_attn_position_outside_cache_flags(qw, ctx, oracle):
