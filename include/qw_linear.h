@@ -246,6 +246,22 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
                           const void* k, const void* v, qw_dtype in_dtype, int ld_in, void* out,
                           qw_dtype out_dtype, int ld_out, hipStream_t stream);
 
+/* ---- token embedding and decode-step bookkeeping ----------------------------
+ * out[m][0..hidden) = table[ids[m]][0..hidden) (table row-major [vocab][hidden],
+ * F32 or BF16; out F32, BF16 or F16 with row stride ld_out, 0 = hidden; ids
+ * device int32 [M]).  Replaces TokenEmbedding::forward / CudaTokenEmbedding
+ * (token_embedding_cuda.cu:28-58, the BF16 table of the tied embedding).  An
+ * id outside [0, vocab) gives a zero row and sets the device error flag.
+ * hidden must be a multiple of 4. */
+qw_status qw_embedding_gather(qw_ctx* ctx, const void* table, qw_dtype table_dtype, int vocab, int hidden,
+                              const int32_t* ids, int M, void* out, qw_dtype out_dtype, int ld_out,
+                              hipStream_t stream);
+/* positions[i] += delta for i < n (device int32), as a kernel, so that a
+ * captured decode step advances its own cache positions on every replay.  No
+ * counterpart in the reference, whose engine passes the position from the
+ * host each step (cuda_engine.cu:308-325). */
+qw_status qw_positions_add(qw_ctx* ctx, int32_t* positions, int n, int delta, hipStream_t stream);
+
 /* ---- lm_head + greedy argmax -------------------------------------------------
  * token_ids[m] = argmax_v sum_k E[v][k]*h[m][k]; ties go to the LOWEST index
  * (std::max_element, sampler.cpp:41-43).  max_logit (optional) receives the

@@ -1008,6 +1008,32 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
     return QW_OK;
 }
 
+qw_status qw_embedding_gather(qw_ctx* ctx, const void* table, qw_dtype table_dtype, int vocab, int hidden,
+                              const int32_t* ids, int M, void* out, qw_dtype out_dtype, int ld_out,
+                              hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!table || !ids || !out) return fail(ctx, QW_ERR_NULL, "embedding: NULL argument");
+    if (table_dtype != QW_F32 && table_dtype != QW_BF16) return fail(ctx, QW_ERR_DTYPE, "embedding: table must be F32 or BF16");
+    if (!valid_act(out_dtype)) return fail(ctx, QW_ERR_DTYPE, "embedding: output dtype unsupported");
+    if (vocab < 1 || hidden < 4 || hidden % 4 || M < 1)
+        return fail(ctx, QW_ERR_SHAPE, "embedding: vocab=%d, hidden=%d, M=%d", vocab, hidden, M);
+    if (ld_out == 0) ld_out = hidden;
+    if (ld_out < hidden || ld_out % 4) return fail(ctx, QW_ERR_SHAPE, "embedding: ld_out=%d", ld_out);
+    hipError_t e = qwk::launch_embed_gather(table, (int)table_dtype, vocab, hidden, ids, M, out, (int)out_dtype, ld_out,
+                                            ctx->mlp_ctl + 3, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "embedding launch");
+    return QW_OK;
+}
+
+qw_status qw_positions_add(qw_ctx* ctx, int32_t* positions, int n, int delta, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!positions) return fail(ctx, QW_ERR_NULL, "positions: NULL");
+    if (n < 1) return fail(ctx, QW_ERR_SHAPE, "positions: n=%d", n);
+    hipError_t e = qwk::launch_positions_add(positions, n, delta, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "positions launch");
+    return QW_OK;
+}
+
 qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* down, const void* x,
                        qw_dtype xdt, const float* gamma, float eps, const void* residual,
                        qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream) {

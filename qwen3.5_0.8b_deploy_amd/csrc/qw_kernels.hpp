@@ -158,6 +158,11 @@ struct AttnArgs {
 size_t attn_bytes_per_row(int nh, int hd, int nsplit);
 hipError_t launch_attn(const AttnArgs& a, hipStream_t stream);
 
+// Token-embedding gather and the decode-step position advance (qw_embed.hip).
+hipError_t launch_embed_gather(const void* table, int tdt, int vocab, int K, const int32_t* ids, int M, void* out,
+                               int odt, int ld_out, unsigned* err, hipStream_t stream);
+hipError_t launch_positions_add(int32_t* pos, int n, int delta, hipStream_t stream);
+
 // Weight packing (qw_pack.hip).  src is a device buffer W[N][K] in src_dt.
 // Output rows are written to physical tile `tile_of_row(o)` (GLU interleave
 // handled by the caller through tile_mul/tile_add: pt = t*tile_mul+tile_add).

@@ -31,7 +31,7 @@ EXPORTS = [
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
-    "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
+    "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_embedding_gather", "qw_positions_add", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
 
 
@@ -126,6 +126,8 @@ def lib():
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
         "qw_gdn_decode": ([_vp, ctypes.POINTER(GdnParams), _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i,
                            _vp], _i),
+        "qw_embedding_gather": ([_vp, _vp, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp], _i),
+        "qw_positions_add": ([_vp, _vp, _i, _i, _vp], _i),
         "qw_attn_forward": ([_vp, ctypes.POINTER(AttnParams), ctypes.POINTER(KVCache), _i, _i, _vp, _i, _vp, _vp,
                              _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp], _i),
         "qw_gdn_prefill": ([_vp, ctypes.POINTER(GdnParams), _i, _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i,
@@ -509,3 +511,14 @@ def attn_forward(ctx, q_norm_weight, k_norm_weight, cache, positions, q, gate, k
     ctx.check(lib().qw_attn_forward(ctx.handle, ctypes.byref(p), ctypes.byref(c), rows // tokens, tokens,
                                     _ptr(positions), max_len, _ptr(q), _ptr(gate), q_head_stride, _ptr(k), _ptr(v),
                                     _torch_code(q), ld_in, _ptr(out), _torch_code(out), ld_out, _stream(stream)))
+
+
+def embedding_gather(ctx, table, ids, out, ld_out=0, stream=None):
+    """out[m] = table[ids[m]] (table [vocab][hidden] F32 or BF16; ids int32)."""
+    ctx.check(lib().qw_embedding_gather(ctx.handle, _ptr(table), _torch_code(table), table.shape[0], table.shape[1],
+                                        _ptr(ids), ids.shape[0], _ptr(out), _torch_code(out),
+                                        ld_out or out.stride(0), _stream(stream)))
+
+
+def positions_add(ctx, positions, delta=1, stream=None):
+    ctx.check(lib().qw_positions_add(ctx.handle, _ptr(positions), positions.numel(), delta, _stream(stream)))
