@@ -387,6 +387,7 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
 
     extra.update(run_gdn(qw, ctx, torch, timer, stream, randn, args))
     extra.update(run_attn(qw, ctx, torch, timer, stream, randn, args))
+    extra.update(run_decode_model(qw, ctx, torch, timer, stream, randn, args))
 
     # config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each
     for fmt, name in ((qw.WFMT_BF16, "bf16"), (qw.WFMT_INT8, "int8")):
@@ -411,6 +412,60 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         del Es
     torch.cuda.synchronize()
     return extra
+
+
+def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
+    """The whole greedy decode step of the 24-layer model (engine.py: embedding
+    gather, 18 Gated-DeltaNet + 6 full-attention layers, fused MLPs, final norm,
+    lm_head argmax over 248320 tokens, position advance) captured as one graph
+    and replayed per token; BF16 weights (random init, real shapes), INT8 KV
+    cache, B sequences at a context of 1024 tokens (random cache contents and
+    recurrent states)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("qw_engine", os.path.join(os.path.dirname(os.path.abspath(__file__)), "qwen3.5_0.8b_deploy_amd", "engine.py"))
+    em = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(em)
+    f32 = torch.float32
+    layers = []
+    for i in range(LAYERS):
+        L = {"in_norm": randn(H, std=0.1, dtype=f32), "post_norm": randn(H, std=0.1, dtype=f32),
+             "gate": randn(I, H, std=0.02, dtype=f32), "up": randn(I, H, std=0.02, dtype=f32),
+             "down": randn(H, I, std=0.02, dtype=f32)}
+        if em.is_linear_layer(i):
+            L.update(qkv=randn(em.CD, H, std=0.02, dtype=f32), a=randn(em.LNH, H, std=0.02, dtype=f32),
+                     b=randn(em.LNH, H, std=0.02, dtype=f32), z=randn(em.LNH * em.VD, H, std=0.02, dtype=f32),
+                     conv=randn(em.CD, em.CK, std=0.5, dtype=f32), out=randn(H, em.LNH * em.VD, std=0.02, dtype=f32),
+                     A_log=randn(em.LNH, std=0.5, dtype=f32), dt_bias=randn(em.LNH, std=0.5, dtype=f32),
+                     norm_w=1.0 + randn(em.VD, std=0.1, dtype=f32))
+        else:
+            L.update(q=randn(em.FNH * 2 * em.HD, H, std=0.02, dtype=f32), k=randn(em.FNKV * em.HD, H, std=0.02, dtype=f32),
+                     v=randn(em.FNKV * em.HD, H, std=0.02, dtype=f32), q_norm=randn(em.HD, std=0.1, dtype=f32),
+                     k_norm=randn(em.HD, std=0.1, dtype=f32), o=randn(H, em.FNH * em.HD, std=0.02, dtype=f32))
+        layers.append(L)
+    embed = randn(V, H, std=0.02)  # BF16 table, tied with the lm_head
+    final_norm = randn(H, std=0.1, dtype=f32)
+    out = {}
+    ctxlen = 1024
+    for B in (1, 32):
+        eng = em.DecodeEngine(qw, ctx, layers, final_norm, embed, B, ctxlen + 256)
+        eng.reset(torch.randint(0, V, (B,)).tolist(), [ctxlen] * B)
+        for P in eng.layers:
+            if P["linear"]:
+                P["rs"].normal_(0.0, 0.1)
+            else:
+                P["cache"][0].random_(-127, 128)
+                P["cache"][1].random_(-127, 128)
+                P["cache"][2].uniform_(0.001, 0.01)
+                P["cache"][3].uniform_(0.001, 0.01)
+        g = graphed(qw, ctx, stream, lambda: eng.step(stream=stream))
+        n = max(8, args.steps)
+        ms = timer.run(g.launch, n, 2)
+        out[f"decode_model_B{B}_ctx{ctxlen}"] = {"ms_per_step": round(ms, 3), "tok_per_s": round(B / (ms * 1e-3), 1)}
+        log("decode model", B, out[f"decode_model_B{B}_ctx{ctxlen}"])
+        del eng, g
+    del layers, embed
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_attn(qw, ctx, torch, timer, stream, randn, args):
