@@ -117,3 +117,114 @@ class DecodeEngine:
         qw.rmsnorm(ctx, x, self.final_norm, self.xn, stream=stream)
         qw.lmhead_argmax(ctx, self.E, self.xn, self.ids, stream=stream)
         qw.positions_add(ctx, self.pos, 1, stream=stream)
+
+
+# ---------------------------------------------------------------------------
+# Weight loaders.  The reference carries three layouts of the same tensors,
+# all raw little-endian FP32:
+#   (A) a directory tree, one file per tensor, matrices [out][in] as the CPU
+#       operators consume them: weights/language/embed_tokens.bin,
+#       weights/language_backbone/layer_N/{input_layernorm, post_layernorm,
+#       mlp_gate, mlp_up, mlp_down, linear_qkv, linear_a, linear_b, linear_z,
+#       linear_conv1d, linear_A_log, linear_dt_bias, linear_norm, linear_out,
+#       full_q, full_k, full_v, full_q_norm, full_k_norm, full_o}.bin and
+#       weights/language_backbone/final_norm.bin
+#       (tests/integration/e2e_validate.cpp:37-84,126);
+#   (B) one flat vector per layer as CudaEngine::set_layer_weights slices it
+#       (cuda_engine.cu:244-298): the common prefix (norms, MLP), then the
+#       whole linear-attention section, then the whole full-attention section,
+#       matrices [out][in];
+#   (C) the files of scripts/export_real_weights.py: weights/layer_XX.bin with
+#       the common prefix and only the layer type's own section, every matrix
+#       transposed to [in][out] by its transpose_if_needed (:43-48), plus
+#       norm.bin and embedding.bin.
+# All three load into the `layers` dicts DecodeEngine takes ([out][in]).
+
+_COMMON = [("in_norm", (H,)), ("post_norm", (H,)), ("gate", (I, H)), ("up", (I, H)), ("down", (H, I))]
+_LINEAR = [("qkv", (CD, H)), ("a", (LNH, H)), ("b", (LNH, H)), ("z", (LNH * VD, H)), ("conv", (CD, CK)),
+           ("out", (H, LNH * VD)), ("A_log", (LNH,)), ("dt_bias", (LNH,)), ("norm_w", (VD,))]
+_FULL = [("q", (FNH * 2 * HD, H)), ("k", (FNKV * HD, H)), ("v", (FNKV * HD, H)), ("q_norm", (HD,)),
+         ("k_norm", (HD,)), ("o", (H, FNH * HD))]
+_DIR_NAMES = {"in_norm": "input_layernorm", "post_norm": "post_layernorm", "gate": "mlp_gate", "up": "mlp_up",
+              "down": "mlp_down", "qkv": "linear_qkv", "a": "linear_a", "b": "linear_b", "z": "linear_z",
+              "conv": "linear_conv1d", "A_log": "linear_A_log", "dt_bias": "linear_dt_bias", "norm_w": "linear_norm",
+              "out": "linear_out", "q": "full_q", "k": "full_k", "v": "full_v", "q_norm": "full_q_norm",
+              "k_norm": "full_k_norm", "o": "full_o"}
+
+
+def _read_f32(path, count=None):
+    import numpy as np
+    a = np.fromfile(path, dtype="<f4")
+    if count is not None and a.size != count:
+        raise ValueError(f"{path}: {a.size} floats, expected {count}")
+    return a
+
+
+def _split(flat, fields, transposed=False, offset=0):
+    import numpy as np
+    out = {}
+    for name, shape in fields:
+        n = int(np.prod(shape))
+        if offset + n > flat.size:
+            raise ValueError(f"flat layer too short at {name}: {flat.size} < {offset + n}")
+        a = flat[offset:offset + n]
+        if len(shape) == 2 and name != "conv":
+            a = a.reshape(shape[::-1]).T if transposed else a.reshape(shape)
+        else:
+            a = a.reshape(shape)
+        out[name] = np.ascontiguousarray(a, dtype=np.float32)
+        offset += n
+    return out, offset
+
+
+def flat_layer_size(kind):
+    """Floats in one flat layer: 'engine' (B, both sections) or 'linear' /
+    'full' (C, one section)."""
+    import numpy as np
+    n = lambda fs: sum(int(np.prod(s)) for _, s in fs)
+    return n(_COMMON) + {"engine": n(_LINEAR) + n(_FULL), "linear": n(_LINEAR), "full": n(_FULL)}[kind]
+
+
+def layer_from_engine_flat(flat, layer_idx):
+    """(B): the CudaEngine::set_layer_weights vector of one layer."""
+    L, off = _split(flat, _COMMON)
+    lin, off = _split(flat, _LINEAR, offset=off)
+    full, off = _split(flat, _FULL, offset=off)
+    if off != flat.size:
+        raise ValueError(f"flat layer has {flat.size} floats, expected {off}")
+    L.update(lin if is_linear_layer(layer_idx) else full)
+    return L
+
+
+def layer_from_export_flat(flat, layer_idx):
+    """(C): one layer_XX.bin of export_real_weights.py (matrices stored [in][out])."""
+    L, off = _split(flat, _COMMON, transposed=True)
+    sec, off = _split(flat, _LINEAR if is_linear_layer(layer_idx) else _FULL, transposed=True, offset=off)
+    if off != flat.size:
+        raise ValueError(f"layer_{layer_idx:02d}.bin has {flat.size} floats, expected {off}")
+    L.update(sec)
+    return L
+
+
+def load_dir_tree(root, num_layers=24, vocab=V_DEFAULT):
+    """(A): returns (layers, final_norm, embed) as numpy float32 arrays."""
+    import os
+    import numpy as np
+    layers = []
+    for i in range(num_layers):
+        pre = os.path.join(root, "language_backbone", f"layer_{i}")
+        fields = _COMMON + (_LINEAR if is_linear_layer(i) else _FULL)
+        layers.append({n: _read_f32(os.path.join(pre, _DIR_NAMES[n] + ".bin"), int(np.prod(s))).reshape(s)
+                       for n, s in fields})
+    final_norm = _read_f32(os.path.join(root, "language_backbone", "final_norm.bin"), H)
+    embed = np.fromfile(os.path.join(root, "language", "embed_tokens.bin"), dtype="<f4").reshape(-1, H)
+    return layers, final_norm, embed
+
+
+def load_export_files(root, num_layers=24):
+    """(C): weights/layer_XX.bin, norm.bin, embedding.bin; (layers, final_norm, embed)."""
+    import os
+    layers = [layer_from_export_flat(_read_f32(os.path.join(root, f"layer_{i:02d}.bin")), i) for i in range(num_layers)]
+    final_norm = _read_f32(os.path.join(root, "norm.bin"), H)
+    embed = _read_f32(os.path.join(root, "embedding.bin")).reshape(-1, H)
+    return layers, final_norm, embed
