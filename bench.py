@@ -11,8 +11,10 @@ captured once in a HIP graph and replayed.
 
 value = algorithmic bytes of the step / step time (GB/s), with
   per layer: W 22,020,096 B + x M*1024*2 + y M*1024*2 + gamma 1024*4.
-roofline: the dominant kernel (the fused gate/up GEMV, 14.68 MB of weights
-per launch) timed with HIP events around each launch on its own stream.
+roofline: the dominant kernel -- the one-launch MLP kernel (qwk::mlp_kernel,
+22.02 MB of weights per launch), which is the whole headline step (24
+launches) -- timed with HIP events on the step's own stream over the timed
+region.
 cpu_baseline: the reference's own MLP::forward_batch (oracle/_ref, compiled
 from the reference sources; FP32, 1 thread) on a bounded sample, expressed
 in the same algorithmic-bytes unit.  Falls back to the oracle port when
@@ -37,7 +39,7 @@ H, I, V = 1024, 3584, 248320
 LAYERS = 24
 LINEAR_LAYERS = [i for i in range(24) if i % 4 != 3]   # 18 Gated-DeltaNet layers
 COPY_BYTES = 64 << 20   # calibration copy for the HBM traffic counters
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gateup_glu_bf16_M1.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_mlp_fused_bf16_M1.txt")
 METRIC = "decode GEMV HBM GB/s (% of peak) at M=1; prefill GEMM TFLOPS (% MFMA peak)"
 
 
@@ -165,8 +167,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-kernel", action="store_true",
-                    help="counter pass: only the dominant kernel (eager launches) and a 64 MiB "
-                         "calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
+                    help="counter pass: only the dominant kernel (eager one-launch MLP blocks) and a "
+                         "64 MiB calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -207,11 +209,10 @@ def main():
 
     h1 = randn(1, H)
     if args.profile_kernel:
-        hmid = torch.empty(1, I, device="cuda", dtype=torch.bfloat16)
         with torch.cuda.stream(stream):
             for _ in range(4):
                 for l in range(LAYERS):
-                    qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l])
+                    qw.mlp_fused(ctx, gu[l], dn[l], h1, h1, gamma=gam[l], residual=h1)
             src = torch.empty(COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16).fill_(1.0)
             dst = torch.empty_like(src)
             for _ in range(4):
@@ -226,20 +227,25 @@ def main():
     value = step_bytes / (ms * 1e-3) / 1e9
     log(f"headline: {ms * 1e3:.1f} us/step, {value:.0f} GB/s")
 
-    # Dominant kernel: the fused RMSNorm + gate/up + SiLU*mul GEMV.  Its
-    # average launch duration is timed with HIP events on its own stream over
-    # a graph of the 24 layers' launches back to back (so the figure includes
-    # the graph's inter-kernel gap and is an upper bound on the duration).
+    # Dominant kernel: the one-launch MLP kernel, 24 launches per step.  Its
+    # average launch duration is the timed region of the step graph (HIP
+    # events on the stream the kernels run on) over the 24 launches, so it
+    # includes the graph's inter-kernel gap and is an upper bound.
+    k_us = ms * 1e3 / LAYERS
+    k_bytes = mlp_bytes(1)
+    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
+    log(f"mlp kernel: {k_us:.2f} us avg, {k_gbs:.0f} GB/s")
+    # the separate fused RMSNorm + gate/up + SiLU*mul GEMV (the two-launch form)
     hmid = torch.empty(1, I, device="cuda", dtype=torch.bfloat16)
     g_gu = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l]) for l in range(LAYERS)])
-    k_us = 1e3 * timer.run(g_gu.launch, args.steps, args.warmup) / LAYERS
-    k_bytes = gateup_bytes(1)
-    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
-    log(f"gate/up kernel: {k_us:.2f} us avg, {k_gbs:.0f} GB/s")
+    gu_us = 1e3 * timer.run(g_gu.launch, args.steps, args.warmup) / LAYERS
+    log(f"gate/up kernel: {gu_us:.2f} us avg, {gateup_bytes(1) / (gu_us * 1e-6) / 1e9:.0f} GB/s")
 
     extra = {}
     if not args.quick:
         extra = run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args)
+    extra["gateup_glu_kernel_bf16_M1"] = {"us_per_launch": round(gu_us, 3),
+                                          "GBps": round(gateup_bytes(1) / (gu_us * 1e-6) / 1e9, 1)}
 
     cpu = None
     if not args.no_cpu:
@@ -268,7 +274,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "qwk::skinny_kernel<BF16 weights, BF16 x, CT=1, GLU> (fused RMSNorm+gate/up+SiLU*mul)",
+            "kernel": "qwk::mlp_kernel<BF16 weights, BF16 x, RMSNorm, gamma> (one-launch RMSNorm+gate/up+SiLU*mul+down+residual)",
             "achieved": round(k_gbs, 2),
             "peak": HBM_PEAK,
             "unit": "GB/s",

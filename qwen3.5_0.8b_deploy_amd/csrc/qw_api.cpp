@@ -26,7 +26,7 @@ struct qw_ctx {
     int min_items = 0;       // split K until a launch has this many items (0: never)
     int force_nw = 0;        // waves per skinny workgroup (0: automatic)
     int force_nw_glu = 0;    // same, GLU weights only
-    bool mlp_fused = false;  // one-launch MLP block (QW_MLP_FUSED=1)
+    bool mlp_fused = true;   // one-launch MLP block at decode sizes (QW_MLP_FUSED=0: two launches)
     bool gemv = true;        // register-direct GEMV for M <= 32 (QW_GEMV=0: skinny kernel)
     int gemm_min_m = kGemmMinM;  // tokens from which BF16 calls may use the MFMA GEMM
     bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
@@ -84,7 +84,8 @@ constexpr size_t kKeysBytes = 64 * 1024;         // 8192 tokens
 constexpr size_t kDoneBytes = 256;
 constexpr size_t kPartialsBytes = 32u << 20;
 constexpr size_t kFixedBytes = kCountersBytes + kKeysBytes + kDoneBytes + kPartialsBytes;
-constexpr int kMaxCounters = (int)(kCountersBytes / 4);
+constexpr int kMlpCounterWords = 4096;  // tail of the counter region: the one-launch MLP's slots
+constexpr int kMaxCounters = (int)(kCountersBytes / 4) - kMlpCounterWords;
 constexpr int kMaxKeys = (int)(kKeysBytes / 8);
 constexpr int kSkinnyMaxM = 32;
 
@@ -1053,11 +1054,16 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
     const size_t per_tok = (size_t)I * dsize(hdt);
     int chunk = (int)std::min<size_t>((size_t)M, ctx->scratch_bytes / per_tok);
     if (chunk < 1) return fail(ctx, QW_ERR_WORKSPACE, "workspace too small for one token of the MLP");
-    // one launch for the whole block when the activations fit the LDS
+    // decode: the whole block in one launch (16-bit activations, BF16 or
+    // INT8 weights, up to 16 tokens, Qwen-sized projections)
+    const int wfi = (int)gateup->wf;
     if (ctx->mlp_fused && M <= 16 && (size_t)M * per_tok <= ctx->scratch_bytes &&
-        valid_act(xdt) && valid_act(ydt) && (!residual || valid_act(residual_dtype)) &&
-        aligned(x, 16) && (H * dsize(xdt)) % 16 == 0 && (!gamma || aligned(gamma, 16)) &&
-        qwk::mlp_fused_lds_bytes(gateup->wf, (int)xdt, M, H, I) <= qwk::kSkinnyMaxLds) {
+        ((gateup->wf == QW_WFMT_BF16 && xdt == QW_BF16) ||
+         (gateup->wf == QW_WFMT_INT8_ROWSCALE && (xdt == QW_F16 || xdt == QW_BF16))) &&
+        valid_act(ydt) && (!residual || valid_act(residual_dtype)) && down->wf == gateup->wf &&
+        gateup->ksteps <= qwk::mlp_fused_max_ksteps(wfi, false) && qwk::mlp_counter_words() <= kMlpCounterWords &&
+        down->ksteps <= qwk::mlp_fused_max_ksteps(wfi, true) &&
+        aligned(x, 16) && (H * dsize(xdt)) % 16 == 0 && (!gamma || aligned(gamma, 16))) {
         if (norm && !(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
         qwk::MlpArgs p{};
         qwk::SkinnyArgs& u = p.up;
@@ -1072,10 +1078,11 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         d.y = y; d.ydt = ydt; d.ldy = H;
         d.vec_store = (H % 4 == 0) && aligned(y, 16) && (!residual || aligned(residual, 16));
         p.ctl = ctx->mlp_ctl;
+        p.cnt = ctx->counters + kMaxCounters;
+
         p.n_up = u.n_groups;
         p.n_down = d.n_groups;
-        const int grid = std::min(p.n_up + p.n_down, ctx->num_cus * 2);
-        hipError_t e = qwk::launch_mlp_fused(p, gateup->wf, (int)xdt, grid, stream);
+        hipError_t e = qwk::launch_mlp_fused(p, wfi, (int)xdt, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "fused MLP launch");
         return QW_OK;
     }

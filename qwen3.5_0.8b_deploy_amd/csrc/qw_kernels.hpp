@@ -95,12 +95,16 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax
 struct MlpArgs {
     SkinnyArgs up;
     SkinnyArgs down;
-    unsigned* ctl;   // [0] ticket, [1] up tiles done, [2] workgroups exited, [3] error flag
+    unsigned* ctl;   // [3]: error flag (a wait that expired)
+    unsigned* cnt;   // completion / exit counter slots, zero between launches (mlp_counter_words())
     int n_up;
     int n_down;
 };
-size_t mlp_fused_lds_bytes(int wf, int xdt, int M, int H, int I);
-hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, int grid, hipStream_t stream);
+// largest k-step count per projection the one-launch MLP holds in registers
+// (0: weight format not supported)
+int mlp_fused_max_ksteps(int wf, bool down);
+int mlp_counter_words();
+hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t stream);
 
 // Gated-DeltaNet decode step (qw_gdn.hip): one token of each of B sequences.
 struct GdnArgs {

@@ -317,4 +317,88 @@ __device__ __forceinline__ void issue_weights(const SkinnyArgs& a, __amdgpu_buff
                            (uint32_t)(grp * RT + rt) * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
 }
 
+// ---------------------------------------------------------------------------
+// register-direct activation operands (qw_gemv.hip, qw_mlp.hip)
+// ---------------------------------------------------------------------------
+// Activation fragments of one k-step as loaded: KE elements of XDT for each
+// of the CT token tiles of the lane, and the matching (1 + gamma) weights
+// (shared by the tiles).
+template <int WF, int XDT, int CT> struct XFrag {
+    static constexpr int KE = WTraits<WF>::KE;
+    static constexpr int N16 = KE * 2 / 16;  // 16-byte loads per lane and tile (XDT is 16-bit)
+    u32x4 v[CT][N16];
+    f32x4 gam[KE / 4];
+};
+
+template <int WF, int XDT, int CT, bool GAM>
+__device__ __forceinline__ void load_xfrag(__amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t gr, const uint32_t (&xoff)[CT],
+                                           uint32_t goff, XFrag<WF, XDT, CT>& f) {
+    constexpr int KE = WTraits<WF>::KE;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int h = 0; h < XFrag<WF, XDT, CT>::N16; ++h)
+            f.v[ct][h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xoff[ct] + 16 * h, 0, 0));
+    if constexpr (GAM) {
+#pragma unroll
+        for (int h = 0; h < KE / 4; ++h)
+            f.gam[h] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, goff + 16 * h, 0, 0));
+    }
+}
+
+// B operand of one token tile from a loaded fragment.  NORM: accumulate the
+// squares; GAM: multiply by (1 + gamma) (without GAM the weight carries the
+// norm weight and the activation bits pass through).
+template <int WF, int XDT, int CT, bool NORM, bool GAM>
+__device__ __forceinline__ BOps<WF, XDT> make_bops(const XFrag<WF, XDT, CT>& f, int ct, float& ss) {
+    constexpr int KE = WTraits<WF>::KE;
+    BOps<WF, XDT> b;
+    constexpr bool SAME = (WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16);
+    constexpr bool RAW = !GAM && SAME;
+    if constexpr (NORM && RAW) {
+#pragma unroll
+        for (int p = 0; p < KE / 2; ++p) {
+            const uint32_t w = f.v[ct][p >> 2][p & 3];
+            const float e0 = XDT == DT_BF16 ? bf16_bits_to_f32(w & 0xffffu) : f16_bits_to_f32(w & 0xffffu);
+            const float e1 = XDT == DT_BF16 ? bf16_bits_to_f32(w >> 16) : f16_bits_to_f32(w >> 16);
+            ss += e0 * e0 + e1 * e1;
+        }
+    }
+    if constexpr (RAW) {
+        if constexpr (WF == WF_BF16) {
+            b.hi = __builtin_bit_cast(bf16x8, f.v[ct][0]);
+        } else {
+            b.hi0 = __builtin_bit_cast(f16x8, f.v[ct][0]);
+            b.hi1 = __builtin_bit_cast(f16x8, f.v[ct][1]);
+        }
+    } else {
+        uint32_t out[KE / 2];
+#pragma unroll
+        for (int p = 0; p < KE / 2; ++p) {
+            const uint32_t w = f.v[ct][p >> 2][p & 3];
+            float e0, e1;
+            if constexpr (XDT == DT_BF16) {
+                e0 = bf16_bits_to_f32(w & 0xffffu);
+                e1 = bf16_bits_to_f32(w >> 16);
+            } else {
+                e0 = f16_bits_to_f32(w & 0xffffu);
+                e1 = f16_bits_to_f32(w >> 16);
+            }
+            if constexpr (NORM) ss += e0 * e0 + e1 * e1;
+            if constexpr (GAM) {
+                e0 *= 1.0f + f.gam[(2 * p) >> 2][(2 * p) & 3];
+                e1 *= 1.0f + f.gam[(2 * p + 1) >> 2][(2 * p + 1) & 3];
+            }
+            out[p] = op_bits<WF>(e0) | (op_bits<WF>(e1) << 16);
+        }
+        if constexpr (WF == WF_BF16) {
+            b.hi = __builtin_bit_cast(bf16x8, u32x4{out[0], out[1], out[2], out[3]});
+        } else {
+            b.hi0 = __builtin_bit_cast(f16x8, u32x4{out[0], out[1], out[2], out[3]});
+            b.hi1 = __builtin_bit_cast(f16x8, u32x4{out[4], out[5], out[6], out[7]});
+        }
+    }
+    return b;
+}
+
 }  // namespace qwk
