@@ -362,15 +362,14 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         xa = randn(M, H, dtype=torch.float16)
         att = randn(M, 2048, dtype=torch.float16)            # attention-core stand-in
         big = torch.empty(M, 8192, device="cuda", dtype=torch.float16)
-        hmid = torch.empty(M, I, device="cuda", dtype=torch.float16)
         res = randn(M, H, dtype=torch.float16)
 
         def body():
             for L in layers:
                 qw.linear(ctx, L["in"], xa, big[:, :L["n_in"]])
                 qw.linear(ctx, L["out"], att, res, residual=res)
-                qw.linear(ctx, L["gu"], xa, hmid)
-                qw.linear(ctx, L["down"], hmid, res, residual=res)
+                # the MLP block: one launch at M <= 16, else gate/up then down
+                qw.mlp_fused(ctx, L["gu"], L["down"], xa, res, residual=res)
         g = graphed(qw, ctx, stream, body)
         ms = timer.run(g.launch, steps, 2)
         act = 0

@@ -26,7 +26,8 @@ struct qw_ctx {
     int min_items = 0;       // split K until a launch has this many items (0: never)
     int force_nw = 0;        // waves per skinny workgroup (0: automatic)
     int force_nw_glu = 0;    // same, GLU weights only
-    bool mlp_fused = true;   // one-launch MLP block at decode sizes (QW_MLP_FUSED=0: two launches)
+    int mlp_fused = -1;      // one-launch MLP block at decode sizes: -1 auto (BF16 weights, where it
+                             // measured faster), 1 also INT8 (QW_MLP_FUSED=1), 0 never (QW_MLP_FUSED=0)
     bool gemv = true;        // register-direct GEMV for M <= 32 (QW_GEMV=0: skinny kernel)
     int gemm_min_m = kGemmMinM;  // tokens from which BF16 calls may use the MFMA GEMM
     bool gemm_forced = false;    // QW_GEMM_MIN_M given: GEMM from gemm_min_m tokens on, always
@@ -168,7 +169,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     auto nw_of = [](const char* v) { const int n = atoi(v); return (n == 4 || n == 8 || n == 16) ? n : 0; };
     if (const char* v = getenv("QW_SKINNY_NW")) c->force_nw = nw_of(v);
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
-    if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0;
+    if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0 ? 1 : 0;
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
@@ -1054,12 +1055,13 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
     const size_t per_tok = (size_t)I * dsize(hdt);
     int chunk = (int)std::min<size_t>((size_t)M, ctx->scratch_bytes / per_tok);
     if (chunk < 1) return fail(ctx, QW_ERR_WORKSPACE, "workspace too small for one token of the MLP");
-    // decode: the whole block in one launch (16-bit activations, BF16 or
-    // INT8 weights, up to 16 tokens, Qwen-sized projections)
+    // decode: the whole block in one launch (BF16 or INT8 weights, up to 16
+    // tokens of 16-bit activations or 4 of FP32, Qwen-sized projections)
     const int wfi = (int)gateup->wf;
-    if (ctx->mlp_fused && M <= 16 && (size_t)M * per_tok <= ctx->scratch_bytes &&
-        ((gateup->wf == QW_WFMT_BF16 && xdt == QW_BF16) ||
-         (gateup->wf == QW_WFMT_INT8_ROWSCALE && (xdt == QW_F16 || xdt == QW_BF16))) &&
+    const bool one_launch = ctx->mlp_fused > 0 || (ctx->mlp_fused < 0 && gateup->wf == QW_WFMT_BF16);
+    if (one_launch && M <= qwk::mlp_fused_max_m((int)xdt) && (size_t)M * per_tok <= ctx->scratch_bytes &&
+        ((gateup->wf == QW_WFMT_BF16 && (xdt == QW_BF16 || xdt == QW_F32)) ||
+         (gateup->wf == QW_WFMT_INT8_ROWSCALE && (xdt == QW_F16 || xdt == QW_BF16 || xdt == QW_F32))) &&
         valid_act(ydt) && (!residual || valid_act(residual_dtype)) && down->wf == gateup->wf &&
         gateup->ksteps <= qwk::mlp_fused_max_ksteps(wfi, false) && qwk::mlp_counter_words() <= kMlpCounterWords &&
         down->ksteps <= qwk::mlp_fused_max_ksteps(wfi, true) &&

@@ -104,6 +104,7 @@ struct MlpArgs {
 // (0: weight format not supported)
 int mlp_fused_max_ksteps(int wf, bool down);
 int mlp_counter_words();
+int mlp_fused_max_m(int xdt);  // tokens the one-launch MLP takes for activations of this dtype
 hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t stream);
 
 // Gated-DeltaNet decode step (qw_gdn.hip): one token of each of B sequences.

@@ -53,6 +53,12 @@ constexpr int MLP_NWD = MLP_NW / MLP_DG;
 // top counter, each on its own 256-byte line, so that no single address
 // takes hundreds of atomics at once (they serialize at the coherence point).
 constexpr int MLP_SLOTS = 32, MLP_EXIT_SLOTS = 8, MLP_SLOT_STRIDE = 64;
+// FP32 activations (the engine's residual stream) are staged into LDS as
+// hi + lo planes of the MFMA input type, for up to this many tokens
+constexpr int MLP_F32_MAX_M = 4, MLP_MAX_K = 1024;
+constexpr int MLP_F32_LDS = (MLP_F32_MAX_M + 1) * (MLP_MAX_K + 8) * 2 * 2;
+
+int mlp_fused_max_m(int xdt) { return xdt == DT_F32 ? MLP_F32_MAX_M : 16; }
 
 // k-steps per wave: gate/up (K = H, 16 waves) and down (K = I, 8 waves per
 // tile) at the Qwen3.5-0.8B shape (H = 1024, I = 3584); smaller shapes
@@ -114,7 +120,8 @@ __device__ __forceinline__ void reduce_runs(f32x4 (&red)[NW][2][64], float (&red
     }
 }
 
-// WF: weight format (gate/up and down share it); XDT: 16-bit dtype of x.
+// WF: weight format (gate/up and down share it); XDT: dtype of x (16-bit
+// read straight into registers, FP32 staged through LDS).
 // The intermediate h is held in the MFMA input type of WF (BF16, or F16 for
 // INT8 weights), which is what the down projection consumes.
 template <int WF, int XDT, bool NORM, bool GAM>
@@ -126,6 +133,9 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
     constexpr int HDT = WF == WF_BF16 ? DT_BF16 : DT_F16;
     __shared__ f32x4 red[NW][2][64];
     __shared__ float red_ss[NW][16];
+    __shared__ __attribute__((aligned(16))) uint8_t xs_f32[XDT == DT_F32 ? MLP_F32_LDS : 16];
+    __shared__ float ss_tok[16];
+    __shared__ float ss_scratch[XDT == DT_F32 ? MLP_NW * 16 : 1];
 
     const int lane = threadIdx.x & 63;
     const int wave_id = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -140,40 +150,77 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
         wave_range<NW>(0, a.ksteps, wave_id, kb, kend);
         const int n = kend - kb;
         const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_groups * 2 * a.ksteps * 1024u));
-        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
         const __amdgpu_buffer_rsrc_t gr = make_rsrc(GAM ? (const void*)a.gamma : a.x, GAM ? (uint32_t)a.K * 4u : 0u);
         const __amdgpu_buffer_rsrc_t sr =
             make_rsrc(a.scales ? (const void*)a.scales : a.x, a.scales ? (uint32_t)a.n_groups * 2 * 64u : 0u);
-        const uint32_t xrow = r < a.M ? (uint32_t)(r * a.ldx + g * KE) * 2u : OOB;
-        const uint32_t grow = r < a.M ? (uint32_t)(g * KE) * 4u : OOB;
-        // activations (small, needed first), then the weights, then the scales
-        XFrag<WF, XDT, 1> X[UA];
-#pragma unroll
-        for (int u = 0; u < UA; ++u) {
-            const uint32_t ko = (uint32_t)(kb + u) * 4u * KE;
-            const uint32_t xo[1] = {u < n ? xrow + ko * 2u : OOB};
-            load_xfrag<WF, XDT, 1, GAM>(xr, gr, xo, u < n ? grow + ko * 4u : OOB, X[u]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        u32x4 A[UA][2];
-        issue_weights<2, UA>(a, wrs, grp, kb, n, lane, A);
-        u32x4 sc[2];  // per-row scales (INT8 weights only)
-        if constexpr (WF == WF_I8) {
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-                sc[rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       sr, (uint32_t)(((grp * 2 + rt) * 16 + g * 4) * 4), 0, 0));
-        }
-        __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first wait
         f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
         float ss = 0.0f;
+        u32x4 sc[2];  // per-row scales (INT8 weights only)
+        u32x4 A[UA][2];
+        auto issue_rest = [&]() {
+            issue_weights<2, UA>(a, wrs, grp, kb, n, lane, A);
+            if constexpr (WF == WF_I8) {
 #pragma unroll
-        for (int u = 0; u < UA; ++u) {
-            const BOps<WF, XDT> b = make_bops<WF, XDT, 1, NORM, GAM>(X[u], 0, ss);
+                for (int rt = 0; rt < 2; ++rt)
+                    sc[rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                           sr, (uint32_t)(((grp * 2 + rt) * 16 + g * 4) * 4), 0, 0));
+            }
+        };
+        if constexpr (XDT == DT_F32) {
+            // x (times 1 + gamma) staged into LDS as hi + lo planes; the weight
+            // loads are issued between the staging's loads and its LDS writes
+            const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 4u));
+            const int kr = a.K;
+            auto stage = [&](auto sq_tag) {
+                constexpr int SQ = decltype(sq_tag)::value;
+                XStage<XDT, SQ> st;
+                stage_issue<WF, XDT, NW, SQ, NORM>(a, xr, gr, 0, kr, st);
+                __builtin_amdgcn_sched_barrier(0);
+                issue_rest();
+                __builtin_amdgcn_sched_barrier(0);
+                stage_finish<WF, XDT, 1, NW, SQ, NORM>(a, xr, gr, 0, kr, st, xs_f32, ss_tok, ss_scratch);
+            };
+            const int rp = 1 << (32 - __builtin_clz((unsigned)a.M));
+            const int cpt = ((kr / 8) * rp + NW * 64 - 1) / (NW * 64);
+            if (cpt <= 1) stage(std::integral_constant<int, 1>{});
+            else stage(std::integral_constant<int, 2>{});
+            __syncthreads();
+            constexpr int OS = OpSize<WF>::v;
+            const int ls = lds_row_elems<WF>(kr);
+            const int plane_bytes = (a.M + 1) * ls * OS;
+            const int xrow = min(r, a.M);  // row M of the staging is zero
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) acc[rt] = unit_mfma<WF, XDT>(A[u][rt], b, acc[rt]);
+            for (int u = 0; u < UA; ++u) {
+                BOps<WF, XDT> b;
+                const int relk = (kb + u) * 4 * KE + g * KE;
+                read_bops<WF, XDT>(b, xs_f32 + ((int64_t)xrow * ls + relk) * OS, plane_bytes);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) acc[rt] = unit_mfma<WF, XDT>(A[u][rt], b, acc[rt]);
+            }
+            if (NORM && r < 16) ss = ss_tok[r];
+        } else {
+            const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
+            const uint32_t xrow = r < a.M ? (uint32_t)(r * a.ldx + g * KE) * 2u : OOB;
+            const uint32_t grow = r < a.M ? (uint32_t)(g * KE) * 4u : OOB;
+            // activations (small, needed first), then the weights, then the scales
+            XFrag<WF, XDT, 1> X[UA];
+#pragma unroll
+            for (int u = 0; u < UA; ++u) {
+                const uint32_t ko = (uint32_t)(kb + u) * 4u * KE;
+                const uint32_t xo[1] = {u < n ? xrow + ko * 2u : OOB};
+                load_xfrag<WF, XDT, 1, GAM>(xr, gr, xo, u < n ? grow + ko * 4u : OOB, X[u]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            issue_rest();
+            __builtin_amdgcn_sched_barrier(0);  // every load is in flight before the first wait
+#pragma unroll
+            for (int u = 0; u < UA; ++u) {
+                const BOps<WF, XDT> b = make_bops<WF, XDT, 1, NORM, GAM>(X[u], 0, ss);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) acc[rt] = unit_mfma<WF, XDT>(A[u][rt], b, acc[rt]);
+            }
         }
-        reduce_runs<NW, NW, 2, NORM>(red, red_ss, acc, ss, wave_id, lane);
+        reduce_runs<NW, NW, 2, NORM && XDT != DT_F32>(red, red_ss, acc, ss, wave_id, lane);
         if (wave_id == 0) {
             const float inv = NORM ? 1.0f / sqrtf(ss / (float)a.K + a.eps) : 1.0f;
             f32x4 gt = acc[0] * inv, up = acc[1] * inv;
@@ -313,7 +360,7 @@ static hipError_t launch_mlp2(const MlpArgs& p, bool norm, bool gam, hipStream_t
 }
 
 hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t stream) {
-    if (p.up.M < 1 || p.up.M > 16) return hipErrorInvalidValue;
+    if (p.up.M < 1 || p.up.M > mlp_fused_max_m(xdt) || p.up.K > MLP_MAX_K) return hipErrorInvalidValue;
     if (p.up.ksteps > mlp_fused_max_ksteps(wf, false) || p.down.ksteps > mlp_fused_max_ksteps(wf, true))
         return hipErrorInvalidValue;
     const bool norm = (p.up.flags & EP_NORM) != 0;
@@ -321,6 +368,8 @@ hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t strea
     if (wf == WF_BF16 && xdt == DT_BF16) return launch_mlp2<WF_BF16, DT_BF16>(p, norm, gam, stream);
     if (wf == WF_I8 && xdt == DT_F16) return launch_mlp2<WF_I8, DT_F16>(p, norm, gam, stream);
     if (wf == WF_I8 && xdt == DT_BF16) return launch_mlp2<WF_I8, DT_BF16>(p, norm, gam, stream);
+    if (wf == WF_BF16 && xdt == DT_F32) return launch_mlp2<WF_BF16, DT_F32>(p, norm, gam, stream);
+    if (wf == WF_I8 && xdt == DT_F32) return launch_mlp2<WF_I8, DT_F32>(p, norm, gam, stream);
     return hipErrorInvalidValue;
 }
 

@@ -231,10 +231,13 @@ def test_silu_mul(qw, ctx, oracle, relerr):
     assert relerr(host(h), ref) <= 1e-6
 
 
-@pytest.mark.parametrize("fmt,M", [("bf16", 1), ("bf16", 8), ("int8", 1), ("int8", 16), ("f32", 2)])
+@pytest.mark.parametrize("fmt,M", [("bf16", 1), ("bf16", 8), ("int8", 1), ("int8", 16), ("f32", 2),
+                                   ("bf16x32", 1), ("bf16x32", 4), ("int8x32", 3)])
 def test_mlp_one_launch_path(qw, oracle, relerr, fmt, M):
-    """The single-launch MLP kernel (enabled with QW_MLP_FUSED=1 at context
-    creation) against the oracle, repeated to check its counters reset."""
+    """The single-launch MLP kernel (the decode default; QW_MLP_FUSED=1 set
+    explicitly) against the oracle, repeated to check its counters reset.
+    bf16x32 / int8x32: FP32 activations (staged through LDS as hi + lo),
+    the engine's residual stream; f32: FP32 weights (two-launch path)."""
     import os
     os.environ["QW_MLP_FUSED"] = "1"
     try:
@@ -242,8 +245,10 @@ def test_mlp_one_launch_path(qw, oracle, relerr, fmt, M):
     finally:
         del os.environ["QW_MLP_FUSED"]
     H, I = 1024, 3584
-    f = {"bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8, "f32": qw.WFMT_F32}[fmt]
-    xdt = {"bf16": torch.bfloat16, "int8": torch.float16, "f32": torch.float32}[fmt]
+    f = {"bf16": qw.WFMT_BF16, "int8": qw.WFMT_INT8, "f32": qw.WFMT_F32,
+         "bf16x32": qw.WFMT_BF16, "int8x32": qw.WFMT_INT8}[fmt]
+    xdt = {"bf16": torch.bfloat16, "int8": torch.float16, "f32": torch.float32,
+           "bf16x32": torch.float32, "int8x32": torch.float32}[fmt]
     G, U, D = _mlp_weights(oracle, H, I, 441)
     gamma = oracle.normal((H,), 444, 0.0, 0.02)
     x = oracle.normal((M, H), 445)
@@ -257,7 +262,7 @@ def test_mlp_one_launch_path(qw, oracle, relerr, fmt, M):
     assert c.device_error() == 0
     assert all(torch.equal(ys[0], y) for y in ys[1:])
     xs = host(xt)
-    if fmt == "int8":
+    if fmt in ("int8", "int8x32"):
         qgu, sgu = gu.unpack()
         qd, sd = dn.unpack()
         Gd = qgu[:I].astype(np.float32) * sgu[:I, None]
@@ -265,7 +270,7 @@ def test_mlp_one_launch_path(qw, oracle, relerr, fmt, M):
         Dd = qd.astype(np.float32) * sd[:, None]
         ref = oracle.mlp_block(Gd, Ud, Dd, gamma, xs)
         bar = 1e-3
-    elif fmt == "bf16":
+    elif fmt in ("bf16", "bf16x32"):
         ref = oracle.mlp_block_f64(G, U, D, gamma, xs)
         bar = 1e-2
     else:
