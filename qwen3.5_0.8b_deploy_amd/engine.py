@@ -29,6 +29,7 @@ CD = LNH * (2 * KD + VD)                    # conv dim 6144
 LIN_IN = CD + LNH * VD + 2 * LNH            # stacked [qkv | z | a | b] = 8224
 FNH, FNKV, HD = 8, 2, 256                   # full attention
 FULL_IN = FNH * 2 * HD + 2 * FNKV * HD      # stacked [q|gate interleaved | k | v] = 5120
+NORM_FIRST_MIN_BATCH = 12                   # above this many sequences, RMSNorm once into BF16
 
 
 def is_linear_layer(i):
@@ -45,13 +46,24 @@ class DecodeEngine:
     q_norm, k_norm, o.  embed: [vocab][H] (F32 or BF16, the tied lm_head)."""
 
     def __init__(self, qw, ctx, layers, final_norm, embed, batch, capacity, fmt=None, lm_fmt=None,
-                 kv_int8=True):
+                 kv_int8=True, norm_first=None):
         import torch
         self.qw, self.ctx, self.B = qw, ctx, batch
         fmt = qw.WFMT_BF16 if fmt is None else fmt
         lm_fmt = qw.WFMT_BF16 if lm_fmt is None else lm_fmt
         dev = "cuda"
         self.act = torch.float32 if fmt == qw.WFMT_F32 else torch.bfloat16
+        # Where the layer input is RMSNorm-ed: inside the projection (its
+        # prologue stages the FP32 residual stream per workgroup), or once into
+        # a BF16 buffer that the register-direct GEMV reads.  The prologue wins
+        # for few sequences (one launch fewer: ~4.4 us each in the step graph);
+        # with many, every workgroup re-staging x (M x 4 KB) costs more than
+        # the extra launch.  Measured whole-step crossover between 8 and 16
+        # sequences (B=8: 1.108 vs 1.206 ms, B=16: 1.487 vs 1.449 ms, B=32:
+        # 2.57 vs 1.85 ms).  BF16 weights only: FP32 weights keep FP32 x.
+        if norm_first is None:
+            norm_first = self.act == torch.bfloat16 and batch > NORM_FIRST_MIN_BATCH
+        self.norm_first = bool(norm_first)
         self.layers = []
         for i, L in enumerate(layers):
             P = {"linear": is_linear_layer(i), "in_norm": L["in_norm"], "post_norm": L["post_norm"]}
@@ -76,6 +88,7 @@ class DecodeEngine:
         self.capacity = capacity
         self.x = torch.zeros(batch, H, device=dev)
         self.xn = torch.zeros(batch, H, device=dev)
+        self.xh = torch.zeros(batch, H, device=dev, dtype=torch.bfloat16)  # RMSNorm-ed x (norm_first)
         self.row = torch.zeros(batch, max(LIN_IN, FULL_IN), device=dev)
         self.core = torch.zeros(batch, LNH * VD, device=dev, dtype=self.act)
         self.ids = torch.zeros(batch, dtype=torch.int32, device=dev)
@@ -94,6 +107,15 @@ class DecodeEngine:
                 for c in P["cache"]:
                     c.zero_()
 
+    def _project_in(self, P, r, stream):
+        """The layer's stacked input projection of RMSNorm(x) * (1 + in_norm)."""
+        qw, ctx = self.qw, self.ctx
+        if self.norm_first:
+            qw.rmsnorm(ctx, self.x, P["in_norm"], self.xh, stream=stream)
+            qw.linear(ctx, P["in"], self.xh, r, stream=stream)
+        else:
+            qw.linear(ctx, P["in"], self.x, r, gamma=P["in_norm"], stream=stream)
+
     def step(self, stream=None):
         """One greedy token for every sequence: ids <- next ids, positions += 1."""
         qw, ctx, x, row = self.qw, self.ctx, self.x, self.row
@@ -101,19 +123,23 @@ class DecodeEngine:
         for P in self.layers:
             if P["linear"]:
                 r = row[:, :LIN_IN]
-                qw.linear(ctx, P["in"], x, r, gamma=P["in_norm"], stream=stream)
+                self._project_in(P, r, stream)
                 qw.gdn_decode(ctx, P["conv"], P["A_log"], P["dt_bias"], P["norm_w"], r[:, :CD],
                               r[:, CD:CD + LNH * VD], r[:, CD + LNH * VD:CD + LNH * VD + LNH],
                               r[:, CD + LNH * VD + LNH:], P["cs"], P["rs"], self.core, LNH, ld_in=row.stride(0),
                               stream=stream)
             else:
                 r = row[:, :FULL_IN]
-                qw.linear(ctx, P["in"], x, r, gamma=P["in_norm"], stream=stream)
+                self._project_in(P, r, stream)
                 qw.attn_forward(ctx, P["q_norm"], P["k_norm"], P["cache"], self.pos, r[:, 0:], r[:, HD:],
                                 r[:, FNH * 2 * HD:], r[:, FNH * 2 * HD + FNKV * HD:], self.core, tokens=1,
                                 q_head_stride=2 * HD, ld_in=row.stride(0), max_len=self.capacity, stream=stream)
             qw.linear(ctx, P["out"], self.core, x, residual=x, stream=stream)
-            qw.mlp_fused(ctx, P["gateup"], P["down"], x, x, gamma=P["post_norm"], residual=x, stream=stream)
+            if self.norm_first:
+                qw.rmsnorm(ctx, x, P["post_norm"], self.xh, stream=stream)
+                qw.mlp_fused(ctx, P["gateup"], P["down"], self.xh, x, residual=x, stream=stream)
+            else:
+                qw.mlp_fused(ctx, P["gateup"], P["down"], x, x, gamma=P["post_norm"], residual=x, stream=stream)
         qw.rmsnorm(ctx, x, self.final_norm, self.xn, stream=stream)
         qw.lmhead_argmax(ctx, self.E, self.xn, self.ids, stream=stream)
         qw.positions_add(ctx, self.pos, 1, stream=stream)

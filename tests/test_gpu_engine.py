@@ -165,3 +165,37 @@ def test_engine_eager_equals_graph(qw, ctx, oracle):
             g.launch(stream)
             stream.synchronize()
             assert torch.equal(e1.ids, e2.ids) and torch.equal(e1.x, e2.x)
+
+
+def test_engine_norm_first_matches_prologue(qw, ctx, oracle, relerr):
+    """BF16 engine: RMSNorm once into a BF16 buffer (the path for more than 12
+    sequences) against the projections' own RMSNorm prologue on the FP32
+    residual stream (the few-sequence path), same weights and tokens.  The
+    only difference is x rounded to BF16 before the projections (the
+    prologue keeps it as a BF16 hi + lo pair), so the hidden states agree to
+    the BF16 bar (1e-2) and the greedy ids agree wherever the two engines
+    saw the same history."""
+    em = _engine_mod()
+    B, V = 6, 1024
+    layers = make_layers(oracle, 4, 5000)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    tl = [{k: dev(v) for k, v in L.items()} for L in layers]
+    fn, emb = dev(oracle.normal((em.H,), 5999, 0.0, 0.1)), dev(oracle.normal((V, em.H), 5998)).bfloat16()
+    e1 = em.DecodeEngine(qw, ctx, tl, fn, emb, B, 8, norm_first=True)
+    e2 = em.DecodeEngine(qw, ctx, tl, fn, emb, B, 8, norm_first=False)
+    assert e1.norm_first and not e2.norm_first
+    start = [3, 4, 100, 511, 7, 1000]
+    e1.reset(start)
+    e2.reset(start)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        e1.step(stream=stream)
+        e2.step(stream=stream)
+        stream.synchronize()
+    assert ctx.device_error() == 0
+    x1, x2 = e1.x.cpu().numpy(), e2.x.cpu().numpy()
+    for b in range(B):
+        assert relerr(x1[b], x2[b].astype(np.float64)) <= 1e-2, (b, relerr(x1[b], x2[b].astype(np.float64)))
+    # the automatic choice: norm-first only for BF16 weights above 12 sequences
+    assert em.DecodeEngine(qw, ctx, tl, fn, emb, 13, 8).norm_first
+    assert not em.DecodeEngine(qw, ctx, tl, fn, emb, 12, 8).norm_first
