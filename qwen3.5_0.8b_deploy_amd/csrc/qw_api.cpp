@@ -35,6 +35,7 @@ struct qw_ctx {
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
+    bool attn_fused = true;      // one-launch INT8 decode attention (QW_ATTN_FUSED=0: prep / split / combine)
     int attn_prefill_min = 16;   // tokens per sequence from which the query-block attention kernel runs (QW_ATTN_PREFILL_MIN)  // tokens per sequence from which the chunked GDN form runs (QW_GDN_CHUNK_MIN)
     uint8_t* ws = nullptr;
     size_t ws_bytes = 0;
@@ -174,6 +175,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
+    if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
     if (const char* v = getenv("QW_ATTN_PREFILL_MIN")) c->attn_prefill_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GDN_CHUNK_MIN")) c->gdn_chunk_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
@@ -999,6 +1001,18 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
     if (seg < 1) return fail(ctx, QW_ERR_WORKSPACE, "attn: workspace too small for one row");
     a.split = split;
     a.nsplit = nsplit;
+    // one new token per sequence over an INT8 cache: one launch per segment
+    // (q/k/v preparation and the split merge inside the attention kernel)
+    // when the launch is small (at most 16 splits: one wave merges a head's
+    // splits with device-coherent loads, which at hundreds of splits costs
+    // more than the two launches; at most one workgroup per CU: with more,
+    // every workgroup redoing its q heads and the hand-off cost more than the
+    // launches save -- measured B=1 context 512: 21.3 vs 23.3 us, B=32
+    // context 4096: 100.7 vs 96.2 us)
+    a.cnt = (tokens == 1 && ctx->attn_fused && (int)cache->dtype == (int)QW_I8 && nsplit <= 16 &&
+             seg * nkv * nsplit <= ctx->num_cus && seg * nkv <= kMaxCounters)
+                ? ctx->counters
+                : nullptr;
     // rows in order, so every row finds the keys of the rows before it in the cache
     for (int64_t r0 = 0; r0 < rows_all; r0 += seg) {
         a.row0 = (int)r0;

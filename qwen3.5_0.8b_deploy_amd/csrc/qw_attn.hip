@@ -298,6 +298,64 @@ __global__ __launch_bounds__(256) void attn_split(AttnArgs a) {
 // splits, else 4).  The split maxima are reduced over all threads; each wave
 // then sums the partial outputs of every NW-th split, eight splits' loads in
 // flight; the wave sums are merged in LDS.
+// Merge of ns split partials (o, max, sum) of one (row, head) by one wave,
+// in a fixed order; COH: device-coherent loads (partials written by other
+// workgroups of the same launch).  Returns the unnormalized o and the sum.
+template <bool COH>
+__device__ __forceinline__ float part_ld(const float* p) {
+    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+
+template <int HD, bool COH>
+__device__ __forceinline__ void merge_splits_wave(const float* pp, int ns, int lane, float (&o)[HD / 64], float& l) {
+    constexpr int E = HD / 64;
+    float M = -INFINITY;
+    for (int s = lane; s < ns; s += 64) M = fmaxf(M, part_ld<COH>(pp + s * (HD + 2) + HD));
+    M = wave_max(M);
+    l = 0.0f;
+    for (int s = lane; s < ns; s += 64)
+        l += __expf(part_ld<COH>(pp + s * (HD + 2) + HD) - M) * part_ld<COH>(pp + s * (HD + 2) + HD + 1);
+    l = wave_sum(l);
+#pragma unroll
+    for (int e = 0; e < E; ++e) o[e] = 0.0f;
+    int s = 0;
+    for (; s + 7 < ns; s += 8) {  // splits s .. s+7
+        float w[8], v[8][E];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            w[u] = part_ld<COH>(pp + (s + u) * (HD + 2) + HD);
+#pragma unroll
+            for (int e = 0; e < E; ++e) v[u][e] = part_ld<COH>(pp + (s + u) * (HD + 2) + lane * E + e);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float wu = __expf(w[u] - M);
+#pragma unroll
+            for (int e = 0; e < E; ++e) o[e] += wu * v[u][e];
+        }
+    }
+    for (; s < ns; ++s) {
+        const float wu = __expf(part_ld<COH>(pp + s * (HD + 2) + HD) - M);
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] += wu * part_ld<COH>(pp + s * (HD + 2) + lane * E + e);
+    }
+}
+
+// out = o / l * sigmoid(gate) for the E dims of this lane
+template <int HD>
+__device__ __forceinline__ void gate_store(const AttnArgs& a, int r, int h, int lane, const float (&o)[HD / 64], float inv) {
+    constexpr int E = HD / 64;
+    const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + lane * E;
+    const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float y = o[e] * inv * (1.0f / (1.0f + __expf(-at_load(a.gate, a.in_dt, gi + e))));
+        if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = y;
+        else store_act(a.out, a.out_dt, oi + e, y);
+    }
+}
+
 template <int HD, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
     constexpr int E = HD / 64;
@@ -310,6 +368,12 @@ __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
     const float* pp = a.part + ((int64_t)rl * a.nh + h) * a.nsplit * (HD + 2);
     __shared__ float red[2][NW];
     __shared__ __attribute__((aligned(16))) float osum[NW][HD];
+    if constexpr (NW == 1) {
+        float o[E], l;
+        merge_splits_wave<HD, false>(pp, ns, lane, o, l);
+        gate_store<HD>(a, r, h, lane, o, L > 0 ? 1.0f / l : 0.0f);
+        return;
+    }
     float M = -INFINITY;
     for (int s = threadIdx.x; s < ns; s += 64 * NW) M = fmaxf(M, pp[s * (HD + 2) + HD]);
     M = wave_max(M);
@@ -771,7 +835,20 @@ __global__ __launch_bounds__(256) void attn_prefill_i8h(AttnArgs a) {
 // at the end; a lone split writes the output, otherwise a partial.
 constexpr int AD_KT = 64;  // keys per tile
 
-template <int HD>
+// FUSED (one new token per sequence): the kernel also does the work of
+// attn_prep and attn_combine, saving two launches per decode step:
+//   * every workgroup normalizes and rotates its G query heads itself (one
+//     wave each) from the projection output;
+//   * the workgroup whose key range holds the new position P computes the
+//     new token's K and V of its KV head (norm, RoPE, INT8 codes and scale,
+//     as attn_prep), writes them to the cache for later steps, and puts the
+//     same codes and scales into its LDS tile in place of the cache's (so
+//     nothing in this launch reads the slot it writes);
+//   * the splits of a (row, KV head) hand their partials over with
+//     agent-scope stores and an arrival count; the last one to arrive merges
+//     them (merge_splits_wave, as attn_combine) and writes the gated output.
+// No workgroup waits for another, so the launch cannot stall.
+template <int HD, bool FUSED>
 __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
     constexpr int KB = HD / 16, DT = HD / 16, E = HD / 64;
     constexpr int KHP = HD + 8, VHP = AD_KT + 4;
@@ -786,7 +863,8 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
     const int G = a.nh / a.nkv;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
     if (k0 >= k1) {  // uniform over the workgroup
-        if (L == 0 && a.nsplit == 1 && wave < G) {
+        if (FUSED && L == 0 && s == 0 && g == 0 && threadIdx.x == 0) *a.err = 1u;
+        if (L == 0 && (a.nsplit == 1 || (FUSED && s == 0)) && wave < G) {
             const int64_t oi = (int64_t)r * a.ld_out + (int64_t)(g * G + wave) * HD + lane * E;
 #pragma unroll
             for (int e = 0; e < E; ++e) {
@@ -830,10 +908,87 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
             psc = (threadIdx.x < AD_KT ? a.ks : a.vs)[slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv];
         }
     };
+    // fused: q of the G heads (wave w: head g*G + w), and -- in the workgroup
+    // that holds position P -- the new K and V of head g, as attn_prep
+    const bool owner = FUSED && k1 == L;  // this split's range ends at P
+    __shared__ __attribute__((aligned(16))) float qs[FUSED ? 4 : 1][FUSED ? HD : 1];
+    __shared__ float rc[FUSED ? HD / 2 : 1], rs[FUSED ? HD / 2 : 1];
+    __shared__ int8_t newkv[FUSED ? 2 : 1][FUSED ? HD : 1];
+    __shared__ float newsc[2];
+    if constexpr (FUSED) {
+        // the first tile's loads go out before the q work: they do not depend
+        // on it (a stale slot P is replaced in LDS below), and the q loads
+        // then wait for the tile instead of the tile waiting for the q work
+        issue(k0);
+        if ((int)threadIdx.x < a.rot / 2) {
+            const float freq = 1.0f / powf(a.theta, (float)(2 * threadIdx.x) / (float)a.rot);
+            const float ang = (float)P * freq;
+            rc[threadIdx.x] = cosf(ang);
+            rs[threadIdx.x] = sinf(ang);
+        }
+        __syncthreads();
+        const int64_t row = (int64_t)r * a.ld_in;
+        // items: q head g*G + it for it < G; then (owner) it = G: k, G+1: v of head g
+        for (int it = wave; it < G + (owner ? 2 : 0); it += 4) {
+            const bool isq = it < G, isk = it == G;
+            const void* src = isq ? a.q : (isk ? a.k : a.v);
+            const int64_t base = row + (isq ? (int64_t)(g * G + it) * a.q_hs : (int64_t)g * HD) + lane * E;
+            float x[E];
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = at_load(src, a.in_dt, base + e);
+            if (it <= G) {  // q or k: RMSNorm (1 + w), then RoPE on d < rot
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < E; ++e) ss += x[e] * x[e];
+                ss = wave_sum(ss);
+                const float rms = sqrtf(ss / (float)HD + 1e-6f);
+                const float* w = isq ? a.qn_w : a.kn_w;
+#pragma unroll
+                for (int e = 0; e < E; ++e) x[e] = x[e] / rms * (1.0f + w[lane * E + e]);
+#pragma unroll
+                for (int e = 0; e < E; e += 2) {
+                    const int d = lane * E + e;
+                    if (d < a.rot) {
+                        const float c = rc[d / 2], sn = rs[d / 2];
+                        const float x0 = x[e], x1 = x[e + 1];
+                        x[e] = x0 * c - x1 * sn;
+                        x[e + 1] = x0 * sn + x1 * c;
+                    }
+                }
+            }
+            if (isq) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) qs[it][lane * E + e] = x[e];
+                continue;
+            }
+            // the new token's INT8 codes and scale (kv 0: K, 1: V)
+            const int kv = isk ? 0 : 1;
+            float m = 0.0f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) m = fmaxf(m, fabsf(x[e]));
+            m = wave_max(m);
+            float sc = m / 127.0f;
+            sc = sc > 1e-8f ? sc : 1.0f;
+            const int64_t slot = ((int64_t)b * a.cap + P) * a.nkv + g;
+            int8_t* cdst = reinterpret_cast<int8_t*>(isk ? a.kc : a.vc) + slot * HD + lane * E;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const int8_t c = (int8_t)fmaxf(-127.0f, fminf(127.0f, roundf(x[e] / sc)));
+                cdst[e] = c;
+                newkv[kv][lane * E + e] = c;
+            }
+            if (lane == 0) {
+                (isk ? a.ks : a.vs)[slot] = sc;
+                newsc[kv] = sc;
+            }
+        }
+        __syncthreads();
+    }
     // B operand: column li = query head g*G + li of this row (zero for li >= G)
     f16x4 qh[KB];
     {
-        const float* qp = a.qn + ((int64_t)rl * a.nh + g * G + min(li, G - 1)) * HD + 4 * lg;
+        const float* qp = FUSED ? &qs[min(li, G - 1)][4 * lg]
+                                : a.qn + ((int64_t)rl * a.nh + g * G + min(li, G - 1)) * HD + 4 * lg;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             const f32x4 v = li < G ? *reinterpret_cast<const f32x4*>(qp + 16 * kb) : f32x4{0, 0, 0, 0};
@@ -841,7 +996,7 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
             for (int q = 0; q < 4; ++q) qh[kb][q] = (_Float16)v[q];
         }
     }
-    issue(k0);  // after the q loads, so that waiting for q does not wait for the tile
+    if constexpr (!FUSED) issue(k0);  // after the q loads, so that waiting for q does not wait for the tile
     const float scale = 1.0f / sqrtf((float)HD);
     f32x4 acc[DT];
 #pragma unroll
@@ -871,6 +1026,15 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
         if (threadIdx.x < 2 * AD_KT) (threadIdx.x < AD_KT ? ksc : vsc)[threadIdx.x & (AD_KT - 1)] = psc;
         if (kt + AD_KT < k1) issue(kt + AD_KT);
         __syncthreads();
+        if (owner && P < kt + AD_KT) {  // the tile of position P: its K/V from this launch, not the cache
+            const int jp = P - kt;
+            for (int d = threadIdx.x; d < HD; d += 256) {
+                Kh[jp * KHP + d] = (_Float16)newkv[0][d];
+                VhT[d * VHP + jp] = (_Float16)newkv[1][d];
+            }
+            if (threadIdx.x < 2) (threadIdx.x == 0 ? ksc : vsc)[jp] = newsc[threadIdx.x];
+            __syncthreads();
+        }
         const int kw = 16 * wave;  // this wave's quarter of the tile
         if (kt + kw >= k1) continue;
         f32x4 sacc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -921,44 +1085,83 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
         for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(&ow[(wave * 4 + li) * HD + 16 * dt + 4 * lg]) = acc[dt];
     }
     __syncthreads();
-    if (wave >= G) return;
-    const int col = wave, h = g * G + col;  // wave w now finishes query head g*G + w
-    float M = -INFINITY;
+    // wave w < G finishes query head g*G + w: merge the four waves' columns
+    auto wave_merge = [&](float (&o)[E], float& M, float& lt) {
+        const int col = wave;
+        M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][col]);
-    float wsc[4], lt = 0.0f;
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w][col]);
+        float wsc[4];
+        lt = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        wsc[w] = wm[w][col] == -INFINITY ? 0.0f : __expf(wm[w][col] - M);
-        lt += wsc[w] * wl[w][col];
-    }
-    float o[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const int d = lane * E + e;
-        float v = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) v += wsc[w] * ow[(w * 4 + col) * HD + d];
-        o[e] = v;
-    }
-    if (a.nsplit == 1) {
-        const float inv = 1.0f / lt;
-        const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + lane * E;
-        const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
+        for (int w = 0; w < 4; ++w) {
+            wsc[w] = wm[w][col] == -INFINITY ? 0.0f : __expf(wm[w][col] - M);
+            lt += wsc[w] * wl[w][col];
+        }
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const float y = o[e] * inv * (1.0f / (1.0f + __expf(-at_load(a.gate, a.in_dt, gi + e))));
-            if (a.out_dt == DT_F32) reinterpret_cast<float*>(a.out)[oi + e] = y;
-            else store_act(a.out, a.out_dt, oi + e, y);
-        }
-        return;
-    }
-    float* dst = a.part + (((int64_t)rl * a.nh + h) * a.nsplit + s) * (HD + 2);
+            const int d = lane * E + e;
+            float v = 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) dst[lane * E + e] = o[e];
-    if (lane == 0) {
-        dst[HD] = M;
-        dst[HD + 1] = lt;
+            for (int w = 0; w < 4; ++w) v += wsc[w] * ow[(w * 4 + col) * HD + d];
+            o[e] = v;
+        }
+    };
+    const int h = g * G + wave;
+    if constexpr (!FUSED) {
+        if (wave >= G) return;
+        float o[E], M, lt;
+        wave_merge(o, M, lt);
+        if (a.nsplit == 1) {
+            gate_store<HD>(a, r, h, lane, o, 1.0f / lt);
+            return;
+        }
+        float* dst = a.part + (((int64_t)rl * a.nh + h) * a.nsplit + s) * (HD + 2);
+#pragma unroll
+        for (int e = 0; e < E; ++e) dst[lane * E + e] = o[e];
+        if (lane == 0) {
+            dst[HD] = M;
+            dst[HD + 1] = lt;
+        }
+    } else {
+        const int ns = (L + a.split - 1) / a.split;  // splits holding keys of this row
+        __shared__ unsigned last_s;
+        if (wave < G) {
+            float o[E], M, lt;
+            wave_merge(o, M, lt);
+            if (ns == 1) {
+                gate_store<HD>(a, r, h, lane, o, 1.0f / lt);
+            } else {
+                // hand-off: agent-scope stores of the partial
+                float* dst = a.part + (((int64_t)rl * a.nh + h) * a.nsplit + s) * (HD + 2);
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    __hip_atomic_store(dst + lane * E + e, o[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (lane == 0) {
+                    __hip_atomic_store(dst + HD, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(dst + HD + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        if (ns > 1) {  // uniform over the workgroup
+            // every wave waits for its stores' completion, then one arrival
+            // count per workgroup; the last split of (row, g) merges them all
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                unsigned* cnt = a.cnt + (int64_t)rl * a.nkv + g;
+                const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last_s = old == (unsigned)(ns - 1) ? 1u : 0u;
+                if (old == (unsigned)(ns - 1)) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (last_s && wave < G) {
+                const float* pp = a.part + ((int64_t)rl * a.nh + h) * a.nsplit * (HD + 2);
+                float om[E], l;
+                merge_splits_wave<HD, true>(pp, ns, lane, om, l);
+                gate_store<HD>(a, r, h, lane, om, 1.0f / l);
+            }
+        }
     }
 }
 
@@ -975,8 +1178,8 @@ static void launch_combine(const AttnArgs& a, hipStream_t stream) {
 
 template <int HD>
 static hipError_t launch_attn_hd(const AttnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_prep<HD>, dim3(a.rows), dim3(64 * std::min(16, a.nh + 2 * a.nkv)), 0, stream, a);
     if (a.prefill) {
+        hipLaunchKernelGGL(attn_prep<HD>, dim3(a.rows), dim3(64 * std::min(16, a.nh + 2 * a.nkv)), 0, stream, a);
         // INT8: query blocks x key splits (f16 MFMA), merged by attn_combine;
         // FP32: one workgroup per query block over all its keys (FP32 MFMA)
         if (a.kv_dt == DT_I8) {
@@ -988,7 +1191,12 @@ static hipError_t launch_attn_hd(const AttnArgs& a, hipStream_t stream) {
         }
         return hipGetLastError();
     }
-    if (a.kv_dt == DT_I8) hipLaunchKernelGGL(attn_decode_i8h<HD>, dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+    if (a.kv_dt == DT_I8 && a.T == 1 && a.cnt) {  // one launch: prep and combine inside
+        hipLaunchKernelGGL((attn_decode_i8h<HD, true>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(attn_prep<HD>, dim3(a.rows), dim3(64 * std::min(16, a.nh + 2 * a.nkv)), 0, stream, a);
+    if (a.kv_dt == DT_I8) hipLaunchKernelGGL((attn_decode_i8h<HD, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((attn_split<HD, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
     launch_combine<HD>(a, stream);
     return hipGetLastError();

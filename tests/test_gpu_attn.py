@@ -235,3 +235,38 @@ def test_attn_prefill_kernel_matches_split_path(qw, oracle, relerr, int8):
     assert relerr(outs[1], outs[0]) <= (5e-3 if int8 else 2e-5) and relerr(outs[2], outs[0]) <= 2e-5
     ref0, _ = oracle_stream(oracle, st, st.rows[0, :200], int8, 1.0e7, ROT, cap)
     assert relerr(outs[0][:200], ref0) <= (5e-3 if int8 else 2e-5)
+
+
+@pytest.mark.parametrize("io", ["f32", "bf16"])
+def test_attn_one_launch_decode_matches_three_launches(qw, oracle, io):
+    """One new token per sequence over an INT8 cache runs as one launch (the
+    attention kernel normalizes q, writes the new K/V and merges its splits
+    itself).  It computes exactly what the prep / split / combine launches
+    compute: the same outputs and the same cache contents, bit for bit, over
+    a prefill and 6 decode steps of 3 sequences at ragged positions -- short
+    rows (one split) and long rows (9 splits) in the same launches."""
+    B, cap = 3, 1200
+    starts = [5, 300, 1100]
+    st = Stream(oracle, B, max(starts) + 6, 900)
+    tdt = torch.float32 if io == "f32" else torch.bfloat16
+    res = []
+    for env in ({}, {"QW_ATTN_FUSED": "0"}):
+        c = _ctx_with(qw, env)
+        cache = qw.kv_cache(B, cap, int8=True)
+        for b in range(B):  # prefill each sequence's prefix (same kernels for both contexts)
+            sub = tuple(x[b:b + 1] for x in cache)
+            run_gpu(qw, c, st, sub, dev(st.rows[b, :starts[b]], tdt), [0], starts[b], 1.0e7, ROT)
+        outs = []
+        for s in range(6):
+            rows = np.stack([st.rows[b, starts[b] + s] for b in range(B)])
+            outs.append(run_gpu(qw, c, st, cache, dev(rows, tdt), [p + s for p in starts], 1, 1.0e7, ROT,
+                                out_dtype=tdt))
+        torch.cuda.synchronize()
+        assert c.device_error() == 0
+        res.append(([o.clone() for o in outs], [x.clone() for x in cache]))
+        c.close()
+    (o1, c1), (o0, c0) = res
+    for s in range(6):
+        assert torch.equal(o1[s], o0[s]), s
+    for x1, x0 in zip(c1, c0):
+        assert torch.equal(x1, x0)
