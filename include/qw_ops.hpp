@@ -15,6 +15,8 @@
 //   linear_attention_cuda.hpp:11-90)   -> HipLinearAttention / HipLinearAttnState
 //   qwen::cuda::CudaFullAttention / CudaKVCache (whole layer,
 //   full_attention_cuda.hpp:11-90)     -> HipFullAttention / HipKVCache
+//   qwen::cuda::CudaEngine (whole model, one sequence,
+//   cuda_engine.hpp:85-133)            -> HipEngine
 //
 // Same argument meaning as the reference: weights arrive as host
 // std::vector<float> in row-major [out][in]; activations are caller-owned
@@ -802,6 +804,331 @@ class HipFullAttention {
     int* d_pos_ = nullptr;
     mutable float *d_row_ = nullptr, *d_core_ = nullptr;
     mutable int cap_ = 0;
+};
+
+
+// ---------------------------------------------------------------------------
+// Whole model for one sequence: the drop-in for CudaEngine
+// (cuda_engine.hpp:85-133, cuda_engine.cu:244-479).
+//   set_layer_weights(i, flat)  slices the reference flat layer layout
+//       (cuda_engine.cu:244-298, WEIGHT_FORMAT.md): norms and MLP, then the
+//       whole linear-attention section, then the whole full-attention
+//       section, matrices [out][in]; the section of the layer's type is packed;
+//   forward(in, out, position)  one token: every layer, then the final norm
+//       (out = RMSNorm(x) * (1 + w), as CudaEngine::forward);
+//   forward_batch_prefill / _graph / _decode(in, out, positions, n)  n
+//       consecutive tokens of the sequence from host positions[0] on (the
+//       reference's contract for these calls: positions[b] = positions[0] + b).
+// Layer types follow the CPU backbone: layer i is Gated-DeltaNet unless
+// i % 4 == 3 (language_common.hpp is_linear_layer).  The reference CUDA
+// engine instead runs every layer as full attention (cuda_engine.cu:252-254);
+// the CPU operator is the specification here.  Each layer is
+//   x += attn(RMSNorm(x) * (1 + w_in));  x += MLP(RMSNorm(x) * (1 + w_post))
+// with the norms inside the projections' prologues, the residual adds in
+// their epilogues and the MLP in qw_mlp_fused (language_backbone.cpp:54-88).
+// Weights are stored in `format` (FP32 default, the reference's precision);
+// the KV cache is FP32 by default (the CPU KVCache) or INT8.
+class HipEngine {
+  public:
+    static constexpr int LNH = 16, LKD = 128, LVD = 128, LCK = 4;  // Gated-DeltaNet heads, dims, conv taps
+    static constexpr int FNH = 8, FNKV = 2, FHD = 256;             // full attention heads, KV heads, head dim
+
+    HipEngine(int num_layers, int hidden_size, int intermediate_size, int vocab_size, int max_seq_len,
+              qw_wfmt format = QW_WFMT_F32, bool int8_kv_cache = false, std::shared_ptr<Context> ctx = nullptr)
+        : nl_(num_layers), H_(hidden_size), I_(intermediate_size), V_(vocab_size), max_seq_(max_seq_len),
+          fmt_(format), kv_int8_(int8_kv_cache),
+          ctx_(ctx ? std::move(ctx) : Context::default_for_current_device()) {
+        if (nl_ < 1 || H_ < 64 || H_ % 64 || I_ < 64 || I_ % 64 || max_seq_ < 1)
+            throw Error(QW_ERR_SHAPE, "HipEngine: bad model shape");
+        layers_.resize(nl_);
+        for (int i = 0; i < nl_; ++i) layers_[i].linear = is_linear_layer(i);
+        alloc(d_pos_, 1);
+        ensure(1);
+    }
+    ~HipEngine() {
+        for (auto& L : layers_) free_layer(L);
+        for (void* p : {(void*)d_x_, (void*)d_row_, (void*)d_core_, (void*)d_pos_, (void*)d_final_norm_, (void*)d_out_})
+            if (p) (void)hipFree(p);
+    }
+    HipEngine(const HipEngine&) = delete;
+    HipEngine& operator=(const HipEngine&) = delete;
+
+    static bool is_linear_layer(int i) { return i % 4 != 3; }
+
+    // floats of one flat layer vector (every section present, as the reference slices it)
+    size_t flat_layer_size() const {
+        const size_t H = H_, I = I_, cd = LNH * (2 * LKD + LVD);
+        return 2 * H + 3 * I * H + cd * H + 2 * (size_t)LNH * H + (size_t)LNH * LVD * H + cd * LCK + H * LNH * LVD +
+               2 * LNH + LVD + (size_t)FNH * FHD * 2 * H + 2 * (size_t)FNKV * FHD * H + 2 * FHD + H * FNH * FHD;
+    }
+
+    void set_layer_weights(int layer_idx, const std::vector<float>& weights_flat) {
+        if (layer_idx < 0 || layer_idx >= nl_) throw Error(QW_ERR_INVALID, "HipEngine::set_layer_weights: layer index");
+        if (weights_flat.size() < flat_layer_size())
+            throw Error(QW_ERR_SHAPE, "HipEngine::set_layer_weights: flat vector shorter than " +
+                                          std::to_string(flat_layer_size()) + " floats");
+        Layer& L = layers_[layer_idx];
+        free_layer(L);
+        const float* p = weights_flat.data();
+        auto take = [&](size_t n) {
+            const float* q = p;
+            p += n;
+            return q;
+        };
+        const size_t H = H_, I = I_, cd = LNH * (2 * LKD + LVD), lv = (size_t)LNH * LVD;
+        const float* in_norm = take(H);
+        const float* post_norm = take(H);
+        const float* gate = take(I * H);
+        const float* up = take(I * H);
+        const float* down = take(H * I);
+        const float* qkv = take(cd * H);
+        const float* la = take((size_t)LNH * H);
+        const float* lb = take((size_t)LNH * H);
+        const float* lz = take(lv * H);
+        const float* conv = take(cd * LCK);
+        const float* lout = take(H * lv);
+        const float* alog = take(LNH);
+        const float* dtb = take(LNH);
+        const float* lnorm = take(LVD);
+        const float* fq = take((size_t)FNH * FHD * 2 * H);
+        const float* fk = take((size_t)FNKV * FHD * H);
+        const float* fv = take((size_t)FNKV * FHD * H);
+        const float* fqn = take(FHD);
+        const float* fkn = take(FHD);
+        const float* fo = take(H * FNH * FHD);
+        L.in_norm = upload(in_norm, H);
+        L.post_norm = upload(post_norm, H);
+        qw_weight* w = nullptr;
+        ctx_->check(qw_weight_pack_glu(ctx_->get(), gate, up, QW_F32, fmt_, I_, H_, nullptr, nullptr, &w),
+                    "HipEngine gate/up");
+        L.gateup.reset(w);
+        L.down = pack_ptr(down, H_, I_, "HipEngine down");
+        if (L.linear) {
+            const void* parts[4] = {qkv, lz, la, lb};
+            const int Ns[4] = {(int)cd, (int)lv, LNH, LNH};
+            ctx_->check(qw_weight_pack_concat(ctx_->get(), 4, parts, Ns, QW_F32, fmt_, H_, nullptr, &w),
+                        "HipEngine linear in_proj");
+            L.in.reset(w);
+            L.out = pack_ptr(lout, H_, (int)lv, "HipEngine linear out_proj");
+            L.conv = upload(conv, cd * LCK);
+            L.A_log = upload(alog, LNH);
+            L.dt_bias = upload(dtb, LNH);
+            L.norm_w = upload(lnorm, LVD);
+            alloc(L.conv_state, cd * (LCK - 1));
+            alloc(L.rec_state, (size_t)LNH * LKD * LVD);
+        } else {
+            const void* parts[3] = {fq, fk, fv};
+            const int Ns[3] = {FNH * FHD * 2, FNKV * FHD, FNKV * FHD};
+            ctx_->check(qw_weight_pack_concat(ctx_->get(), 3, parts, Ns, QW_F32, fmt_, H_, nullptr, &w),
+                        "HipEngine full in_proj");
+            L.in.reset(w);
+            L.out = pack_ptr(fo, H_, FNH * FHD, "HipEngine full o_proj");
+            L.q_norm = upload(fqn, FHD);
+            L.k_norm = upload(fkn, FHD);
+            const size_t es = kv_int8_ ? 1 : 4, n = (size_t)max_seq_ * FNKV * FHD;
+            if (hipMalloc(&L.kc, n * es) != hipSuccess || hipMalloc(&L.vc, n * es) != hipSuccess)
+                throw Error(QW_ERR_HIP, "HipEngine: KV cache hipMalloc");
+            if (kv_int8_) {
+                alloc(L.ks, (size_t)max_seq_ * FNKV);
+                alloc(L.vs, (size_t)max_seq_ * FNKV);
+            }
+        }
+        L.ready = true;
+        reset_layer_state(L);
+    }
+
+    void set_final_norm_weight(const std::vector<float>& weight) {
+        if ((int)weight.size() != H_) throw Error(QW_ERR_SHAPE, "HipEngine::set_final_norm_weight: expected hidden floats");
+        if (d_final_norm_) (void)hipFree(d_final_norm_);
+        d_final_norm_ = upload(weight.data(), H_);
+    }
+
+    // the tied lm_head (CudaEngine keeps one for its callers; forward does not apply it)
+    void set_lm_head_weight(const std::vector<float>& weight) {
+        if ((int64_t)weight.size() != (int64_t)V_ * H_) throw Error(QW_ERR_SHAPE, "HipEngine::set_lm_head_weight");
+        lm_head_ = std::make_unique<HipLMHead>(H_, V_, QW_WFMT_BF16, ctx_);
+        lm_head_->set_weight(weight);
+    }
+    HipLMHead* lm_head() const { return lm_head_.get(); }
+
+    void forward(const float* d_input, float* d_output, int position, hipStream_t stream = nullptr) {
+        run(d_input, d_output, position, 1, stream);
+    }
+    void forward_batch_prefill(const float* d_input, float* d_output, const int* positions, int batch_size,
+                               hipStream_t stream = nullptr) {
+        if (!positions || batch_size < 1) throw Error(QW_ERR_INVALID, "HipEngine::forward_batch_prefill: positions");
+        run(d_input, d_output, positions[0], batch_size, stream);
+    }
+    void forward_batch_prefill_graph(const float* d_input, float* d_output, const int* positions, int batch_size,
+                                     hipStream_t stream = nullptr) {
+        forward_batch_prefill(d_input, d_output, positions, batch_size, stream);
+    }
+    void forward_batch_decode(const float* d_input, float* d_output, const int* positions, int batch_size,
+                              hipStream_t stream = nullptr) {
+        forward_batch_prefill(d_input, d_output, positions, batch_size, stream);
+    }
+    void forward_host(const std::vector<float>& input, std::vector<float>& output, int position) {
+        if ((int)input.size() != H_) throw Error(QW_ERR_SHAPE, "HipEngine::forward_host: expected hidden floats");
+        ensure(1);
+        if (hipMemcpy(d_row_, input.data(), H_ * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipEngine::forward_host upload");
+        float* in = d_row_;  // staged in the projection buffer, copied into x before any projection writes it
+        run(in, d_out_, position, 1, nullptr);
+        output = get_output();
+    }
+    // the last forward_host output
+    std::vector<float> get_output() const {
+        std::vector<float> h(H_);
+        if (hipMemcpy(h.data(), d_out_, H_ * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipEngine::get_output");
+        return h;
+    }
+    void reset_cache() {
+        for (auto& L : layers_)
+            if (L.ready) reset_layer_state(L);
+        length_ = 0;
+    }
+    bool ready() const {
+        if (!d_final_norm_) return false;
+        for (const auto& L : layers_)
+            if (!L.ready) return false;
+        return true;
+    }
+    int num_layers() const { return nl_; }
+    int length() const { return length_; }  // tokens in the cache (one past the last position)
+
+  private:
+    struct Layer {
+        bool linear = false, ready = false;
+        float *in_norm = nullptr, *post_norm = nullptr;
+        detail::WeightPtr in, out, gateup, down;
+        float *conv = nullptr, *A_log = nullptr, *dt_bias = nullptr, *norm_w = nullptr;
+        float *conv_state = nullptr, *rec_state = nullptr;
+        float *q_norm = nullptr, *k_norm = nullptr;
+        void *kc = nullptr, *vc = nullptr;
+        float *ks = nullptr, *vs = nullptr;
+    };
+
+    void run(const float* d_input, float* d_output, int p0, int T, hipStream_t stream) {
+        if (!ready()) throw Error(QW_ERR_STATE, "HipEngine: weights not set");
+        if (p0 < 0 || p0 + T > max_seq_)
+            throw Error(QW_ERR_SHAPE, "HipEngine: positions " + std::to_string(p0) + ".." + std::to_string(p0 + T - 1) +
+                                          " outside max_seq_len " + std::to_string(max_seq_));
+        ensure(T);
+        qw_ctx* c = ctx_->get();
+        const int cd = LNH * (2 * LKD + LVD), lv = LNH * LVD, lin_in = cd + lv + 2 * LNH;
+        const int full_in = FNH * 2 * FHD + 2 * FNKV * FHD, ld_row = std::max(lin_in, full_in);
+        if (hipMemcpyAsync(d_x_, d_input, (size_t)T * H_ * sizeof(float), hipMemcpyDeviceToDevice, stream) !=
+                hipSuccess ||
+            hipMemcpyAsync(d_pos_, &p0, sizeof(int), hipMemcpyHostToDevice, stream) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipEngine: input upload");
+        qw_epilogue norm{}, res{};
+        norm.flags = QW_EP_NORM_X;
+        norm.eps = 1e-6f;
+        res.flags = QW_EP_RESIDUAL;
+        res.residual = d_x_;
+        res.residual_dtype = QW_F32;
+        for (auto& L : layers_) {
+            norm.gamma = L.in_norm;
+            ctx_->check(qw_linear(c, L.in.get(), d_x_, QW_F32, 0, T, d_row_, QW_F32, ld_row, &norm, stream),
+                        "HipEngine in_proj");
+            if (L.linear) {
+                qw_gdn_params gp{LNH, LKD, LVD, LCK, L.conv, L.A_log, L.dt_bias, L.norm_w};
+                const float* r = d_row_;
+                ctx_->check(qw_gdn_prefill(c, &gp, 1, T, r, r + cd, r + cd + lv, r + cd + lv + LNH, QW_F32, ld_row,
+                                           L.conv_state, L.rec_state, d_core_, QW_F32, lv, stream),
+                            "HipEngine Gated-DeltaNet");
+            } else {
+                qw_attn_params ap{FNH, FNKV, FHD, FHD / 4, 1.0e7f, L.q_norm, L.k_norm};
+                qw_kv_cache kv{kv_int8_ ? QW_I8 : QW_F32, L.kc, L.vc, L.ks, L.vs, max_seq_};
+                const float* r = d_row_;
+                ctx_->check(qw_attn_forward(c, &ap, &kv, 1, T, d_pos_, p0 + T, r, r + FHD, 2 * FHD, r + FNH * 2 * FHD,
+                                            r + FNH * 2 * FHD + FNKV * FHD, QW_F32, ld_row, d_core_, QW_F32, lv,
+                                            stream),
+                            "HipEngine attention");
+            }
+            ctx_->check(qw_linear(c, L.out.get(), d_core_, QW_F32, 0, T, d_x_, QW_F32, 0, &res, stream),
+                        "HipEngine out_proj");
+            ctx_->check(qw_mlp_fused(c, L.gateup.get(), L.down.get(), d_x_, QW_F32, L.post_norm, 1e-6f, d_x_, QW_F32,
+                                     d_x_, QW_F32, T, stream),
+                        "HipEngine MLP");
+        }
+        ctx_->check(qw_rmsnorm(c, d_x_, QW_F32, d_final_norm_, 1e-6f, d_output, QW_F32, T, H_, stream),
+                    "HipEngine final norm");
+        if (hipStreamSynchronize(stream) != hipSuccess) throw Error(QW_ERR_HIP, "HipEngine: sync");
+        length_ = std::max(length_, p0 + T);
+    }
+
+    void ensure(int T) {
+        if (T <= cap_) return;
+        const int cd = LNH * (2 * LKD + LVD), lv = LNH * LVD;
+        const int ld_row = std::max(cd + lv + 2 * LNH, FNH * 2 * FHD + 2 * FNKV * FHD);
+        for (float** p : {&d_x_, &d_row_, &d_core_, &d_out_})
+            if (*p) {
+                (void)hipFree(*p);
+                *p = nullptr;
+            }
+        alloc(d_x_, (size_t)T * H_);
+        alloc(d_row_, (size_t)T * ld_row);
+        alloc(d_core_, (size_t)T * std::max(lv, FNH * FHD));
+        alloc(d_out_, (size_t)H_);
+        cap_ = T;
+    }
+    void reset_layer_state(Layer& L) {
+        const int cd = LNH * (2 * LKD + LVD);
+        if (L.linear) {
+            zero(L.conv_state, (size_t)cd * (LCK - 1) * sizeof(float));
+            zero(L.rec_state, (size_t)LNH * LKD * LVD * sizeof(float));
+        } else {
+            const size_t n = (size_t)max_seq_ * FNKV * FHD * (kv_int8_ ? 1 : 4);
+            zero(L.kc, n);
+            zero(L.vc, n);
+            if (kv_int8_) {
+                zero(L.ks, (size_t)max_seq_ * FNKV * sizeof(float));
+                zero(L.vs, (size_t)max_seq_ * FNKV * sizeof(float));
+            }
+        }
+    }
+    static void zero(void* p, size_t bytes) {
+        if (p && hipMemset(p, 0, bytes) != hipSuccess) throw Error(QW_ERR_HIP, "HipEngine: hipMemset");
+    }
+    static void alloc(float*& p, size_t n) {
+        if (hipMalloc(&p, n * sizeof(float)) != hipSuccess) throw Error(QW_ERR_HIP, "HipEngine: hipMalloc");
+    }
+    static void alloc(int*& p, size_t n) {
+        if (hipMalloc(&p, n * sizeof(int)) != hipSuccess) throw Error(QW_ERR_HIP, "HipEngine: hipMalloc");
+    }
+    static float* upload(const float* h, size_t n) {
+        float* d = nullptr;
+        alloc(d, n);
+        if (hipMemcpy(d, h, n * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            throw Error(QW_ERR_HIP, "HipEngine: upload");
+        return d;
+    }
+    detail::WeightPtr pack_ptr(const float* w, int N, int K, const char* name) {
+        qw_weight* out = nullptr;
+        ctx_->check(qw_weight_pack(ctx_->get(), w, QW_F32, fmt_, N, K, nullptr, &out), name);
+        return detail::WeightPtr(out);
+    }
+    static void free_layer(Layer& L) {
+        for (void* p : {(void*)L.in_norm, (void*)L.post_norm, (void*)L.conv, (void*)L.A_log, (void*)L.dt_bias,
+                        (void*)L.norm_w, (void*)L.conv_state, (void*)L.rec_state, (void*)L.q_norm, (void*)L.k_norm,
+                        L.kc, L.vc, (void*)L.ks, (void*)L.vs})
+            if (p) (void)hipFree(p);
+        const bool linear = L.linear;
+        L = Layer{};
+        L.linear = linear;
+    }
+
+    int nl_, H_, I_, V_, max_seq_;
+    qw_wfmt fmt_;
+    bool kv_int8_;
+    std::shared_ptr<Context> ctx_;
+    std::vector<Layer> layers_;
+    std::unique_ptr<HipLMHead> lm_head_;
+    float *d_x_ = nullptr, *d_row_ = nullptr, *d_core_ = nullptr, *d_out_ = nullptr, *d_final_norm_ = nullptr;
+    int* d_pos_ = nullptr;
+    int cap_ = 0, length_ = 0;
 };
 
 }  // namespace hip

@@ -12,6 +12,7 @@
 #include "qw_ops.hpp"
 #include "qw_oracle.h"
 
+using qwen::hip::HipEngine;
 using qwen::hip::HipFullAttention;
 using qwen::hip::HipFullAttnProjections;
 using qwen::hip::HipKVCache;
@@ -378,6 +379,137 @@ static void test_errors() {
     report("HipMLP::set_weights shape check", threw ? 0.0 : 1.0, 0.0);
 }
 
+
+// Whole model (HipEngine, the CudaEngine drop-in): 4 layers in the backbone
+// pattern (Gated-DeltaNet, Gated-DeltaNet, Gated-DeltaNet, full attention) at
+// the real shapes, weights through set_layer_weights' flat layout, FP32
+// weights and cache; a 3-token prefill then 2 single-token steps, each output
+// against the oracle composed token by token (norm, projections,
+// orc_gdn_step / orc_full_attn_seq, residuals, MLP, final norm), bar 1e-4.
+static void test_engine() {
+    const int NL = 4, H = 1024, I = 3584, V = 512, S = 16;
+    const int LNH = 16, KD = 128, VD = 128, CK = 4, CD = LNH * (2 * KD + VD), LV = LNH * VD;
+    const int FNH = 8, FNKV = 2, HD = 256;
+    HipEngine eng(NL, H, I, V, S);
+    struct W {
+        std::vector<float> in_norm, post_norm, gate, up, down, qkv, a, b, z, conv, out, alog, dtb, nw, q, k, v, qn, kn, o;
+    };
+    std::vector<W> ws(NL);
+    for (int l = 0; l < NL; ++l) {
+        W& w = ws[l];
+        const uint64_t s = 5000 + 100 * l;
+        w.in_norm = normal(H, s, 0.1f);
+        w.post_norm = normal(H, s + 1, 0.1f);
+        w.gate = normal((size_t)I * H, s + 2, 0.03f);
+        w.up = normal((size_t)I * H, s + 3, 0.03f);
+        w.down = normal((size_t)H * I, s + 4, 0.02f);
+        w.qkv = normal((size_t)CD * H, s + 5, 0.03f);
+        w.a = normal((size_t)LNH * H, s + 6, 0.03f);
+        w.b = normal((size_t)LNH * H, s + 7, 0.03f);
+        w.z = normal((size_t)LV * H, s + 8, 0.03f);
+        w.conv = normal((size_t)CD * CK, s + 9, 0.5f);
+        w.out = normal((size_t)H * LV, s + 10, 0.02f);
+        w.alog = normal(LNH, s + 11, 0.5f);
+        w.dtb = normal(LNH, s + 12, 0.5f);
+        w.nw = normal(VD, s + 13, 0.1f);
+        for (auto& x : w.nw) x += 1.0f;
+        w.q = normal((size_t)FNH * HD * 2 * H, s + 14, 0.03f);
+        w.k = normal((size_t)FNKV * HD * H, s + 15, 0.03f);
+        w.v = normal((size_t)FNKV * HD * H, s + 16, 0.03f);
+        w.qn = normal(HD, s + 17, 0.1f);
+        w.kn = normal(HD, s + 18, 0.1f);
+        w.o = normal((size_t)H * FNH * HD, s + 19, 0.02f);
+        std::vector<float> flat;
+        for (const auto* part : {&w.in_norm, &w.post_norm, &w.gate, &w.up, &w.down, &w.qkv, &w.a, &w.b, &w.z,
+                                 &w.conv, &w.out, &w.alog, &w.dtb, &w.nw, &w.q, &w.k, &w.v, &w.qn, &w.kn, &w.o})
+            flat.insert(flat.end(), part->begin(), part->end());
+        if (flat.size() != eng.flat_layer_size()) {
+            report("HipEngine flat layer size", 1.0, 0.0);
+            return;
+        }
+        eng.set_layer_weights(l, flat);
+    }
+    auto final_norm = normal(H, 5999, 0.1f);
+    report("HipEngine not ready before the final norm", eng.ready() ? 1.0 : 0.0, 0.0);
+    eng.set_final_norm_weight(final_norm);
+    report("HipEngine ready", eng.ready() ? 0.0 : 1.0, 0.0);
+
+    const int T = 5, P0 = 3;
+    auto xin = normal((size_t)T * H, 5998);
+    // GPU: tokens 0..2 in one prefill call, then 3 and 4 one by one
+    Dev dx(xin), dy((size_t)T * H);
+    const int pos[P0] = {0, 1, 2};
+    eng.forward_batch_prefill(dx.p, dy.p, pos, P0);
+    for (int t = P0; t < T; ++t) eng.forward(dx.p + (size_t)t * H, dy.p + (size_t)t * H, t);
+    auto got = dy.get();
+    // oracle, token by token
+    std::vector<std::vector<float>> cs(NL), rs(NL), kc(NL), vc(NL);
+    for (int l = 0; l < NL; ++l) {
+        cs[l].assign((size_t)CD * (CK - 1), 0.0f);
+        rs[l].assign((size_t)LNH * KD * VD, 0.0f);
+        kc[l].assign((size_t)S * FNKV * HD, 0.0f);
+        vc[l].assign((size_t)S * FNKV * HD, 0.0f);
+    }
+    std::vector<float> ref((size_t)T * H), x(H), xn(H), mx(CD), rz(LV), rA(LNH), rB(LNH), core(LV), y(H),
+        qraw((size_t)FNH * 2 * HD), q((size_t)FNH * HD), g((size_t)FNH * HD), k((size_t)FNKV * HD),
+        v((size_t)FNKV * HD), fcore((size_t)FNH * HD), ks(S * FNKV), vs(S * FNKV);
+    for (int t = 0; t < T; ++t) {
+        x.assign(xin.begin() + (size_t)t * H, xin.begin() + (size_t)(t + 1) * H);
+        for (int l = 0; l < NL; ++l) {
+            const W& w = ws[l];
+            orc_rmsnorm(x.data(), w.in_norm.data(), xn.data(), 1, H, 1e-6f);
+            if (HipEngine::is_linear_layer(l)) {
+                orc_linear_f32(w.qkv.data(), xn.data(), mx.data(), 1, CD, H);
+                orc_linear_f32(w.z.data(), xn.data(), rz.data(), 1, LV, H);
+                orc_linear_f32(w.a.data(), xn.data(), rA.data(), 1, LNH, H);
+                orc_linear_f32(w.b.data(), xn.data(), rB.data(), 1, LNH, H);
+                orc_gdn_step(1, LNH, KD, VD, CK, mx.data(), rA.data(), rB.data(), rz.data(), w.conv.data(),
+                             w.alog.data(), w.dtb.data(), w.nw.data(), cs[l].data(), rs[l].data(), core.data());
+                orc_linear_f32(w.out.data(), core.data(), y.data(), 1, H, LV);
+            } else {
+                orc_linear_f32(w.q.data(), xn.data(), qraw.data(), 1, FNH * 2 * HD, H);
+                orc_split_q_gate(qraw.data(), q.data(), g.data(), 1, FNH, HD);
+                orc_linear_f32(w.k.data(), xn.data(), k.data(), 1, FNKV * HD, H);
+                orc_linear_f32(w.v.data(), xn.data(), v.data(), 1, FNKV * HD, H);
+                orc_full_attn_seq(1, t, FNH, FNKV, HD, HD / 4, 1.0e7f, w.qn.data(), w.kn.data(), q.data(), g.data(),
+                                  k.data(), v.data(), 0, kc[l].data(), vc[l].data(), ks.data(), vs.data(),
+                                  fcore.data());
+                orc_linear_f32(w.o.data(), fcore.data(), y.data(), 1, H, FNH * HD);
+            }
+            for (int i = 0; i < H; ++i) x[i] += y[i];
+            orc_rmsnorm(x.data(), w.post_norm.data(), xn.data(), 1, H, 1e-6f);
+            orc_mlp(w.gate.data(), w.up.data(), w.down.data(), xn.data(), y.data(), 1, H, I);
+            for (int i = 0; i < H; ++i) x[i] += y[i];
+        }
+        orc_rmsnorm(x.data(), final_norm.data(), ref.data() + (size_t)t * H, 1, H, 1e-6f);
+    }
+    std::vector<float> g3(got.begin(), got.begin() + (size_t)P0 * H), r3(ref.begin(), ref.begin() + (size_t)P0 * H);
+    std::vector<float> g2(got.begin() + (size_t)P0 * H, got.end()), r2(ref.begin() + (size_t)P0 * H, ref.end());
+    report("HipEngine forward_batch_prefill (3 tokens)", relerr(g3, r3), 1e-4);
+    report("HipEngine forward (positions 3, 4)", relerr(g2, r2), 1e-4);
+    report("HipEngine length", eng.length() == T ? 0.0 : 1.0, 0.0);
+    // reset_cache: position 0 again gives token 0's output; forward_host the same
+    eng.reset_cache();
+    std::vector<float> x0(xin.begin(), xin.begin() + H), h0;
+    eng.forward_host(x0, h0, 0);
+    std::vector<float> r0(ref.begin(), ref.begin() + H);
+    report("HipEngine reset_cache + forward_host", relerr(h0, r0), 1e-4);
+    bool threw = false;
+    try {
+        eng.set_layer_weights(0, std::vector<float>(100, 0.0f));
+    } catch (const qwen::hip::Error& e) {
+        threw = e.status == QW_ERR_SHAPE;
+    }
+    report("HipEngine::set_layer_weights short vector throws", threw ? 0.0 : 1.0, 0.0);
+    threw = false;
+    try {
+        eng.forward(dx.p, dy.p, S);  // position past max_seq_len
+    } catch (const qwen::hip::Error& e) {
+        threw = e.status == QW_ERR_SHAPE;
+    }
+    report("HipEngine position past max_seq_len throws", threw ? 0.0 : 1.0, 0.0);
+}
+
 int main() {
     try {
         test_errors();
@@ -387,6 +519,7 @@ int main() {
         test_linear_attention();
         test_full_attention();
         test_lmhead_and_sampler();
+        test_engine();
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
         return 1;
