@@ -425,7 +425,7 @@ def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
     lm_head argmax over 248320 tokens, position advance) captured as one graph
     and replayed per token; BF16 weights (random init, real shapes), INT8 KV
     cache, B sequences at a context of 1024 tokens (random cache contents and
-    recurrent states)."""
+    recurrent states).  Then the whole-model prefill of 1024-token prompts."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("qw_engine", os.path.join(os.path.dirname(os.path.abspath(__file__)), "qwen3.5_0.8b_deploy_amd", "engine.py"))
     em = importlib.util.module_from_spec(spec)
@@ -468,6 +468,31 @@ def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
         out[f"decode_model_B{B}_ctx{ctxlen}"] = {"ms_per_step": round(ms, 3), "tok_per_s": round(B / (ms * 1e-3), 1)}
         log("decode model", B, out[f"decode_model_B{B}_ctx{ctxlen}"])
         del eng, g
+    # whole-model prefill of a 1024-token prompt per sequence (engine.prefill:
+    # embedding, 24 layers with M = B*1024 rows, final norm, next-token
+    # argmax), from position 0 with cleared states; the reset is outside the
+    # timed region
+    T = 1024
+    for B in (1, 16):
+        eng = em.DecodeEngine(qw, ctx, layers, final_norm, embed, B, T + 256)
+        prompt = torch.randint(0, V, (B, T), device="cuda", dtype=torch.int32)
+        times = []
+        with torch.cuda.stream(stream):
+            for it in range(4):
+                eng.reset([0] * B)
+                torch.cuda.synchronize()
+                t0 = torch.cuda.Event(enable_timing=True)
+                t1 = torch.cuda.Event(enable_timing=True)
+                t0.record(stream)
+                eng.prefill(prompt, stream=stream)
+                t1.record(stream)
+                torch.cuda.synchronize()
+                if it:  # the first pass warms up
+                    times.append(t0.elapsed_time(t1))
+        ms = sorted(times)[len(times) // 2]
+        out[f"prefill_model_B{B}_T{T}"] = {"ms": round(ms, 3), "tok_per_s": round(B * T / (ms * 1e-3), 1)}
+        log("prefill model", B, out[f"prefill_model_B{B}_T{T}"])
+        del eng
     del layers, embed
     torch.cuda.empty_cache()
     return out

@@ -107,6 +107,55 @@ class DecodeEngine:
                 for c in P["cache"]:
                     c.zero_()
 
+    def prefill(self, ids, stream=None):
+        """T prompt tokens of every sequence in one pass (ids: device int32
+        [B][T]), from each sequence's current position -- the batched
+        counterpart of step(), as CudaEngine::forward_batch_prefill
+        (cuda_engine.cu:354-389) for B sequences.  Every projection sees
+        M = B*T rows (the MFMA GEMM from 33 rows on, so the layer inputs are
+        RMSNorm-ed once into the weights' activation type), Gated-DeltaNet runs
+        its chunked form from 24 tokens on and full attention its query-block
+        kernel from 16.  The states and caches advance by T; self.ids receives
+        the greedy next token of every sequence and self.pos += T."""
+        import torch
+        qw, ctx = self.qw, self.ctx
+        B, T = ids.shape
+        if B != self.B:
+            raise ValueError(f"prefill: ids has {B} sequences, the engine {self.B}")
+        M = B * T
+        dev = self.x.device
+        X = torch.empty(M, H, device=dev)
+        Xn = torch.empty(M, H, device=dev, dtype=self.act)
+        row = torch.empty(M, max(LIN_IN, FULL_IN), device=dev)
+        core = torch.empty(M, LNH * VD, device=dev, dtype=self.act)
+        qw.embedding_gather(ctx, self.embed, ids.reshape(-1).contiguous(), X, stream=stream)
+        for P in self.layers:
+            qw.rmsnorm(ctx, X, P["in_norm"], Xn, stream=stream)
+            if P["linear"]:
+                r = row[:, :LIN_IN]
+                qw.linear(ctx, P["in"], Xn, r, stream=stream)
+                qw.gdn_prefill(ctx, P["conv"], P["A_log"], P["dt_bias"], P["norm_w"], r[:, :CD],
+                               r[:, CD:CD + LNH * VD], r[:, CD + LNH * VD:CD + LNH * VD + LNH],
+                               r[:, CD + LNH * VD + LNH:], P["cs"], P["rs"], core, LNH, T, ld_in=row.stride(0),
+                               stream=stream)
+            else:
+                r = row[:, :FULL_IN]
+                qw.linear(ctx, P["in"], Xn, r, stream=stream)
+                qw.attn_forward(ctx, P["q_norm"], P["k_norm"], P["cache"], self.pos, r[:, 0:], r[:, HD:],
+                                r[:, FNH * 2 * HD:], r[:, FNH * 2 * HD + FNKV * HD:], core, tokens=T,
+                                q_head_stride=2 * HD, ld_in=row.stride(0), max_len=self.capacity, stream=stream)
+            qw.linear(ctx, P["out"], core, X, residual=X, stream=stream)
+            qw.rmsnorm(ctx, X, P["post_norm"], Xn, stream=stream)
+            qw.mlp_fused(ctx, P["gateup"], P["down"], Xn, X, residual=X, stream=stream)
+        if stream is None:
+            self.x.copy_(X.view(B, T, H)[:, T - 1])
+        else:
+            with torch.cuda.stream(stream):
+                self.x.copy_(X.view(B, T, H)[:, T - 1])
+        qw.rmsnorm(ctx, self.x, self.final_norm, self.xn, stream=stream)
+        qw.lmhead_argmax(ctx, self.E, self.xn, self.ids, stream=stream)
+        qw.positions_add(ctx, self.pos, T, stream=stream)
+
     def _project_in(self, P, r, stream):
         """The layer's stacked input projection of RMSNorm(x) * (1 + in_norm)."""
         qw, ctx = self.qw, self.ctx

@@ -25,6 +25,10 @@ pytestmark = pytest.mark.gpu
 
 torch = pytest.importorskip("torch")
 
+
+def host(t):
+    return t.float().cpu().numpy()
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
@@ -199,3 +203,44 @@ def test_engine_norm_first_matches_prologue(qw, ctx, oracle, relerr):
     # the automatic choice: norm-first only for BF16 weights above 12 sequences
     assert em.DecodeEngine(qw, ctx, tl, fn, emb, 13, 8).norm_first
     assert not em.DecodeEngine(qw, ctx, tl, fn, emb, 12, 8).norm_first
+
+
+def test_engine_prefill_matches_steps(qw, ctx, oracle, relerr):
+    """prefill(T tokens) == T teacher-forced decode steps: the same next ids,
+    last hidden state, Gated-DeltaNet states and KV caches, then the same
+    greedy continuation.  FP32 weights and cache; T = 40 takes the chunked
+    Gated-DeltaNet (>= 24 tokens) and the query-block attention (>= 16), each
+    pinned separately against the serial kernels at 2e-5; bar 1e-4."""
+    em = _engine_mod()
+    B, T, V, cap = 2, 40, 1024, 64
+    layers = make_layers(oracle, 4, 6000)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    tl = [{k: dev(v) for k, v in L.items()} for L in layers]
+    fn, emb = dev(oracle.normal((em.H,), 6999, 0.0, 0.1)), dev(oracle.normal((V, em.H), 6998))
+    kw = dict(fmt=qw.WFMT_F32, lm_fmt=qw.WFMT_F32, kv_int8=False)
+    ea = em.DecodeEngine(qw, ctx, tl, fn, emb, B, cap, **kw)
+    eb = em.DecodeEngine(qw, ctx, tl, fn, emb, B, cap, **kw)
+    prompt = torch.from_numpy(np.random.default_rng(7).integers(0, V, (B, T)).astype(np.int32)).cuda()
+    ea.reset([0] * B)
+    eb.reset([0] * B)
+    ea.prefill(prompt)
+    for t in range(T):
+        eb.ids.copy_(prompt[:, t])
+        eb.step()
+    torch.cuda.synchronize()
+    assert ctx.device_error() == 0
+    assert ea.pos.tolist() == [T] * B and eb.pos.tolist() == [T] * B
+    assert torch.equal(ea.ids, eb.ids), (ea.ids, eb.ids)
+    assert relerr(host(ea.x), host(eb.x).astype(np.float64)) <= 1e-4
+    for Pa, Pb in zip(ea.layers, eb.layers):
+        if Pa["linear"]:
+            assert relerr(host(Pa["rs"]), host(Pb["rs"]).astype(np.float64)) <= 1e-4
+            assert relerr(host(Pa["cs"]), host(Pb["cs"]).astype(np.float64)) <= 1e-4
+        else:
+            for ca, cb in zip(Pa["cache"][:2], Pb["cache"][:2]):
+                assert relerr(host(ca[:, :T]), host(cb[:, :T]).astype(np.float64)) <= 1e-4
+    for _ in range(3):  # the greedy continuation agrees
+        ea.step()
+        eb.step()
+        torch.cuda.synchronize()
+        assert torch.equal(ea.ids, eb.ids)
