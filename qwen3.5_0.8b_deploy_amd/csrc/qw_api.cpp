@@ -35,6 +35,7 @@ struct qw_ctx {
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
+    int attn_vcoal = -1;         // INT8 decode V loads: -1 by launch size, 0 scattered, 1 coalesced (QW_ATTN_VCOAL)
     bool attn_fused = true;      // one-launch INT8 decode attention (QW_ATTN_FUSED=0: prep / split / combine)
     int attn_prefill_min = 16;   // tokens per sequence from which the query-block attention kernel runs (QW_ATTN_PREFILL_MIN)  // tokens per sequence from which the chunked GDN form runs (QW_GDN_CHUNK_MIN)
     uint8_t* ws = nullptr;
@@ -176,6 +177,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
+    if (const char* v = getenv("QW_ATTN_VCOAL")) c->attn_vcoal = atoi(v) != 0 ? 1 : 0;
     if (const char* v = getenv("QW_ATTN_PREFILL_MIN")) c->attn_prefill_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GDN_CHUNK_MIN")) c->gdn_chunk_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
@@ -1015,6 +1017,9 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
              seg * nkv * nsplit <= ctx->num_cus && seg * nkv <= kMaxCounters)
                 ? ctx->counters
                 : nullptr;
+    // coalesced V loads once the launch has a workgroup per CU (see attn_decode_i8h)
+    a.vcoal = ctx->attn_vcoal < 0 ? ((int64_t)std::min<int64_t>(seg, rows_all) * nkv * nsplit >= ctx->num_cus ? 1 : 0)
+                                  : ctx->attn_vcoal;
     // rows in order, so every row finds the keys of the rows before it in the cache
     for (int64_t r0 = 0; r0 < rows_all; r0 += seg) {
         a.row0 = (int)r0;

@@ -848,13 +848,23 @@ constexpr int AD_KT = 64;  // keys per tile
 //     agent-scope stores and an arrival count; the last one to arrive merges
 //     them (merge_splits_wave, as attn_combine) and writes the gated output.
 // No workgroup waits for another, so the launch cannot stall.
-template <int HD, bool FUSED>
+template <int HD, bool FUSED, bool VCOAL>
 __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
     constexpr int KB = HD / 16, DT = HD / 16, E = HD / 64;
     constexpr int KHP = HD + 8, VHP = AD_KT + 4;
     constexpr int KPER = AD_KT * HD / 16 / 256;  // 16-code K chunks per thread
-    constexpr int VPER = AD_KT * HD / 16 / 256;  // 4x4 V blocks per thread
-    constexpr int KT4 = AD_KT / 4;               // lanes take consecutive 4-key groups: conflict-free V^T stores
+    // V tile loads, two patterns (VCOAL chosen per launch):
+    //   VCOAL: 16 codes of each of 4 consecutive keys per thread, consecutive
+    //     threads on consecutive 16-byte chunks of a key row (coalesced rows);
+    //   else: 4 codes of each of 4 consecutive keys per thread, consecutive
+    //     threads on consecutive key groups (conflict-free V^T stores).
+    // Measured: the coalesced rows win once the launch fills the chip (B=32,
+    // context 4096: 84 vs 97 us; B=1, context 32768: 42 vs 43 us) and lose
+    // with few workgroups (B=1, context 4096, 64 workgroups: 33 vs 24 us).
+    constexpr int VNG = AD_KT / 4 * (HD / 16);  // 4-key x 16-dim groups of the V tile
+    constexpr int VPG = (VNG + 255) / 256;      // per thread
+    constexpr int VPER = AD_KT * HD / 16 / 256;  // 4x4 V blocks per thread (scattered pattern)
+    constexpr int KT4 = AD_KT / 4;
     const int s = blockIdx.x, g = blockIdx.y, rl = blockIdx.z, r = a.row0 + rl;
     const int b = r / a.T, t = r % a.T;
     const int P = a.pos[b] + t;
@@ -884,7 +894,8 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
     const uint8_t* vbase = reinterpret_cast<const uint8_t*>(a.vc);
     const int64_t slot0 = (int64_t)b * a.cap * a.nkv + g;
     u32x4 kpre[KPER];
-    uint32_t vpre[VPER][4];
+    u32x4 vpre[VCOAL ? VPG : 1][4];
+    uint32_t vpre4[VCOAL ? 1 : VPER][4];
     float psc = 0.0f;
     auto issue = [&](int kt) {
         const int n = min(AD_KT, k1 - kt);
@@ -894,13 +905,25 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
             // keys past the range read the range's last key: finite, masked out later
             kpre[i] = *reinterpret_cast<const u32x4*>(kbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + part * 16);
         }
+        if constexpr (VCOAL) {
+            for (int i = 0; i < VPG; ++i) {  // V: 16 codes of each of 4 consecutive keys
+                const int grp = threadIdx.x + 256 * i, c = grp % (HD / 16), k4 = grp / (HD / 16);
 #pragma unroll
-        for (int i = 0; i < VPER; ++i) {
-            const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
+                for (int q = 0; q < 4; ++q) {
+                    const int j = 4 * k4 + q;
+                    if (VNG % 256 == 0 || grp < VNG)
+                        vpre[i][q] = *reinterpret_cast<const u32x4*>(vbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + 16 * c);
+                }
+            }
+        } else {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int j = 4 * k4 + q;
-                vpre[i][q] = *reinterpret_cast<const uint32_t*>(vbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + 4 * d4);
+            for (int i = 0; i < VPER; ++i) {  // V: 4 codes of each of 4 consecutive keys
+                const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int j = 4 * k4 + q;
+                    vpre4[i][q] = *reinterpret_cast<const uint32_t*>(vbase + (slot0 + (int64_t)(kt + min(j, n - 1)) * a.nkv) * HD + 4 * d4);
+                }
             }
         }
         if (threadIdx.x < 2 * AD_KT) {
@@ -1015,13 +1038,30 @@ __global__ __launch_bounds__(256) void attn_decode_i8h(AttnArgs a) {
             dst[0] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hv[0], hv[1], 0, 1, 2, 3, 4, 5, 6, 7));
             dst[1] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hv[2], hv[3], 0, 1, 2, 3, 4, 5, 6, 7));
         }
+        if constexpr (VCOAL) {
+            for (int i = 0; i < VPG; ++i) {
+                const int grp = threadIdx.x + 256 * i, c = grp % (HD / 16), k4 = grp / (HD / 16);
+                if (VNG % 256 == 0 || grp < VNG) {
 #pragma unroll
-        for (int i = 0; i < VPER; ++i) {
-            const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
-            uint32_t tw[4];
-            transpose4x4(vpre[i], tw);  // tw[e]: dim 4*d4 + e of keys 4*k4 .. 4*k4+3
+                    for (int blk = 0; blk < 4; ++blk) {
+                        const uint32_t w4[4] = {vpre[i][0][blk], vpre[i][1][blk], vpre[i][2][blk], vpre[i][3][blk]};
+                        uint32_t tw[4];
+                        transpose4x4(w4, tw);  // tw[e]: dim 16*c + 4*blk + e of keys 4*k4 .. 4*k4+3
 #pragma unroll
-            for (int e = 0; e < 4; ++e) *reinterpret_cast<f16x4*>(&VhT[(4 * d4 + e) * VHP + 4 * k4]) = i8x4_to_h4(tw[e]);
+                        for (int e = 0; e < 4; ++e)
+                            *reinterpret_cast<f16x4*>(&VhT[(16 * c + 4 * blk + e) * VHP + 4 * k4]) = i8x4_to_h4(tw[e]);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < VPER; ++i) {
+                const int blk = threadIdx.x + 256 * i, k4 = blk % (KT4), d4 = blk / (KT4);
+                uint32_t tw[4];
+                transpose4x4(vpre4[i], tw);  // tw[e]: dim 4*d4 + e of keys 4*k4 .. 4*k4+3
+#pragma unroll
+                for (int e = 0; e < 4; ++e) *reinterpret_cast<f16x4*>(&VhT[(4 * d4 + e) * VHP + 4 * k4]) = i8x4_to_h4(tw[e]);
+            }
         }
         if (threadIdx.x < 2 * AD_KT) (threadIdx.x < AD_KT ? ksc : vsc)[threadIdx.x & (AD_KT - 1)] = psc;
         if (kt + AD_KT < k1) issue(kt + AD_KT);
@@ -1192,11 +1232,13 @@ static hipError_t launch_attn_hd(const AttnArgs& a, hipStream_t stream) {
         return hipGetLastError();
     }
     if (a.kv_dt == DT_I8 && a.T == 1 && a.cnt) {  // one launch: prep and combine inside
-        hipLaunchKernelGGL((attn_decode_i8h<HD, true>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+        if (a.vcoal) hipLaunchKernelGGL((attn_decode_i8h<HD, true, true>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((attn_decode_i8h<HD, true, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(attn_prep<HD>, dim3(a.rows), dim3(64 * std::min(16, a.nh + 2 * a.nkv)), 0, stream, a);
-    if (a.kv_dt == DT_I8) hipLaunchKernelGGL((attn_decode_i8h<HD, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+    if (a.kv_dt == DT_I8 && a.vcoal) hipLaunchKernelGGL((attn_decode_i8h<HD, false, true>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
+    else if (a.kv_dt == DT_I8) hipLaunchKernelGGL((attn_decode_i8h<HD, false, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
     else hipLaunchKernelGGL((attn_split<HD, false>), dim3(a.nsplit, a.nkv, a.rows), dim3(256), 0, stream, a);
     launch_combine<HD>(a, stream);
     return hipGetLastError();

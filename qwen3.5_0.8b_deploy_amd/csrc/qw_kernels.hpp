@@ -159,6 +159,7 @@ struct AttnArgs {
     int prefill;           // query-block kernel: tokens [tb, tb + ntok) of sequences [b0, b0 + nb)
     int b0, nb, tb, ntok;  // (the rows of the segment are then contiguous: row0 = b0*T + tb)
     unsigned* cnt;         // one-launch decode (T == 1, INT8): arrival counters [rows][nkv], zero between launches
+    int vcoal;             // INT8 decode: coalesced V row loads (launches that fill the chip)
 };
 // workspace bytes per row for a given split count
 size_t attn_bytes_per_row(int nh, int hd, int nsplit);
