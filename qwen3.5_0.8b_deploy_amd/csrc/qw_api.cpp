@@ -35,6 +35,7 @@ struct qw_ctx {
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
+    int attn_split = 0;          // keys per decode split, 0 = by size (QW_ATTN_SPLIT forces a multiple of 64)
     int attn_vcoal = -1;         // INT8 decode V loads: -1 by launch size, 0 scattered, 1 coalesced (QW_ATTN_VCOAL)
     bool attn_fused = true;      // one-launch INT8 decode attention (QW_ATTN_FUSED=0: prep / split / combine)
     int attn_prefill_min = 16;   // tokens per sequence from which the query-block attention kernel runs (QW_ATTN_PREFILL_MIN)  // tokens per sequence from which the chunked GDN form runs (QW_GDN_CHUNK_MIN)
@@ -177,6 +178,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
+    if (const char* v = getenv("QW_ATTN_SPLIT")) c->attn_split = std::max(0, atoi(v)) / 64 * 64;
     if (const char* v = getenv("QW_ATTN_VCOAL")) c->attn_vcoal = atoi(v) != 0 ? 1 : 0;
     if (const char* v = getenv("QW_ATTN_PREFILL_MIN")) c->attn_prefill_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GDN_CHUNK_MIN")) c->gdn_chunk_min = std::max(1, atoi(v));
@@ -998,7 +1000,8 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
     // few tokens per sequence: key-split rows; keys per split about two
     // workgroups per CU, 128 .. 1024 keys each
     const int64_t want = (int64_t)len * rows_all * nkv / (2LL * ctx->num_cus);
-    const int split = (int)std::min<int64_t>(1024, std::max<int64_t>(128, want)) / 64 * 64;
+    int split = (int)std::min<int64_t>(1024, std::max<int64_t>(128, want)) / 64 * 64;
+    if (ctx->attn_split > 0) split = ctx->attn_split;  // forced (QW_ATTN_SPLIT, multiple of 64)
     const int nsplit = (len + split - 1) / split;
     const size_t per_row = qwk::attn_bytes_per_row(nh, hd, nsplit);
     const int64_t seg = std::min<int64_t>({rows_all, (int64_t)(ws / per_row), (int64_t)65535});
