@@ -34,6 +34,7 @@ struct qw_ctx {
     int gemm_tile_m = 0;         // tokens per GEMM block (QW_GEMM_TILE_M: 128 or 256; 0 = by shape)
     int gemm_waves = 8;          // waves per 256-token GEMM block (QW_GEMM_WAVES: 4 or 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
+    int gemm_splitk = 0;         // K splits per GEMM tile (QW_GEMM_SPLITK; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
     int attn_split = 0;          // keys per decode split, 0 = by size (QW_ATTN_SPLIT forces a multiple of 64)
     int attn_vcoal = -1;         // INT8 decode V loads: -1 by launch size, 0 scattered, 1 coalesced (QW_ATTN_VCOAL)
@@ -176,6 +177,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
+    if (const char* v = getenv("QW_GEMM_SPLITK")) c->gemm_splitk = std::max(0, std::min(8, atoi(v)));
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
     if (const char* v = getenv("QW_ATTN_SPLIT")) c->attn_split = std::max(0, atoi(v)) / 64 * 64;
@@ -658,7 +660,8 @@ static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
 //   - up to ~128-192 tokens the small-M kernels win on every shape (gate/up
 //     M=128: 15.5 us vs 26.2 us with 64-row blocks);
 //   - 1024-row weights (out, down): small-M kernels up to at least 512 tokens
-//     (down M=512: 33 us vs 82 us for the best GEMM);
+//     (down M=512: 33 us vs 82 us for the best GEMM); at 1024 tokens 64-row
+//     blocks with 2 K splits (down 47 vs 69 us, out 35 vs 41 us);
 //   - 4096..8192-row weights at 256..512 tokens: 64-row blocks (QKV+Z M=256:
 //     26 us vs 38 us with 256-row blocks vs 42 us small-M); from 1024 tokens
 //     256-row blocks (M=1024, 8 distinct weights each: QKV+Z 36.8 vs 61.1 us,
@@ -669,7 +672,7 @@ static int gemm_route(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M
     const int nb256 = (W->phys_tiles * 16 + 255) / 256;
     if (ctx->gemm_forced) return ctx->gemm_rows ? ctx->gemm_rows : (M <= 1024 && nb256 < 128 ? 64 : 256);
     int rows;
-    if (nb256 < 16) rows = M >= 1536 ? 256 : 0;
+    if (nb256 < 16) rows = M >= 1536 ? 256 : (M >= 1024 ? 64 : 0);
     else if (nb256 >= 128) rows = M >= 128 ? 256 : 0;
     else if (M <= 192) rows = 0;
     else rows = M < 1024 ? 64 : 256;
@@ -724,6 +727,24 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, int rows, const void*
     a.done = ctx->done;
     a.ids = ids;
     a.maxv = maxv;
+    // split-K (64-row blocks) where the tiles leave most CUs idle (the
+    // 1024-row projections at a few hundred tokens): up to 4 K splits, at
+    // least 8 K-blocks each,
+    // while the partial tiles fit the workspace (QW_GEMM_SPLITK forces S)
+    a.splitk = 1;
+    const int tiles = a.nblk_n * a.nblk_m;
+    if (!ids && rows == 64) {
+        // about one workgroup per CU (M=1024 on 1024 rows: 128 tiles, 2 splits
+        // 47 us vs 51 us with 4 for the down projection)
+        int S = ctx->gemm_splitk > 0 ? ctx->gemm_splitk
+                                     : (tiles * 2 <= ctx->num_cus ? std::min(4, ctx->num_cus / tiles) : 1);
+        S = std::max(1, std::min(S, W->ksteps / 8));
+        const size_t per = (size_t)qwk::gemm_acc_floats_per_thread(a.rows, a.tile_m, a.waves) * a.waves * 64 * 4;
+        while (S > 1 && ((size_t)tiles * S * per > ctx->partials_bytes || tiles > kMaxCounters)) --S;
+        a.splitk = S;
+        a.partials = reinterpret_cast<float*>(ctx->partials);
+        a.counters = ctx->counters;
+    }
     if ((uint64_t)W->bytes >= (1ull << 31) || (uint64_t)M * ldx * 2 >= (1ull << 31))
         return fail(ctx, QW_ERR_SHAPE, "operands above 2 GiB are not supported");
     hipError_t e = qwk::launch_gemm(a, W->wf, (int)xdt, W->glu != 0, ids != nullptr, stream);

@@ -150,6 +150,13 @@ void gemm_kernel(GemmArgs a) {
     const int nwg = gridDim.x;
     int b = blockIdx.x;
     if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
+    // split-K (64-row blocks only): consecutive ids after the XCD order are
+    // the splits of one tile
+    constexpr bool SPLITK = RW == 64 && !ARGMAX;
+    const int S = SPLITK ? max(1, a.splitk) : 1;
+    const int sk = b % S;
+    b /= S;
+    const int tile = b;
     // grouped raster: G_GROUP_M token blocks x all weight blocks per group,
     // token block fastest, so the workgroups resident on one XCD at a time
     // share both their activation blocks and their weight blocks in its L2
@@ -164,7 +171,9 @@ void gemm_kernel(GemmArgs a) {
 
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_tiles * a.ksteps * 1024u));
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2u));
-    const int nkb = a.ksteps;  // K-blocks of one 32-deep k-step
+    // K-blocks (one 32-deep k-step each) of this workgroup's split
+    const int kb_lo = (int)((int64_t)sk * a.ksteps / S);
+    const int nkb = (int)((int64_t)(sk + 1) * a.ksteps / S) - kb_lo;
 
     // The UPW units this wave moves per K-block: unit u = wave*UPW + q of the
     // stage is weight tile u (u < WU) or activation unit v = u - WU (sub-step
@@ -188,7 +197,7 @@ void gemm_kernel(GemmArgs a) {
     }
     auto dma = [&](int kb, int q) {
         uint8_t* dst = lds + (kb % G_NS) * G_STAGE + (wave * UPW + q) * 1024;
-        lds_dma16(rsq[q], dst, vbase[q] + (uint32_t)kb * vstep[q]);
+        lds_dma16(rsq[q], dst, vbase[q] + (uint32_t)(kb + kb_lo) * vstep[q]);
     };
 
     f32x16 acc[NBW][MB];
@@ -311,6 +320,61 @@ void gemm_kernel(GemmArgs a) {
     };
     for (int kb = 0; kb < nkb - 1; ++kb) kblock(kb, std::false_type{});
     kblock(nkb - 1, std::true_type{});
+
+    // ---- split-K hand-off: agent-scope stores of this split's tile, wait
+    // for their completion, one arrival count per tile; the last split to
+    // arrive sums all S partial tiles in split order (its own included) and
+    // runs the epilogue, the others leave.  The counter returns to zero.
+    if constexpr (SPLITK) {
+        if (S > 1) {
+            constexpr int PER = NBW * MB * 16;  // accumulator floats per lane
+            constexpr int P16 = PER / 4;          // 16-byte pieces per lane
+            // partial tiles [tile][split][thread][PER], written and read with
+            // device-coherent (sc1) 16-byte accesses
+            const uint64_t pbytes = (uint64_t)(a.nblk_n * a.nblk_m) * S * (NW * 64) * PER * 4;
+            const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials, (uint32_t)min(pbytes, (uint64_t)0x7fffffff));
+            const uint32_t tbase = (uint32_t)(((uint64_t)tile * S * (NW * 64) + threadIdx.x) * PER * 4);
+            const uint32_t sstride = (uint32_t)((NW * 64) * PER * 4);
+#pragma unroll
+            for (int i = 0; i < NBW; ++i)
+#pragma unroll
+                for (int j = 0; j < MB; ++j)
+#pragma unroll
+                    for (int e4 = 0; e4 < 4; ++e4) {
+                        const f32x4 v = {acc[i][j][4 * e4], acc[i][j][4 * e4 + 1], acc[i][j][4 * e4 + 2], acc[i][j][4 * e4 + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs,
+                                                               tbase + sk * sstride + ((i * MB + j) * 4 + e4) * 16, 0,
+                                                               AUX_SC1);
+                    }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __shared__ unsigned last_s;
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                const unsigned old = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                last_s = old == (unsigned)(S - 1) ? 1u : 0u;
+                if (old == (unsigned)(S - 1)) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (!last_s) return;  // uniform over the workgroup
+#pragma unroll
+            for (int i = 0; i < NBW; ++i)
+#pragma unroll
+                for (int j = 0; j < MB; ++j) acc[i][j] = f32x16{};
+            for (int s2 = 0; s2 < S; ++s2) {  // split order; all of a split's loads in flight at once
+                f32x4 pv[P16];
+#pragma unroll
+                for (int p = 0; p < P16; ++p)
+                    pv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, tbase + s2 * sstride + p * 16, 0,
+                                                                                           AUX_SC1));
+#pragma unroll
+                for (int i = 0; i < NBW; ++i)
+#pragma unroll
+                    for (int j = 0; j < MB; ++j)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) acc[i][j][e] += pv[(i * MB + j) * 4 + e / 4][e % 4];
+            }
+        }
+    }
 
     // ---- epilogue ----
     // accumulator item q of lane l: weight row i = 8*(q/4) + 4*(l/32) + q%4 of
@@ -464,7 +528,7 @@ static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, int threads
 
 template <int WF, int XDT, int BM, int NW, int RW>
 static hipError_t launch_bm(const GemmArgs& a, bool glu, bool argmax, hipStream_t stream) {
-    const int grid = a.nblk_n * a.nblk_m;
+    const int grid = a.nblk_n * a.nblk_m * ((RW == 64 && !argmax) ? std::max(1, a.splitk) : 1);
     const size_t lds = GTile<BM, NW, WF, RW>::lds_bytes();
     if (argmax) return launch_gemm_k(gemm_kernel<WF, XDT, false, true, BM, NW, RW>, a, grid, NW * 64, lds, stream);
     if (glu) return launch_gemm_k(gemm_kernel<WF, XDT, true, false, BM, NW, RW>, a, grid, NW * 64, lds, stream);
@@ -492,6 +556,12 @@ static hipError_t launch_wf(const GemmArgs& a, bool glu, bool argmax, hipStream_
         else return launch_bm<WF, XDT, 128, 4, 256>(a, glu, argmax, stream);
     }
     return hipErrorInvalidValue;
+}
+
+int gemm_acc_floats_per_thread(int rows, int tile_m, int waves) {
+    const int wr = rows == 256 ? 2 : 1;           // waves along the rows
+    const int wt = tile_m / (waves / wr);         // tokens per wave
+    return (rows / wr / 32) * (wt / 32) * 16;     // NBW * MB * 16
 }
 
 bool gemm_supported(int wf, int xdt) {

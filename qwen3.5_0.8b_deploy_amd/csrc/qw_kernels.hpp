@@ -86,7 +86,11 @@ struct GemmArgs {
     unsigned* done;
     int32_t* ids;
     float* maxv;
+    int splitk;              // K splits per tile (1: none; not with argmax)
+    float* partials;         // split-K partial tiles [tiles][splitk][threads][acc floats]
+    unsigned* counters;      // split-K arrival counters per tile (self-resetting)
 };
+int gemm_acc_floats_per_thread(int rows, int tile_m, int waves);
 bool gemm_supported(int wf, int xdt);
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream);
 

@@ -258,3 +258,31 @@ def test_gemm_int8_lmhead_argmax(qw, ctx, oracle, M):
     torch.cuda.synchronize()
     ref_ids, _ = oracle.lmhead_argmax_int8(q, sc, host(ht))
     assert np.array_equal(ids.cpu().numpy(), ref_ids)
+
+
+@pytest.mark.parametrize("K", [2048, 3584])
+def test_gemm_splitk_default_route(qw, oracle, relerr, K):
+    """The default routing of a 1024-row projection at 1024 tokens (the
+    prefill out / down projections): 64-row blocks with the K range split
+    over 2 workgroups per tile, partial tiles handed to the last split, which
+    adds them in split order and runs the residual epilogue.  Same FP32 bar
+    as the unsplit GEMM (2e-5 vs FP64 on the stored operands); two calls in a
+    row give identical results (the arrival counters return to zero)."""
+    M, N = 1024, 1024
+    c = qw.Context(0)
+    W = oracle.normal((N, K), 760 + K, 0.0, 0.02)
+    x = oracle.normal((M, K), 761)
+    r = oracle.normal((M, N), 762)
+    w = qw.Weight.pack(c, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    ys = []
+    for _ in range(2):
+        y = dev(r)
+        qw.linear(c, w, xt, y, residual=y)
+        ys.append(y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W), host(xt)) + r
+    assert relerr(host(ys[0]), ref) <= 2e-5
+    assert torch.equal(ys[0], ys[1])
+    del w
+    c.close()
