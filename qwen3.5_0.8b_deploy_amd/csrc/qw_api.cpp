@@ -659,9 +659,12 @@ static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
 // replayed from a graph, as in a decode step), BF16 and INT8 alike:
 //   - up to ~128-192 tokens the small-M kernels win on every shape (gate/up
 //     M=128: 15.5 us vs 26.2 us with 64-row blocks);
-//   - 1024-row weights (out, down): small-M kernels up to at least 512 tokens
-//     (down M=512: 33 us vs 82 us for the best GEMM); at 1024 tokens 64-row
-//     blocks with 2 K splits (down 47 vs 69 us, out 35 vs 41 us);
+//   - 1024-row weights (out, down): small-M kernels up to 256 tokens (down
+//     M=256: 17.8 us vs 26.2 us for split-K 64-row blocks); past 512 tokens,
+//     and past 256 when K > 2048, 64-row blocks with split-K (BF16 down M=384
+//     31.2 vs 38.8 us, M=768 42.6 vs 64.5 us; out M=768 29.7 vs 37.4 us; at
+//     M=320..512 with K=2048 the small-M kernels win or tie, out M=320 19.3
+//     vs 22.3 us);
 //   - 4096..8192-row weights at 256..512 tokens: 64-row blocks (QKV+Z M=256:
 //     26 us vs 38 us with 256-row blocks vs 42 us small-M); from 1024 tokens
 //     256-row blocks (M=1024, 8 distinct weights each: QKV+Z 36.8 vs 61.1 us,
@@ -672,7 +675,7 @@ static int gemm_route(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M
     const int nb256 = (W->phys_tiles * 16 + 255) / 256;
     if (ctx->gemm_forced) return ctx->gemm_rows ? ctx->gemm_rows : (M <= 1024 && nb256 < 128 ? 64 : 256);
     int rows;
-    if (nb256 < 16) rows = M >= 1536 ? 256 : (M >= 1024 ? 64 : 0);
+    if (nb256 < 16) rows = M >= 1536 ? 256 : ((M > 512 || (M > 256 && W->K > 2048)) ? 64 : 0);
     else if (nb256 >= 128) rows = M >= 128 ? 256 : 0;
     else if (M <= 192) rows = 0;
     else rows = M < 1024 ? 64 : 256;

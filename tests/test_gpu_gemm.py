@@ -260,15 +260,15 @@ def test_gemm_int8_lmhead_argmax(qw, ctx, oracle, M):
     assert np.array_equal(ids.cpu().numpy(), ref_ids)
 
 
-@pytest.mark.parametrize("K", [2048, 3584])
-def test_gemm_splitk_default_route(qw, oracle, relerr, K):
-    """The default routing of a 1024-row projection at 1024 tokens (the
-    prefill out / down projections): 64-row blocks with the K range split
-    over 2 workgroups per tile, partial tiles handed to the last split, which
+@pytest.mark.parametrize("K,M", [(2048, 1024), (3584, 1024), (3584, 384), (2048, 700), (3584, 700)])
+def test_gemm_splitk_default_route(qw, oracle, relerr, K, M):
+    """The default routing of a 1024-row projection at a few hundred to 1024
+    tokens (the prefill out / down projections): 64-row blocks with the K
+    range split over 2-4 workgroups per tile (M=700: a ragged last block), partial tiles handed to the last split, which
     adds them in split order and runs the residual epilogue.  Same FP32 bar
     as the unsplit GEMM (2e-5 vs FP64 on the stored operands); two calls in a
     row give identical results (the arrival counters return to zero)."""
-    M, N = 1024, 1024
+    N = 1024
     c = qw.Context(0)
     W = oracle.normal((N, K), 760 + K, 0.0, 0.02)
     x = oracle.normal((M, K), 761)
