@@ -468,12 +468,12 @@ def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
         out[f"decode_model_B{B}_ctx{ctxlen}"] = {"ms_per_step": round(ms, 3), "tok_per_s": round(B / (ms * 1e-3), 1)}
         log("decode model", B, out[f"decode_model_B{B}_ctx{ctxlen}"])
         del eng, g
-    # whole-model prefill of a 1024-token prompt per sequence (engine.prefill:
-    # embedding, 24 layers with M = B*1024 rows, final norm, next-token
-    # argmax), from position 0 with cleared states; the reset is outside the
-    # timed region
-    T = 1024
-    for B in (1, 16):
+    # whole-model prefill of a T-token prompt per sequence (engine.prefill:
+    # embedding, 24 layers with M = B*T rows, final norm, next-token argmax),
+    # from position 0 with cleared states; the reset is outside the timed
+    # region.  T=512 at B=1 is a mid-size prompt, where the 1024-row
+    # projections sit between the small-M kernels and the split-K GEMM
+    for B, T in ((1, 1024), (16, 1024), (1, 512)):
         eng = em.DecodeEngine(qw, ctx, layers, final_norm, embed, B, T + 256)
         prompt = torch.randint(0, V, (B, T), device="cuda", dtype=torch.int32)
         times = []
@@ -491,7 +491,7 @@ def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
                     times.append(t0.elapsed_time(t1))
         ms = sorted(times)[len(times) // 2]
         out[f"prefill_model_B{B}_T{T}"] = {"ms": round(ms, 3), "tok_per_s": round(B * T / (ms * 1e-3), 1)}
-        log("prefill model", B, out[f"prefill_model_B{B}_T{T}"])
+        log("prefill model", B, T, out[f"prefill_model_B{B}_T{T}"])
         del eng
     del layers, embed
     torch.cuda.empty_cache()
