@@ -665,10 +665,12 @@ static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
 //     31.2 vs 38.8 us, M=768 42.6 vs 64.5 us; out M=768 29.7 vs 37.4 us; at
 //     M=320..512 with K=2048 the small-M kernels win or tie, out M=320 19.3
 //     vs 22.3 us);
-//   - 4096..8192-row weights at 256..512 tokens: 64-row blocks (QKV+Z M=256:
-//     26 us vs 38 us with 256-row blocks vs 42 us small-M); from 1024 tokens
-//     256-row blocks (M=1024, 8 distinct weights each: QKV+Z 36.8 vs 61.1 us,
-//     gate/up 30.9 vs 44.1 us, Q+gate/K/V 32.6 vs 40.8 us);
+//   - 4096..8192-row weights from ~256 tokens: 64-row blocks while they make
+//     at most 512 tiles (QKV+Z M=256: 26 us vs 38 us with 256-row blocks vs
+//     42 us small-M; 4096 rows at M=1024 22.0 vs 27.3 us), 256-row blocks
+//     past that (8192 rows at M=768: 30.4 vs 40.3 us; M=1024, 8 distinct
+//     weights each: QKV+Z 36.8 vs 61.1 us, gate/up 30.9 vs 44.1 us,
+//     Q+gate/K/V 32.6 vs 40.8 us);
 //   - lm_head-size weights (>= 128 row blocks): 256-row blocks from 128.
 static int gemm_route(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M) {
     if (!gemm_ok(W, xdt) || M < ctx->gemm_min_m) return 0;
@@ -678,7 +680,7 @@ static int gemm_route(const qw_ctx* ctx, const qw_weight* W, qw_dtype xdt, int M
     if (nb256 < 16) rows = M >= 1536 ? 256 : ((M > 512 || (M > 256 && W->K > 2048)) ? 64 : 0);
     else if (nb256 >= 128) rows = M >= 128 ? 256 : 0;
     else if (M <= 192) rows = 0;
-    else rows = M < 1024 ? 64 : 256;
+    else rows = (W->phys_tiles * 16 + 63) / 64 * ((M + 127) / 128) <= 512 ? 64 : 256;
     if (rows && ctx->gemm_rows) rows = ctx->gemm_rows;
     return rows;
 }
