@@ -187,7 +187,13 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
 
 /* Reads and clears the context's device error flag: non-zero when a kernel
  * gave up a bounded wait (a fused MLP down task whose gate/up inputs never
- * completed); its outputs are then invalid.  Synchronizes the device. */
+ * completed within 0.2 s), when an attention token fell outside its cache, or
+ * when an embedding id was outside the vocabulary; the outputs of that call
+ * are then invalid.  Synchronizes the device; when the flag was set it also
+ * returns the fused MLP's completion counters to zero, so later launches on
+ * the context are valid again.  The eager and graph-replayed decode steps do
+ * not read the flag themselves: callers check it after a step (engine.py's
+ * DecodeEngine does, see check()). */
 qw_status qw_device_error(qw_ctx* ctx, int* flag);
 
 /* ---- gated full attention (between the projections) -------------------------

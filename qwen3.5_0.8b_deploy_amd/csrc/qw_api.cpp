@@ -1165,10 +1165,18 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
 qw_status qw_device_error(qw_ctx* ctx, int* flag) {
     if (!ctx || !flag) return QW_ERR_NULL;
     unsigned v = 0;
-    hipError_t e = hipMemcpy(&v, ctx->mlp_ctl + 3, sizeof v, hipMemcpyDeviceToHost);
+    hipSetDevice(ctx->device);
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(&v, ctx->mlp_ctl + 3, sizeof v, hipMemcpyDeviceToHost);
     if (e == hipSuccess && v) {
-        const unsigned zero = 0;
-        e = hipMemcpy(ctx->mlp_ctl + 3, &zero, sizeof zero, hipMemcpyHostToDevice);
+        // A one-launch MLP whose bounded wait expired left its down workgroups'
+        // exit counts reset while late gate/up workgroups still counted
+        // themselves done: with every kernel finished (the synchronize above),
+        // return the MLP's counter slots to zero together with the flag, so
+        // that the next launch waits for its own gate/up results.
+        e = hipMemset(ctx->counters + kMaxCounters, 0, (size_t)kMlpCounterWords * sizeof(unsigned));
+        if (e == hipSuccess) e = hipMemset(ctx->mlp_ctl + 3, 0, sizeof(unsigned));
+        if (e == hipSuccess) e = hipDeviceSynchronize();
     }
     if (e != hipSuccess) return hip_fail(ctx, e, "reading the device error flag");
     *flag = (int)v;

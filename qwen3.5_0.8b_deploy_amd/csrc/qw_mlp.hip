@@ -28,9 +28,11 @@
 // workgroups come first in the grid so they are resident first; gate/up
 // workgroups never wait, so the wait always ends (whatever the number of
 // resident workgroups, as long as the waiting ones fit).  The wait is still
-// bounded: after ~0.2 s of polling it sets the error flag (read with
-// qw_device_error) instead of hanging.  The last down workgroup to leave
-// returns the counters to zero (no memset: graph-capture safe).
+// bounded: after 0.2 s by the constant 100 MHz real-time counter it sets the
+// error flag (read with qw_device_error, which also returns the counters to
+// zero, since late gate/up arrivals of such a launch leave counts behind)
+// instead of hanging.  The last down workgroup to leave returns the counters
+// to zero (no memset: graph-capture safe).
 //
 // Operands follow the register-direct GEMV (qw_gemv.hip): each lane loads
 // its MFMA B operand straight from global memory in the packed weights'
@@ -279,7 +281,8 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
         __builtin_amdgcn_sched_barrier(0);
         // wait for every gate/up tile pair (bounded): wave 0 sums the done slots
         if (wave_id == 0) {
-            unsigned it = 0;
+            // s_memrealtime counts at a constant 100 MHz: 20M ticks = 0.2 s
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             for (;;) {
                 unsigned v = lane < MLP_SLOTS
                                  ? __hip_atomic_load(&p.cnt[lane * MLP_SLOT_STRIDE], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -288,7 +291,7 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
                 for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
                 if (v >= (unsigned)p.n_up) break;
                 __builtin_amdgcn_s_sleep(1);
-                if (++it > (1u << 22)) {
+                if (__builtin_amdgcn_s_memrealtime() - t0 > 20000000ull) {
                     if (lane == 0) __hip_atomic_store(&p.ctl[3], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }

@@ -107,7 +107,18 @@ class DecodeEngine:
                 for c in P["cache"]:
                     c.zero_()
 
-    def prefill(self, ids, stream=None):
+    def check(self):
+        """Raise if a kernel of the steps since the last check raised the
+        context's device error flag (a token outside its KV cache, an
+        embedding id outside the vocabulary, or an expired wait of the
+        one-launch MLP): their outputs are invalid.  Reads and clears the flag
+        (synchronizes the device), so it is never called inside a graph
+        capture; after replaying a captured step, call it from the host."""
+        flag = self.ctx.device_error()
+        if flag:
+            raise RuntimeError(f"device error flag {flag}: the last steps' outputs are invalid")
+
+    def prefill(self, ids, stream=None, check=None):
         """T prompt tokens of every sequence in one pass (ids: device int32
         [B][T]), from each sequence's current position -- the batched
         counterpart of step(), as CudaEngine::forward_batch_prefill
@@ -116,7 +127,9 @@ class DecodeEngine:
         RMSNorm-ed once into the weights' activation type), Gated-DeltaNet runs
         its chunked form from 24 tokens on and full attention its query-block
         kernel from 16.  The states and caches advance by T; self.ids receives
-        the greedy next token of every sequence and self.pos += T."""
+        the greedy next token of every sequence and self.pos += T.
+        check (default: when no stream is given) reads the device error flag
+        afterwards and raises if it was set (see check())."""
         import torch
         qw, ctx = self.qw, self.ctx
         B, T = ids.shape
@@ -155,6 +168,8 @@ class DecodeEngine:
         qw.rmsnorm(ctx, self.x, self.final_norm, self.xn, stream=stream)
         qw.lmhead_argmax(ctx, self.E, self.xn, self.ids, stream=stream)
         qw.positions_add(ctx, self.pos, T, stream=stream)
+        if check if check is not None else stream is None:
+            self.check()
 
     def _project_in(self, P, r, stream):
         """The layer's stacked input projection of RMSNorm(x) * (1 + in_norm)."""
@@ -165,8 +180,11 @@ class DecodeEngine:
         else:
             qw.linear(ctx, P["in"], self.x, r, gamma=P["in_norm"], stream=stream)
 
-    def step(self, stream=None):
-        """One greedy token for every sequence: ids <- next ids, positions += 1."""
+    def step(self, stream=None, check=None):
+        """One greedy token for every sequence: ids <- next ids, positions += 1.
+        check (default: when no stream is given, i.e. never while a graph is
+        captured on a stream) reads the device error flag afterwards and
+        raises if it was set (see check())."""
         qw, ctx, x, row = self.qw, self.ctx, self.x, self.row
         qw.embedding_gather(ctx, self.embed, self.ids, x, stream=stream)
         for P in self.layers:
@@ -192,6 +210,8 @@ class DecodeEngine:
         qw.rmsnorm(ctx, x, self.final_norm, self.xn, stream=stream)
         qw.lmhead_argmax(ctx, self.E, self.xn, self.ids, stream=stream)
         qw.positions_add(ctx, self.pos, 1, stream=stream)
+        if check if check is not None else stream is None:
+            self.check()
 
 
 # ---------------------------------------------------------------------------

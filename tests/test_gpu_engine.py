@@ -290,3 +290,34 @@ def test_engine_bf16_matches_oracle(qw, ctx, oracle, relerr, norm_first):
         err = relerr(x_gpu[b], x)
         print("bf16 engine", norm_first, b, err)
         assert err <= 1e-2, err
+
+
+def test_engine_check_raises_on_device_error(qw, ctx, oracle, relerr):
+    """A token past the KV cache raises the device flag; the eager step reads
+    it and raises.  The read clears the flag (and returns the one-launch MLP's
+    counters to zero), after which a one-launch MLP is exact again."""
+    em = _engine_mod()
+    B, V, cap = 1, 512, 2
+    layers = make_layers(oracle, 4, 9000)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    tl = [{k: dev(v) for k, v in L.items()} for L in layers]
+    fn, emb = dev(oracle.normal((em.H,), 9999, 0.0, 0.1)), dev(oracle.normal((V, em.H), 9998)).bfloat16()
+    eng = em.DecodeEngine(qw, ctx, tl, fn, emb, B, cap)
+    eng.reset([3], positions=[cap - 1])
+    eng.step()                      # position cap-1: inside the cache
+    with pytest.raises(RuntimeError, match="device error flag"):
+        eng.step()                  # position cap: outside
+    assert ctx.device_error() == 0
+    # the one-launch MLP after the reset of its counters
+    H, I = em.H, em.I
+    G, U, D = (oracle.normal(s, 9100 + i, 0.0, 0.02) for i, s in enumerate([(I, H), (I, H), (H, I)]))
+    gu = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16)
+    dn = qw.Weight.pack(ctx, D, qw.WFMT_BF16)
+    x = dev(oracle.normal((1, H), 9103)).bfloat16()
+    for _ in range(2):
+        y = torch.empty(1, H, device="cuda")
+        qw.mlp_fused(ctx, gu, dn, x, y, gamma=None, residual=x)
+        torch.cuda.synchronize()
+        ref = oracle.mlp_f64(oracle.round_bf16(G), oracle.round_bf16(U), oracle.round_bf16(D), host(x)) + host(x)
+        assert relerr(host(y), ref) <= 2e-3
+    assert ctx.device_error() == 0
