@@ -277,6 +277,23 @@ qw_status qw_positions_add(qw_ctx* ctx, int32_t* positions, int n, int delta, hi
 qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M,
                            int32_t* token_ids, float* max_logit, hipStream_t stream);
 
+/* The same lm_head + greedy argmax for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): no qw_ctx and no workspace.  No counterpart in the
+ * reference.  E is given by the device pointers of an already packed weight
+ * (qw_weight_device_ptrs of a qw_weight_pack result, or any buffer in that
+ * packed order; E_scales for INT8_ROWSCALE, else NULL) with its V rows and
+ * K inputs.  The argmax keys live in a fixed per-device array inside the
+ * library (2.3 KB, held until the process ends), so M is at most 256
+ * (QW_ERR_SHAPE beyond).  Runs on the current device with the kernels and
+ * routes of qw_lmhead_argmax on a default context, so its results equal that
+ * entry point's bit for bit.  Calls that overlap on one device share the
+ * array and race: serialize them (one stream, or events).  Errors are
+ * status codes only (there is no context for qw_last_error). */
+qw_status qw_lmhead_argmax_noalloc(const void* E_packed, const float* E_scales, qw_wfmt fmt, int V, int K,
+                                   const void* h, qw_dtype hdt, int M, int32_t* token_ids, float* max_logit,
+                                   hipStream_t stream);
+
 /* Greedy argmax of materialized logits [M][ld] (F32, BF16 or F16):
  * token_ids[m] = lowest index of the row maximum.  Replaces
  * GpuGreedyArgmaxSampler::sample (gpu_sampler_argmax.cu:69-93: block argmax +

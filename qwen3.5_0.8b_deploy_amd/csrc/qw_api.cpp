@@ -14,6 +14,7 @@
 #include <string>
 
 #include "../../include/qw_linear.h"
+#include "qw_internal.hpp"
 #include "qw_kernels.hpp"
 
 constexpr int kGemmMinM = 33;  // default token count from which the MFMA GEMM is used
@@ -858,6 +859,47 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     return run_skinny(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream,
                       kSkinnyMaxM);
 }
+
+}  // extern "C"
+
+namespace qwi {
+
+qw_status lmhead_argmax_scratch(int device, const void* packed, const float* scales, qw_wfmt fmt, int V, int K,
+                                const void* h, qw_dtype hdt, int M, int32_t* token_ids, float* max_logit,
+                                unsigned long long* keys, unsigned* done, hipStream_t stream) {
+    if (!packed || !h || !token_ids) return QW_ERR_NULL;
+    if (fmt != QW_WFMT_F32 && fmt != QW_WFMT_BF16 && fmt != QW_WFMT_INT8_ROWSCALE) return QW_ERR_DTYPE;
+    if (fmt == QW_WFMT_INT8_ROWSCALE && !scales) return QW_ERR_NULL;
+    if (V < 1 || K < 64 || K % 64 != 0 || M < 1) return QW_ERR_SHAPE;
+    if (!aligned(packed, 16) || (scales && !aligned(scales, 16))) return QW_ERR_ALIGN;
+    // a context and a weight descriptor on the stack: nothing is allocated
+    qw_ctx c;
+    c.device = device;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        c.num_cus = cus;
+    c.keys = keys;
+    c.done = done;
+    qw_weight W;
+    W.packed = static_cast<uint8_t*>(const_cast<void*>(packed));
+    W.scales = fmt == QW_WFMT_INT8_ROWSCALE ? const_cast<float*>(scales) : nullptr;
+    W.N = V;
+    W.K = K;
+    W.wf = fmt;
+    W.phys_tiles = (V + 15) / 16;
+    W.ksteps = K / (4 * ke_of(fmt));
+    W.bytes = (size_t)W.phys_tiles * W.ksteps * 1024;
+    W.owns = false;
+    qw_status s = check_linear(&c, &W, h, hdt, K, M, nullptr, QW_F32, 0, nullptr, false);
+    if (s != QW_OK) return s;
+    if (const int rows = gemm_route(&c, &W, hdt, M))
+        return run_gemm(&c, &W, rows, h, hdt, K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
+    return run_skinny(&c, &W, h, hdt, K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream, kSkinnyMaxM);
+}
+
+}  // namespace qwi
+
+extern "C" {
 
 static qw_status gdn_run(qw_ctx* ctx, const qw_gdn_params* p, int batch, int tokens, const void* mixed_qkv,
                          const void* z, const void* a, const void* b, qw_dtype in_dtype, int ld_in,

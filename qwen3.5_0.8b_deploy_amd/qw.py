@@ -30,7 +30,7 @@ EXPORTS = [
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
-    "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
+    "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_embedding_gather", "qw_positions_add", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
 
@@ -134,6 +134,7 @@ def lib():
                             _i, _vp], _i),
         "qw_device_error": ([_vp, _vp], _i),
         "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+        "qw_lmhead_argmax_noalloc": ([_vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp], _i),
         "qw_argmax_rows": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
         "qw_rmsnorm": ([_vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _vp], _i),
         "qw_residual_rmsnorm": ([_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _f, _i, _i, _vp], _i),
@@ -391,6 +392,17 @@ def lmhead_argmax(ctx, E, h, ids, max_logit=None, stream=None):
     M = h.shape[0] if h.dim() == 2 else 1
     ctx.check(lib().qw_lmhead_argmax(ctx.handle, E.handle, _ptr(h), _torch_code(h), M, _ptr(ids),
                                      _ptr(max_logit), _stream(stream)))
+
+
+def lmhead_argmax_noalloc(E, h, ids, max_logit=None, stream=None):
+    """qw_lmhead_argmax_noalloc over the packed device data of Weight E (no
+    context: the argmax keys live in the library's per-device array)."""
+    M = h.shape[0] if h.dim() == 2 else 1
+    packed, scales = E.device_ptrs()
+    st = lib().qw_lmhead_argmax_noalloc(packed, scales, E.fmt, E.N, E.K, _ptr(h), _torch_code(h), M, _ptr(ids),
+                                        _ptr(max_logit), _stream(stream))
+    if st != OK:
+        raise QwError(st, lib().qw_status_string(st).decode())
 
 
 def argmax_rows(ctx, logits, ids, max_logit=None, stream=None):
