@@ -185,6 +185,25 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
                        qw_dtype xdt, const float* gamma, float eps, const void* residual,
                        qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream);
 
+/* L consecutive MLP blocks: for l < L, x = x + down_l(silu(gate_l.n_l(x)) *
+ * (up_l.n_l(x))) with n_l(x) = RMSNorm(x) * (1 + gamma[l]) (eps), x rounded
+ * to xdt after every block; x [M][1024] in, y [M][1024] out (y may alias x).
+ * The chain of CudaLayer::forward's post-norm + MLP + residual steps
+ * (cuda_engine.cu:119-124) over consecutive layers, i.e. L calls of
+ * qw_mlp_fused(x, gamma[l], residual = x, y), equal to them within FP32
+ * summation order.  gamma NULL (or all entries NULL): every gateup weight
+ * carries its norm weight (qw_weight_fold_norm).  At decode (M <= 2, BF16
+ * weights with BF16 x or INT8 weights with F16 x, the Qwen3.5-0.8B shape
+ * H = 1024, I = 3584, a device with >= 256 CUs, L <= 48) all blocks run in
+ * ONE persistent launch that streams block l+1's weights while block l's
+ * data hand-offs are in flight; otherwise it makes the L qw_mlp_fused calls
+ * (QW_MLP_STACK=0 forces those).  The persistent launch needs the GPU to
+ * itself (its 256 workgroups must all be resident); a hand-off that does not
+ * arrive within 0.2 s raises the device error flag instead of hanging. */
+qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const qw_weight* const* down,
+                       const float* const* gamma, float eps, const void* x, qw_dtype xdt, void* y, int M,
+                       hipStream_t stream);
+
 /* Reads and clears the context's device error flag: non-zero when a kernel
  * gave up a bounded wait (a fused MLP down task whose gate/up inputs never
  * completed within 0.2 s), when an attention token fell outside its cache, or

@@ -48,6 +48,9 @@ struct qw_ctx {
     unsigned long long* keys = nullptr;    // argmax keys
     unsigned* done = nullptr;              // argmax completion counter
     unsigned* mlp_ctl = nullptr;           // fused MLP: ticket, up done, exited, error flag
+    unsigned* stack_epoch = nullptr;       // persistent MLP stack: launch epoch, abort word
+    uint64_t* stack_words = nullptr;       // persistent MLP stack: hand-off words
+    bool mlp_stack = true;                 // QW_MLP_STACK=0: per-layer launches in qw_mlp_stack
     float4* partials = nullptr;
     size_t partials_bytes = 0;
     uint8_t* scratch = nullptr;            // MLP intermediate h
@@ -89,7 +92,8 @@ constexpr size_t kCountersBytes = 64 * 1024;     // 16384 tiles
 constexpr size_t kKeysBytes = 64 * 1024;         // 8192 tokens
 constexpr size_t kDoneBytes = 256;
 constexpr size_t kPartialsBytes = 32u << 20;
-constexpr size_t kFixedBytes = kCountersBytes + kKeysBytes + kDoneBytes + kPartialsBytes;
+constexpr size_t kStackBytes = 512 * 1024;  // hand-off words of the persistent MLP stack (zeroed at init)
+constexpr size_t kFixedBytes = kCountersBytes + kKeysBytes + kDoneBytes + kStackBytes + kPartialsBytes;
 constexpr int kMlpCounterWords = 4096;  // tail of the counter region: the one-launch MLP's slots
 constexpr int kMaxCounters = (int)(kCountersBytes / 4) - kMlpCounterWords;
 constexpr int kMaxKeys = (int)(kKeysBytes / 8);
@@ -176,6 +180,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_SKINNY_NW_GLU")) c->force_nw_glu = nw_of(v);
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0 ? 1 : 0;
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
+    if (const char* v = getenv("QW_MLP_STACK")) c->mlp_stack = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_SPLITK")) c->gemm_splitk = std::max(0, std::min(8, atoi(v)));
@@ -202,7 +207,9 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     c->keys = reinterpret_cast<unsigned long long*>(p); p += kKeysBytes;
     c->done = reinterpret_cast<unsigned*>(p);
     c->mlp_ctl = c->done + 16;
+    c->stack_epoch = c->done + 32;
     p += kDoneBytes;
+    c->stack_words = reinterpret_cast<uint64_t*>(p); p += kStackBytes;
     c->partials = reinterpret_cast<float4*>(p); p += kPartialsBytes;
     c->partials_bytes = kPartialsBytes;
     {
@@ -216,7 +223,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     }
     // counters, keys and the completion counter start at zero; every kernel
     // that uses them returns them to zero before it exits.
-    if (hipMemset(c->ws, 0, kCountersBytes + kKeysBytes + kDoneBytes) != hipSuccess ||
+    if (hipMemset(c->ws, 0, kCountersBytes + kKeysBytes + kDoneBytes + kStackBytes) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         hipFree(c->ws);
         delete c;
@@ -1200,6 +1207,59 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         if (residual) e2.residual = static_cast<const uint8_t*>(residual) + (size_t)m0 * H * dsize(residual_dtype);
         s = qw_linear(ctx, down, ctx->scratch, hdt, I, mc, yc, ydt, H, residual ? &e2 : nullptr, stream);
         if (s != QW_OK) return s;
+    }
+    return QW_OK;
+}
+
+qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const qw_weight* const* down,
+                       const float* const* gamma, float eps, const void* x, qw_dtype xdt, void* y, int M,
+                       hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!gateup || !down || !x || !y) return fail(ctx, QW_ERR_NULL, "mlp_stack: NULL argument");
+    if (L < 1) return fail(ctx, QW_ERR_SHAPE, "mlp_stack: L=%d must be >= 1", L);
+    if (M < 1) return fail(ctx, QW_ERR_SHAPE, "mlp_stack: M=%d must be >= 1", M);
+    if (!valid_act(xdt)) return fail(ctx, QW_ERR_DTYPE, "mlp_stack: activation dtype unsupported");
+    bool one = ctx->mlp_stack && L <= qwk::kMlpStackMaxLayers && M <= qwk::mlp_stack_max_m() &&
+               ctx->num_cus >= qwk::mlp_stack_grid() && aligned(x, 16) && aligned(y, 16) &&
+               qwk::mlp_stack_ws_bytes() <= kStackBytes && eps > 0.0f;
+    for (int l = 0; l < L; ++l) {
+        if (!gateup[l] || !down[l]) return fail(ctx, QW_ERR_NULL, "mlp_stack: layer %d weight is NULL", l);
+        const qw_weight* gu = gateup[l];
+        const qw_weight* dn = down[l];
+        const bool g = gamma && gamma[l];
+        one = one && gu->glu && !dn->glu && gu->K == 1024 && gu->N == 3584 && dn->K == 3584 && dn->N == 1024 &&
+              gu->wf == gateup[0]->wf && dn->wf == gu->wf &&
+              ((gu->wf == QW_WFMT_BF16 && xdt == QW_BF16) || (gu->wf == QW_WFMT_INT8_ROWSCALE && xdt == QW_F16)) &&
+              (g ? !gu->norm_folded : gu->norm_folded) && (g == (gamma && gamma[0] != nullptr));
+    }
+    if (one) {
+        qwk::MlpStackArgs a{};
+        for (int l = 0; l < L; ++l) {
+            a.gu[l] = gateup[l]->packed;
+            a.dn[l] = down[l]->packed;
+            a.gu_scales[l] = gateup[l]->scales;
+            a.dn_scales[l] = down[l]->scales;
+            a.gamma[l] = gamma ? gamma[l] : nullptr;
+        }
+        a.x = x;
+        a.y = y;
+        a.M = M;
+        a.L = L;
+        a.eps = eps;
+        a.hbuf = ctx->stack_words;
+        a.epoch = ctx->stack_epoch;
+        a.err = ctx->mlp_ctl + 3;
+        hipError_t e = qwk::launch_mlp_stack(a, (int)gateup[0]->wf, (int)xdt, stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "MLP stack launch");
+        return QW_OK;
+    }
+    // one qw_mlp_fused per block, in place on y
+    const void* in = x;
+    for (int l = 0; l < L; ++l) {
+        qw_status s = qw_mlp_fused(ctx, gateup[l], down[l], in, xdt, gamma ? gamma[l] : nullptr, eps, in, xdt, y, xdt,
+                                   M, stream);
+        if (s != QW_OK) return s;
+        in = y;
     }
     return QW_OK;
 }

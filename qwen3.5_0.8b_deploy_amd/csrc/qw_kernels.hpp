@@ -111,6 +111,30 @@ int mlp_counter_words();
 int mlp_fused_max_m(int xdt);  // tokens the one-launch MLP takes for activations of this dtype
 hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t stream);
 
+// L consecutive MLP blocks in one persistent launch (qw_mlpstack.hip), decode
+// (M <= mlp_stack_max_m() tokens) at H = 1024, I = 3584, on 256 resident
+// workgroups; x and y [M][1024] in the activation dtype (y may alias x).
+constexpr int kMlpStackMaxLayers = 48;
+struct MlpStackArgs {
+    const uint8_t* gu[kMlpStackMaxLayers];        // packed GLU gate/up weights
+    const uint8_t* dn[kMlpStackMaxLayers];        // packed down weights
+    const float* gu_scales[kMlpStackMaxLayers];   // INT8 per-row scales (physical rows)
+    const float* dn_scales[kMlpStackMaxLayers];
+    const float* gamma[kMlpStackMaxLayers];       // RMSNorm weights (all NULL: folded into gate/up)
+    const void* x;
+    void* y;
+    int M, L;
+    float eps;
+    uint64_t* hbuf;     // hand-off words, mlp_stack_ws_bytes() zeroed once (h words, then the partials)
+    uint64_t* pbuf;     // set by launch_mlp_stack
+    unsigned* epoch;    // [2]: launch epoch (advanced by every launch), abort word
+    unsigned* err;      // device error flag
+};
+size_t mlp_stack_ws_bytes();
+int mlp_stack_max_m();
+int mlp_stack_grid();
+hipError_t launch_mlp_stack(const MlpStackArgs& a, int wf, int xdt, hipStream_t stream);
+
 // Gated-DeltaNet decode step (qw_gdn.hip): one token of each of B sequences.
 struct GdnArgs {
     int B, T, nh, kd, vd, K;  // B sequences of T consecutive tokens; row = b*T + t

@@ -30,7 +30,7 @@ EXPORTS = [
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
-    "qw_linear", "qw_mlp_fused", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
+    "qw_linear", "qw_mlp_fused", "qw_mlp_stack", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_embedding_gather", "qw_positions_add", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
 ]
 
@@ -134,6 +134,7 @@ def lib():
                             _i, _vp], _i),
         "qw_device_error": ([_vp, _vp], _i),
         "qw_lmhead_argmax": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp], _i),
+        "qw_mlp_stack": ([_vp, _i, _vp, _vp, _vp, _f, _vp, _i, _vp, _i, _vp], _i),
         "qw_lmhead_argmax_noalloc": ([_vp, _vp, _i, _i, _i, _vp, _i, _i, _vp, _vp, _vp], _i),
         "qw_argmax_rows": ([_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
         "qw_rmsnorm": ([_vp, _vp, _i, _vp, _f, _vp, _i, _i, _i, _vp], _i),
@@ -386,6 +387,18 @@ def mlp_fused(ctx, gateup, down, x, y, gamma=None, eps=1e-6, residual=None, stre
                                  _ptr(gamma), eps, _ptr(residual),
                                  _torch_code(residual) if residual is not None else F32,
                                  _ptr(y), _torch_code(y), M, _stream(stream)))
+
+
+def mlp_stack(ctx, gateups, downs, x, y, gammas=None, eps=1e-6, stream=None):
+    """L consecutive MLP blocks (qw_mlp_stack): x [M][1024] -> y, y may be x.
+    gammas: L device float tensors, or None when the weights carry the norm."""
+    L = len(gateups)
+    M = x.shape[0] if x.dim() == 2 else 1
+    gu = (ctypes.c_void_p * L)(*[w.handle.value for w in gateups])
+    dn = (ctypes.c_void_p * L)(*[w.handle.value for w in downs])
+    gm = None if gammas is None else (ctypes.c_void_p * L)(*[g.data_ptr() for g in gammas])
+    ctx.check(lib().qw_mlp_stack(ctx.handle, L, gu, dn, gm, eps, _ptr(x), _torch_code(x), _ptr(y), M,
+                                 _stream(stream)))
 
 
 def lmhead_argmax(ctx, E, h, ids, max_logit=None, stream=None):
