@@ -7,14 +7,17 @@ down GEMV with residual add -- for all 24 layers of Qwen3.5-0.8B, BF16
 weights N(0,0.02) random-initialised per layer, BF16 activations, FP32
 accumulate.  24 distinct layers (528 MB of weights) exceed the 256 MB
 Infinity Cache, so every step streams the weights from HBM.  The step is
-captured once in a HIP graph and replayed.
+one qw_mlp_stack call (all 24 blocks in one persistent launch that streams
+block l+1's weights during block l's hand-offs), captured once in a HIP
+graph and replayed; the same 24 blocks as 24 qw_mlp_fused launches are
+reported under extra.
 
 value = algorithmic bytes of the step / step time (GB/s), with
   per layer: W 22,020,096 B + x M*1024*2 + y M*1024*2 + gamma 1024*4.
-roofline: the dominant kernel -- the one-launch MLP kernel (qwk::mlp_kernel,
-22.02 MB of weights per launch), which is the whole headline step (24
-launches) -- timed with HIP events on the step's own stream over the timed
-region.
+roofline: the dominant kernel -- the persistent MLP stack kernel
+(qwk::mlp_stack_kernel, 528.5 MB of weights per launch), which is the whole
+headline step (one launch) -- timed with HIP events on the step's own stream
+over the timed region.
 cpu_baseline: the reference's own MLP::forward_batch (oracle/_ref, compiled
 from the reference sources; FP32, 1 thread) on a bounded sample, expressed
 in the same algorithmic-bytes unit.  Falls back to the oracle port when
@@ -39,7 +42,7 @@ H, I, V = 1024, 3584, 248320
 LAYERS = 24
 LINEAR_LAYERS = [i for i in range(24) if i % 4 != 3]   # 18 Gated-DeltaNet layers
 COPY_BYTES = 64 << 20   # calibration copy for the HBM traffic counters
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_mlp_fused_bf16_M1.txt")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_mlp_stack_bf16_M1.txt")
 METRIC = "decode GEMV HBM GB/s (% of peak) at M=1; prefill GEMM TFLOPS (% MFMA peak)"
 
 
@@ -167,7 +170,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--profile-kernel", action="store_true",
-                    help="counter pass: only the dominant kernel (eager one-launch MLP blocks) and a "
+                    help="counter pass: only the dominant kernel (4 eager MLP stack launches) and a "
                          "64 MiB calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -211,8 +214,7 @@ def main():
     if args.profile_kernel:
         with torch.cuda.stream(stream):
             for _ in range(4):
-                for l in range(LAYERS):
-                    qw.mlp_fused(ctx, gu[l], dn[l], h1, h1, gamma=gam[l], residual=h1)
+                qw.mlp_stack(ctx, gu, dn, h1, h1, gammas=gam, stream=stream)
             src = torch.empty(COPY_BYTES // 2, device="cuda", dtype=torch.bfloat16).fill_(1.0)
             dst = torch.empty_like(src)
             for _ in range(4):
@@ -221,20 +223,27 @@ def main():
         log("profile pass done")
         ctx.close()
         return
-    g_mlp = graphed(qw, ctx, stream, mlp_step(h1, 1))
+    g_mlp = graphed(qw, ctx, stream, lambda: qw.mlp_stack(ctx, gu, dn, h1, h1, gammas=gam, stream=stream))
     ms = timer.run(g_mlp.launch, args.steps, args.warmup)
     step_bytes = LAYERS * mlp_bytes(1)
     value = step_bytes / (ms * 1e-3) / 1e9
+    err = ctx.device_error()
+    if err:
+        raise RuntimeError(f"device error flag {err} after the headline step")
     log(f"headline: {ms * 1e3:.1f} us/step, {value:.0f} GB/s")
 
-    # Dominant kernel: the one-launch MLP kernel, 24 launches per step.  Its
-    # average launch duration is the timed region of the step graph (HIP
-    # events on the stream the kernels run on) over the 24 launches, so it
-    # includes the graph's inter-kernel gap and is an upper bound.
-    k_us = ms * 1e3 / LAYERS
-    k_bytes = mlp_bytes(1)
+    # Dominant kernel: the persistent MLP stack kernel, one launch per step.
+    # Its average launch duration is the timed region of the step graph (HIP
+    # events on the stream the kernel runs on) over the launches, so it
+    # includes the graph's launch gap and is an upper bound.
+    k_us = ms * 1e3
+    k_bytes = step_bytes
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
-    log(f"mlp kernel: {k_us:.2f} us avg, {k_gbs:.0f} GB/s")
+    log(f"mlp stack kernel: {k_us:.2f} us avg, {k_gbs:.0f} GB/s")
+    # the same 24 blocks as 24 one-launch MLP kernels (qw_mlp_fused)
+    g_pl = graphed(qw, ctx, stream, mlp_step(h1, 1))
+    pl_ms = timer.run(g_pl.launch, args.steps, args.warmup)
+    log(f"per-block launches: {pl_ms * 1e3:.1f} us/step, {step_bytes / (pl_ms * 1e-3) / 1e9:.0f} GB/s")
     # the separate fused RMSNorm + gate/up + SiLU*mul GEMV (the two-launch form)
     hmid = torch.empty(1, I, device="cuda", dtype=torch.bfloat16)
     g_gu = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, gu[l], h1, hmid, gamma=gam[l]) for l in range(LAYERS)])
@@ -246,6 +255,10 @@ def main():
         extra = run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args)
     extra["gateup_glu_kernel_bf16_M1"] = {"us_per_launch": round(gu_us, 3),
                                           "GBps": round(gateup_bytes(1) / (gu_us * 1e-6) / 1e9, 1)}
+    extra["mlp_per_block_launches_bf16_M1"] = {
+        "us_per_step": round(pl_ms * 1e3, 1), "us_per_block": round(pl_ms * 1e3 / LAYERS, 2),
+        "GBps": round(step_bytes / (pl_ms * 1e-3) / 1e9, 1),
+        "pct_hbm": round(100 * step_bytes / (pl_ms * 1e-3) / 1e9 / HBM_PEAK, 1)}
 
     cpu = None
     if not args.no_cpu:
@@ -268,13 +281,14 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights, N(0,1) activations; random init, no checkpoint)",
         "config": {
             "workload": "fused MLP block decode step (RMSNorm+gate/up+SiLU*mul+down+residual), "
-                        "24 Qwen3.5-0.8B layers, BF16 weights, M=1 (BASELINE configs[1]); HIP graph replay",
+                        "24 Qwen3.5-0.8B layers, BF16 weights, M=1 (BASELINE configs[1]); one qw_mlp_stack "
+                        "launch, HIP graph replay",
             "global_batch": 1, "seq_len": 1, "hidden": H, "intermediate": I, "layers": LAYERS,
             "bytes_per_step": step_bytes, "pct_of_hbm_peak": round(100 * value / HBM_PEAK, 2),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "qwk::mlp_kernel<BF16 weights, BF16 x, RMSNorm, gamma> (one-launch RMSNorm+gate/up+SiLU*mul+down+residual)",
+            "kernel": "qwk::mlp_stack_kernel<BF16 weights, BF16 x, gamma, M=1> (24 RMSNorm+gate/up+SiLU*mul+down+residual blocks, one persistent launch)",
             "achieved": round(k_gbs, 2),
             "peak": HBM_PEAK,
             "unit": "GB/s",

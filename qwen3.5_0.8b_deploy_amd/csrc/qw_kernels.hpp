@@ -125,8 +125,8 @@ struct MlpStackArgs {
     void* y;
     int M, L;
     float eps;
-    uint64_t* hbuf;     // hand-off words, mlp_stack_ws_bytes() zeroed once (h words, then the partials)
-    uint64_t* pbuf;     // set by launch_mlp_stack
+    uint64_t* hbuf;     // hand-off words, mlp_stack_ws_bytes() zeroed once (h words, then the x words)
+    uint64_t* xbuf;     // set by launch_mlp_stack
     unsigned* epoch;    // [2]: launch epoch (advanced by every launch), abort word
     unsigned* err;      // device error flag
 };

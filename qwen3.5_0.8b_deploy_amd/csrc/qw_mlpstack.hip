@@ -2,25 +2,32 @@
 // (decode, M <= 2 tokens, Qwen3.5-0.8B shape H = 1024, I = 3584):
 //     for l < L:  x = x + down_l( silu(gate_l . n_l(x)) * (up_l . n_l(x)) ),
 //                 n_l(x) = RMSNorm(x) * (1 + gamma_l),  x rounded to its dtype
-// -- the same result as L calls of qw_mlp_fused(y = residual = x).
+// -- the result of L calls of qw_mlp_fused(y = residual = x), with the
+// FP32 partial sums grouped differently (8 K slices of 4 k-steps for
+// gate/up).
 //
 // Why.  One MLP block streams 22 MB of BF16 weights, about 3.5 us at the
 // HBM rate, but a launch per block pays its start/end (~3 us) and its two
 // data hand-offs serially, and no weight of block l+1 moves while block l
-// waits for its hand-offs.  Here the weights of every block are requested
-// as soon as the registers that hold them are free, a full block ahead of
-// their use, so HBM streams continuously while the hand-offs run.
+// waits for its hand-offs.  Here each block's weights are requested as soon
+// as the registers that hold them are free, so they stream while the
+// previous block's hand-offs are in flight.
 //
 // Work split (grid = 256 workgroups of 16 waves, one per CU, all resident):
-//   * gate/up role, waves 0..7 of workgroup p < I/16: the gate/up tile pair p
-//     (intermediate rows [16p, 16p+16)), the K = H reduction cut in eight
+//   * workgroups 0..191: gate/up.  Waves 8g..8g+7 own tile pair wg + 192 g
+//     (intermediate rows [16p, 16p+16) of gate and up; the second group
+//     exists in workgroups 0..31 only), the K = H reduction cut in eight
 //     128-wide slices, one per wave;
-//   * down role, waves 8..15 of every workgroup w: down tile w/4 (output rows
-//     [16(w/4), +16)) over the K quarter w%4 (896 intermediate rows), cut in
-//     eight by wave.
-// The two roles never wait for each other inside a workgroup (no workgroup
-// barrier): each role's eight waves reduce their partial tiles through LDS,
-// and the last of the eight to arrive (an LDS counter) runs the epilogue.
+//   * workgroups 192..255: down tile wg - 192 (output rows [16t, 16t+16))
+//     over the full K = I, cut in eight 448-wide slices (waves 8..15); waves
+//     0..7 poll the h slices of waves 8..15 and hand them over through LDS,
+//     so the waves that stream weights never poll (vector-memory loads retire
+//     in order: a poll issued behind a weight stream waits for all of it).
+// A workgroup barrier is used once, at the start; the eight waves of a tile
+// reduce their partial tiles through LDS, and the last of them to arrive (an
+// LDS counter) runs the epilogue.  The others issue the next block's weight
+// loads only after that epilogue's stores (loads issued just before would
+// hold them up in the CU's memory pipeline).
 //
 // Hand-offs carry their own validity: every word written for another
 // workgroup is a 64-bit agent-scope store of (tag << 32 | payload), tag =
@@ -28,23 +35,21 @@
 // every tag is the expected one -- no counters, no fences, no memset (a
 // 64-bit store is seen whole or not at all).  `epoch` is a device word read
 // by every wave at the start and advanced by workgroup 0 at the very end, so
-// words of earlier launches never match.  Payloads:
-//   * h (gate/up -> down): two 16-bit h values (the down MFMA input type),
-//     h_buf[layer & 1][m][I/2];
-//   * down partials (down -> gate/up of the next block, and the final x):
-//     one FP32 value, p_buf[layer & 1][quarter][m][H].  The consumer forms
-//     x_{l+1} = round(x_l + ((P0 + P1) + P2) + P3) itself, in a fixed order,
-//     so every workgroup holds bit-identical copies.
+// words of earlier launches never match.  Payloads, two 16-bit values each:
+//   * h (gate/up -> down): h_buf[layer & 1][m][I/2], the down MFMA input type;
+//   * x (down -> gate/up of the next block): x_buf[layer & 1][m][H/2], the
+//     block output rounded to the activation dtype (the last block's is also
+//     written to y).
 // Buffers alternate by layer parity: a slot of layer l+2 is written only
 // after every reader of layer l has passed (each layer's hand-offs depend on
-// all of the previous one's).
+// all of the previous one's).  A poll reads only the words the wave needs
+// (one to four per lane), since poll traffic slows every other access.
 //
-// Polls read one word per lane (a few hundred bytes per wave) until those are
-// valid, then the full set once, so waiting costs little memory traffic.
 // Every wait is bounded (0.2 s of the 100 MHz real-time counter): on expiry
 // it raises the error flag (qw_device_error) and the launch's abort word, and
-// every wave stops waiting, so the grid always drains.  Workgroups must all be resident: the launcher takes one
-// workgroup per CU and refuses devices with fewer than 256 CUs.
+// every wave stops waiting, so the grid always drains.  Workgroups must all be
+// resident: the launcher takes one workgroup per CU and refuses devices with
+// fewer than 256 CUs.
 //
 // Reference: the post-norm + MLP + residual chain of CudaLayer::forward
 // (cuda_engine.cu:119-124) over consecutive layers, i.e. CudaMLP::forward_add_
@@ -58,21 +63,31 @@ constexpr int MS_NW = 16;          // waves per workgroup: 8 gate/up + 8 down
 constexpr int MS_RW = 8;           // waves per role
 constexpr int MS_MAXM = 4;         // tokens
 constexpr int MS_H = 1024, MS_I = 3584;
-constexpr int MS_Q = 4;            // K quarters of a down tile
-constexpr int MS_GRID = (MS_H / 16) * MS_Q;  // 256 down pieces = 256 workgroups
+constexpr int MS_GRID = 256;       // workgroups: one per CU
+constexpr int MS_DT = MS_H / 16;   // down tiles (64), on workgroups [MS_D0, MS_GRID)
+constexpr int MS_D0 = MS_GRID - MS_DT;
 constexpr int MS_SPAN = 128;       // K values per wave slice (both roles, both formats)
 constexpr int MS_LROW = MS_SPAN + 8;  // LDS row of a wave's B slice (16-byte pad)
+constexpr int MS_DSPAN = MS_I / MS_RW;  // intermediate rows of a down wave's slice (448)
+constexpr int MS_DROW = MS_DSPAN + 8;    // LDS row of a down wave's h slice (16-byte pad)
 
-size_t mlp_stack_ws_bytes() { return (size_t)2 * MS_MAXM * (MS_I / 2) * 8 + (size_t)2 * MS_Q * MS_MAXM * MS_H * 8; }
+constexpr size_t MS_HWORDS = (size_t)2 * MS_MAXM * (MS_I / 2);   // h words: [parity][token][I/2]
+constexpr size_t MS_XWORDS = (size_t)2 * MS_MAXM * (MS_H / 2);   // x words: [parity][token][H/2]
+size_t mlp_stack_ws_bytes() { return (MS_HWORDS + MS_XWORDS) * 8; }
 int mlp_stack_max_m() { return 2; }  // register budget: two tokens per lane slice
 int mlp_stack_grid() { return MS_GRID; }
 
 struct MsLds {
-    uint16_t bs[MS_NW][MS_MAXM][MS_LROW];  // per-wave B slices (MFMA input type bits; 16-byte rows)
-    f32x4 red_gu[MS_RW][2][64];  // gate/up role partial tiles
-    f32x4 red_dn[MS_RW][64];     // down role partial tiles
-    float red_ss[MS_RW][MS_MAXM];
-    unsigned cnt_gu, cnt_dn;
+    uint16_t bs[MS_NW][MS_MAXM][MS_LROW];  // gate/up waves' B slices (MFMA input type bits; 16-byte rows)
+    uint16_t bd[MS_RW][MS_MAXM][MS_DROW];  // down waves' h slices, deposited by their pollers
+    f32x4 red_gu[2][MS_RW][2][64];         // gate/up partial tiles of the workgroup's (up to) two pairs
+    f32x4 red_dn[MS_RW][64];               // down partial tiles
+    float red_ss[2][MS_RW][MS_MAXM];
+    float xt[MS_MAXM][16];                 // x of this workgroup's down tile rows
+    unsigned cnt_gu[2], cnt_dn;            // arrivals at the reductions (reset by the last arriver)
+    unsigned done_gu[2], done_dn;          // blocks whose epilogue has been issued
+    unsigned hflag[MS_RW];                 // blocks whose h slice has been deposited for down wave d
+    unsigned cnt_fin;                      // workgroup 0: gate/up waves that saw the final x
 };
 
 __device__ __forceinline__ uint32_t ms_tag(uint32_t epoch, int layer) { return (epoch << 6) | (uint32_t)(layer + 1); }
@@ -93,33 +108,31 @@ struct MsAbort {
     uint32_t epoch;
 };
 
-// Pause between polls; false once the wait that started at t0 has run 0.2 s
-// of the 100 MHz real-time counter (then the error flag and the abort word
-// are raised) or as soon as another wave of this launch has aborted.
-__device__ __forceinline__ bool ms_pause(const MsAbort& ab, uint64_t t0, bool& dead) {
-    const unsigned v = __hip_atomic_load(ab.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool expired = __builtin_amdgcn_s_memrealtime() - t0 > 20000000ull;
-    if (v == ab.epoch + 1u || expired) {
-        if (expired) {
-            __hip_atomic_store(ab.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(ab.abort, ab.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// After a poll that did not find its words (the it-th miss of this wait):
+// false once the wait that began at t0 has run 0.2 s of the 100 MHz real-time
+// counter (then the error flag and the abort word are raised) or when another
+// wave of this launch has aborted.  The clock is read on every 64th miss
+// only, and the abort word once a wait has lasted 1 ms (waits last
+// microseconds): thousands of waves polling one address would serialize at
+// its memory channel and slow every hand-off.
+__device__ __forceinline__ bool ms_pause(const MsAbort& ab, uint64_t t0, unsigned& it, bool& dead) {
+    if ((++it & 63u) == 0u) {
+        const uint64_t el = __builtin_amdgcn_s_memrealtime() - t0;
+        if (el > 100000ull) {
+            const bool expired = el > 20000000ull;
+            const unsigned seen = __hip_atomic_load(ab.abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (seen == ab.epoch + 1u || expired) {
+                if (expired) {
+                    __hip_atomic_store(ab.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(ab.abort, ab.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                dead = true;
+                return false;
+            }
         }
-        dead = true;
-        return false;
     }
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(1);
     return true;
-}
-
-// Bounded wait until every lane's probe word carries `tag` (probe = nullptr:
-// nothing to wait for in that lane).
-__device__ __forceinline__ void ms_wait(const uint64_t* probe, uint32_t tag, const MsAbort& ab, uint64_t t0,
-                                        bool& dead) {
-    while (!dead) {
-        const bool ok = probe == nullptr || (uint32_t)(ms_load(probe) >> 32) == tag;
-        if (__all(ok)) return;
-        if (!ms_pause(ab, t0, dead)) return;
-    }
 }
 
 // x rounded to the activation dtype
@@ -134,16 +147,17 @@ __device__ __forceinline__ void lds_fence_wave() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// B operand of k-step u of a wave's slice: lane (j, g) reads token j's
-// elements [u*4*KE + g*KE, +KE) of the slice (zeros for j >= M).
+// B operand of one k-step from an LDS slice [token][k] of row stride `ld`
+// elements: lane (j, g) reads token j's elements [k + g*KE, +KE) (zeros for
+// j >= M).
 template <int WF>
-__device__ __forceinline__ BOps<WF, (WF == WF_BF16 ? DT_BF16 : DT_F16)> ms_bops(const uint16_t (*bs)[MS_LROW], int u,
+__device__ __forceinline__ BOps<WF, (WF == WF_BF16 ? DT_BF16 : DT_F16)> ms_bops(const uint16_t* base, int ld, int k,
                                                                                  int lane, int M) {
     constexpr int KE = WTraits<WF>::KE;
     constexpr int XDT = WF == WF_BF16 ? DT_BF16 : DT_F16;
     const int j = lane & 15, g = lane >> 4;
     BOps<WF, XDT> b;
-    const uint16_t* p = &bs[j < M ? j : 0][u * 4 * KE + g * KE];
+    const uint16_t* p = base + (j < M ? j : 0) * ld + k + g * KE;
     if constexpr (WF == WF_BF16) {
         u32x4 v = *reinterpret_cast<const u32x4*>(p);
         if (j >= M) v = u32x4{0u, 0u, 0u, 0u};
@@ -157,6 +171,36 @@ __device__ __forceinline__ BOps<WF, (WF == WF_BF16 ? DT_BF16 : DT_F16)> ms_bops(
     return b;
 }
 
+// Bounded wait until the LDS counter c reaches `target` (deposits by the
+// other role of this workgroup).  The clock is read on every 256th miss.
+__device__ __forceinline__ void ms_wait_lds(unsigned* c, unsigned target, const MsAbort& ab, bool& dead) {
+    uint64_t t0 = 0;
+    unsigned it = 0;
+    while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+        if ((it & 255u) == 0u) {
+            const uint64_t now = __builtin_amdgcn_s_memrealtime();
+            if (it == 0u) {
+                t0 = now;
+            } else if (now - t0 > 20000000ull) {
+                __hip_atomic_store(ab.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(ab.abort, ab.epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                dead = true;
+                return;
+            }
+        }
+        ++it;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");  // the deposited data is read only after the count
+}
+
+// One LDS deposit done: the data writes complete, then the counter.
+__device__ __forceinline__ void ms_deposit(unsigned* c, int lane) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    if (lane == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // WF: weight format (BF16 or INT8); XDT: activation / output dtype (BF16, or
 // F16 for INT8 weights); GAM: per-layer gamma pointers given (else the norm
 // weight is folded into the gate/up weights); MT: tokens the registers are
@@ -168,7 +212,9 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     constexpr int KS_GU = MS_H / (4 * KE);                 // k-steps of a gate/up tile (32 / 16)
     constexpr int KS_DN = MS_I / (4 * KE);                 // k-steps of a down tile (112 / 56)
     constexpr int U_GU = KS_GU / MS_RW;                    // per gate/up wave (4 / 2)
-    constexpr int U_DN = (KS_DN / MS_Q + MS_RW - 1) / MS_RW;  // per down wave, at most (4 / 2)
+    constexpr int U_DN = KS_DN / MS_RW;                    // per down wave (14 / 7)
+    constexpr int HWD = MS_DSPAN / 2;                      // h words per token of a down wave's slice (224)
+    constexpr int NH = (HWD + 63) / 64;                    // per lane (4)
     extern __shared__ __attribute__((aligned(16))) uint8_t ms_raw[];
     MsLds& S = *reinterpret_cast<MsLds*>(ms_raw);
 
@@ -177,32 +223,46 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     const int j = lane & 15, g = lane >> 4;
     const int wg = blockIdx.x;
     const int M = a.M;
+    const bool dn_wg = wg >= MS_D0;          // a down workgroup (tile t, full K); else gate/up
+    const int t = wg - MS_D0;
     // every wave holds the epoch before the barrier, so workgroup 0 can only
     // advance it (at the very end, after all hand-offs) once all have read it
     const uint32_t epoch = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x < MS_RW) S.hflag[threadIdx.x] = 0u;
     if (threadIdx.x == 0) {
-        S.cnt_gu = 0u;
+        S.cnt_gu[0] = S.cnt_gu[1] = 0u;
+        S.done_gu[0] = S.done_gu[1] = 0u;
         S.cnt_dn = 0u;
+        S.done_dn = 0u;
+        S.cnt_fin = 0u;
+    }
+    if (dn_wg && threadIdx.x < 16 * MS_MAXM) {  // the down tile's rows of the first block input
+        const int m = threadIdx.x >> 4, r = threadIdx.x & 15;
+        S.xt[m][r] = m < M ? load_act(a.x, XDT, (int64_t)m * MS_H + t * 16 + r) : 0.0f;
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __syncthreads();  // the only workgroup barrier: counters set before either role uses them
+    __syncthreads();  // the only workgroup barrier
     bool dead = false;
     const MsAbort ab{a.err, a.epoch + 1, epoch};
     uint64_t* const hbuf = a.hbuf;
-    uint64_t* const pbuf = a.pbuf;
+    uint64_t* const xbuf = a.xbuf;
 
-    if (wave < MS_RW) {
-        // ===================== gate/up role =====================
-        const int p = wg;
+    if (!dn_wg) {
+        // ===================== gate/up =====================
+        // group grp (waves 8 grp .. 8 grp + 7) owns tile pair p; per block:
+        // poll this wave's x slice (the down workgroups' words) -> gate/up
+        // partial tiles -> the last of the eight stores h; the next block's
+        // weights are requested only after that store (loads issued earlier
+        // would hold up the store in the CU's memory pipeline), and they have
+        // the whole down half of the block to arrive
+        const int grp = wave / MS_RW, w = wave % MS_RW;
+        const int p = wg + MS_D0 * grp;
         if (p >= MS_I / 16) return;
-        const int w = wave;
         const int k0 = w * MS_SPAN;            // this wave's K slice [k0, k0 + 128)
         const uint32_t tile_bytes = (uint32_t)KS_GU * 1024u;
-        // this lane's slice elements: e = lane + 64 i (i < 2M): token e >> 7, k0 + (e & 127)
-        float xv[2 * MT];
         u32x4 A[U_GU][2];
         float gm[2] = {0.f, 0.f};
-        u32x4 sc[2];
+        u32x4 sc[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
         auto issue = [&](int l) {
             const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.gu[l], (uint32_t)(MS_I / 16) * 2u * tile_bytes);
 #pragma unroll
@@ -214,8 +274,8 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                                    wr, lane * 16, (uint32_t)(p * 2 + rt) * tile_bytes + (uint32_t)(w * U_GU + u) * 1024u,
                                    AUX_NT));
             if constexpr (GAM) {
-                gm[0] = a.gamma[l][k0 + lane];
-                gm[1] = a.gamma[l][k0 + 64 + lane];
+                gm[0] = a.gamma[l][k0 + 2 * lane];
+                gm[1] = a.gamma[l][k0 + 2 * lane + 1];
             }
             if constexpr (WF == WF_I8) {
 #pragma unroll
@@ -223,69 +283,47 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     sc[rt] = *reinterpret_cast<const u32x4*>(a.gu_scales[l] + (p * 2 + rt) * 16 + g * 4);
             }
         };
-        // the layer input: x as given
+        // this lane's elements of the slice: k0 + 2*lane + {0, 1} of every token
+        float xv[MT][2];
 #pragma unroll
-        for (int i = 0; i < 2 * MT; ++i)
-            xv[i] = (i >> 1) < M ? load_act(a.x, XDT, (int64_t)(i >> 1) * MS_H + k0 + (lane + 64 * (i & 1))) : 0.0f;
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) xv[m][e] = m < M ? load_act(a.x, XDT, (int64_t)m * MS_H + k0 + 2 * lane + e) : 0.0f;
         issue(0);
         for (int l = 0; l <= a.L; ++l) {
             if (l > 0) {
-                // x_l = round(x_{l-1} + ((P0 + P1) + P2) + P3) from the partials of block l-1
+                // x of block l: one word (two rows) per lane and token
                 const uint32_t tg = ms_tag(epoch, l - 1);
-                const uint64_t* P = pbuf + (size_t)((l - 1) & 1) * MS_Q * MS_MAXM * MS_H;
+                const uint64_t* X = xbuf + (size_t)((l - 1) & 1) * MS_MAXM * (MS_H / 2) + k0 / 2 + lane;
                 const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-                ms_wait(P + k0 + lane, tg, ab, t0, dead);  // quarter 0, token 0 of this lane's first element
+                unsigned it = 0;
+                uint64_t v[MT];
                 for (;;) {
-                    // tokens two at a time: 16 words in flight per lane
                     bool ok = true;
-                    float nx[2 * MT];
 #pragma unroll
-                    for (int m0 = 0; m0 < MT; m0 += 2) {
-                        uint64_t v[2][2][MS_Q];
-#pragma unroll
-                        for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-                            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                                for (int q = 0; q < MS_Q; ++q)
-                                    v[mm][h][q] = (m0 + mm < MT && m0 + mm < M)
-                                                      ? ms_load(P + ((size_t)q * MS_MAXM + m0 + mm) * MS_H + k0 + lane + 64 * h)
-                                                      : ((uint64_t)tg << 32);
-#pragma unroll
-                        for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-                            for (int h = 0; h < 2; ++h) {
-                                const int i = 2 * (m0 + mm) + h;
-                                if (i >= 2 * MT) continue;
-                                float sum = 0.0f;
-#pragma unroll
-                                for (int q = 0; q < MS_Q; ++q) {
-                                    ok = ok && (uint32_t)(v[mm][h][q] >> 32) == tg;
-                                    sum += __uint_as_float((uint32_t)v[mm][h][q]);
-                                }
-                                nx[i] = m0 + mm < M ? round_act<XDT>(xv[i] + sum) : xv[i];
-                            }
+                    for (int m = 0; m < MT; ++m) {
+                        v[m] = m < M ? ms_load(X + (size_t)m * (MS_H / 2)) : ((uint64_t)tg << 32);
+                        ok = ok && (uint32_t)(v[m] >> 32) == tg;
                     }
-                    if (__all(ok) || dead) {
+                    if (__all(ok) || dead) break;
+                    if (!ms_pause(ab, t0, it, dead)) break;
+                }
 #pragma unroll
-                        for (int i = 0; i < 2 * MT; ++i) xv[i] = nx[i];
-                        break;
-                    }
-                    if (!ms_pause(ab, t0, dead)) break;
+                for (int m = 0; m < MT; ++m) {
+                    const uint32_t w2 = (uint32_t)v[m];
+                    xv[m][0] = XDT == DT_BF16 ? bf16_bits_to_f32(w2 & 0xffffu) : f16_bits_to_f32(w2 & 0xffffu);
+                    xv[m][1] = XDT == DT_BF16 ? bf16_bits_to_f32(w2 >> 16) : f16_bits_to_f32(w2 >> 16);
                 }
             }
             if (l == a.L) {
-                // after the last block: workgroup 0 writes the result
-                if (wg == 0) {
-#pragma unroll
-                    for (int i = 0; i < 2 * MT; ++i)
-                        if ((i >> 1) < M)
-                            store_act(a.y, XDT, (int64_t)(i >> 1) * MS_H + k0 + lane + 64 * (i & 1), xv[i]);
-                    if (w == 0) {
-                        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                        if (lane == 0)
-                            __hip_atomic_store(a.epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
+                // workgroup 0: once all eight slices of the final x have been
+                // seen, every workgroup has read the epoch: advance it
+                if (wg == 0 && grp == 0) {
+                    unsigned old = 0;
+                    if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_fin, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    old = __shfl(old, 0);
+                    if (old == MS_RW - 1 && lane == 0)
+                        __hip_atomic_store(a.epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
                 break;
             }
@@ -293,13 +331,12 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             float ss[MT];
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const float a0 = xv[2 * m], a1 = xv[2 * m + 1];
+                const float a0 = xv[m][0], a1 = xv[m][1];
                 ss[m] = a0 * a0 + a1 * a1;
                 if (m < M) {
-                    const float b0 = GAM ? a0 * (1.0f + gm[0]) : a0;
-                    const float b1 = GAM ? a1 * (1.0f + gm[1]) : a1;
-                    S.bs[wave][m][lane] = (uint16_t)op_bits<WF>(b0);
-                    S.bs[wave][m][lane + 64] = (uint16_t)op_bits<WF>(b1);
+                    const uint32_t b0 = op_bits<WF>(GAM ? a0 * (1.0f + gm[0]) : a0);
+                    const uint32_t b1 = op_bits<WF>(GAM ? a1 * (1.0f + gm[1]) : a1);
+                    *reinterpret_cast<uint32_t*>(&S.bs[wave][m][2 * lane]) = b0 | (b1 << 16);
                 }
             }
 #pragma unroll
@@ -310,59 +347,100 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < U_GU; ++u) {
-                const auto b = ms_bops<WF>(S.bs[wave], u, lane, M);
+                const auto b = ms_bops<WF>(&S.bs[wave][0][0], MS_LROW, u * 4 * KE, lane, M);
                 accg = unit_mfma<WF, OPDT>(A[u][0], b, accg);
                 accu = unit_mfma<WF, OPDT>(A[u][1], b, accu);
             }
-            u32x4 sc_cur[2] = {sc[0], sc[1]};
-            if (l + 1 < a.L) issue(l + 1);  // the next block's weights stream during the hand-offs
             // reduce the eight slices: the last wave to arrive runs the epilogue
-            S.red_gu[w][0][lane] = accg;
-            S.red_gu[w][1][lane] = accu;
+            S.red_gu[grp][w][0][lane] = accg;
+            S.red_gu[grp][w][1][lane] = accu;
 #pragma unroll
             for (int m = 0; m < MT; ++m)
-                if (lane == m) S.red_ss[w][m] = ss[m];
+                if (lane == m) S.red_ss[grp][w][m] = ss[m];
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             unsigned old = 0;
-            if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_gu, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_gu[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             old = __shfl(old, 0);
-            if (old != MS_RW - 1) continue;
-            if (lane == 0) __hip_atomic_store(&S.cnt_gu, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            f32x4 gs = S.red_gu[0][0][lane], us = S.red_gu[0][1][lane];
+            if (old == MS_RW - 1) {
+                if (lane == 0) __hip_atomic_store(&S.cnt_gu[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                f32x4 gs = S.red_gu[grp][0][0][lane], us = S.red_gu[grp][0][1][lane];
 #pragma unroll
-            for (int v = 1; v < MS_RW; ++v) {
-                gs += S.red_gu[v][0][lane];
-                us += S.red_gu[v][1][lane];
-            }
-            float sst = 0.0f;
-            const int jj = j < M ? j : 0;
+                for (int v = 1; v < MS_RW; ++v) {
+                    gs += S.red_gu[grp][v][0][lane];
+                    us += S.red_gu[grp][v][1][lane];
+                }
+                float sst = 0.0f;
+                const int jj = j < M ? j : 0;
 #pragma unroll
-            for (int v = 0; v < MS_RW; ++v) sst += S.red_ss[v][jj];
-            const float inv = 1.0f / sqrtf(sst / (float)MS_H + a.eps);
-            if constexpr (WF == WF_I8) {
-                gs *= as_f32x4(sc_cur[0]);
-                us *= as_f32x4(sc_cur[1]);
-            }
-            uint32_t hb[4];
+                for (int v = 0; v < MS_RW; ++v) sst += S.red_ss[grp][v][jj];
+                const float inv = 1.0f / sqrtf(sst / (float)MS_H + a.eps);
+                if constexpr (WF == WF_I8) {
+                    gs *= as_f32x4(sc[0]);
+                    us *= as_f32x4(sc[1]);
+                }
+                uint32_t hb[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) hb[i] = op_bits<WF>(silu_f(gs[i] * inv) * (us[i] * inv));
-            if (j < M) {
-                const uint32_t tg = ms_tag(epoch, l);
-                uint64_t* hw = hbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_I / 2) + (p * 16 + g * 4) / 2;
-                ms_store(hw, tg, hb[0] | (hb[1] << 16));
-                ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
+                for (int i = 0; i < 4; ++i) hb[i] = op_bits<WF>(silu_f(gs[i] * inv) * (us[i] * inv));
+                if (j < M) {
+                    const uint32_t tg = ms_tag(epoch, l);
+                    uint64_t* hw = hbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_I / 2) + (p * 16 + g * 4) / 2;
+                    ms_store(hw, tg, hb[0] | (hb[1] << 16));
+                    ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
+                }
+                if (lane == 0) __hip_atomic_store(&S.done_gu[grp], (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+                ms_wait_lds(&S.done_gu[grp], (unsigned)(l + 1), ab, dead);
             }
+            if (l + 1 < a.L) issue(l + 1);  // the next block's weights stream during the hand-offs
+        }
+    } else if (wave < MS_RW) {
+        // ===================== h pollers of the down waves =====================
+        // wave w polls the h slice of down wave w (intermediate rows
+        // [448 w, 448 w + 448)) and deposits it in LDS; a poller issues no
+        // weight loads, so its polls never wait behind a weight stream
+        const int w = wave;
+        const uint64_t* hw0 = hbuf + (size_t)(MS_DSPAN / 2) * w;
+        for (int l = 0; l < a.L; ++l) {
+            const uint32_t tg = ms_tag(epoch, l);
+            const uint64_t* hl = hw0 + (size_t)(l & 1) * MS_MAXM * (MS_I / 2);
+            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            unsigned it = 0;
+            uint64_t v[MT][NH];
+            for (;;) {
+                bool ok = true;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+#pragma unroll
+                    for (int i = 0; i < NH; ++i) {
+                        const int e = lane + 64 * i;
+                        v[m][i] = (m < M && e < HWD) ? ms_load(hl + (size_t)m * (MS_I / 2) + e) : ((uint64_t)tg << 32);
+                        ok = ok && (uint32_t)(v[m][i] >> 32) == tg;
+                    }
+                if (__all(ok) || dead) break;
+                if (!ms_pause(ab, t0, it, dead)) break;
+            }
+            // LDS only once valid: the down wave may still be reading the
+            // previous block's slice until then (h of block l+1 exists only
+            // after this workgroup's x of block l has been published)
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int i = 0; i < NH; ++i) {
+                    const int e = lane + 64 * i;
+                    if (m < M && e < HWD) *reinterpret_cast<uint32_t*>(&S.bd[w][m][2 * e]) = (uint32_t)v[m][i];
+                }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) __hip_atomic_store(&S.hflag[w], (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     } else {
-        // ===================== down role =====================
+        // ===================== down =====================
+        // per block: the h slice (LDS, from the poller) -> partial tile ->
+        // the last of the eight adds the partials to x of the tile's rows and
+        // publishes them as 16-bit pairs (after the last block also as y);
+        // the next block's weights are requested after that
         const int d = wave - MS_RW;
-        const int t = wg / MS_Q, q = wg % MS_Q;
-        const int kq0 = q * (KS_DN / MS_Q);
-        int kb, kend;
-        wave_range<MS_RW>(kq0, kq0 + KS_DN / MS_Q, d, kb, kend);
-        const int n = kend - kb;
-        const int kspan = n * 4 * KE;             // K values of this wave (<= 128)
-        const int hk0 = kb * 4 * KE;              // first intermediate row
+        const int kb = d * U_DN;                  // this wave's k-steps [kb, kb + U_DN)
         const uint32_t tile_bytes = (uint32_t)KS_DN * 1024u;
         u32x4 A[U_DN];
         u32x4 sc = u32x4{0u, 0u, 0u, 0u};
@@ -372,58 +450,52 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             for (int u = 0; u < U_DN; ++u)
                 A[u] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               wr, u < n ? lane * 16 : OOB, (uint32_t)t * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
+                               wr, lane * 16, (uint32_t)t * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
             if constexpr (WF == WF_I8) sc = *reinterpret_cast<const u32x4*>(a.dn_scales[l] + t * 16 + g * 4);
         };
         issue(0);
         for (int l = 0; l < a.L; ++l) {
             const uint32_t tg = ms_tag(epoch, l);
-            const uint64_t* hl = hbuf + (size_t)(l & 1) * MS_MAXM * (MS_I / 2);
-            // words of token m: hl[m][hk0/2 + lane], lane < kspan/2
-            const bool mine = lane < kspan / 2;
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            ms_wait(mine ? hl + hk0 / 2 + lane : nullptr, tg, ab, t0, dead);
-            for (;;) {
-                bool ok = true;
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    if (m < M && mine) {
-                        const uint64_t v = ms_load(hl + (size_t)m * (MS_I / 2) + hk0 / 2 + lane);
-                        ok = ok && (uint32_t)(v >> 32) == tg;
-                        S.bs[wave][m][2 * lane] = (uint16_t)(v & 0xffffu);
-                        S.bs[wave][m][2 * lane + 1] = (uint16_t)((v >> 16) & 0xffffu);
-                    }
-                }
-                if (__all(ok) || dead) break;
-                if (!ms_pause(ab, t0, dead)) break;
-            }
-            lds_fence_wave();
+            ms_wait_lds(&S.hflag[d], (unsigned)(l + 1), ab, dead);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < U_DN; ++u) {
-                if (u < n) {
-                    const auto b = ms_bops<WF>(S.bs[wave], u, lane, M);
-                    acc = unit_mfma<WF, OPDT>(A[u], b, acc);
-                }
+                const auto b = ms_bops<WF>(&S.bd[d][0][0], MS_DROW, u * 4 * KE, lane, M);
+                acc = unit_mfma<WF, OPDT>(A[u], b, acc);
             }
-            const u32x4 sc_cur = sc;
-            if (l + 1 < a.L) issue(l + 1);
             S.red_dn[d][lane] = acc;
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             unsigned old = 0;
             if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_dn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             old = __shfl(old, 0);
-            if (old != MS_RW - 1) continue;
-            if (lane == 0) __hip_atomic_store(&S.cnt_dn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            f32x4 s = S.red_dn[0][lane];
+            if (old == MS_RW - 1) {
+                if (lane == 0) __hip_atomic_store(&S.cnt_dn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                f32x4 s = S.red_dn[0][lane];
 #pragma unroll
-            for (int v = 1; v < MS_RW; ++v) s += S.red_dn[v][lane];
-            if constexpr (WF == WF_I8) s *= as_f32x4(sc_cur);
-            if (j < M) {
-                uint64_t* pw = pbuf + (((size_t)(l & 1) * MS_Q + q) * MS_MAXM + j) * MS_H + t * 16 + g * 4;
+                for (int v = 1; v < MS_RW; ++v) s += S.red_dn[v][lane];
+                if constexpr (WF == WF_I8) s *= as_f32x4(sc);
+                if (j < M) {
+                    uint32_t xb[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ms_store(pw + i, tg, __float_as_uint(s[i]));
+                    for (int i = 0; i < 4; ++i) {
+                        const float xn = round_act<XDT>(S.xt[j][g * 4 + i] + s[i]);
+                        S.xt[j][g * 4 + i] = xn;
+                        xb[i] = XDT == DT_BF16 ? f32_to_bf16_bits(xn) : f32_to_f16_bits(xn);
+                    }
+                    uint64_t* xw = xbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_H / 2) + (t * 16 + g * 4) / 2;
+                    ms_store(xw, tg, xb[0] | (xb[1] << 16));
+                    ms_store(xw + 1, tg, xb[2] | (xb[3] << 16));
+                    if (l + 1 == a.L) {
+                        uint32_t* yw = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (size_t)j * MS_H + t * 16 + g * 4);
+                        yw[0] = xb[0] | (xb[1] << 16);
+                        yw[1] = xb[2] | (xb[3] << 16);
+                    }
+                }
+                if (lane == 0) __hip_atomic_store(&S.done_dn, (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            } else {
+                ms_wait_lds(&S.done_dn, (unsigned)(l + 1), ab, dead);
             }
+            if (l + 1 < a.L) issue(l + 1);  // the next block's weights stream during the hand-offs
         }
     }
 }
@@ -458,7 +530,7 @@ static hipError_t launch_ms1(const MlpStackArgs& a, hipStream_t st) {
 hipError_t launch_mlp_stack(const MlpStackArgs& a, int wf, int xdt, hipStream_t stream) {
     if (a.L < 1 || a.L > kMlpStackMaxLayers || a.M < 1 || a.M > mlp_stack_max_m()) return hipErrorInvalidValue;
     MlpStackArgs b = a;
-    b.pbuf = a.hbuf + (size_t)2 * MS_MAXM * (MS_I / 2);  // the partials follow the h words
+    b.xbuf = a.hbuf + MS_HWORDS;  // the x words follow the h words
     if (wf == WF_BF16 && xdt == DT_BF16) return launch_ms1<WF_BF16, DT_BF16>(b, stream);
     if (wf == WF_I8 && xdt == DT_F16) return launch_ms1<WF_I8, DT_F16>(b, stream);
     return hipErrorInvalidValue;

@@ -2,12 +2,12 @@
 persistent launch) against L calls of qw_mlp_fused and against the oracle's
 FP64 block composition.
 
-Bars: BF16 weights <= 1e-2 normwise vs FP64 on the BF16-rounded weights with
-x rounded to BF16 after every block (the persistent launch sums the down
-projection's K quarters in another order than qw_mlp_fused, so the two agree
-to a few BF16 roundings of the hidden state, <= 1e-2); INT8 weights <= 1e-3
-vs the FP32 dequant-then-matmul composition on the same q, s and x roundings.
-Every launch must leave the device error flag clear.
+Bars: BF16 weights <= 1e-2 normwise vs FP64 on the BF16-rounded weights
+with x rounded to BF16 after every block, and vs L qw_mlp_fused calls (the
+same math with the gate/up K slices summed in another grouping, which moves
+a BF16 rounding of the hidden state now and then); INT8 weights <= 1e-3 vs the dequant-then-matmul composition on
+the same q, s and F16 roundings.  Every launch must leave the device error
+flag clear.
 """
 import numpy as np
 import pytest
@@ -66,6 +66,9 @@ def test_mlp_stack_bf16(qw, ctx, oracle, relerr, M, L):
     assert ctx.device_error() == 0
     ref = _ref_bf16(oracle, layers, host(x0))
     assert relerr(host(y), ref) <= 1e-2
+    # same math as the per-block launches; the K slices of the gate/up
+    # reduction are summed in another grouping, which moves a BF16 rounding of
+    # the hidden state now and then
     assert relerr(host(y), host(z).astype(np.float64)) <= 1e-2
     # a second launch on other inputs (new epoch tags), in place
     x1 = dev(oracle.normal((M, H), 2299 + M), torch.bfloat16)
@@ -130,6 +133,9 @@ def test_mlp_stack_int8(qw, ctx, oracle, relerr, M):
     x0 = dev(oracle.normal((M, H), 2699), torch.float16)
     y = torch.empty_like(x0)
     qw.mlp_stack(ctx, gu, dn, x0, y, gammas=gms)
+    z = x0.clone()
+    for l in range(L):   # the two-launch INT8 MLP path (qw_mlp_fused's default for INT8)
+        qw.mlp_fused(ctx, gu[l], dn[l], z, z, gamma=gms[l], residual=z)
     torch.cuda.synchronize()
     assert ctx.device_error() == 0
     x = host(x0).astype(np.float64)
@@ -142,6 +148,7 @@ def test_mlp_stack_int8(qw, ctx, oracle, relerr, M):
         h = f16(g / (1.0 + np.exp(-g)) * u)
         x = f16(x + (h @ qd.astype(np.float64).T) * sd)
     assert relerr(host(y), x) <= 1e-3
+    assert relerr(host(y), host(z).astype(np.float64)) <= 1e-3
 
 
 def test_mlp_stack_graph_replays(qw, ctx, oracle, relerr):
