@@ -169,6 +169,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma-separated extra workloads to run (cfg1, cfg2, cfg3, "
+                    "prefill, gdn, attn, model, lmhead; default all), e.g. for a profiler pass over one of them")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="counter pass: only the dominant kernel (4 eager MLP stack launches) and a "
                          "64 MiB calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -307,9 +309,11 @@ def main():
 def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
     extra = {}
     steps = max(5, args.steps // 2)
+    only = set(filter(None, args.only.split(",")))
+    want = lambda name: not only or name in only
 
     # config 2: fused MLP at decode batches
-    for M in (8, 32, 128):
+    for M in ((8, 32, 128) if want("cfg2") else ()):
         hb = randn(M, H)
         g = graphed(qw, ctx, stream, lambda hb=hb: [qw.mlp_fused(ctx, gu[l], dn[l], hb, hb, gamma=gam[l], residual=hb)
                                                    for l in range(LAYERS)])
@@ -322,7 +326,25 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
                                         "tok_per_s_stack": round(M / (ms * 1e-3), 1)}
         log("cfg2", M, extra[f"cfg2_mlp_bf16_M{M}"])
 
-    # config 1: FP32 GEMV x[1,1024] . W[1024->3584], 36 rotating copies (528 MB)
+    extra.update(run_cfg1(qw, ctx, torch, timer, stream, randn, steps) if want("cfg1") else {})
+    extra.update(run_cfg3(qw, ctx, torch, timer, stream, randn, steps) if want("cfg3") else {})
+    if want("prefill"):
+        extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
+    if want("gdn"):
+        extra.update(run_gdn(qw, ctx, torch, timer, stream, randn, args))
+    if want("attn"):
+        extra.update(run_attn(qw, ctx, torch, timer, stream, randn, args))
+    if want("model"):
+        extra.update(run_decode_model(qw, ctx, torch, timer, stream, randn, args))
+    if want("lmhead"):
+        extra.update(run_lmhead(qw, ctx, torch, timer, stream, randn, steps))
+    torch.cuda.synchronize()
+    return extra
+
+
+def run_cfg1(qw, ctx, torch, timer, stream, randn, steps):
+    """Config 1: FP32 GEMV x[1,1024] . W[1024->3584], 36 rotating copies (528 MB)."""
+    extra = {}
     ws = []
     for _ in range(36):
         w = randn(I, H, std=0.02, dtype=torch.float32)
@@ -337,6 +359,12 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
                                  "pct_hbm": round(100 * b / ms / 1e6 / HBM_PEAK, 1)}
     log("cfg1", extra["cfg1_gemv_f32_M1"])
     del ws, g
+    return extra
+
+
+def run_cfg3(qw, ctx, torch, timer, stream, randn, steps):
+    """Config 3: INT8 weight-only projections of all 24 layers, FP16 activations."""
+    extra = {}
 
     # config 3: INT8 weight-only projections of all 24 layers, FP16 activations
     def i8(n, k):
@@ -402,13 +430,12 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         del g
     del layers
 
-    extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
+    return extra
 
-    extra.update(run_gdn(qw, ctx, torch, timer, stream, randn, args))
-    extra.update(run_attn(qw, ctx, torch, timer, stream, randn, args))
-    extra.update(run_decode_model(qw, ctx, torch, timer, stream, randn, args))
 
-    # config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each
+def run_lmhead(qw, ctx, torch, timer, stream, randn, steps):
+    """Config 5: tied lm_head + greedy argmax, BF16 and INT8, 2 rotating copies each."""
+    extra = {}
     for fmt, name in ((qw.WFMT_BF16, "bf16"), (qw.WFMT_INT8, "int8")):
         Es = []
         for c in range(2):
