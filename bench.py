@@ -170,7 +170,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma-separated extra workloads to run (cfg1, cfg2, cfg3, "
-                    "prefill, gdn, attn, model, lmhead; default all), e.g. for a profiler pass over one of them")
+                    "int8gemv, prefill, gdn, attn, model, lmhead; default all), e.g. for a profiler pass over one of them")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="counter pass: only the dominant kernel (4 eager MLP stack launches) and a "
                          "64 MiB calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -328,6 +328,7 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
 
     extra.update(run_cfg1(qw, ctx, torch, timer, stream, randn, steps) if want("cfg1") else {})
     extra.update(run_cfg3(qw, ctx, torch, timer, stream, randn, steps) if want("cfg3") else {})
+    extra.update(run_int8_gemv(qw, ctx, torch, timer, stream, randn, steps) if want("int8gemv") else {})
     if want("prefill"):
         extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
     if want("gdn"):
@@ -431,6 +432,49 @@ def run_cfg3(qw, ctx, torch, timer, stream, randn, steps):
     del layers
 
     return extra
+
+
+def run_int8_gemv(qw, ctx, torch, timer, stream, randn, steps):
+    """The north star's own kernel line: one INT8 weight-only decode GEMV at
+    M=1 (x[1,1024] F16 times an INT8 W[3584,1024] with per-row scales), 80
+    distinct weights (294 MB, beyond the 256 MB Infinity Cache) replayed from
+    a graph, so every launch streams its 3.67 MB from HBM; and the same for
+    the gate/up GLU pair (7.3 MB per launch, SiLU*mul fused)."""
+    out = {}
+    n_copies = 80
+
+    def i8(n, k, seed):
+        q = torch.randint(-127, 128, (n, k), generator=torch.Generator(device="cuda").manual_seed(seed),
+                          device="cuda", dtype=torch.int8)
+        s = torch.rand(n, generator=torch.Generator(device="cuda").manual_seed(seed + 1), device="cuda") * 1e-3 + 1e-4
+        return q, s
+
+    x = randn(1, H, dtype=torch.float16)
+    ws = []
+    for c in range(n_copies):
+        q, s_ = i8(I, H, 7000 + 2 * c)
+        ws.append(qw.Weight.pack_device(ctx, q, qw.WFMT_INT8, scales=s_))
+    y = torch.empty(1, I, device="cuda", dtype=torch.float16)
+    g = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, w, x, y) for w in ws])
+    us = 1e3 * timer.run(g.launch, max(5, steps), 2) / n_copies
+    b = I * H + I * 4 + H * 2 + I * 2
+    out["int8_gemv_3584x1024_M1"] = {"us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                                     "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK, 1), "bytes_per_launch": b}
+    log("int8 gemv", out["int8_gemv_3584x1024_M1"])
+    del g, ws
+    gus = []
+    for c in range(n_copies // 2):
+        qg, sg = i8(I, H, 8000 + 4 * c)
+        qu, su = i8(I, H, 8002 + 4 * c)
+        gus.append(qw.Weight.pack_glu_device(ctx, qg, qu, qw.WFMT_INT8, sg, su))
+    g = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, w, x, y) for w in gus])
+    us = 1e3 * timer.run(g.launch, max(5, steps), 2) / len(gus)
+    b = 2 * I * H + 2 * I * 4 + H * 2 + I * 2
+    out["int8_gemv_gateup_glu_M1"] = {"us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                                      "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK, 1), "bytes_per_launch": b}
+    log("int8 gemv glu", out["int8_gemv_gateup_glu_M1"])
+    del g, gus
+    return out
 
 
 def run_lmhead(qw, ctx, torch, timer, stream, randn, steps):
