@@ -17,7 +17,8 @@
 #include "qw_internal.hpp"
 #include "qw_kernels.hpp"
 
-constexpr int kGemmMinM = 33;  // default token count from which the MFMA GEMM is used
+constexpr int kGemmMinM = 33;
+constexpr int kWideMinM = 17;  // default token count from which the weight-stationary kernel is used  // default token count from which the MFMA GEMM is used
 constexpr int kGdnChunkMin = 24;  // tokens per sequence from which the chunked Gated-DeltaNet form runs (measured crossover 20-26)
 
 struct qw_ctx {
@@ -37,6 +38,12 @@ struct qw_ctx {
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     int gemm_splitk = 0;         // K splits per GEMM tile (QW_GEMM_SPLITK; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
+    bool wide = true;            // weight-stationary kernel for wide_min..wide_max tokens (QW_WIDE=0: off)
+    int wide_min = kWideMinM;    // QW_WIDE_MIN
+    int wide_max = qwk::kWideMaxM;  // QW_WIDE_MAX
+    int wide_s = 0;              // K splits (QW_WIDE_S; 0 = planned)
+    int wide_dbg = 0;            // QW_WIDE_DBG: timing probes (wrong results)
+    int wide_cfg = 0;            // blocks x waves per block (QW_WIDE_CFG 1: 4x1, 2: 2x2, 3: 1x4; 0 = planned)
     int attn_split = 0;          // keys per decode split, 0 = by size (QW_ATTN_SPLIT forces a multiple of 64)
     int attn_vcoal = -1;         // INT8 decode V loads: -1 by launch size, 0 scattered, 1 coalesced (QW_ATTN_VCOAL)
     bool attn_fused = true;      // one-launch INT8 decode attention (QW_ATTN_FUSED=0: prep / split / combine)
@@ -190,6 +197,12 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_ATTN_VCOAL")) c->attn_vcoal = atoi(v) != 0 ? 1 : 0;
     if (const char* v = getenv("QW_ATTN_PREFILL_MIN")) c->attn_prefill_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_GDN_CHUNK_MIN")) c->gdn_chunk_min = std::max(1, atoi(v));
+    if (const char* v = getenv("QW_WIDE")) c->wide = atoi(v) != 0;
+    if (const char* v = getenv("QW_WIDE_MIN")) c->wide_min = std::max(1, atoi(v));
+    if (const char* v = getenv("QW_WIDE_MAX")) c->wide_max = std::min(qwk::kWideMaxM, atoi(v));
+    if (const char* v = getenv("QW_WIDE_S")) c->wide_s = std::max(0, atoi(v));
+    if (const char* v = getenv("QW_WIDE_DBG")) c->wide_dbg = atoi(v);
+    if (const char* v = getenv("QW_WIDE_CFG")) c->wide_cfg = std::max(0, std::min(3, atoi(v)));
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;
@@ -655,6 +668,70 @@ static qw_status run_skinny(qw_ctx* ctx, const qw_weight* W, const void* x, qw_d
     return QW_OK;
 }
 
+// Weight-stationary launch (qw_wide.hip) for wide_min..wide_max tokens.
+// Returns QW_ERR_SHAPE without launching when no configuration fits, so the
+// caller can take the small-M kernels instead.
+static qw_status run_wide(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt, int ldx, int M, void* y,
+                          qw_dtype ydt, int ldy, const qw_epilogue* ep, hipStream_t stream) {
+    qwk::WideArgs wa{};
+    qwk::SkinnyArgs& a = wa.s;
+    a.w = W->packed;
+    a.scales = W->scales;
+    a.x = x;
+    a.ldx = ldx;
+    a.M = M;
+    a.K = W->K;
+    a.N = W->N;
+    a.n_groups = (W->N + 15) / 16;
+    a.ksteps = W->ksteps;
+    a.flags = ep ? ep->flags : 0u;
+    if (ep && (ep->flags & QW_EP_RESIDUAL)) {
+        a.res = ep->residual;
+        a.res_dt = ep->residual_dtype;
+        a.ld_res = ep->ld_residual ? ep->ld_residual : W->N;
+    }
+    if (ep && (ep->flags & QW_EP_NORM_X)) {
+        a.gamma = ep->gamma;
+        a.eps = ep->eps;
+    }
+    a.y = y;
+    a.ydt = ydt;
+    a.ldy = ldy;
+    if (ep && (ep->flags & QW_EP_SPLIT)) {
+        a.y2 = ep->y2;
+        a.split_period = ep->split_period;
+    }
+    bool vec = (W->N % 4 == 0) && (ldy % 4 == 0) && aligned(y, 16);
+    if (a.flags & QW_EP_SPLIT) vec = vec && aligned(a.y2, 16);
+    if (a.flags & QW_EP_RESIDUAL) vec = vec && (a.ld_res % 4 == 0) && aligned(a.res, 16);
+    a.vec_store = vec ? 1 : 0;
+    a.partials = ctx->partials;
+    a.counters = ctx->counters;
+    qwk::WidePlan p{};
+    if (!qwk::wide_plan(a, W->wf, W->glu != 0, ctx->num_cus, ctx->partials_bytes, kMaxCounters, ctx->wide_s,
+                        ctx->wide_cfg, p))
+        return QW_ERR_SHAPE;
+    if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * dsize(xdt) >= (1ull << 32))
+        return QW_ERR_SHAPE;
+    a.S = p.S;
+    wa.nblocks = p.nblocks;
+    wa.n_ptiles = p.n_ptiles;
+    wa.off_gamma = p.off_gamma;
+    wa.off_res = p.off_res;
+    wa.off_scales = p.off_scales;
+    wa.res_lds = p.res_lds;
+    wa.T = p.T;
+    wa.Mg = p.Mg;
+    wa.ngrp = p.ngrp;
+    wa.dbg = ctx->wide_dbg;
+    if (ctx->wide_dbg & 8)
+        fprintf(stderr, "wide N=%d K=%d M=%d glu=%d: S=%d T=%d NB=%d KW=%d CT=%d grid=%d smem=%zu\n", W->N, W->K, M,
+                W->glu, p.S, p.T, p.NB, p.KW, p.CT, p.grid, p.smem);
+    hipError_t e = qwk::launch_wide(wa, p, W->wf, (int)xdt, W->glu != 0, stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "weight-stationary kernel launch");
+    return QW_OK;
+}
+
 // MFMA GEMM launch for many tokens: BF16 weights with BF16 activations, INT8
 // weights with F16 or BF16 activations.
 static bool gemm_ok(const qw_weight* W, qw_dtype xdt) {
@@ -819,6 +896,12 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     if (W && ldy == 0) ldy = (ep && (ep->flags & QW_EP_SPLIT)) ? W->N / 2 : W->N;
     qw_status s = check_linear(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, true);
     if (s != QW_OK) return s;
+    // weight-stationary kernel: every weight byte once for all tokens
+    if (ctx->wide && !(ctx->gemm_forced && M >= ctx->gemm_min_m) && M >= ctx->wide_min && M <= ctx->wide_max &&
+        qwk::wide_supported(W->wf, (int)xdt, M)) {
+        s = run_wide(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, stream);
+        if (s != QW_ERR_SHAPE) return s;
+    }
     if (const int rows = gemm_route(ctx, W, xdt, M)) {
         const bool norm = ep && (ep->flags & QW_EP_NORM_X);
         if (!norm) return run_gemm(ctx, W, rows, x, xdt, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream);

@@ -85,24 +85,6 @@ template <int BM, int NW, int WF, int RW> struct GTile {
     }
 };
 
-// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
-// memory operations are outstanding, leaving the other counters alone
-constexpr unsigned vm_wait(int n) { return 0x0F70u | ((unsigned)n & 15u) | (((unsigned)n >> 4) << 14); }
-
-// One 1 KB unit global -> LDS (buffer_load_dwordx4 ... lds; M0 = LDS base of
-// the unit, lane l lands at +16*l).  Written as inline assembly so that the
-// compiler does not treat the asynchronous LDS write as a hazard for the
-// later LDS reads and wait for every load in flight: the K-loop waits for
-// exactly the stage it consumes (vector-memory counters retire in order)
-// and a barrier publishes it.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds_unit, uint32_t voff) {
-    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds_unit;
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(m0), "v"(voff), "s"(rs)
-                 : "memory", "m0");
-}
-
 // Element-wise store for outputs whose row count or alignment rules out the
 // 4-wide stores.
 __device__ __forceinline__ void gemm_store_slow(const GemmArgs& a, int m, int row, f32x4 o4) {

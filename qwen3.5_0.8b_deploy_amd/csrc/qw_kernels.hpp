@@ -61,6 +61,36 @@ hipError_t launch_gemv(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argm
 hipError_t launch_skinny(const SkinnyArgs& a, int wf, int xdt, bool glu, bool argmax, int nw, int grid,
                          hipStream_t stream);
 
+// Weight-stationary projection for 17..512 tokens (qw_wide.hip): BF16
+// weights with BF16 activations, INT8 weights with F16 activations; no
+// argmax.  The host plans the K splits and the workgroup shape (wide_plan).
+constexpr size_t kWideMaxLds = 144 * 1024;
+constexpr int kWideMaxM = 512;
+struct WideArgs {
+    SkinnyArgs s;      // operands, epilogue, split count (s.S), counters and partials
+    int nblocks;       // blocks of two physical 16-row tiles (GLU: one gate/up pair)
+    int n_ptiles;      // physical tiles of the packed weight
+    int off_gamma;     // LDS offsets of the norm-weight slice, residual tiles, scales
+    int off_res;
+    int off_scales;
+    int res_lds;       // 1: the residual is staged in LDS (4-wide aligned path)
+    int T;             // token groups (each Mg tokens, its own workgroups)
+    int Mg;
+    int ngrp;          // block groups (NB blocks each; a multiple of 8 when T > 1)
+    int dbg;           // timing probes only (wrong results): 1 no MFMAs, 2 no split-K hand-off, 4 no staging
+};
+struct WidePlan {
+    int S, T, Mg, ngrp, NB, KW, CT, grid;
+    size_t smem;
+    int off_gamma, off_res, off_scales, nblocks, n_ptiles, res_lds;
+};
+bool wide_supported(int wf, int xdt, int M);
+// false when no configuration fits (LDS, workspace); force_s / force_cfg
+// (1..3: 4x1, 2x2, 1x4 blocks x waves per block) pin the choice when nonzero
+bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partials_cap, int max_counters, int force_s,
+               int force_cfg, WidePlan& p);
+hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream);
+
 // LDS double-buffered MFMA GEMM for many tokens (qw_gemm.hip).
 struct GemmArgs {
     const uint8_t* w;        // packed weight

@@ -1,0 +1,601 @@
+// qw_wide.hip -- weight-stationary projection kernel for 17..256 tokens
+// (decode at larger batches, short prefill chunks) on gfx950.
+//
+// Every weight byte is read from HBM exactly once per launch, for all M
+// tokens: a wave holds a block of two 16-row tiles (a gate/up pair for GLU
+// weights) of one K range in MFMA A registers, and runs them against every
+// token tile of the activations, which sit in LDS.  The tokens are the MFMA
+// N side (16 per tile, up to 16 tiles), so the weights are the stationary
+// operand and the activations are re-read from LDS, not from HBM.
+//
+// Work decomposition.  K is cut into S splits so that the activation slice
+// [M][K/S] of a split fits the workgroup's LDS.  A workgroup is one split of
+// NB blocks; its NB x KW waves split the split's K range KW ways per block.
+// The grid is (blocks / NB) x S workgroups, sized on the host to fill the
+// CUs once (one workgroup per CU; no grid-stride loop), and workgroup w
+// takes split w % S, so the workgroups of one XCD (w % 8) share one
+// activation slice in their L2.
+//
+// Data flow of a workgroup.
+//   1. Direct-to-LDS loads (buffer_load_dwordx4 ... lds, no VGPRs) bring the
+//      activation slice in MFMA B-operand order: one 1 KB unit per (k-step,
+//      token tile) in which lane l = r + 16 g holds the 8 k of token r the
+//      MFMA reads from that lane.  The RMSNorm weight slice, the INT8 row
+//      scales and the residual rows of the epilogue come the same way.
+//   2. The weight k-steps of the wave are issued next (up to U per wave in
+//      flight, unconditionally; unused slots read out of range), so the
+//      small loads above are ahead of them in the in-order vector-memory
+//      counter: one s_waitcnt vmcnt(U*RT) and a barrier publish them.
+//   3. RMSNorm prologue (when asked): one LDS pass takes the per-token sums of
+//      squares of the split's range (fixed order) and multiplies (1 + gamma)
+//      into the staged activations.
+//   4. MFMAs (16x16x32 bf16, or f16 on exactly converted INT8 units), each
+//      weight unit against all token tiles; further weight chunks are issued
+//      after a chunk is consumed.
+//   5. The KW partial tiles of a block meet in LDS (fixed order); the split
+//      partials meet through the workspace: agent-scope (sc1) 16-byte stores,
+//      s_waitcnt, one arrival count per block; the last of the S workgroups
+//      sums the S partials in split order (deterministic), returns the counter
+//      to zero (graph-safe, no memset) and runs the epilogue.
+//   6. Epilogue: 1/rms, INT8 row scale, SiLU(gate)*up, residual, Q/gate
+//      de-interleave, 4-wide stores.
+//
+// Reference operators replaced at these token counts: the grid (N, M)
+// int8_gemv_batch_kernel (mlp_cuda.cu:158-180), which reads every weight row
+// once per token, and the cuBLAS GemmEx / SGEMM calls of the batch forward
+// paths (bf16_gemm.cuh:89, cublas_utils.cuh:60-83).
+#include "qw_stream.hpp"
+
+namespace qwk {
+
+constexpr int kWideMaxS = 8;  // K splits per launch: the finishing wave loads all of them at once
+
+template <int WF> struct WideT {
+    static constexpr int KS = 4 * WTraits<WF>::KE;  // K elements per k-step
+    static constexpr int XU = WF == WF_I8 ? 2 : 1;  // LDS units per (k-step, token tile)
+    static constexpr int KEW = WTraits<WF>::KE;     // K elements per lane group of a k-step
+};
+
+// Residual region of a block's output tile: [CT*16 tokens][16 rows] elements
+// of rs bytes, in 1 KB units of 32 (rs = 2) or 16 (rs = 4) tokens.
+__device__ __forceinline__ int res_units(int CT, int rs) { return CT * rs / 4; }
+
+template <int WF, int XDT, int CT, bool GLU, int NB, int KW, int U>
+__global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
+    constexpr int NW = NB * KW;
+    constexpr int RT = 2;                 // physical tiles per block
+    constexpr int RO = GLU ? 1 : 2;       // output tiles per block
+    constexpr int KS = WideT<WF>::KS, XU = WideT<WF>::XU, KEW = WideT<WF>::KEW;
+    static_assert(WF == WF_BF16 || WF == WF_I8, "16-bit MFMA weight formats only");
+    static_assert((WF == WF_BF16 && XDT == DT_BF16) || (WF == WF_I8 && XDT == DT_F16),
+                  "activations arrive in the MFMA input type");
+    const SkinnyArgs& a = wa.s;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float ss_tok[CT * 16];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int S = a.S;
+    // workgroup -> (block group bg, token group t, split s); the T token
+    // groups of a block group sit 8 workgroups apart, i.e. on one XCD, where
+    // the later ones find its weights in L2
+    const int T = wa.T;
+    const int s = (int)blockIdx.x % S;
+    const int q = (int)blockIdx.x / S;
+    const int t = T > 1 ? (q / 8) % T : 0;
+    const int bg = T > 1 ? (q % 8) + 8 * (q / (8 * T)) : q;
+    const int M0 = t * wa.Mg;                 // this workgroup's tokens [M0, M0 + Mt)
+    const int Mt = min(wa.Mg, a.M - M0);
+    const int cgrp = bg * T + t;              // counter / partials group
+    const int bl = wave / KW, kw = wave % KW;
+    const int blk = bg * NB + bl;
+    const bool blk_ok = blk < wa.nblocks;
+    const bool norm = (a.flags & EP_NORM) != 0;
+    const bool gam = norm && a.gamma != nullptr;
+    const bool want_res = (a.flags & EP_RESIDUAL) != 0;
+
+    // this workgroup's split [ks0, ks1) and the wave's part [kb, kend)
+    const int ks0 = (s * a.ksteps) / S, ks1 = ((s + 1) * a.ksteps) / S;
+    const int nks = ks1 - ks0;
+    const int kb0 = ks0 + (kw * nks) / KW, kend = ks0 + ((kw + 1) * nks) / KW;
+
+    // ---- 1. small operands, direct to LDS ----
+    const int xunits = CT * nks * XU;
+    uint8_t* const xl = lds;
+    uint8_t* const gl = lds + wa.off_gamma;
+    uint8_t* const rl = lds + wa.off_res;
+    uint8_t* const sl = lds + wa.off_scales;
+    {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2));
+        for (int u = wave; u < ((wa.dbg & 4) ? 0 : xunits); u += NW) {
+            const int h = u % XU, t = u / XU;
+            const int ct = t % CT, ksr = t / CT;
+            const int m = ct * 16 + r;
+            const int k = (ks0 + ksr) * KS + g * KEW + h * 8;
+            lds_dma16(xr, xl + u * 1024, m < Mt ? (uint32_t)(((M0 + m) * a.ldx + k) * 2) : OOB);
+        }
+        if (gam) {
+            const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.gamma, (uint32_t)a.K * 4u);
+            const int gunits = (nks * KS * 4 + 1023) / 1024;
+            for (int u = wave; u < gunits; u += NW) {
+                const int k = ks0 * KS + u * 256 + lane * 4;
+                lds_dma16(gr, gl + u * 1024, k < ks1 * KS ? (uint32_t)(k * 4) : OOB);
+            }
+        }
+        if (wa.res_lds && want_res) {
+            // residual rows of the block's output tiles: [token][16 rows]
+            const int rs = a.res_dt == DT_F32 ? 4 : 2;
+            const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.res, (uint32_t)((uint64_t)a.M * a.ld_res * rs));
+            const int per = res_units(CT, rs);
+            for (int u = wave; u < NB * RO * per; u += NW) {
+                const int bt = u / per, j = u % per;  // bt = block-in-group * RO + output tile
+                const int b2 = bg * NB + bt / RO;
+                const int row0 = (GLU ? b2 : b2 * 2 + bt % RO) * 16;
+                const int tpu = 1024 / (16 * rs);  // tokens per unit: 32 (16-bit) or 16 (FP32)
+                const int lpt = 64 / tpu;          // lanes per token, 16 / lpt rows each
+                const int tok = j * tpu + lane / lpt;
+                const int rofs = (lane % lpt) * (16 / lpt);
+                const bool ok = b2 < wa.nblocks && tok < Mt && row0 < a.N;
+                lds_dma16(rr, rl + u * 1024,
+                          ok ? (uint32_t)(((int64_t)(M0 + tok) * a.ld_res + row0 + rofs) * rs) : OOB);
+            }
+        }
+        if (a.scales) {
+            const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.scales, (uint32_t)wa.n_ptiles * 64u);
+            for (int u = wave; u < NB; u += NW) {
+                const int b2 = bg * NB + u;
+                lds_dma16(sr, sl + u * 1024, lane < 8 && b2 < wa.nblocks ? (uint32_t)((b2 * 32 + lane * 4) * 4) : OOB);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 2. weights: the first chunk of this wave's k-steps ----
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)wa.n_ptiles * a.ksteps * 1024u));
+    const uint32_t tile_bytes = (uint32_t)a.ksteps * 1024u;
+    uint32_t tbase[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const int pt = blk * 2 + rt;
+        tbase[rt] = blk_ok && pt < wa.n_ptiles ? (uint32_t)pt * tile_bytes + lane * 16 : OOB;
+    }
+    u32x4 A[U][RT];
+    auto issue = [&](int k0, int n) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+                A[u][rt] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               wrs, (u < n && tbase[rt] != OOB) ? tbase[rt] + (uint32_t)(k0 + u) * 1024u : OOB, 0,
+                               AUX_NT));
+    };
+    int kb = kb0;
+    int n = min(U, kend - kb);
+    issue(kb, n);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vm_wait(U * RT));  // everything issued before the weights has landed
+    __syncthreads();
+
+    // ---- 3. RMSNorm prologue: sums of squares of the split, (1 + gamma) ----
+    if (norm) {
+        for (int ct = wave; ct < CT; ct += NW) {
+            float ss = 0.0f;
+            for (int ksr = 0; ksr < nks; ++ksr) {
+#pragma unroll
+                for (int h = 0; h < XU; ++h) {
+                    uint8_t* p = xl + ((ksr * CT + ct) * XU + h) * 1024 + lane * 16;
+                    u32x4 raw = *reinterpret_cast<u32x4*>(p);
+                    float f[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t hb = (raw[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+                        f[e] = XDT == DT_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+                        ss += f[e] * f[e];
+                    }
+                    if (gam) {
+                        const float* gp = reinterpret_cast<const float*>(gl) + ksr * KS + g * KEW + h * 8;
+                        const f32x4 g0 = reinterpret_cast<const f32x4*>(gp)[0];
+                        const f32x4 g1 = reinterpret_cast<const f32x4*>(gp)[1];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            f[e] *= 1.0f + g0[e];
+                            f[e + 4] *= 1.0f + g1[e];
+                        }
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            raw[q] = op_bits<WF>(f[2 * q]) | (op_bits<WF>(f[2 * q + 1]) << 16);
+                        *reinterpret_cast<u32x4*>(p) = raw;
+                    }
+                }
+            }
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (g == 0) ss_tok[ct * 16 + r] = ss;
+        }
+        __syncthreads();
+    }
+
+    // ---- 4. MFMAs ----
+    f32x4 acc[RT][CT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto step = [&](int u, int ksr) {
+        const uint8_t* xp = xl + (ksr * CT * XU) * 1024 + lane * 16;
+        if constexpr (WF == WF_BF16) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const bf16x8 b = *reinterpret_cast<const bf16x8*>(xp + ct * 1024);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_bf16(__builtin_bit_cast(bf16x8, A[u][rt]), b, acc[rt][ct]);
+            }
+        } else {
+            f16x8 a0[RT], a1[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) i8unit_to_f16(A[u][rt], a0[rt], a1[rt]);
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const f16x8 b0 = *reinterpret_cast<const f16x8*>(xp + ct * 2048);
+                const f16x8 b1 = *reinterpret_cast<const f16x8*>(xp + ct * 2048 + 1024);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
+                    acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
+                }
+            }
+        }
+    };
+    for (;;) {
+        if (wa.dbg & 1) {
+        } else if (n == U) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) step(u, kb + u - ks0);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (u < n) step(u, kb + u - ks0);
+        }
+        kb += n;
+        if (kb >= kend) break;
+        n = min(U, kend - kb);
+        issue(kb, n);
+    }
+
+    // ---- 5. reduction over the KW parts and the S splits ----
+    // The workgroup's output is NB blocks x CT token tiles ("units", each
+    // both physical tiles of a block for one token tile).  Every wave writes
+    // its accumulators to LDS (over the activations), then wave w owns units
+    // w, w + NW, ...: it sums their KW parts in a fixed order and, with S > 1,
+    // hands them over through the workspace.  The last workgroup of a block
+    // group to arrive loads all S partials of its units at once, sums them
+    // in split order and runs their epilogue, so the epilogue is spread over
+    // all waves.
+    constexpr int NU = NB * CT;                 // units per workgroup
+    constexpr int UPW = (NU + NW - 1) / NW;     // units per wave (upper bound)
+    __syncthreads();                            // every wave is done with the activations
+    {
+        f32x4* red = reinterpret_cast<f32x4*>(lds);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) red[(((bl * KW + kw) * RT + rt) * CT + ct) * 64 + lane] = acc[rt][ct];
+    }
+    __syncthreads();
+    f32x4 u_acc[UPW][RT];
+    float u_ss[UPW];
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {
+        const int u = wave + i * NW;
+        const int ub = u / CT, uc = u % CT;
+        const f32x4* red = reinterpret_cast<const f32x4*>(lds);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (u < NU) {
+#pragma unroll
+                for (int k2 = 0; k2 < KW; ++k2) v += red[(((ub * KW + k2) * RT + rt) * CT + uc) * 64 + lane];
+            }
+            u_acc[i][rt] = v;
+        }
+        u_ss[i] = (norm && u < NU) ? ss_tok[uc * 16 + r] : 0.0f;
+    }
+
+    if (S > 1 && !(wa.dbg & 2)) {
+        // partials: [group][split][unit][lane] RT x 16 bytes, then the sums of
+        // squares [group][split][unit][lane] x 4 bytes; device-coherent (sc1)
+        const int ngrp = wa.ngrp * T;
+        const uint64_t vbytes = (uint64_t)ngrp * S * NU * 64 * RT * 16;
+        const uint64_t pbytes = vbytes + (uint64_t)ngrp * S * NU * 64 * 4;
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials, (uint32_t)min(pbytes, (uint64_t)0x7fffffff));
+        auto voff = [&](int s2, int u, int rt) {
+            return (uint32_t)(((((uint64_t)cgrp * S + s2) * NU + u) * 64 + lane) * RT + rt) * 16u;
+        };
+        auto soff = [&](int s2, int u) {
+            return (uint32_t)(vbytes + ((((uint64_t)cgrp * S + s2) * NU + u) * 64 + lane) * 4u);
+        };
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) {
+            const int u = wave + i * NW;
+            if (u < NU) {
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, u_acc[i][rt]), prs, voff(s, u, rt),
+                                                           0, AUX_SC1);
+                if (norm) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(u_ss[i]), prs, soff(s, u), 0, AUX_SC1);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __shared__ unsigned last_s;
+        __syncthreads();  // every wave's partials are complete
+        if (threadIdx.x == 0) {
+            const unsigned old = __hip_atomic_fetch_add(&a.counters[cgrp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last_s = old == (unsigned)(S - 1) ? 1u : 0u;
+            if (old == (unsigned)(S - 1)) __hip_atomic_store(&a.counters[cgrp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_s) return;  // uniform over the workgroup
+        // all S partials of this wave's units in flight at once, then summed
+        // in split order
+#pragma unroll
+        for (int i = 0; i < UPW; ++i) {
+            const int u = wave + i * NW;
+            if (u >= NU) continue;
+            f32x4 pv[kWideMaxS][RT];
+            float ps[kWideMaxS];
+#pragma unroll
+            for (int s2 = 0; s2 < kWideMaxS; ++s2) {
+                if (s2 < S) {
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        pv[s2][rt] = __builtin_bit_cast(
+                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff(s2, u, rt), 0, AUX_SC1));
+                    ps[s2] = norm ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, soff(s2, u), 0, AUX_SC1))
+                                  : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) u_acc[i][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            u_ss[i] = 0.0f;
+#pragma unroll
+            for (int s2 = 0; s2 < kWideMaxS; ++s2) {
+                if (s2 < S) {
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) u_acc[i][rt] += pv[s2][rt];
+                    u_ss[i] += ps[s2];
+                }
+            }
+        }
+    }
+
+    // ---- 6. epilogue of this wave's units ----
+    const int rs = a.res_dt == DT_F32 ? 4 : 2;
+#pragma unroll
+    for (int i = 0; i < UPW; ++i) {
+        const int u = wave + i * NW;
+        if (u >= NU) continue;
+        const int ub = u / CT, ct = u % CT;
+        const int blk2 = bg * NB + ub;
+        const int m = ct * 16 + r;
+        if (blk2 >= wa.nblocks || m >= Mt) continue;
+        const float inv = norm ? 1.0f / sqrtf(u_ss[i] / (float)a.K + a.eps) : 1.0f;
+        f32x4 sc[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            sc[rt] = a.scales ? *reinterpret_cast<const f32x4*>(sl + ub * 1024 + (rt * 16 + g * 4) * 4)
+                              : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+        for (int ro = 0; ro < RO; ++ro) {
+            const int tile = GLU ? blk2 : blk2 * 2 + ro;
+            const int o = tile * 16 + g * 4;
+            if (o >= a.N) continue;
+            f32x4 v;
+            if constexpr (GLU) {
+                const f32x4 gt = u_acc[i][0] * inv * sc[0];
+                const f32x4 up = u_acc[i][1] * inv * sc[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = silu_f(gt[e]) * up[e];
+            } else {
+                v = u_acc[i][ro] * inv * sc[ro];
+            }
+            if (a.vec_store) {
+                if (want_res) {
+                    const uint8_t* rp = rl + (ub * RO + ro) * res_units(CT, rs) * 1024 + (m * 16 + g * 4) * rs;
+                    if (rs == 4) {
+                        v += *reinterpret_cast<const f32x4*>(rp);
+                    } else {
+                        const u32x2 w = *reinterpret_cast<const u32x2*>(rp);
+                        v += epi_res(a.res_dt, u32x4{0u, 0u, 0u, 0u}, w);
+                    }
+                }
+                void* dst = a.y;
+                int col = o;
+                if (a.flags & EP_SPLIT) {
+                    const int sb = o / a.split_period;
+                    dst = (sb & 1) ? a.y2 : a.y;
+                    col = (sb >> 1) * a.split_period + (o - sb * a.split_period);
+                }
+                store_act4(dst, a.ydt, (int64_t)(M0 + m) * a.ldy + col, v);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int oi = o + e;
+                    if (oi >= a.N) break;
+                    float vi = v[e];
+                    if (want_res) vi += load_act(a.res, a.res_dt, (int64_t)(M0 + m) * a.ld_res + oi);
+                    void* dst = a.y;
+                    int col = oi;
+                    if (a.flags & EP_SPLIT) {
+                        const int sb = oi / a.split_period;
+                        dst = (sb & 1) ? a.y2 : a.y;
+                        col = (sb >> 1) * a.split_period + (oi - sb * a.split_period);
+                    }
+                    store_act(dst, a.ydt, (int64_t)(M0 + m) * a.ldy + col, vi);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+namespace {
+
+// weight k-steps per wave in flight (fewer with 16 token tiles, whose
+// accumulators take half the register file)
+constexpr int wide_u(int CT) { return CT >= 16 ? 4 : 8; }
+
+int ct_of(int M) { return M <= 32 ? 2 : (M <= 64 ? 4 : (M <= 128 ? 8 : 16)); }  // token tiles of 16
+
+// LDS bytes of a configuration: activations (or, after the MFMAs, the KW
+// partial tiles), the norm-weight slice, the residual tiles, the scales.
+struct WideLayout {
+    size_t x, gamma, res, scales, total;
+    int off_gamma, off_res, off_scales;
+};
+
+WideLayout wide_layout(int wf, int CT, int nks, int NB, int KW, bool glu, bool gamma, bool res, int rs, bool scales) {
+    const int KS = wf == WF_I8 ? 64 : 32, XU = wf == WF_I8 ? 2 : 1;
+    WideLayout L{};
+    const size_t xb = (size_t)CT * nks * XU * 1024;
+    const size_t red = (size_t)NB * KW * 2 * CT * 1024;  // every wave's accumulators
+    L.x = std::max(xb, red);
+    L.gamma = gamma ? (size_t)((nks * KS * 4 + 1023) / 1024) * 1024 : 0;
+    L.res = res ? (size_t)NB * (glu ? 1 : 2) * (CT * rs / 4) * 1024 : 0;
+    L.scales = scales ? (size_t)NB * 1024 : 0;
+    L.off_gamma = (int)L.x;
+    L.off_res = (int)(L.x + L.gamma);
+    L.off_scales = (int)(L.x + L.gamma + L.res);
+    L.total = L.x + L.gamma + L.res + L.scales;
+    return L;
+}
+
+template <typename Kern>
+hipError_t launch_w(Kern k, const WideArgs& a, int nw, int grid, size_t smem, hipStream_t st) {
+    static bool configured = false;  // one attribute call per instantiation
+    if (!configured) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideMaxLds);
+        if (e != hipSuccess) return e;
+        configured = true;
+    }
+    hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), smem, st, a);
+    return hipGetLastError();
+}
+
+template <int WF, int XDT, int CT, bool GLU>
+hipError_t launch_ct(const WideArgs& a, int NB, int KW, int grid, size_t smem, hipStream_t st) {
+    constexpr int U = wide_u(CT);
+    if (NB == 4 && KW == 1) return launch_w(wide_kernel<WF, XDT, CT, GLU, 4, 1, U>, a, 4, grid, smem, st);
+    if (NB == 2 && KW == 2) return launch_w(wide_kernel<WF, XDT, CT, GLU, 2, 2, U>, a, 4, grid, smem, st);
+    if constexpr (CT < 16) {  // 16 token tiles with four K parts per block would spill
+        if (NB == 1 && KW == 4) return launch_w(wide_kernel<WF, XDT, CT, GLU, 1, 4, U>, a, 4, grid, smem, st);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int WF, int XDT, bool GLU>
+hipError_t launch_glu(const WideArgs& a, int CT, int NB, int KW, int grid, size_t smem, hipStream_t st) {
+    switch (CT) {
+        case 2: return launch_ct<WF, XDT, 2, GLU>(a, NB, KW, grid, smem, st);
+        case 4: return launch_ct<WF, XDT, 4, GLU>(a, NB, KW, grid, smem, st);
+        case 8: return launch_ct<WF, XDT, 8, GLU>(a, NB, KW, grid, smem, st);
+        case 16: return launch_ct<WF, XDT, 16, GLU>(a, NB, KW, grid, smem, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool wide_supported(int wf, int xdt, int M) {
+    return M >= 1 && M <= kWideMaxM && ((wf == WF_BF16 && xdt == DT_BF16) || (wf == WF_I8 && xdt == DT_F16));
+}
+
+bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partials_cap, int max_counters, int force_s,
+               int force_cfg, WidePlan& p) {
+    const int n_ptiles = glu ? 2 * s.n_groups : s.n_groups;
+    const int nblocks = glu ? s.n_groups : (s.n_groups + 1) / 2;
+    const bool gamma = (s.flags & EP_NORM) && s.gamma;
+    const bool res = (s.flags & EP_RESIDUAL) && s.vec_store;
+    const int rs = s.res_dt == DT_F32 ? 4 : 2;
+    static const int cfgs[3][2] = {{4, 1}, {2, 2}, {1, 4}};
+    bool found = false;
+    // preference: enough workgroups to stream from most CUs, then no K split
+    // (no hand-off), then the most workgroups within one per CU, then fewer
+    // K splits, then fewer token groups
+    auto better = [&](int S, int grid, int T) {
+        if (!found) return true;
+        const bool full = 4 * grid >= 3 * num_cus, pfull = 4 * p.grid >= 3 * num_cus;
+        if (full != pfull) return full;
+        if ((S == 1) != (p.S == 1)) return S == 1;
+        if (grid != p.grid) return grid > p.grid;
+        if (S != p.S) return S < p.S;
+        return T < p.T;
+    };
+    for (int T = 1; T <= 8; T *= 2) {
+        const int Mg = (s.M + T - 1) / T;
+        if (T > 1 && Mg < 16) break;
+        if (Mg > 16 * 16) continue;  // at most 16 token tiles per group
+        const int CT = ct_of(Mg);
+        for (int S = 1; S <= std::min(s.ksteps, kWideMaxS); ++S) {
+            if (force_s && S != force_s) continue;
+            const int nks = (s.ksteps + S - 1) / S;
+            for (int c = 0; c < 3; ++c) {
+                if (force_cfg && c + 1 != force_cfg) continue;
+                const int NB = cfgs[c][0], KW = cfgs[c][1];
+                if (nks < KW || (CT >= 16 && KW == 4)) continue;
+                const WideLayout L = wide_layout(wf, CT, nks, NB, KW, glu, gamma, res, rs, s.scales != nullptr);
+                if (L.total > kWideMaxLds) continue;
+                // keep the direct-to-LDS loads of a wave plus its weight loads
+                // within the 63 the vector-memory counter holds (past that the
+                // wave stalls at issue until the first ones land)
+                const int XU = wf == WF_I8 ? 2 : 1, KS = wf == WF_I8 ? 64 : 32;
+                const int nw = NB * KW;
+                auto per = [nw](int units) { return (units + nw - 1) / nw; };
+                const int small = per(CT * nks * XU) + (gamma ? per((nks * KS * 4 + 1023) / 1024) : 0) +
+                                  (res ? per(NB * (glu ? 1 : 2) * CT * rs / 4) : 0) + (s.scales ? 1 : 0);
+                if (small + 2 * wide_u(CT) > 63) continue;
+                int ngrp = (nblocks + NB - 1) / NB;
+                if (T > 1) ngrp = (ngrp + 7) / 8 * 8;  // token groups 8 workgroups apart
+                if (S > 1 && (size_t)ngrp * T * S * NB * CT * 64 * (2 * 16 + 4) > partials_cap) continue;
+                if (S > 1 && ngrp * T > max_counters) continue;
+                const int grid = ngrp * T * S;
+                if (grid > num_cus && !(force_s || force_cfg)) continue;
+                if (better(S, grid, T)) {
+                    found = true;
+                    p.S = S;
+                    p.T = T;
+                    p.Mg = Mg;
+                    p.ngrp = ngrp;
+                    p.NB = NB;
+                    p.KW = KW;
+                    p.CT = CT;
+                    p.grid = grid;
+                    p.smem = L.total;
+                    p.off_gamma = L.off_gamma;
+                    p.off_res = L.off_res;
+                    p.off_scales = L.off_scales;
+                    p.nblocks = nblocks;
+                    p.n_ptiles = n_ptiles;
+                    p.res_lds = res ? 1 : 0;
+                }
+            }
+        }
+    }
+    return found;
+}
+
+hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream) {
+    if (!wide_supported(wf, xdt, a.s.M) || p.smem > kWideMaxLds) return hipErrorInvalidValue;
+    if (wf == WF_BF16) {
+        if (glu) return launch_glu<WF_BF16, DT_BF16, true>(a, p.CT, p.NB, p.KW, p.grid, p.smem, stream);
+        return launch_glu<WF_BF16, DT_BF16, false>(a, p.CT, p.NB, p.KW, p.grid, p.smem, stream);
+    }
+    if (glu) return launch_glu<WF_I8, DT_F16, true>(a, p.CT, p.NB, p.KW, p.grid, p.smem, stream);
+    return launch_glu<WF_I8, DT_F16, false>(a, p.CT, p.NB, p.KW, p.grid, p.smem, stream);
+}
+
+}  // namespace qwk

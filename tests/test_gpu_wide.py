@@ -1,0 +1,261 @@
+"""GPU parity of the weight-stationary projection kernel (qw_wide.hip), which
+takes 17..512 tokens on BF16 weights (BF16 activations) and INT8 weights (F16
+activations).
+
+The contexts here switch the MFMA GEMM off (QW_GEMM_MIN_M) so every call runs
+the weight-stationary kernel, at token counts that exercise each token-tile
+count (2, 4, 8, 16 tiles of 16) and token-group split (up to 8 groups of
+at most 256 tokens), ragged last tiles, odd tile counts (the last
+block of two tiles half empty), a partial last tile (N = 24), every K-split
+/ workgroup shape the planner can pick (forced through QW_WIDE_S and
+QW_WIDE_CFG), and every epilogue: residual (FP32 and BF16, in place), GLU
+with and without the RMSNorm prologue (per-call gamma and a folded norm
+weight), the Q/gate split, and the element-wise store path of unaligned
+outputs.
+
+Bars as for the other projection kernels: BF16 weights <= 2e-5 normwise vs
+FP64 on the stored operands (FP32 output), and <= 1e-2 with the RMSNorm
+prologue (the normalized activations are rounded to BF16 for the MFMA);
+INT8 weights <= 1e-3 normwise vs the reference's dequant-then-matmul
+(mlp_cuda.cu:158-180) and per element on outputs above a tenth of the RMS.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda").to(dtype)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def _elementwise(got, ref, bar):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    floor = np.sqrt(np.mean(ref ** 2)) / 10
+    assert np.all(np.abs(got - ref) <= bar * np.maximum(np.abs(ref), floor))
+
+
+def _ctx(qw, **env):
+    """A context created with the given QW_* settings (read at qw_init)."""
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return qw.Context(0)
+    finally:
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+@pytest.fixture(scope="module")
+def wctx(qw):
+    c = _ctx(qw, QW_GEMM_MIN_M=1 << 30)
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
+MS = [17, 32, 33, 64, 100, 128, 129, 200, 256, 300, 384, 512]
+
+
+@pytest.mark.parametrize("M", MS)
+@pytest.mark.parametrize("N,K", [(1024, 2048), (8192, 1024), (1040, 1024), (24, 1024)])
+def test_bf16_plain(qw, wctx, oracle, relerr, N, K, M):
+    W = oracle.normal((N, K), 3000 + N + K, 0.0, 0.02)
+    x = oracle.normal((M, K), 3001 + M)
+    w = qw.Weight.pack(wctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    y = torch.full((M, N), 7.0, device="cuda")
+    qw.linear(wctx, w, xt, y)
+    torch.cuda.synchronize()
+    assert wctx.device_error() == 0
+    assert relerr(host(y), oracle.linear_f64(oracle.round_bf16(W), host(xt))) <= 2e-5
+
+
+@pytest.mark.parametrize("M", [17, 64, 128, 256, 512])
+@pytest.mark.parametrize("rdt", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_bf16_residual_down(qw, wctx, oracle, relerr, M, rdt):
+    """down (1024 x 3584, many K splits) with the residual added in place."""
+    W = oracle.normal((1024, 3584), 3010, 0.0, 0.02)
+    x = oracle.normal((M, 3584), 3011 + M)
+    r = oracle.normal((M, 1024), 3012)
+    w = qw.Weight.pack(wctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    y = dev(r, rdt)
+    r_used = host(y)
+    qw.linear(wctx, w, xt, y, residual=y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W), host(xt)) + r_used
+    assert relerr(host(y), ref) <= (2e-5 if rdt == torch.float32 else 8e-3)
+
+
+@pytest.mark.parametrize("M", [20, 48, 128, 256, 384, 512])
+@pytest.mark.parametrize("norm", ["none", "gamma", "folded"])
+def test_bf16_glu(qw, wctx, oracle, relerr, M, norm):
+    I, H = 3584, 1024
+    G = oracle.normal((I, H), 3020, 0.0, 0.02)
+    U = oracle.normal((I, H), 3021, 0.0, 0.02)
+    gamma = oracle.normal((H,), 3022, 0.0, 0.02)
+    x = oracle.normal((M, H), 3023 + M)
+    w = qw.Weight.pack_glu(wctx, G, U, qw.WFMT_BF16)
+    if norm == "folded":
+        w.fold_norm(dev(gamma))
+    xt = dev(x, torch.bfloat16)
+    h = torch.empty(M, I, device="cuda")
+    qw.linear(wctx, w, xt, h, gamma=dev(gamma) if norm == "gamma" else None, norm=norm == "folded")
+    torch.cuda.synchronize()
+    xs = oracle.rmsnorm_f64(host(xt), gamma) if norm != "none" else host(xt).astype(np.float64)
+    g = xs @ oracle.round_bf16(G).astype(np.float64).T
+    u = xs @ oracle.round_bf16(U).astype(np.float64).T
+    ref = g / (1.0 + np.exp(-g)) * u
+    assert relerr(host(h), ref) <= (1e-2 if norm != "none" else 1e-4)
+
+
+@pytest.mark.parametrize("M", [40, 128])
+def test_bf16_split_q_gate(qw, wctx, oracle, relerr, M):
+    heads, D, K = 8, 256, 1024
+    W = oracle.normal((2 * heads * D, K), 3030, 0.0, 0.02)
+    x = oracle.normal((M, K), 3031)
+    w = qw.Weight.pack(wctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    q = torch.empty(M, heads * D, device="cuda")
+    g = torch.empty(M, heads * D, device="cuda")
+    qw.linear(wctx, w, xt, q, y2=g, split_period=D)
+    torch.cuda.synchronize()
+    full = oracle.linear_f64(oracle.round_bf16(W), host(xt))
+    q_ref, g_ref = oracle.split_q_gate(full.astype(np.float32), heads, D)
+    assert relerr(host(q), q_ref) <= 1e-5 and relerr(host(g), g_ref) <= 1e-5
+
+
+def test_bf16_unaligned_output(qw, wctx, oracle, relerr):
+    """A row pitch that is not a multiple of 4 takes the element-wise stores
+    (residual read from global memory)."""
+    M, N, K = 50, 1024, 2048
+    W = oracle.normal((N, K), 3040, 0.0, 0.02)
+    x = oracle.normal((M, K), 3041)
+    r = oracle.normal((M, N), 3042)
+    w = qw.Weight.pack(wctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    ybuf = torch.zeros(M, N + 3, device="cuda")
+    y = ybuf[:, :N]
+    y.copy_(dev(r))
+    qw.linear(wctx, w, xt, y, residual=y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_f64(oracle.round_bf16(W), host(xt)) + r
+    assert relerr(host(y), ref) <= 2e-5
+    assert torch.all(ybuf[:, N:] == 0)
+
+
+@pytest.mark.parametrize("M", [17, 32, 64, 128, 256, 384, 512])
+@pytest.mark.parametrize("N,K", [(1024, 3584), (6144, 1024), (512, 1024), (1024, 2048)])
+def test_int8_plain(qw, wctx, oracle, relerr, N, K, M):
+    q = oracle.int8_uniform((N, K), 3100 + N + K)
+    s = oracle.uniform((N,), 3101 + N, 1e-3, 2e-2)
+    x = oracle.normal((M, K), 3102 + M)
+    w = qw.Weight.pack(wctx, q, qw.WFMT_INT8, scales=s)
+    xt = dev(x, torch.float16)
+    y = torch.empty(M, N, device="cuda")
+    qw.linear(wctx, w, xt, y)
+    torch.cuda.synchronize()
+    ref = oracle.linear_int8(q, s, host(xt))
+    assert relerr(host(y), ref) <= 1e-3
+    _elementwise(host(y), ref, 1e-3)
+
+
+@pytest.mark.parametrize("M", [24, 128, 256, 512])
+def test_int8_glu_and_residual(qw, wctx, oracle, relerr, M):
+    I, H = 3584, 1024
+    qg = oracle.int8_uniform((I, H), 3110)
+    qu = oracle.int8_uniform((I, H), 3111)
+    sg = oracle.uniform((I,), 3112, 1e-3, 2e-2)
+    su = oracle.uniform((I,), 3113, 1e-3, 2e-2)
+    qd = oracle.int8_uniform((H, I), 3114)
+    sd = oracle.uniform((H,), 3115, 1e-3, 2e-2)
+    x = oracle.normal((M, H), 3116)
+    r = oracle.normal((M, H), 3117)
+    gu = qw.Weight.pack_glu(wctx, qg, qu, qw.WFMT_INT8, gate_scales=sg, up_scales=su)
+    dn = qw.Weight.pack(wctx, qd, qw.WFMT_INT8, scales=sd)
+    xt = dev(x, torch.float16)
+    h = torch.empty(M, I, device="cuda", dtype=torch.float16)
+    qw.linear(wctx, gu, xt, h)
+    y = dev(r)   # FP32: the INT8 down outputs reach ~6e4
+    r_used = host(y)
+    qw.linear(wctx, dn, h, y, residual=y)
+    torch.cuda.synchronize()
+    xs = host(xt)
+    g = oracle.linear_int8(qg, sg, xs).astype(np.float64)
+    u = oracle.linear_int8(qu, su, xs).astype(np.float64)
+    h_ref = g / (1.0 + np.exp(-g)) * u
+    assert relerr(host(h), h_ref) <= 1e-3
+    y_ref = oracle.linear_int8(qd, sd, host(h)).astype(np.float64) + r_used
+    assert relerr(host(y), y_ref) <= 1e-3
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+@pytest.mark.parametrize("S", [1, 2, 3, 7])
+def test_forced_shapes(qw, oracle, relerr, cfg, S):
+    """Every workgroup shape (4x1, 2x2, 1x4 blocks x waves) at several K
+    splits, including uneven ones, on BF16 and INT8 weights."""
+    c = _ctx(qw, QW_GEMM_MIN_M=1 << 30, QW_WIDE_CFG=cfg, QW_WIDE_S=S)
+    try:
+        M, N, K = 40, 2080, 2048
+        W = oracle.normal((N, K), 3200, 0.0, 0.02)
+        x = oracle.normal((M, K), 3201)
+        w = qw.Weight.pack(c, W, qw.WFMT_BF16)
+        xt = dev(x, torch.bfloat16)
+        y = torch.empty(M, N, device="cuda")
+        qw.linear(c, w, xt, y)
+        q = oracle.int8_uniform((N, K), 3202)
+        s = oracle.uniform((N,), 3203, 1e-3, 2e-2)
+        w8 = qw.Weight.pack(c, q, qw.WFMT_INT8, scales=s)
+        x16 = dev(x, torch.float16)
+        y8 = torch.empty(M, N, device="cuda")
+        qw.linear(c, w8, x16, y8)
+        torch.cuda.synchronize()
+        assert relerr(host(y), oracle.linear_f64(oracle.round_bf16(W), host(xt))) <= 2e-5
+        assert relerr(host(y8), oracle.linear_int8(q, s, host(x16))) <= 1e-3
+        del w, w8
+    finally:
+        torch.cuda.synchronize()
+        c.close()
+
+
+def test_repeatable_and_graph_safe(qw, wctx, oracle):
+    """Bit-identical results over repeated calls (fixed reduction orders, the
+    split-K counters return to zero), eager and replayed from a graph."""
+    M, N, K = 128, 1024, 3584
+    W = oracle.normal((N, K), 3300, 0.0, 0.02)
+    x = oracle.normal((M, K), 3301)
+    w = qw.Weight.pack(wctx, W, qw.WFMT_BF16)
+    xt = dev(x, torch.bfloat16)
+    y0 = torch.empty(M, N, device="cuda")
+    qw.linear(wctx, w, xt, y0)
+    torch.cuda.synchronize()
+    y = torch.empty(M, N, device="cuda")
+    for _ in range(20):
+        y.zero_()
+        qw.linear(wctx, w, xt, y)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        g = qw.Graph(wctx, stream)
+        with g:
+            qw.linear(wctx, w, xt, y, stream=stream)
+        for _ in range(5):
+            y.zero_()
+            g.launch(stream)
+            stream.synchronize()
+            assert torch.equal(y, y0)
+    torch.cuda.synchronize()
