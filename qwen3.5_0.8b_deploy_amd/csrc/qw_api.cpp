@@ -42,6 +42,7 @@ struct qw_ctx {
     int wide_min = kWideMinM;    // QW_WIDE_MIN
     int wide_max = qwk::kWideMaxM;  // QW_WIDE_MAX
     int wide_s = 0;              // K splits (QW_WIDE_S; 0 = planned)
+    bool wide_norm_sep = false;  // RMSNorm prologue as a separate launch (QW_WIDE_NORM_SEP=1) instead of in the kernel
     int wide_dbg = 0;            // QW_WIDE_DBG: timing probes (wrong results)
     int wide_cfg = 0;            // blocks x waves per block (QW_WIDE_CFG 1: 4x1, 2: 2x2, 3: 1x4; 0 = planned)
     int attn_split = 0;          // keys per decode split, 0 = by size (QW_ATTN_SPLIT forces a multiple of 64)
@@ -201,6 +202,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_WIDE_MIN")) c->wide_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_WIDE_MAX")) c->wide_max = std::min(qwk::kWideMaxM, atoi(v));
     if (const char* v = getenv("QW_WIDE_S")) c->wide_s = std::max(0, atoi(v));
+    if (const char* v = getenv("QW_WIDE_NORM_SEP")) c->wide_norm_sep = atoi(v) != 0;
     if (const char* v = getenv("QW_WIDE_DBG")) c->wide_dbg = atoi(v);
     if (const char* v = getenv("QW_WIDE_CFG")) c->wide_cfg = std::max(0, std::min(3, atoi(v)));
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
@@ -899,7 +901,20 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     // weight-stationary kernel: every weight byte once for all tokens
     if (ctx->wide && !(ctx->gemm_forced && M >= ctx->gemm_min_m) && M >= ctx->wide_min && M <= ctx->wide_max &&
         qwk::wide_supported(W->wf, (int)xdt, M)) {
-        s = run_wide(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, stream);
+        const bool norm = ep && (ep->flags & QW_EP_NORM_X);
+        if (norm && ctx->wide_norm_sep && (size_t)M * W->K * dsize(xdt) <= ctx->xnorm_bytes) {
+            // RMSNorm into the workspace (one row per workgroup), then the
+            // projection of the normalized activations: cheaper than the
+            // in-kernel LDS pass, whose conversions are VALU-bound at many tokens
+            hipError_t e = qwk::launch_rmsnorm_ld(x, (int)xdt, ldx, ep->gamma, ep->eps, ctx->xnorm, (int)xdt, W->K,
+                                                  M, W->K, stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "rmsnorm launch");
+            qw_epilogue e2 = *ep;
+            e2.flags &= ~(unsigned)QW_EP_NORM_X;
+            s = run_wide(ctx, W, ctx->xnorm, xdt, W->K, M, y, ydt, ldy, &e2, stream);
+        } else {
+            s = run_wide(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, stream);
+        }
         if (s != QW_ERR_SHAPE) return s;
     }
     if (const int rows = gemm_route(ctx, W, xdt, M)) {

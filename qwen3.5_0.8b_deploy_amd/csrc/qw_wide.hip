@@ -5,8 +5,10 @@
 // tokens: a wave holds a block of two 16-row tiles (a gate/up pair for GLU
 // weights) of one K range in MFMA A registers, and runs them against every
 // token tile of the activations, which sit in LDS.  The tokens are the MFMA
-// N side (16 per tile, up to 16 tiles), so the weights are the stationary
-// operand and the activations are re-read from LDS, not from HBM.
+// N side (16 per tile, up to 8 tiles), so the weights are the stationary
+// operand and the activations are re-read from LDS, not from HBM.  More than
+// 128 tokens run as token groups of at most 128 (workgroups of their own,
+// the weights then come from L2 for the later groups).
 //
 // Work decomposition.  K is cut into S splits so that the activation slice
 // [M][K/S] of a split fits the workgroup's LDS.  A workgroup is one split of
@@ -26,17 +28,19 @@
 //      flight, unconditionally; unused slots read out of range), so the
 //      small loads above are ahead of them in the in-order vector-memory
 //      counter: one s_waitcnt vmcnt(U*RT) and a barrier publish them.
-//   3. RMSNorm prologue (when asked): one LDS pass takes the per-token sums of
-//      squares of the split's range (fixed order) and multiplies (1 + gamma)
-//      into the staged activations.
-//   4. MFMAs (16x16x32 bf16, or f16 on exactly converted INT8 units), each
-//      weight unit against all token tiles; further weight chunks are issued
-//      after a chunk is consumed.
+//   3. MFMAs (16x16x32 bf16, or f16 on exactly converted INT8 units), each
+//      weight unit against all token tiles, the B operands read one k-step
+//      ahead; further weight chunks are issued after a chunk is consumed.
+//   4. RMSNorm prologue (when asked), inside the MFMA stream: the per-token
+//      sums of squares are the diagonal of X X^T (one more MFMA per token
+//      tile and k-step), and (1 + gamma) scales the weight operand, so the
+//      staged activations are used as they are.
 //   5. The KW partial tiles of a block meet in LDS (fixed order); the split
-//      partials meet through the workspace: agent-scope (sc1) 16-byte stores,
-//      s_waitcnt, one arrival count per block; the last of the S workgroups
-//      sums the S partials in split order (deterministic), returns the counter
-//      to zero (graph-safe, no memset) and runs the epilogue.
+//      partials meet through the workspace: device-coherent (sc1) 16-byte
+//      stores, s_waitcnt, one arrival count per block group; the last of the S
+//      workgroups sums the S partials in split order (deterministic), returns
+//      the counter to zero (graph-safe, no memset) and runs the epilogue,
+//      spread over its waves.
 //   6. Epilogue: 1/rms, INT8 row scale, SiLU(gate)*up, residual, Q/gate
 //      de-interleave, 4-wide stores.
 //
@@ -60,7 +64,7 @@ template <int WF> struct WideT {
 // of rs bytes, in 1 KB units of 32 (rs = 2) or 16 (rs = 4) tokens.
 __device__ __forceinline__ int res_units(int CT, int rs) { return CT * rs / 4; }
 
-template <int WF, int XDT, int CT, bool GLU, int NB, int KW, int U>
+template <int WF, int XDT, int CT, bool GLU, bool NORM, int NB, int KW, int U>
 __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
     constexpr int NW = NB * KW;
     constexpr int RT = 2;                 // physical tiles per block
@@ -71,7 +75,7 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
                   "activations arrive in the MFMA input type");
     const SkinnyArgs& a = wa.s;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-    __shared__ float ss_tok[CT * 16];
+    __shared__ float ss_part[KW][CT * 16];  // sums of squares of each K part of the split
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -91,8 +95,8 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
     const int bl = wave / KW, kw = wave % KW;
     const int blk = bg * NB + bl;
     const bool blk_ok = blk < wa.nblocks;
-    const bool norm = (a.flags & EP_NORM) != 0;
-    const bool gam = norm && a.gamma != nullptr;
+    constexpr bool norm = NORM;  // the host sets NORM exactly when the call asks for EP_NORM
+    const bool gam = NORM && a.gamma != nullptr;
     const bool want_res = (a.flags & EP_RESIDUAL) != 0;
 
     // this workgroup's split [ks0, ks1) and the wave's part [kb, kend)
@@ -178,90 +182,138 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
     __builtin_amdgcn_s_waitcnt(vm_wait(U * RT));  // everything issued before the weights has landed
     __syncthreads();
 
-    // ---- 3. RMSNorm prologue: sums of squares of the split, (1 + gamma) ----
-    if (norm) {
-        for (int ct = wave; ct < CT; ct += NW) {
-            float ss = 0.0f;
-            for (int ksr = 0; ksr < nks; ++ksr) {
-#pragma unroll
-                for (int h = 0; h < XU; ++h) {
-                    uint8_t* p = xl + ((ksr * CT + ct) * XU + h) * 1024 + lane * 16;
-                    u32x4 raw = *reinterpret_cast<u32x4*>(p);
-                    float f[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const uint32_t hb = (raw[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                        f[e] = XDT == DT_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
-                        ss += f[e] * f[e];
-                    }
-                    if (gam) {
-                        const float* gp = reinterpret_cast<const float*>(gl) + ksr * KS + g * KEW + h * 8;
-                        const f32x4 g0 = reinterpret_cast<const f32x4*>(gp)[0];
-                        const f32x4 g1 = reinterpret_cast<const f32x4*>(gp)[1];
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            f[e] *= 1.0f + g0[e];
-                            f[e + 4] *= 1.0f + g1[e];
-                        }
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            raw[q] = op_bits<WF>(f[2 * q]) | (op_bits<WF>(f[2 * q + 1]) << 16);
-                        *reinterpret_cast<u32x4*>(p) = raw;
-                    }
-                }
-            }
-            ss += __shfl_xor(ss, 16);
-            ss += __shfl_xor(ss, 32);
-            if (g == 0) ss_tok[ct * 16 + r] = ss;
-        }
-        __syncthreads();
-    }
-
-    // ---- 4. MFMAs ----
+    // ---- 3. MFMAs (and the RMSNorm prologue) ----
     f32x4 acc[RT][CT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto step = [&](int u, int ksr) {
+    // B operands (one 16-byte LDS read per token tile and unit) of a k-step
+    // are read one k-step ahead, so their LDS latency hides under the MFMAs
+    // of the previous k-step.
+    u32x4 B[2][CT][XU];
+    auto read_b = [&](int buf, int ksr) {
         const uint8_t* xp = xl + (ksr * CT * XU) * 1024 + lane * 16;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int h = 0; h < XU; ++h) B[buf][ct][h] = *reinterpret_cast<const u32x4*>(xp + (ct * XU + h) * 1024);
+    };
+    // RMSNorm prologue inside the MFMA stream: the sums of squares of the
+    // tokens are the diagonal of X X^T, one extra MFMA per token tile and
+    // k-step on the B operands already in registers (the block-0 waves of
+    // the workgroup take them); (1 + gamma) scales the weight operand of the
+    // k-step (A), so the staged activations are used as they are.
+    f32x4 accss[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) accss[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool do_ss = NORM && bl == 0;
+    auto mma = [&](int u, int buf, int ksr) {
         if constexpr (WF == WF_BF16) {
+            u32x4 av[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) av[rt] = A[u][rt];
+            if (gam) {
+                const float* gp = reinterpret_cast<const float*>(gl) + ksr * KS + g * KEW;
+                const f32x4 g0 = reinterpret_cast<const f32x4*>(gp)[0];
+                const f32x4 g1 = reinterpret_cast<const f32x4*>(gp)[1];
+                float gs[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    gs[e] = 1.0f + g0[e];
+                    gs[e + 4] = 1.0f + g1[e];
+                }
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int q2 = 0; q2 < 4; ++q2) {
+                        const uint32_t w = av[rt][q2];
+                        const float lo = bf16_bits_to_f32(w & 0xffffu) * gs[2 * q2];
+                        const float hi = bf16_bits_to_f32(w >> 16) * gs[2 * q2 + 1];
+                        av[rt][q2] = f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+                    }
+            }
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
-                const bf16x8 b = *reinterpret_cast<const bf16x8*>(xp + ct * 1024);
+                const bf16x8 b = __builtin_bit_cast(bf16x8, B[buf][ct][0]);
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_bf16(__builtin_bit_cast(bf16x8, A[u][rt]), b, acc[rt][ct]);
+                for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_bf16(__builtin_bit_cast(bf16x8, av[rt]), b, acc[rt][ct]);
+                if (do_ss) accss[ct] = mfma_bf16(b, b, accss[ct]);
             }
         } else {
             f16x8 a0[RT], a1[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) i8unit_to_f16(A[u][rt], a0[rt], a1[rt]);
+            if (gam) {
+                // (1 + gamma) as f16, multiplied into the exact f16 weights
+                const float* gp = reinterpret_cast<const float*>(gl) + ksr * KS + g * KEW;
+                f16x8 gs0, gs1;
+#pragma unroll
+                for (int e4 = 0; e4 < 2; ++e4) {
+                    const f32x4 v0 = reinterpret_cast<const f32x4*>(gp)[e4];
+                    const f32x4 v1 = reinterpret_cast<const f32x4*>(gp)[e4 + 2];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        gs0[e4 * 4 + e] = (_Float16)(1.0f + v0[e]);
+                        gs1[e4 * 4 + e] = (_Float16)(1.0f + v1[e]);
+                    }
+                }
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    a0[rt] = a0[rt] * gs0;
+                    a1[rt] = a1[rt] * gs1;
+                }
+            }
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
-                const f16x8 b0 = *reinterpret_cast<const f16x8*>(xp + ct * 2048);
-                const f16x8 b1 = *reinterpret_cast<const f16x8*>(xp + ct * 2048 + 1024);
+                const f16x8 b0 = __builtin_bit_cast(f16x8, B[buf][ct][0]);
+                const f16x8 b1 = __builtin_bit_cast(f16x8, B[buf][ct][1]);
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) {
                     acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
                     acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
                 }
+                if (do_ss) {
+                    accss[ct] = mfma_f16(b0, b0, accss[ct]);
+                    accss[ct] = mfma_f16(b1, b1, accss[ct]);
+                }
             }
         }
     };
+    if (kb < kend) read_b(0, kb - ks0);
     for (;;) {
         if (wa.dbg & 1) {
         } else if (n == U) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) step(u, kb + u - ks0);
+            for (int u = 0; u < U; ++u) {
+                if (u + 1 < U || kb + U < kend) read_b((u + 1) & 1, kb + u + 1 - ks0);
+                mma(u, u & 1, kb + u - ks0);
+            }
         } else {
 #pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (u < n) step(u, kb + u - ks0);
+            for (int u = 0; u < U; ++u) {
+                if (u < n) {
+                    if (u + 1 < n) read_b((u + 1) & 1, kb + u + 1 - ks0);
+                    mma(u, u & 1, kb + u - ks0);
+                }
+            }
         }
         kb += n;
         if (kb >= kend) break;
         n = min(U, kend - kb);
         issue(kb, n);
+    }
+
+    if (do_ss) {
+        // diagonal of the 16x16 tile: token r sits in lane (r, r / 4), element r % 4
+        if (g == (r >> 2)) {
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                const f32x4 v = accss[ct];
+                const int e = r & 3;
+                ss_part[kw][ct * 16 + r] = e == 0 ? v[0] : (e == 1 ? v[1] : (e == 2 ? v[2] : v[3]));
+            }
+        }
     }
 
     // ---- 5. reduction over the KW parts and the S splits ----
@@ -300,7 +352,12 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
             }
             u_acc[i][rt] = v;
         }
-        u_ss[i] = (norm && u < NU) ? ss_tok[uc * 16 + r] : 0.0f;
+        float sq = 0.0f;
+        if (norm && u < NU) {
+#pragma unroll
+            for (int pp = 0; pp < KW; ++pp) sq += ss_part[pp][uc * 16 + r];
+        }
+        u_ss[i] = sq;
     }
 
     if (S > 1 && !(wa.dbg & 2)) {
@@ -444,11 +501,9 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
 // ---------------------------------------------------------------------------
 namespace {
 
-// weight k-steps per wave in flight (fewer with 16 token tiles, whose
-// accumulators take half the register file)
-constexpr int wide_u(int CT) { return CT >= 16 ? 4 : 8; }
+constexpr int kWideU = 8;  // weight k-steps per wave in flight
 
-int ct_of(int M) { return M <= 32 ? 2 : (M <= 64 ? 4 : (M <= 128 ? 8 : 16)); }  // token tiles of 16
+int ct_of(int M) { return M <= 32 ? 2 : (M <= 64 ? 4 : 8); }  // token tiles of 16 (at most 128 tokens)
 
 // LDS bytes of a configuration: activations (or, after the MFMAs, the KW
 // partial tiles), the norm-weight slice, the residual tiles, the scales.
@@ -486,15 +541,19 @@ hipError_t launch_w(Kern k, const WideArgs& a, int nw, int grid, size_t smem, hi
     return hipGetLastError();
 }
 
+template <int WF, int XDT, int CT, bool GLU, bool NORM>
+hipError_t launch_n(const WideArgs& a, int NB, int KW, int grid, size_t smem, hipStream_t st) {
+    constexpr int U = kWideU;
+    if (NB == 4 && KW == 1) return launch_w(wide_kernel<WF, XDT, CT, GLU, NORM, 4, 1, U>, a, 4, grid, smem, st);
+    if (NB == 2 && KW == 2) return launch_w(wide_kernel<WF, XDT, CT, GLU, NORM, 2, 2, U>, a, 4, grid, smem, st);
+    if (NB == 1 && KW == 4) return launch_w(wide_kernel<WF, XDT, CT, GLU, NORM, 1, 4, U>, a, 4, grid, smem, st);
+    return hipErrorInvalidValue;
+}
+
 template <int WF, int XDT, int CT, bool GLU>
 hipError_t launch_ct(const WideArgs& a, int NB, int KW, int grid, size_t smem, hipStream_t st) {
-    constexpr int U = wide_u(CT);
-    if (NB == 4 && KW == 1) return launch_w(wide_kernel<WF, XDT, CT, GLU, 4, 1, U>, a, 4, grid, smem, st);
-    if (NB == 2 && KW == 2) return launch_w(wide_kernel<WF, XDT, CT, GLU, 2, 2, U>, a, 4, grid, smem, st);
-    if constexpr (CT < 16) {  // 16 token tiles with four K parts per block would spill
-        if (NB == 1 && KW == 4) return launch_w(wide_kernel<WF, XDT, CT, GLU, 1, 4, U>, a, 4, grid, smem, st);
-    }
-    return hipErrorInvalidValue;
+    if (a.s.flags & EP_NORM) return launch_n<WF, XDT, CT, GLU, true>(a, NB, KW, grid, smem, st);
+    return launch_n<WF, XDT, CT, GLU, false>(a, NB, KW, grid, smem, st);
 }
 
 template <int WF, int XDT, bool GLU>
@@ -503,7 +562,6 @@ hipError_t launch_glu(const WideArgs& a, int CT, int NB, int KW, int grid, size_
         case 2: return launch_ct<WF, XDT, 2, GLU>(a, NB, KW, grid, smem, st);
         case 4: return launch_ct<WF, XDT, 4, GLU>(a, NB, KW, grid, smem, st);
         case 8: return launch_ct<WF, XDT, 8, GLU>(a, NB, KW, grid, smem, st);
-        case 16: return launch_ct<WF, XDT, 16, GLU>(a, NB, KW, grid, smem, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -538,7 +596,7 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
     for (int T = 1; T <= 8; T *= 2) {
         const int Mg = (s.M + T - 1) / T;
         if (T > 1 && Mg < 16) break;
-        if (Mg > 16 * 16) continue;  // at most 16 token tiles per group
+        if (Mg > 8 * 16) continue;  // at most 8 token tiles per group (16 would spill registers)
         const int CT = ct_of(Mg);
         for (int S = 1; S <= std::min(s.ksteps, kWideMaxS); ++S) {
             if (force_s && S != force_s) continue;
@@ -546,7 +604,7 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
             for (int c = 0; c < 3; ++c) {
                 if (force_cfg && c + 1 != force_cfg) continue;
                 const int NB = cfgs[c][0], KW = cfgs[c][1];
-                if (nks < KW || (CT >= 16 && KW == 4)) continue;
+                if (nks < KW) continue;
                 const WideLayout L = wide_layout(wf, CT, nks, NB, KW, glu, gamma, res, rs, s.scales != nullptr);
                 if (L.total > kWideMaxLds) continue;
                 // keep the direct-to-LDS loads of a wave plus its weight loads
@@ -557,7 +615,7 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
                 auto per = [nw](int units) { return (units + nw - 1) / nw; };
                 const int small = per(CT * nks * XU) + (gamma ? per((nks * KS * 4 + 1023) / 1024) : 0) +
                                   (res ? per(NB * (glu ? 1 : 2) * CT * rs / 4) : 0) + (s.scales ? 1 : 0);
-                if (small + 2 * wide_u(CT) > 63) continue;
+                if (small + 2 * kWideU > 63) continue;
                 int ngrp = (nblocks + NB - 1) / NB;
                 if (T > 1) ngrp = (ngrp + 7) / 8 * 8;  // token groups 8 workgroups apart
                 if (S > 1 && (size_t)ngrp * T * S * NB * CT * 64 * (2 * 16 + 4) > partials_cap) continue;

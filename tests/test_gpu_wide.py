@@ -4,8 +4,8 @@ activations).
 
 The contexts here switch the MFMA GEMM off (QW_GEMM_MIN_M) so every call runs
 the weight-stationary kernel, at token counts that exercise each token-tile
-count (2, 4, 8, 16 tiles of 16) and token-group split (up to 8 groups of
-at most 256 tokens), ragged last tiles, odd tile counts (the last
+count (2, 4, 8 tiles of 16) and token-group split (up to 8 groups of at
+most 128 tokens), ragged last tiles, odd tile counts (the last
 block of two tiles half empty), a partial last tile (N = 24), every K-split
 / workgroup shape the planner can pick (forced through QW_WIDE_S and
 QW_WIDE_CFG), and every epilogue: residual (FP32 and BF16, in place), GLU
@@ -100,9 +100,21 @@ def test_bf16_residual_down(qw, wctx, oracle, relerr, M, rdt):
     assert relerr(host(y), ref) <= (2e-5 if rdt == torch.float32 else 8e-3)
 
 
+@pytest.fixture(scope="module")
+def wctx_sep_norm(qw):
+    """The RMSNorm prologue as a separate normalization launch instead of
+    inside the weight-stationary kernel."""
+    c = _ctx(qw, QW_GEMM_MIN_M=1 << 30, QW_WIDE_NORM_SEP=1)
+    yield c
+    torch.cuda.synchronize()
+    c.close()
+
+
 @pytest.mark.parametrize("M", [20, 48, 128, 256, 384, 512])
-@pytest.mark.parametrize("norm", ["none", "gamma", "folded"])
-def test_bf16_glu(qw, wctx, oracle, relerr, M, norm):
+@pytest.mark.parametrize("norm", ["none", "gamma", "folded", "gamma_sep", "folded_sep"])
+def test_bf16_glu(qw, wctx, wctx_sep_norm, oracle, relerr, M, norm):
+    if norm.endswith("_sep"):
+        wctx, norm = wctx_sep_norm, norm[: -len("_sep")]
     I, H = 3584, 1024
     G = oracle.normal((I, H), 3020, 0.0, 0.02)
     U = oracle.normal((I, H), 3021, 0.0, 0.02)
@@ -259,3 +271,30 @@ def test_repeatable_and_graph_safe(qw, wctx, oracle):
             stream.synchronize()
             assert torch.equal(y, y0)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M", [24, 128, 300])
+@pytest.mark.parametrize("sep", [False, True])
+def test_int8_glu_norm(qw, wctx, wctx_sep_norm, oracle, relerr, M, sep):
+    """INT8 gate/up with the RMSNorm prologue (F16 activations): against the
+    dequant-then-matmul of the FP64-normalized activations."""
+    c = wctx_sep_norm if sep else wctx
+    I, H = 3584, 1024
+    qg = oracle.int8_uniform((I, H), 3400)
+    qu = oracle.int8_uniform((I, H), 3401)
+    sg = oracle.uniform((I,), 3402, 1e-3, 2e-2)
+    su = oracle.uniform((I,), 3403, 1e-3, 2e-2)
+    gamma = oracle.normal((H,), 3404, 0.0, 0.02)
+    x = oracle.normal((M, H), 3405)
+    gu = qw.Weight.pack_glu(c, qg, qu, qw.WFMT_INT8, gate_scales=sg, up_scales=su)
+    xt = dev(x, torch.float16)
+    h = torch.empty(M, I, device="cuda")
+    qw.linear(c, gu, xt, h, gamma=dev(gamma))
+    torch.cuda.synchronize()
+    xs = oracle.rmsnorm_f64(host(xt), gamma)
+    g = oracle.linear_int8_f64(qg, sg, xs)
+    u = oracle.linear_int8_f64(qu, su, xs)
+    ref = g / (1.0 + np.exp(-g)) * u
+    # the weights times (1 + gamma), or the normalized activations, are
+    # rounded to F16 for the MFMA (2^-11 per term)
+    assert relerr(host(h), ref) <= 2e-3
