@@ -169,7 +169,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma-separated extra workloads to run (cfg1, cfg2, cfg3, "
+    ap.add_argument("--only", default="", help="comma-separated extra workloads to run (cfg1, cfg2, cfg3, wide, "
                     "int8gemv, prefill, gdn, attn, model, lmhead; default all), e.g. for a profiler pass over one of them")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="counter pass: only the dominant kernel (4 eager MLP stack launches) and a "
@@ -312,15 +312,25 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
     only = set(filter(None, args.only.split(",")))
     want = lambda name: not only or name in only
 
-    # config 2: fused MLP at decode batches
+    # config 2: fused MLP at decode batches.  The RMSNorm weight is a model
+    # constant, so it is folded into the gate/up columns once at load time
+    # (qw_weight_fold_norm); the kernels still normalize every token.
+    gu_f = []
+    if want("cfg2"):
+        for l in range(LAYERS):
+            g_, u_ = randn(I, H, std=0.02), randn(I, H, std=0.02)
+            w = qw.Weight.pack_glu_device(ctx, g_, u_, qw.WFMT_BF16)
+            w.fold_norm(gam[l])
+            gu_f.append(w)
+            del g_, u_
     for M in ((8, 32, 128) if want("cfg2") else ()):
         hb = randn(M, H)
-        g = graphed(qw, ctx, stream, lambda hb=hb: [qw.mlp_fused(ctx, gu[l], dn[l], hb, hb, gamma=gam[l], residual=hb)
+        g = graphed(qw, ctx, stream, lambda hb=hb: [qw.mlp_fused(ctx, gu_f[l], dn[l], hb, hb, residual=hb)
                                                    for l in range(LAYERS)])
         ms = timer.run(g.launch, steps, 2)
         b = LAYERS * mlp_bytes(M)
         fl = LAYERS * 2.0 * M * 3 * H * I
-        extra[f"cfg2_mlp_bf16_M{M}"] = {"us_per_layer": round(ms * 1e3 / LAYERS, 2),
+        extra[f"cfg2_mlp_bf16_M{M}"] = {"us_per_layer": round(ms * 1e3 / LAYERS, 2), "norm": "gamma folded into gate/up",
                                         "GBps": round(b / ms / 1e6, 1),
                                         "TFLOPs": round(fl / ms / 1e9, 2),
                                         "tok_per_s_stack": round(M / (ms * 1e-3), 1)}
@@ -328,7 +338,9 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
 
     extra.update(run_cfg1(qw, ctx, torch, timer, stream, randn, steps) if want("cfg1") else {})
     extra.update(run_cfg3(qw, ctx, torch, timer, stream, randn, steps) if want("cfg3") else {})
+    del gu_f
     extra.update(run_int8_gemv(qw, ctx, torch, timer, stream, randn, steps) if want("int8gemv") else {})
+    extra.update(run_wide(qw, ctx, torch, timer, stream, randn, steps) if want("wide") else {})
     if want("prefill"):
         extra.update(run_prefill(qw, ctx, torch, timer, stream, randn, args))
     if want("gdn"):
@@ -474,6 +486,56 @@ def run_int8_gemv(qw, ctx, torch, timer, stream, randn, steps):
                                       "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK, 1), "bytes_per_launch": b}
     log("int8 gemv glu", out["int8_gemv_gateup_glu_M1"])
     del g, gus
+    return out
+
+
+def run_wide(qw, ctx, torch, timer, stream, randn, steps):
+    """Per-launch lines of the weight-stationary kernel (qw_wide.hip) at 32 and
+    128 tokens: the gate/up GLU pair (BF16 and INT8) and the down projection
+    with the residual, 24 distinct weights per graph so every launch streams
+    its weights from HBM."""
+    out = {}
+    n_copies = 24
+    for fmt in ("bf16", "int8"):
+        wf = qw.WFMT_BF16 if fmt == "bf16" else qw.WFMT_INT8
+        xdt = torch.bfloat16 if fmt == "bf16" else torch.float16
+        wb = 2 if fmt == "bf16" else 1
+
+        def mk(n, k, seed):
+            if fmt == "bf16":
+                return randn(n, k, std=0.02), None
+            q = torch.randint(-127, 128, (n, k), generator=torch.Generator(device="cuda").manual_seed(seed),
+                              device="cuda", dtype=torch.int8)
+            return q, torch.rand(n, generator=torch.Generator(device="cuda").manual_seed(seed + 1),
+                                 device="cuda") * 1e-3 + 1e-4
+
+        gus, dns = [], []
+        for c in range(n_copies):
+            (a_, sa), (b_, sb) = mk(I, H, 9000 + 4 * c), mk(I, H, 9002 + 4 * c)
+            gus.append(qw.Weight.pack_glu_device(ctx, a_, b_, wf, sa, sb))
+            d_, sd = mk(H, I, 9500 + 2 * c)
+            dns.append(qw.Weight.pack_device(ctx, d_, wf, scales=sd))
+        for M in (32, 128):
+            x = randn(M, H, dtype=xdt)
+            h = torch.empty(M, I, device="cuda", dtype=xdt)
+            r = randn(M, H, dtype=xdt)
+            g = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, w, x, h) for w in gus])
+            us = 1e3 * timer.run(g.launch, max(5, steps), 2) / n_copies
+            b = 2 * I * H * wb + (2 * I * 4 if fmt == "int8" else 0) + M * H * 2 + M * I * 2
+            out[f"wide_gateup_{fmt}_M{M}"] = {"us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                                              "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK, 1),
+                                              "bytes_per_launch": b}
+            log("wide", fmt, M, out[f"wide_gateup_{fmt}_M{M}"])
+            del g
+            g = graphed(qw, ctx, stream, lambda: [qw.linear(ctx, w, h, r, residual=r) for w in dns])
+            us = 1e3 * timer.run(g.launch, max(5, steps), 2) / n_copies
+            b = H * I * wb + (H * 4 if fmt == "int8" else 0) + M * I * 2 + 2 * M * H * 2
+            out[f"wide_down_{fmt}_M{M}"] = {"us_per_launch": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                                            "pct_hbm": round(100 * b / us / 1e3 / HBM_PEAK, 1),
+                                            "bytes_per_launch": b}
+            log("wide", fmt, M, out[f"wide_down_{fmt}_M{M}"])
+            del g
+        del gus, dns
     return out
 
 
