@@ -441,6 +441,34 @@ def run_cfg3(qw, ctx, torch, timer, stream, randn, steps):
                                           "TFLOPs": round(fl / ms / 1e9, 2)}
         log("cfg3", M, extra[f"cfg3_int8_stack_M{M}"])
         del g
+    # The same 24 layers as ONE persistent projection chain (qw_chain) at
+    # decode sizes, in the model's dependency order: in -> out (reading the
+    # first 2048 outputs of in, the attention core's stand-in) + residual ->
+    # gate/up -> down + residual -> the next layer's in.
+    for M in (1, 2):
+        xa = randn(M, H, dtype=torch.float16)
+        xo = torch.empty(M, H, device="cuda", dtype=torch.float16)
+        slots = [{"len": H, "init": xa, "out": xo}, {"len": 8192}, {"len": I}]
+        ops = []
+        for L in layers:
+            ops += [{"w": L["in"], "in": 0, "out": 1}, {"w": L["out"], "in": 1, "out": 0, "residual": True},
+                    {"w": L["gu"], "in": 0, "out": 2}, {"w": L["down"], "in": 2, "out": 0, "residual": True}]
+        ch = qw.Chain(ctx, qw.F16, M, slots, ops)
+        g = graphed(qw, ctx, stream, lambda: ch.launch(stream))
+        ms = timer.run(g.launch, steps, 2)
+        if ctx.device_error():
+            raise RuntimeError("device error flag after the projection chain")
+        act = 0
+        for li in range(LAYERS):
+            n_in = 8192 if li in LINEAR_LAYERS else 5120
+            act += M * 2 * (1024 + n_in + 2048 + 1024 * 2 + 1024 + I + I + 1024 * 2)
+        b = wbytes + act
+        extra[f"cfg3_int8_chain_M{M}"] = {"us_per_step": round(ms * 1e3, 1), "GBps": round(b / ms / 1e6, 1),
+                                          "pct_hbm": round(100 * b / ms / 1e6 / HBM_PEAK, 1),
+                                          "launches": 1, "ops": len(ops)}
+        log("cfg3 chain", M, extra[f"cfg3_int8_chain_M{M}"])
+        del g
+        ch.close()
     del layers
 
     return extra

@@ -204,6 +204,52 @@ qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const
                        const float* const* gamma, float eps, const void* x, qw_dtype xdt, void* y, int M,
                        hipStream_t stream);
 
+/* ---- a chain of dependent projections in one launch (decode) -----------------
+ * The projection sequence of a decoder layer between its attention /
+ * Gated-DeltaNet cores (CudaLayer::forward, cuda_engine.cu:105-124: the input
+ * and output projections of CudaLinearAttention / CudaFullAttention,
+ * linear_attention_cuda.cu:174-187, full_attention_cuda.cu:451-600, and
+ * CudaMLP::forward_add_residual, mlp_cuda.cu:295-337), over several layers,
+ * at M <= 2 decode tokens, as ONE persistent launch.  Activations live in
+ * "slots" (vectors of `len` 16-bit values per token, BF16 for BF16 weights,
+ * F16 for INT8 weights); op i computes
+ *     slot[out][m][n] = epi( sum_k W[n][k] * pre(slot[in][m][in_offset + k]) )
+ * with pre = RMSNorm(.) * (1 + gamma) over the K inputs (norm = 1; gamma
+ * NULL when the weight carries it), epi = SiLU(gate)*up for GLU weights,
+ * + the slot's previous value (residual = 1), the result rounded to the
+ * slot's type -- the result of the same qw_linear calls with 16-bit outputs,
+ * within FP32 summation order.  Every op must read the previous op's output
+ * slot (op 0: a slot with `init`), never its own output slot, and K <= 3584;
+ * at most 128 ops per chain.
+ * The plan (op table, slot storage) is built once on the device by
+ * qw_chain_create and replayed by qw_chain_launch (capture-safe: no memset, no
+ * allocation).  It needs the GPU to itself (its 256 workgroups of 1024 threads
+ * must all be resident); a hand-off that does not arrive within 0.2 s raises
+ * the device error flag instead of hanging.  No counterpart class in the
+ * reference: its decode runs these projections as separate kernel launches. */
+typedef struct qw_chain qw_chain;
+typedef struct qw_chain_slot {
+    int len;           /* values per token (a multiple of 16) */
+    const void* init;  /* device [M][ld_init] values imported at launch start, or NULL */
+    int ld_init;       /* 0: len */
+    void* out;         /* device [M][ld_out]: ops writing the slot also store their rows here, or NULL */
+    int ld_out;        /* 0: len */
+} qw_chain_slot;
+typedef struct qw_chain_op {
+    const qw_weight* w;  /* BF16 or INT8 (one format per chain); GLU allowed */
+    int in;              /* input slot */
+    int in_offset;       /* first input element (a multiple of 64) */
+    int out;             /* output slot (not `in`) */
+    int residual;        /* 1: add the output slot's previous values */
+    int norm;            /* 1: RMSNorm prologue on the input */
+    const float* gamma;  /* its weight [K], or NULL when folded into w */
+    float eps;
+} qw_chain_op;
+qw_status qw_chain_create(qw_ctx* ctx, qw_dtype act_dtype, int M, int n_slots, const qw_chain_slot* slots,
+                          int n_ops, const qw_chain_op* ops, qw_chain** out);
+qw_status qw_chain_launch(qw_chain* chain, hipStream_t stream);
+qw_status qw_chain_destroy(qw_chain* chain);
+
 /* Reads and clears the context's device error flag: non-zero when a kernel
  * gave up a bounded wait (a fused MLP down task whose gate/up inputs never
  * completed within 0.2 s), when an attention token fell outside its cache, or

@@ -12,6 +12,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "../../include/qw_linear.h"
 #include "qw_internal.hpp"
@@ -1359,6 +1360,190 @@ qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const
         if (s != QW_OK) return s;
         in = y;
     }
+    return QW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// projection chains
+// ---------------------------------------------------------------------------
+
+struct qw_chain {
+    qw_ctx* ctx = nullptr;
+    qwk::ChainArgs args{};
+    int wf = 0, adt = 0;
+    uint8_t* mem = nullptr;  // op table, epoch words, slot words
+    uint64_t* trace = nullptr;  // QW_CHAIN_TRACE=<file>: per-op stamps of the last launch, written at destroy
+    std::string trace_path;
+};
+
+qw_status qw_chain_create(qw_ctx* ctx, qw_dtype act_dtype, int M, int n_slots, const qw_chain_slot* slots,
+                          int n_ops, const qw_chain_op* ops, qw_chain** out) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!slots || !ops || !out) return fail(ctx, QW_ERR_NULL, "chain: NULL argument");
+    *out = nullptr;
+    if (M < 1 || M > qwk::chain_max_m()) return fail(ctx, QW_ERR_SHAPE, "chain: M=%d outside 1..%d", M, qwk::chain_max_m());
+    if (n_slots < 1 || n_slots > 64 || n_ops < 1 || n_ops > qwk::kChainMaxOps)
+        return fail(ctx, QW_ERR_SHAPE, "chain: %d slots / %d ops out of range", n_slots, n_ops);
+    if (ctx->num_cus < qwk::chain_grid()) return fail(ctx, QW_ERR_INVALID, "chain: needs %d CUs", qwk::chain_grid());
+    const int wf = ops[0].w ? (int)ops[0].w->wf : -1;
+    if (!((wf == QW_WFMT_BF16 && act_dtype == QW_BF16) || (wf == QW_WFMT_INT8_ROWSCALE && act_dtype == QW_F16)))
+        return fail(ctx, QW_ERR_DTYPE, "chain: BF16 weights with BF16 slots or INT8 weights with F16 slots");
+    size_t words = 0;
+    std::vector<size_t> slot_word0(n_slots);
+    int n_imports = 0;
+    for (int s = 0; s < n_slots; ++s) {
+        const qw_chain_slot& sl = slots[s];
+        if (sl.len < 16 || sl.len % 16) return fail(ctx, QW_ERR_SHAPE, "chain: slot %d length %d", s, sl.len);
+        if (sl.init && ((sl.ld_init ? sl.ld_init : sl.len) < sl.len || (sl.ld_init % 2) || !aligned(sl.init, 4)))
+            return fail(ctx, QW_ERR_SHAPE, "chain: slot %d init layout", s);
+        if (sl.out && ((sl.ld_out ? sl.ld_out : sl.len) < sl.len || (sl.ld_out % 2) || !aligned(sl.out, 4)))
+            return fail(ctx, QW_ERR_SHAPE, "chain: slot %d out layout", s);
+        if (sl.init && ++n_imports > qwk::kChainMaxImports)
+            return fail(ctx, QW_ERR_SHAPE, "chain: more than %d imported slots", qwk::kChainMaxImports);
+        slot_word0[s] = words;
+        words += (size_t)M * (sl.len / 2);
+    }
+    // per slot: the writer of its current values (op index + 1, 0 = imported,
+    // -1 = none) and how many rows of it that writer produced
+    std::vector<int> writer(n_slots), rows(n_slots);
+    for (int s = 0; s < n_slots; ++s) {
+        writer[s] = slots[s].init ? 0 : -1;
+        rows[s] = slots[s].init ? slots[s].len : 0;
+    }
+    std::vector<qwk::ChainOp> dev(n_ops);
+    int base = 0;
+    for (int i = 0; i < n_ops; ++i) {
+        const qw_chain_op& op = ops[i];
+        const qw_weight* W = op.w;
+        if (!W) return fail(ctx, QW_ERR_NULL, "chain: op %d weight is NULL", i);
+        if ((int)W->wf != wf) return fail(ctx, QW_ERR_DTYPE, "chain: op %d weight format differs", i);
+        if (op.in < 0 || op.in >= n_slots || op.out < 0 || op.out >= n_slots || op.in == op.out)
+            return fail(ctx, QW_ERR_INVALID, "chain: op %d slots %d -> %d", i, op.in, op.out);
+        if (i > 0 && op.in != ops[i - 1].out)
+            return fail(ctx, QW_ERR_INVALID, "chain: op %d must read op %d's output slot", i, i - 1);
+        if (writer[op.in] < 0) return fail(ctx, QW_ERR_INVALID, "chain: op %d reads slot %d before any value", i, op.in);
+        if (W->K > qwk::kChainMaxK || op.in_offset < 0 || op.in_offset % 64 || op.in_offset + W->K > rows[op.in])
+            return fail(ctx, QW_ERR_SHAPE, "chain: op %d input [%d, %d) of %d rows", i, op.in_offset,
+                        op.in_offset + W->K, rows[op.in]);
+        if (W->N % 16 || W->N > slots[op.out].len) return fail(ctx, QW_ERR_SHAPE, "chain: op %d N=%d", i, W->N);
+        if (op.residual && (writer[op.out] < 0 || rows[op.out] < W->N))
+            return fail(ctx, QW_ERR_INVALID, "chain: op %d residual rows not written before", i);
+        if (op.norm && !op.gamma && !W->norm_folded)
+            return fail(ctx, QW_ERR_NULL, "chain: op %d norm without gamma or folded weight", i);
+        if (op.gamma && (W->norm_folded || !op.norm)) return fail(ctx, QW_ERR_INVALID, "chain: op %d gamma", i);
+        if (op.norm && !(op.eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "chain: op %d eps", i);
+        const int n_blk = W->glu ? W->N / 16 : W->phys_tiles;
+        if (n_blk > qwk::chain_max_blocks()) return fail(ctx, QW_ERR_SHAPE, "chain: op %d has %d blocks", i, n_blk);
+        const int RT = W->glu ? 2 : 1;
+        const int per_wg = (n_blk + qwk::chain_grid() - 1) / qwk::chain_grid();
+        const int units = per_wg * W->ksteps;
+        const int per_wave = (units + qwk::chain_compute_waves() - 1) / qwk::chain_compute_waves();
+        if (per_wave * RT > qwk::chain_max_loads(wf) || W->ksteps < 10)
+            return fail(ctx, QW_ERR_SHAPE, "chain: op %d needs %d weight loads per wave", i, per_wave * RT);
+        qwk::ChainOp& d = dev[i];
+        d.w = W->packed;
+        d.scales = W->scales;
+        d.glu = W->glu;
+        d.n_blk = n_blk;
+        d.ksteps = W->ksteps;
+        d.K = W->K;
+        d.N = W->N;
+        d.in_ld = slots[op.in].len / 2;
+        d.in_off = op.in_offset;
+        d.in_tag = writer[op.in];
+        d.gamma = op.gamma;
+        d.norm = op.norm ? 1 : 0;
+        d.eps = op.eps;
+        d.out_ld = slots[op.out].len / 2;
+        d.exp = static_cast<uint16_t*>(slots[op.out].out);
+        d.exp_ld = slots[op.out].ld_out ? slots[op.out].ld_out : slots[op.out].len;
+        d.residual = op.residual ? 1 : 0;
+        d.res_tag = op.residual ? writer[op.out] : 0;
+        // consecutive ops continue the round robin where the last one ended,
+        // so a small op after a small op lands on other CUs
+        d.base = base;
+        base = (base + n_blk) % qwk::chain_grid();
+        writer[op.out] = i + 1;
+        rows[op.out] = std::max(rows[op.out], W->N);
+    }
+    qw_chain* ch = new qw_chain();
+    ch->ctx = ctx;
+    ch->wf = wf;
+    ch->adt = (int)act_dtype;
+    const size_t op_bytes = ((sizeof(qwk::ChainOp) * n_ops + 255) / 256) * 256;
+    const size_t total = op_bytes + 256 + words * 8;
+    hipSetDevice(ctx->device);
+    if (hipMalloc(&ch->mem, total) != hipSuccess) {
+        delete ch;
+        return fail(ctx, QW_ERR_NOMEM, "chain: hipMalloc of %zu bytes failed", total);
+    }
+    uint64_t* wbase = reinterpret_cast<uint64_t*>(ch->mem + op_bytes + 256);
+    for (int i = 0; i < n_ops; ++i) {
+        dev[i].in_words = wbase + slot_word0[ops[i].in];
+        dev[i].out_words = wbase + slot_word0[ops[i].out];
+    }
+    hipError_t e = hipMemcpy(ch->mem, dev.data(), sizeof(qwk::ChainOp) * n_ops, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(ch->mem + op_bytes, 0, 256 + words * 8);
+    // epoch 1: the zeroed slot words (tag 0) never match a tag of a launch
+    const unsigned one = 1u;
+    if (e == hipSuccess) e = hipMemcpy(ch->mem + op_bytes, &one, sizeof one, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        hipFree(ch->mem);
+        delete ch;
+        return hip_fail(ctx, e, "chain setup");
+    }
+    qwk::ChainArgs& A = ch->args;
+    A.ops = reinterpret_cast<const qwk::ChainOp*>(ch->mem);
+    A.n_ops = n_ops;
+    A.M = M;
+    A.epoch = reinterpret_cast<unsigned*>(ch->mem + op_bytes);
+    A.err = ctx->mlp_ctl + 3;
+    for (int s = 0; s < n_slots; ++s) {
+        if (!slots[s].init) continue;
+        qwk::ChainImport& im = A.imports[A.n_imports++];
+        im.words_ptr = wbase + slot_word0[s];
+        im.words = slots[s].len / 2;
+        im.src = slots[s].init;
+        im.ld = slots[s].ld_init ? slots[s].ld_init : slots[s].len;
+    }
+    if (const char* tp = getenv("QW_CHAIN_TRACE")) {
+        // timing probe: [op][4][256] s_memrealtime stamps (input polled, input
+        // seen by compute wave 0, its MFMAs done, epilogue issued) of the last
+        // launch, dumped to the file at destroy
+        if (hipMalloc(&ch->trace, (size_t)n_ops * 4 * 256 * 8) == hipSuccess) {
+            hipMemset(ch->trace, 0, (size_t)n_ops * 4 * 256 * 8);
+            A.trace = ch->trace;
+            ch->trace_path = tp;
+        }
+    }
+    *out = ch;
+    return QW_OK;
+}
+
+qw_status qw_chain_launch(qw_chain* ch, hipStream_t stream) {
+    if (!ch) return QW_ERR_NULL;
+    hipError_t e = qwk::launch_chain(ch->args, ch->wf, ch->adt, stream);
+    if (e != hipSuccess) return hip_fail(ch->ctx, e, "chain launch");
+    return QW_OK;
+}
+
+qw_status qw_chain_destroy(qw_chain* ch) {
+    if (!ch) return QW_ERR_NULL;
+    hipSetDevice(ch->ctx->device);
+    hipDeviceSynchronize();
+    if (ch->trace) {
+        std::vector<uint64_t> h((size_t)ch->args.n_ops * 4 * 256);
+        if (hipMemcpy(h.data(), ch->trace, h.size() * 8, hipMemcpyDeviceToHost) == hipSuccess) {
+            if (FILE* f = fopen(ch->trace_path.c_str(), "wb")) {
+                fwrite(h.data(), 8, h.size(), f);
+                fclose(f);
+            }
+        }
+        hipFree(ch->trace);
+    }
+    hipFree(ch->mem);
+    delete ch;
     return QW_OK;
 }
 

@@ -165,6 +165,54 @@ int mlp_stack_max_m();
 int mlp_stack_grid();
 hipError_t launch_mlp_stack(const MlpStackArgs& a, int wf, int xdt, hipStream_t stream);
 
+// A chain of dependent projections in one persistent launch (qw_chain.hip),
+// decode (M <= chain_max_m() tokens); the op table lives in device memory.
+constexpr int kChainMaxK = 3584;     // inputs per op (the largest Qwen3.5-0.8B K)
+constexpr int kChainMaxImports = 8;  // slots fed from buffers at launch start
+constexpr int kChainMaxOps = 128;    // ops per chain (the op table is held in LDS)
+struct ChainOp {
+    const uint8_t* w;          // packed weight
+    const float* scales;       // INT8 per physical row, or nullptr
+    int glu;                   // 1: blocks are gate/up tile pairs (SiLU*mul)
+    int n_blk;                 // output blocks (16 rows each)
+    int ksteps;                // k-steps of the packed weight
+    int K, N;                  // inputs, outputs (N = 16 * n_blk)
+    const uint64_t* in_words;  // input slot words [M][in_ld]
+    int in_ld, in_off;         // words per token row; first input element (even)
+    int in_tag;                // tag of the input's writer: op index + 1, 0 = imported
+    const float* gamma;        // RMSNorm weight of the prologue, or nullptr
+    int norm;                  // 1: RMSNorm prologue (gamma, or folded into the weight)
+    float eps;
+    uint64_t* out_words;       // output slot words [M][out_ld]
+    int out_ld;
+    uint16_t* exp;             // plain copy of the output [M][exp_ld], or nullptr
+    int exp_ld;
+    int residual;              // 1: add the slot's previous values of the output rows
+    int res_tag;               // tag of their writer
+    int base;                  // first workgroup of the round robin over the blocks
+};
+struct ChainImport {
+    uint64_t* words_ptr;       // slot words [M][words]
+    int words;                 // words per token row
+    const void* src;           // [M][ld] 16-bit values
+    int ld;
+};
+struct ChainArgs {
+    const ChainOp* ops;
+    int n_ops, M;
+    ChainImport imports[kChainMaxImports];
+    int n_imports;
+    unsigned* epoch;           // [2]: launch epoch (advanced by every launch), abort word
+    unsigned* err;             // device error flag
+    uint64_t* trace;           // timing probe [op][4][256] real-time stamps, or nullptr (QW_CHAIN_TRACE)
+};
+int chain_grid();
+int chain_max_m();
+int chain_max_blocks();        // output blocks per op
+int chain_max_loads(int wf);   // weight loads per compute wave and op
+int chain_compute_waves();
+hipError_t launch_chain(const ChainArgs& a, int wf, int xdt, hipStream_t stream);
+
 // Gated-DeltaNet decode step (qw_gdn.hip): one token of each of B sequences.
 struct GdnArgs {
     int B, T, nh, kd, vd, K;  // B sequences of T consecutive tokens; row = b*T + t

@@ -32,6 +32,7 @@ EXPORTS = [
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_mlp_stack", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_embedding_gather", "qw_positions_add", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
+    "qw_chain_create", "qw_chain_launch", "qw_chain_destroy",
 ]
 
 
@@ -81,6 +82,29 @@ class Epilogue(ctypes.Structure):
         ("eps", ctypes.c_float),
         ("split_period", ctypes.c_int),
         ("y2", ctypes.c_void_p),
+    ]
+
+
+class ChainSlot(ctypes.Structure):
+    _fields_ = [
+        ("len", ctypes.c_int),
+        ("init", ctypes.c_void_p),
+        ("ld_init", ctypes.c_int),
+        ("out", ctypes.c_void_p),
+        ("ld_out", ctypes.c_int),
+    ]
+
+
+class ChainOp(ctypes.Structure):
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("in_", ctypes.c_int),
+        ("in_offset", ctypes.c_int),
+        ("out", ctypes.c_int),
+        ("residual", ctypes.c_int),
+        ("norm", ctypes.c_int),
+        ("gamma", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
     ]
 
 
@@ -144,6 +168,9 @@ def lib():
         "qw_graph_end": ([_vp, _vp, pp], _i),
         "qw_graph_launch": ([_vp, _vp], _i),
         "qw_graph_destroy": ([_vp], _i),
+        "qw_chain_create": ([_vp, _i, _i, _i, ctypes.POINTER(ChainSlot), _i, ctypes.POINTER(ChainOp), pp], _i),
+        "qw_chain_launch": ([_vp, _vp], _i),
+        "qw_chain_destroy": ([_vp], _i),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -441,6 +468,58 @@ def residual_rmsnorm(ctx, residual_in, a, residual_out, normed, gamma, eps=1e-6,
 def silu_mul(ctx, g, u, h, stream=None):
     ctx.check(lib().qw_silu_mul(ctx.handle, _ptr(g), _ptr(u), _ptr(h), _torch_code(g), g.numel(),
                                 _stream(stream)))
+
+
+class Chain:
+    """A chain of dependent projections run as one persistent launch
+    (qw_chain_create / qw_chain_launch).
+
+    slots: list of dicts {len, init (tensor [M][>=len] or None), out (tensor or None)};
+    ops: list of dicts {w: Weight, in, out, in_offset=0, residual=False,
+    gamma=None (tensor), norm=False, eps=1e-6}.  The tensors must stay alive
+    as long as the chain (their device addresses are baked into the plan)."""
+
+    def __init__(self, ctx, act_code, M, slots, ops):
+        self.ctx, self._keep = ctx, []
+        ss = (ChainSlot * len(slots))()
+        for i, sl in enumerate(slots):
+            ss[i].len = sl["len"]
+            for key, ldk in (("init", "ld_init"), ("out", "ld_out")):
+                t = sl.get(key)
+                if t is not None:
+                    setattr(ss[i], key, t.data_ptr())
+                    setattr(ss[i], ldk, t.stride(0) if t.dim() == 2 else 0)
+                    self._keep.append(t)
+        oo = (ChainOp * len(ops))()
+        for i, op in enumerate(ops):
+            oo[i].w = op["w"].handle.value
+            oo[i].in_ = op["in"]
+            oo[i].in_offset = op.get("in_offset", 0)
+            oo[i].out = op["out"]
+            oo[i].residual = 1 if op.get("residual") else 0
+            g = op.get("gamma")
+            oo[i].norm = 1 if (op.get("norm") or g is not None) else 0
+            if g is not None:
+                oo[i].gamma = g.data_ptr()
+                self._keep.append(g)
+            oo[i].eps = op.get("eps", 1e-6)
+            self._keep.append(op["w"])
+        self._h = ctypes.c_void_p()
+        ctx.check(lib().qw_chain_create(ctx.handle, act_code, M, len(slots), ss, len(ops), oo, ctypes.byref(self._h)))
+
+    def launch(self, stream=None):
+        self.ctx.check(lib().qw_chain_launch(self._h, _stream(stream)))
+
+    def close(self):
+        if self._h:
+            lib().qw_chain_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class Graph:
