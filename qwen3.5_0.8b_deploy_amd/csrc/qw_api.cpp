@@ -953,6 +953,41 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
     return run_skinny(ctx, W, x, xdt, ldx, M, y, ydt, ldy, ep, nullptr, nullptr, stream, tg);
 }
 
+// The lm_head route shared by the context and no-allocation entry points:
+// the weight-stationary argmax from wide_min tokens where it applies, else
+// the GEMM or the small-M kernels.
+static qw_status lmhead_route(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M, int32_t* ids,
+                              float* maxv, hipStream_t stream) {
+    if (ctx->wide && !(ctx->gemm_forced && M >= ctx->gemm_min_m) && M >= ctx->wide_min && M <= ctx->wide_max &&
+        !E->glu && aligned(E->packed, 16)) {
+        qwk::WideArgmaxArgs a{};
+        int grid = 0;
+        size_t smem = 0;
+        if (qwk::wide_argmax_plan(E->wf, (int)hdt, M, E->K, ctx->num_cus, a, grid, smem)) {
+            a.w = E->packed;
+            a.scales = E->scales;
+            a.x = h;
+            a.ldx = E->K;
+            a.M = M;
+            a.K = E->K;
+            a.V = E->N;
+            a.n_tiles = E->phys_tiles;
+            a.n_blk = (E->phys_tiles + 1) / 2;
+            a.keys = ctx->keys;
+            a.done = ctx->done;
+            a.ids = ids;
+            a.maxv = maxv;
+            a.dbg = ctx->wide_dbg;
+            hipError_t e = qwk::launch_wide_argmax(a, E->wf, (int)hdt, grid, smem, stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "weight-stationary lm_head launch");
+            return QW_OK;
+        }
+    }
+    if (const int rows = gemm_route(ctx, E, hdt, M))
+        return run_gemm(ctx, E, rows, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, ids, maxv, stream);
+    return run_skinny(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, ids, maxv, stream, kSkinnyMaxM);
+}
+
 qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M,
                            int32_t* token_ids, float* max_logit, hipStream_t stream) {
     qw_status s = check_linear(ctx, E, h, hdt, E ? E->K : 0, M, nullptr, QW_F32, 0, nullptr, false);
@@ -960,10 +995,7 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
     if (!token_ids) return fail(ctx, QW_ERR_NULL, "token_ids is NULL");
     if (E->glu) return fail(ctx, QW_ERR_INVALID, "lm_head weight cannot be a GLU pair");
     if (M > kMaxKeys) return fail(ctx, QW_ERR_WORKSPACE, "M=%d exceeds %d argmax slots", M, kMaxKeys);
-    if (const int rows = gemm_route(ctx, E, hdt, M))
-        return run_gemm(ctx, E, rows, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
-    return run_skinny(ctx, E, h, hdt, E->K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream,
-                      kSkinnyMaxM);
+    return lmhead_route(ctx, E, h, hdt, M, token_ids, max_logit, stream);
 }
 
 }  // extern "C"
@@ -998,9 +1030,7 @@ qw_status lmhead_argmax_scratch(int device, const void* packed, const float* sca
     W.owns = false;
     qw_status s = check_linear(&c, &W, h, hdt, K, M, nullptr, QW_F32, 0, nullptr, false);
     if (s != QW_OK) return s;
-    if (const int rows = gemm_route(&c, &W, hdt, M))
-        return run_gemm(&c, &W, rows, h, hdt, K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream);
-    return run_skinny(&c, &W, h, hdt, K, M, nullptr, QW_F32, 0, nullptr, token_ids, max_logit, stream, kSkinnyMaxM);
+    return lmhead_route(&c, &W, h, hdt, M, token_ids, max_logit, stream);
 }
 
 }  // namespace qwi

@@ -91,6 +91,24 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
                int force_cfg, WidePlan& p);
 hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream);
 
+// Tied lm_head + greedy argmax, weight-stationary (qw_wide.hip), 1..256 tokens.
+struct WideArgmaxArgs {
+    const uint8_t* w;          // packed E (non-GLU)
+    const float* scales;       // INT8 per-row scales or nullptr
+    const void* x;             // [M][ldx] hidden states
+    int ldx, M, K, V;
+    int n_tiles, n_blk;        // 16-row tiles, 32-row blocks
+    int ksteps;
+    int T, Mg, CT;             // token groups of Mg tokens, CT 16-token tiles each
+    unsigned long long* keys;  // [M] (self-resetting)
+    unsigned* done;            // completion counter (self-resetting)
+    int32_t* ids;
+    float* maxv;
+    int dbg;                   // timing probes only (wrong results): 1 no MFMAs
+};
+bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs& a, int& grid, size_t& smem);
+hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid, size_t smem, hipStream_t stream);
+
 // LDS double-buffered MFMA GEMM for many tokens (qw_gemm.hip).
 struct GemmArgs {
     const uint8_t* w;        // packed weight

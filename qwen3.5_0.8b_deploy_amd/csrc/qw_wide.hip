@@ -497,6 +497,218 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
 }
 
 // ---------------------------------------------------------------------------
+// Tied lm_head with the fused greedy argmax at 17..256 tokens.
+//
+// The same weight-stationary idea for a weight far larger than the grid: the
+// activations of a token group (at most 64 tokens) are staged once per
+// workgroup (direct-to-LDS, B-operand order), and each of its four waves walks 32-row
+// blocks of E (grid stride over all workgroups of its token group) in
+// chunks of 8 k-steps, two chunks in flight (the loads of chunk s+2 are
+// issued as chunk s is consumed; they are unconditional, so the compiler
+// counts them and waits for exactly the chunk it uses).  A block's logits
+// never leave the registers: each lane keeps, per token tile, the running
+// maximum of the orderable key (logit, ~row) -- ties go to the lowest row.
+// At the end the waves' keys meet in LDS, one 64-bit atomic max per
+// token and workgroup merges the grid, and the last workgroup (completion
+// counter) decodes the keys into ids and returns keys and counter to zero.
+// Replaces lm_head_gemv_kernel_optimized + block_argmax_kernel
+// (lm_head_cuda.cu:38-99, gpu_sampler_argmax.cu:14-43) at these batches.
+// ---------------------------------------------------------------------------
+constexpr int kArgU = 8;  // k-steps per chunk
+
+constexpr int kArgNW = 4;  // waves per workgroup (eight measured slower: 92 vs 86 us BF16 at 32 tokens)
+
+template <int WF, int XDT, int CT>
+__global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs a) {
+    constexpr int NW = kArgNW, RT = 2, U = kArgU;
+    constexpr int KS = WideT<WF>::KS, XU = WideT<WF>::XU, KEW = WideT<WF>::KEW;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ unsigned long long kbest[NW][CT * 16];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int T = a.T;
+    const int b = (int)blockIdx.x;
+    const int t = (b / 8) % T;                       // token group (8 workgroups apart: one XCD)
+    const int gi = (b % 8) + 8 * (b / (8 * T));      // workgroup within the token group
+    const int Gt = (int)gridDim.x / T;
+    const int M0 = t * a.Mg, Mt = min(a.Mg, a.M - M0);
+    const int nch = a.ksteps / U;                    // chunks per block
+    const int gw = gi * NW + wave, stride = Gt * NW;
+    const int nblk_w = gw < a.n_blk ? (a.n_blk - gw + stride - 1) / stride : 0;
+    const int nseq = nblk_w * nch;
+
+    // ---- activations of the token group -> LDS (issued before the weights) ----
+    {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2));
+        const int xunits = CT * a.ksteps * XU;
+        for (int u = wave; u < xunits; u += NW) {
+            const int h = u % XU, q = u / XU;
+            const int ct = q % CT, ks = q / CT;
+            const int m = ct * 16 + r;
+            const int k = ks * KS + g * KEW + h * 8;
+            lds_dma16(xr, lds + u * 1024, m < Mt ? (uint32_t)(((M0 + m) * a.ldx + k) * 2) : OOB);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const uint32_t tile_bytes = (uint32_t)a.ksteps * 1024u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_tiles * tile_bytes));
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scales ? (const void*)a.scales : a.x,
+                                                 a.scales ? (uint32_t)a.n_tiles * 64u : 0u);
+    u32x4 A0[U][RT], A1[U][RT];
+    u32x4 S0[RT], S1[RT];
+    // chunk s of this wave: block gw + (s / nch) * stride, k-steps from (s % nch) * U;
+    // the row scales come with a block's first chunk
+    auto issue = [&](int s, auto& A, auto& S) {
+        const int blk = gw + (s / nch) * stride;
+        const int c = s % nch;
+        const bool ok = s < nseq;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int pt = 2 * blk + rt;
+            const bool tok = ok && pt < a.n_tiles;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                A[u][rt] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               wrs, tok ? (uint32_t)pt * tile_bytes + (uint32_t)(c * U + u) * 1024u + lane * 16 : OOB, 0,
+                               AUX_NT));
+            S[rt] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, tok && c == 0 ? (uint32_t)((pt * 16 + g * 4) * 4) : OOB,
+                                                             0, 0));
+        }
+    };
+    issue(0, A0, S0);
+    issue(1, A1, S1);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vm_wait(2 * RT * (U + 1)));  // the activations have landed
+    __syncthreads();
+    if constexpr (WF == WF_I8 && XDT == DT_BF16) {
+        // BF16 activations for the f16 MFMA of INT8 weights: converted once in
+        // LDS (exact in the f16 normal range)
+        uint32_t* xw = reinterpret_cast<uint32_t*>(lds);
+        const int nwords = CT * a.ksteps * XU * 256;
+        for (int i = threadIdx.x; i < nwords; i += NW * 64) {
+            const uint32_t v = xw[i];
+            xw[i] = f32_to_f16_bits(bf16_bits_to_f32(v & 0xffffu)) | (f32_to_f16_bits(bf16_bits_to_f32(v >> 16)) << 16);
+        }
+        __syncthreads();
+    }
+
+    f32x4 acc[RT][CT];
+    f32x4 sc[RT];
+    unsigned long long best[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) best[ct] = 0ull;
+    auto body = [&](int s, auto& A, auto& S) {
+        if (s >= nseq) return;
+        const int c = s % nch;
+        if (a.dbg & 1) {  // timing probe: the weight stream alone
+            if (c == nch - 1) best[0] = max(best[0], (unsigned long long)A[0][0][0] + A[U - 1][1][3]);
+            return;
+        }
+        if (c == 0) {
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                sc[rt] = a.scales ? as_f32x4(S[rt]) : f32x4{1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int ks = c * U + u;
+            const uint8_t* xp = lds + (ks * CT * XU) * 1024 + lane * 16;
+            if constexpr (WF == WF_BF16) {
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const bf16x8 bb = *reinterpret_cast<const bf16x8*>(xp + ct * 1024);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        acc[rt][ct] = mfma_bf16(__builtin_bit_cast(bf16x8, A[u][rt]), bb, acc[rt][ct]);
+                }
+            } else {
+                f16x8 a0[RT], a1[RT];
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) i8unit_to_f16(A[u][rt], a0[rt], a1[rt]);
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const f16x8 b0 = *reinterpret_cast<const f16x8*>(xp + ct * 2048);
+                    const f16x8 b1 = *reinterpret_cast<const f16x8*>(xp + ct * 2048 + 1024);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
+                        acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
+                    }
+                }
+            }
+        }
+        if (c == nch - 1) {  // the block's logits: into the running keys
+            const int blk = gw + (s / nch) * stride;
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                if (ct * 16 + r >= Mt) continue;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const f32x4 v = acc[rt][ct] * sc[rt];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = blk * 32 + rt * 16 + g * 4 + e;
+                        if (row < a.V) {
+                            const unsigned long long kk = argmax_key(v[e], (uint32_t)row);
+                            best[ct] = kk > best[ct] ? kk : best[ct];
+                        }
+                    }
+                }
+            }
+        }
+    };
+    for (int s = 0; s < nseq; s += 2) {
+        body(s, A0, S0);
+        issue(s + 2, A0, S0);
+        body(s + 1, A1, S1);
+        issue(s + 3, A1, S1);
+    }
+
+    // ---- keys: the four row groups of a lane's token, the waves, the grid ----
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+#pragma unroll
+        for (int sh = 16; sh <= 32; sh <<= 1) {
+            const unsigned long long o = __shfl_xor(best[ct], sh);
+            best[ct] = o > best[ct] ? o : best[ct];
+        }
+        if (g == 0) kbest[wave][ct * 16 + r] = best[ct];
+    }
+    __syncthreads();
+    if (threadIdx.x < CT * 16 && (int)threadIdx.x < Mt) {
+        unsigned long long k = kbest[0][threadIdx.x];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) k = kbest[w][threadIdx.x] > k ? kbest[w][threadIdx.x] : k;
+        if (k != 0ull) __hip_atomic_fetch_max(&a.keys[M0 + threadIdx.x], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the key updates are device-scope read-modify-writes: their completion
+    // orders them before this workgroup's completion count
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ unsigned last;
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    for (int m = threadIdx.x; m < a.M; m += NW * 64) {
+        const unsigned long long kk = __hip_atomic_exchange(&a.keys[m], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.ids[m] = (int32_t)key_index(kk);
+        if (a.maxv) a.maxv[m] = key_value(kk);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 namespace {
@@ -644,6 +856,43 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
         }
     }
     return found;
+}
+
+bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs& a, int& grid, size_t& smem) {
+    if (!((wf == WF_BF16 && xdt == DT_BF16) || (wf == WF_I8 && (xdt == DT_F16 || xdt == DT_BF16))) || M < 1 ||
+        M > 256)
+        return false;
+    const int ks = K / (wf == WF_I8 ? 64 : 32);
+    if (ks % kArgU != 0) return false;
+    const int T = (M + 63) / 64;
+    const int Mg = (M + T - 1) / T;
+    const int CT = Mg <= 32 ? 2 : 4;
+    smem = (size_t)CT * ks * (wf == WF_I8 ? 2 : 1) * 1024;
+    if (smem > kWideMaxLds) return false;
+    grid = num_cus / (8 * T) * (8 * T);
+    if (grid < 8 * T) return false;
+    a.T = T;
+    a.Mg = Mg;
+    a.CT = CT;
+    a.ksteps = ks;
+    return true;
+}
+
+hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid, size_t smem, hipStream_t stream) {
+    auto go = [&](auto kern) {
+        static bool configured = false;
+        (void)configured;
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideMaxLds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kArgNW * 64), smem, stream, a);
+        return hipGetLastError();
+    };
+    if (wf == WF_BF16) return a.CT == 2 ? go(wide_argmax_kernel<WF_BF16, DT_BF16, 2>)
+                                        : go(wide_argmax_kernel<WF_BF16, DT_BF16, 4>);
+    if (xdt == DT_BF16)
+        return a.CT == 2 ? go(wide_argmax_kernel<WF_I8, DT_BF16, 2>) : go(wide_argmax_kernel<WF_I8, DT_BF16, 4>);
+    return a.CT == 2 ? go(wide_argmax_kernel<WF_I8, DT_F16, 2>) : go(wide_argmax_kernel<WF_I8, DT_F16, 4>);
 }
 
 hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream) {

@@ -2,8 +2,10 @@
 the benchmark itself takes (default contexts, no forced kernel choice).
 
 Config 5: the tied lm_head + greedy argmax over E[248320][1024] (BF16, and
-INT8 per-row scaled from the same BF16 E), M in {1, 32, 128}; M = 128 runs
-the GEMM with 256-row blocks, M <= 32 the small-M kernels.  Reference:
+INT8 per-row scaled from the same BF16 E), M in {1, 17, 32, 64, 128, 200,
+256}; from 17 tokens the weight-stationary argmax kernel runs (token groups of
+at most 64 tokens: 2 or 4 token tiles, 1 to 4 groups), M = 1 the small-M
+kernel.  Reference:
 LMHead::forward (src/backend/cpu/core/heads/lm_head.cpp:24-39) followed by
 Sampler::sample_greedy (sampler.cpp:41-43, std::max_element: the first
 maximum wins).  Expected ids come from the C oracle's sequential FP32
@@ -56,7 +58,7 @@ def lm(qw):
     h[128][1024] with the planted rows."""
     import oracle
     g = torch.Generator().manual_seed(5)
-    h = torch.empty(128, H).normal_(0.0, 1.0, generator=g).bfloat16()
+    h = torch.empty(256, H).normal_(0.0, 1.0, generator=g).bfloat16()
     E = torch.empty(V, H).normal_(0.0, 0.02, generator=g)
     hf = h.float()
     c = 0.0625  # exact in BF16 and, as the row maximum, in INT8 (q = +-127)
@@ -117,7 +119,7 @@ def _run(qw, d, w, hx, M):
     return got, mx.cpu().numpy()
 
 
-@pytest.mark.parametrize("M", [1, 32, 128])
+@pytest.mark.parametrize("M", [1, 17, 32, 64, 128, 200, 256])
 def test_cfg5_lmhead_bf16_full_vocab(qw, lm, M):
     d = lm
     o = d["oracle"]
@@ -144,7 +146,7 @@ def test_cfg5_lmhead_bf16_full_vocab(qw, lm, M):
         assert int(g2[0]) == UNIQUE_T2
 
 
-@pytest.mark.parametrize("M", [1, 32, 128])
+@pytest.mark.parametrize("M", [1, 17, 32, 64, 128, 200, 256])
 def test_cfg5_lmhead_int8_full_vocab(qw, lm, M):
     """INT8 E quantized on the device from the BF16 E (the recipe of
     mlp_cuda.cu:22-39), F16 activations.  The oracle is the reference's

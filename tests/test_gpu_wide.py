@@ -298,3 +298,42 @@ def test_int8_glu_norm(qw, wctx, wctx_sep_norm, oracle, relerr, M, sep):
     # the weights times (1 + gamma), or the normalized activations, are
     # rounded to F16 for the MFMA (2^-11 per term)
     assert relerr(host(h), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("M", [17, 40, 100, 256])
+@pytest.mark.parametrize("fmt", ["bf16", "int8", "int8_bf16x"])
+def test_lmhead_argmax_odd_vocab(qw, ctx, oracle, fmt, M):
+    """The weight-stationary lm_head argmax on a vocabulary of 627 tiles (the
+    last block holds one tile, its last 8 rows past the end): ids equal the
+    oracle's (LMHead::forward + Sampler::sample_greedy, lm_head.cpp:24-39,
+    sampler.cpp:41-43) where its top-2 gap is clear, the maximum planted in
+    the last row is found, and exact ties resolve to the lowest row.
+    "int8_bf16x": INT8 weights with BF16 activations (converted to f16 in
+    LDS, exact for these magnitudes)."""
+    V, K = 10024, 1024
+    E = oracle.normal((V, K), 3500, 0.0, 0.02)
+    h = oracle.normal((M, K), 3501)
+    hb = oracle.round_f16(h) if fmt == "int8" else oracle.round_bf16(h)
+    c = 0.0625
+    E[V - 1] = c * np.sign(hb[0])        # token 0: unique maximum in the last row
+    E[[4100, 4101, 9999]] = c * np.sign(hb[1])  # token 1: exact tie -> 4100
+    Eb = oracle.round_bf16(E)
+    if fmt == "bf16":
+        w = qw.Weight.pack(ctx, Eb, qw.WFMT_BF16)
+        x = dev(hb, torch.bfloat16)
+        logits = hb.astype(np.float64) @ Eb.astype(np.float64).T
+    else:
+        w = qw.Weight.pack(ctx, Eb, qw.WFMT_INT8)
+        q, s = w.unpack()
+        x = dev(hb, torch.float16 if fmt == "int8" else torch.bfloat16)
+        logits = (hb.astype(np.float64) @ q.astype(np.float64).T) * s.astype(np.float64)[None, :]
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    qw.lmhead_argmax(ctx, w, x, ids)
+    torch.cuda.synchronize()
+    got = ids.cpu().numpy()
+    assert int(got[0]) == V - 1
+    assert int(got[1]) == 4100
+    for t in range(2, M):
+        srt = np.sort(logits[t])
+        if srt[-1] - srt[-2] > 1e-3:
+            assert int(got[t]) == int(np.argmax(logits[t])), t

@@ -3,8 +3,8 @@ nothing (its argmax keys live in a fixed per-device array inside the
 library), against qw_lmhead_argmax on the same packed weights: identical ids
 and winning logits, bit for bit, on two calls in a row (the second with fewer
 tokens, so stale keys of the first would show), over BF16 and INT8 weights
-and both routes (M = 128: the GEMM; M <= 32: the small-M kernels).  Called
-through the C ABI (ctypes)."""
+and both routes (M = 32, 128, 200: the weight-stationary argmax kernel;
+M = 5: the small-M kernels).  Called through the C ABI (ctypes)."""
 import numpy as np
 import pytest
 
@@ -20,7 +20,7 @@ def test_noalloc_matches_lmhead_argmax(qw, ctx, oracle, fmt):
     wf = qw.WFMT_BF16 if fmt == "bf16" else qw.WFMT_INT8
     w = qw.Weight.pack(ctx, E, wf)
     hdt = torch.bfloat16 if fmt == "bf16" else torch.float16
-    for M, seed in ((128, 1502), (5, 1503), (32, 1504)):
+    for M, seed in ((200, 1505), (128, 1502), (5, 1503), (32, 1504)):
         h = torch.from_numpy(oracle.normal((M, K), seed)).cuda().to(hdt)
         ids_a = torch.full((M,), -1, dtype=torch.int32, device="cuda")
         mx_a = torch.empty(M, device="cuda")
