@@ -1,0 +1,225 @@
+// qw_gemm_da.hip -- the prefill GEMM for BF16 weights and BF16 activations
+// at many tokens ("direct-A"):  y[m][n] = sum_k W[n][k] * x[m][k] (+ epilogue).
+//
+// Shape.  A workgroup of 4 waves computes 256 weight rows x 128 tokens; wave
+// w owns rows 64w..64w+63 for all 128 tokens (4 x 8 blocks of the 16x16x32
+// bf16 MFMA, 128 accumulators), so two workgroups share a CU and each covers
+// the other's prologue, barriers and epilogue.
+//
+// Operands.  A packed 1 KB weight unit (16 rows x one 32-deep k-step, lane
+// l = r + 16g holding row r's k 8g..8g+7) is exactly the A operand of the
+// 16x16x32 MFMA, and the four row tiles of a wave belong to it alone: the
+// weights go straight from memory into a ring of VGPRs, D k-steps ahead,
+// without LDS.  The activations are shared by the four waves: each k-step's
+// 8 token units (16 tokens x 32 k, same lane order, i.e. the B operand)
+// arrive through direct-to-LDS loads into one of NS stages, one barrier per
+// k-step publishes them, and each wave reads its B fragments one k-step
+// ahead, column by column as the previous ones retire.
+//
+// Per CU and k-step this moves 32 KB of weights (VGPRs) and 16 KB of
+// activations (LDS), and reads 64 KB of B fragments from LDS, for 256 MFMAs.
+//
+// Epilogue.  Per 16-token column the wave stages its results as FP32
+// [token][row] in a private LDS buffer (silu(gate)*up first for a GLU
+// weight: the packer interleaves gate and up tiles, so a pair of row tiles
+// becomes one output tile in registers), then reads them back as 4-row
+// pieces and stores whole 128-byte (or 64-byte) token rows, adding the
+// residual and applying the Q/gate de-interleave on the way.
+//
+// Buffers.  The weight and activation buffer descriptors start at the
+// workgroup's first row / token and end at the operands' end, so rows past
+// the end read zeros and per-lane offsets stay fixed; the k-step goes in the
+// scalar offset.
+//
+// Reference operators replaced: the cuBLAS GemmEx / SGEMM projections of the
+// batched paths (bf16_gemm.cuh:82-122, cublas_utils.cuh:48-93,
+// full_attention_cuda.cu:708-714, linear_attention_cuda.cu:589-615).
+#include "qw_stream.hpp"
+
+namespace qwk {
+
+namespace {
+
+constexpr int DA_D = 4;        // weight k-steps in flight per wave
+constexpr int DA_NS = 4;       // activation stages
+constexpr int DA_STG = 8192;   // one stage: 8 token units of 1 KB
+constexpr int DA_GROUP_M = 8;  // token blocks per raster group
+
+template <bool GLU> struct DaEpi {
+    static constexpr int ROWS = GLU ? 32 : 64;   // output rows per wave
+    static constexpr int PITCH = ROWS + 4;       // floats per staged token
+    static constexpr int BYTES = 16 * PITCH * 4; // one 16-token column
+    static constexpr int LPT = ROWS / 4;         // lanes per token when reading back
+    static constexpr int TPR = 64 / LPT;         // tokens per read
+};
+
+// One 1 KB unit global -> LDS with a scalar offset (see lds_dma16).
+__device__ __forceinline__ void lds_dma16_so(__amdgpu_buffer_rsrc_t rs, uint8_t* lds_unit, uint32_t voff, int soff) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds_unit;
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs), "s"(soff)
+                 : "memory", "m0");
+}
+
+}  // namespace
+
+template <bool GLU>
+__global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
+    using E = DaEpi<GLU>;
+    constexpr int D = DA_D, NS = DA_NS;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float* const epw = reinterpret_cast<float*>(lds + NS * DA_STG + wave * E::BYTES);
+
+    // XCD-aware order (consecutive ids go to different XCDs: give each XCD a
+    // contiguous range), then a grouped raster: DA_GROUP_M token blocks x all
+    // weight blocks per group, token block fastest
+    const int nwg = gridDim.x;
+    int b = blockIdx.x;
+    if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
+    const int per_group = DA_GROUP_M * a.nblk_n;
+    const int group = b / per_group;
+    const int first_m = group * DA_GROUP_M;
+    const int gm = min(DA_GROUP_M, a.nblk_m - first_m);
+    const int in_group = b - group * per_group;
+    const int m0 = (first_m + in_group % gm) * 128;
+    const int nt0 = (in_group / gm) * 16;
+    const int ks_n = a.ksteps;
+
+    const __amdgpu_buffer_rsrc_t wrs =
+        make_rsrc(a.w + (size_t)nt0 * ks_n * 1024, (uint32_t)((a.n_tiles - nt0) * ks_n * 1024));
+    const __amdgpu_buffer_rsrc_t xrs =
+        make_rsrc(static_cast<const uint16_t*>(a.x) + (size_t)m0 * a.ldx, (uint32_t)((a.M - m0) * a.ldx * 2));
+    uint32_t va[4], vb[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) va[i] = (uint32_t)(((wave * 4 + i) * ks_n * 64 + lane) * 16);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+        vb[q] = (uint32_t)((((wave * 2 + q) * 16 + (lane & 15)) * a.ldx + (lane >> 4) * 8) * 2);
+    // k-steps past the end reload the last one (never used)
+    auto kc = [&](int ks) { return __builtin_amdgcn_readfirstlane(min(ks, ks_n - 1)); };
+    auto dma = [&](int ks) {
+        uint8_t* st = lds + (ks % NS) * DA_STG + wave * 2048;
+        const int so = kc(ks) * 64;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) lds_dma16_so(xrs, st + q * 1024, vb[q], so);
+    };
+    u32x4 A[D][4], B[8];
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto loadA = [&](u32x4 (&dst)[4], int ks) {
+        const int so = kc(ks) * 1024;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, va[i], so, 0);
+    };
+
+    // prologue: activation stages 0..NS-2, weight k-steps 0..D-1
+#pragma unroll
+    for (int s0 = 0; s0 < NS - 1; ++s0) dma(s0);
+#pragma unroll
+    for (int d = 0; d < D; ++d) loadA(A[d], d);
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) B[j] = *reinterpret_cast<const u32x4*>(lds + j * 1024 + lane * 16);
+
+    for (int ks0 = 0; ks0 < ks_n; ks0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int ks = ks0 + u;
+            // this wave's activation loads of k-step ks+1 have landed (after
+            // them came the 4 weight loads of their k-step and 6 loads per
+            // later one), then the barrier publishes everyone's and frees
+            // the stage of ks-1 for k-step ks+NS-1
+            __builtin_amdgcn_s_waitcnt(vm_wait(4 + 6 * (NS - 3)));
+            __syncthreads();
+            dma(ks + NS - 1);
+            const uint8_t* stn = lds + ((ks + 1) % NS) * DA_STG + lane * 16;
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[u][i]),
+                                                                       __builtin_bit_cast(bf16x8, B[j]), acc[i][j],
+                                                                       0, 0, 0);
+                B[j] = *reinterpret_cast<const u32x4*>(stn + j * 1024);
+            }
+            __builtin_amdgcn_s_setprio(0);
+            loadA(A[u], ks + D);
+        }
+    }
+
+    // ---- epilogue: accumulator item e of lane l = row 4(l/16)+e of the row
+    // tile, token l%16 of the token tile
+    const int g = lane >> 4;
+    const bool has_res = (a.flags & EP_RESIDUAL) != 0;
+    const bool has_split = (a.flags & EP_SPLIT) != 0;
+    const int sp_log = a.split_period > 0 ? 31 - __builtin_clz((unsigned)a.split_period) : 0;
+    const int row_w = (GLU ? (nt0 >> 1) : nt0) * 16 + wave * E::ROWS;  // first output row of the wave
+    const int rsub = (lane % E::LPT) * 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        float* eb = epw;
+#pragma unroll
+        for (int i = 0; i < (GLU ? 2 : 4); ++i) {
+            f32x4 o;
+            if constexpr (GLU) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = silu_f(acc[2 * i][j][e]) * acc[2 * i + 1][j][e];
+            } else {
+                o = acc[i][j];
+            }
+            *reinterpret_cast<f32x4*>(eb + (lane & 15) * E::PITCH + 16 * i + 4 * g) = o;
+        }
+#pragma unroll
+        for (int c = 0; c < 16 / E::TPR; ++c) {
+            const int tok = c * E::TPR + lane / E::LPT;
+            f32x4 o = *reinterpret_cast<const f32x4*>(eb + tok * E::PITCH + rsub);
+            const int m = m0 + 16 * j + tok;
+            const int row = row_w + rsub;
+            if (m < a.M && row < a.N) {
+                if (has_res) o += load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + row);
+                void* dst = a.y;
+                int col = row;
+                if (has_split) {  // power-of-two period: shifts only
+                    dst = ((row >> sp_log) & 1) ? a.y2 : a.y;
+                    col = ((row >> (sp_log + 1)) << sp_log) + (row & (a.split_period - 1));
+                }
+                store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, o);
+            }
+        }
+    }
+}
+
+bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax) {
+    if (wf != WF_BF16 || xdt != DT_BF16 || argmax || a.splitk > 1) return false;
+    if (a.N % 4 != 0 || !a.vec_store) return false;
+    if ((a.flags & EP_SPLIT) && (a.split_period < 4 || (a.split_period & (a.split_period - 1)) != 0)) return false;
+    if ((uint64_t)a.M * a.ldx * 2 >= (1ull << 31) || (uint64_t)a.n_tiles * a.ksteps * 1024 >= (1ull << 31)) return false;
+    return a.ksteps % DA_D == 0;
+}
+
+size_t gemm_da_lds_bytes(bool glu) {
+    return (size_t)DA_NS * DA_STG + 4 * (glu ? DaEpi<true>::BYTES : DaEpi<false>::BYTES);
+}
+
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, hipStream_t stream) {
+    GemmArgs b = a;
+    b.nblk_n = (a.n_tiles * 16 + 255) / 256;
+    b.nblk_m = (a.M + 127) / 128;
+    const int grid = b.nblk_n * b.nblk_m;
+    const size_t lds = gemm_da_lds_bytes(glu);
+    auto go = [&](auto k) {
+        hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, stream, b);
+        return hipGetLastError();
+    };
+    return glu ? go(gemm_da_kernel<true>) : go(gemm_da_kernel<false>);
+}
+
+}  // namespace qwk

@@ -141,6 +141,11 @@ struct GemmArgs {
 int gemm_acc_floats_per_thread(int rows, int tile_m, int waves);
 bool gemm_supported(int wf, int xdt);
 hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax, hipStream_t stream);
+// Direct-A GEMM (qw_gemm_da.hip): BF16 x BF16, 256-row x 128-token blocks,
+// two workgroups per CU; plain, GLU, residual and split epilogues.
+bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax);
+size_t gemm_da_lds_bytes(bool glu);
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, hipStream_t stream);
 
 // Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass
 // (x -> h, y = the h buffer), `down` the down pass (h -> y).

@@ -13,16 +13,20 @@ pytestmark = pytest.mark.gpu
 torch = pytest.importorskip("torch")
 
 
-@pytest.fixture(scope="module", params=["128x4", "256x4", "256x8", "r64"])
+@pytest.fixture(scope="module", params=["128x4", "256x4", "256x8", "r64", "da"])
 def ctx(qw, request):
     """A context that takes the GEMM for every BF16 / INT8 call from 33 tokens
     on (the default routing sends small-N shapes to the chunked small-M
     kernels), with each block shape: 256 rows x 128 tokens x 4 waves, 256 x
     256 x 4, 256 x 256 x 8 (INT8 weights always run 8 waves on 256-row
-    blocks), and 64 rows x 128 tokens x 4 waves ("r64")."""
+    blocks), 64 rows x 128 tokens x 4 waves ("r64"), and the direct-A kernel
+    (qw_gemm_da.hip) on every BF16 x BF16 call it can take ("da"; INT8,
+    argmax and shapes it does not take run the 256-row GEMM)."""
     import os
     if request.param == "r64":
         env = {"QW_GEMM_MIN_M": "33", "QW_GEMM_ROWS": "64"}
+    elif request.param == "da":
+        env = {"QW_GEMM_MIN_M": "33", "QW_GEMM_ROWS": "256", "QW_GEMM_DA": "2"}
     else:
         tile, waves = request.param.split("x")
         env = {"QW_GEMM_MIN_M": "33", "QW_GEMM_TILE_M": tile, "QW_GEMM_WAVES": waves, "QW_GEMM_ROWS": "256"}
