@@ -41,8 +41,12 @@ namespace qwk {
 namespace {
 
 constexpr int DA_D = 4;        // weight k-steps in flight per wave
-constexpr int DA_NS = 4;       // activation stages
-constexpr int DA_STG = 8192;   // one stage: 8 token units of 1 KB
+constexpr int DA_NS = 4;       // activation stages (row-gather loads: one k-step each)
+constexpr int DA_STG = 8192;   // one such stage: 8 token units of 1 KB
+constexpr int DA_NS2 = 3;      // activation stages (line loads: two k-steps each)
+constexpr int DA_U2 = 1152;    // one 8-token x 64-k unit (1 KB) + 128 B: the two units of a
+                               // 16-token tile sit 128 B apart modulo 256 (no bank conflicts)
+constexpr int DA_STG2 = 16 * DA_U2;
 constexpr int DA_GROUP_M = 8;  // token blocks per raster group
 
 template <bool GLU> struct DaEpi {
@@ -64,14 +68,15 @@ __device__ __forceinline__ void lds_dma16_so(__amdgpu_buffer_rsrc_t rs, uint8_t*
 
 }  // namespace
 
-template <bool GLU>
+template <bool GLU, bool LINE>
 __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
     using E = DaEpi<GLU>;
-    constexpr int D = DA_D, NS = DA_NS;
+    constexpr int D = DA_D, NS = LINE ? DA_NS2 : DA_NS;
+    constexpr int STG = LINE ? DA_STG2 : DA_STG;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float* const epw = reinterpret_cast<float*>(lds + NS * DA_STG + wave * E::BYTES);
+    float* const epw = reinterpret_cast<float*>(lds + NS * STG + wave * E::BYTES);
 
     // XCD-aware order (consecutive ids go to different XCDs: give each XCD a
     // contiguous range), then a grouped raster: DA_GROUP_M token blocks x all
@@ -92,20 +97,11 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
         make_rsrc(a.w + (size_t)nt0 * ks_n * 1024, (uint32_t)((a.n_tiles - nt0) * ks_n * 1024));
     const __amdgpu_buffer_rsrc_t xrs =
         make_rsrc(static_cast<const uint16_t*>(a.x) + (size_t)m0 * a.ldx, (uint32_t)((a.M - m0) * a.ldx * 2));
-    uint32_t va[4], vb[2];
+    uint32_t va[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) va[i] = (uint32_t)(((wave * 4 + i) * ks_n * 64 + lane) * 16);
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-        vb[q] = (uint32_t)((((wave * 2 + q) * 16 + (lane & 15)) * a.ldx + (lane >> 4) * 8) * 2);
     // k-steps past the end reload the last one (never used)
     auto kc = [&](int ks) { return __builtin_amdgcn_readfirstlane(min(ks, ks_n - 1)); };
-    auto dma = [&](int ks) {
-        uint8_t* st = lds + (ks % NS) * DA_STG + wave * 2048;
-        const int so = kc(ks) * 64;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) lds_dma16_so(xrs, st + q * 1024, vb[q], so);
-    };
     u32x4 A[D][4], B[8];
     f32x4 acc[4][8];
 #pragma unroll
@@ -117,41 +113,110 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, va[i], so, 0);
     };
+    auto mfma_step = [&](int u, const uint8_t* stn, int noff0, int noff1) {
+        // column j's B is refilled (k-step ks+1) as soon as its MFMAs are issued
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[u][i]),
+                                                                   __builtin_bit_cast(bf16x8, B[j]), acc[i][j], 0, 0, 0);
+            B[j] = *reinterpret_cast<const u32x4*>(stn + j * (LINE ? 2 * DA_U2 : 1024) + (LINE ? noff0 : 0));
+        }
+        __builtin_amdgcn_s_setprio(0);
+        (void)noff1;
+    };
 
-    // prologue: activation stages 0..NS-2, weight k-steps 0..D-1
+    if constexpr (!LINE) {
+        // one k-step per stage: lane l = r + 16g of unit q loads token r's
+        // k 8g..8g+7 (16 rows x 64 B per load)
+        uint32_t vb[2];
 #pragma unroll
-    for (int s0 = 0; s0 < NS - 1; ++s0) dma(s0);
+        for (int q = 0; q < 2; ++q)
+            vb[q] = (uint32_t)((((wave * 2 + q) * 16 + (lane & 15)) * a.ldx + (lane >> 4) * 8) * 2);
+        auto dma = [&](int ks) {
+            uint8_t* st = lds + (ks % NS) * STG + wave * 2048;
+            const int so = kc(ks) * 64;
 #pragma unroll
-    for (int d = 0; d < D; ++d) loadA(A[d], d);
-    __builtin_amdgcn_s_waitcnt(vm_wait(0));
-    __syncthreads();
+            for (int q = 0; q < 2; ++q) lds_dma16_so(xrs, st + q * 1024, vb[q], so);
+        };
 #pragma unroll
-    for (int j = 0; j < 8; ++j) B[j] = *reinterpret_cast<const u32x4*>(lds + j * 1024 + lane * 16);
-
-    for (int ks0 = 0; ks0 < ks_n; ks0 += D) {
+        for (int s0 = 0; s0 < NS - 1; ++s0) dma(s0);
 #pragma unroll
-        for (int u = 0; u < D; ++u) {
-            const int ks = ks0 + u;
-            // this wave's activation loads of k-step ks+1 have landed (after
-            // them came the 4 weight loads of their k-step and 6 loads per
-            // later one), then the barrier publishes everyone's and frees
-            // the stage of ks-1 for k-step ks+NS-1
-            __builtin_amdgcn_s_waitcnt(vm_wait(4 + 6 * (NS - 3)));
-            __syncthreads();
-            dma(ks + NS - 1);
-            const uint8_t* stn = lds + ((ks + 1) % NS) * DA_STG + lane * 16;
-            __builtin_amdgcn_s_setprio(1);
+        for (int d = 0; d < D; ++d) loadA(A[d], d);
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        __syncthreads();
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 8; ++j) B[j] = *reinterpret_cast<const u32x4*>(lds + j * 1024 + lane * 16);
+        for (int ks0 = 0; ks0 < ks_n; ks0 += D) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, A[u][i]),
-                                                                       __builtin_bit_cast(bf16x8, B[j]), acc[i][j],
-                                                                       0, 0, 0);
-                B[j] = *reinterpret_cast<const u32x4*>(stn + j * 1024);
+            for (int u = 0; u < D; ++u) {
+                const int ks = ks0 + u;
+                // this wave's activation loads of k-step ks+1 have landed
+                // (after them came the 4 weight loads of their k-step and 6
+                // loads per later one), then the barrier publishes everyone's
+                // and frees the stage of ks-1 for k-step ks+NS-1
+                __builtin_amdgcn_s_waitcnt(vm_wait(4 + 6 * (NS - 3)));
+                __syncthreads();
+                dma(ks + NS - 1);
+                mfma_step(u, lds + ((ks + 1) % NS) * STG + lane * 16, 0, 0);
+                loadA(A[u], ks + D);
             }
-            __builtin_amdgcn_s_setprio(0);
-            loadA(A[u], ks + D);
+        }
+    } else {
+        // two k-steps (one 128-byte line of each token row) per stage: the
+        // two loads of a 16-token tile each take 8 tokens x 8 16-byte chunks,
+        // lane l taking chunk c = l/8 of token t = (l%8) ^ c, which lands at
+        // 16 l; a B fragment read (lane = token t + 16 g of k-step s) then
+        // finds chunk c = 4s + g of token t at 16 (8c + (t%8 ^ c)) of unit
+        // t/8: whole-line loads, conflict-free reads
+        uint32_t vb[4];
+        const int c_ld = lane >> 3, t_ld = (lane & 7) ^ c_ld;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int unit = wave * 4 + q;  // = 2 * token tile + half
+            vb[q] = (uint32_t)(((unit * 8 + t_ld) * a.ldx + c_ld * 8) * 2);
+        }
+        auto dma = [&](int p) {  // k-steps 2p, 2p+1
+            uint8_t* st = lds + (p % NS) * STG + wave * 4 * DA_U2;
+            const int so = __builtin_amdgcn_readfirstlane(min(p, (ks_n >> 1) - 1)) * 128;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) lds_dma16_so(xrs, st + q * DA_U2, vb[q], so);
+        };
+        const int t_rd = lane & 15, g_rd = lane >> 4;
+        auto roff = [&](int s) {  // read offset of k-step parity s within a tile's pair of units
+            const int c = 4 * s + g_rd;
+            return (t_rd >> 3) * DA_U2 + 16 * (8 * c + ((t_rd & 7) ^ c));
+        };
+        const int ro0 = roff(0), ro1 = roff(1);
+#pragma unroll
+        for (int s0 = 0; s0 < NS; ++s0) dma(s0);
+#pragma unroll
+        for (int d = 0; d < D; ++d) loadA(A[d], d);
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 8; ++j) B[j] = *reinterpret_cast<const u32x4*>(lds + j * 2 * DA_U2 + ro0);
+        for (int ks0 = 0; ks0 < ks_n; ks0 += D) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const int ks = ks0 + u;
+                const int p = ks >> 1;
+                if (u & 1) {
+                    // second k-step of pair p: our loads of pair p+1 have
+                    // landed (after them: 4 weight loads, 12 loads per later
+                    // pair, 4 of this pair's first k-step), publish; pair p's
+                    // stage is free for pair p+NS
+                    __builtin_amdgcn_s_waitcnt(vm_wait(8 + 12 * (NS - 2)));
+                    __syncthreads();
+                    dma(p + NS);
+                    mfma_step(u, lds + ((p + 1) % NS) * STG, ro0, 0);
+                } else {
+                    mfma_step(u, lds + (p % NS) * STG, ro1, 0);
+                }
+                loadA(A[u], ks + D);
+            }
         }
     }
 
@@ -198,6 +263,7 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
 }
 
 bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax) {
+    if (a.ldx % 8 != 0) return false;  // 16-byte activation chunks
     if (wf != WF_BF16 || xdt != DT_BF16 || argmax || a.splitk > 1) return false;
     if (a.N % 4 != 0 || !a.vec_store) return false;
     if ((a.flags & EP_SPLIT) && (a.split_period < 4 || (a.split_period & (a.split_period - 1)) != 0)) return false;
@@ -205,21 +271,29 @@ bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax) {
     return a.ksteps % DA_D == 0;
 }
 
-size_t gemm_da_lds_bytes(bool glu) {
-    return (size_t)DA_NS * DA_STG + 4 * (glu ? DaEpi<true>::BYTES : DaEpi<false>::BYTES);
+size_t gemm_da_lds_bytes(bool glu, bool line) {
+    return (size_t)(line ? DA_NS2 * DA_STG2 : DA_NS * DA_STG) + 4 * (glu ? DaEpi<true>::BYTES : DaEpi<false>::BYTES);
 }
 
-hipError_t launch_gemm_da(const GemmArgs& a, bool glu, hipStream_t stream) {
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream) {
     GemmArgs b = a;
     b.nblk_n = (a.n_tiles * 16 + 255) / 256;
     b.nblk_m = (a.M + 127) / 128;
     const int grid = b.nblk_n * b.nblk_m;
-    const size_t lds = gemm_da_lds_bytes(glu);
+    const size_t lds = gemm_da_lds_bytes(glu, line);
     auto go = [&](auto k) {
+        static bool configured = false;  // one attribute call per instantiation
+        if (!configured) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            configured = true;
+        }
         hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, stream, b);
         return hipGetLastError();
     };
-    return glu ? go(gemm_da_kernel<true>) : go(gemm_da_kernel<false>);
+    if (line) return glu ? go(gemm_da_kernel<true, true>) : go(gemm_da_kernel<false, true>);
+    return glu ? go(gemm_da_kernel<true, false>) : go(gemm_da_kernel<false, false>);
 }
 
 }  // namespace qwk

@@ -144,8 +144,10 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax
 // Direct-A GEMM (qw_gemm_da.hip): BF16 x BF16, 256-row x 128-token blocks,
 // two workgroups per CU; plain, GLU, residual and split epilogues.
 bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax);
-size_t gemm_da_lds_bytes(bool glu);
-hipError_t launch_gemm_da(const GemmArgs& a, bool glu, hipStream_t stream);
+size_t gemm_da_lds_bytes(bool glu, bool line);
+// line: activation loads of whole 128-byte row lines (two k-steps, swizzled
+// into LDS) instead of 64-byte row pieces
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream);
 
 // Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass
 // (x -> h, y = the h buffer), `down` the down pass (h -> y).

@@ -123,8 +123,79 @@ hipError_t launch_rmsnorm(const void* x, int xdt, const void* add, void* sum_out
     return hipGetLastError();
 }
 
+// 16-bit rows with K % 8 == 0: one wave per row, 16-byte loads and stores,
+// the row in registers (up to 8 chunks of 512), the sum of squares reduced
+// within the wave (fixed order).  Four rows per workgroup.
+template <int XDT, int YDT>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(const uint16_t* x, int ldx, const float* gamma, float eps,
+                                                          uint16_t* y, int ldy, int M, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const uint16_t* xr = x + (int64_t)row * ldx;
+    uint16_t* yr = y + (int64_t)row * ldy;
+    u32x4 v[8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int k = c * 512 + lane * 8;
+        v[c] = u32x4{0u, 0u, 0u, 0u};
+        if (k < K) v[c] = *reinterpret_cast<const u32x4*>(xr + k);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t h = (v[c][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            const float f = XDT == DT_BF16 ? bf16_bits_to_f32(h) : f16_bits_to_f32(h);
+            ss += f * f;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int k = c * 512 + lane * 8;
+        if (k >= K) continue;
+        f32x4 g0 = {0.f, 0.f, 0.f, 0.f}, g1 = {0.f, 0.f, 0.f, 0.f};
+        if (gamma) {
+            g0 = *reinterpret_cast<const f32x4*>(gamma + k);
+            g1 = *reinterpret_cast<const f32x4*>(gamma + k + 4);
+        }
+        u32x4 o;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int e = 2 * e2 + h2;
+                const uint32_t hb = (v[c][e2] >> (16 * h2)) & 0xffffu;
+                const float f = XDT == DT_BF16 ? bf16_bits_to_f32(hb) : f16_bits_to_f32(hb);
+                const float r = f * inv * (1.0f + (e < 4 ? g0[e & 3] : g1[e & 3]));
+                w |= (YDT == DT_BF16 ? f32_to_bf16_bits(r) : f32_to_f16_bits(r)) << (16 * h2);
+            }
+            o[e2] = w;
+        }
+        *reinterpret_cast<u32x4*>(yr + k) = o;
+    }
+}
+
 hipError_t launch_rmsnorm_ld(const void* x, int xdt, int ldx, const float* gamma, float eps, void* y, int ydt,
                              int ldy, int M, int K, hipStream_t stream) {
+    const bool h16 = (xdt == DT_BF16 || xdt == DT_F16) && (ydt == DT_BF16 || ydt == DT_F16);
+    if (h16 && K % 8 == 0 && K <= 4096 && ldx % 8 == 0 && ldy % 8 == 0 && ((uintptr_t)x & 15) == 0 &&
+        ((uintptr_t)y & 15) == 0 && ((uintptr_t)gamma & 15) == 0) {
+        const dim3 grid((M + 3) / 4);
+        auto go = [&](auto k) {
+            hipLaunchKernelGGL(k, grid, dim3(256), 0, stream, static_cast<const uint16_t*>(x), ldx, gamma, eps,
+                               static_cast<uint16_t*>(y), ldy, M, K);
+        };
+        if (xdt == DT_BF16) {
+            if (ydt == DT_BF16) go(rmsnorm_vec_kernel<DT_BF16, DT_BF16>);
+            else go(rmsnorm_vec_kernel<DT_BF16, DT_F16>);
+        } else {
+            if (ydt == DT_BF16) go(rmsnorm_vec_kernel<DT_F16, DT_BF16>);
+            else go(rmsnorm_vec_kernel<DT_F16, DT_F16>);
+        }
+        return hipGetLastError();
+    }
     if (K > NORM_MAX_PER_THREAD * 256) return hipErrorInvalidValue;
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(M), dim3(256), 0, stream, x, xdt, nullptr, nullptr, gamma, eps, y, ydt,
                        K, ldx, ldy);
