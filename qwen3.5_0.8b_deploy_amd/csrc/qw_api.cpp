@@ -39,6 +39,7 @@ struct qw_ctx {
     int gemm_da = 1;             // direct-A GEMM for BF16 x BF16 256-row blocks (QW_GEMM_DA: 0 off,
                                  // 1 where its blocks fill the chip, 2 wherever it applies)
     bool gemm_da_line = true;    // its activation loads as whole row lines (QW_GEMM_DA_LINE=0: row pieces)
+    int gemm_da_group = 0;       // its token blocks per raster group (QW_GEMM_DA_GROUP; 0: 8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     int gemm_splitk = 0;         // K splits per GEMM tile (QW_GEMM_SPLITK; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
@@ -197,6 +198,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_DA")) c->gemm_da = std::max(0, std::min(2, atoi(v)));
     if (const char* v = getenv("QW_GEMM_DA_LINE")) c->gemm_da_line = atoi(v) != 0;
+    if (const char* v = getenv("QW_GEMM_DA_GROUP")) c->gemm_da_group = std::max(0, atoi(v));
     if (const char* v = getenv("QW_GEMM_SPLITK")) c->gemm_splitk = std::max(0, std::min(8, atoi(v)));
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
@@ -850,6 +852,7 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, int rows, const void*
     if (ctx->gemm_da && rows == 256 && !ctx->gemm_tile_m &&
         (ctx->gemm_da == 2 || (W->phys_tiles * 16 + 255) / 256 * ((M + 127) / 128) >= ctx->num_cus) &&
         qwk::gemm_da_fits(a, W->wf, (int)xdt, ids != nullptr)) {
+        a.group_m = ctx->gemm_da_group;
         hipError_t e = qwk::launch_gemm_da(a, W->glu != 0, ctx->gemm_da_line, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
         return QW_OK;

@@ -84,10 +84,11 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
     const int nwg = gridDim.x;
     int b = blockIdx.x;
     if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
-    const int per_group = DA_GROUP_M * a.nblk_n;
+    const int GM = a.group_m > 0 ? a.group_m : DA_GROUP_M;
+    const int per_group = GM * a.nblk_n;
     const int group = b / per_group;
-    const int first_m = group * DA_GROUP_M;
-    const int gm = min(DA_GROUP_M, a.nblk_m - first_m);
+    const int first_m = group * GM;
+    const int gm = min(GM, a.nblk_m - first_m);
     const int in_group = b - group * per_group;
     const int m0 = (first_m + in_group % gm) * 128;
     const int nt0 = (in_group / gm) * 16;

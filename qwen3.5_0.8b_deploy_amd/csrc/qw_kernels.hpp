@@ -137,6 +137,7 @@ struct GemmArgs {
     int splitk;              // K splits per tile (1: none; not with argmax)
     float* partials;         // split-K partial tiles [tiles][splitk][threads][acc floats]
     unsigned* counters;      // split-K arrival counters per tile (self-resetting)
+    int group_m;             // direct-A kernel: token blocks per raster group (0: 8)
 };
 int gemm_acc_floats_per_thread(int rows, int tile_m, int waves);
 bool gemm_supported(int wf, int xdt);
