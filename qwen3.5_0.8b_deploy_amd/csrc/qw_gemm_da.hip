@@ -44,8 +44,7 @@ constexpr int DA_D = 4;        // weight k-steps in flight per wave
 constexpr int DA_NS = 4;       // activation stages (row-gather loads: one k-step each)
 constexpr int DA_STG = 8192;   // one such stage: 8 token units of 1 KB
 constexpr int DA_NS2 = 3;      // activation stages (line loads: two k-steps each)
-constexpr int DA_U2 = 1152;    // one 8-token x 64-k unit (1 KB) + 128 B: the two units of a
-                               // 16-token tile sit 128 B apart modulo 256 (no bank conflicts)
+constexpr int DA_U2 = 1024;    // one 8-token x 64-k unit
 constexpr int DA_STG2 = 16 * DA_U2;
 constexpr int DA_GROUP_M = 8;  // token blocks per raster group
 
@@ -167,16 +166,18 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
         }
     } else {
         // two k-steps (one 128-byte line of each token row) per stage: the
-        // two loads of a 16-token tile each take 8 tokens x 8 16-byte chunks,
-        // lane l taking chunk c = l/8 of token t = (l%8) ^ c, which lands at
-        // 16 l; a B fragment read (lane = token t + 16 g of k-step s) then
-        // finds chunk c = 4s + g of token t at 16 (8c + (t%8 ^ c)) of unit
-        // t/8: whole-line loads, conflict-free reads
+        // two loads (h = 0, 1) of a 16-token tile each take 8 tokens x 8
+        // 16-byte chunks; chunk c of token t lands in slot (8c + (t ^ c)) ^ 8h
+        // of its unit (lane l of the load takes the chunk of slot l).  A B
+        // fragment read (lane = token t + 16 g of k-step s, chunk c = 4s + g)
+        // then hits 16 different 16-byte bank groups per 16 lanes: whole-line
+        // loads, conflict-free reads
         uint32_t vb[4];
-        const int c_ld = lane >> 3, t_ld = (lane & 7) ^ c_ld;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int unit = wave * 4 + q;  // = 2 * token tile + half
+            const int unit = wave * 4 + q;  // = 2 * token tile + h
+            const int sl = lane ^ (8 * (unit & 1));
+            const int c_ld = sl >> 3, t_ld = (sl & 7) ^ c_ld;
             vb[q] = (uint32_t)(((unit * 8 + t_ld) * a.ldx + c_ld * 8) * 2);
         }
         auto dma = [&](int p) {  // k-steps 2p, 2p+1
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
         const int t_rd = lane & 15, g_rd = lane >> 4;
         auto roff = [&](int s) {  // read offset of k-step parity s within a tile's pair of units
             const int c = 4 * s + g_rd;
-            return (t_rd >> 3) * DA_U2 + 16 * (8 * c + ((t_rd & 7) ^ c));
+            return (t_rd >> 3) * DA_U2 + 16 * ((8 * c + ((t_rd & 7) ^ c)) ^ (8 * (t_rd >> 3)));
         };
         const int ro0 = roff(0), ro1 = roff(1);
 #pragma unroll
