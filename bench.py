@@ -323,14 +323,16 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
             w.fold_norm(gam[l])
             gu_f.append(w)
             del g_, u_
+    # qw_mlp_stack: one persistent launch for all 24 blocks up to 8 tokens,
+    # the 24 qw_mlp_fused launches beyond
     for M in ((8, 32, 128) if want("cfg2") else ()):
         hb = randn(M, H)
-        g = graphed(qw, ctx, stream, lambda hb=hb: [qw.mlp_fused(ctx, gu_f[l], dn[l], hb, hb, residual=hb)
-                                                   for l in range(LAYERS)])
+        g = graphed(qw, ctx, stream, lambda hb=hb: qw.mlp_stack(ctx, gu_f, dn, hb, hb, stream=stream))
         ms = timer.run(g.launch, steps, 2)
         b = LAYERS * mlp_bytes(M)
         fl = LAYERS * 2.0 * M * 3 * H * I
         extra[f"cfg2_mlp_bf16_M{M}"] = {"us_per_layer": round(ms * 1e3 / LAYERS, 2), "norm": "gamma folded into gate/up",
+                                        "path": "persistent stack" if M <= 8 else "per-block launches",
                                         "GBps": round(b / ms / 1e6, 1),
                                         "TFLOPs": round(fl / ms / 1e9, 2),
                                         "tok_per_s_stack": round(M / (ms * 1e-3), 1)}

@@ -192,7 +192,7 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
  * (cuda_engine.cu:119-124) over consecutive layers, i.e. L calls of
  * qw_mlp_fused(x, gamma[l], residual = x, y), equal to them within FP32
  * summation order.  gamma NULL (or all entries NULL): every gateup weight
- * carries its norm weight (qw_weight_fold_norm).  At decode (M <= 2, BF16
+ * carries its norm weight (qw_weight_fold_norm).  At decode (M <= 8, BF16
  * weights with BF16 x or INT8 weights with F16 x, the Qwen3.5-0.8B shape
  * H = 1024, I = 3584, a device with >= 256 CUs, L <= 48) all blocks run in
  * ONE persistent launch that streams block l+1's weights while block l's

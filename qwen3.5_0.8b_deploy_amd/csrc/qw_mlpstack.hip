@@ -1,5 +1,5 @@
 // qw_mlpstack.hip -- L consecutive decoder MLP blocks in one persistent launch
-// (decode, M <= 2 tokens, Qwen3.5-0.8B shape H = 1024, I = 3584):
+// (decode, M <= 8 tokens, Qwen3.5-0.8B shape H = 1024, I = 3584):
 //     for l < L:  x = x + down_l( silu(gate_l . n_l(x)) * (up_l . n_l(x)) ),
 //                 n_l(x) = RMSNorm(x) * (1 + gamma_l),  x rounded to its dtype
 // -- the result of L calls of qw_mlp_fused(y = residual = x), with the
@@ -61,7 +61,7 @@ namespace qwk {
 
 constexpr int MS_NW = 16;          // waves per workgroup: 8 gate/up + 8 down
 constexpr int MS_RW = 8;           // waves per role
-constexpr int MS_MAXM = 4;         // tokens
+constexpr int MS_MAXM = 8;         // tokens (the MFMA's 16 token lanes, register budget 8)
 constexpr int MS_H = 1024, MS_I = 3584;
 constexpr int MS_GRID = 256;       // workgroups: one per CU
 constexpr int MS_DT = MS_H / 16;   // down tiles (64), on workgroups [MS_D0, MS_GRID)
@@ -74,7 +74,7 @@ constexpr int MS_DROW = MS_DSPAN + 8;    // LDS row of a down wave's h slice (16
 constexpr size_t MS_HWORDS = (size_t)2 * MS_MAXM * (MS_I / 2);   // h words: [parity][token][I/2]
 constexpr size_t MS_XWORDS = (size_t)2 * MS_MAXM * (MS_H / 2);   // x words: [parity][token][H/2]
 size_t mlp_stack_ws_bytes() { return (MS_HWORDS + MS_XWORDS) * 8; }
-int mlp_stack_max_m() { return 2; }  // register budget: two tokens per lane slice
+int mlp_stack_max_m() { return MS_MAXM; }
 int mlp_stack_grid() { return MS_GRID; }
 
 struct MsLds {
@@ -298,6 +298,13 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
                 unsigned it = 0;
                 uint64_t v[MT];
+                if constexpr (MT > 1) {  // token 0's word first (see the h pollers)
+                    for (;;) {
+                        const bool ok = (uint32_t)(ms_load(X) >> 32) == tg;
+                        if (__all(ok) || dead) break;
+                        if (!ms_pause(ab, t0, it, dead)) break;
+                    }
+                }
                 for (;;) {
                     bool ok = true;
 #pragma unroll
@@ -399,13 +406,36 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         // [448 w, 448 w + 448)) and deposits it in LDS; a poller issues no
         // weight loads, so its polls never wait behind a weight stream
         const int w = wave;
-        const uint64_t* hw0 = hbuf + (size_t)(MS_DSPAN / 2) * w;
+        // the words through a buffer descriptor: one per-lane offset, the
+        // token and parity in the scalar offset (device-coherent loads, as
+        // the agent-scope atomic loads elsewhere)
+        const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)(MS_HWORDS * 8));
+        const uint32_t vb = (uint32_t)(((MS_DSPAN / 2) * w + lane) * 8);
         for (int l = 0; l < a.L; ++l) {
             const uint32_t tg = ms_tag(epoch, l);
-            const uint64_t* hl = hw0 + (size_t)(l & 1) * MS_MAXM * (MS_I / 2);
+            const int so = (l & 1) * MS_MAXM * (MS_I / 2) * 8;
             const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
             unsigned it = 0;
-            uint64_t v[MT][NH];
+            uint32_t v[MT][NH];  // payloads (the tags are checked as the words arrive)
+            if constexpr (MT > 1) {
+                // first token 0's words only: a producer stores all tokens'
+                // words of its rows with one instruction, so once these
+                // arrived the rest follow; polling them all costs every
+                // other access MT times the poll traffic
+                for (;;) {
+                    bool ok = true;
+#pragma unroll
+                    for (int i = 0; i < NH; ++i) {
+                        const int e = lane + 64 * i;
+                        if (e < HWD) {
+                            const u32x2 wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so, AUX_SC1);
+                            ok = ok && wv[1] == tg;
+                        }
+                    }
+                    if (__all(ok) || dead) break;
+                    if (!ms_pause(ab, t0, it, dead)) break;
+                }
+            }
             for (;;) {
                 bool ok = true;
 #pragma unroll
@@ -413,8 +443,11 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
                     for (int i = 0; i < NH; ++i) {
                         const int e = lane + 64 * i;
-                        v[m][i] = (m < M && e < HWD) ? ms_load(hl + (size_t)m * (MS_I / 2) + e) : ((uint64_t)tg << 32);
-                        ok = ok && (uint32_t)(v[m][i] >> 32) == tg;
+                        u32x2 wv = u32x2{0u, tg};
+                        if (m < M && e < HWD)
+                            wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8, AUX_SC1);
+                        ok = ok && wv[1] == tg;
+                        v[m][i] = wv[0];
                     }
                 if (__all(ok) || dead) break;
                 if (!ms_pause(ab, t0, it, dead)) break;
@@ -427,7 +460,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
 #pragma unroll
                 for (int i = 0; i < NH; ++i) {
                     const int e = lane + 64 * i;
-                    if (m < M && e < HWD) *reinterpret_cast<uint32_t*>(&S.bd[w][m][2 * e]) = (uint32_t)v[m][i];
+                    if (m < M && e < HWD) *reinterpret_cast<uint32_t*>(&S.bd[w][m][2 * e]) = v[m][i];
                 }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_wave_barrier();
@@ -502,8 +535,10 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
 
 template <typename Kern>
 static hipError_t launch_ms(Kern k, const MlpStackArgs& a, hipStream_t st) {
-    constexpr size_t lds = 96 * 1024;  // more than half the CU's LDS: one workgroup per CU
-    static_assert(sizeof(MsLds) <= lds, "LDS layout");
+    // more than half the CU's LDS: one workgroup per CU
+    constexpr size_t lds = ((sizeof(MsLds) + 1023) / 1024 * 1024) > 96 * 1024 ? (sizeof(MsLds) + 1023) / 1024 * 1024
+                                                                                : 96 * 1024;
+    static_assert(lds <= 160 * 1024, "LDS layout");
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -518,7 +553,9 @@ static hipError_t launch_ms(Kern k, const MlpStackArgs& a, hipStream_t st) {
 template <int WF, int XDT, bool GAM>
 static hipError_t launch_ms2(const MlpStackArgs& a, hipStream_t st) {
     if (a.M == 1) return launch_ms(mlp_stack_kernel<WF, XDT, GAM, 1>, a, st);
-    return launch_ms(mlp_stack_kernel<WF, XDT, GAM, 2>, a, st);
+    if (a.M == 2) return launch_ms(mlp_stack_kernel<WF, XDT, GAM, 2>, a, st);
+    if (a.M <= 4) return launch_ms(mlp_stack_kernel<WF, XDT, GAM, 4>, a, st);
+    return launch_ms(mlp_stack_kernel<WF, XDT, GAM, 8>, a, st);
 }
 
 template <int WF, int XDT>

@@ -48,7 +48,7 @@ def _ref_bf16(oracle, layers, x):
     return x
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
 @pytest.mark.parametrize("L", [1, 5])
 def test_mlp_stack_bf16(qw, ctx, oracle, relerr, M, L):
     layers = _layers(oracle, L, 2100 + L)
@@ -65,7 +65,13 @@ def test_mlp_stack_bf16(qw, ctx, oracle, relerr, M, L):
     torch.cuda.synchronize()
     assert ctx.device_error() == 0
     ref = _ref_bf16(oracle, layers, host(x0))
-    assert relerr(host(y), ref) <= 1e-2
+    # BF16 hidden state rounded after every block: against FP64 both the stack
+    # and the per-block launches drift toward the 1e-2 bar over 5 blocks
+    # (measured up to 1.4e-2 for both, identical); the stack is held to the
+    # per-block launches' error plus one rounding step
+    e_stack, e_blocks = relerr(host(y), ref), relerr(host(z), ref)
+    print("first launch rel err: stack", e_stack, "per-block", e_blocks)
+    assert e_stack <= max(1e-2, 1.34 * e_blocks + 2e-3)
     # same math as the per-block launches; the K slices of the gate/up
     # reduction are summed in another grouping, which moves a BF16 rounding of
     # the hidden state now and then
@@ -73,10 +79,20 @@ def test_mlp_stack_bf16(qw, ctx, oracle, relerr, M, L):
     # a second launch on other inputs (new epoch tags), in place
     x1 = dev(oracle.normal((M, H), 2299 + M), torch.bfloat16)
     r1 = _ref_bf16(oracle, layers, host(x1))
+    z1 = x1.clone()
     qw.mlp_stack(ctx, gu, dn, x1, x1, gammas=gms)
+    for l in range(L):
+        qw.mlp_fused(ctx, gu[l], dn[l], z1, z1, gamma=gms[l], residual=z1)
     torch.cuda.synchronize()
     assert ctx.device_error() == 0
-    assert relerr(host(x1), r1) <= 1e-2
+    # the BF16 hidden state is rounded after every block, so over 5 blocks the
+    # stack and the per-block launches each sit near the 1e-2 BF16 bar against
+    # FP64; the stack may not be worse than the per-block launches by more
+    # than one BF16 rounding step
+    e_stack, e_blocks = relerr(host(x1), r1), relerr(host(z1), r1)
+    print("second launch rel err: stack", e_stack, "per-block", e_blocks)
+    assert e_stack <= max(1e-2, 1.34 * e_blocks + 2e-3)
+    assert relerr(host(x1), host(z1).astype(np.float64)) <= 1e-2
 
 
 def test_mlp_stack_bf16_folded_norm_24_layers(qw, ctx, oracle, relerr):
@@ -112,7 +128,7 @@ def test_mlp_stack_bf16_folded_norm_24_layers(qw, ctx, oracle, relerr):
     assert e_stack <= 3e-2 and e_stack <= 1.34 * e_blocks + 2e-3
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 8])
 def test_mlp_stack_int8(qw, ctx, oracle, relerr, M):
     """INT8 weights (per-row scales), F16 x; the reference composition is the
     dequant-then-matmul of the same q and s (in FP64) with the kernel's F16
@@ -184,8 +200,8 @@ def test_mlp_stack_graph_replays(qw, ctx, oracle, relerr):
 
 
 def test_mlp_stack_fallback_more_tokens(qw, ctx, oracle, relerr):
-    """M = 5 takes the per-block launches: identical to qw_mlp_fused calls."""
-    L, M = 2, 5
+    """M = 9 takes the per-block launches: identical to qw_mlp_fused calls."""
+    L, M = 2, 9
     layers = _layers(oracle, L, 2900)
     gu = [qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16) for G, U, _, _ in layers]
     dn = [qw.Weight.pack(ctx, D, qw.WFMT_BF16) for _, _, D, _ in layers]
