@@ -535,8 +535,7 @@ static hipError_t launch_ch(Kern k, const ChainArgs& a, hipStream_t st) {
     static_assert(sizeof(ChLds) <= 160 * 1024, "LDS layout");
     static bool configured = false;
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)lds);
+        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
         if (e != hipSuccess) return e;
         configured = true;
     }

@@ -499,8 +499,7 @@ template <typename Kern>
 static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, int threads, size_t lds, hipStream_t st) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
         if (e != hipSuccess) return e;
         configured = true;
     }

@@ -286,8 +286,7 @@ hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t st
     auto go = [&](auto k) {
         static bool configured = false;  // one attribute call per instantiation
         if (!configured) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
             if (e != hipSuccess) return e;
             configured = true;
         }

@@ -6,6 +6,18 @@
 
 namespace qwk {
 
+// Maximum dynamic LDS of a kernel.  The attribute is not a stream operation,
+// so it is set in the relaxed capture mode: a first launch of a kernel inside
+// a thread's stream capture (qw_graph_begin) must not invalidate the capture.
+inline hipError_t set_max_lds(const void* kernel, int bytes) {
+    hipStreamCaptureMode m = hipStreamCaptureModeRelaxed;
+    const hipError_t e0 = hipThreadExchangeStreamCaptureMode(&m);
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e0 == hipSuccess) (void)hipThreadExchangeStreamCaptureMode(&m);
+    return e;
+}
+
+
 // One skinny (small-M) projection launch.  See qw_skinny.hip.
 struct SkinnyArgs {
     const uint8_t* w;        // packed weight (tile order)

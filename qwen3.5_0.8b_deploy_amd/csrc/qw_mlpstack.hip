@@ -541,8 +541,7 @@ static hipError_t launch_ms(Kern k, const MlpStackArgs& a, hipStream_t st) {
     static_assert(lds <= 160 * 1024, "LDS layout");
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)lds);
+        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
         if (e != hipSuccess) return e;
         configured = true;
     }

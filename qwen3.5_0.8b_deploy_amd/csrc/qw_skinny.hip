@@ -395,8 +395,7 @@ template <typename Kern>
 static hipError_t launch_k(Kern k, const SkinnyArgs& a, int nw, int grid, size_t smem, hipStream_t st) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSkinnyMaxLds);
+        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)kSkinnyMaxLds);
         if (e != hipSuccess) return e;
         configured = true;
     }

@@ -744,8 +744,7 @@ template <typename Kern>
 hipError_t launch_w(Kern k, const WideArgs& a, int nw, int grid, size_t smem, hipStream_t st) {
     static bool configured = false;  // one attribute call per instantiation
     if (!configured) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideMaxLds);
+        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)kWideMaxLds);
         if (e != hipSuccess) return e;
         configured = true;
     }
@@ -882,8 +881,7 @@ hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid
     auto go = [&](auto kern) {
         static bool configured = false;
         (void)configured;
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kWideMaxLds);
+        hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), (int)kWideMaxLds);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kArgNW * 64), smem, stream, a);
         return hipGetLastError();
