@@ -213,6 +213,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_WIDE_NORM_SEP")) c->wide_norm_sep = atoi(v) != 0;
     if (const char* v = getenv("QW_WIDE_DBG")) c->wide_dbg = atoi(v);
     if (const char* v = getenv("QW_WIDE_CFG")) c->wide_cfg = std::max(0, std::min(3, atoi(v)));
+    if (const char* v = getenv("QW_WIDE_T")) c->wide_cfg |= std::max(0, std::min(8, atoi(v))) << 4;  // token groups
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
         c->gemm_min_m = std::max(1, atoi(v));
         c->gemm_forced = true;

@@ -791,6 +791,8 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
     const bool res = (s.flags & EP_RESIDUAL) && s.vec_store;
     const int rs = s.res_dt == DT_F32 ? 4 : 2;
     static const int cfgs[3][2] = {{4, 1}, {2, 2}, {1, 4}};
+    const int force_t = force_cfg >> 4;  // token groups (measurement)
+    force_cfg &= 15;
     bool found = false;
     // preference: enough workgroups to stream from most CUs, then no K split
     // (no hand-off), then the most workgroups within one per CU, then fewer
@@ -805,6 +807,7 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
         return T < p.T;
     };
     for (int T = 1; T <= 8; T *= 2) {
+        if (force_t && T != force_t) continue;
         const int Mg = (s.M + T - 1) / T;
         if (T > 1 && Mg < 16) break;
         if (Mg > 8 * 16) continue;  // at most 8 token tiles per group (16 would spill registers)
@@ -832,7 +835,7 @@ bool wide_plan(const SkinnyArgs& s, int wf, bool glu, int num_cus, size_t partia
                 if (S > 1 && (size_t)ngrp * T * S * NB * CT * 64 * (2 * 16 + 4) > partials_cap) continue;
                 if (S > 1 && ngrp * T > max_counters) continue;
                 const int grid = ngrp * T * S;
-                if (grid > num_cus && !(force_s || force_cfg)) continue;
+                if (grid > num_cus && !(force_s || force_cfg || force_t)) continue;
                 if (better(S, grid, T)) {
                     found = true;
                     p.S = S;
