@@ -1222,10 +1222,24 @@ qw_status qw_attn_forward(qw_ctx* ctx, const qw_attn_params* p, const qw_kv_cach
         }
         return QW_OK;
     }
-    // few tokens per sequence: key-split rows; keys per split about two
-    // workgroups per CU, 128 .. 1024 keys each
-    const int64_t want = (int64_t)len * rows_all * nkv / (2LL * ctx->num_cus);
-    int split = (int)std::min<int64_t>(1024, std::max<int64_t>(128, want)) / 64 * 64;
+    // few tokens per sequence: key-split rows.  Keys per split (a multiple
+    // of 64 in 128..1024) minimize the busiest CU's work: the workgroups
+    // spread round-robin over the CUs, so a CU gets ceil(W / CUs) of them,
+    // each costing its keys plus ~64 keys' worth of fixed work (q, partials).
+    // B=1 at context 32769: 320 keys (206 workgroups) 30 us against 34 us
+    // for 128 keys (514 workgroups: a second round for two of them).
+    int split = 128;
+    {
+        int64_t best = -1;
+        for (int sp = 128; sp <= 1024; sp += 64) {
+            const int64_t w = (int64_t)rows_all * nkv * ((len + sp - 1) / sp);
+            const int64_t cost = (w + ctx->num_cus - 1) / ctx->num_cus * (sp + 64);
+            if (best < 0 || cost < best) {
+                best = cost;
+                split = sp;
+            }
+        }
+    }
     if (ctx->attn_split > 0) split = ctx->attn_split;  // forced (QW_ATTN_SPLIT, multiple of 64)
     const int nsplit = (len + split - 1) / split;
     const size_t per_row = qwk::attn_bytes_per_row(nh, hd, nsplit);

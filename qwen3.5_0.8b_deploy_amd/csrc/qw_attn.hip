@@ -356,9 +356,14 @@ __device__ __forceinline__ void gate_store(const AttnArgs& a, int r, int h, int 
     }
 }
 
-template <int HD, int NW>
+// DC > 1 (many splits): blockIdx.z takes HD/DC of the head's dims, so more
+// workgroups share the split partials' reads (each recomputes M and l from
+// the splits' two floats).
+template <int HD, int NW, int DC = 1>
 __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
-    constexpr int E = HD / 64;
+    static_assert(DC == 1 || NW > 1, "dim chunks with the multi-wave merge");
+    constexpr int E = HD / 64 / DC;  // dims per lane
+    const int d0 = (int)blockIdx.z * (HD / DC);
     const int rl = blockIdx.x, h = blockIdx.y, r = a.row0 + rl;
     const int b = r / a.T, t = r % a.T;
     const int P = a.pos[b] + t;
@@ -367,7 +372,7 @@ __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
     const int ns = (L + a.split - 1) / a.split;
     const float* pp = a.part + ((int64_t)rl * a.nh + h) * a.nsplit * (HD + 2);
     __shared__ float red[2][NW];
-    __shared__ __attribute__((aligned(16))) float osum[NW][HD];
+    __shared__ __attribute__((aligned(16))) float osum[NW][HD / DC];
     if constexpr (NW == 1) {
         float o[E], l;
         merge_splits_wave<HD, false>(pp, ns, lane, o, l);
@@ -398,7 +403,7 @@ __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
         for (int u = 0; u < 8; ++u) {
             w[u] = pp[(s + NW * u) * (HD + 2) + HD];
 #pragma unroll
-            for (int e = 0; e < E; ++e) v[u][e] = pp[(s + NW * u) * (HD + 2) + lane * E + e];
+            for (int e = 0; e < E; ++e) v[u][e] = pp[(s + NW * u) * (HD + 2) + d0 + lane * E + e];
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -410,7 +415,7 @@ __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
     for (; s < ns; s += NW) {
         const float wu = __expf(pp[s * (HD + 2) + HD] - M);
 #pragma unroll
-        for (int e = 0; e < E; ++e) o[e] += wu * pp[s * (HD + 2) + lane * E + e];
+        for (int e = 0; e < E; ++e) o[e] += wu * pp[s * (HD + 2) + d0 + lane * E + e];
     }
     if (NW > 1) {
 #pragma unroll
@@ -429,8 +434,8 @@ __global__ __launch_bounds__(64 * NW) void attn_combine(AttnArgs a) {
         }
     }
     const float inv = L > 0 ? 1.0f / l : 0.0f;
-    const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + lane * E;
-    const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + lane * E;
+    const int64_t gi = (int64_t)r * a.ld_in + (int64_t)h * a.q_hs + d0 + lane * E;
+    const int64_t oi = (int64_t)r * a.ld_out + (int64_t)h * HD + d0 + lane * E;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
         const int d = lane * E + e;
@@ -1213,7 +1218,7 @@ template <int HD>
 static void launch_combine(const AttnArgs& a, hipStream_t stream) {
     if (a.nsplit <= 1) return;
     if (a.nsplit <= 16) hipLaunchKernelGGL((attn_combine<HD, 1>), dim3(a.rows, a.nh), dim3(64), 0, stream, a);
-    else hipLaunchKernelGGL((attn_combine<HD, 4>), dim3(a.rows, a.nh), dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((attn_combine<HD, 4, HD / 64>), dim3(a.rows, a.nh, HD / 64), dim3(256), 0, stream, a);
 }
 
 template <int HD>
