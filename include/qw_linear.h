@@ -185,6 +185,25 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
                        qw_dtype xdt, const float* gamma, float eps, const void* residual,
                        qw_dtype residual_dtype, void* y, qw_dtype ydt, int M, hipStream_t stream);
 
+/* The tail of a decoder layer: the out-projection with its residual, then
+ * the post-norm MLP with its residual, on the FP32 residual stream x [M][H]:
+ *     x = x + W_out . core;   x = x + down(silu(gate.n(x)) * up.n(x)),
+ *     n(x) = RMSNorm(x) * (1 + gamma)   (gamma NULL: the norm folded into gateup)
+ * core [M][>= K_out] (row stride ld_core, 0 = K_out) in the MFMA input type
+ * (BF16).  The equivalent of qw_linear(W_out, core, residual = x, y = x)
+ * followed by qw_mlp_fused(x, gamma, residual = x, y = x), which is what it
+ * runs by default.  With QW_LAYER_TAIL=1 in the environment of qw_init, at
+ * decode sizes (M <= 4, BF16 or INT8 weights, W_out [H][<= 2048]) it runs as
+ * one launch in which the first gate/up workgroups compute the out-projection
+ * and hand x_mid to the rest (same results within rounding; measured ~0.7 us
+ * per layer slower than the two launches in a replayed decode graph).  Replaces the out-projection + post_norm forward_with_residual + MLP
+ * forward_add_residual steps of CudaLayer::forward (cuda_engine.cu:118-124,
+ * with the out-projections of linear_attention_cuda.cu:174-187 and
+ * full_attention_cuda.cu:708-714). */
+qw_status qw_layer_tail(qw_ctx* ctx, const qw_weight* w_out, const void* core, qw_dtype core_dtype, int ld_core,
+                        const qw_weight* gateup, const qw_weight* down, const float* gamma, float eps, float* x,
+                        int M, hipStream_t stream);
+
 /* L consecutive MLP blocks: for l < L, x = x + down_l(silu(gate_l.n_l(x)) *
  * (up_l.n_l(x))) with n_l(x) = RMSNorm(x) * (1 + gamma[l]) (eps), x rounded
  * to xdt after every block; x [M][1024] in, y [M][1024] out (y may alias x).

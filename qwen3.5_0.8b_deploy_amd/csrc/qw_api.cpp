@@ -64,6 +64,7 @@ struct qw_ctx {
     unsigned* stack_epoch = nullptr;       // persistent MLP stack: launch epoch, abort word
     uint64_t* stack_words = nullptr;       // persistent MLP stack: hand-off words
     bool mlp_stack = true;                 // QW_MLP_STACK=0: per-layer launches in qw_mlp_stack
+    bool layer_tail = false;               // QW_LAYER_TAIL=1: qw_layer_tail in one launch (measured slower)
     float4* partials = nullptr;
     size_t partials_bytes = 0;
     uint8_t* scratch = nullptr;            // MLP intermediate h
@@ -194,6 +195,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_MLP_FUSED")) c->mlp_fused = atoi(v) != 0 ? 1 : 0;
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (const char* v = getenv("QW_MLP_STACK")) c->mlp_stack = atoi(v) != 0;
+    if (const char* v = getenv("QW_LAYER_TAIL")) c->layer_tail = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_DA")) c->gemm_da = std::max(0, std::min(2, atoi(v)));
@@ -1373,6 +1375,76 @@ qw_status qw_mlp_fused(qw_ctx* ctx, const qw_weight* gateup, const qw_weight* do
         if (s != QW_OK) return s;
     }
     return QW_OK;
+}
+
+qw_status qw_layer_tail(qw_ctx* ctx, const qw_weight* w_out, const void* core, qw_dtype core_dtype, int ld_core,
+                        const qw_weight* gateup, const qw_weight* down, const float* gamma, float eps, float* x,
+                        int M, hipStream_t stream) {
+    if (!ctx) return QW_ERR_NULL;
+    if (!w_out || !core || !gateup || !down || !x) return fail(ctx, QW_ERR_NULL, "layer_tail: NULL argument");
+    if (w_out->glu) return fail(ctx, QW_ERR_INVALID, "layer_tail: w_out must not be a GLU weight");
+    if (!gateup->glu || down->glu) return fail(ctx, QW_ERR_INVALID, "layer_tail: gateup must be GLU, down not");
+    const int H = gateup->K;
+    if (w_out->N != H || down->N != H || down->K != gateup->N)
+        return fail(ctx, QW_ERR_SHAPE, "layer_tail: w_out [%d][%d], gateup [%d][%d], down [%d][%d] do not chain",
+                    w_out->N, w_out->K, gateup->N, gateup->K, down->N, down->K);
+    if (M < 1) return fail(ctx, QW_ERR_SHAPE, "layer_tail: M=%d must be >= 1", M);
+    const int ldc = ld_core ? ld_core : w_out->K;
+    if (ldc < w_out->K) return fail(ctx, QW_ERR_SHAPE, "layer_tail: ld_core %d < K %d", ldc, w_out->K);
+    if (gateup->norm_folded && gamma)
+        return fail(ctx, QW_ERR_INVALID, "layer_tail: gateup already carries the norm weight: pass gamma = NULL");
+    const bool norm = gamma != nullptr || gateup->norm_folded;
+    const int wfi = (int)gateup->wf;
+    const qw_dtype hdt = gateup->wf == QW_WFMT_BF16 ? QW_BF16 : QW_F16;
+    // one launch: the fused MLP's decode route with the out-projection stage
+    const bool one = ctx->layer_tail && ctx->mlp_fused != 0 && core_dtype == QW_BF16 &&
+                     (gateup->wf == QW_WFMT_BF16 || gateup->wf == QW_WFMT_INT8_ROWSCALE) &&
+                     w_out->wf == gateup->wf && down->wf == gateup->wf && M <= qwk::mlp_fused_max_m(QW_F32) &&
+                     H <= 1024 && H % 16 == 0 && (H + 15) / 16 <= (gateup->N + 15) / 16 &&
+                     w_out->ksteps <= qwk::mlp_pre_max_ksteps(wfi) &&
+                     w_out->K % (gateup->wf == QW_WFMT_BF16 ? 32 : 64) == 0 &&
+                     gateup->ksteps <= qwk::mlp_fused_max_ksteps(wfi, false) &&
+                     down->ksteps <= qwk::mlp_fused_max_ksteps(wfi, true) &&
+                     qwk::mlp_counter_words() <= kMlpCounterWords && (size_t)M * gateup->N * dsize(hdt) <= ctx->scratch_bytes &&
+                     (size_t)M * H * 4 <= ctx->partials_bytes && aligned(x, 16) && aligned(core, 16) && ldc % 8 == 0 &&
+                     (!gamma || aligned(gamma, 16));
+    if (one) {
+        if (norm && !(eps > 0.0f)) return fail(ctx, QW_ERR_INVALID, "eps must be > 0");
+        float* xmid = reinterpret_cast<float*>(ctx->partials);
+        qwk::MlpArgs p{};
+        qwk::SkinnyArgs& o = p.pre;
+        o.w = w_out->packed; o.scales = w_out->scales; o.x = core; o.ldx = ldc; o.M = M; o.K = w_out->K; o.N = H;
+        o.n_groups = (H + 15) / 16; o.S = 1; o.ksteps = w_out->ksteps; o.n_items = o.n_groups;
+        o.flags = QW_EP_RESIDUAL; o.res = x; o.res_dt = QW_F32; o.ld_res = H;
+        o.y = xmid; o.ydt = QW_F32; o.ldy = H;
+        p.xmid = xmid;
+        qwk::SkinnyArgs& u = p.up;
+        u.w = gateup->packed; u.scales = gateup->scales; u.x = x; u.ldx = H; u.M = M; u.K = H; u.N = gateup->N;
+        u.n_groups = (gateup->N + 15) / 16; u.S = 1; u.ksteps = gateup->ksteps; u.n_items = u.n_groups;
+        u.flags = norm ? QW_EP_NORM_X : 0u; u.gamma = gamma; u.eps = eps;
+        u.y = ctx->scratch; u.ydt = hdt; u.ldy = gateup->N;
+        qwk::SkinnyArgs& d = p.down;
+        d.w = down->packed; d.scales = down->scales; d.x = ctx->scratch; d.ldx = gateup->N; d.M = M; d.K = gateup->N;
+        d.N = H; d.n_groups = (H + 15) / 16; d.S = 1; d.ksteps = down->ksteps; d.n_items = d.n_groups;
+        d.flags = QW_EP_RESIDUAL; d.res = xmid; d.res_dt = QW_F32; d.ld_res = H;
+        d.y = x; d.ydt = QW_F32; d.ldy = H;
+        d.vec_store = 1;
+        p.ctl = ctx->mlp_ctl;
+        p.cnt = ctx->counters + kMaxCounters;
+        p.n_up = u.n_groups;
+        p.n_down = d.n_groups;
+        hipError_t e = qwk::launch_mlp_fused(p, wfi, (int)QW_F32, stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "layer tail launch");
+        return QW_OK;
+    }
+    qw_epilogue ep{};
+    ep.flags = QW_EP_RESIDUAL;
+    ep.residual = x;
+    ep.residual_dtype = QW_F32;
+    ep.ld_residual = H;
+    qw_status s = qw_linear(ctx, w_out, core, core_dtype, ldc, M, x, QW_F32, H, &ep, stream);
+    if (s != QW_OK) return s;
+    return qw_mlp_fused(ctx, gateup, down, x, QW_F32, gamma, eps, x, QW_F32, x, QW_F32, M, stream);
 }
 
 qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const qw_weight* const* down,

@@ -171,11 +171,17 @@ struct MlpArgs {
     unsigned* cnt;   // completion / exit counter slots, zero between launches (mlp_counter_words())
     int n_up;
     int n_down;
+    // optional out-projection ahead of the block (qw_layer_tail): pre.w != null
+    // -> x_mid = x + pre.w . pre.x (FP32 x only) written to xmid [M][H], and the
+    // block runs on x_mid with x_mid as its residual
+    SkinnyArgs pre;
+    float* xmid;
 };
 // largest k-step count per projection the one-launch MLP holds in registers
 // (0: weight format not supported)
 int mlp_fused_max_ksteps(int wf, bool down);
 int mlp_counter_words();
+int mlp_pre_max_ksteps(int wf);  // k-steps of the out-projection stage (qw_layer_tail)
 int mlp_fused_max_m(int xdt);  // tokens the one-launch MLP takes for activations of this dtype
 hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t stream);
 

@@ -55,6 +55,8 @@ constexpr int MLP_NWD = MLP_NW / MLP_DG;
 // top counter, each on its own 256-byte line, so that no single address
 // takes hundreds of atomics at once (they serialize at the coherence point).
 constexpr int MLP_SLOTS = 32, MLP_EXIT_SLOTS = 8, MLP_SLOT_STRIDE = 64;
+// out-projection tiles done (qw_layer_tail), after the exit slots and the top counter
+constexpr int MLP_PRE_SLOTS = 8, MLP_PRE_BASE = (MLP_SLOTS + MLP_EXIT_SLOTS + 1) * MLP_SLOT_STRIDE;
 // FP32 activations (the engine's residual stream) are staged into LDS as
 // hi + lo planes of the MFMA input type, for up to this many tokens
 constexpr int MLP_F32_MAX_M = 4, MLP_MAX_K = 1024;
@@ -69,7 +71,16 @@ template <int WF> struct MlpUnits;
 template <> struct MlpUnits<WF_BF16> { static constexpr int UA = 2, UB = 14; };
 template <> struct MlpUnits<WF_I8> { static constexpr int UA = 1, UB = 7; };
 
-int mlp_counter_words() { return (MLP_SLOTS + MLP_EXIT_SLOTS + 1) * MLP_SLOT_STRIDE; }
+int mlp_counter_words() { return MLP_PRE_BASE + MLP_PRE_SLOTS * MLP_SLOT_STRIDE; }
+
+// the out-projection ahead of the block: one 16-row tile over the whole K per
+// workgroup, K cut in sixteen by wave
+template <int WF> struct MlpPreUnits { static constexpr int U = 2 * MlpUnits<WF>::UA; };
+int mlp_pre_max_ksteps(int wf) {
+    if (wf == WF_BF16) return MLP_NW * MlpPreUnits<WF_BF16>::U;
+    if (wf == WF_I8) return MLP_NW * MlpPreUnits<WF_I8>::U;
+    return 0;
+}
 
 int mlp_fused_max_ksteps(int wf, bool down) {
     if (wf == WF_BF16) return down ? MLP_NWD * MlpUnits<WF_BF16>::UB : MLP_NW * MlpUnits<WF_BF16>::UA;
@@ -122,12 +133,97 @@ __device__ __forceinline__ void reduce_runs(f32x4 (&red)[NW][2][64], float (&red
     }
 }
 
+// Out-projection tile t of qw_layer_tail (a gate/up workgroup, before its own
+// work): x_mid rows [16t, 16t+16) = x + W_o . core, FP32, K (the core width)
+// cut in sixteen by wave and reduced in a fixed order, the residual added as
+// the separate projection's epilogue adds it.  Wave 0 stores the rows with
+// device-coherent stores, waits for them and counts the tile done.
+template <int WF>
+__device__ __forceinline__ void mlp_pre_tile(const MlpArgs& p, int t, int wave_id, int lane, f32x4 (&red)[MLP_NW][2][64],
+                                             float (&red_ss)[MLP_NW][16]) {
+    constexpr int U = MlpPreUnits<WF>::U;
+    constexpr int KE = WTraits<WF>::KE;
+    const SkinnyArgs& o = p.pre;
+    const int r = lane & 15, g = lane >> 4;
+    int kb, kend;
+    wave_range<MLP_NW>(0, o.ksteps, wave_id, kb, kend);
+    const int n = kend - kb;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(o.w, (uint32_t)((uint64_t)o.n_groups * o.ksteps * 1024u));
+    const __amdgpu_buffer_rsrc_t cr = make_rsrc(o.x, (uint32_t)((uint64_t)o.M * o.ldx * 2u));
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(o.scales ? (const void*)o.scales : o.x, o.scales ? (uint32_t)o.n_groups * 64u : 0u);
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(o.res, (uint32_t)((uint64_t)o.M * o.ld_res * 4u));
+    const uint32_t crow = r < o.M ? (uint32_t)(r * o.ldx + g * KE) * 2u : OOB;
+    // the core fragments (small, needed first), the weights, the scales and the residual rows
+    XFrag<WF, DT_BF16, 1> X[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t xo[1] = {u < n ? crow + (uint32_t)(kb + u) * 4u * KE * 2u : OOB};
+        load_xfrag<WF, DT_BF16, 1, false>(cr, cr, xo, OOB, X[u]);
+    }
+    u32x4 A[U][1];
+    issue_weights<1, U>(o, wrs, t, kb, n, lane, A);
+    u32x4 sc = u32x4{0u, 0u, 0u, 0u};
+    if constexpr (WF == WF_I8)
+        sc = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(sr, (uint32_t)((t * 16 + g * 4) * 4), 0, 0));
+    const int ro = t * 16 + g * 4;
+    const bool mine = r < o.M && ro < o.N;
+    const u32x4 xin = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, mine ? (uint32_t)(r * o.ld_res + ro) * 4u : OOB, 0, 0));
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
+    float ss = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const BOps<WF, DT_BF16> b = make_bops<WF, DT_BF16, 1, false, false>(X[u], 0, ss);
+        acc[0] = unit_mfma<WF, DT_BF16>(A[u][0], b, acc[0]);
+    }
+    reduce_runs<MLP_NW, MLP_NW, 1, false>(red, red_ss, acc, ss, wave_id, lane);
+    if (wave_id == 0) {
+        f32x4 v = acc[0];
+        if constexpr (WF == WF_I8) v *= as_f32x4(sc);
+        v += as_f32x4(xin);
+        if (mine) {
+            unsigned* dst = reinterpret_cast<unsigned*>(p.xmid + (int64_t)r * o.ldy + ro);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) __hip_atomic_store(dst + i, __float_as_uint(v[i]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (lane == 0)
+            __hip_atomic_fetch_add(&p.cnt[MLP_PRE_BASE + (t % MLP_PRE_SLOTS) * MLP_SLOT_STRIDE], 1u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Bounded wait (wave 0, then the workgroup) until every out-projection tile is done.
+__device__ __forceinline__ void mlp_pre_wait(const MlpArgs& p, int wave_id, int lane) {
+    if (wave_id == 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (;;) {
+            unsigned v = lane < MLP_PRE_SLOTS ? __hip_atomic_load(&p.cnt[MLP_PRE_BASE + lane * MLP_SLOT_STRIDE],
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                              : 0u;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+            if (v >= (unsigned)p.pre.n_groups) break;
+            __builtin_amdgcn_s_sleep(1);
+            if (__builtin_amdgcn_s_memrealtime() - t0 > 20000000ull) {
+                if (lane == 0) __hip_atomic_store(&p.ctl[3], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // WF: weight format (gate/up and down share it); XDT: dtype of x (16-bit
 // read straight into registers, FP32 staged through LDS).
 // The intermediate h is held in the MFMA input type of WF (BF16, or F16 for
 // INT8 weights), which is what the down projection consumes.
-template <int WF, int XDT, bool NORM, bool GAM>
+// PRE (FP32 x only): the out-projection of qw_layer_tail runs first (gate/up
+// workgroups [0, pre.n_groups) take one tile each), and the block reads x_mid.
+template <int WF, int XDT, bool NORM, bool GAM, bool PRE>
 __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void mlp_kernel(MlpArgs p) {
+    static_assert(!PRE || XDT == DT_F32, "the out-projection stage feeds the FP32 staging");
     const int n_dwg = (p.n_down + MLP_DG - 1) / MLP_DG;
     constexpr int NW = MLP_NW;
     constexpr int KE = WTraits<WF>::KE;
@@ -170,17 +266,26 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
         };
         if constexpr (XDT == DT_F32) {
             // x (times 1 + gamma) staged into LDS as hi + lo planes; the weight
-            // loads are issued between the staging's loads and its LDS writes
-            const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 4u));
+            // loads are issued between the staging's loads and its LDS writes.
+            // PRE: the out-projection tile first (if this workgroup has one),
+            // then the weights, the wait for every tile, and x_mid staged with
+            // device-coherent loads (written in this launch)
+            const __amdgpu_buffer_rsrc_t xr = make_rsrc(PRE ? (const void*)p.xmid : a.x, (uint32_t)((uint64_t)a.M * a.ldx * 4u));
             const int kr = a.K;
+            if constexpr (PRE) {
+                if (grp < p.pre.n_groups) mlp_pre_tile<WF>(p, grp, wave_id, lane, red, red_ss);
+                issue_rest();
+                mlp_pre_wait(p, wave_id, lane);
+            }
             auto stage = [&](auto sq_tag) {
                 constexpr int SQ = decltype(sq_tag)::value;
+                constexpr int XA = PRE ? AUX_SC1 : 0;
                 XStage<XDT, SQ> st;
-                stage_issue<WF, XDT, NW, SQ, NORM>(a, xr, gr, 0, kr, st);
+                stage_issue<WF, XDT, NW, SQ, NORM, XA>(a, xr, gr, 0, kr, st);
                 __builtin_amdgcn_sched_barrier(0);
-                issue_rest();
+                if constexpr (!PRE) issue_rest();
                 __builtin_amdgcn_sched_barrier(0);
-                stage_finish<WF, XDT, 1, NW, SQ, NORM>(a, xr, gr, 0, kr, st, xs_f32, ss_tok, ss_scratch);
+                stage_finish<WF, XDT, 1, NW, SQ, NORM, XA>(a, xr, gr, 0, kr, st, xs_f32, ss_tok, ss_scratch);
             };
             const int rp = 1 << (32 - __builtin_clz((unsigned)a.M));
             const int cpt = ((kr / 8) * rp + NW * 64 - 1) / (NW * 64);
@@ -274,8 +379,9 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
         const bool res_ok = want_res && a.vec_store && has_tile && r < a.M && ro < a.N;
         const uint32_t ri = (uint32_t)((int64_t)r * a.ld_res + ro);
         const bool res32 = a.res_dt == DT_F32;
-        const u32x4 rv32 = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, res_ok && res32 ? ri * 4 : OOB, 0, 0));
+        // PRE: the residual is x_mid, written in this launch: loaded after the wait
+        u32x4 rv32 = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, res_ok && res32 && !PRE ? ri * 4 : OOB, 0, 0));
         const u32x2 rv16 = __builtin_bit_cast(
             u32x2, __builtin_amdgcn_raw_buffer_load_b64(rr, res_ok && !res32 ? ri * 2 : OOB, 0, 0));
         __builtin_amdgcn_sched_barrier(0);
@@ -298,6 +404,8 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
             }
         }
         __syncthreads();
+        if constexpr (PRE)
+            rv32 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, res_ok && res32 ? ri * 4 : OOB, 0, AUX_SC1));
         const uint32_t xrow = r < a.M ? (uint32_t)(r * a.ldx + g * KE) * 2u : OOB;
         XFrag<WF, HDT, 1> X[UB];
         load_frags<WF, HDT, UB, AUX_SC1>(hr, xrow, kb, n, X);
@@ -346,6 +454,11 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
                         __hip_atomic_store(&p.cnt[q * MLP_SLOT_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     for (int q = 0; q < MLP_EXIT_SLOTS; ++q)
                         __hip_atomic_store(&ex[q * MLP_SLOT_STRIDE], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if constexpr (PRE) {
+                        for (int q = 0; q < MLP_PRE_SLOTS; ++q)
+                            __hip_atomic_store(&p.cnt[MLP_PRE_BASE + q * MLP_SLOT_STRIDE], 0u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                    }
                     __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
             }
@@ -353,12 +466,12 @@ __global__ __launch_bounds__(MLP_NW * 64) __attribute__((amdgpu_waves_per_eu(4))
     }
 }
 
-template <int WF, int XDT>
+template <int WF, int XDT, bool PRE = false>
 static hipError_t launch_mlp2(const MlpArgs& p, bool norm, bool gam, hipStream_t st) {
     const dim3 grid((p.n_down + MLP_DG - 1) / MLP_DG + p.n_up), block(MLP_NW * 64);
-    if (norm && gam) hipLaunchKernelGGL((mlp_kernel<WF, XDT, true, true>), grid, block, 0, st, p);
-    else if (norm) hipLaunchKernelGGL((mlp_kernel<WF, XDT, true, false>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((mlp_kernel<WF, XDT, false, false>), grid, block, 0, st, p);
+    if (norm && gam) hipLaunchKernelGGL((mlp_kernel<WF, XDT, true, true, PRE>), grid, block, 0, st, p);
+    else if (norm) hipLaunchKernelGGL((mlp_kernel<WF, XDT, true, false, PRE>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((mlp_kernel<WF, XDT, false, false, PRE>), grid, block, 0, st, p);
     return hipGetLastError();
 }
 
@@ -368,6 +481,16 @@ hipError_t launch_mlp_fused(const MlpArgs& p, int wf, int xdt, hipStream_t strea
         return hipErrorInvalidValue;
     const bool norm = (p.up.flags & EP_NORM) != 0;
     const bool gam = norm && p.up.gamma != nullptr;
+    if (p.pre.w) {
+        // the out-projection stage: FP32 x, BF16 core, one tile per gate/up workgroup
+        if (xdt != DT_F32 || !p.xmid || p.pre.n_groups > p.n_up || p.pre.ksteps > mlp_pre_max_ksteps(wf) ||
+            p.pre.M != p.up.M || p.pre.N != p.up.K || p.up.x != p.pre.res || p.down.res != p.xmid ||
+            p.pre.ldy != p.up.ldx || p.pre.ld_res != p.up.ldx)
+            return hipErrorInvalidValue;
+        if (wf == WF_BF16) return launch_mlp2<WF_BF16, DT_F32, true>(p, norm, gam, stream);
+        if (wf == WF_I8) return launch_mlp2<WF_I8, DT_F32, true>(p, norm, gam, stream);
+        return hipErrorInvalidValue;
+    }
     if (wf == WF_BF16 && xdt == DT_BF16) return launch_mlp2<WF_BF16, DT_BF16>(p, norm, gam, stream);
     if (wf == WF_I8 && xdt == DT_F16) return launch_mlp2<WF_I8, DT_F16>(p, norm, gam, stream);
     if (wf == WF_I8 && xdt == DT_BF16) return launch_mlp2<WF_I8, DT_BF16>(p, norm, gam, stream);

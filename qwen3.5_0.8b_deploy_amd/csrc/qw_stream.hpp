@@ -318,7 +318,6 @@ __device__ __forceinline__ void wave_range(int ks0, int ks1, int wave_id, int& k
     kend = ks0 + ((wave_id + 1) * cnt) / NW;
 }
 
-// Issue the weight loads of k-steps [kb, kb+n) (n <= U) of tile group grp.
 // Issue the weight loads of k-steps [kb, kb+n) (n <= U) of tile group grp;
 // the U - n unused slots are issued out of range (zeros, no traffic).
 template <int RT, int U>

@@ -201,12 +201,14 @@ class DecodeEngine:
                 qw.attn_forward(ctx, P["q_norm"], P["k_norm"], P["cache"], self.pos, r[:, 0:], r[:, HD:],
                                 r[:, FNH * 2 * HD:], r[:, FNH * 2 * HD + FNKV * HD:], self.core, tokens=1,
                                 q_head_stride=2 * HD, ld_in=row.stride(0), max_len=self.capacity, stream=stream)
-            qw.linear(ctx, P["out"], self.core, x, residual=x, stream=stream)
             if self.norm_first:
+                qw.linear(ctx, P["out"], self.core, x, residual=x, stream=stream)
                 qw.rmsnorm(ctx, x, P["post_norm"], self.xh, stream=stream)
                 qw.mlp_fused(ctx, P["gateup"], P["down"], self.xh, x, residual=x, stream=stream)
             else:
-                qw.mlp_fused(ctx, P["gateup"], P["down"], x, x, gamma=P["post_norm"], residual=x, stream=stream)
+                # out-projection + residual, post-norm MLP + residual: one launch at decode sizes
+                qw.layer_tail(ctx, P["out"], self.core, P["gateup"], P["down"], x, gamma=P["post_norm"],
+                              stream=stream)
         qw.rmsnorm(ctx, x, self.final_norm, self.xn, stream=stream)
         qw.lmhead_argmax(ctx, self.E, self.xn, self.ids, stream=stream)
         qw.positions_add(ctx, self.pos, 1, stream=stream)

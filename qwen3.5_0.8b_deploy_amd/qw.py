@@ -30,7 +30,7 @@ EXPORTS = [
     "qw_abi_version", "qw_weight_pack", "qw_weight_pack_glu", "qw_weight_pack_device",
     "qw_weight_pack_glu_device", "qw_weight_pack_concat", "qw_weight_pack_concat_device", "qw_weight_wrap_packed",
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
-    "qw_linear", "qw_mlp_fused", "qw_mlp_stack", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
+    "qw_linear", "qw_mlp_fused", "qw_layer_tail", "qw_mlp_stack", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_embedding_gather", "qw_positions_add", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
     "qw_chain_create", "qw_chain_launch", "qw_chain_destroy",
 ]
@@ -148,6 +148,7 @@ def lib():
         "qw_weight_unpack": ([_vp, _vp, _vp, _vp], _i),
         "qw_linear": ([_vp, _vp, _vp, _i, _i, _i, _vp, _i, _i, ctypes.POINTER(Epilogue), _vp], _i),
         "qw_mlp_fused": ([_vp, _vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _i, _i, _vp], _i),
+        "qw_layer_tail": ([_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _f, _vp, _i, _vp], _i),
         "qw_gdn_decode": ([_vp, ctypes.POINTER(GdnParams), _i, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _i, _i,
                            _vp], _i),
         "qw_embedding_gather": ([_vp, _vp, _i, _i, _i, _vp, _i, _vp, _i, _i, _vp], _i),
@@ -414,6 +415,18 @@ def mlp_fused(ctx, gateup, down, x, y, gamma=None, eps=1e-6, residual=None, stre
                                  _ptr(gamma), eps, _ptr(residual),
                                  _torch_code(residual) if residual is not None else F32,
                                  _ptr(y), _torch_code(y), M, _stream(stream)))
+
+
+def layer_tail(ctx, w_out, core, gateup, down, x, gamma=None, eps=1e-6, stream=None):
+    """qw_layer_tail: x += w_out.core, then x += MLP(RMSNorm(x) (1 + gamma)), on
+    the FP32 residual stream x [M][H] in place; core [M][>=K_out] BF16."""
+    import torch
+    M = x.shape[0] if x.dim() == 2 else 1
+    if x.dtype != torch.float32:
+        raise TypeError("layer_tail: x must be float32")
+    ldc = core.stride(0) if core.dim() == 2 else 0
+    ctx.check(lib().qw_layer_tail(ctx.handle, w_out.handle, _ptr(core), _torch_code(core), ldc, gateup.handle,
+                                  down.handle, _ptr(gamma), eps, _ptr(x), M, _stream(stream)))
 
 
 def mlp_stack(ctx, gateups, downs, x, y, gammas=None, eps=1e-6, stream=None):
