@@ -64,6 +64,7 @@ struct qw_ctx {
     unsigned* stack_epoch = nullptr;       // persistent MLP stack: launch epoch, abort word
     uint64_t* stack_words = nullptr;       // persistent MLP stack: hand-off words
     bool mlp_stack = true;                 // QW_MLP_STACK=0: per-layer launches in qw_mlp_stack
+    int gemm_da_split = -1;                // QW_GEMM_DA_SPLIT: split-K direct-A for few blocks (-1 auto, 0 off, S)
     bool layer_tail = false;               // QW_LAYER_TAIL=1: qw_layer_tail in one launch (measured slower)
     float4* partials = nullptr;
     size_t partials_bytes = 0;
@@ -105,7 +106,7 @@ namespace {
 constexpr size_t kCountersBytes = 64 * 1024;     // 16384 tiles
 constexpr size_t kKeysBytes = 64 * 1024;         // 8192 tokens
 constexpr size_t kDoneBytes = 256;
-constexpr size_t kPartialsBytes = 32u << 20;
+constexpr size_t kPartialsBytes = 64u << 20;
 constexpr size_t kStackBytes = 512 * 1024;  // hand-off words of the persistent MLP stack (zeroed at init)
 constexpr size_t kFixedBytes = kCountersBytes + kKeysBytes + kDoneBytes + kStackBytes + kPartialsBytes;
 constexpr int kMlpCounterWords = 4096;  // tail of the counter region: the one-launch MLP's slots
@@ -196,6 +197,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMV")) c->gemv = atoi(v) != 0;
     if (const char* v = getenv("QW_MLP_STACK")) c->mlp_stack = atoi(v) != 0;
     if (const char* v = getenv("QW_LAYER_TAIL")) c->layer_tail = atoi(v) != 0;
+    if (const char* v = getenv("QW_GEMM_DA_SPLIT")) c->gemm_da_split = atoi(v);
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_DA")) c->gemm_da = std::max(0, std::min(2, atoi(v)));
@@ -853,15 +855,54 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, int rows, const void*
     }
     if ((uint64_t)W->bytes >= (1ull << 31) || (uint64_t)M * ldx * 2 >= (1ull << 31))
         return fail(ctx, QW_ERR_SHAPE, "operands above 2 GiB are not supported");
-    // the direct-A kernel (256 x 128 blocks, two per CU) where its blocks
-    // fill the chip at least once over (the prefill shapes)
-    if (ctx->gemm_da && rows == 256 && !ctx->gemm_tile_m &&
-        (ctx->gemm_da == 2 || (W->phys_tiles * 16 + 255) / 256 * ((M + 127) / 128) >= ctx->num_cus) &&
+    // the direct-A kernel (256 x 128 blocks, two per CU) wherever its blocks
+    // occupy at least half the CUs: the prefill shapes, and from a few hundred
+    // tokens on the wide projections (measured at 520 / 1024 tokens: gate/up
+    // 30.7 / 28.3 -> 23.0 / 23.6 us, QKV+Z 34.3 -> 25.6 us at 520, Q+gate+K+V
+    // 30.8 -> 24.2 us at 1024).  Fewer blocks keep the 64-row split-K GEMM: a
+    // split-K direct-A kernel measured 1.7-2.9x slower on the 1024-row
+    // projections (its last workgroup reads every partial tile through one CU)
+    if (ctx->gemm_da && (rows == 256 || rows == 64) && !ctx->gemm_tile_m &&
+        (ctx->gemm_da == 2 || 2 * ((W->phys_tiles * 16 + 255) / 256 * ((M + 127) / 128)) >= ctx->num_cus) &&
         qwk::gemm_da_fits(a, W->wf, (int)xdt, ids != nullptr)) {
         a.group_m = ctx->gemm_da_group;
         hipError_t e = qwk::launch_gemm_da(a, W->glu != 0, ctx->gemm_da_line, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
         return QW_OK;
+    }
+    // fewer blocks than half the CUs (the 1024-row projections up to ~4000
+    // tokens): the direct-A kernel with K split S ways into partial tiles, then
+    // the reduce + epilogue kernel.  S is the fewest splits that give half the
+    // CUs a workgroup (each split a multiple of the weight ring and >= 8
+    // k-steps, the partials within the workspace): at 1024 tokens 128-224
+    // workgroups measured best (down 46.8 -> 24 us, out 34.0 -> 20.5 us; 448
+    // workgroups 30.5 us), at 3072 tokens S = 2 (down 94 -> 40 us, out 61 ->
+    // 30 us).  QW_GEMM_DA_SPLIT forces S (0: off)
+    const int da_blocks = (W->phys_tiles * 16 + 255) / 256 * ((M + 127) / 128);
+    if (ctx->gemm_da && ctx->gemm_da_split != 0 && (rows == 256 || rows == 64) && !ctx->gemm_tile_m && !ids &&
+        (ctx->gemm_da_split > 0 || 2 * da_blocks < ctx->num_cus)) {
+        qwk::GemmArgs d = a;
+        d.splitk = 1;
+        d.group_m = ctx->gemm_da_group;
+        d.partials = reinterpret_cast<float*>(ctx->partials);
+        int S = 0;
+        if (qwk::gemm_da_fits(d, W->wf, (int)xdt, false)) {
+            for (int sc = 2; sc <= 32; ++sc) {
+                if (W->ksteps % (4 * sc) != 0 || W->ksteps / sc < 8) continue;
+                if (qwk::gemm_da_split_bytes(d, sc) > ctx->partials_bytes) break;
+                if (ctx->gemm_da_split > 0) {
+                    if (sc == ctx->gemm_da_split) S = sc;
+                    continue;
+                }
+                S = sc;
+                if (2 * da_blocks * sc >= ctx->num_cus) break;
+            }
+        }
+        if (S >= 2) {
+            hipError_t e = qwk::launch_gemm_da_split(d, W->glu != 0, ctx->gemm_da_line, S, stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
+            return QW_OK;
+        }
     }
     hipError_t e = qwk::launch_gemm(a, W->wf, (int)xdt, W->glu != 0, ids != nullptr, stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "GEMM launch");

@@ -26,6 +26,15 @@
 // pieces and stores whole 128-byte (or 64-byte) token rows, adding the
 // residual and applying the Q/gate de-interleave on the way.
 //
+// Split-K (few blocks: the 1024-row projections at a few hundred to a few
+// thousand tokens).  The S workgroups of a block take contiguous k-step
+// ranges (multiples of the weight ring) and store their FP32 accumulators to
+// a partial buffer [block][split][piece][thread] (coalesced, no epilogue);
+// a second kernel (gemm_da_reduce), one workgroup per block and accumulator
+// piece, sums the S partials in split order and runs the same epilogue
+// per element.  One workgroup reducing a whole block would read S x 128 KB
+// through one CU, which measured slower than not splitting.
+//
 // Buffers.  The weight and activation buffer descriptors start at the
 // workgroup's first row / token and end at the operands' end, so rows past
 // the end read zeros and per-lane offsets stay fixed; the k-step goes in the
@@ -65,9 +74,24 @@ __device__ __forceinline__ void lds_dma16_so(__amdgpu_buffer_rsrc_t rs, uint8_t*
                  : "memory", "m0");
 }
 
+// Block `tile` of the grouped raster: DA_GROUP_M token blocks x all weight
+// blocks per group, token block fastest -> first token m0, first 16-row tile nt0.
+__device__ __forceinline__ void da_tile(const GemmArgs& a, int tile, int& m0, int& nt0) {
+    const int GM = a.group_m > 0 ? a.group_m : DA_GROUP_M;
+    const int per_group = GM * a.nblk_n;
+    const int group = tile / per_group;
+    const int first_m = group * GM;
+    const int gm = min(GM, a.nblk_m - first_m);
+    const int in_group = tile - group * per_group;
+    m0 = (first_m + in_group % gm) * 128;
+    nt0 = (in_group / gm) * 16;
+}
+
 }  // namespace
 
-template <bool GLU, bool LINE>
+// PART: one K split of a block (blockIdx = block * splitk + split after the
+// XCD order), partial accumulators out, no epilogue.
+template <bool GLU, bool LINE, bool PART>
 __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
     using E = DaEpi<GLU>;
     constexpr int D = DA_D, NS = LINE ? DA_NS2 : DA_NS;
@@ -78,28 +102,26 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
     float* const epw = reinterpret_cast<float*>(lds + NS * STG + wave * E::BYTES);
 
     // XCD-aware order (consecutive ids go to different XCDs: give each XCD a
-    // contiguous range), then a grouped raster: DA_GROUP_M token blocks x all
-    // weight blocks per group, token block fastest
+    // contiguous range; the splits of a block are consecutive in it), then
+    // the grouped raster
     const int nwg = gridDim.x;
     int b = blockIdx.x;
     if ((nwg & 7) == 0) b = (b & 7) * (nwg >> 3) + (b >> 3);
-    const int GM = a.group_m > 0 ? a.group_m : DA_GROUP_M;
-    const int per_group = GM * a.nblk_n;
-    const int group = b / per_group;
-    const int first_m = group * GM;
-    const int gm = min(GM, a.nblk_m - first_m);
-    const int in_group = b - group * per_group;
-    const int m0 = (first_m + in_group % gm) * 128;
-    const int nt0 = (in_group / gm) * 16;
-    const int ks_n = a.ksteps;
+    const int S = PART ? a.splitk : 1;
+    const int sk = PART ? b % S : 0;
+    if constexpr (PART) b /= S;
+    int m0, nt0;
+    da_tile(a, b, m0, nt0);
+    const int ks_n = a.ksteps / S;  // k-steps of this split (a multiple of D)
+    const int kbase = sk * ks_n;
 
     const __amdgpu_buffer_rsrc_t wrs =
-        make_rsrc(a.w + (size_t)nt0 * ks_n * 1024, (uint32_t)((a.n_tiles - nt0) * ks_n * 1024));
+        make_rsrc(a.w + (size_t)nt0 * a.ksteps * 1024, (uint32_t)((a.n_tiles - nt0) * a.ksteps * 1024));
     const __amdgpu_buffer_rsrc_t xrs =
         make_rsrc(static_cast<const uint16_t*>(a.x) + (size_t)m0 * a.ldx, (uint32_t)((a.M - m0) * a.ldx * 2));
     uint32_t va[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) va[i] = (uint32_t)(((wave * 4 + i) * ks_n * 64 + lane) * 16);
+    for (int i = 0; i < 4; ++i) va[i] = (uint32_t)(((wave * 4 + i) * a.ksteps * 64 + lane) * 16);
     // k-steps past the end reload the last one (never used)
     auto kc = [&](int ks) { return __builtin_amdgcn_readfirstlane(min(ks, ks_n - 1)); };
     u32x4 A[D][4], B[8];
@@ -109,7 +131,7 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto loadA = [&](u32x4 (&dst)[4], int ks) {
-        const int so = kc(ks) * 1024;
+        const int so = (kbase + kc(ks)) * 1024;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, va[i], so, 0);
     };
@@ -137,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
             vb[q] = (uint32_t)((((wave * 2 + q) * 16 + (lane & 15)) * a.ldx + (lane >> 4) * 8) * 2);
         auto dma = [&](int ks) {
             uint8_t* st = lds + (ks % NS) * STG + wave * 2048;
-            const int so = kc(ks) * 64;
+            const int so = (kbase + kc(ks)) * 64;
 #pragma unroll
             for (int q = 0; q < 2; ++q) lds_dma16_so(xrs, st + q * 1024, vb[q], so);
         };
@@ -182,7 +204,7 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
         }
         auto dma = [&](int p) {  // k-steps 2p, 2p+1
             uint8_t* st = lds + (p % NS) * STG + wave * 4 * DA_U2;
-            const int so = __builtin_amdgcn_readfirstlane(min(p, (ks_n >> 1) - 1)) * 128;
+            const int so = kbase * 64 + __builtin_amdgcn_readfirstlane(min(p, (ks_n >> 1) - 1)) * 128;
 #pragma unroll
             for (int q = 0; q < 4; ++q) lds_dma16_so(xrs, st + q * DA_U2, vb[q], so);
         };
@@ -220,6 +242,16 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
                 loadA(A[u], ks + D);
             }
         }
+    }
+
+    if constexpr (PART) {
+        // partial pieces [block][split][piece i*8+j][thread]
+        f32x4* pp = reinterpret_cast<f32x4*>(a.partials) + ((size_t)b * S + sk) * 32 * 256 + threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pp[(i * 8 + j) * 256] = acc[i][j];
+        return;
     }
 
     // ---- epilogue: accumulator item e of lane l = row 4(l/16)+e of the row
@@ -264,6 +296,48 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
     }
 }
 
+// The split-K epilogue: workgroup (block, piece) sums the S partial pieces of
+// its 256 threads in split order and stores them as gemm_da_kernel's epilogue
+// would (the GLU pairs gate piece 2i with up piece 2i+1 of the same column).
+template <bool GLU>
+__global__ __launch_bounds__(256) void gemm_da_reduce(GemmArgs a) {
+    constexpr int PP = GLU ? 16 : 32;  // output pieces per block
+    const int blk = blockIdx.x / PP, q = blockIdx.x % PP;
+    const int i = q / 8, j = q % 8;    // row tile (pair for GLU) and token column
+    const int S = a.splitk;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4;
+    const f32x4* pp = reinterpret_cast<const f32x4*>(a.partials) + (size_t)blk * S * 32 * 256 + tid;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    const int p0 = GLU ? (2 * i) * 8 + j : i * 8 + j, p1 = (2 * i + 1) * 8 + j;
+    for (int sp = 0; sp < S; ++sp) {
+        s0 += pp[((size_t)sp * 32 + p0) * 256];
+        if (GLU) s1 += pp[((size_t)sp * 32 + p1) * 256];
+    }
+    f32x4 o;
+    if constexpr (GLU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = silu_f(s0[e]) * s1[e];
+    } else {
+        o = s0;
+    }
+    int m0, nt0;
+    da_tile(a, blk, m0, nt0);
+    const int rows_w = GLU ? 32 : 64;
+    const int row = (GLU ? (nt0 >> 1) : nt0) * 16 + wave * rows_w + i * 16 + 4 * g;
+    const int m = m0 + 16 * j + (lane & 15);
+    if (m < a.M && row < a.N) {
+        if (a.flags & EP_RESIDUAL) o += load_act4(a.res, a.res_dt, (int64_t)m * a.ld_res + row);
+        void* dst = a.y;
+        int col = row;
+        if (a.flags & EP_SPLIT) {
+            const int sp_log = 31 - __builtin_clz((unsigned)a.split_period);
+            dst = ((row >> sp_log) & 1) ? a.y2 : a.y;
+            col = ((row >> (sp_log + 1)) << sp_log) + (row & (a.split_period - 1));
+        }
+        store_act4(dst, a.ydt, (int64_t)m * a.ldy + col, o);
+    }
+}
+
 bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax) {
     if (a.ldx % 8 != 0) return false;  // 16-byte activation chunks
     if (wf != WF_BF16 || xdt != DT_BF16 || argmax || a.splitk > 1) return false;
@@ -293,8 +367,38 @@ hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t st
         hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, stream, b);
         return hipGetLastError();
     };
-    if (line) return glu ? go(gemm_da_kernel<true, true>) : go(gemm_da_kernel<false, true>);
-    return glu ? go(gemm_da_kernel<true, false>) : go(gemm_da_kernel<false, false>);
+    if (line) return glu ? go(gemm_da_kernel<true, true, false>) : go(gemm_da_kernel<false, true, false>);
+    return glu ? go(gemm_da_kernel<true, false, false>) : go(gemm_da_kernel<false, false, false>);
+}
+
+size_t gemm_da_split_bytes(const GemmArgs& a, int S) {
+    return (size_t)((a.n_tiles * 16 + 255) / 256) * ((a.M + 127) / 128) * S * 32 * 256 * 16;
+}
+
+hipError_t launch_gemm_da_split(const GemmArgs& a, bool glu, bool line, int S, hipStream_t stream) {
+    if (S < 2 || a.ksteps % (DA_D * S) != 0 || !a.partials) return hipErrorInvalidValue;
+    GemmArgs b = a;
+    b.nblk_n = (a.n_tiles * 16 + 255) / 256;
+    b.nblk_m = (a.M + 127) / 128;
+    b.splitk = S;
+    const int blocks = b.nblk_n * b.nblk_m;
+    const size_t lds = gemm_da_lds_bytes(glu, line);
+    auto go = [&](auto k) {
+        static bool configured = false;  // one attribute call per instantiation
+        if (!configured) {
+            hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
+            if (e != hipSuccess) return e;
+            configured = true;
+        }
+        hipLaunchKernelGGL(k, dim3(blocks * S), dim3(256), lds, stream, b);
+        return hipGetLastError();
+    };
+    hipError_t e = line ? (glu ? go(gemm_da_kernel<true, true, true>) : go(gemm_da_kernel<false, true, true>))
+                        : (glu ? go(gemm_da_kernel<true, false, true>) : go(gemm_da_kernel<false, false, true>));
+    if (e != hipSuccess) return e;
+    if (glu) hipLaunchKernelGGL(gemm_da_reduce<true>, dim3(blocks * 16), dim3(256), 0, stream, b);
+    else hipLaunchKernelGGL(gemm_da_reduce<false>, dim3(blocks * 32), dim3(256), 0, stream, b);
+    return hipGetLastError();
 }
 
 }  // namespace qwk

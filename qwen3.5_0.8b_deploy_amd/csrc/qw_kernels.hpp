@@ -161,6 +161,10 @@ size_t gemm_da_lds_bytes(bool glu, bool line);
 // line: activation loads of whole 128-byte row lines (two k-steps, swizzled
 // into LDS) instead of 64-byte row pieces
 hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream);
+// split-K form: S K splits (a.ksteps a multiple of 4 S) into a.partials
+// (gemm_da_split_bytes), then the reduce + epilogue kernel
+size_t gemm_da_split_bytes(const GemmArgs& a, int S);
+hipError_t launch_gemm_da_split(const GemmArgs& a, bool glu, bool line, int S, hipStream_t stream);
 
 // Fused MLP block in one launch (qw_mlp.hip): `up` is the gate/up GLU pass
 // (x -> h, y = the h buffer), `down` the down pass (h -> y).
