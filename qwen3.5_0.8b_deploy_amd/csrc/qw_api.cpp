@@ -49,6 +49,8 @@ struct qw_ctx {
     int wide_s = 0;              // K splits (QW_WIDE_S; 0 = planned)
     bool wide_norm_sep = false;  // RMSNorm prologue as a separate launch (QW_WIDE_NORM_SEP=1) instead of in the kernel
     int wide_dbg = 0;            // QW_WIDE_DBG: timing probes (wrong results)
+    int stack_dbg = 0;           // QW_MLP_STACK_DBG: timing probes of the MLP stack (wrong results)
+    int stack_gap = 20;          // QW_MLP_STACK_GAP: 10 ns ticks between a gate/up group's weight k-steps
     int wide_cfg = 0;            // blocks x waves per block (QW_WIDE_CFG 1: 4x1, 2: 2x2, 3: 1x4; 0 = planned)
     int attn_split = 0;          // keys per decode split, 0 = by size (QW_ATTN_SPLIT forces a multiple of 64)
     int attn_vcoal = -1;         // INT8 decode V loads: -1 by launch size, 0 scattered, 1 coalesced (QW_ATTN_VCOAL)
@@ -216,6 +218,8 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_WIDE_S")) c->wide_s = std::max(0, atoi(v));
     if (const char* v = getenv("QW_WIDE_NORM_SEP")) c->wide_norm_sep = atoi(v) != 0;
     if (const char* v = getenv("QW_WIDE_DBG")) c->wide_dbg = atoi(v);
+    if (const char* v = getenv("QW_MLP_STACK_DBG")) c->stack_dbg = atoi(v);
+    if (const char* v = getenv("QW_MLP_STACK_GAP")) c->stack_gap = std::max(0, std::min(1000, atoi(v)));
     if (const char* v = getenv("QW_WIDE_CFG")) c->wide_cfg = std::max(0, std::min(3, atoi(v)));
     if (const char* v = getenv("QW_WIDE_T")) c->wide_cfg |= std::max(0, std::min(8, atoi(v))) << 4;  // token groups
     if (const char* v = getenv("QW_GEMM_MIN_M")) {
@@ -1526,6 +1530,8 @@ qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const
         a.hbuf = ctx->stack_words;
         a.epoch = ctx->stack_epoch;
         a.err = ctx->mlp_ctl + 3;
+        a.dbg = ctx->stack_dbg;
+        a.gap = ctx->stack_gap;
         hipError_t e = qwk::launch_mlp_stack(a, (int)gateup[0]->wf, (int)xdt, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "MLP stack launch");
         return QW_OK;

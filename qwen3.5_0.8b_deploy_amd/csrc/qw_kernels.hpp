@@ -207,6 +207,8 @@ struct MlpStackArgs {
     uint64_t* xbuf;     // set by launch_mlp_stack
     unsigned* epoch;    // [2]: launch epoch (advanced by every launch), abort word
     unsigned* err;      // device error flag
+    int dbg;            // timing probes (wrong results): 1 no gate/up weight loads, 2 no down weight loads
+    int gap;            // 100 MHz ticks between the k-steps of a gate/up group's weight requests
 };
 size_t mlp_stack_ws_bytes();
 int mlp_stack_max_m();

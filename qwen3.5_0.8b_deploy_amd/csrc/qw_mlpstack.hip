@@ -265,14 +265,29 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         u32x4 sc[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
         auto issue = [&](int l) {
             const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.gu[l], (uint32_t)(MS_I / 16) * 2u * tile_bytes);
+            if (a.dbg & 1) {  // timing probe: no gate/up weight traffic (wrong results)
 #pragma unroll
-            for (int u = 0; u < U_GU; ++u)
+                for (int u = 0; u < U_GU; ++u) A[u][0] = A[u][1] = u32x4{(uint32_t)l, 0u, 0u, 0u};
+                return;
+            }
+            // the k-steps go out a.gap ticks of the 100 MHz clock apart: all
+            // of a workgroup's gate/up weights requested at once, right after
+            // its epilogue stores, delay the hand-off words then in flight
+            // (24 BF16 blocks at M = 1 with a per-call gamma: 184 us per step
+            // at once, 162 us at 20 ticks apart, 143 us with no gate/up weight
+            // loads at all; 10 to 40 ticks measure alike)
+            const uint64_t tb = __builtin_amdgcn_s_memrealtime();
+#pragma unroll
+            for (int u = 0; u < U_GU; ++u) {
+                if (u > 0 && a.gap > 0)
+                    while (__builtin_amdgcn_s_memrealtime() - tb < (uint64_t)(u * a.gap)) __builtin_amdgcn_s_sleep(1);
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt)
                     A[u][rt] = __builtin_bit_cast(
                         u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                    wr, lane * 16, (uint32_t)(p * 2 + rt) * tile_bytes + (uint32_t)(w * U_GU + u) * 1024u,
                                    AUX_NT));
+            }
             if constexpr (GAM) {
                 gm[0] = a.gamma[l][k0 + 2 * lane];
                 gm[1] = a.gamma[l][k0 + 2 * lane + 1];
@@ -479,6 +494,11 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         u32x4 sc = u32x4{0u, 0u, 0u, 0u};
         auto issue = [&](int l) {
             const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.dn[l], (uint32_t)(MS_H / 16) * tile_bytes);
+            if (a.dbg & 2) {  // timing probe: no down weight traffic (wrong results)
+#pragma unroll
+                for (int u = 0; u < U_DN; ++u) A[u] = u32x4{(uint32_t)l, 0u, 0u, 0u};
+                return;
+            }
 #pragma unroll
             for (int u = 0; u < U_DN; ++u)
                 A[u] = __builtin_bit_cast(
