@@ -443,6 +443,23 @@ def run_cfg3(qw, ctx, torch, timer, stream, randn, steps):
                                           "TFLOPs": round(fl / ms / 1e9, 2)}
         log("cfg3", M, extra[f"cfg3_int8_stack_M{M}"])
         del g
+    # The config-3 MLP blocks alone (INT8 gate/up and down, F16 activations,
+    # per-call RMSNorm weight) as one persistent qw_mlp_stack launch.
+    gams = [randn(H, std=0.02, dtype=torch.float32) for _ in range(LAYERS)]
+    for M in (1, 8):
+        xs = randn(M, H, dtype=torch.float16)
+        g = graphed(qw, ctx, stream, lambda xs=xs: qw.mlp_stack(ctx, [L["gu"] for L in layers],
+                                                                [L["down"] for L in layers], xs, xs, gammas=gams,
+                                                                stream=stream))
+        ms = timer.run(g.launch, steps, 2)
+        if ctx.device_error():
+            raise RuntimeError("device error flag after the INT8 MLP stack")
+        b = LAYERS * (3 * H * I + (2 * I + H) * 4 + M * H * 2 * 2 + H * 4)
+        extra[f"cfg3_int8_mlp_stack_M{M}"] = {"us_per_layer": round(ms * 1e3 / LAYERS, 2),
+                                              "GBps": round(b / ms / 1e6, 1),
+                                              "pct_hbm": round(100 * b / ms / 1e6 / HBM_PEAK, 1)}
+        log("cfg3 int8 mlp stack", M, extra[f"cfg3_int8_mlp_stack_M{M}"])
+        del g
     # The same 24 layers as ONE persistent projection chain (qw_chain) at
     # decode sizes, in the model's dependency order: in -> out (reading the
     # first 2048 outputs of in, the attention core's stand-in) + residual ->
