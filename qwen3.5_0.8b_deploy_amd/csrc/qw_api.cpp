@@ -40,6 +40,8 @@ struct qw_ctx {
                                  // 1 where its blocks fill the chip, 2 wherever it applies)
     bool gemm_da_line = true;    // its activation loads as whole row lines (QW_GEMM_DA_LINE=0: row pieces)
     int gemm_da_group = 0;       // its token blocks per raster group (QW_GEMM_DA_GROUP; 0: 8)
+    int gemm_da_waves = 0;       // its waves per block: 4 (256 rows, two blocks per CU) or 8 (512 rows, one);
+                                 // 0: 8 where the 512-row blocks cover every CU (QW_GEMM_DA_W8=0/1 forces 4/8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
     int gemm_splitk = 0;         // K splits per GEMM tile (QW_GEMM_SPLITK; 0 = by shape)
     int gdn_chunk_min = kGdnChunkMin;
@@ -205,6 +207,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_DA")) c->gemm_da = std::max(0, std::min(2, atoi(v)));
     if (const char* v = getenv("QW_GEMM_DA_LINE")) c->gemm_da_line = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_DA_GROUP")) c->gemm_da_group = std::max(0, atoi(v));
+    if (const char* v = getenv("QW_GEMM_DA_W8")) c->gemm_da_waves = atoi(v) != 0 ? 8 : 4;
     if (const char* v = getenv("QW_GEMM_SPLITK")) c->gemm_splitk = std::max(0, std::min(8, atoi(v)));
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
@@ -870,7 +873,10 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, int rows, const void*
         (ctx->gemm_da == 2 || 2 * ((W->phys_tiles * 16 + 255) / 256 * ((M + 127) / 128)) >= ctx->num_cus) &&
         qwk::gemm_da_fits(a, W->wf, (int)xdt, ids != nullptr)) {
         a.group_m = ctx->gemm_da_group;
-        hipError_t e = qwk::launch_gemm_da(a, W->glu != 0, ctx->gemm_da_line, stream);
+        const int nwv = ctx->gemm_da_waves
+                            ? ctx->gemm_da_waves
+                            : ((W->phys_tiles * 16 + 511) / 512 * ((M + 127) / 128) >= ctx->num_cus ? 8 : 4);
+        hipError_t e = qwk::launch_gemm_da(a, W->glu != 0, ctx->gemm_da_line, stream, nwv);
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
         return QW_OK;
     }

@@ -76,7 +76,7 @@ __device__ __forceinline__ void lds_dma16_so(__amdgpu_buffer_rsrc_t rs, uint8_t*
 
 // Block `tile` of the grouped raster: DA_GROUP_M token blocks x all weight
 // blocks per group, token block fastest -> first token m0, first 16-row tile nt0.
-__device__ __forceinline__ void da_tile(const GemmArgs& a, int tile, int& m0, int& nt0) {
+__device__ __forceinline__ void da_tile(const GemmArgs& a, int tile, int& m0, int& nt0, int tiles_per_blk = 16) {
     const int GM = a.group_m > 0 ? a.group_m : DA_GROUP_M;
     const int per_group = GM * a.nblk_n;
     const int group = tile / per_group;
@@ -84,15 +84,19 @@ __device__ __forceinline__ void da_tile(const GemmArgs& a, int tile, int& m0, in
     const int gm = min(GM, a.nblk_m - first_m);
     const int in_group = tile - group * per_group;
     m0 = (first_m + in_group % gm) * 128;
-    nt0 = (in_group / gm) * 16;
+    nt0 = (in_group / gm) * tiles_per_blk;
 }
 
 }  // namespace
 
 // PART: one K split of a block (blockIdx = block * splitk + split after the
 // XCD order), partial accumulators out, no epilogue.
-template <bool GLU, bool LINE, bool PART>
-__global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
+// NWV waves (4, or 8 with line loads): 64 * NWV weight rows per block, the
+// activation stages shared by all of them.
+template <bool GLU, bool LINE, bool PART, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV, NWV == 4 ? 2 : 1) void gemm_da_kernel(GemmArgs a) {
+    static_assert(NWV == 4 || (NWV == 8 && LINE && !PART), "8 waves: line loads, no split");
+    constexpr int QN = 16 / NWV;  // activation units per wave and stage (line loads)
     using E = DaEpi<GLU>;
     constexpr int D = DA_D, NS = LINE ? DA_NS2 : DA_NS;
     constexpr int STG = LINE ? DA_STG2 : DA_STG;
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
     const int sk = PART ? b % S : 0;
     if constexpr (PART) b /= S;
     int m0, nt0;
-    da_tile(a, b, m0, nt0);
+    da_tile(a, b, m0, nt0, 4 * NWV);
     const int ks_n = a.ksteps / S;  // k-steps of this split (a multiple of D)
     const int kbase = sk * ks_n;
 
@@ -194,19 +198,19 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
         // fragment read (lane = token t + 16 g of k-step s, chunk c = 4s + g)
         // then hits 16 different 16-byte bank groups per 16 lanes: whole-line
         // loads, conflict-free reads
-        uint32_t vb[4];
+        uint32_t vb[QN];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int unit = wave * 4 + q;  // = 2 * token tile + h
+        for (int q = 0; q < QN; ++q) {
+            const int unit = wave * QN + q;  // = 2 * token tile + h
             const int sl = lane ^ (8 * (unit & 1));
             const int c_ld = sl >> 3, t_ld = (sl & 7) ^ c_ld;
             vb[q] = (uint32_t)(((unit * 8 + t_ld) * a.ldx + c_ld * 8) * 2);
         }
         auto dma = [&](int p) {  // k-steps 2p, 2p+1
-            uint8_t* st = lds + (p % NS) * STG + wave * 4 * DA_U2;
+            uint8_t* st = lds + (p % NS) * STG + wave * QN * DA_U2;
             const int so = kbase * 64 + __builtin_amdgcn_readfirstlane(min(p, (ks_n >> 1) - 1)) * 128;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) lds_dma16_so(xrs, st + q * DA_U2, vb[q], so);
+            for (int q = 0; q < QN; ++q) lds_dma16_so(xrs, st + q * DA_U2, vb[q], so);
         };
         const int t_rd = lane & 15, g_rd = lane >> 4;
         auto roff = [&](int s) {  // read offset of k-step parity s within a tile's pair of units
@@ -229,10 +233,10 @@ __global__ __launch_bounds__(256, 2) void gemm_da_kernel(GemmArgs a) {
                 const int p = ks >> 1;
                 if (u & 1) {
                     // second k-step of pair p: our loads of pair p+1 have
-                    // landed (after them: 4 weight loads, 12 loads per later
-                    // pair, 4 of this pair's first k-step), publish; pair p's
-                    // stage is free for pair p+NS
-                    __builtin_amdgcn_s_waitcnt(vm_wait(8 + 12 * (NS - 2)));
+                    // landed (after them: 4 weight loads, QN + 8 loads per
+                    // later pair, 4 of this pair's first k-step), publish;
+                    // pair p's stage is free for pair p+NS
+                    __builtin_amdgcn_s_waitcnt(vm_wait(8 + (QN + 8) * (NS - 2)));
                     __syncthreads();
                     dma(p + NS);
                     mfma_step(u, lds + ((p + 1) % NS) * STG, ro0, 0);
@@ -347,16 +351,18 @@ bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax) {
     return a.ksteps % DA_D == 0;
 }
 
-size_t gemm_da_lds_bytes(bool glu, bool line) {
-    return (size_t)(line ? DA_NS2 * DA_STG2 : DA_NS * DA_STG) + 4 * (glu ? DaEpi<true>::BYTES : DaEpi<false>::BYTES);
+size_t gemm_da_lds_bytes(bool glu, bool line, int nwv) {
+    return (size_t)(line ? DA_NS2 * DA_STG2 : DA_NS * DA_STG) + nwv * (glu ? DaEpi<true>::BYTES : DaEpi<false>::BYTES);
 }
 
-hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream) {
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream, int nwv) {
+    if (nwv == 8 && !line) nwv = 4;
     GemmArgs b = a;
-    b.nblk_n = (a.n_tiles * 16 + 255) / 256;
+    const int rows = 64 * nwv;
+    b.nblk_n = (a.n_tiles * 16 + rows - 1) / rows;
     b.nblk_m = (a.M + 127) / 128;
     const int grid = b.nblk_n * b.nblk_m;
-    const size_t lds = gemm_da_lds_bytes(glu, line);
+    const size_t lds = gemm_da_lds_bytes(glu, line, nwv);
     auto go = [&](auto k) {
         static bool configured = false;  // one attribute call per instantiation
         if (!configured) {
@@ -364,9 +370,10 @@ hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t st
             if (e != hipSuccess) return e;
             configured = true;
         }
-        hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, stream, b);
+        hipLaunchKernelGGL(k, dim3(grid), dim3(64 * nwv), lds, stream, b);
         return hipGetLastError();
     };
+    if (nwv == 8) return glu ? go(gemm_da_kernel<true, true, false, 8>) : go(gemm_da_kernel<false, true, false, 8>);
     if (line) return glu ? go(gemm_da_kernel<true, true, false>) : go(gemm_da_kernel<false, true, false>);
     return glu ? go(gemm_da_kernel<true, false, false>) : go(gemm_da_kernel<false, false, false>);
 }
@@ -382,7 +389,7 @@ hipError_t launch_gemm_da_split(const GemmArgs& a, bool glu, bool line, int S, h
     b.nblk_m = (a.M + 127) / 128;
     b.splitk = S;
     const int blocks = b.nblk_n * b.nblk_m;
-    const size_t lds = gemm_da_lds_bytes(glu, line);
+    const size_t lds = gemm_da_lds_bytes(glu, line, 4);
     auto go = [&](auto k) {
         static bool configured = false;  // one attribute call per instantiation
         if (!configured) {

@@ -157,10 +157,10 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int xdt, bool glu, bool argmax
 // Direct-A GEMM (qw_gemm_da.hip): BF16 x BF16, 256-row x 128-token blocks,
 // two workgroups per CU; plain, GLU, residual and split epilogues.
 bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax);
-size_t gemm_da_lds_bytes(bool glu, bool line);
+size_t gemm_da_lds_bytes(bool glu, bool line, int nwv);
 // line: activation loads of whole 128-byte row lines (two k-steps, swizzled
 // into LDS) instead of 64-byte row pieces
-hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream);
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream, int nwv = 4);
 // split-K form: S K splits (a.ksteps a multiple of 4 S) into a.partials
 // (gemm_da_split_bytes), then the reduce + epilogue kernel
 size_t gemm_da_split_bytes(const GemmArgs& a, int S);
