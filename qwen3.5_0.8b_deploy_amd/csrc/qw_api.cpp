@@ -52,7 +52,8 @@ struct qw_ctx {
     bool wide_norm_sep = false;  // RMSNorm prologue as a separate launch (QW_WIDE_NORM_SEP=1) instead of in the kernel
     int wide_dbg = 0;            // QW_WIDE_DBG: timing probes (wrong results)
     int stack_dbg = 0;           // QW_MLP_STACK_DBG: timing probes of the MLP stack (wrong results)
-    int stack_gap = 20;          // QW_MLP_STACK_GAP: 10 ns ticks between a gate/up group's weight k-steps
+    int stack_gap = -1;          // QW_MLP_STACK_GAP: 10 ns ticks between a gate/up group's weight k-steps
+                                 // (-1: 20 for BF16 weights, 120 for INT8, the measured best of each)
     int wide_cfg = 0;            // blocks x waves per block (QW_WIDE_CFG 1: 4x1, 2: 2x2, 3: 1x4; 0 = planned)
     int attn_split = 0;          // keys per decode split, 0 = by size (QW_ATTN_SPLIT forces a multiple of 64)
     int attn_vcoal = -1;         // INT8 decode V loads: -1 by launch size, 0 scattered, 1 coalesced (QW_ATTN_VCOAL)
@@ -1537,7 +1538,7 @@ qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const
         a.epoch = ctx->stack_epoch;
         a.err = ctx->mlp_ctl + 3;
         a.dbg = ctx->stack_dbg;
-        a.gap = ctx->stack_gap;
+        a.gap = ctx->stack_gap >= 0 ? ctx->stack_gap : (gateup[0]->wf == QW_WFMT_INT8_ROWSCALE ? 120 : 20);
         hipError_t e = qwk::launch_mlp_stack(a, (int)gateup[0]->wf, (int)xdt, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "MLP stack launch");
         return QW_OK;

@@ -305,7 +305,8 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             // its epilogue stores, delay the hand-off words then in flight
             // (24 BF16 blocks at M = 1 with a per-call gamma: 184 us per step
             // at once, 162 us at 20 ticks apart, 143 us with no gate/up weight
-            // loads at all; 10 to 40 ticks measure alike)
+            // loads at all; 10 to 60 ticks measure alike; INT8, two k-steps
+            // per wave: 6.60 / 6.24 / 5.99 us per block at 0 / 20 / 120 ticks)
             const uint64_t tb = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
             for (int u = 0; u < U_GU; ++u) {
