@@ -269,6 +269,16 @@ qw_status qw_chain_create(qw_ctx* ctx, qw_dtype act_dtype, int M, int n_slots, c
 qw_status qw_chain_launch(qw_chain* chain, hipStream_t stream);
 qw_status qw_chain_destroy(qw_chain* chain);
 
+/* Test hooks of the two persistent kernels above (no counterpart in the
+ * reference): read (*get) and/or set (*set) the launch epoch whose low bits
+ * tag their hand-off words -- 26 bits for qw_mlp_stack, 22 for a chain (whose
+ * low 22 bits may not be 0).  The epoch advances once per launch; the launch
+ * at which the tag's field wraps clears the words first, so a word written
+ * 2^26 (2^22) launches earlier never matches.  Setting the epoch just below
+ * the wrap lets a test run launches across it.  Synchronizes the device. */
+qw_status qw_mlp_stack_epoch(qw_ctx* ctx, const unsigned* set, unsigned* get);
+qw_status qw_chain_epoch(qw_chain* chain, const unsigned* set, unsigned* get);
+
 /* Reads and clears the context's device error flag: non-zero when a kernel
  * gave up a bounded wait (a fused MLP down task whose gate/up inputs never
  * completed within 0.2 s), when an attention token fell outside its cache, or
@@ -371,7 +381,9 @@ qw_status qw_lmhead_argmax(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dt
  * library (2.3 KB, held until the process ends), so M is at most 256
  * (QW_ERR_SHAPE beyond).  Runs on the current device with the kernels and
  * routes of qw_lmhead_argmax on a default context, so its results equal that
- * entry point's bit for bit.  Calls that overlap on one device share the
+ * entry point's bit for bit on a context created without QW_* routing
+ * overrides in the environment (this entry point always takes the default
+ * routes and ignores those variables).  Calls that overlap on one device share the
  * array and race: serialize them (one stream, or events).  Errors are
  * status codes only (there is no context for qw_last_error). */
 qw_status qw_lmhead_argmax_noalloc(const void* E_packed, const float* E_scales, qw_wfmt fmt, int V, int K,

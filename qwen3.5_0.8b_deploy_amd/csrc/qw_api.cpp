@@ -11,12 +11,29 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/qw_linear.h"
 #include "qw_internal.hpp"
 #include "qw_kernels.hpp"
+
+hipError_t qwk::ensure_max_lds(const void* kernel, int bytes) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, int> done;  // (device, kernel) -> largest size set
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(mu);
+    int& have = done[{dev, kernel}];
+    if (have >= bytes) return hipSuccess;
+    e = set_max_lds(kernel, bytes);
+    if (e == hipSuccess) have = bytes;
+    return e;
+}
 
 constexpr int kGemmMinM = 33;
 constexpr int kWideMinM = 17;  // default token count from which the weight-stationary kernel is used  // default token count from which the MFMA GEMM is used
@@ -1689,6 +1706,8 @@ qw_status qw_chain_create(qw_ctx* ctx, qw_dtype act_dtype, int M, int n_slots, c
     A.n_ops = n_ops;
     A.M = M;
     A.epoch = reinterpret_cast<unsigned*>(ch->mem + op_bytes);
+    A.words = wbase;
+    A.n_words = (uint32_t)words;
     A.err = ctx->mlp_ctl + 3;
     for (int s = 0; s < n_slots; ++s) {
         if (!slots[s].init) continue;
@@ -1736,6 +1755,29 @@ qw_status qw_chain_destroy(qw_chain* ch) {
     hipFree(ch->mem);
     delete ch;
     return QW_OK;
+}
+
+// Test hooks: read and/or set the launch epoch of the persistent kernels'
+// hand-off words (synchronous; no launch may be in flight on the device).
+static qw_status epoch_rw(qw_ctx* ctx, unsigned* word, const unsigned* set, unsigned* get) {
+    hipSetDevice(ctx->device);
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess && get) e = hipMemcpy(get, word, sizeof(unsigned), hipMemcpyDeviceToHost);
+    if (e == hipSuccess && set) e = hipMemcpy(word, set, sizeof(unsigned), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) return hip_fail(ctx, e, "epoch word access");
+    return QW_OK;
+}
+
+qw_status qw_mlp_stack_epoch(qw_ctx* ctx, const unsigned* set, unsigned* get) {
+    if (!ctx) return QW_ERR_NULL;
+    return epoch_rw(ctx, ctx->stack_epoch, set, get);
+}
+
+qw_status qw_chain_epoch(qw_chain* ch, const unsigned* set, unsigned* get) {
+    if (!ch) return QW_ERR_NULL;
+    if (set && (*set & ((1u << 22) - 1u)) == 0u) return fail(ch->ctx, QW_ERR_INVALID, "chain epoch: the low 22 bits may not be 0");
+    return epoch_rw(ch->ctx, ch->args.epoch, set, get);
 }
 
 qw_status qw_device_error(qw_ctx* ctx, int* flag) {

@@ -15,7 +15,7 @@
 // values; tag = epoch << 10 | op + 1, 0 for the values imported at launch
 // start), written with agent-scope stores and polled until every tag is the
 // one expected; `epoch` advances once per launch, so no word needs clearing
-// (graph replays included).
+// (graph replays included) except when the tag's 22 epoch bits wrap (below).
 //
 // Work split (grid = 256 workgroups of 16 waves, one per CU, all resident):
 // op o's output blocks (16-row tiles, or gate/up tile pairs) go round robin to
@@ -76,6 +76,15 @@ struct ChLds {
 };
 
 __device__ __forceinline__ uint32_t ch_tag(uint32_t epoch, int op_tag) { return (epoch << 10) | (uint32_t)op_tag; }
+// The tag keeps 22 bits of the epoch.  The epoch skips the values whose field
+// is 0 (an import tag would then be 0, the value of a cleared word), so the
+// field runs 1 .. 2^22 - 1, and the launch at which it returns to 1 clears
+// every slot word first (wrap_clear_words).
+constexpr uint32_t CH_EFIELD = (1u << 22) - 1u;
+__device__ __forceinline__ uint32_t ch_next_epoch(uint32_t e) {
+    const uint32_t n = e + 1u;
+    return (n & CH_EFIELD) == 0u ? n + 1u : n;
+}
 
 __device__ __forceinline__ uint64_t ch_load(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -167,6 +176,9 @@ __global__ __launch_bounds__(CH_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     const int wg = blockIdx.x;
     const int M = a.M;
     const uint32_t epoch = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool dead = false;
+    // the launch at which the epoch field returns to 1 clears the slot words
+    if ((epoch & CH_EFIELD) == 1u && epoch > CH_EFIELD) wrap_clear_words(a.words, a.n_words, a.epoch + 2, a.err, &L.cnt, dead);
     if (threadIdx.x < 2 * CH_NP) L.ready[threadIdx.x / CH_NP][threadIdx.x % CH_NP] = 0u;
     if (threadIdx.x == 0) {
         L.cnt = 0u;
@@ -179,8 +191,7 @@ __global__ __launch_bounds__(CH_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         const int n = a.n_ops * (int)(sizeof(ChainOp) / 4);
         for (int i = threadIdx.x; i < n; i += CH_NW * 64) dst[i] = src[i];
     }
-    __syncthreads();  // the only workgroup barrier
-    bool dead = false;
+    __syncthreads();  // the only workgroup barrier (besides the wrap clear's)
     const ChAbort ab{a.err, a.epoch + 1, epoch};
 
     if (wave < CH_NP) {
@@ -336,7 +347,7 @@ __global__ __launch_bounds__(CH_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 if (__all(ok) || dead) break;
                 if (!ch_pause(ab, t0, it, dead)) break;
             }
-            if (lane == 0) __hip_atomic_store(a.epoch, epoch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) __hip_atomic_store(a.epoch, ch_next_epoch(epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
@@ -533,11 +544,9 @@ template <typename Kern>
 static hipError_t launch_ch(Kern k, const ChainArgs& a, hipStream_t st) {
     constexpr size_t lds = sizeof(ChLds);
     static_assert(sizeof(ChLds) <= 160 * 1024, "LDS layout");
-    static bool configured = false;
-    if (!configured) {
-        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
+    {
+        hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)lds);
         if (e != hipSuccess) return e;
-        configured = true;
     }
     hipLaunchKernelGGL(k, dim3(CH_GRID), dim3(CH_NW * 64), lds, st, a);
     return hipGetLastError();

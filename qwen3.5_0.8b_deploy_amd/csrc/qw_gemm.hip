@@ -405,7 +405,7 @@ void gemm_kernel(GemmArgs a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (threadIdx.x == 0) {
-            const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             best_s[0][0] = (old == gridDim.x - 1) ? 1ull : 0ull;
         }
         __syncthreads();
@@ -497,11 +497,9 @@ void gemm_kernel(GemmArgs a) {
 
 template <typename Kern>
 static hipError_t launch_gemm_k(Kern k, const GemmArgs& a, int grid, int threads, size_t lds, hipStream_t st) {
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
+    {
+        hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)lds);
         if (e != hipSuccess) return e;
-        configured = true;
     }
     hipLaunchKernelGGL(k, dim3(grid), dim3(threads), lds, st, a);
     return hipGetLastError();

@@ -364,11 +364,9 @@ hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t st
     const int grid = b.nblk_n * b.nblk_m;
     const size_t lds = gemm_da_lds_bytes(glu, line, nwv);
     auto go = [&](auto k) {
-        static bool configured = false;  // one attribute call per instantiation
-        if (!configured) {
-            hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
+        {
+            hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)lds);
             if (e != hipSuccess) return e;
-            configured = true;
         }
         hipLaunchKernelGGL(k, dim3(grid), dim3(64 * nwv), lds, stream, b);
         return hipGetLastError();
@@ -391,11 +389,9 @@ hipError_t launch_gemm_da_split(const GemmArgs& a, bool glu, bool line, int S, h
     const int blocks = b.nblk_n * b.nblk_m;
     const size_t lds = gemm_da_lds_bytes(glu, line, 4);
     auto go = [&](auto k) {
-        static bool configured = false;  // one attribute call per instantiation
-        if (!configured) {
-            hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
+        {
+            hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)lds);
             if (e != hipSuccess) return e;
-            configured = true;
         }
         hipLaunchKernelGGL(k, dim3(blocks * S), dim3(256), lds, stream, b);
         return hipGetLastError();

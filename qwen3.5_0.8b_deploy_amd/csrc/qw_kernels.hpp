@@ -17,6 +17,11 @@ inline hipError_t set_max_lds(const void* kernel, int bytes) {
     return e;
 }
 
+// set_max_lds once per (kernel, size): a thread-safe table keyed on the
+// kernel's address remembers the largest size set, so each instantiation is
+// configured before its first launch and again when a launch asks for more.
+hipError_t ensure_max_lds(const void* kernel, int bytes);
+
 
 // One skinny (small-M) projection launch.  See qw_skinny.hip.
 struct SkinnyArgs {
@@ -205,7 +210,7 @@ struct MlpStackArgs {
     float eps;
     uint64_t* hbuf;     // hand-off words, mlp_stack_ws_bytes() zeroed once (h words, then the x words)
     uint64_t* xbuf;     // set by launch_mlp_stack
-    unsigned* epoch;    // [2]: launch epoch (advanced by every launch), abort word
+    unsigned* epoch;    // [3]: launch epoch (advanced by every launch), abort word, wrap barrier counter
     unsigned* err;      // device error flag
     int dbg;            // timing probes (wrong results): 1 no gate/up weight loads, 2 no down weight loads
     int gap;            // 100 MHz ticks between the k-steps of a gate/up group's weight requests
@@ -252,7 +257,9 @@ struct ChainArgs {
     int n_ops, M;
     ChainImport imports[kChainMaxImports];
     int n_imports;
-    unsigned* epoch;           // [2]: launch epoch (advanced by every launch), abort word
+    unsigned* epoch;           // [3]: launch epoch (advanced by every launch), abort word, wrap barrier counter
+    uint64_t* words;           // every slot word of the chain (cleared when the epoch field wraps)
+    uint32_t n_words;
     unsigned* err;             // device error flag
     uint64_t* trace;           // timing probe [op][4][256] real-time stamps, or nullptr (QW_CHAIN_TRACE)
 };

@@ -35,7 +35,9 @@
 // every tag is the expected one -- no counters, no fences, no memset (a
 // 64-bit store is seen whole or not at all).  `epoch` is a device word read
 // by every wave at the start and advanced by workgroup 0 at the very end, so
-// words of earlier launches never match.  Payloads, two 16-bit values each:
+// words of earlier launches never match; the tag keeps 26 bits of it, and
+// the launch at which those wrap to zero clears every word first
+// (wrap_clear_words).  Payloads, two 16-bit values each:
 //   * h (gate/up -> down): h_buf[layer & 1][m][I/2], the down MFMA input type;
 //   * x (down -> gate/up of the next block): x_buf[layer & 1][m][H/2], the
 //     block output rounded to the activation dtype (the last block's is also
@@ -91,6 +93,7 @@ struct MsLds {
 };
 
 __device__ __forceinline__ uint32_t ms_tag(uint32_t epoch, int layer) { return (epoch << 6) | (uint32_t)(layer + 1); }
+constexpr uint32_t MS_EFIELD = (1u << 26) - 1u;  // the epoch bits a tag keeps
 
 __device__ __forceinline__ uint64_t ms_load(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -258,6 +261,12 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     // every wave holds the epoch before the barrier, so workgroup 0 can only
     // advance it (at the very end, after all hand-offs) once all have read it
     const uint32_t epoch = __hip_atomic_load(a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool dead = false;
+    // the epoch's 26-bit tag field wraps every 2^26 launches: that launch
+    // zeroes the hand-off words first (grid barrier), so no word written
+    // 2^26 launches ago can match a tag of this launch
+    if ((epoch & MS_EFIELD) == 0u && epoch != 0u)
+        wrap_clear_words(a.hbuf, MS_HWORDS + MS_XWORDS, a.epoch + 2, a.err, &S.cnt_fin, dead);
     if (threadIdx.x < MS_RW) S.hflag[threadIdx.x] = 0u;
     if (threadIdx.x == 0) {
         S.cnt_gu[0] = S.cnt_gu[1] = 0u;
@@ -271,8 +280,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         S.xt[m][r] = m < M ? load_act(a.x, XDT, (int64_t)m * MS_H + t * 16 + r) : 0.0f;
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    __syncthreads();  // the only workgroup barrier
-    bool dead = false;
+    __syncthreads();  // the only workgroup barrier (besides the wrap clear's)
     const MsAbort ab{a.err, a.epoch + 1, epoch};
     uint64_t* const hbuf = a.hbuf;
     uint64_t* const xbuf = a.xbuf;
@@ -594,11 +602,9 @@ static hipError_t launch_ms(Kern k, const MlpStackArgs& a, hipStream_t st) {
     constexpr size_t lds = ((sizeof(MsLds) + 1023) / 1024 * 1024) > 96 * 1024 ? (sizeof(MsLds) + 1023) / 1024 * 1024
                                                                                 : 96 * 1024;
     static_assert(lds <= 160 * 1024, "LDS layout");
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)lds);
+    {
+        hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)lds);
         if (e != hipSuccess) return e;
-        configured = true;
     }
     hipLaunchKernelGGL(k, dim3(MS_GRID), dim3(MS_NW * 64), lds, st, a);
     return hipGetLastError();

@@ -366,7 +366,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(SkinnyArgs ain) {
         // them before this workgroup's completion count.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         old = __shfl(old, 0);
         if (old == gridDim.x - 1) {
             for (int m = lane; m < ain.M; m += 64) {
@@ -393,11 +393,9 @@ size_t skinny_lds_bytes(int wf, int xdt, int M, int ksteps_per_split) {
 
 template <typename Kern>
 static hipError_t launch_k(Kern k, const SkinnyArgs& a, int nw, int grid, size_t smem, hipStream_t st) {
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)kSkinnyMaxLds);
+    {
+        hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)kSkinnyMaxLds);
         if (e != hipSuccess) return e;
-        configured = true;
     }
     hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), smem, st, a);
     return hipGetLastError();

@@ -57,6 +57,45 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* ld
                  : "memory", "m0");
 }
 
+// Epoch wrap of the persistent kernels' tagged hand-off words.  A word is
+// (tag << 32 | payload) with the launch epoch in the tag's high bits; once
+// the epoch's field wraps, a word written 2^bits launches earlier (a token
+// slot unused since, when M varies) would carry the tag a consumer now waits
+// for.  The launch at which the field wraps calls this first, with every
+// thread of every workgroup: each workgroup zeroes its share of the words
+// (tag 0 never matches a live tag), and a grid barrier on the monotonic
+// counter `bar` (+gridDim.x per wrap, so it never needs a reset) keeps every
+// producer's first store behind every clear.  All workgroups are resident
+// (the callers' launch contract), so the barrier completes; the wait is
+// bounded (0.2 s) and raises the error flag on expiry.  `flag` is an LDS word
+// the caller initializes afterwards (it carries the outcome to every wave).
+__device__ __forceinline__ void wrap_clear_words(uint64_t* words, size_t n, unsigned* bar, unsigned* err, unsigned* flag,
+                                                 bool& dead) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        __hip_atomic_store(words + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // release: this workgroup's clears are visible before its arrival
+        const unsigned old = __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned target = (old / gridDim.x + 1u) * gridDim.x;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        unsigned d = 0u;
+        while (__hip_atomic_load(bar, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > 20000000ull) {
+                __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                d = 1u;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        *flag = d;
+    }
+    __syncthreads();
+    if (*flag) dead = true;
+    __syncthreads();
+}
+
 // ---------------------------------------------------------------------------
 // LDS layout of the staged activations: nops planes (hi, lo) of (M + 1) rows
 // of `ls` op-elements; row M is all zero and serves tokens >= M.  The row

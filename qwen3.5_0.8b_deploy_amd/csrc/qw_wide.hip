@@ -689,13 +689,14 @@ __global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs
         for (int w = 1; w < NW; ++w) k = kbest[w][threadIdx.x] > k ? kbest[w][threadIdx.x] : k;
         if (k != 0ull) __hip_atomic_fetch_max(&a.keys[M0 + threadIdx.x], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // the key updates are device-scope read-modify-writes: their completion
-    // orders them before this workgroup's completion count
+    // the key updates are device-scope read-modify-writes, complete before
+    // the completion count; the count is an acquire-release RMW, so the last
+    // workgroup's key exchanges are ordered after every workgroup's updates
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __shared__ unsigned last;
     if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         last = old == gridDim.x - 1 ? 1u : 0u;
     }
     __syncthreads();
@@ -742,11 +743,9 @@ WideLayout wide_layout(int wf, int CT, int nks, int NB, int KW, bool glu, bool g
 
 template <typename Kern>
 hipError_t launch_w(Kern k, const WideArgs& a, int nw, int grid, size_t smem, hipStream_t st) {
-    static bool configured = false;  // one attribute call per instantiation
-    if (!configured) {
-        hipError_t e = set_max_lds(reinterpret_cast<const void*>(k), (int)kWideMaxLds);
+    {
+        hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(k), (int)kWideMaxLds);
         if (e != hipSuccess) return e;
-        configured = true;
     }
     hipLaunchKernelGGL(k, dim3(grid), dim3(nw * 64), smem, st, a);
     return hipGetLastError();
@@ -882,9 +881,7 @@ bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs
 
 hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid, size_t smem, hipStream_t stream) {
     auto go = [&](auto kern) {
-        static bool configured = false;
-        (void)configured;
-        hipError_t e = set_max_lds(reinterpret_cast<const void*>(kern), (int)kWideMaxLds);
+        hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(kern), (int)kWideMaxLds);
         if (e != hipSuccess) return e;
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kArgNW * 64), smem, stream, a);
         return hipGetLastError();

@@ -129,7 +129,8 @@ class DecodeEngine:
         kernel from 16.  The states and caches advance by T; self.ids receives
         the greedy next token of every sequence and self.pos += T.
         check (default: when no stream is given) reads the device error flag
-        afterwards and raises if it was set (see check())."""
+        afterwards and raises if it was set (see check()); that read
+        synchronizes the device (check=False keeps the call asynchronous)."""
         import torch
         qw, ctx = self.qw, self.ctx
         B, T = ids.shape
@@ -184,7 +185,10 @@ class DecodeEngine:
         """One greedy token for every sequence: ids <- next ids, positions += 1.
         check (default: when no stream is given, i.e. never while a graph is
         captured on a stream) reads the device error flag afterwards and
-        raises if it was set (see check())."""
+        raises if it was set (see check()); that read synchronizes the device,
+        so an eager step with the default blocks the host until it is done.
+        Pass check=False (or a stream) to keep eager steps asynchronous and
+        call check() every N steps instead."""
         qw, ctx, x, row = self.qw, self.ctx, self.x, self.row
         qw.embedding_gather(ctx, self.embed, self.ids, x, stream=stream)
         for P in self.layers:

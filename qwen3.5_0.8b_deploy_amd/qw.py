@@ -32,7 +32,7 @@ EXPORTS = [
     "qw_weight_free", "qw_weight_fold_norm", "qw_weight_info", "qw_weight_device_ptrs", "qw_weight_unpack",
     "qw_linear", "qw_mlp_fused", "qw_layer_tail", "qw_mlp_stack", "qw_device_error", "qw_lmhead_argmax", "qw_lmhead_argmax_noalloc", "qw_argmax_rows", "qw_rmsnorm", "qw_residual_rmsnorm",
     "qw_silu_mul", "qw_gdn_decode", "qw_gdn_prefill", "qw_attn_forward", "qw_embedding_gather", "qw_positions_add", "qw_graph_begin", "qw_graph_end", "qw_graph_launch", "qw_graph_destroy",
-    "qw_chain_create", "qw_chain_launch", "qw_chain_destroy",
+    "qw_chain_create", "qw_chain_launch", "qw_chain_destroy", "qw_mlp_stack_epoch", "qw_chain_epoch",
 ]
 
 
@@ -172,6 +172,8 @@ def lib():
         "qw_chain_create": ([_vp, _i, _i, _i, ctypes.POINTER(ChainSlot), _i, ctypes.POINTER(ChainOp), pp], _i),
         "qw_chain_launch": ([_vp, _vp], _i),
         "qw_chain_destroy": ([_vp], _i),
+        "qw_mlp_stack_epoch": ([_vp, _vp, _vp], _i),
+        "qw_chain_epoch": ([_vp, _vp, _vp], _i),
     }
     for name, (args, res) in sigs.items():
         fn = getattr(L, name)
@@ -224,6 +226,14 @@ class Context:
         """Read (and clear) the device error flag (synchronizes)."""
         v = ctypes.c_int()
         self.check(lib().qw_device_error(self._h, ctypes.byref(v)))
+        return v.value
+
+    def stack_epoch(self, set_to=None):
+        """Test hook: the persistent MLP stack's launch epoch (returned before
+        an optional set; synchronizes)."""
+        v = ctypes.c_uint()
+        st = ctypes.byref(ctypes.c_uint(set_to)) if set_to is not None else None
+        self.check(lib().qw_mlp_stack_epoch(self._h, st, ctypes.byref(v)))
         return v.value
 
     def close(self):
@@ -522,6 +532,14 @@ class Chain:
 
     def launch(self, stream=None):
         self.ctx.check(lib().qw_chain_launch(self._h, _stream(stream)))
+
+    def epoch(self, set_to=None):
+        """Test hook: the chain's launch epoch (returned before an optional
+        set; synchronizes)."""
+        v = ctypes.c_uint()
+        st = ctypes.byref(ctypes.c_uint(set_to)) if set_to is not None else None
+        self.ctx.check(lib().qw_chain_epoch(self._h, st, ctypes.byref(v)))
+        return v.value
 
     def close(self):
         if self._h:

@@ -207,3 +207,36 @@ def test_chain_rejects_bad_plans(qw, ctx, oracle):
             qw.Chain(ctx, qw.F16, 1, slots, ops)
     with pytest.raises(qw.QwError):  # BF16 slots for INT8 weights
         qw.Chain(ctx, qw.BF16, 1, slots, [{"w": w["in"], "in": 0, "out": 1}])
+
+
+def test_chain_epoch_wrap(qw, ctx, oracle):
+    """The tag keeps 22 bits of the launch epoch.  Launches run across the
+    wrap (epoch set just below it through the test hook): the epoch skips the
+    field value 0, the launch at which the field returns to 1 clears every
+    slot word behind a grid barrier, and every launch equals the first one."""
+    fmt, M = "int8", 2
+    layers = _layers(oracle, fmt, 2, 4400)
+    ws = [_pack(qw, ctx, fmt, L) for L in layers]
+    xt = dev(oracle.normal((M, 1024), 4401), torch.float16)
+    xout = torch.zeros(M, 1024, device="cuda", dtype=torch.float16)
+    bigout = torch.zeros(M, 8192, device="cuda", dtype=torch.float16)
+    ch = _build(qw, ctx, fmt, layers, ws, xt, xout, bigout, M)
+    ch.launch()
+    torch.cuda.synchronize()
+    first = xout.clone()
+    wrap = 1 << 22
+    ch.epoch(set_to=wrap - 2)
+    seen = []
+    for _ in range(4):
+        xout.zero_()
+        seen.append(ch.epoch())
+        ch.launch()
+        torch.cuda.synchronize()
+        assert torch.equal(xout, first)
+    seen.append(ch.epoch())
+    # wrap - 2, wrap - 1, (wrap skipped: field 0) wrap + 1 = the clearing launch, wrap + 2, ...
+    assert seen == [wrap - 2, wrap - 1, wrap + 1, wrap + 2, wrap + 3]
+    with pytest.raises(qw.QwError):
+        ch.epoch(set_to=wrap)
+    assert ctx.device_error() == 0
+    ch.close()

@@ -20,8 +20,10 @@ reference itself decides.  Planted exact ties (identical rows) straddle
 lowest index; a unique maximum is planted in the last row (248319).
 
 Config 4: each projection of the 24-layer prefill stack at M = 16384 on the
-default route (256x256 blocks, RMSNorm prologue through the workspace,
-residual epilogues), against FP64 on a sample of 320 tokens (every output
+default route (the direct-A GEMM, qw_gemm_da.hip: 8-wave blocks of 512
+weight rows x 128 tokens, as every projection at this M makes at least one
+such block per CU; RMSNorm prologue through the workspace, residual
+epilogues), against FP64 on a sample of 320 tokens (every output
 row), plus bitwise repeatability of a second run.  Reference: the batch
 GemmEx / SGEMM call sites bf16_gemm.cuh:89, full_attention_cuda.cu:708-714
 and the prefill stack cuda_engine.cu:391-479.

@@ -2,11 +2,16 @@
 persistent launch) against L calls of qw_mlp_fused and against the oracle's
 FP64 block composition.
 
-Bars: BF16 weights <= 1e-2 normwise vs FP64 on the BF16-rounded weights
-with x rounded to BF16 after every block, and vs L qw_mlp_fused calls (the
-same math with the gate/up K slices summed in another grouping, which moves
-a BF16 rounding of the hidden state now and then); INT8 weights <= 1e-3 vs the dequant-then-matmul composition on
-the same q, s and F16 roundings.  Every launch must leave the device error
+Bars: BF16 weights, one block: <= 1e-2 normwise vs FP64 on the BF16-rounded
+weights; L blocks with x rounded to BF16 after every block: every block
+<= 1e-2 against FP64 on its own input (teacher forcing), and end to end
+<= 1e-2 + 2 e_ref vs the FP64 composition, e_ref being the distance of the
+reference's own BF16 chain (BF16-in / BF16-out GEMVs) on the same inputs
+(test_mlp_stack_bench_configs states why); vs L qw_mlp_fused calls <= 1e-2
+(the same math with the gate/up K slices summed in another grouping, which
+moves a BF16 rounding of the hidden state now and then).  INT8 weights
+<= 1e-3 vs the dequant-then-matmul composition on the same q, s and F16
+roundings.  Every launch must leave the device error
 flag clear.
 """
 import numpy as np
@@ -48,6 +53,32 @@ def _ref_bf16(oracle, layers, x):
     return x
 
 
+def _ref_bf16_block(oracle, G, U, D, gam, x):
+    """One MLP block as the reference's BF16 path computes it: every GEMV a
+    cublasGemmEx with BF16 operands and BF16 output, FP32 accumulation
+    (bf16_gemv / bf16_gemv_add, bf16_gemm.cuh:82-120): the normalized input,
+    gate, up, h and the new hidden state each rounded to BF16."""
+    x = np.asarray(x, np.float32)
+    inv = (1.0 / np.sqrt((x.astype(np.float64) ** 2).mean(axis=1, keepdims=True) + 1e-6)).astype(np.float32)
+    xn = oracle.round_bf16(x * inv * (1.0 + np.asarray(gam, np.float32))[None, :])
+    g = oracle.round_bf16(xn @ G.T)
+    u = oracle.round_bf16(xn @ U.T)
+    h = oracle.round_bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+    return oracle.round_bf16((h @ D.T + x).astype(np.float32))
+
+
+def _chain_bar(oracle, layers, x, ref64):
+    """The multi-block BF16 bar: 1e-2 + 2 e_ref, e_ref = the distance from the
+    FP64 composition `ref64` of the reference's own BF16 chain on the same
+    inputs (_ref_bf16_block composed over the layers); see
+    test_mlp_stack_bench_configs for why."""
+    x = np.asarray(x, np.float32)
+    for G, U, D, gam in layers:
+        x = _ref_bf16_block(oracle, oracle.round_bf16(G), oracle.round_bf16(U), oracle.round_bf16(D), gam, x)
+    den = np.abs(ref64).max()
+    return 1e-2 + 2.0 * float(np.abs(x - ref64).max() / den)
+
+
 @pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
 @pytest.mark.parametrize("L", [1, 5])
 def test_mlp_stack_bf16(qw, ctx, oracle, relerr, M, L):
@@ -65,33 +96,29 @@ def test_mlp_stack_bf16(qw, ctx, oracle, relerr, M, L):
     torch.cuda.synchronize()
     assert ctx.device_error() == 0
     ref = _ref_bf16(oracle, layers, host(x0))
-    # BF16 hidden state rounded after every block: against FP64 both the stack
-    # and the per-block launches drift toward the 1e-2 bar over 5 blocks
-    # (measured up to 1.4e-2 for both, identical); the stack is held to the
-    # per-block launches' error plus one rounding step
+    # the multi-block bar (1e-2 for one block)
     e_stack, e_blocks = relerr(host(y), ref), relerr(host(z), ref)
-    print("first launch rel err: stack", e_stack, "per-block", e_blocks)
-    assert e_stack <= max(1e-2, 1.34 * e_blocks + 2e-3)
+    bar = _chain_bar(oracle, layers, host(x0), ref)
+    print("first launch rel err: stack", e_stack, "per-block", e_blocks, "bar", bar)
+    assert e_stack <= bar and e_blocks <= bar
     # same math as the per-block launches; the K slices of the gate/up
     # reduction are summed in another grouping, which moves a BF16 rounding of
     # the hidden state now and then
     assert relerr(host(y), host(z).astype(np.float64)) <= 1e-2
     # a second launch on other inputs (new epoch tags), in place
     x1 = dev(oracle.normal((M, H), 2299 + M), torch.bfloat16)
-    r1 = _ref_bf16(oracle, layers, host(x1))
+    x1h = host(x1)
+    r1 = _ref_bf16(oracle, layers, x1h)
     z1 = x1.clone()
     qw.mlp_stack(ctx, gu, dn, x1, x1, gammas=gms)
     for l in range(L):
         qw.mlp_fused(ctx, gu[l], dn[l], z1, z1, gamma=gms[l], residual=z1)
     torch.cuda.synchronize()
     assert ctx.device_error() == 0
-    # the BF16 hidden state is rounded after every block, so over 5 blocks the
-    # stack and the per-block launches each sit near the 1e-2 BF16 bar against
-    # FP64; the stack may not be worse than the per-block launches by more
-    # than one BF16 rounding step
     e_stack, e_blocks = relerr(host(x1), r1), relerr(host(z1), r1)
-    print("second launch rel err: stack", e_stack, "per-block", e_blocks)
-    assert e_stack <= max(1e-2, 1.34 * e_blocks + 2e-3)
+    bar = _chain_bar(oracle, layers, x1h, r1)
+    print("second launch rel err: stack", e_stack, "per-block", e_blocks, "bar", bar)
+    assert e_stack <= bar and e_blocks <= bar
     assert relerr(host(x1), host(z1).astype(np.float64)) <= 1e-2
 
 
@@ -120,12 +147,16 @@ def test_mlp_stack_bf16_folded_norm_24_layers(qw, ctx, oracle, relerr):
         Uf = oracle.round_bf16(oracle.round_bf16(U) * (1.0 + gam)[None, :].astype(np.float32))
         yb = oracle.mlp_block_f64(Gf, Uf, oracle.round_bf16(D), np.zeros(H, np.float32), x.astype(np.float32))
         x = oracle.round_bf16(yb.astype(np.float32)).astype(np.float64)
-    # 24 BF16 roundings of the hidden state compound: the bar is the one-block
-    # bar per ~8 blocks, and the persistent launch may not be worse than the
-    # per-block launches by more than a third
+    # the multi-block bar, on the folded weights
+    xf = host(x0)
+    for G, U, D, gam in layers:
+        Gf = oracle.round_bf16(oracle.round_bf16(G) * (1.0 + gam)[None, :].astype(np.float32))
+        Uf = oracle.round_bf16(oracle.round_bf16(U) * (1.0 + gam)[None, :].astype(np.float32))
+        xf = _ref_bf16_block(oracle, Gf, Uf, oracle.round_bf16(D), np.zeros(H, np.float32), xf)
+    bar = 1e-2 + 2.0 * relerr(xf, x)
     e_stack, e_blocks = relerr(host(y), x), relerr(host(z), x)
-    print("24-layer rel err: stack", e_stack, "per-block", e_blocks)
-    assert e_stack <= 3e-2 and e_stack <= 1.34 * e_blocks + 2e-3
+    print("24-layer rel err: stack", e_stack, "per-block", e_blocks, "bar", bar)
+    assert e_stack <= bar and e_blocks <= bar
 
 
 @pytest.mark.parametrize("M", [1, 2, 8])
@@ -214,3 +245,143 @@ def test_mlp_stack_fallback_more_tokens(qw, ctx, oracle, relerr):
         qw.mlp_fused(ctx, gu[l], dn[l], z, z, gamma=gms[l], residual=z)
     torch.cuda.synchronize()
     assert torch.equal(y, z)
+
+
+def test_mlp_stack_epoch_wrap_varying_m(qw, ctx, oracle):
+    """The tag keeps 26 bits of the launch epoch.  A launch with 8 tokens
+    leaves words of tokens 1..7 behind; launches with 1 token then run up to
+    the wrap (epoch set just below it through the test hook), where the
+    launch whose field is 0 clears every word behind a grid barrier; an
+    8-token launch at the first launch's field value then equals the same
+    launch at a fresh epoch (stale words would have matched its tags)."""
+    L = 3
+    layers = _layers(oracle, L, 3100)
+    gu = [qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16) for G, U, _, _ in layers]
+    dn = [qw.Weight.pack(ctx, D, qw.WFMT_BF16) for _, _, D, _ in layers]
+    gms = [dev(gam) for *_, gam in layers]
+    xa = dev(oracle.normal((8, H), 3190), torch.bfloat16)
+    xb = dev(oracle.normal((8, H), 3191), torch.bfloat16)
+    x1 = dev(oracle.normal((1, H), 3192), torch.bfloat16)
+
+    def run(x):
+        y = torch.empty_like(x)
+        qw.mlp_stack(ctx, gu, dn, x, y, gammas=gms)
+        torch.cuda.synchronize()
+        return y
+
+    ref_b, ref_1 = run(xb), run(x1)
+    f = 1 << 26
+    ctx.stack_epoch(set_to=2 * f + 5)
+    run(xa)                               # field 5: tokens 0..7, both parities
+    ctx.stack_epoch(set_to=3 * f - 2)
+    seen = []
+    for _ in range(3):                    # fields f-2, f-1 and 0 (the clearing launch)
+        seen.append(ctx.stack_epoch())
+        assert torch.equal(run(x1), ref_1)
+    assert seen == [3 * f - 2, 3 * f - 1, 3 * f]
+    assert ctx.stack_epoch() == 3 * f + 1
+    ctx.stack_epoch(set_to=3 * f + 5)     # field 5 again, as the 8-token launch above
+    assert torch.equal(run(xb), ref_b)
+    assert ctx.device_error() == 0
+
+
+_BENCH_LAYERS = {}
+
+
+def _bench_layers(oracle):
+    """24 layers shaped as bench.py's: BF16-rounded N(0, 0.02) weights, a
+    per-layer RMSNorm weight N(0, 0.02) (the norm scales by 1 + w)."""
+    if not _BENCH_LAYERS:
+        out = []
+        for l in range(24):
+            G, U, D = (oracle.round_bf16(oracle.normal(s, 3300 + 10 * l + i, 0.0, 0.02))
+                       for i, s in enumerate([(I, H), (I, H), (H, I)]))
+            out.append((G, U, D, oracle.normal((H,), 3303 + 10 * l, 0.0, 0.02)))
+        _BENCH_LAYERS["v"] = out
+    return _BENCH_LAYERS["v"]
+
+
+@pytest.mark.parametrize("route", ["headline_M1_gamma", "cfg2_M8_folded"])
+def test_mlp_stack_bench_configs(qw, ctx, oracle, relerr, route):
+    """The two configurations bench.py times on the persistent stack, exactly:
+    24 BF16 blocks in one launch replayed from a graph in place, M = 1 with a
+    per-call gamma (the headline) and M = 8 with gamma folded into gate/up
+    (configs[1] at M = 8).
+
+    Bars (the multi-block bar of the parity contract):
+      * every block, against FP64 of that block on the kernel's own BF16 input
+        (teacher forcing): <= 1e-2, the per-call BF16 bar.  The input of
+        block l is the output of the launch of the first l - 1 blocks: a
+        block's arithmetic does not depend on L, so prefixes are bit-identical
+        to the 24-block launch's intermediate states (checked at the end);
+      * end to end, against the FP64 composition with the hidden state rounded
+        to BF16 after every block: <= 1e-2 + 2 e_ref, where e_ref is how far the
+        reference's own BF16 chain (every GEMV a BF16-in / BF16-out GemmEx with
+        FP32 accumulation, bf16_gemm.cuh:82-120, composed over the same blocks,
+        _ref_bf16_block) lands from that FP64 composition on the same inputs.
+        Once a summation-order difference flips one BF16 rounding of the
+        hidden state, the residual path carries that unit to the end, so no
+        FP32-accumulating chain reproduces the FP64 one closer than such flips
+        add up to; the kernel's flips are independent of the reference's, so
+        its distance may be up to twice e_ref, plus the one-block bar."""
+    M, folded = (1, False) if route == "headline_M1_gamma" else (8, True)
+    layers = _bench_layers(oracle)
+    L = len(layers)
+    gu, dn, gms, ref_w = [], [], [], []
+    for G, U, D, gam in layers:
+        w = qw.Weight.pack_glu(ctx, G, U, qw.WFMT_BF16)
+        if folded:
+            w.fold_norm(dev(gam))
+            fold = (1.0 + gam)[None, :].astype(np.float32)
+            ref_w.append((oracle.round_bf16(G * fold), oracle.round_bf16(U * fold), D, np.zeros(H, np.float32)))
+        else:
+            gms.append(dev(gam))
+            ref_w.append((G, U, D, gam))
+        gu.append(w)
+        dn.append(qw.Weight.pack(ctx, D, qw.WFMT_BF16))
+    x0 = dev(oracle.normal((M, H), 3399 + M), torch.bfloat16)
+
+    def stack(n, x, y, stream=None):
+        qw.mlp_stack(ctx, gu[:n], dn[:n], x, y, gammas=(gms[:n] if gms else None), stream=stream)
+
+    # teacher-forced per-block bar on every block
+    prev = host(x0)
+    ys = []
+    for n in range(1, L + 1):
+        y = torch.empty_like(x0)
+        stack(n, x0, y)
+        torch.cuda.synchronize()
+        ys.append(host(y))
+        G, U, D, gam = ref_w[n - 1]
+        e = relerr(ys[-1], oracle.mlp_block_f64(G, U, D, gam, prev))
+        assert e <= 1e-2, f"block {n}: {e}"
+        prev = ys[-1]
+    assert ctx.device_error() == 0
+
+    # the bench form: the 24-block launch captured once, replayed in place
+    buf = x0.clone()
+    stream = torch.cuda.Stream()
+    g = qw.Graph(ctx, stream)
+    with torch.cuda.stream(stream):
+        stream.synchronize()
+        with g:
+            stack(L, buf, buf, stream=stream)
+    for _ in range(3):
+        buf.copy_(x0)
+        torch.cuda.synchronize()
+        g.launch(stream)
+        stream.synchronize()
+        assert np.array_equal(host(buf), ys[-1])
+    assert ctx.device_error() == 0
+
+    # end-to-end bar against the FP64 composition
+    x64 = host(x0).astype(np.float64)
+    xr = host(x0)
+    for G, U, D, gam in ref_w:
+        x64 = oracle.round_bf16(oracle.mlp_block_f64(G, U, D, gam, x64.astype(np.float32)).astype(np.float32))
+        x64 = x64.astype(np.float64)
+        xr = _ref_bf16_block(oracle, G, U, D, gam, xr)
+    e_ref = relerr(xr, x64)
+    e = relerr(ys[-1], x64)
+    print(f"{route}: 24-block rel err {e:.3e}; reference BF16 chain {e_ref:.3e}")
+    assert e <= 1e-2 + 2.0 * e_ref

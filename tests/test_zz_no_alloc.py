@@ -42,3 +42,34 @@ def test_noalloc_rejects_beyond_max(qw, ctx, oracle):
     with pytest.raises(qw.QwError) as e:
         qw.lmhead_argmax_noalloc(w, h, ids)
     assert e.value.status == qw.ERR_SHAPE
+
+
+@pytest.mark.parametrize("M", [1, 64])
+def test_noalloc_graph_replays(qw, ctx, oracle, M):
+    """Captured once in a graph (the use the entry point exists for) and
+    replayed with new activations copied in between, eager work of the
+    program between the replays: every replay's ids and winning logits equal
+    an eager qw_lmhead_argmax on the same activations."""
+    V, K = 30000, 1024
+    w = qw.Weight.pack(ctx, oracle.normal((V, K), 1520, 0.0, 0.02), qw.WFMT_BF16)
+    h = torch.zeros(M, K, device="cuda", dtype=torch.bfloat16)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    mx = torch.empty(M, device="cuda")
+    stream = torch.cuda.Stream()
+    g = qw.Graph(ctx, stream)
+    with torch.cuda.stream(stream):
+        stream.synchronize()
+        with g:
+            qw.lmhead_argmax_noalloc(w, h, ids, mx, stream=stream)
+    for rep in range(4):
+        hv = torch.from_numpy(oracle.normal((M, K), 1530 + rep)).cuda().to(torch.bfloat16)
+        h.copy_(hv)
+        torch.cuda.synchronize()
+        g.launch(stream)
+        stream.synchronize()
+        ids_e = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+        mx_e = torch.empty(M, device="cuda")
+        qw.lmhead_argmax(ctx, w, hv, ids_e, mx_e)
+        torch.cuda.synchronize()
+        assert torch.equal(ids, ids_e), rep
+        assert torch.equal(mx, mx_e), rep
