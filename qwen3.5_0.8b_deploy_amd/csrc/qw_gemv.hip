@@ -373,7 +373,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         // before this workgroup's completion count
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         old = __shfl(old, 0);
         if (old == gridDim.x - 1) {
             for (int mm = lane; mm < ain.M; mm += 64) {

@@ -117,6 +117,7 @@ struct WideArgmaxArgs {
     int n_tiles, n_blk;        // 16-row tiles, 32-row blocks
     int ksteps;
     int T, Mg, CT;             // token groups of Mg tokens, CT 16-token tiles each
+    int nw;                    // waves per workgroup (4 or 8; 0: the plan chooses)
     unsigned long long* keys;  // [M] (self-resetting)
     unsigned* done;            // completion counter (self-resetting)
     int32_t* ids;

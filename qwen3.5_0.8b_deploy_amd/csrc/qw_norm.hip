@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* logits, in
         if (b) __hip_atomic_fetch_max(&keys[m], b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         const unsigned total = gridDim.x * gridDim.y;
-        const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = (old == total - 1) ? 1 : 0;
     }
     __syncthreads();

@@ -516,11 +516,11 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
 // ---------------------------------------------------------------------------
 constexpr int kArgU = 8;  // k-steps per chunk
 
-constexpr int kArgNW = 4;  // waves per workgroup (eight measured slower: 92 vs 86 us BF16 at 32 tokens)
+constexpr int kArgNW = 4;  // waves per workgroup at up to 32 tokens per group (eight measured slower: 92 vs 86 us BF16 at 32 tokens)
 
-template <int WF, int XDT, int CT>
-__global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs a) {
-    constexpr int NW = kArgNW, RT = 2, U = kArgU;
+template <int WF, int XDT, int CT, int NW>
+__global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) {
+    constexpr int RT = 2, U = kArgU;
     constexpr int KS = WideT<WF>::KS, XU = WideT<WF>::XU, KEW = WideT<WF>::KEW;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ unsigned long long kbest[NW][CT * 16];
@@ -599,9 +599,18 @@ __global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs
 
     f32x4 acc[RT][CT];
     f32x4 sc[RT];
+    // per token tile: this lane's running maximum and its row.  A lane visits
+    // its rows in increasing order, so the strict compare keeps the lowest
+    // row of a tie; the keys are formed once, at the end.
+    float bv[CT];
+    uint32_t bi[CT];
     unsigned long long best[CT];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) best[ct] = 0ull;
+    for (int ct = 0; ct < CT; ++ct) {
+        bv[ct] = -__builtin_inff();
+        bi[ct] = 0xffffffffu;
+        best[ct] = 0ull;
+    }
     auto body = [&](int s, auto& A, auto& S) {
         if (s >= nseq) return;
         const int c = s % nch;
@@ -645,23 +654,36 @@ __global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs
                 }
             }
         }
-        if (c == nch - 1) {  // the block's logits: into the running keys
+        if (c == nch - 1) {  // the block's logits: into the running maxima
             const int blk = gw + (s / nch) * stride;
+            const int row0 = blk * 32 + g * 4;
+            if (blk * 32 + 32 <= a.V) {  // every row of the block is a vocabulary row
 #pragma unroll
-            for (int ct = 0; ct < CT; ++ct) {
-                if (ct * 16 + r >= Mt) continue;
+                for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    const f32x4 v = acc[rt][ct] * sc[rt];
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const f32x4 v = acc[rt][ct] * sc[rt];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int row = blk * 32 + rt * 16 + g * 4 + e;
-                        if (row < a.V) {
-                            const unsigned long long kk = argmax_key(v[e], (uint32_t)row);
-                            best[ct] = kk > best[ct] ? kk : best[ct];
+                        for (int e = 0; e < 4; ++e) {
+                            const bool gt = v[e] > bv[ct];
+                            bv[ct] = gt ? v[e] : bv[ct];
+                            bi[ct] = gt ? (uint32_t)(row0 + rt * 16 + e) : bi[ct];
                         }
                     }
-                }
+            } else {
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const f32x4 v = acc[rt][ct] * sc[rt];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int row = row0 + rt * 16 + e;
+                            const bool gt = row < a.V && v[e] > bv[ct];
+                            bv[ct] = gt ? v[e] : bv[ct];
+                            bi[ct] = gt ? (uint32_t)row : bi[ct];
+                        }
+                    }
             }
         }
     };
@@ -673,6 +695,9 @@ __global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs
     }
 
     // ---- keys: the four row groups of a lane's token, the waves, the grid ----
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+        if (bi[ct] != 0xffffffffu && ct * 16 + r < Mt) best[ct] = argmax_key(bv[ct], bi[ct]);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
 #pragma unroll
@@ -689,14 +714,17 @@ __global__ __launch_bounds__(kArgNW * 64) void wide_argmax_kernel(WideArgmaxArgs
         for (int w = 1; w < NW; ++w) k = kbest[w][threadIdx.x] > k ? kbest[w][threadIdx.x] : k;
         if (k != 0ull) __hip_atomic_fetch_max(&a.keys[M0 + threadIdx.x], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // the key updates are device-scope read-modify-writes, complete before
-    // the completion count; the count is an acquire-release RMW, so the last
-    // workgroup's key exchanges are ordered after every workgroup's updates
+    // the key updates are device-scope read-modify-writes, performed at the
+    // memory side (past the per-XCD L2s) and complete before the completion
+    // count is issued; the last workgroup's exchanges are device-scope RMWs
+    // too, so they see every update without a cache maintenance fence (an
+    // acquire-release count, whose L2 write-back and invalidate run in every
+    // workgroup, measured 45 -> 70 us on the INT8 lm_head at one token)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __shared__ unsigned last;
     if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = old == gridDim.x - 1 ? 1u : 0u;
     }
     __syncthreads();
@@ -876,6 +904,12 @@ bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs
     a.Mg = Mg;
     a.CT = CT;
     a.ksteps = ks;
+    // waves per workgroup: 64-token groups fill the LDS (one workgroup per
+    // CU); with INT8 weights 8 waves give each SIMD two, to overlap one's
+    // MFMAs with the other's conversions and LDS reads (128 tokens: 110 ->
+    // 93 us); BF16 weights measured better with 4 (128 -> 145 us with 8).
+    // Smaller groups run two 4-wave workgroups per CU
+    if (a.nw == 0) a.nw = CT == 4 && wf == WF_I8 ? 8 : 4;
     return true;
 }
 
@@ -883,14 +917,21 @@ hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid
     auto go = [&](auto kern) {
         hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(kern), (int)kWideMaxLds);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kArgNW * 64), smem, stream, a);
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(a.nw * 64), smem, stream, a);
         return hipGetLastError();
     };
-    if (wf == WF_BF16) return a.CT == 2 ? go(wide_argmax_kernel<WF_BF16, DT_BF16, 2>)
-                                        : go(wide_argmax_kernel<WF_BF16, DT_BF16, 4>);
-    if (xdt == DT_BF16)
-        return a.CT == 2 ? go(wide_argmax_kernel<WF_I8, DT_BF16, 2>) : go(wide_argmax_kernel<WF_I8, DT_BF16, 4>);
-    return a.CT == 2 ? go(wide_argmax_kernel<WF_I8, DT_F16, 2>) : go(wide_argmax_kernel<WF_I8, DT_F16, 4>);
+    const bool w8 = a.nw == 8;
+    if (a.nw != 4 && a.nw != 8) return hipErrorInvalidValue;
+    if (wf == WF_BF16) {
+        if (a.CT == 2) return w8 ? go(wide_argmax_kernel<WF_BF16, DT_BF16, 2, 8>) : go(wide_argmax_kernel<WF_BF16, DT_BF16, 2, 4>);
+        return w8 ? go(wide_argmax_kernel<WF_BF16, DT_BF16, 4, 8>) : go(wide_argmax_kernel<WF_BF16, DT_BF16, 4, 4>);
+    }
+    if (xdt == DT_BF16) {
+        if (a.CT == 2) return w8 ? go(wide_argmax_kernel<WF_I8, DT_BF16, 2, 8>) : go(wide_argmax_kernel<WF_I8, DT_BF16, 2, 4>);
+        return w8 ? go(wide_argmax_kernel<WF_I8, DT_BF16, 4, 8>) : go(wide_argmax_kernel<WF_I8, DT_BF16, 4, 4>);
+    }
+    if (a.CT == 2) return w8 ? go(wide_argmax_kernel<WF_I8, DT_F16, 2, 8>) : go(wide_argmax_kernel<WF_I8, DT_F16, 2, 4>);
+    return w8 ? go(wide_argmax_kernel<WF_I8, DT_F16, 4, 8>) : go(wide_argmax_kernel<WF_I8, DT_F16, 4, 4>);
 }
 
 hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream) {
