@@ -118,6 +118,7 @@ struct WideArgmaxArgs {
     int ksteps;
     int T, Mg, CT;             // token groups of Mg tokens, CT 16-token tiles each
     int nw;                    // waves per workgroup (4 or 8; 0: the plan chooses)
+    int wcache;                // weight loads: 1 default cache policy, 0 non-temporal, -1 the plan chooses
     unsigned long long* keys;  // [M] (self-resetting)
     unsigned* done;            // completion counter (self-resetting)
     int32_t* ids;

@@ -518,7 +518,7 @@ constexpr int kArgU = 8;  // k-steps per chunk
 
 constexpr int kArgNW = 4;  // waves per workgroup at up to 32 tokens per group (eight measured slower: 92 vs 86 us BF16 at 32 tokens)
 
-template <int WF, int XDT, int CT, int NW>
+template <int WF, int XDT, int CT, int NW, int WAUX>
 __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) {
     constexpr int RT = 2, U = kArgU;
     constexpr int KS = WideT<WF>::KS, XU = WideT<WF>::XU, KEW = WideT<WF>::KEW;
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
                 A[u][rt] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                wrs, tok ? (uint32_t)pt * tile_bytes + (uint32_t)(c * U + u) * 1024u + lane * 16 : OOB, 0,
-                               AUX_NT));
+                               WAUX));
             S[rt] = __builtin_bit_cast(
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, tok && c == 0 ? (uint32_t)((pt * 16 + g * 4) * 4) : OOB,
                                                              0, 0));
@@ -910,6 +910,7 @@ bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs
     // 93 us); BF16 weights measured better with 4 (128 -> 145 us with 8).
     // Smaller groups run two 4-wave workgroups per CU
     if (a.nw == 0) a.nw = CT == 4 && wf == WF_I8 ? 8 : 4;
+    if (a.wcache < 0) a.wcache = T > 1 ? 1 : 0;
     return true;
 }
 
@@ -920,18 +921,21 @@ hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid
         hipLaunchKernelGGL(kern, dim3(grid), dim3(a.nw * 64), smem, stream, a);
         return hipGetLastError();
     };
-    const bool w8 = a.nw == 8;
     if (a.nw != 4 && a.nw != 8) return hipErrorInvalidValue;
-    if (wf == WF_BF16) {
-        if (a.CT == 2) return w8 ? go(wide_argmax_kernel<WF_BF16, DT_BF16, 2, 8>) : go(wide_argmax_kernel<WF_BF16, DT_BF16, 2, 4>);
-        return w8 ? go(wide_argmax_kernel<WF_BF16, DT_BF16, 4, 8>) : go(wide_argmax_kernel<WF_BF16, DT_BF16, 4, 4>);
-    }
-    if (xdt == DT_BF16) {
-        if (a.CT == 2) return w8 ? go(wide_argmax_kernel<WF_I8, DT_BF16, 2, 8>) : go(wide_argmax_kernel<WF_I8, DT_BF16, 2, 4>);
-        return w8 ? go(wide_argmax_kernel<WF_I8, DT_BF16, 4, 8>) : go(wide_argmax_kernel<WF_I8, DT_BF16, 4, 4>);
-    }
-    if (a.CT == 2) return w8 ? go(wide_argmax_kernel<WF_I8, DT_F16, 2, 8>) : go(wide_argmax_kernel<WF_I8, DT_F16, 2, 4>);
-    return w8 ? go(wide_argmax_kernel<WF_I8, DT_F16, 4, 8>) : go(wide_argmax_kernel<WF_I8, DT_F16, 4, 4>);
+    // 16-token-tile pairs run one token group (weights streamed once,
+    // non-temporal); 64-token groups may be several, whose later groups read
+    // the weights from L2 if the loads keep the default cache policy
+    auto pick = [&](auto wfc, auto xdtc) {
+        constexpr int W = decltype(wfc)::value, X = decltype(xdtc)::value;
+        if (a.CT == 2) return a.nw == 8 ? go(wide_argmax_kernel<W, X, 2, 8, AUX_NT>) : go(wide_argmax_kernel<W, X, 2, 4, AUX_NT>);
+        if (a.wcache)
+            return a.nw == 8 ? go(wide_argmax_kernel<W, X, 4, 8, 0>) : go(wide_argmax_kernel<W, X, 4, 4, 0>);
+        return a.nw == 8 ? go(wide_argmax_kernel<W, X, 4, 8, AUX_NT>) : go(wide_argmax_kernel<W, X, 4, 4, AUX_NT>);
+    };
+    using I = std::integral_constant<int, WF_I8>;
+    if (wf == WF_BF16) return pick(std::integral_constant<int, WF_BF16>{}, std::integral_constant<int, DT_BF16>{});
+    if (xdt == DT_BF16) return pick(I{}, std::integral_constant<int, DT_BF16>{});
+    return pick(I{}, std::integral_constant<int, DT_F16>{});
 }
 
 hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream) {
