@@ -518,9 +518,9 @@ constexpr int kArgU = 8;  // k-steps per chunk
 
 constexpr int kArgNW = 4;  // waves per workgroup at up to 32 tokens per group (eight measured slower: 92 vs 86 us BF16 at 32 tokens)
 
-template <int WF, int XDT, int CT, int NW, int WAUX>
+template <int WF, int XDT, int CT, int NW, int WAUX, int U = kArgU, int NCH = 2>
 __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) {
-    constexpr int RT = 2, U = kArgU;
+    constexpr int RT = 2;
     constexpr int KS = WideT<WF>::KS, XU = WideT<WF>::XU, KEW = WideT<WF>::KEW;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ unsigned long long kbest[NW][CT * 16];
@@ -557,33 +557,35 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_tiles * tile_bytes));
     const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.scales ? (const void*)a.scales : a.x,
                                                  a.scales ? (uint32_t)a.n_tiles * 64u : 0u);
-    u32x4 A0[U][RT], A1[U][RT];
-    u32x4 S0[RT], S1[RT];
-    // chunk s of this wave: block gw + (s / nch) * stride, k-steps from (s % nch) * U;
-    // the row scales come with a block's first chunk
-    auto issue = [&](int s, auto& A, auto& S) {
-        const int blk = gw + (s / nch) * stride;
-        const int c = s % nch;
-        const bool ok = s < nseq;
+    u32x4 AR[NCH][U][RT];  // a ring of NCH chunks in flight
+    u32x4 SR[NCH][RT];
+    // The wave's chunks in order: block gw + i * stride, k-steps from c * U
+    // (c < nch), walked by a cursor (no division).  Loads are unconditional
+    // and branch-free: blocks past the end lie beyond the descriptors' ranges
+    // and read zeros, so every chunk issues the same loads and the compiler
+    // waits for exactly the chunk a body consumes.  The row scales come with
+    // every chunk (one 16-byte load per tile, used at a block's first chunk).
+    int ib = gw, ic = 0;  // issue cursor
+    auto issue = [&](auto& A, auto& S) {
+        const uint32_t kb = (uint32_t)ic * U * 1024u + lane * 16;
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            const int pt = 2 * blk + rt;
-            const bool tok = ok && pt < a.n_tiles;
+            const uint32_t pt = 2u * (uint32_t)ib + rt;
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 A[u][rt] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               wrs, tok ? (uint32_t)pt * tile_bytes + (uint32_t)(c * U + u) * 1024u + lane * 16 : OOB, 0,
-                               WAUX));
-            S[rt] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, tok && c == 0 ? (uint32_t)((pt * 16 + g * 4) * 4) : OOB,
-                                                             0, 0));
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, pt * tile_bytes + kb + (uint32_t)u * 1024u, 0, WAUX));
+            S[rt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (pt * 16 + g * 4) * 4, 0, 0));
+        }
+        if (++ic == nch) {
+            ic = 0;
+            ib += stride;
         }
     };
-    issue(0, A0, S0);
-    issue(1, A1, S1);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) issue(AR[c], SR[c]);
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(vm_wait(2 * RT * (U + 1)));  // the activations have landed
+    __builtin_amdgcn_s_waitcnt(vm_wait(NCH * RT * (U + 1)));  // the activations have landed
     __syncthreads();
     if constexpr (WF == WF_I8 && XDT == DT_BF16) {
         // BF16 activations for the f16 MFMA of INT8 weights: converted once in
@@ -611,9 +613,13 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
         bi[ct] = 0xffffffffu;
         best[ct] = 0ull;
     }
+    int bb = gw, bc = 0;  // body cursor
     auto body = [&](int s, auto& A, auto& S) {
-        if (s >= nseq) return;
-        const int c = s % nch;
+        const int c = bc, blk = bb;
+        if (++bc == nch) {
+            bc = 0;
+            bb += stride;
+        }
         if (a.dbg & 1) {  // timing probe: the weight stream alone
             if (c == nch - 1) best[0] = max(best[0], (unsigned long long)A[0][0][0] + A[U - 1][1][3]);
             return;
@@ -654,8 +660,7 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
                 }
             }
         }
-        if (c == nch - 1) {  // the block's logits: into the running maxima
-            const int blk = gw + (s / nch) * stride;
+        if (c == nch - 1 && s < nseq) {  // the block's logits: into the running maxima
             const int row0 = blk * 32 + g * 4;
             if (blk * 32 + 32 <= a.V) {  // every row of the block is a vocabulary row
 #pragma unroll
@@ -687,11 +692,12 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
             }
         }
     };
-    for (int s = 0; s < nseq; s += 2) {
-        body(s, A0, S0);
-        issue(s + 2, A0, S0);
-        body(s + 1, A1, S1);
-        issue(s + 3, A1, S1);
+    for (int s = 0; s < nseq; s += NCH) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            body(s + c, AR[c], SR[c]);  // past nseq: zeros, no key update
+            issue(AR[c], SR[c]);
+        }
     }
 
     // ---- keys: the four row groups of a lane's token, the waves, the grid ----
@@ -909,6 +915,7 @@ bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs
     // MFMAs with the other's conversions and LDS reads (128 tokens: 110 ->
     // 93 us); BF16 weights measured better with 4 (128 -> 145 us with 8).
     // Smaller groups run two 4-wave workgroups per CU
+    if (a.nw == 16 && CT != 4) a.nw = 0;  // 16 waves only for 64-token groups
     if (a.nw == 0) a.nw = CT == 4 && wf == WF_I8 ? 8 : 4;
     if (a.wcache < 0) a.wcache = T > 1 ? 1 : 0;
     return true;
@@ -921,15 +928,21 @@ hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid
         hipLaunchKernelGGL(kern, dim3(grid), dim3(a.nw * 64), smem, stream, a);
         return hipGetLastError();
     };
-    if (a.nw != 4 && a.nw != 8) return hipErrorInvalidValue;
+    if (a.nw != 4 && a.nw != 8 && !(a.nw == 16 && a.CT == 4)) return hipErrorInvalidValue;
     // 16-token-tile pairs run one token group (weights streamed once,
     // non-temporal); 64-token groups may be several, whose later groups read
     // the weights from L2 if the loads keep the default cache policy
     auto pick = [&](auto wfc, auto xdtc) {
         constexpr int W = decltype(wfc)::value, X = decltype(xdtc)::value;
         if (a.CT == 2) return a.nw == 8 ? go(wide_argmax_kernel<W, X, 2, 8, AUX_NT>) : go(wide_argmax_kernel<W, X, 2, 4, AUX_NT>);
-        if (a.wcache)
+        // 16 waves: 2 k-steps per chunk (the VGPR budget of 4 waves per SIMD)
+        if (a.wcache) {
+            if (a.nw == 16) return go(wide_argmax_kernel<W, X, 4, 16, 0, 2>);
+            if (a.nw == 8 && a.ring == 4) return go(wide_argmax_kernel<W, X, 4, 8, 0, 4, 4>);
             return a.nw == 8 ? go(wide_argmax_kernel<W, X, 4, 8, 0>) : go(wide_argmax_kernel<W, X, 4, 4, 0>);
+        }
+        if (a.nw == 16) return go(wide_argmax_kernel<W, X, 4, 16, AUX_NT, 2>);
+        if (a.nw == 8 && a.ring == 4) return go(wide_argmax_kernel<W, X, 4, 8, AUX_NT, 4, 4>);
         return a.nw == 8 ? go(wide_argmax_kernel<W, X, 4, 8, AUX_NT>) : go(wide_argmax_kernel<W, X, 4, 4, AUX_NT>);
     };
     using I = std::integral_constant<int, WF_I8>;
