@@ -69,6 +69,8 @@ struct qw_ctx {
     bool wide_norm_sep = false;  // RMSNorm prologue as a separate launch (QW_WIDE_NORM_SEP=1) instead of in the kernel
     int wide_dbg = 0;            // QW_WIDE_DBG: timing probes (wrong results)
     int stack_dbg = 0;           // QW_MLP_STACK_DBG: timing probes of the MLP stack (wrong results)
+    uint64_t* stack_trace = nullptr;       // QW_MLP_STACK_TRACE=<file>: per-block timestamps of the last stack launch
+    std::string stack_trace_path;
     int stack_gap = -1;          // QW_MLP_STACK_GAP: 10 ns ticks between a gate/up group's weight k-steps
                                  // (-1: 20 for BF16 weights, 120 for INT8, the measured best of each)
     int wide_cfg = 0;            // blocks x waves per block (QW_WIDE_CFG 1: 4x1, 2: 2x2, 3: 1x4; 0 = planned)
@@ -246,6 +248,15 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_WIDE_NORM_SEP")) c->wide_norm_sep = atoi(v) != 0;
     if (const char* v = getenv("QW_WIDE_DBG")) c->wide_dbg = atoi(v);
     if (const char* v = getenv("QW_MLP_STACK_DBG")) c->stack_dbg = atoi(v);
+    if (const char* v = getenv("QW_MLP_STACK_TRACE")) {
+        // timing probe: [layer][workgroup][4] s_memrealtime stamps of the last
+        // launch (x seen and h stored by gate/up, h seen and x stored by down),
+        // written to the file at qw_destroy
+        if (hipMalloc(&c->stack_trace, (size_t)qwk::kMlpStackMaxLayers * 256 * 4 * 8) == hipSuccess) {
+            hipMemset(c->stack_trace, 0, (size_t)qwk::kMlpStackMaxLayers * 256 * 4 * 8);
+            c->stack_trace_path = v;
+        }
+    }
     if (const char* v = getenv("QW_MLP_STACK_GAP")) c->stack_gap = std::max(0, std::min(1000, atoi(v)));
     if (const char* v = getenv("QW_WIDE_CFG")) c->wide_cfg = std::max(0, std::min(3, atoi(v)));
     if (const char* v = getenv("QW_WIDE_T")) c->wide_cfg |= std::max(0, std::min(8, atoi(v))) << 4;  // token groups
@@ -295,6 +306,17 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
 qw_status qw_destroy(qw_ctx* ctx) {
     if (!ctx) return QW_ERR_NULL;
     hipSetDevice(ctx->device);
+    if (ctx->stack_trace) {
+        std::vector<uint64_t> h((size_t)qwk::kMlpStackMaxLayers * 256 * 4);
+        hipDeviceSynchronize();
+        if (hipMemcpy(h.data(), ctx->stack_trace, h.size() * 8, hipMemcpyDeviceToHost) == hipSuccess) {
+            if (FILE* f = fopen(ctx->stack_trace_path.c_str(), "wb")) {
+                fwrite(h.data(), 8, h.size(), f);
+                fclose(f);
+            }
+        }
+        hipFree(ctx->stack_trace);
+    }
     if (ctx->ws) hipFree(ctx->ws);
     if (ctx->arena) hipFree(ctx->arena);
     delete ctx;
@@ -1564,6 +1586,7 @@ qw_status qw_mlp_stack(qw_ctx* ctx, int L, const qw_weight* const* gateup, const
         a.epoch = ctx->stack_epoch;
         a.err = ctx->mlp_ctl + 3;
         a.dbg = ctx->stack_dbg;
+        a.trace = ctx->stack_trace;
         a.gap = ctx->stack_gap >= 0 ? ctx->stack_gap : (gateup[0]->wf == QW_WFMT_INT8_ROWSCALE ? 120 : 20);
         hipError_t e = qwk::launch_mlp_stack(a, (int)gateup[0]->wf, (int)xdt, stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "MLP stack launch");

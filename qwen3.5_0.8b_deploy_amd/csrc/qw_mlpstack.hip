@@ -361,16 +361,31 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                         if (!ms_pause(ab, t0, it, dead)) break;
                     }
                 }
+                // a word once seen is not loaded again: the remaining polls
+                // are only those of words still in flight
+                bool got[MT];
+#pragma unroll
+                for (int m = 0; m < MT; ++m) got[m] = m >= M;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) v[m] = (uint64_t)tg << 32;
                 for (;;) {
                     bool ok = true;
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
-                        v[m] = m < M ? ms_load(X + (size_t)m * (MS_H / 2)) : ((uint64_t)tg << 32);
-                        ok = ok && (uint32_t)(v[m] >> 32) == tg;
+                        if (!got[m]) {
+                            const uint64_t wv = ms_load(X + (size_t)m * (MS_H / 2));
+                            if ((uint32_t)(wv >> 32) == tg) {
+                                v[m] = wv;
+                                got[m] = true;
+                            }
+                        }
+                        ok = ok && got[m];
                     }
                     if (__all(ok) || dead) break;
                     if (!ms_pause(ab, t0, it, dead)) break;
                 }
+                if (a.trace && grp == 0 && w == 0 && lane == 0)
+                    a.trace[((size_t)(l - 1) * MS_GRID + wg) * 4 + 0] = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     const uint32_t w2 = (uint32_t)v[m];
@@ -450,6 +465,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     ms_store(hw, tg, hb[0] | (hb[1] << 16));
                     ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
                 }
+                if (a.trace && grp == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 4 + 1] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.done_gu[grp], (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             } else {
                 ms_wait_lds(&S.done_gu[grp], (unsigned)(l + 1), ab, dead);
@@ -492,22 +508,36 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     if (!ms_pause(ab, t0, it, dead)) break;
                 }
             }
+            // a word once seen is not loaded again (fewer polls on the lines
+            // every down workgroup reads)
+            bool got[MT][NH];
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int i = 0; i < NH; ++i) {
+                    got[m][i] = !(m < M && lane + 64 * i < HWD);
+                    v[m][i] = 0u;
+                }
             for (;;) {
                 bool ok = true;
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
 #pragma unroll
                     for (int i = 0; i < NH; ++i) {
-                        const int e = lane + 64 * i;
-                        u32x2 wv = u32x2{0u, tg};
-                        if (m < M && e < HWD)
-                            wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8, AUX_SC1);
-                        ok = ok && wv[1] == tg;
-                        v[m][i] = wv[0];
+                        if (!got[m][i]) {
+                            const u32x2 wv =
+                                __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8, AUX_SC1);
+                            if (wv[1] == tg) {
+                                v[m][i] = wv[0];
+                                got[m][i] = true;
+                            }
+                        }
+                        ok = ok && got[m][i];
                     }
                 if (__all(ok) || dead) break;
                 if (!ms_pause(ab, t0, it, dead)) break;
             }
+            if (a.trace && w == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 4 + 2] = __builtin_amdgcn_s_memrealtime();
             // LDS only once valid: the down wave may still be reading the
             // previous block's slice until then (h of block l+1 exists only
             // after this workgroup's x of block l has been published)
@@ -581,6 +611,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     uint64_t* xw = xbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_H / 2) + (t * 16 + g * 4) / 2;
                     ms_store(xw, tg, xb[0] | (xb[1] << 16));
                     ms_store(xw + 1, tg, xb[2] | (xb[3] << 16));
+                    if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 4 + 3] = __builtin_amdgcn_s_memrealtime();
                     if (l + 1 == a.L) {
                         uint32_t* yw = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (size_t)j * MS_H + t * 16 + g * 4);
                         yw[0] = xb[0] | (xb[1] << 16);
