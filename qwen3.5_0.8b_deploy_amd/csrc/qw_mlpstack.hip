@@ -361,8 +361,12 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                         if (!ms_pause(ab, t0, it, dead)) break;
                     }
                 }
-                // a word once seen is not loaded again: the remaining polls
-                // are only those of words still in flight
+                // one token: a word once seen is not loaded again, so the
+                // remaining polls are only those of words still in flight
+                // (24 BF16 blocks: 159.5 -> 154.7 us); with several tokens the
+                // per-word branches cost more than they save (8 tokens: 11.5
+                // -> 20.8 us per block), so every round reloads every word
+                constexpr bool SKIP = MT == 1;
                 bool got[MT];
 #pragma unroll
                 for (int m = 0; m < MT; ++m) got[m] = m >= M;
@@ -372,14 +376,19 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     bool ok = true;
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
-                        if (!got[m]) {
-                            const uint64_t wv = ms_load(X + (size_t)m * (MS_H / 2));
-                            if ((uint32_t)(wv >> 32) == tg) {
-                                v[m] = wv;
-                                got[m] = true;
+                        if (SKIP) {
+                            if (!got[m]) {
+                                const uint64_t wv = ms_load(X + (size_t)m * (MS_H / 2));
+                                if ((uint32_t)(wv >> 32) == tg) {
+                                    v[m] = wv;
+                                    got[m] = true;
+                                }
                             }
+                            ok = ok && got[m];
+                        } else {
+                            v[m] = m < M ? ms_load(X + (size_t)m * (MS_H / 2)) : ((uint64_t)tg << 32);
+                            ok = ok && (uint32_t)(v[m] >> 32) == tg;
                         }
-                        ok = ok && got[m];
                     }
                     if (__all(ok) || dead) break;
                     if (!ms_pause(ab, t0, it, dead)) break;
@@ -508,8 +517,10 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     if (!ms_pause(ab, t0, it, dead)) break;
                 }
             }
-            // a word once seen is not loaded again (fewer polls on the lines
-            // every down workgroup reads)
+            // one token: a word once seen is not loaded again (fewer polls on
+            // the lines every down workgroup reads); several tokens reload
+            // every word (see the x polls)
+            constexpr bool SKIP = MT == 1;
             bool got[MT][NH];
 #pragma unroll
             for (int m = 0; m < MT; ++m)
@@ -524,15 +535,25 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 for (int m = 0; m < MT; ++m)
 #pragma unroll
                     for (int i = 0; i < NH; ++i) {
-                        if (!got[m][i]) {
-                            const u32x2 wv =
-                                __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8, AUX_SC1);
-                            if (wv[1] == tg) {
-                                v[m][i] = wv[0];
-                                got[m][i] = true;
+                        if (SKIP) {
+                            if (!got[m][i]) {
+                                const u32x2 wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i,
+                                                                                      so + m * (MS_I / 2) * 8, AUX_SC1);
+                                if (wv[1] == tg) {
+                                    v[m][i] = wv[0];
+                                    got[m][i] = true;
+                                }
                             }
+                            ok = ok && got[m][i];
+                        } else {
+                            const int e = lane + 64 * i;
+                            u32x2 wv = u32x2{0u, tg};
+                            if (m < M && e < HWD)
+                                wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8,
+                                                                          AUX_SC1);
+                            ok = ok && wv[1] == tg;
+                            v[m][i] = wv[0];
                         }
-                        ok = ok && got[m][i];
                     }
                 if (__all(ok) || dead) break;
                 if (!ms_pause(ab, t0, it, dead)) break;
