@@ -45,6 +45,10 @@
 // full_attention_cuda.cu:708-714, linear_attention_cuda.cu:589-615).
 #include "qw_stream.hpp"
 
+#ifndef QW_DA_SCHED
+#define QW_DA_SCHED 1
+#endif
+
 namespace qwk {
 
 namespace {
@@ -150,6 +154,16 @@ __global__ __launch_bounds__(64 * NWV, NWV == 4 ? 2 : 1) void gemm_da_kernel(Gem
                                                                    __builtin_bit_cast(bf16x8, B[j]), acc[i][j], 0, 0, 0);
             B[j] = *reinterpret_cast<const u32x4*>(stn + j * (LINE ? 2 * DA_U2 : 1024) + (LINE ? noff0 : 0));
         }
+#if QW_DA_SCHED
+        // keep column j's fragment read right behind its four MFMAs (the
+        // scheduler otherwise gathers the eight reads near the end of the
+        // step, and the next step's first MFMAs wait for them)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#endif
         __builtin_amdgcn_s_setprio(0);
         (void)noff1;
     };
