@@ -614,6 +614,15 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
         best[ct] = 0ull;
     }
     int bb = gw, bc = 0;  // body cursor
+    u32x4 Bn[CT][XU];     // B fragments of the next k-step
+    auto read_bn = [&](int ks) {
+        const uint8_t* xp = lds + (ks * CT * XU) * 1024 + lane * 16;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+            for (int h = 0; h < XU; ++h) Bn[ct][h] = *reinterpret_cast<const u32x4*>(xp + (ct * XU + h) * 1024);
+    };
+    read_bn(0);
     auto body = [&](int s, auto& A, auto& S) {
         const int c = bc, blk = bb;
         if (++bc == nch) {
@@ -634,12 +643,20 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
+            // this k-step's B fragments were read during the previous one;
+            // the next k-step's (the next chunk's or block's first past the
+            // end of this one) are read now, under these MFMAs
             const int ks = c * U + u;
-            const uint8_t* xp = lds + (ks * CT * XU) * 1024 + lane * 16;
+            u32x4 Bc[CT][XU];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+                for (int h = 0; h < XU; ++h) Bc[ct][h] = Bn[ct][h];
+            read_bn(ks + 1 == a.ksteps ? 0 : ks + 1);
             if constexpr (WF == WF_BF16) {
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
-                    const bf16x8 bb = *reinterpret_cast<const bf16x8*>(xp + ct * 1024);
+                    const bf16x8 bb = __builtin_bit_cast(bf16x8, Bc[ct][0]);
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt)
                         acc[rt][ct] = mfma_bf16(__builtin_bit_cast(bf16x8, A[u][rt]), bb, acc[rt][ct]);
@@ -650,8 +667,8 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
                 for (int rt = 0; rt < RT; ++rt) i8unit_to_f16(A[u][rt], a0[rt], a1[rt]);
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
-                    const f16x8 b0 = *reinterpret_cast<const f16x8*>(xp + ct * 2048);
-                    const f16x8 b1 = *reinterpret_cast<const f16x8*>(xp + ct * 2048 + 1024);
+                    const f16x8 b0 = __builtin_bit_cast(f16x8, Bc[ct][0]);
+                    const f16x8 b1 = __builtin_bit_cast(f16x8, Bc[ct][1]);
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) {
                         acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
