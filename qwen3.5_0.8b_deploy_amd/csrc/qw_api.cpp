@@ -11,10 +11,8 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <map>
 #include <mutex>
 #include <string>
-#include <utility>
 #include <vector>
 
 #include "../../include/qw_linear.h"
@@ -22,17 +20,29 @@
 #include "qw_kernels.hpp"
 
 hipError_t qwk::ensure_max_lds(const void* kernel, int bytes) {
+    // a fixed table (no heap allocation, so the no-allocation entry point may
+    // take this path); when it is full the attribute is simply set again
+    struct Entry {
+        int dev;
+        const void* kernel;
+        int bytes;
+    };
     static std::mutex mu;
-    static std::map<std::pair<int, const void*>, int> done;  // (device, kernel) -> largest size set
+    static Entry table[1024];
+    static int used = 0;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     std::lock_guard<std::mutex> lk(mu);
-    int& have = done[{dev, kernel}];
-    if (have >= bytes) return hipSuccess;
+    Entry* hit = nullptr;
+    for (int i = 0; i < used; ++i)
+        if (table[i].dev == dev && table[i].kernel == kernel) hit = &table[i];
+    if (hit && hit->bytes >= bytes) return hipSuccess;
     e = set_max_lds(kernel, bytes);
-    if (e == hipSuccess) have = bytes;
-    return e;
+    if (e != hipSuccess) return e;
+    if (hit) hit->bytes = bytes;
+    else if (used < 1024) table[used++] = Entry{dev, kernel, bytes};
+    return hipSuccess;
 }
 
 constexpr int kGemmMinM = 33;
