@@ -259,11 +259,13 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_WIDE_DBG")) c->wide_dbg = atoi(v);
     if (const char* v = getenv("QW_MLP_STACK_DBG")) c->stack_dbg = atoi(v);
     if (const char* v = getenv("QW_MLP_STACK_TRACE")) {
-        // timing probe: [layer][workgroup][4] s_memrealtime stamps of the last
-        // launch (x seen and h stored by gate/up, h seen and x stored by down),
+        // timing probe: [layer][workgroup][16] s_memrealtime stamps of the last
+        // launch (x seen and h stored by gate/up, h seen and x stored by down;
+        // 4..11: x seen by gate/up wave w, h seen by down poller w; 12: the
+        // last arriver starts its epilogue),
         // written to the file at qw_destroy
-        if (hipMalloc(&c->stack_trace, (size_t)qwk::kMlpStackMaxLayers * 256 * 4 * 8) == hipSuccess) {
-            hipMemset(c->stack_trace, 0, (size_t)qwk::kMlpStackMaxLayers * 256 * 4 * 8);
+        if (hipMalloc(&c->stack_trace, (size_t)qwk::kMlpStackMaxLayers * 256 * 16 * 8) == hipSuccess) {
+            hipMemset(c->stack_trace, 0, (size_t)qwk::kMlpStackMaxLayers * 256 * 16 * 8);
             c->stack_trace_path = v;
         }
     }
@@ -317,7 +319,7 @@ qw_status qw_destroy(qw_ctx* ctx) {
     if (!ctx) return QW_ERR_NULL;
     hipSetDevice(ctx->device);
     if (ctx->stack_trace) {
-        std::vector<uint64_t> h((size_t)qwk::kMlpStackMaxLayers * 256 * 4);
+        std::vector<uint64_t> h((size_t)qwk::kMlpStackMaxLayers * 256 * 16);
         hipDeviceSynchronize();
         if (hipMemcpy(h.data(), ctx->stack_trace, h.size() * 8, hipMemcpyDeviceToHost) == hipSuccess) {
             if (FILE* f = fopen(ctx->stack_trace_path.c_str(), "wb")) {

@@ -147,6 +147,26 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Sum over the 64 lanes of a wave with DPP moves only (no LDS crossbar, unlike
+// __shfl_xor's ds_bpermute): pairs, quads, half rows and rows by quad_perm /
+// row_half_mirror / row_mirror (every lane then holds its row's sum), then
+// row_bcast:15 and row_bcast:31 carry the row sums upward, so lane 63 holds
+// the total (the other lanes hold partial sums).  Fixed order: deterministic.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xF, false);
+    return v + __builtin_bit_cast(float, o);
+}
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xF>(v);  // row_mirror
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 
 // Orderable key of (value, index): larger value wins, then LOWER index wins.

@@ -217,7 +217,7 @@ struct MlpStackArgs {
     unsigned* err;      // device error flag
     int dbg;            // timing probes (wrong results): 1 no gate/up weight loads, 2 no down weight loads
     int gap;            // 100 MHz ticks between the k-steps of a gate/up group's weight requests
-    uint64_t* trace;    // timing probe [layer][workgroup][4] real-time stamps of the last launch, or nullptr
+    uint64_t* trace;    // timing probe [layer][workgroup][16] real-time stamps of the last launch, or nullptr
 };
 size_t mlp_stack_ws_bytes();
 int mlp_stack_max_m();

@@ -393,8 +393,11 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     if (__all(ok) || dead) break;
                     if (!ms_pause(ab, t0, it, dead)) break;
                 }
-                if (a.trace && grp == 0 && w == 0 && lane == 0)
-                    a.trace[((size_t)(l - 1) * MS_GRID + wg) * 4 + 0] = __builtin_amdgcn_s_memrealtime();
+                if (a.trace && grp == 0 && lane == 0) {
+                    const uint64_t now = __builtin_amdgcn_s_memrealtime();
+                    if (w == 0) a.trace[((size_t)(l - 1) * MS_GRID + wg) * 16 + 0] = now;
+                    a.trace[((size_t)(l - 1) * MS_GRID + wg) * 16 + 4 + w] = now;  // per wave
+                }
 #pragma unroll
                 for (int m = 0; m < MT; ++m) {
                     const uint32_t w2 = (uint32_t)v[m];
@@ -426,10 +429,10 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     *reinterpret_cast<uint32_t*>(&S.bs[wave][m][2 * lane]) = b0 | (b1 << 16);
                 }
             }
+            // per-token sums of squares of the slice: DPP adds, the total in
+            // lane 63 (no LDS round trips on the way to the MFMAs)
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
-#pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) ss[m] += __shfl_xor(ss[m], off);
+            for (int m = 0; m < MT; ++m) ss[m] = wave_sum_to_lane63(ss[m]);
             lds_fence_wave();
             f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -441,25 +444,38 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             // reduce the eight slices: the last wave to arrive runs the epilogue
             S.red_gu[grp][w][0][lane] = accg;
             S.red_gu[grp][w][1][lane] = accu;
+            if (lane == 63) {
 #pragma unroll
-            for (int m = 0; m < MT; ++m)
-                if (lane == m) S.red_ss[grp][w][m] = ss[m];
+                for (int m = 0; m < MT; ++m) S.red_ss[grp][w][m] = ss[m];
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             unsigned old = 0;
             if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_gu[grp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __shfl(old, 0);
+            old = __builtin_amdgcn_readfirstlane(old);
             if (old == MS_RW - 1) {
+                if (a.trace && grp == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 12] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.cnt_gu[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                f32x4 gs = S.red_gu[grp][0][0][lane], us = S.red_gu[grp][0][1][lane];
+                // the partials summed in wave order
+                const int jj = j < M ? j : 0;
+                f32x4 pv[MS_RW];
+                float ps[MS_RW];
+#pragma unroll
+                for (int v = 0; v < MS_RW; ++v) {
+                    pv[v] = S.red_gu[grp][v][0][lane];
+                    ps[v] = S.red_ss[grp][v][jj];
+                }
+                f32x4 gs = pv[0];
+                float sst = ps[0];
 #pragma unroll
                 for (int v = 1; v < MS_RW; ++v) {
-                    gs += S.red_gu[grp][v][0][lane];
-                    us += S.red_gu[grp][v][1][lane];
+                    gs += pv[v];
+                    sst += ps[v];
                 }
-                float sst = 0.0f;
-                const int jj = j < M ? j : 0;
 #pragma unroll
-                for (int v = 0; v < MS_RW; ++v) sst += S.red_ss[grp][v][jj];
+                for (int v = 0; v < MS_RW; ++v) pv[v] = S.red_gu[grp][v][1][lane];
+                f32x4 us = pv[0];
+#pragma unroll
+                for (int v = 1; v < MS_RW; ++v) us += pv[v];
                 const float inv = 1.0f / sqrtf(sst / (float)MS_H + a.eps);
                 if constexpr (WF == WF_I8) {
                     gs *= as_f32x4(sc[0]);
@@ -474,7 +490,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     ms_store(hw, tg, hb[0] | (hb[1] << 16));
                     ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
                 }
-                if (a.trace && grp == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 4 + 1] = __builtin_amdgcn_s_memrealtime();
+                if (a.trace && grp == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 1] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.done_gu[grp], (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             } else {
                 ms_wait_lds(&S.done_gu[grp], (unsigned)(l + 1), ab, dead);
@@ -558,7 +574,11 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 if (__all(ok) || dead) break;
                 if (!ms_pause(ab, t0, it, dead)) break;
             }
-            if (a.trace && w == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 4 + 2] = __builtin_amdgcn_s_memrealtime();
+            if (a.trace && lane == 0) {
+                const uint64_t now = __builtin_amdgcn_s_memrealtime();
+                if (w == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 2] = now;
+                a.trace[((size_t)l * MS_GRID + wg) * 16 + 4 + w] = now;  // per poller
+            }
             // LDS only once valid: the down wave may still be reading the
             // previous block's slice until then (h of block l+1 exists only
             // after this workgroup's x of block l has been published)
@@ -614,12 +634,16 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             unsigned old = 0;
             if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_dn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            old = __shfl(old, 0);
+            old = __builtin_amdgcn_readfirstlane(old);
             if (old == MS_RW - 1) {
+                if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 12] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.cnt_dn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                f32x4 s = S.red_dn[0][lane];
+                f32x4 pd[MS_RW];
 #pragma unroll
-                for (int v = 1; v < MS_RW; ++v) s += S.red_dn[v][lane];
+                for (int v = 0; v < MS_RW; ++v) pd[v] = S.red_dn[v][lane];
+                f32x4 s = pd[0];
+#pragma unroll
+                for (int v = 1; v < MS_RW; ++v) s += pd[v];
                 if constexpr (WF == WF_I8) s *= as_f32x4(sc);
                 if (j < M) {
                     uint32_t xb[4];
@@ -632,7 +656,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                     uint64_t* xw = xbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_H / 2) + (t * 16 + g * 4) / 2;
                     ms_store(xw, tg, xb[0] | (xb[1] << 16));
                     ms_store(xw + 1, tg, xb[2] | (xb[3] << 16));
-                    if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 4 + 3] = __builtin_amdgcn_s_memrealtime();
+                    if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 3] = __builtin_amdgcn_s_memrealtime();
                     if (l + 1 == a.L) {
                         uint32_t* yw = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (size_t)j * MS_H + t * 16 + g * 4);
                         yw[0] = xb[0] | (xb[1] << 16);
