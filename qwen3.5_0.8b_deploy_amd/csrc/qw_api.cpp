@@ -99,7 +99,6 @@ struct qw_ctx {
     uint64_t* stack_words = nullptr;       // persistent MLP stack: hand-off words
     bool mlp_stack = true;                 // QW_MLP_STACK=0: per-layer launches in qw_mlp_stack
     int argmax_cache = -1;                 // QW_ARGMAX_CACHE: weight-load cache policy of that kernel (-1 auto, 0 NT, 1 default)
-    int argmax_ring = 0;                   // QW_ARGMAX_RING: chunks in flight of that kernel's 8-wave form (0 auto)
     int argmax_nw = 0;                     // QW_ARGMAX_NW: waves per weight-stationary argmax workgroup (0 auto, 4, 8)
     int gemm_da_split = -1;                // QW_GEMM_DA_SPLIT: split-K direct-A for few blocks (-1 auto, 0 off, S)
     bool layer_tail = false;               // QW_LAYER_TAIL=1: qw_layer_tail in one launch (measured slower)
@@ -236,8 +235,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_LAYER_TAIL")) c->layer_tail = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_DA_SPLIT")) c->gemm_da_split = atoi(v);
     if (const char* v = getenv("QW_ARGMAX_CACHE")) c->argmax_cache = atoi(v) ? 1 : 0;
-    if (const char* v = getenv("QW_ARGMAX_RING")) c->argmax_ring = atoi(v);
-    if (const char* v = getenv("QW_ARGMAX_NW")) c->argmax_nw = (atoi(v) == 4 || atoi(v) == 8 || atoi(v) == 16) ? atoi(v) : 0;
+    if (const char* v = getenv("QW_ARGMAX_NW")) c->argmax_nw = (atoi(v) == 4 || atoi(v) == 8) ? atoi(v) : 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
     if (const char* v = getenv("QW_GEMM_DA")) c->gemm_da = std::max(0, std::min(2, atoi(v)));
@@ -1095,7 +1093,6 @@ static qw_status lmhead_route(qw_ctx* ctx, const qw_weight* E, const void* h, qw
         qwk::WideArgmaxArgs a{};
         a.nw = ctx->argmax_nw;
         a.wcache = ctx->argmax_cache;
-        a.ring = ctx->argmax_ring;
         int grid = 0;
         size_t smem = 0;
         if (qwk::wide_argmax_plan(E->wf, (int)hdt, M, E->K, ctx->num_cus, a, grid, smem)) {

@@ -118,7 +118,6 @@ struct WideArgmaxArgs {
     int ksteps;
     int T, Mg, CT;             // token groups of Mg tokens, CT 16-token tiles each
     int nw;                    // waves per workgroup (4 or 8; 0: the plan chooses)
-    int ring;                  // 64-token groups, 8 waves: 4 = four chunks of 4 k-steps in flight (else two of 8)
     int wcache;                // weight loads: 1 default cache policy, 0 non-temporal, -1 the plan chooses
     unsigned long long* keys;  // [M] (self-resetting)
     unsigned* done;            // completion counter (self-resetting)

@@ -932,7 +932,6 @@ bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs
     // MFMAs with the other's conversions and LDS reads (128 tokens: 110 ->
     // 93 us); BF16 weights measured better with 4 (128 -> 145 us with 8).
     // Smaller groups run two 4-wave workgroups per CU
-    if (a.nw == 16 && CT != 4) a.nw = 0;  // 16 waves only for 64-token groups
     if (a.nw == 0) a.nw = CT == 4 && wf == WF_I8 ? 8 : 4;
     if (a.wcache < 0) a.wcache = T > 1 ? 1 : 0;
     return true;
@@ -945,21 +944,15 @@ hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid
         hipLaunchKernelGGL(kern, dim3(grid), dim3(a.nw * 64), smem, stream, a);
         return hipGetLastError();
     };
-    if (a.nw != 4 && a.nw != 8 && !(a.nw == 16 && a.CT == 4)) return hipErrorInvalidValue;
+    if (a.nw != 4 && a.nw != 8) return hipErrorInvalidValue;
     // 16-token-tile pairs run one token group (weights streamed once,
     // non-temporal); 64-token groups may be several, whose later groups read
     // the weights from L2 if the loads keep the default cache policy
     auto pick = [&](auto wfc, auto xdtc) {
         constexpr int W = decltype(wfc)::value, X = decltype(xdtc)::value;
         if (a.CT == 2) return a.nw == 8 ? go(wide_argmax_kernel<W, X, 2, 8, AUX_NT>) : go(wide_argmax_kernel<W, X, 2, 4, AUX_NT>);
-        // 16 waves: 2 k-steps per chunk (the VGPR budget of 4 waves per SIMD)
-        if (a.wcache) {
-            if (a.nw == 16) return go(wide_argmax_kernel<W, X, 4, 16, 0, 2>);
-            if (a.nw == 8 && a.ring == 4) return go(wide_argmax_kernel<W, X, 4, 8, 0, 4, 4>);
+        if (a.wcache)
             return a.nw == 8 ? go(wide_argmax_kernel<W, X, 4, 8, 0>) : go(wide_argmax_kernel<W, X, 4, 4, 0>);
-        }
-        if (a.nw == 16) return go(wide_argmax_kernel<W, X, 4, 16, AUX_NT, 2>);
-        if (a.nw == 8 && a.ring == 4) return go(wide_argmax_kernel<W, X, 4, 8, AUX_NT, 4, 4>);
         return a.nw == 8 ? go(wide_argmax_kernel<W, X, 4, 8, AUX_NT>) : go(wide_argmax_kernel<W, X, 4, 4, AUX_NT>);
     };
     using I = std::integral_constant<int, WF_I8>;
