@@ -67,6 +67,7 @@ struct qw_ctx {
                                  // 1 where its blocks fill the chip, 2 wherever it applies)
     bool gemm_da_line = true;    // its activation loads as whole row lines (QW_GEMM_DA_LINE=0: row pieces)
     int gemm_da_group = 0;       // its token blocks per raster group (QW_GEMM_DA_GROUP; 0: 8)
+    int gemm_da_persist = 1;     // its 8-wave form as one persistent workgroup per CU (QW_GEMM_DA_PERSIST=0: off)
     int gemm_da_waves = 0;       // its waves per block: 4 (256 rows, two blocks per CU) or 8 (512 rows, one);
                                  // 0: 8 where the 512-row blocks cover every CU (QW_GEMM_DA_W8=0/1 forces 4/8)
     int gemm_rows = 0;           // weight rows per GEMM block (QW_GEMM_ROWS: 64 or 256; 0 = by shape)
@@ -242,6 +243,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_DA_LINE")) c->gemm_da_line = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_DA_GROUP")) c->gemm_da_group = std::max(0, atoi(v));
     if (const char* v = getenv("QW_GEMM_DA_W8")) c->gemm_da_waves = atoi(v) != 0 ? 8 : 4;
+    if (const char* v = getenv("QW_GEMM_DA_PERSIST")) c->gemm_da_persist = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_SPLITK")) c->gemm_splitk = std::max(0, std::min(8, atoi(v)));
     if (const char* v = getenv("QW_GEMM_ROWS")) c->gemm_rows = atoi(v) == 64 ? 64 : 256;
     if (const char* v = getenv("QW_ATTN_FUSED")) c->attn_fused = atoi(v) != 0;
@@ -932,7 +934,8 @@ static qw_status run_gemm(qw_ctx* ctx, const qw_weight* W, int rows, const void*
         const int nwv = ctx->gemm_da_waves
                             ? ctx->gemm_da_waves
                             : ((W->phys_tiles * 16 + 511) / 512 * ((M + 127) / 128) >= ctx->num_cus ? 8 : 4);
-        hipError_t e = qwk::launch_gemm_da(a, W->glu != 0, ctx->gemm_da_line, stream, nwv);
+        hipError_t e = qwk::launch_gemm_da(a, W->glu != 0, ctx->gemm_da_line, stream, nwv,
+                                           ctx->gemm_da_persist ? ctx->num_cus : 0);
         if (e != hipSuccess) return hip_fail(ctx, e, "gemm launch");
         return QW_OK;
     }

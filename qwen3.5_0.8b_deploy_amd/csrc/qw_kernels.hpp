@@ -167,7 +167,9 @@ bool gemm_da_fits(const GemmArgs& a, int wf, int xdt, bool argmax);
 size_t gemm_da_lds_bytes(bool glu, bool line, int nwv);
 // line: activation loads of whole 128-byte row lines (two k-steps, swizzled
 // into LDS) instead of 64-byte row pieces
-hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream, int nwv = 4);
+// persist_wgs >= 8 with nwv 8: the persistent form, at most persist_wgs
+// workgroups (one per CU)
+hipError_t launch_gemm_da(const GemmArgs& a, bool glu, bool line, hipStream_t stream, int nwv = 4, int persist_wgs = 0);
 // split-K form: S K splits (a.ksteps a multiple of 4 S) into a.partials
 // (gemm_da_split_bytes), then the reduce + epilogue kernel
 size_t gemm_da_split_bytes(const GemmArgs& a, int S);
