@@ -264,19 +264,22 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
                     a1[rt] = a1[rt] * gs1;
                 }
             }
+            // the first half-unit's MFMAs of every tile, then the second's
+            // (each accumulator sums in the same order, with the other tiles'
+            // independent MFMAs between its two)
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
                 const f16x8 b0 = __builtin_bit_cast(f16x8, B[buf][ct][0]);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
+                if (do_ss) accss[ct] = mfma_f16(b0, b0, accss[ct]);
+            }
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
                 const f16x8 b1 = __builtin_bit_cast(f16x8, B[buf][ct][1]);
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
-                    acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
-                }
-                if (do_ss) {
-                    accss[ct] = mfma_f16(b0, b0, accss[ct]);
-                    accss[ct] = mfma_f16(b1, b1, accss[ct]);
-                }
+                for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
+                if (do_ss) accss[ct] = mfma_f16(b1, b1, accss[ct]);
             }
         }
     };
@@ -665,15 +668,19 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
                 f16x8 a0[RT], a1[RT];
 #pragma unroll
                 for (int rt = 0; rt < RT; ++rt) i8unit_to_f16(A[u][rt], a0[rt], a1[rt]);
+                // the first half-unit's MFMAs of every tile, then the second's:
+                // RT * CT independent MFMAs between the two of each accumulator
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
                     const f16x8 b0 = __builtin_bit_cast(f16x8, Bc[ct][0]);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
+                }
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
                     const f16x8 b1 = __builtin_bit_cast(f16x8, Bc[ct][1]);
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt) {
-                        acc[rt][ct] = mfma_f16(a0[rt], b0, acc[rt][ct]);
-                        acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
-                    }
+                    for (int rt = 0; rt < RT; ++rt) acc[rt][ct] = mfma_f16(a1[rt], b1, acc[rt][ct]);
                 }
             }
         }
