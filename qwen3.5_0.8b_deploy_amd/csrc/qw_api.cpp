@@ -100,6 +100,7 @@ struct qw_ctx {
     uint64_t* stack_words = nullptr;       // persistent MLP stack: hand-off words
     bool mlp_stack = true;                 // QW_MLP_STACK=0: per-layer launches in qw_mlp_stack
     int argmax_cache = -1;                 // QW_ARGMAX_CACHE: weight-load cache policy of that kernel (-1 auto, 0 NT, 1 default)
+    int argmax_wide_min_i8 = 8;            // QW_ARGMAX_WIDE_MIN_I8: INT8 lm_head tokens from which the weight-stationary argmax runs
     int argmax_nw = 0;                     // QW_ARGMAX_NW: waves per weight-stationary argmax workgroup (0 auto, 4, 8)
     int gemm_da_split = -1;                // QW_GEMM_DA_SPLIT: split-K direct-A for few blocks (-1 auto, 0 off, S)
     bool layer_tail = false;               // QW_LAYER_TAIL=1: qw_layer_tail in one launch (measured slower)
@@ -236,6 +237,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_LAYER_TAIL")) c->layer_tail = atoi(v) != 0;
     if (const char* v = getenv("QW_GEMM_DA_SPLIT")) c->gemm_da_split = atoi(v);
     if (const char* v = getenv("QW_ARGMAX_CACHE")) c->argmax_cache = atoi(v) ? 1 : 0;
+    if (const char* v = getenv("QW_ARGMAX_WIDE_MIN_I8")) c->argmax_wide_min_i8 = std::max(1, atoi(v));
     if (const char* v = getenv("QW_ARGMAX_NW")) c->argmax_nw = (atoi(v) == 4 || atoi(v) == 8) ? atoi(v) : 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
@@ -1091,7 +1093,11 @@ qw_status qw_linear(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dtype xdt
 // the GEMM or the small-M kernels.
 static qw_status lmhead_route(qw_ctx* ctx, const qw_weight* E, const void* h, qw_dtype hdt, int M, int32_t* ids,
                               float* maxv, hipStream_t stream) {
-    if (ctx->wide && !(ctx->gemm_forced && M >= ctx->gemm_min_m) && M >= ctx->wide_min && M <= ctx->wide_max &&
+    // INT8 E takes the weight-stationary argmax from 8 tokens (8 / 12 / 16
+    // tokens: 50.4 / 50.5 / 50.6 us against 58.0 / 58.1 / 59.4 us for the
+    // skinny kernel); BF16 E from wide_min (the two measure alike at 8..16)
+    const int wmin = E->wf == QW_WFMT_INT8_ROWSCALE ? std::min(ctx->wide_min, ctx->argmax_wide_min_i8) : ctx->wide_min;
+    if (ctx->wide && !(ctx->gemm_forced && M >= ctx->gemm_min_m) && M >= wmin && M <= ctx->wide_max &&
         !E->glu && aligned(E->packed, 16)) {
         qwk::WideArgmaxArgs a{};
         a.nw = ctx->argmax_nw;

@@ -148,7 +148,7 @@ def test_cfg5_lmhead_bf16_full_vocab(qw, lm, M):
         assert int(g2[0]) == UNIQUE_T2
 
 
-@pytest.mark.parametrize("M", [1, 17, 32, 64, 128, 200, 256])
+@pytest.mark.parametrize("M", [1, 8, 17, 32, 64, 128, 200, 256])
 def test_cfg5_lmhead_int8_full_vocab(qw, lm, M):
     """INT8 E quantized on the device from the BF16 E (the recipe of
     mlp_cuda.cu:22-39), F16 activations.  The oracle is the reference's
