@@ -173,3 +173,21 @@ def test_waves_glu_bf16(qw, ctx_w, oracle, relerr, M):
     g = xs @ oracle.round_bf16(G).astype(np.float64).T
     u = xs @ oracle.round_bf16(U).astype(np.float64).T
     assert relerr(host(h), g / (1.0 + np.exp(-g)) * u) <= 4e-3
+
+
+@pytest.mark.parametrize("K,M", [(2048, 777), (3584, 1536), (2048, 4100)])
+def test_waves_residual_bf16_inplace(qw, ctx_w, oracle, relerr, K, M):
+    """BF16 residual added in place (y = residual), the prefill's out and
+    down projections: the persistent kernel brings the residual rows of
+    tokens 64..127 of each block into LDS before the block's k-loop."""
+    W = oracle.normal((1024, K), 7360 + K, 0.0, 0.02)
+    xt = dev(oracle.normal((M, K), 7361 + M), torch.bfloat16)
+    r = dev(oracle.normal((M, 1024), 7362), torch.bfloat16)
+
+    def run(c, w):
+        y = r.clone()
+        qw.linear(c, w, xt, y, residual=y)
+        return [y]
+    (y,) = _both(qw, ctx_w, lambda c: qw.Weight.pack(c, W, qw.WFMT_BF16), run)
+    ref = oracle.linear_f64(oracle.round_bf16(W), host(xt)) + host(r)
+    assert relerr(host(y), ref) <= 4e-3
