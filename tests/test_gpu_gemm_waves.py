@@ -134,17 +134,20 @@ def test_waves_q_gate(qw, ctx_w, oracle, relerr):
     assert relerr(host(q), q_ref) <= 1e-5 and relerr(host(g), g_ref) <= 1e-5
 
 
-@pytest.mark.parametrize("N,K,M", [(8224, 1024, 1000), (5120, 1024, 1536), (4096, 2048, 777), (1040, 512, 900)])
-def test_waves_bf16_rows(qw, ctx_w, oracle, relerr, N, K, M):
+@pytest.mark.parametrize("N,K,M,pad", [(8224, 1024, 1000, 72), (5120, 1024, 1536, 72), (4096, 2048, 777, 72),
+                                       (1040, 512, 900, 72), (4096, 1024, 1100, 4)])
+def test_waves_bf16_rows(qw, ctx_w, oracle, relerr, N, K, M, pad):
     """BF16 outputs into a wider row stride (the prefill's stacked input
     projections write y[:, :N] of a [M][8192+] buffer): the persistent kernel
     keeps half of each block's outputs in LDS and stores them during the next
     block's k-steps (K >= 1024), so ragged token and row blocks, a K of 2048
     (stores spread over the first 32 of 64 k-steps) and K = 512 (stored at
-    once) are covered; the bytes past N of every row stay untouched."""
+    once) are covered, and a row stride that is not a multiple of 8 (rows
+    not 16-byte aligned: stored at once); the bytes past N of every row stay
+    untouched."""
     W = oracle.normal((N, K), 7340 + N + K, 0.0, 0.02)
     xt = dev(oracle.normal((M, K), 7341 + M), torch.bfloat16)
-    ld = N + 72
+    ld = N + pad
 
     def run(c, w):
         big = torch.full((M, ld), 7.0, device="cuda", dtype=torch.bfloat16)
