@@ -198,6 +198,61 @@ def test_mlp_stack_int8(qw, ctx, oracle, relerr, M):
     assert relerr(host(y), host(z).astype(np.float64)) <= 1e-3
 
 
+@pytest.mark.parametrize("M", [1, 8])
+def test_mlp_stack_int8_bench_config(qw, ctx, oracle, relerr, M):
+    """The INT8 configuration bench.py times on the persistent stack
+    (cfg3_int8_mlp_stack_M1 / _M8): 24 INT8 blocks with per-row scales and a
+    per-call gamma, F16 x, one launch.  Teacher-forced per-block bar: the
+    launch of the first n blocks against the FP64 block n (dequant-then-
+    matmul of the same q and s, with the kernel's F16 roundings of
+    x * (1 + gamma), h and the hidden state) on the output of the first
+    n - 1: <= 1e-3, the INT8 bar; the full launch equals the last prefix."""
+    L = 24
+    layers = []
+    for l in range(L):
+        (qg, sg), (qu, su), (qd, sd) = (oracle.quantize_rowscale(oracle.normal(s, 4600 + 10 * l + i, 0.0, 0.02))
+                                        for i, s in enumerate([(I, H), (I, H), (H, I)]))
+        gam = oracle.normal((H,), 4608 + 10 * l, 0.0, 0.02)
+        layers.append((qg, qu, qd, sg, su, sd, gam))
+    gu = [qw.Weight.pack_glu(ctx, qg, qu, qw.WFMT_INT8, gate_scales=sg, up_scales=su)
+          for qg, qu, _, sg, su, _, _ in layers]
+    dn = [qw.Weight.pack(ctx, qd, qw.WFMT_INT8, scales=sd) for _, _, qd, _, _, sd, _ in layers]
+    gms = [dev(L_[6]) for L_ in layers]
+    x0 = dev(oracle.normal((M, H), 4699 + M), torch.float16)
+    f16 = lambda a: a.astype(np.float16).astype(np.float64)
+    prev = host(x0).astype(np.float64)
+    last = None
+    for n in range(1, L + 1):
+        y = torch.empty_like(x0)
+        qw.mlp_stack(ctx, gu[:n], dn[:n], x0, y, gammas=gms[:n])
+        torch.cuda.synchronize()
+        got = host(y).astype(np.float64)
+        qg, qu, qd, sg, su, sd, gam = layers[n - 1]
+        inv = 1.0 / np.sqrt((prev * prev).mean(axis=1, keepdims=True) + 1e-6)
+        b = f16(prev * (1.0 + gam.astype(np.float64))[None, :])
+        g = (b @ qg.astype(np.float64).T) * sg * inv
+        u = (b @ qu.astype(np.float64).T) * su * inv
+        h = f16(g / (1.0 + np.exp(-g)) * u)
+        ref = f16(prev + (h @ qd.astype(np.float64).T) * sd)
+        e = relerr(got, ref)
+        assert e <= 1e-3, f"block {n}: {e}"
+        prev = got
+        last = y
+    assert ctx.device_error() == 0
+    # the graph-replayed form the bench times gives the same bits
+    z = torch.empty_like(x0)
+    s_ = torch.cuda.Stream()
+    with torch.cuda.stream(s_):
+        g_ = qw.Graph(ctx, s_)
+        with g_:
+            qw.mlp_stack(ctx, gu, dn, x0, z, gammas=gms, stream=s_)
+        for _ in range(3):
+            g_.launch(s_)
+    s_.synchronize()
+    assert torch.equal(z, last)
+    assert ctx.device_error() == 0
+
+
 def test_mlp_stack_graph_replays(qw, ctx, oracle, relerr):
     """Captured once, replayed three times with eager work between: every
     replay (a new epoch each) equals the eager result."""
