@@ -447,7 +447,8 @@ __global__ __launch_bounds__(512, 1) void gemm_da_persist_kernel(GemmArgs a) {
     constexpr int RB = GLU ? 512 : 1024;  // bytes of one token's output row in a block
     constexpr int DT0 = GLU ? 0 : 64;     // first deferred token of a block
     const bool defer = (a.flags & (EP_RESIDUAL | EP_SPLIT)) == 0 && a.ydt == DT_BF16 && ks_n >= 32 &&
-                       (a.N & 7) == 0 && (a.ldy & 7) == 0 && a.vec_store;  // 16-byte aligned row pieces
+                       (a.N & 7) == 0 && (a.ldy & 7) == 0 && a.vec_store &&  // 16-byte aligned row pieces
+                       (long long)a.M * a.ldy * 2 < 0x7ffffff0ll;  // the dropped-store offset lies past every row
     bool pending = false;
     int pm0 = 0, prow0 = 0;  // first token / output row of the block in ob
     auto ob_put = [&]() {
