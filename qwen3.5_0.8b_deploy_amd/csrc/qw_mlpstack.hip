@@ -23,6 +23,8 @@
 //     0..7 poll the h slices of waves 8..15 and hand them over through LDS,
 //     so the waves that stream weights never poll (vector-memory loads retire
 //     in order: a poll issued behind a weight stream waits for all of it).
+//     With INT8 weights and one token the down waves poll their own slices
+//     instead (their weights have landed by the time h can arrive).
 // A workgroup barrier is used once, at the start; the eight waves of a tile
 // reduce their partial tiles through LDS, and the last of them to arrive (an
 // LDS counter) runs the epilogue.  The others issue the next block's weight
@@ -248,6 +250,11 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     constexpr int U_DN = KS_DN / MS_RW;                    // per down wave (14 / 7)
     constexpr int HWD = MS_DSPAN / 2;                      // h words per token of a down wave's slice (224)
     constexpr int NH = (HWD + 63) / 64;                    // per lane (4)
+    // INT8 weights, one token: the down waves poll their own h slices (no
+    // poller -> LDS -> flag hop; 24 blocks 6.0 -> 5.87 us per block); with
+    // BF16 weights (twice the bytes in flight ahead of the first poll) that
+    // measured slower (162.5 -> 166 us per 24 blocks), and more tokens spill
+    constexpr bool SELF = WF == WF_I8 && MT == 1;
     extern __shared__ __attribute__((aligned(16))) uint8_t ms_raw[];
     MsLds& S = *reinterpret_cast<MsLds*>(ms_raw);
 
@@ -284,6 +291,97 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     const MsAbort ab{a.err, a.epoch + 1, epoch};
     uint64_t* const hbuf = a.hbuf;
     uint64_t* const xbuf = a.xbuf;
+
+    // The h slice of down wave w for block l (intermediate rows [448 w, 448 w +
+    // 448)): polled through a buffer descriptor (one per-lane offset, the
+    // token and parity in the scalar offset, device-coherent loads) and
+    // deposited in the wave's LDS rows once every tag matched.
+    auto poll_h = [&](int w, int l) {
+        const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)(MS_HWORDS * 8));
+        const uint32_t vb = (uint32_t)(((MS_DSPAN / 2) * w + lane) * 8);
+        const uint32_t tg = ms_tag(epoch, l);
+        const int so = (l & 1) * MS_MAXM * (MS_I / 2) * 8;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        unsigned it = 0;
+        uint32_t v[MT][NH];  // payloads (the tags are checked as the words arrive)
+        if constexpr (MT > 1) {
+            // first token 0's words only: a producer stores all tokens'
+            // words of its rows with one instruction, so once these
+            // arrived the rest follow; polling them all costs every
+            // other access MT times the poll traffic
+            for (;;) {
+                bool ok = true;
+#pragma unroll
+                for (int i = 0; i < NH; ++i) {
+                    const int e = lane + 64 * i;
+                    if (e < HWD) {
+                        const u32x2 wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so, AUX_SC1);
+                        ok = ok && wv[1] == tg;
+                    }
+                }
+                if (__all(ok) || dead) break;
+                if (!ms_pause(ab, t0, it, dead)) break;
+            }
+        }
+        // one token: a word once seen is not loaded again (fewer polls on
+        // the lines every down workgroup reads); several tokens reload
+        // every word (see the x polls)
+        constexpr bool SKIP = MT == 1;
+        bool got[MT][NH];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < NH; ++i) {
+                got[m][i] = !(m < M && lane + 64 * i < HWD);
+                v[m][i] = 0u;
+            }
+        for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+#pragma unroll
+                for (int i = 0; i < NH; ++i) {
+                    if (SKIP) {
+                        if (!got[m][i]) {
+                            const u32x2 wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i,
+                                                                                  so + m * (MS_I / 2) * 8, AUX_SC1);
+                            if (wv[1] == tg) {
+                                v[m][i] = wv[0];
+                                got[m][i] = true;
+                            }
+                        }
+                        ok = ok && got[m][i];
+                    } else {
+                        const int e = lane + 64 * i;
+                        u32x2 wv = u32x2{0u, tg};
+                        if (m < M && e < HWD)
+                            wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8,
+                                                                      AUX_SC1);
+                        ok = ok && wv[1] == tg;
+                        v[m][i] = wv[0];
+                    }
+                }
+            if (__all(ok) || dead) break;
+            if (!ms_pause(ab, t0, it, dead)) break;
+        }
+        if (a.trace && lane == 0) {
+            const uint64_t now = __builtin_amdgcn_s_memrealtime();
+            if (w == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 2] = now;
+            a.trace[((size_t)l * MS_GRID + wg) * 16 + 4 + w] = now;  // per poller
+        }
+        // LDS only once valid: the down wave may still be reading the
+        // previous block's slice until then (h of block l+1 exists only
+        // after this workgroup's x of block l has been published)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int i = 0; i < NH; ++i) {
+                const int e = lane + 64 * i;
+                if (m < M && e < HWD) *reinterpret_cast<uint32_t*>(&S.bd[w][m][2 * e]) = v[m][i];
+            }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+    };
 
     if (!dn_wg) {
         // ===================== gate/up =====================
@@ -499,98 +597,13 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         }
     } else if (wave < MS_RW) {
         // ===================== h pollers of the down waves =====================
-        // wave w polls the h slice of down wave w (intermediate rows
-        // [448 w, 448 w + 448)) and deposits it in LDS; a poller issues no
-        // weight loads, so its polls never wait behind a weight stream
+        // wave w polls the h slice of down wave w and deposits it in LDS; a
+        // poller issues no weight loads, so its polls never wait behind a
+        // weight stream
+        if constexpr (SELF) return;  // the down waves poll their own slices
         const int w = wave;
-        // the words through a buffer descriptor: one per-lane offset, the
-        // token and parity in the scalar offset (device-coherent loads, as
-        // the agent-scope atomic loads elsewhere)
-        const __amdgpu_buffer_rsrc_t hrs = make_rsrc(hbuf, (uint32_t)(MS_HWORDS * 8));
-        const uint32_t vb = (uint32_t)(((MS_DSPAN / 2) * w + lane) * 8);
         for (int l = 0; l < a.L; ++l) {
-            const uint32_t tg = ms_tag(epoch, l);
-            const int so = (l & 1) * MS_MAXM * (MS_I / 2) * 8;
-            const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-            unsigned it = 0;
-            uint32_t v[MT][NH];  // payloads (the tags are checked as the words arrive)
-            if constexpr (MT > 1) {
-                // first token 0's words only: a producer stores all tokens'
-                // words of its rows with one instruction, so once these
-                // arrived the rest follow; polling them all costs every
-                // other access MT times the poll traffic
-                for (;;) {
-                    bool ok = true;
-#pragma unroll
-                    for (int i = 0; i < NH; ++i) {
-                        const int e = lane + 64 * i;
-                        if (e < HWD) {
-                            const u32x2 wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so, AUX_SC1);
-                            ok = ok && wv[1] == tg;
-                        }
-                    }
-                    if (__all(ok) || dead) break;
-                    if (!ms_pause(ab, t0, it, dead)) break;
-                }
-            }
-            // one token: a word once seen is not loaded again (fewer polls on
-            // the lines every down workgroup reads); several tokens reload
-            // every word (see the x polls)
-            constexpr bool SKIP = MT == 1;
-            bool got[MT][NH];
-#pragma unroll
-            for (int m = 0; m < MT; ++m)
-#pragma unroll
-                for (int i = 0; i < NH; ++i) {
-                    got[m][i] = !(m < M && lane + 64 * i < HWD);
-                    v[m][i] = 0u;
-                }
-            for (;;) {
-                bool ok = true;
-#pragma unroll
-                for (int m = 0; m < MT; ++m)
-#pragma unroll
-                    for (int i = 0; i < NH; ++i) {
-                        if (SKIP) {
-                            if (!got[m][i]) {
-                                const u32x2 wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i,
-                                                                                      so + m * (MS_I / 2) * 8, AUX_SC1);
-                                if (wv[1] == tg) {
-                                    v[m][i] = wv[0];
-                                    got[m][i] = true;
-                                }
-                            }
-                            ok = ok && got[m][i];
-                        } else {
-                            const int e = lane + 64 * i;
-                            u32x2 wv = u32x2{0u, tg};
-                            if (m < M && e < HWD)
-                                wv = __builtin_amdgcn_raw_buffer_load_b64(hrs, vb + 512 * i, so + m * (MS_I / 2) * 8,
-                                                                          AUX_SC1);
-                            ok = ok && wv[1] == tg;
-                            v[m][i] = wv[0];
-                        }
-                    }
-                if (__all(ok) || dead) break;
-                if (!ms_pause(ab, t0, it, dead)) break;
-            }
-            if (a.trace && lane == 0) {
-                const uint64_t now = __builtin_amdgcn_s_memrealtime();
-                if (w == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 2] = now;
-                a.trace[((size_t)l * MS_GRID + wg) * 16 + 4 + w] = now;  // per poller
-            }
-            // LDS only once valid: the down wave may still be reading the
-            // previous block's slice until then (h of block l+1 exists only
-            // after this workgroup's x of block l has been published)
-#pragma unroll
-            for (int m = 0; m < MT; ++m)
-#pragma unroll
-                for (int i = 0; i < NH; ++i) {
-                    const int e = lane + 64 * i;
-                    if (m < M && e < HWD) *reinterpret_cast<uint32_t*>(&S.bd[w][m][2 * e]) = v[m][i];
-                }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_wave_barrier();
+            poll_h(w, l);
             if (lane == 0) __hip_atomic_store(&S.hflag[w], (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     } else {
@@ -623,7 +636,8 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
         for (int l = 0; l < a.L; ++l) {
             const uint32_t tg = ms_tag(epoch, l);
             cv.convert(A);
-            ms_wait_lds(&S.hflag[d], (unsigned)(l + 1), ab, dead);
+            if constexpr (SELF) poll_h(d, l);
+            else ms_wait_lds(&S.hflag[d], (unsigned)(l + 1), ab, dead);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < U_DN; ++u) {
