@@ -86,6 +86,9 @@ struct MsLds {
     uint16_t bd[MS_RW][MS_MAXM][MS_DROW];  // down waves' h slices, deposited by their pollers
     f32x4 red_gu[2][MS_RW][2][64];         // gate/up partial tiles of the workgroup's (up to) two pairs
     f32x4 red_dn[MS_RW][64];               // down partial tiles
+    // up to 4 tokens: the M token columns only, [row quad + 4 * token]
+    f32x4 rc_gu[2][MS_RW][16][2];
+    f32x4 rc_dn[MS_RW][16];
     float red_ss[2][MS_RW][MS_MAXM];
     float xt[MS_MAXM][16];                 // x of this workgroup's down tile rows
     unsigned cnt_gu[2], cnt_dn;            // arrivals at the reductions (reset by the last arriver)
@@ -229,6 +232,14 @@ __device__ __forceinline__ void ms_wait_lds(unsigned* c, unsigned target, const 
     asm volatile("" ::: "memory");  // the deposited data is read only after the count
 }
 
+// Sum over the eight consecutive lanes of a group (every lane then holds its
+// group's sum): quad_perm pairs and quads, then row_half_mirror.  Fixed order.
+__device__ __forceinline__ float group8_sum(float v) {
+    v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+    return dpp_add<0x141, 0xF>(v);  // row_half_mirror
+}
+
 // One LDS deposit done: the data writes complete, then the counter.
 __device__ __forceinline__ void ms_deposit(unsigned* c, int lane) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -255,12 +266,27 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
     // BF16 weights (twice the bytes in flight ahead of the first poll) that
     // measured slower (162.5 -> 166 us per 24 blocks), and more tokens spill
     constexpr bool SELF = WF == WF_I8 && MT == 1;
+    // Partial-tile reduction up to 4 tokens (CMP): a wave writes only the M
+    // token columns of its partial tile to LDS (combo c = row quad + 4 *
+    // token, one f32x4 each); the last wave's lane 8 q + v reads wave v's
+    // combos q, q + 8 and sums them over v with DPP adds, so the epilogue
+    // reads 4 M f32x4 per wave instead of eight full tiles, and stores each
+    // round's tokens as soon as they are summed (token 0 first: the pollers
+    // wait for it).  24 blocks, us per block, BF16 / INT8: one token 6.74 ->
+    // 6.51 / 5.94 -> 5.80, two 7.65 -> 7.20 / 7.13 -> 6.92, four 8.79 -> 8.20
+    // / 8.32 -> 7.76.  Eight tokens keep the full tiles (10.36 against 10.77
+    // compact, 12.05 with every token's words in one store instruction).
+    constexpr bool CMP = MT <= 4;
+    constexpr int NC = 4 * MT;            // combos the registers are sized for
+    constexpr int NR = (NC + 7) / 8;      // combos per epilogue lane
     extern __shared__ __attribute__((aligned(16))) uint8_t ms_raw[];
     MsLds& S = *reinterpret_cast<MsLds*>(ms_raw);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int j = lane & 15, g = lane >> 4;
+    const int gq = MT <= 4 ? ((lane >> 3) & 3) : g;  // row quad of the epilogue lane's rows (scales)
+    const int ev = lane & 7, eq = lane >> 3;  // epilogue lane: wave ev, combos eq + 8 r
     const int wg = blockIdx.x;
     const int M = a.M;
     const bool dn_wg = wg >= MS_D0;          // a down workgroup (tile t, full K); else gate/up
@@ -432,7 +458,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             if constexpr (WF == WF_I8) {
 #pragma unroll
                 for (int rt = 0; rt < 2; ++rt)
-                    sc[rt] = *reinterpret_cast<const u32x4*>(a.gu_scales[l] + (p * 2 + rt) * 16 + g * 4);
+                    sc[rt] = *reinterpret_cast<const u32x4*>(a.gu_scales[l] + (p * 2 + rt) * 16 + gq * 4);
             }
         };
         // this lane's elements of the slice: k0 + 2*lane + {0, 1} of every token
@@ -540,8 +566,15 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 accu = cv.template mfma<OPDT>(2 * u + 1, A[u][1], b, accu);
             }
             // reduce the eight slices: the last wave to arrive runs the epilogue
-            S.red_gu[grp][w][0][lane] = accg;
-            S.red_gu[grp][w][1][lane] = accu;
+            if constexpr (CMP) {
+                if (j < M) {
+                    S.rc_gu[grp][w][g + 4 * j][0] = accg;
+                    S.rc_gu[grp][w][g + 4 * j][1] = accu;
+                }
+            } else {
+                S.red_gu[grp][w][0][lane] = accg;
+                S.red_gu[grp][w][1][lane] = accu;
+            }
             if (lane == 63) {
 #pragma unroll
                 for (int m = 0; m < MT; ++m) S.red_ss[grp][w][m] = ss[m];
@@ -553,40 +586,70 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             if (old == MS_RW - 1) {
                 if (a.trace && grp == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 12] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.cnt_gu[grp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                // the partials summed in wave order
-                const int jj = j < M ? j : 0;
-                f32x4 pv[MS_RW];
-                float ps[MS_RW];
-#pragma unroll
-                for (int v = 0; v < MS_RW; ++v) {
-                    pv[v] = S.red_gu[grp][v][0][lane];
-                    ps[v] = S.red_ss[grp][v][jj];
-                }
-                f32x4 gs = pv[0];
-                float sst = ps[0];
-#pragma unroll
-                for (int v = 1; v < MS_RW; ++v) {
-                    gs += pv[v];
-                    sst += ps[v];
-                }
-#pragma unroll
-                for (int v = 0; v < MS_RW; ++v) pv[v] = S.red_gu[grp][v][1][lane];
-                f32x4 us = pv[0];
-#pragma unroll
-                for (int v = 1; v < MS_RW; ++v) us += pv[v];
-                const float inv = 1.0f / sqrtf(sst / (float)MS_H + a.eps);
-                if constexpr (WF == WF_I8) {
-                    gs *= as_f32x4(sc[0]);
-                    us *= as_f32x4(sc[1]);
-                }
-                uint32_t hb[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) hb[i] = op_bits<WF>(silu_f(gs[i] * inv) * (us[i] * inv));
-                if (j < M) {
+                if constexpr (CMP) {
                     const uint32_t tg = ms_tag(epoch, l);
-                    uint64_t* hw = hbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_I / 2) + (p * 16 + g * 4) / 2;
-                    ms_store(hw, tg, hb[0] | (hb[1] << 16));
-                    ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
+#pragma unroll
+                    for (int r = 0; r < NR; ++r) {
+                        const int c = eq + 8 * r, jt = c >> 2;  // combo: rows [4 gq, 4 gq + 4) of token jt
+                        const int cc = c < NC ? c : 0;
+                        f32x4 gs = S.rc_gu[grp][ev][cc][0], us = S.rc_gu[grp][ev][cc][1];
+                        float sst = S.red_ss[grp][ev][jt < MT ? jt : 0];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            gs[i] = group8_sum(gs[i]);
+                            us[i] = group8_sum(us[i]);
+                        }
+                        sst = group8_sum(sst);
+                        const float inv = 1.0f / sqrtf(sst / (float)MS_H + a.eps);
+                        if constexpr (WF == WF_I8) {
+                            gs *= as_f32x4(sc[0]);
+                            us *= as_f32x4(sc[1]);
+                        }
+                        if (ev == 0 && jt < M) {
+                            uint32_t hb[4];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) hb[i] = op_bits<WF>(silu_f(gs[i] * inv) * (us[i] * inv));
+                            uint64_t* hw = hbuf + ((size_t)(l & 1) * MS_MAXM + jt) * (MS_I / 2) + (p * 16 + gq * 4) / 2;
+                            ms_store(hw, tg, hb[0] | (hb[1] << 16));
+                            ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
+                        }
+                    }
+                } else {
+                    // the partials summed in wave order
+                    const int jj = j < M ? j : 0;
+                    f32x4 pv[MS_RW];
+                    float ps[MS_RW];
+    #pragma unroll
+                    for (int v = 0; v < MS_RW; ++v) {
+                        pv[v] = S.red_gu[grp][v][0][lane];
+                        ps[v] = S.red_ss[grp][v][jj];
+                    }
+                    f32x4 gs = pv[0];
+                    float sst = ps[0];
+    #pragma unroll
+                    for (int v = 1; v < MS_RW; ++v) {
+                        gs += pv[v];
+                        sst += ps[v];
+                    }
+    #pragma unroll
+                    for (int v = 0; v < MS_RW; ++v) pv[v] = S.red_gu[grp][v][1][lane];
+                    f32x4 us = pv[0];
+    #pragma unroll
+                    for (int v = 1; v < MS_RW; ++v) us += pv[v];
+                    const float inv = 1.0f / sqrtf(sst / (float)MS_H + a.eps);
+                    if constexpr (WF == WF_I8) {
+                        gs *= as_f32x4(sc[0]);
+                        us *= as_f32x4(sc[1]);
+                    }
+                    uint32_t hb[4];
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i) hb[i] = op_bits<WF>(silu_f(gs[i] * inv) * (us[i] * inv));
+                    if (j < M) {
+                        const uint32_t tg = ms_tag(epoch, l);
+                        uint64_t* hw = hbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_I / 2) + (p * 16 + g * 4) / 2;
+                        ms_store(hw, tg, hb[0] | (hb[1] << 16));
+                        ms_store(hw + 1, tg, hb[2] | (hb[3] << 16));
+                    }
                 }
                 if (a.trace && grp == 0 && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 1] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.done_gu[grp], (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -629,7 +692,7 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 A[u] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                wr, lane * 16, (uint32_t)t * tile_bytes + (uint32_t)(kb + u) * 1024u, AUX_NT));
-            if constexpr (WF == WF_I8) sc = *reinterpret_cast<const u32x4*>(a.dn_scales[l] + t * 16 + g * 4);
+            if constexpr (WF == WF_I8) sc = *reinterpret_cast<const u32x4*>(a.dn_scales[l] + t * 16 + gq * 4);
         };
         issue(0);
         MsConv<WF, U_DN, (MT <= 4)> cv;
@@ -644,7 +707,11 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
                 const auto b = ms_bops<WF>(&S.bd[d][0][0], MS_DROW, u * 4 * KE, lane, M);
                 acc = cv.template mfma<OPDT>(u, A[u], b, acc);
             }
-            S.red_dn[d][lane] = acc;
+            if constexpr (CMP) {
+                if (j < M) S.rc_dn[d][g + 4 * j] = acc;
+            } else {
+                S.red_dn[d][lane] = acc;
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             unsigned old = 0;
             if (lane == 0) old = __hip_atomic_fetch_add(&S.cnt_dn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -652,29 +719,59 @@ __global__ __launch_bounds__(MS_NW * 64) __attribute__((amdgpu_waves_per_eu(4)))
             if (old == MS_RW - 1) {
                 if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 12] = __builtin_amdgcn_s_memrealtime();
                 if (lane == 0) __hip_atomic_store(&S.cnt_dn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                f32x4 pd[MS_RW];
+                if constexpr (CMP) {
 #pragma unroll
-                for (int v = 0; v < MS_RW; ++v) pd[v] = S.red_dn[v][lane];
-                f32x4 s = pd[0];
+                    for (int r = 0; r < NR; ++r) {
+                        // as the gate/up epilogue: combo c = rows [4 gq, 4 gq + 4) of token jt
+                        const int c = eq + 8 * r, jt = c >> 2;
+                        f32x4 sv = S.rc_dn[ev][c < NC ? c : 0];
 #pragma unroll
-                for (int v = 1; v < MS_RW; ++v) s += pd[v];
-                if constexpr (WF == WF_I8) s *= as_f32x4(sc);
-                if (j < M) {
-                    uint32_t xb[4];
+                        for (int i = 0; i < 4; ++i) sv[i] = group8_sum(sv[i]);
+                        if constexpr (WF == WF_I8) sv *= as_f32x4(sc);
+                        if (ev == 0 && jt < M) {
+                            uint32_t xb[4];
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float xn = round_act<XDT>(S.xt[j][g * 4 + i] + s[i]);
-                        S.xt[j][g * 4 + i] = xn;
-                        xb[i] = XDT == DT_BF16 ? f32_to_bf16_bits(xn) : f32_to_f16_bits(xn);
+                            for (int i = 0; i < 4; ++i) {
+                                const float xn = round_act<XDT>(S.xt[jt][gq * 4 + i] + sv[i]);
+                                S.xt[jt][gq * 4 + i] = xn;
+                                xb[i] = XDT == DT_BF16 ? f32_to_bf16_bits(xn) : f32_to_f16_bits(xn);
+                            }
+                            uint64_t* xw = xbuf + ((size_t)(l & 1) * MS_MAXM + jt) * (MS_H / 2) + (t * 16 + gq * 4) / 2;
+                            ms_store(xw, tg, xb[0] | (xb[1] << 16));
+                            ms_store(xw + 1, tg, xb[2] | (xb[3] << 16));
+                            if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 3] = __builtin_amdgcn_s_memrealtime();
+                            if (l + 1 == a.L) {
+                                uint32_t* yw = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (size_t)jt * MS_H + t * 16 + gq * 4);
+                                yw[0] = xb[0] | (xb[1] << 16);
+                                yw[1] = xb[2] | (xb[3] << 16);
+                            }
+                        }
                     }
-                    uint64_t* xw = xbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_H / 2) + (t * 16 + g * 4) / 2;
-                    ms_store(xw, tg, xb[0] | (xb[1] << 16));
-                    ms_store(xw + 1, tg, xb[2] | (xb[3] << 16));
-                    if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 3] = __builtin_amdgcn_s_memrealtime();
-                    if (l + 1 == a.L) {
-                        uint32_t* yw = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (size_t)j * MS_H + t * 16 + g * 4);
-                        yw[0] = xb[0] | (xb[1] << 16);
-                        yw[1] = xb[2] | (xb[3] << 16);
+                } else {
+                    f32x4 pd[MS_RW];
+    #pragma unroll
+                    for (int v = 0; v < MS_RW; ++v) pd[v] = S.red_dn[v][lane];
+                    f32x4 s = pd[0];
+    #pragma unroll
+                    for (int v = 1; v < MS_RW; ++v) s += pd[v];
+                    if constexpr (WF == WF_I8) s *= as_f32x4(sc);
+                    if (j < M) {
+                        uint32_t xb[4];
+    #pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float xn = round_act<XDT>(S.xt[j][g * 4 + i] + s[i]);
+                            S.xt[j][g * 4 + i] = xn;
+                            xb[i] = XDT == DT_BF16 ? f32_to_bf16_bits(xn) : f32_to_f16_bits(xn);
+                        }
+                        uint64_t* xw = xbuf + ((size_t)(l & 1) * MS_MAXM + j) * (MS_H / 2) + (t * 16 + g * 4) / 2;
+                        ms_store(xw, tg, xb[0] | (xb[1] << 16));
+                        ms_store(xw + 1, tg, xb[2] | (xb[3] << 16));
+                        if (a.trace && lane == 0) a.trace[((size_t)l * MS_GRID + wg) * 16 + 3] = __builtin_amdgcn_s_memrealtime();
+                        if (l + 1 == a.L) {
+                            uint32_t* yw = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(a.y) + (size_t)j * MS_H + t * 16 + g * 4);
+                            yw[0] = xb[0] | (xb[1] << 16);
+                            yw[1] = xb[2] | (xb[3] << 16);
+                        }
                     }
                 }
                 if (lane == 0) __hip_atomic_store(&S.done_dn, (unsigned)(l + 1), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
