@@ -170,7 +170,7 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only (no extra configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma-separated extra workloads to run (cfg1, cfg2, cfg3, wide, "
-                    "int8gemv, prefill, gdn, attn, model, lmhead; default all), e.g. for a profiler pass over one of them")
+                    "int8gemv, prefill, gdn, attn, model, lmhead; decode1 = the B=1 decode step of model alone; default all), e.g. for a profiler pass over one of them")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="counter pass: only the dominant kernel (4 eager MLP stack launches) and a "
                          "64 MiB calibration copy, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -349,8 +349,8 @@ def run_extras(qw, ctx, torch, timer, stream, randn, gu, dn, gam, args):
         extra.update(run_gdn(qw, ctx, torch, timer, stream, randn, args))
     if want("attn"):
         extra.update(run_attn(qw, ctx, torch, timer, stream, randn, args))
-    if want("model"):
-        extra.update(run_decode_model(qw, ctx, torch, timer, stream, randn, args))
+    if want("model") or (only and "decode1" in only):
+        extra.update(run_decode_model(qw, ctx, torch, timer, stream, randn, args, b1_only=not want("model")))
     if want("lmhead"):
         extra.update(run_lmhead(qw, ctx, torch, timer, stream, randn, steps))
     torch.cuda.synchronize()
@@ -613,7 +613,7 @@ def run_lmhead(qw, ctx, torch, timer, stream, randn, steps):
     return extra
 
 
-def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
+def run_decode_model(qw, ctx, torch, timer, stream, randn, args, b1_only=False):
     """The whole greedy decode step of the 24-layer model (engine.py: embedding
     gather, 18 Gated-DeltaNet + 6 full-attention layers, fused MLPs, final norm,
     lm_head argmax over 248320 tokens, position advance) captured as one graph
@@ -645,7 +645,7 @@ def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
     final_norm = randn(H, std=0.1, dtype=f32)
     out = {}
     ctxlen = 1024
-    for B in (1, 32):
+    for B in ((1,) if b1_only else (1, 32)):
         eng = em.DecodeEngine(qw, ctx, layers, final_norm, embed, B, ctxlen + 256)
         eng.reset(torch.randint(0, V, (B,)).tolist(), [ctxlen] * B)
         for P in eng.layers:
@@ -667,7 +667,7 @@ def run_decode_model(qw, ctx, torch, timer, stream, randn, args):
     # from position 0 with cleared states; the reset is outside the timed
     # region.  T=512 at B=1 is a mid-size prompt, where the 1024-row
     # projections sit between the small-M kernels and the split-K GEMM
-    for B, T in ((1, 1024), (16, 1024), (1, 512)):
+    for B, T in (() if b1_only else ((1, 1024), (16, 1024), (1, 512))):
         eng = em.DecodeEngine(qw, ctx, layers, final_norm, embed, B, T + 256)
         prompt = torch.randint(0, V, (B, T), device="cuda", dtype=torch.int32)
         times = []

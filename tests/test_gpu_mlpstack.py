@@ -159,7 +159,7 @@ def test_mlp_stack_bf16_folded_norm_24_layers(qw, ctx, oracle, relerr):
     assert e_stack <= bar and e_blocks <= bar
 
 
-@pytest.mark.parametrize("M", [1, 2, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8])
 def test_mlp_stack_int8(qw, ctx, oracle, relerr, M):
     """INT8 weights (per-row scales), F16 x; the reference composition is the
     dequant-then-matmul of the same q and s (in FP64) with the kernel's F16
