@@ -106,6 +106,7 @@ struct qw_ctx {
     bool layer_tail = false;               // QW_LAYER_TAIL=1: qw_layer_tail in one launch (measured slower)
     float4* partials = nullptr;
     size_t partials_bytes = 0;
+    float4* wide_partials = nullptr;        // the weight-stationary kernel's, every word kWideSentinel
     uint8_t* scratch = nullptr;            // MLP intermediate h
     size_t scratch_bytes = 0;
     uint8_t* xnorm = nullptr;              // RMSNorm-ed activations for the GEMM path
@@ -145,8 +146,12 @@ constexpr size_t kCountersBytes = 64 * 1024;     // 16384 tiles
 constexpr size_t kKeysBytes = 64 * 1024;         // 8192 tokens
 constexpr size_t kDoneBytes = 256;
 constexpr size_t kPartialsBytes = 64u << 20;
+// the weight-stationary kernel's split-K partials, kept at kWideSentinel (the
+// most it can use: one workgroup per CU x 32 units x 64 lanes x 36 bytes)
+constexpr size_t kWidePartialsBytes = 20u << 20;
 constexpr size_t kStackBytes = 512 * 1024;  // hand-off words of the persistent MLP stack (zeroed at init)
-constexpr size_t kFixedBytes = kCountersBytes + kKeysBytes + kDoneBytes + kStackBytes + kPartialsBytes;
+constexpr size_t kFixedBytes =
+    kCountersBytes + kKeysBytes + kDoneBytes + kStackBytes + kPartialsBytes + kWidePartialsBytes;
 constexpr int kMlpCounterWords = 4096;  // tail of the counter region: the one-launch MLP's slots
 constexpr int kMaxCounters = (int)(kCountersBytes / 4) - kMlpCounterWords;
 constexpr int kMaxKeys = (int)(kKeysBytes / 8);
@@ -296,6 +301,7 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     c->stack_words = reinterpret_cast<uint64_t*>(p); p += kStackBytes;
     c->partials = reinterpret_cast<float4*>(p); p += kPartialsBytes;
     c->partials_bytes = kPartialsBytes;
+    c->wide_partials = reinterpret_cast<float4*>(p); p += kWidePartialsBytes;
     {
         // the rest: normalized activations (about a third) and the MLP intermediate
         const size_t rest = workspace_bytes - kFixedBytes;
@@ -307,8 +313,10 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     }
     // counters, keys and the completion counter start at zero; every kernel
     // that uses them returns them to zero before it exits.
+    // The weight-stationary kernel's partials start empty (every word the
+    // sentinel); its finishing workgroups empty what they consumed.
     if (hipMemset(c->ws, 0, kCountersBytes + kKeysBytes + kDoneBytes + kStackBytes) != hipSuccess ||
-        hipDeviceSynchronize() != hipSuccess) {
+        hipMemset(c->wide_partials, 0xff, kWidePartialsBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
         hipFree(c->ws);
         delete c;
         return QW_ERR_HIP;
@@ -793,7 +801,7 @@ static qw_status run_wide(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dty
     a.partials = ctx->partials;
     a.counters = ctx->counters;
     qwk::WidePlan p{};
-    if (!qwk::wide_plan(a, W->wf, W->glu != 0, ctx->num_cus, ctx->partials_bytes, kMaxCounters, ctx->wide_s,
+    if (!qwk::wide_plan(a, W->wf, W->glu != 0, ctx->num_cus, kWidePartialsBytes, kMaxCounters, ctx->wide_s,
                         ctx->wide_cfg, p))
         return QW_ERR_SHAPE;
     if ((uint64_t)W->bytes >= (1ull << 32) || (uint64_t)M * ldx * dsize(xdt) >= (1ull << 32))
@@ -809,6 +817,8 @@ static qw_status run_wide(qw_ctx* ctx, const qw_weight* W, const void* x, qw_dty
     wa.Mg = p.Mg;
     wa.ngrp = p.ngrp;
     wa.dbg = ctx->wide_dbg;
+    wa.wpart = ctx->wide_partials;
+    wa.err = ctx->mlp_ctl + 3;
     if (ctx->wide_dbg & 8)
         fprintf(stderr, "wide N=%d K=%d M=%d glu=%d: S=%d T=%d NB=%d KW=%d CT=%d grid=%d smem=%zu\n", W->N, W->K, M,
                 W->glu, p.S, p.T, p.NB, p.KW, p.CT, p.grid, p.smem);

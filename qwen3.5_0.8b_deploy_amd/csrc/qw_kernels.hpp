@@ -95,7 +95,13 @@ struct WideArgs {
     int Mg;
     int ngrp;          // block groups (NB blocks each; a multiple of 8 when T > 1)
     int dbg;           // timing probes only (wrong results): 1 no MFMAs, 2 no split-K hand-off, 4 no staging
+    float4* wpart;     // split-K partials of this kernel, every word kWideSentinel between launches
+    unsigned* err;     // device error flag (a split's partial never arrived)
 };
+// The bit pattern of an empty partials word.  No partial sum of products of
+// 16-bit operands has it (their NaN payloads leave the low 13 bits zero), and
+// the producers map it to the canonical NaN anyway.
+constexpr uint32_t kWideSentinel = 0xffffffffu;
 struct WidePlan {
     int S, T, Mg, ngrp, NB, KW, CT, grid;
     size_t smem;

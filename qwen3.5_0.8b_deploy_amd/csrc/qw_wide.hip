@@ -36,11 +36,11 @@
 //      tile and k-step), and (1 + gamma) scales the weight operand, so the
 //      staged activations are used as they are.
 //   5. The KW partial tiles of a block meet in LDS (fixed order); the split
-//      partials meet through the workspace: device-coherent (sc1) 16-byte
-//      stores, s_waitcnt, one arrival count per block group; the last of the S
-//      workgroups sums the S partials in split order (deterministic), returns
-//      the counter to zero (graph-safe, no memset) and runs the epilogue,
-//      spread over its waves.
+//      partials meet through a workspace region whose words hold a sentinel
+//      between launches: splits 0..S-2 store theirs (device-coherent, sc1),
+//      split S-1 polls them until no word is the sentinel, sums the S
+//      partials in split order (deterministic), writes the sentinel back
+//      (graph-safe, no memset) and runs the epilogue, spread over its waves.
 //   6. Epilogue: 1/rms, INT8 row scale, SiLU(gate)*up, residual, Q/gate
 //      de-interleave, 4-wide stores.
 //
@@ -324,10 +324,10 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
     // both physical tiles of a block for one token tile).  Every wave writes
     // its accumulators to LDS (over the activations), then wave w owns units
     // w, w + NW, ...: it sums their KW parts in a fixed order and, with S > 1,
-    // hands them over through the workspace.  The last workgroup of a block
-    // group to arrive loads all S partials of its units at once, sums them
-    // in split order and runs their epilogue, so the epilogue is spread over
-    // all waves.
+    // hands them over through the workspace.  The workgroup of the last
+    // split of a block group collects the other S - 1 partials of its units,
+    // sums the S in split order and runs their epilogue, so the epilogue is
+    // spread over all its waves.
     constexpr int NU = NB * CT;                 // units per workgroup
     constexpr int UPW = (NU + NW - 1) / NW;     // units per wave (upper bound)
     __syncthreads();                            // every wave is done with the activations
@@ -364,67 +364,116 @@ __global__ __launch_bounds__(NB * KW * 64) void wide_kernel(WideArgs wa) {
     }
 
     if (S > 1 && !(wa.dbg & 2)) {
-        // partials: [group][split][unit][lane] RT x 16 bytes, then the sums of
-        // squares [group][split][unit][lane] x 4 bytes; device-coherent (sc1)
+        // Split-K hand-off without counters: the partials region holds
+        // kWideSentinel in every word between launches.  Splits 0..S-2 store
+        // their partials (device-coherent, sc1) and are done; split S-1, the
+        // finisher, polls each partner's words until none holds the sentinel
+        // (each 32-bit word is written whole), sums the S partials in split
+        // order -- its own from registers, the same values the others'
+        // stores carry, so the sum is the one the arrival-count hand-off
+        // formed -- and writes the sentinel back.  One memory round trip
+        // after the last partner's stores, instead of store completion, an
+        // arrival count and the reloads.
+        // Layout: [group][split][unit][lane] RT x 16 bytes, then the sums of
+        // squares [group][split][unit][lane] x 4 bytes.
         const int ngrp = wa.ngrp * T;
         const uint64_t vbytes = (uint64_t)ngrp * S * NU * 64 * RT * 16;
         const uint64_t pbytes = vbytes + (uint64_t)ngrp * S * NU * 64 * 4;
-        const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials, (uint32_t)min(pbytes, (uint64_t)0x7fffffff));
+        const __amdgpu_buffer_rsrc_t prs = make_rsrc(wa.wpart, (uint32_t)min(pbytes, (uint64_t)0x7fffffff));
         auto voff = [&](int s2, int u, int rt) {
             return (uint32_t)(((((uint64_t)cgrp * S + s2) * NU + u) * 64 + lane) * RT + rt) * 16u;
         };
         auto soff = [&](int s2, int u) {
             return (uint32_t)(vbytes + ((((uint64_t)cgrp * S + s2) * NU + u) * 64 + lane) * 4u);
         };
+        auto canon = [](float v) {
+            const uint32_t b = __float_as_uint(v);
+            return b == kWideSentinel ? 0x7fc00000u : b;
+        };
+        const int fin = S - 1;
+        if (s != fin) {
 #pragma unroll
-        for (int i = 0; i < UPW; ++i) {
-            const int u = wave + i * NW;
-            if (u < NU) {
+            for (int i = 0; i < UPW; ++i) {
+                const int u = wave + i * NW;
+                if (u < NU) {
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, u_acc[i][rt]), prs, voff(s, u, rt),
-                                                           0, AUX_SC1);
-                if (norm) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(u_ss[i]), prs, soff(s, u), 0, AUX_SC1);
+                    for (int rt = 0; rt < RT; ++rt) {
+                        const f32x4 v = u_acc[i][rt];
+                        __builtin_amdgcn_raw_buffer_store_b128(u32x4{canon(v[0]), canon(v[1]), canon(v[2]), canon(v[3])},
+                                                               prs, voff(s, u, rt), 0, AUX_SC1);
+                    }
+                    if (norm) __builtin_amdgcn_raw_buffer_store_b32(canon(u_ss[i]), prs, soff(s, u), 0, AUX_SC1);
+                }
             }
+            return;
         }
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __shared__ unsigned last_s;
-        __syncthreads();  // every wave's partials are complete
-        if (threadIdx.x == 0) {
-            const unsigned old = __hip_atomic_fetch_add(&a.counters[cgrp], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last_s = old == (unsigned)(S - 1) ? 1u : 0u;
-            if (old == (unsigned)(S - 1)) __hip_atomic_store(&a.counters[cgrp], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!last_s) return;  // uniform over the workgroup
-        // all S partials of this wave's units in flight at once, then summed
-        // in split order
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
 #pragma unroll
         for (int i = 0; i < UPW; ++i) {
             const int u = wave + i * NW;
             if (u >= NU) continue;
             f32x4 pv[kWideMaxS][RT];
             float ps[kWideMaxS];
+            // every partner's words in flight at once, reloaded until all arrived
+            for (unsigned it = 0;; ++it) {
+                bool ok = true;
 #pragma unroll
-            for (int s2 = 0; s2 < kWideMaxS; ++s2) {
-                if (s2 < S) {
+                for (int s2 = 0; s2 < kWideMaxS; ++s2) {
+                    if (s2 < fin) {
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt)
-                        pv[s2][rt] = __builtin_bit_cast(
-                            f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, voff(s2, u, rt), 0, AUX_SC1));
-                    ps[s2] = norm ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, soff(s2, u), 0, AUX_SC1))
-                                  : 0.0f;
+                        for (int rt = 0; rt < RT; ++rt) {
+                            const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(prs, voff(s2, u, rt), 0, AUX_SC1);
+                            ok = ok && w[0] != kWideSentinel && w[1] != kWideSentinel && w[2] != kWideSentinel &&
+                                 w[3] != kWideSentinel;
+                            pv[s2][rt] = __builtin_bit_cast(f32x4, w);
+                        }
+                        if (norm) {
+                            const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(prs, soff(s2, u), 0, AUX_SC1);
+                            ok = ok && w != kWideSentinel;
+                            ps[s2] = __uint_as_float(w);
+                        } else {
+                            ps[s2] = 0.0f;
+                        }
+                    }
                 }
+                if (__all(ok)) break;
+                // bounded wait (0.2 s of the 100 MHz clock): a partial that
+                // never arrives raises the error flag instead of hanging
+                if ((it & 63u) == 63u && __builtin_amdgcn_s_memrealtime() - t0 > 20000000ull) {
+                    __hip_atomic_store(wa.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
             }
+            // the S partials summed in split order, the finisher's own last
+            f32x4 own[RT];
 #pragma unroll
-            for (int rt = 0; rt < RT; ++rt) u_acc[i][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int rt = 0; rt < RT; ++rt) {
+                own[rt] = u_acc[i][rt];
+                u_acc[i][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            const float own_ss = u_ss[i];
             u_ss[i] = 0.0f;
 #pragma unroll
             for (int s2 = 0; s2 < kWideMaxS; ++s2) {
-                if (s2 < S) {
+                if (s2 < fin) {
 #pragma unroll
                     for (int rt = 0; rt < RT; ++rt) u_acc[i][rt] += pv[s2][rt];
                     u_ss[i] += ps[s2];
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) u_acc[i][rt] += own[rt];
+            u_ss[i] += own_ss;
+            // the partners' words emptied for the next launch
+            const u32x4 e4 = u32x4{kWideSentinel, kWideSentinel, kWideSentinel, kWideSentinel};
+#pragma unroll
+            for (int s2 = 0; s2 < kWideMaxS; ++s2) {
+                if (s2 < fin) {
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt)
+                        __builtin_amdgcn_raw_buffer_store_b128(e4, prs, voff(s2, u, rt), 0, AUX_SC1);
+                    if (norm) __builtin_amdgcn_raw_buffer_store_b32(kWideSentinel, prs, soff(s2, u), 0, AUX_SC1);
                 }
             }
         }
