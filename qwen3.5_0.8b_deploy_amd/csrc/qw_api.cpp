@@ -101,6 +101,8 @@ struct qw_ctx {
     bool mlp_stack = true;                 // QW_MLP_STACK=0: per-layer launches in qw_mlp_stack
     int argmax_cache = -1;                 // QW_ARGMAX_CACHE: weight-load cache policy of that kernel (-1 auto, 0 NT, 1 default)
     int argmax_wide_min_i8 = 8;            // QW_ARGMAX_WIDE_MIN_I8: INT8 lm_head tokens from which the weight-stationary argmax runs
+    bool argmax_as = true;                 // QW_ARGMAX_AS=0: no activation-stationary lm_head argmax
+    int argmax_as_min = 65;                // QW_ARGMAX_AS_MIN: tokens from which it runs (to 128)
     int argmax_nw = 0;                     // QW_ARGMAX_NW: waves per weight-stationary argmax workgroup (0 auto, 4, 8)
     int gemm_da_split = -1;                // QW_GEMM_DA_SPLIT: split-K direct-A for few blocks (-1 auto, 0 off, S)
     bool layer_tail = false;               // QW_LAYER_TAIL=1: qw_layer_tail in one launch (measured slower)
@@ -243,6 +245,8 @@ qw_status qw_init(qw_ctx** out, int device, size_t workspace_bytes) {
     if (const char* v = getenv("QW_GEMM_DA_SPLIT")) c->gemm_da_split = atoi(v);
     if (const char* v = getenv("QW_ARGMAX_CACHE")) c->argmax_cache = atoi(v) ? 1 : 0;
     if (const char* v = getenv("QW_ARGMAX_WIDE_MIN_I8")) c->argmax_wide_min_i8 = std::max(1, atoi(v));
+    if (const char* v = getenv("QW_ARGMAX_AS")) c->argmax_as = atoi(v) != 0;
+    if (const char* v = getenv("QW_ARGMAX_AS_MIN")) c->argmax_as_min = std::max(1, atoi(v));
     if (const char* v = getenv("QW_ARGMAX_NW")) c->argmax_nw = (atoi(v) == 4 || atoi(v) == 8) ? atoi(v) : 0;
     if (const char* v = getenv("QW_GEMM_TILE_M")) c->gemm_tile_m = atoi(v) == 256 ? 256 : 128;  // forced
     if (const char* v = getenv("QW_GEMM_WAVES")) c->gemm_waves = atoi(v) == 4 ? 4 : 8;
@@ -1114,7 +1118,11 @@ static qw_status lmhead_route(qw_ctx* ctx, const qw_weight* E, const void* h, qw
         a.wcache = ctx->argmax_cache;
         int grid = 0;
         size_t smem = 0;
-        if (qwk::wide_argmax_plan(E->wf, (int)hdt, M, E->K, ctx->num_cus, a, grid, smem)) {
+        // BF16 E at 65..128 tokens: the activation-stationary form streams E
+        // once instead of once per 64-token group (96-98 against 99-101 us)
+        const bool as = ctx->argmax_as && M >= ctx->argmax_as_min &&
+                        qwk::as_argmax_plan(E->wf, (int)hdt, M, E->K, ctx->num_cus, grid, smem);
+        if (as || qwk::wide_argmax_plan(E->wf, (int)hdt, M, E->K, ctx->num_cus, a, grid, smem)) {
             a.w = E->packed;
             a.scales = E->scales;
             a.x = h;
@@ -1129,7 +1137,8 @@ static qw_status lmhead_route(qw_ctx* ctx, const qw_weight* E, const void* h, qw
             a.ids = ids;
             a.maxv = maxv;
             a.dbg = ctx->wide_dbg;
-            hipError_t e = qwk::launch_wide_argmax(a, E->wf, (int)hdt, grid, smem, stream);
+            hipError_t e = as ? qwk::launch_as_argmax(a, E->wf, (int)hdt, grid, smem, stream)
+                              : qwk::launch_wide_argmax(a, E->wf, (int)hdt, grid, smem, stream);
             if (e != hipSuccess) return hip_fail(ctx, e, "weight-stationary lm_head launch");
             return QW_OK;
         }

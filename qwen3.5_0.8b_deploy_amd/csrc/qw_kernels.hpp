@@ -133,6 +133,11 @@ struct WideArgmaxArgs {
 };
 bool wide_argmax_plan(int wf, int xdt, int M, int K, int num_cus, WideArgmaxArgs& a, int& grid, size_t& smem);
 hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid, size_t smem, hipStream_t stream);
+// The activation-stationary form (BF16 E, 65..128 tokens, K = 1024): E
+// streamed once through an LDS ring, each wave holding one token tile's
+// activations; false where it does not apply.
+bool as_argmax_plan(int wf, int xdt, int M, int K, int num_cus, int& grid, size_t& smem);
+hipError_t launch_as_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid, size_t smem, hipStream_t stream);
 
 // LDS double-buffered MFMA GEMM for many tokens (qw_gemm.hip).
 struct GemmArgs {

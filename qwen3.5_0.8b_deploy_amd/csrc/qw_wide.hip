@@ -817,6 +817,153 @@ __global__ __launch_bounds__(NW * 64) void wide_argmax_kernel(WideArgmaxArgs a) 
 }
 
 // ---------------------------------------------------------------------------
+// Tied lm_head with the fused greedy argmax, activation-stationary, BF16 E,
+// 65..128 tokens (K = 1024).
+//
+// The weight-stationary kernel above holds a token group's activations in LDS,
+// so beyond 64 tokens it runs two token groups and every CU pulls its share
+// of E into registers twice.  Here the roles flip: each of the 8 waves keeps
+// one 16-token tile of the activations in registers for all of K (the MFMA B
+// operands, 128 VGPRs), and E streams through an LDS ring exactly once per
+// workgroup: direct-to-LDS loads of 32-row chunks (both tiles of a block over
+// 16 k-steps, 32 KB), four chunks deep, read by all 8 waves as MFMA A
+// operands.  One barrier per chunk publishes it and frees the slot the chunk
+// three ahead is loaded into.  Each accumulator sums its k-steps in the order
+// the weight-stationary kernel does, so the logits, the maxima and the ids
+// are the same bit for bit; a lane visits its rows in increasing order
+// (strict compare: the lowest row of a tie), and the keys meet as there (one
+// atomic max per token, the last workgroup decodes).
+//
+// Every wave reads every A fragment of E from LDS, 1 KB per MFMA (the
+// weight-stationary kernel reads 0.5 KB of B per MFMA), so the LDS reads, not
+// the stream, bound it: 96-98 us at 65..128 tokens against 99-101 us for the
+// two weight-stationary passes.  With INT8 E it lost (98 against 78 us, the
+// units converted to f16 once per chunk into LDS; 130 us with every wave
+// converting them), so INT8 keeps the weight-stationary kernel.
+// ---------------------------------------------------------------------------
+constexpr int kAsNW = 8;                           // waves: one 16-token tile each
+constexpr int kAsKC = 16;                          // k-steps per chunk
+constexpr int kAsNS = 4;                           // chunks in the LDS ring
+constexpr int kAsChunk = 2 * kAsKC * 1024;         // both tiles' 1 KB units
+constexpr size_t kAsLds = (size_t)kAsNS * kAsChunk;
+
+__global__ __launch_bounds__(kAsNW * 64) void as_argmax_kernel(WideArgmaxArgs a) {
+    constexpr int KSTEPS = 32;                     // k-steps of K = 1024
+    constexpr int CH = KSTEPS / kAsKC;             // chunks per 32-row block
+    constexpr int PER = 2 * kAsKC / kAsNW;         // units a wave loads per chunk
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int G = (int)gridDim.x, wg = (int)blockIdx.x;
+    const int nb = wg < a.n_blk ? (a.n_blk - wg + G - 1) / G : 0;  // blocks wg, wg + G, ...
+    const int nq = nb * CH;                                        // chunks
+    const int m = wave * 16 + r;                                   // this lane's token
+
+    // ---- the wave's token tile, all of K, as B operands ----
+    u32x4 B[KSTEPS];
+    {
+        const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * a.ldx * 2));
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+            B[ks] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           xr, m < a.M ? (uint32_t)((m * a.ldx + ks * 32 + g * 8) * 2) : OOB, 0, 0));
+    }
+
+    // ---- E through the LDS ring ----
+    const uint32_t tile_bytes = (uint32_t)KSTEPS * 1024u;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w, (uint32_t)((uint64_t)a.n_tiles * tile_bytes));
+    // chunk q into slot q % NS: block wg + (q / CH) G, k-steps from (q % CH)
+    // KC; unit u of a chunk is tile u / KC, k-step u % KC.  Every wave issues
+    // the same loads per chunk (chunks past the end read zeros), so one wait
+    // count fits every chunk.
+    auto dma = [&](int q) {
+        uint8_t* slot = lds + (q % kAsNS) * kAsChunk;
+        const int blk = wg + (q / CH) * G;
+        const uint32_t k0 = (uint32_t)(q % CH) * kAsKC * 1024u;
+        const bool ok = q < nq;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const int u = wave * PER + p;
+            const int rt = u / kAsKC, kk = u % kAsKC;
+            lds_dma16(wrs, slot + u * 1024,
+                      ok ? (uint32_t)(2 * blk + rt) * tile_bytes + k0 + (uint32_t)kk * 1024u + lane * 16 : OOB);
+        }
+    };
+#pragma unroll
+    for (int q = 0; q < kAsNS - 1; ++q) dma(q);
+
+    float bv = -__builtin_inff();  // this lane's running maximum of its token and its row
+    uint32_t bi = 0xffffffffu;
+    f32x4 acc[2];
+    for (int i = 0; i < nb; ++i) {
+        const int blk = wg + i * G;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int q = i * CH + c;
+            // chunk q has landed (the NS - 2 after it may still be in flight);
+            // the barrier makes every wave's part of it visible and frees the
+            // slot of q - 1
+            __builtin_amdgcn_s_waitcnt(vm_wait((kAsNS - 2) * PER));
+            __syncthreads();
+            dma(q + kAsNS - 1);
+            const uint8_t* sl = lds + (q % kAsNS) * kAsChunk + lane * 16;
+            if (c == 0) acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < kAsKC; ++kk) {
+                const u32x4 A0 = *reinterpret_cast<const u32x4*>(sl + kk * 1024);
+                const u32x4 A1 = *reinterpret_cast<const u32x4*>(sl + (kAsKC + kk) * 1024);
+                const bf16x8 b = __builtin_bit_cast(bf16x8, B[c * kAsKC + kk]);
+                acc[0] = mfma_bf16(__builtin_bit_cast(bf16x8, A0), b, acc[0]);
+                acc[1] = mfma_bf16(__builtin_bit_cast(bf16x8, A1), b, acc[1]);
+            }
+            if (c == CH - 1) {  // the block's logits: into the running maximum
+                const int row0 = blk * 32 + g * 4;
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = row0 + rt * 16 + e;
+                        const bool gt = row < a.V && acc[rt][e] > bv;
+                        bv = gt ? acc[rt][e] : bv;
+                        bi = gt ? (uint32_t)row : bi;
+                    }
+            }
+        }
+    }
+
+    // ---- keys: the four row groups of a lane's token, then the grid ----
+    unsigned long long best = 0ull;
+    if (bi != 0xffffffffu && m < a.M) best = argmax_key(bv, bi);
+#pragma unroll
+    for (int sh = 16; sh <= 32; sh <<= 1) {
+        const unsigned long long o = __shfl_xor(best, sh);
+        best = o > best ? o : best;
+    }
+    if (g == 0 && m < a.M && best != 0ull)
+        __hip_atomic_fetch_max(&a.keys[m], best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // completion as in the weight-stationary kernel: device-scope RMWs past
+    // the L2s, observed by s_waitcnt before the count
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ unsigned last;
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = old == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    for (int mm = threadIdx.x; mm < a.M; mm += kAsNW * 64) {
+        const unsigned long long kk = __hip_atomic_exchange(&a.keys[mm], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.ids[mm] = (int32_t)key_index(kk);
+        if (a.maxv) a.maxv[mm] = key_value(kk);
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 namespace {
@@ -1015,6 +1162,23 @@ hipError_t launch_wide_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid
     if (wf == WF_BF16) return pick(std::integral_constant<int, WF_BF16>{}, std::integral_constant<int, DT_BF16>{});
     if (xdt == DT_BF16) return pick(I{}, std::integral_constant<int, DT_BF16>{});
     return pick(I{}, std::integral_constant<int, DT_F16>{});
+}
+
+bool as_argmax_plan(int wf, int xdt, int M, int K, int num_cus, int& grid, size_t& smem) {
+    if (!(wf == WF_BF16 && xdt == DT_BF16) || K != 1024 || M < 1 || M > kAsNW * 16 || num_cus < 8) return false;
+    grid = num_cus;
+    smem = kAsLds;
+    return true;
+}
+
+hipError_t launch_as_argmax(const WideArgmaxArgs& a, int wf, int xdt, int grid, size_t smem, hipStream_t stream) {
+    if (!(wf == WF_BF16 && xdt == DT_BF16) || a.K != 1024 || a.M < 1 || a.M > kAsNW * 16 || smem != kAsLds ||
+        a.scales)
+        return hipErrorInvalidValue;
+    hipError_t e = ensure_max_lds(reinterpret_cast<const void*>(as_argmax_kernel), (int)smem);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(as_argmax_kernel, dim3(grid), dim3(kAsNW * 64), smem, stream, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_wide(const WideArgs& a, const WidePlan& p, int wf, int xdt, bool glu, hipStream_t stream) {

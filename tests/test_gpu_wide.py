@@ -300,7 +300,7 @@ def test_int8_glu_norm(qw, wctx, wctx_sep_norm, oracle, relerr, M, sep):
     assert relerr(host(h), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("M", [17, 40, 100, 256])
+@pytest.mark.parametrize("M", [17, 40, 65, 100, 128, 256])
 @pytest.mark.parametrize("fmt", ["bf16", "int8", "int8_bf16x"])
 def test_lmhead_argmax_odd_vocab(qw, ctx, oracle, fmt, M):
     """The weight-stationary lm_head argmax on a vocabulary of 627 tiles (the
@@ -337,3 +337,39 @@ def test_lmhead_argmax_odd_vocab(qw, ctx, oracle, fmt, M):
         srt = np.sort(logits[t])
         if srt[-1] - srt[-2] > 1e-3:
             assert int(got[t]) == int(np.argmax(logits[t])), t
+
+
+@pytest.mark.parametrize("M", [65, 100, 128])
+def test_lmhead_argmax_activation_stationary_matches(qw, ctx, oracle, M):
+    """BF16 E at 65..128 tokens takes the activation-stationary lm_head argmax
+    (E through an LDS ring once, each wave holding a token tile): its ids and
+    winning logits equal the weight-stationary kernel's (a context made with
+    QW_ARGMAX_AS=0) bit for bit, on a vocabulary with an odd tile count, twice
+    in a row (keys and the completion count return to zero)."""
+    import os
+    V, K = 10024, 1024
+    E = oracle.round_bf16(oracle.normal((V, K), 3600, 0.0, 0.02))
+    h = oracle.normal((M, K), 3601 + M)
+    os.environ["QW_ARGMAX_AS"] = "0"
+    try:
+        c2 = qw.Context(0)
+    finally:
+        del os.environ["QW_ARGMAX_AS"]
+    try:
+        w1 = qw.Weight.pack(ctx, E, qw.WFMT_BF16)
+        w2 = qw.Weight.pack(c2, E, qw.WFMT_BF16)
+        x = dev(h, torch.bfloat16)
+        for rep in range(2):
+            ids1 = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+            mx1 = torch.empty(M, device="cuda")
+            qw.lmhead_argmax(ctx, w1, x, ids1, mx1)
+            ids2 = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+            mx2 = torch.empty(M, device="cuda")
+            qw.lmhead_argmax(c2, w2, x, ids2, mx2)
+            torch.cuda.synchronize()
+            assert torch.equal(ids1, ids2), rep
+            assert torch.equal(mx1, mx2), rep
+            assert int(ids1.min()) >= 0
+        assert ctx.device_error() == 0 and c2.device_error() == 0
+    finally:
+        c2.close()

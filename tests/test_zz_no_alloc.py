@@ -44,7 +44,7 @@ def test_noalloc_rejects_beyond_max(qw, ctx, oracle):
     assert e.value.status == qw.ERR_SHAPE
 
 
-@pytest.mark.parametrize("M", [1, 64])
+@pytest.mark.parametrize("M", [1, 64, 100])
 def test_noalloc_graph_replays(qw, ctx, oracle, M):
     """Captured once in a graph (the use the entry point exists for) and
     replayed with new activations copied in between, eager work of the
