@@ -373,3 +373,43 @@ def test_lmhead_argmax_activation_stationary_matches(qw, ctx, oracle, M):
         assert ctx.device_error() == 0 and c2.device_error() == 0
     finally:
         c2.close()
+
+
+def test_splitk_partials_return_to_sentinel(qw, wctx, oracle):
+    """The split-K partials region holds a sentinel between launches; every
+    finishing workgroup writes it back over the words it consumed.  Launches
+    with different plans (split counts, token groups, units per workgroup,
+    with and without the norm prologue) reuse the same words in different
+    layouts, so a word left holding a partial would be taken for a partner's
+    fresh one by a later launch.  The same calls in two different orders, on
+    one context, must give the same outputs bit for bit."""
+    rng = np.random.default_rng(4200)
+    cases = []
+    for N, K, glu in ((1024, 3584, False), (1024, 2048, False), (3584, 1024, True)):
+        if glu:
+            w = qw.Weight.pack_glu(wctx, oracle.normal((N, K), 4201, 0.0, 0.02), oracle.normal((N, K), 4202, 0.0, 0.02),
+                                   qw.WFMT_BF16)
+        else:
+            w = qw.Weight.pack(wctx, oracle.normal((N, K), 4203 + N + K, 0.0, 0.02), qw.WFMT_BF16)
+        for M in (17, 32, 64, 100, 128, 256):
+            x = dev(rng.standard_normal((M, K)).astype(np.float32), torch.bfloat16)
+            gam = dev(rng.standard_normal(K).astype(np.float32) * 0.05) if glu else None
+            cases.append((w, x, gam, N, M))
+
+    def run(order):
+        outs = {}
+        for i in order:
+            w, x, gam, N, M = cases[i]
+            y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+            qw.linear(wctx, w, x, y, gamma=gam)
+            outs[i] = y
+        torch.cuda.synchronize()
+        return outs
+
+    a = run(range(len(cases)))
+    b = run(reversed(range(len(cases))))
+    c = run(rng.permutation(len(cases)))
+    assert wctx.device_error() == 0
+    for i in range(len(cases)):
+        assert torch.equal(a[i], b[i]), i
+        assert torch.equal(a[i], c[i]), i
